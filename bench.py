@@ -1,0 +1,253 @@
+"""Paged-attention hot-path benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-extras] [--no-cpu]
+
+A "step" is one ``ops.paged_attention(use_cuda=True)`` call over BASELINE config 2:
+paged decode, bf16, batch 64, context lengths U[512, 4096] (seed 0), GQA 16q/8kv,
+D=128, 16-token pages, shuffled block ids, pool = pages + 10%. Inputs are resident in
+HBM before timing. Several copies of the pools are rotated so each step streams its
+K/V from HBM rather than from the 256 MB Infinity Cache (config 2's K+V is ~0.6 GB).
+
+``value`` is the algorithmic K+V bytes of one step (every visible key row read once,
+the reference's definition, mini_vllm/bench.py:643) divided by the mean step time,
+W warmup steps then K steps between two synchronizations, timed with HIP events on
+the stream the kernels run on. Extras (configs 3 and 4, a device copy ceiling) are
+reported in the same JSON line. ``cpu_baseline`` times the CPU oracle (the
+reference's gather-then-dense PyTorch path, restated in oracle/) on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (REPO / "mini-vllm_amd", REPO):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+import torch  # noqa: E402
+
+METRIC = "paged-attn decode HBM GB/s (% of peak) + engine decode tok/s, Qwen3-0.6B"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_steps(fn, steps: int, warmup: int) -> tuple[float, list[float]]:
+    """Mean ms per call over `steps` back-to-back calls, plus per-call event times."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    first = torch.cuda.Event(enable_timing=True)
+    last = torch.cuda.Event(enable_timing=True)
+    first.record(stream)
+    for i in range(steps):
+        starts[i].record(stream)
+        fn(i)
+        ends[i].record(stream)
+    last.record(stream)
+    torch.cuda.synchronize()
+    per_call = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return first.elapsed_time(last) / steps, per_call
+
+
+def rotated_batches(index: int, copies: int):
+    """`copies` batches sharing shapes and tables, each with its own K/V pools."""
+    from mini_vllm.workloads import config_batch
+
+    base = config_batch(index, device="cuda", generator_device="cuda")
+    batches = [base]
+    for c in range(1, copies):
+        other = config_batch(index, device="cuda", seed=0, generator_device="cuda")
+        gen = torch.Generator(device="cuda").manual_seed(1000 + c)
+        if other.key_pool.dtype == torch.float8_e4m3fn:
+            # fresh fp8 codes with the same scales: any finite code pattern is valid data
+            other.key_pool = torch.randint(0, 126, other.key_pool.shape, generator=gen,
+                                           device="cuda", dtype=torch.uint8).view(torch.float8_e4m3fn)
+            other.value_pool = torch.randint(0, 126, other.value_pool.shape, generator=gen,
+                                             device="cuda", dtype=torch.uint8).view(torch.float8_e4m3fn)
+        else:
+            other.key_pool = torch.randn(other.key_pool.shape, generator=gen, device="cuda").to(other.key_pool.dtype)
+            other.value_pool = torch.randn(other.value_pool.shape, generator=gen, device="cuda").to(other.value_pool.dtype)
+        batches.append(other)
+    return batches
+
+
+def run_paged(batches, steps, warmup):
+    from mini_vllm.kernels import ops
+
+    outs = [torch.empty_like(b.q) for b in batches]
+
+    def step(i):
+        b = batches[i % len(batches)]
+        ops.paged_attention(*b.args(), use_cuda=True, k_scale=b.k_scale, v_scale=b.v_scale)
+
+    return time_steps(step, steps, warmup)
+
+
+def copy_ceiling(nbytes: int, steps: int = 20) -> float:
+    """GB/s of a device-to-device copy_ (read + write counted), the practical ceiling
+    (method of the reference's mini_vllm/bench.py:448-466)."""
+    n = nbytes // 2
+    src = [torch.empty(n, dtype=torch.bfloat16, device="cuda").normal_() for _ in range(2)]
+    dst = [torch.empty_like(s) for s in src]
+
+    def step(i):
+        dst[i % 2].copy_(src[i % 2])
+
+    ms, _ = time_steps(step, steps, 3)
+    return 2 * n * 2 / (ms * 1e-3) / 1e9
+
+
+def cpu_baseline(seconds_budget: float = 15.0) -> dict:
+    """The CPU oracle on the first sequences of config 2 (bf16 inputs, fp32 math)."""
+    from mini_vllm.workloads import config_batch
+    from oracle.paged_attention import paged_attention as oracle_paged
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    full = config_batch(2, device="cpu")
+    n = 8
+    rows = torch.arange(n)
+    args = (full.q[rows], full.key_pool, full.value_pool, full.block_tables[:n],
+            torch.arange(n + 1, dtype=torch.int32), full.context_lens[:n], full.scale)
+    kv = 2 * sum(full.contexts[:n]) * 8 * 128 * 2
+    oracle_paged(*args)  # warmup
+    times = []
+    start = time.perf_counter()
+    while len(times) < 5 or (time.perf_counter() - start < seconds_budget and len(times) < 50):
+        t0 = time.perf_counter()
+        oracle_paged(*args)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": round(kv / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"config 2 sequences 0-{n - 1} (ctx {full.contexts[:n]}), oracle/paged_attention.py "
+                  f"gather-then-dense in fp32, median of {len(times)} runs, {med * 1e3:.1f} ms",
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--copies", type=int, default=3, help="rotated pool copies (defeat the MALL)")
+    parser.add_argument("--skip-extras", action="store_true")
+    parser.add_argument("--no-cpu", action="store_true")
+    args = parser.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build's hot path (paged attention) is a "
+              "single-GPU kernel and no multi-GPU figure is produced; run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+
+    from mini_vllm.kernels.extension import load_extension
+    from mini_vllm.workloads import prefill_flops
+
+    ext = load_extension()
+    log(f"library {ext.path}; device {torch.cuda.get_device_name(0)}")
+
+    log("config 2: building inputs")
+    batches = rotated_batches(2, args.copies)
+    b = batches[0]
+    kv_bytes = b.kv_bytes()
+    plan = ext.paged_attention_plan(b.q.shape[0], len(b.contexts), 16, 8, 128, 16, 1,
+                                    b.max_context_len, b.q.dtype, b.key_pool.dtype)
+    log(f"config 2: K+V {kv_bytes / 1e6:.1f} MB per step, plan {plan}")
+    ms, per_call = run_paged(batches, args.steps, args.warmup)
+    gbs = kv_bytes / (ms * 1e-3) / 1e9
+    log(f"config 2: {ms * 1e3:.1f} us/step, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of 8 TB/s)")
+
+    extras = {}
+    if not args.skip_extras:
+        del batches
+        torch.cuda.empty_cache()
+        log("config 3: building inputs")
+        pf = rotated_batches(3, 2)
+        flops = prefill_flops(pf[0])
+        pms, _ = run_paged(pf, max(10, args.steps // 2), 3)
+        tflops = flops / (pms * 1e-3) / 1e12
+        extras["config3_prefill"] = {
+            "ms_per_call": round(pms, 4), "gflop": round(flops / 1e9, 3),
+            "tflops": round(tflops, 2), "frac_of_bf16_mfma_peak": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4)}
+        log(f"config 3: {pms * 1e3:.1f} us, {tflops:.1f} TFLOP/s")
+        del pf
+        torch.cuda.empty_cache()
+        log("config 4: building inputs")
+        f8 = rotated_batches(4, 2)
+        f8_bytes = f8[0].kv_bytes() + f8[0].scale_bytes()
+        fms, _ = run_paged(f8, max(10, args.steps // 2), 3)
+        fgbs = f8_bytes / (fms * 1e-3) / 1e9
+        extras["config4_fp8_decode"] = {
+            "ms_per_call": round(fms, 4), "bytes": f8_bytes, "gbs": round(fgbs, 1),
+            "frac_of_hbm_peak": round(fgbs / HBM_PEAK_GBS, 4)}
+        log(f"config 4: {fms * 1e3:.1f} us, {fgbs:.0f} GB/s")
+        del f8
+        torch.cuda.empty_cache()
+        extras["copy_ceiling_gbs"] = round(copy_ceiling(1 << 30), 1)
+        log(f"copy_ ceiling {extras['copy_ceiling_gbs']} GB/s")
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (oracle on host cores)")
+        cpu = cpu_baseline()
+
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/K/V, shuffled block tables)",
+        "config": {
+            "workload": "BASELINE config 2: paged decode, batch 64, ctx U[512,4096] seed 0, "
+                        "GQA 16q/8kv, head_dim 128, 16-token pages",
+            "batch": len(b.contexts),
+            "total_context_tokens": sum(b.contexts),
+            "kv_bytes_per_step": kv_bytes,
+            "rotated_pool_copies": args.copies,
+            "split_plan": plan,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+        "extras": extras,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

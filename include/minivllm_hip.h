@@ -1,0 +1,133 @@
+/* C ABI of libminivllm_hip.so: the MI355X (gfx950) kernels of the Mini-vLLM
+ * paged-attention hot path.
+ *
+ * The reference exposes these ops as the pybind11 module `mini_vllm_C`
+ * (csrc/bindings.cpp:8-32,34-95), taking torch tensors. This library replaces that
+ * module behind the same Python seam (mini_vllm/kernels/ops.py) with plain pointers,
+ * sizes and an explicit stream, so any FFI can bind it.
+ *
+ * Conventions, all entry points:
+ *   - return 0 on success, non-zero on failure; mvllm_last_error() then describes the
+ *     failure (thread-local, valid until the next call on the same thread);
+ *   - the callee never allocates device memory: the caller passes the output and any
+ *     workspace (the reference allocates both with torch inside the call,
+ *     csrc/paged_attention.cu:515-521,678);
+ *   - work is enqueued on `stream` (a hipStream_t; NULL = the null stream) and the call
+ *     never synchronizes: results are ready when the stream reaches this point;
+ *   - tensors are dense and row-major (contiguous) in the shapes given per function;
+ *   - dtype codes: 0 = float32, 1 = float16, 2 = bfloat16, 3 = float8 e4m3fn (OCP).
+ */
+#ifndef MINIVLLM_HIP_H
+#define MINIVLLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MVLLM_DTYPE_F32 0
+#define MVLLM_DTYPE_F16 1
+#define MVLLM_DTYPE_BF16 2
+#define MVLLM_DTYPE_FP8_E4M3 3
+
+#define MVLLM_OK 0
+#define MVLLM_ERR_INVALID 1     /* an argument violates the contract */
+#define MVLLM_ERR_UNSUPPORTED 2 /* valid, but no kernel serves this shape/dtype */
+#define MVLLM_ERR_HIP 3         /* the HIP runtime reported an error */
+#define MVLLM_ERR_WORKSPACE 4   /* workspace smaller than the plan requires */
+
+/* Description of the most recent failure on this thread ("" if none). */
+const char* mvllm_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int mvllm_abi_version(void);
+
+/* How one paged_attention call will be executed. Filled by mvllm_paged_attention_plan;
+ * the caller allocates `workspace_bytes` of device memory (256-byte aligned) and passes
+ * it to mvllm_paged_attention with the same arguments. */
+typedef struct mvllm_paged_plan {
+  int32_t split_tokens;     /* decode: keys per split (0 when nothing is split) */
+  int32_t max_splits;       /* decode: split-axis grid extent */
+  int32_t decode_by_row;    /* 1: the decode kernel serves every query row, prefill rows
+                               included (no MFMA prefill kernel for this shape/dtype) */
+  int32_t prefill_mfma;     /* 1: prefill rows go to the MFMA prefill kernel */
+  uint64_t workspace_bytes; /* split partials; 0 when no split is needed */
+} mvllm_paged_plan;
+
+/* Plan a paged_attention call. Depends only on the host-side sizes below (never on
+ * device data), so it is free to call every iteration. Replaces the grid/split
+ * selection of the reference's launch_paged_attention / splits_for
+ * (csrc/paged_attention.cu:477-521). */
+int mvllm_paged_attention_plan(int32_t num_tokens, int32_t num_seqs, int32_t num_q_heads,
+                               int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                               int32_t max_query_len, int32_t max_context_len, int32_t q_dtype,
+                               int32_t kv_dtype, mvllm_paged_plan* plan);
+
+/* Ragged attention over a paged KV cache: every scheduled token of every sequence in
+ * one call. Replaces `mini_vllm_C.paged_attention` (csrc/bindings.cpp:23-32,81-94 ->
+ * csrc/paged_attention.cu:598-711), called from mini_vllm/kernels/ops.py:239-250.
+ *
+ *   out, q        [num_tokens, num_q_heads, head_dim]           q_dtype
+ *   key_pool,
+ *   value_pool    [num_blocks, block_size, num_kv_heads, head_dim] kv_dtype
+ *   k_scales,
+ *   v_scales      [num_blocks, num_kv_heads] float32, required iff kv_dtype is fp8
+ *                 (element = stored value * scale of its (page, kv head)); else NULL
+ *   block_tables  [num_seqs, max_blocks_per_seq] int32, -1 padded
+ *   cu_seqlens_q  [num_seqs + 1] int32   query rows of sequence s: [cu[s], cu[s+1])
+ *   context_lens  [num_seqs] int32       keys sequence s attends over (S)
+ *   seq_lens      [num_seqs] int32       query tokens of sequence s (L); L == 1 decodes
+ *
+ * Query r (0-based) of a sequence sees keys 0 .. S - L + r (causal with offset S - L).
+ * max_query_len / max_context_len are host-side bounds over the batch (they size the
+ * grid; no device read). scale multiplies q.k (the reference default is 1/sqrt(D)).
+ * head_dim in {32, 64, 128, 256}; block_size a power of two; num_q_heads a multiple
+ * of num_kv_heads; q_dtype in {f32, f16, bf16}; kv_dtype equals q_dtype, or is fp8
+ * (with any q_dtype). */
+int mvllm_paged_attention(void* out, const void* q, const void* key_pool,
+                          const void* value_pool, const float* k_scales, const float* v_scales,
+                          const int32_t* block_tables, const int32_t* cu_seqlens_q,
+                          const int32_t* context_lens, const int32_t* seq_lens,
+                          int32_t num_tokens, int32_t num_seqs, int32_t num_q_heads,
+                          int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                          int64_t num_blocks, int32_t max_blocks_per_seq, int32_t max_query_len,
+                          int32_t max_context_len, float scale, int32_t q_dtype,
+                          int32_t kv_dtype, void* workspace, uint64_t workspace_bytes,
+                          void* stream);
+
+/* RMSNorm over the last dimension: out = T(w * T(x * rsqrt(mean(x^2) + eps))), the sum
+ * of squares in fp32. x, out [rows, dim]; weight [dim]; all of `dtype` (f32/f16/bf16).
+ * Replaces `mini_vllm_C.rmsnorm` (csrc/bindings.cpp:9,44-49 -> csrc/rmsnorm.cu:121-169),
+ * called from mini_vllm/kernels/ops.py:129-130; also serves QK-norm with dim = D. */
+int mvllm_rmsnorm(void* out, const void* x, const void* weight, int64_t rows, int64_t dim,
+                  float eps, int32_t dtype, void* stream);
+
+/* Rotate-halves RoPE at explicit positions. x, out [rows, head_dim] where rows =
+ * tokens * heads (token-major, heads inner); positions [num_positions] of
+ * positions_bytes = 4 (int32) or 8 (int64), token t uses positions[t % num_positions];
+ * cos_table, sin_table [max_positions, head_dim] float32. A position outside
+ * [0, max_positions) yields NaN for that token instead of an out-of-bounds read.
+ * Replaces `mini_vllm_C.rope` (csrc/bindings.cpp:10-13,51-57 -> csrc/rope.cu:115-195),
+ * called from mini_vllm/kernels/ops.py:147-148. */
+int mvllm_rope(void* out, const void* x, const void* positions, int32_t positions_bytes,
+               const float* cos_table, const float* sin_table, int64_t rows, int64_t heads,
+               int64_t head_dim, int64_t num_positions, int64_t max_positions, int32_t dtype,
+               void* stream);
+
+/* out = T(T(g * T(sigmoid(g))) * u) elementwise over n elements of `dtype`.
+ * Replaces `mini_vllm_C.swiglu` (csrc/bindings.cpp:14,59-63 -> csrc/swiglu.cu:87-120),
+ * called from mini_vllm/kernels/ops.py:161-162. */
+int mvllm_swiglu(void* out, const void* gate, const void* up, int64_t n, int32_t dtype,
+                 void* stream);
+
+/* y = a * x + b over n floats: the toolchain smoke test, replacing `mini_vllm_C.hello`
+ * (csrc/bindings.cpp:8,37-42 -> csrc/hello.cu:11-21; mini_vllm/kernels/extension.py:349-353). */
+int mvllm_axpby(float* y, const float* x, float a, float b, int64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MINIVLLM_HIP_H */

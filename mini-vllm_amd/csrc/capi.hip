@@ -1,0 +1,343 @@
+// The C ABI (include/minivllm_hip.h): argument validation, planning and launch.
+//
+// Validation mirrors the refusals of the reference's host entry points
+// (csrc/paged_attention.cu:608-676, rmsnorm.cu:122-144, rope.cu:119-176,
+// swiglu.cu:88-102) for everything expressible without torch tensors; the Python
+// seam checks devices, dtypes and contiguity of the tensors before calling in.
+
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <atomic>
+#include <cstdarg>
+
+#include "../../include/minivllm_hip.h"
+#include "common.hpp"
+#include "elementwise.hpp"
+#include "paged_attention.hpp"
+
+namespace {
+
+thread_local char g_error[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list args;
+  va_start(args, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, args);
+  va_end(args);
+  return code;
+}
+
+int hip_status(hipError_t err, const char* what) {
+  if (err == hipSuccess) return MVLLM_OK;
+  return fail(MVLLM_ERR_HIP, "%s: HIP error %d (%s)", what, static_cast<int>(err),
+              hipGetErrorString(err));
+}
+
+bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+
+// Compute units of the current device, cached per device id.
+int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int cached = cache[dev].load(std::memory_order_relaxed);
+  if (cached > 0) return cached;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0) {
+    cus = 256;
+  }
+  cache[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
+
+int env_int(const char* name, int fallback) {
+  const char* v = getenv(name);
+  if (v == nullptr || *v == '\0') return fallback;
+  return atoi(v);
+}
+
+int check_paged_shape(int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk, int32_t d,
+                      int32_t block_size, int32_t max_q, int32_t max_ctx, int32_t q_dtype,
+                      int32_t kv_dtype) {
+  if (num_tokens < 0 || num_seqs < 0) {
+    return fail(MVLLM_ERR_INVALID, "paged_attention: negative token or sequence count");
+  }
+  if (q_dtype != mvllm::kF32 && q_dtype != mvllm::kF16 && q_dtype != mvllm::kBF16) {
+    return fail(MVLLM_ERR_INVALID,
+                "paged_attention: q dtype code %d is not supported (float32, float16 and "
+                "bfloat16 are; float64 is not supported, the accumulators here are fp32)",
+                q_dtype);
+  }
+  if (kv_dtype != q_dtype && kv_dtype != mvllm::kFP8E4M3) {
+    return fail(MVLLM_ERR_INVALID,
+                "paged_attention: q and the pools must share a dtype (or the pools be "
+                "float8_e4m3fn), got codes %d and %d",
+                q_dtype, kv_dtype);
+  }
+  if (d != 32 && d != 64 && d != 128 && d != 256) {
+    return fail(MVLLM_ERR_UNSUPPORTED,
+                "paged_attention: head dim %d is not supported; this build serves 32, 64, "
+                "128 and 256",
+                d);
+  }
+  if (hk <= 0 || hq <= 0 || hq % hk != 0) {
+    return fail(MVLLM_ERR_INVALID, "paged_attention: H_q (%d) must be a multiple of H_k (%d)",
+                hq, hk);
+  }
+  if (!is_pow2(block_size)) {
+    return fail(MVLLM_ERR_INVALID,
+                "paged_attention: the block size must be a power of two, got %d", block_size);
+  }
+  if (max_q < 1) {
+    return fail(MVLLM_ERR_INVALID, "paged_attention: max_query_len must be >= 1, got %d", max_q);
+  }
+  if (max_ctx < max_q) {
+    return fail(MVLLM_ERR_INVALID,
+                "paged_attention: max_context_len (%d) must be at least max_query_len (%d); a "
+                "pass cannot compute more tokens than it may attend over",
+                max_ctx, max_q);
+  }
+  return MVLLM_OK;
+}
+
+int decode_group_chunk(int group) { return group % 4 == 0 ? 4 : (group % 2 == 0 ? 2 : 1); }
+
+void make_plan(int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk, int32_t d,
+               int32_t block_size, int32_t max_q, int32_t max_ctx, int32_t q_dtype,
+               int32_t kv_dtype, mvllm_paged_plan* plan) {
+  const bool has_prefill = max_q > 1;
+  const bool mfma =
+      has_prefill && mvllm::paged_prefill_supported(q_dtype, kv_dtype, d, hq, hk, block_size);
+  plan->prefill_mfma = mfma ? 1 : 0;
+  plan->decode_by_row = (has_prefill && !mfma) ? 1 : 0;
+
+  // Enough (row, kv head, head chunk) waves to keep every CU streaming: split each
+  // row's context until the grid holds ~16 waves per CU, in splits of 64..1024 keys.
+  const int64_t rows = plan->decode_by_row ? num_tokens : num_seqs;
+  const int64_t waves_per_row = static_cast<int64_t>(hk) * (hq / hk / decode_group_chunk(hq / hk));
+  const int64_t target = static_cast<int64_t>(env_int("MVLLM_DECODE_WAVES_PER_CU", 16)) * device_cus();
+  const int64_t single = rows * waves_per_row > 0 ? rows * waves_per_row : 1;
+  const int64_t wanted = (target + single - 1) / single;
+  int64_t split = (max_ctx + wanted - 1) / wanted;
+  split = (split + 63) / 64 * 64;
+  const int override_split = env_int("MVLLM_DECODE_SPLIT_TOKENS", 0);
+  if (override_split > 0) split = (override_split + 15) / 16 * 16;
+  if (split < 64) split = 64;
+  if (split > mvllm::kMaxSplitTokens) split = mvllm::kMaxSplitTokens;
+  const int64_t max_splits = (max_ctx + split - 1) / split;
+  plan->split_tokens = static_cast<int32_t>(split);
+  plan->max_splits = static_cast<int32_t>(max_splits < 1 ? 1 : max_splits);
+  plan->workspace_bytes = 0;
+  if (plan->max_splits > 1 && rows > 0) {
+    const uint64_t entries = static_cast<uint64_t>(rows) * hq * plan->max_splits;
+    const uint64_t o_bytes = (entries * d * sizeof(float) + 255) / 256 * 256;
+    plan->workspace_bytes = o_bytes + entries * 2 * sizeof(float);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mvllm_last_error(void) { return g_error; }
+
+int mvllm_abi_version(void) { return 1; }
+
+int mvllm_paged_attention_plan(int32_t num_tokens, int32_t num_seqs, int32_t num_q_heads,
+                               int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                               int32_t max_query_len, int32_t max_context_len, int32_t q_dtype,
+                               int32_t kv_dtype, mvllm_paged_plan* plan) {
+  g_error[0] = '\0';
+  if (plan == nullptr) return fail(MVLLM_ERR_INVALID, "paged_attention_plan: plan is NULL");
+  const int rc = check_paged_shape(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                                   block_size, max_query_len, max_context_len, q_dtype, kv_dtype);
+  if (rc != MVLLM_OK) return rc;
+  make_plan(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_query_len,
+            max_context_len, q_dtype, kv_dtype, plan);
+  return MVLLM_OK;
+}
+
+int mvllm_paged_attention(void* out, const void* q, const void* key_pool,
+                          const void* value_pool, const float* k_scales, const float* v_scales,
+                          const int32_t* block_tables, const int32_t* cu_seqlens_q,
+                          const int32_t* context_lens, const int32_t* seq_lens,
+                          int32_t num_tokens, int32_t num_seqs, int32_t num_q_heads,
+                          int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                          int64_t num_blocks, int32_t max_blocks_per_seq, int32_t max_query_len,
+                          int32_t max_context_len, float scale, int32_t q_dtype,
+                          int32_t kv_dtype, void* workspace, uint64_t workspace_bytes,
+                          void* stream) {
+  g_error[0] = '\0';
+  int rc = check_paged_shape(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                             block_size, max_query_len, max_context_len, q_dtype, kv_dtype);
+  if (rc != MVLLM_OK) return rc;
+  if (num_tokens == 0 || num_seqs == 0) return MVLLM_OK;
+  if (out == nullptr || q == nullptr || key_pool == nullptr || value_pool == nullptr ||
+      block_tables == nullptr || cu_seqlens_q == nullptr || context_lens == nullptr ||
+      seq_lens == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "paged_attention: a required pointer is NULL");
+  }
+  if (num_blocks <= 0 || max_blocks_per_seq <= 0) {
+    return fail(MVLLM_ERR_INVALID, "paged_attention: empty pool or block table");
+  }
+  const bool fp8 = kv_dtype == mvllm::kFP8E4M3;
+  if (fp8 != (k_scales != nullptr && v_scales != nullptr) || (!fp8 && (k_scales || v_scales))) {
+    return fail(MVLLM_ERR_INVALID,
+                "paged_attention: k_scales and v_scales are required for a float8 pool and "
+                "only for one");
+  }
+  mvllm_paged_plan plan;
+  make_plan(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_query_len,
+            max_context_len, q_dtype, kv_dtype, &plan);
+  if (plan.workspace_bytes > 0 && (workspace == nullptr || workspace_bytes < plan.workspace_bytes)) {
+    return fail(MVLLM_ERR_WORKSPACE,
+                "paged_attention: workspace of %llu bytes is smaller than the %llu the plan "
+                "needs (call mvllm_paged_attention_plan)",
+                static_cast<unsigned long long>(workspace_bytes),
+                static_cast<unsigned long long>(plan.workspace_bytes));
+  }
+
+  int shift = 0;
+  while ((1 << shift) < block_size) ++shift;
+
+  mvllm::PagedParams p{};
+  p.q = q;
+  p.k_pool = key_pool;
+  p.v_pool = value_pool;
+  p.k_scales = k_scales;
+  p.v_scales = v_scales;
+  p.out = out;
+  p.block_tables = block_tables;
+  p.cu_seqlens_q = cu_seqlens_q;
+  p.context_lens = context_lens;
+  p.seq_lens = seq_lens;
+  p.num_seqs = num_seqs;
+  p.num_tokens = num_tokens;
+  p.hq = num_q_heads;
+  p.hk = num_kv_heads;
+  p.max_blocks = max_blocks_per_seq;
+  p.block_shift = shift;
+  p.block_mask = block_size - 1;
+  p.split_tokens = plan.split_tokens;
+  p.max_splits = plan.max_splits;
+  p.by_row = plan.decode_by_row;
+  p.scale = scale;
+  if (plan.workspace_bytes > 0) {
+    const uint64_t entries = static_cast<uint64_t>(plan.decode_by_row ? num_tokens : num_seqs) *
+                             num_q_heads * plan.max_splits;
+    const uint64_t o_bytes = (entries * head_dim * sizeof(float) + 255) / 256 * 256;
+    p.part_o = static_cast<float*>(workspace);
+    p.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + o_bytes);
+  }
+
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  // Every query length is at most max_query_len and they sum to num_tokens, so when
+  // num_tokens == num_seqs * max_query_len every sequence is a prefill chunk (if
+  // max_query_len > 1) and no decode row exists: skip that launch.
+  const bool all_prefill =
+      max_query_len > 1 && static_cast<int64_t>(num_seqs) * max_query_len == num_tokens;
+  if (plan.decode_by_row || !all_prefill) {
+    rc = hip_status(mvllm::launch_paged_decode(p, q_dtype, kv_dtype, head_dim, s),
+                    "paged_attention: decode launch");
+    if (rc != MVLLM_OK) return rc;
+  }
+  if (plan.prefill_mfma) {
+    rc = hip_status(mvllm::launch_paged_prefill(p, q_dtype, kv_dtype, head_dim, max_query_len, s),
+                    "paged_attention: prefill launch");
+    if (rc != MVLLM_OK) return rc;
+  }
+  return MVLLM_OK;
+}
+
+int mvllm_rmsnorm(void* out, const void* x, const void* weight, int64_t rows, int64_t dim,
+                  float eps, int32_t dtype, void* stream) {
+  g_error[0] = '\0';
+  if (dtype != mvllm::kF32 && dtype != mvllm::kF16 && dtype != mvllm::kBF16) {
+    return fail(MVLLM_ERR_INVALID,
+                "rmsnorm: dtype code %d is not supported; float64 is not supported, this kernel "
+                "accumulates in fp32",
+                dtype);
+  }
+  if (rows < 0 || dim < 0 || dim > (1 << 30)) return fail(MVLLM_ERR_INVALID, "rmsnorm: bad shape");
+  if (rows == 0 || dim == 0) return MVLLM_OK;
+  if (out == nullptr || x == nullptr || weight == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "rmsnorm: a required pointer is NULL");
+  }
+  return hip_status(mvllm::launch_rmsnorm(x, weight, out, rows, static_cast<int>(dim), eps, dtype,
+                                          static_cast<hipStream_t>(stream)),
+                    "rmsnorm: launch");
+}
+
+int mvllm_rope(void* out, const void* x, const void* positions, int32_t positions_bytes,
+               const float* cos_table, const float* sin_table, int64_t rows, int64_t heads,
+               int64_t head_dim, int64_t num_positions, int64_t max_positions, int32_t dtype,
+               void* stream) {
+  g_error[0] = '\0';
+  if (dtype != mvllm::kF32 && dtype != mvllm::kF16 && dtype != mvllm::kBF16) {
+    return fail(MVLLM_ERR_INVALID,
+                "rope: dtype code %d is not supported; float64 is not supported, this kernel "
+                "computes the rotation in fp32",
+                dtype);
+  }
+  if (head_dim <= 0 || head_dim % 2 != 0 || head_dim > (1 << 20)) {
+    return fail(MVLLM_ERR_INVALID, "rope: the head dimension must be even, got %lld",
+                static_cast<long long>(head_dim));
+  }
+  if (positions_bytes != 4 && positions_bytes != 8) {
+    return fail(MVLLM_ERR_INVALID, "rope: positions must be int32 or int64");
+  }
+  if (rows < 0 || heads <= 0 || rows % heads != 0) {
+    return fail(MVLLM_ERR_INVALID, "rope: rows (%lld) must be tokens x heads (%lld)",
+                static_cast<long long>(rows), static_cast<long long>(heads));
+  }
+  if (rows == 0) return MVLLM_OK;
+  if (num_positions <= 0) return fail(MVLLM_ERR_INVALID, "rope: positions is empty");
+  if ((rows / heads) % num_positions != 0) {
+    return fail(MVLLM_ERR_INVALID,
+                "rope: x holds %lld tokens, which is not a multiple of the %lld positions given, "
+                "so the positions cannot broadcast over it",
+                static_cast<long long>(rows / heads), static_cast<long long>(num_positions));
+  }
+  if (max_positions <= 0) return fail(MVLLM_ERR_INVALID, "rope: empty cos/sin tables");
+  if (out == nullptr || x == nullptr || positions == nullptr || cos_table == nullptr ||
+      sin_table == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "rope: a required pointer is NULL");
+  }
+  return hip_status(mvllm::launch_rope(x, positions, positions_bytes, cos_table, sin_table, out,
+                                       rows, heads, static_cast<int>(head_dim), num_positions,
+                                       max_positions, dtype, static_cast<hipStream_t>(stream)),
+                    "rope: launch");
+}
+
+int mvllm_swiglu(void* out, const void* gate, const void* up, int64_t n, int32_t dtype,
+                 void* stream) {
+  g_error[0] = '\0';
+  if (dtype != mvllm::kF32 && dtype != mvllm::kF16 && dtype != mvllm::kBF16) {
+    return fail(MVLLM_ERR_INVALID,
+                "swiglu: dtype code %d is not supported; float64 is not supported, this kernel "
+                "evaluates the sigmoid in fp32",
+                dtype);
+  }
+  if (n < 0) return fail(MVLLM_ERR_INVALID, "swiglu: negative size");
+  if (n == 0) return MVLLM_OK;
+  if (out == nullptr || gate == nullptr || up == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "swiglu: a required pointer is NULL");
+  }
+  return hip_status(
+      mvllm::launch_swiglu(gate, up, out, n, dtype, static_cast<hipStream_t>(stream)),
+      "swiglu: launch");
+}
+
+int mvllm_axpby(float* y, const float* x, float a, float b, int64_t n, void* stream) {
+  g_error[0] = '\0';
+  if (n < 0) return fail(MVLLM_ERR_INVALID, "axpby: negative size");
+  if (n == 0) return MVLLM_OK;
+  if (x == nullptr || y == nullptr) return fail(MVLLM_ERR_INVALID, "axpby: NULL pointer");
+  return hip_status(mvllm::launch_axpby(x, y, a, b, n, static_cast<hipStream_t>(stream)),
+                    "axpby: launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,209 @@
+// Wave64 building blocks shared by every kernel in this library.
+//
+// CDNA4 (gfx950) executes 64-lane wavefronts. Everything here is written for that
+// width: a 16-byte load per lane is the unit of global traffic, and cross-lane
+// reductions inside a 16-lane DPP row are single VALU instructions with a DPP
+// modifier (quad_perm / row_half_mirror / row_mirror), so a 16-lane all-reduce costs
+// four instructions and touches no LDS.
+//
+// Replaces the warp32 helpers of the reference's csrc/kernel_utils.cuh:14-133
+// (warp_reduce_sum/max, block_reduce_*, Vector<T>); the reduction structure is
+// different by design, not translated.
+
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mvllm {
+
+constexpr int kWave = 64;
+
+// Storage type codes shared with the C ABI (include/minivllm_hip.h).
+enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2, kFP8E4M3 = 3 };
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ------------------------------------------------------------------ conversions
+
+struct bf16_t { uint16_t bits; };
+struct f16_t { uint16_t bits; };
+struct fp8_t { uint8_t bits; };
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Round-to-nearest-even fp32 -> bf16, NaN kept quiet. This is the rounding torch's
+// `.to(torch.bfloat16)` performs, which is what parity with the oracle requires.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  _Float16 v;
+  const uint16_t b = static_cast<uint16_t>(h);
+  __builtin_memcpy(&v, &b, 2);
+  return static_cast<float>(v);
+}
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  const _Float16 v = static_cast<_Float16>(f);  // v_cvt_f16_f32, round to nearest even
+  uint16_t b;
+  __builtin_memcpy(&b, &v, 2);
+  return b;
+}
+
+// OCP fp8 e4m3fn (max 448, no infinities) -> fp32, exactly, by placing the 7
+// magnitude bits at the top of an fp32 mantissa/exponent and rescaling by 2^120
+// (the bias difference 127 - 7). Subnormal e4m3 inputs land on fp32 denormals,
+// which HIP keeps by default, so the multiply is exact for every finite code.
+__device__ __forceinline__ float fp8e4m3_to_f32(uint32_t byte) {
+  const float mag = __uint_as_float((byte & 0x7fu) << 20) * 0x1p120f;
+  return (byte & 0x80u) ? -mag : mag;
+}
+
+// Element access for the generic templates: load one element as float.
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static constexpr int kBytes = 4;
+  __device__ static float load(const void* p, int64_t i) { return static_cast<const float*>(p)[i]; }
+  __device__ static void store(void* p, int64_t i, float v) { static_cast<float*>(p)[i] = v; }
+  __device__ static float round(float v) { return v; }
+};
+template <> struct Elem<bf16_t> {
+  static constexpr int kBytes = 2;
+  __device__ static float load(const void* p, int64_t i) {
+    return __uint_as_float(static_cast<uint32_t>(static_cast<const uint16_t*>(p)[i]) << 16);
+  }
+  __device__ static void store(void* p, int64_t i, float v) {
+    static_cast<uint16_t*>(p)[i] = static_cast<uint16_t>(f32_to_bf16_bits(v));
+  }
+  __device__ static float round(float v) { return __uint_as_float(f32_to_bf16_bits(v) << 16); }
+};
+template <> struct Elem<f16_t> {
+  static constexpr int kBytes = 2;
+  __device__ static float load(const void* p, int64_t i) {
+    return f16_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+  }
+  __device__ static void store(void* p, int64_t i, float v) {
+    static_cast<uint16_t*>(p)[i] = static_cast<uint16_t>(f32_to_f16_bits(v));
+  }
+  __device__ static float round(float v) { return f16_bits_to_f32(f32_to_f16_bits(v)); }
+};
+template <> struct Elem<fp8_t> {
+  static constexpr int kBytes = 1;
+  __device__ static float load(const void* p, int64_t i) {
+    return fp8e4m3_to_f32(static_cast<const uint8_t*>(p)[i]);
+  }
+};
+
+// Unpack a 16-byte chunk (four dwords) into N = 16 / sizeof(T) floats.
+template <typename T> struct Chunk;
+template <> struct Chunk<float> {
+  static constexpr int kN = 4;
+  __device__ static void unpack(const u32x4& w, float* out) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = __uint_as_float(w[i]);
+  }
+};
+template <> struct Chunk<bf16_t> {
+  static constexpr int kN = 8;
+  __device__ static void unpack(const u32x4& w, float* out) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = bf16_lo(w[i]);
+      out[2 * i + 1] = bf16_hi(w[i]);
+    }
+  }
+};
+template <> struct Chunk<f16_t> {
+  static constexpr int kN = 8;
+  __device__ static void unpack(const u32x4& w, float* out) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = f16_bits_to_f32(w[i] & 0xffffu);
+      out[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+    }
+  }
+};
+template <> struct Chunk<fp8_t> {
+  static constexpr int kN = 16;
+  __device__ static void unpack(const u32x4& w, float* out) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b) out[4 * i + b] = fp8e4m3_to_f32((w[i] >> (8 * b)) & 0xffu);
+    }
+  }
+};
+
+// 16-byte global load / store through the vector memory path.
+__device__ __forceinline__ u32x4 load16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void store16(void* p, const u32x4& v) {
+  *reinterpret_cast<u32x4*>(p) = v;
+}
+
+// ------------------------------------------------------------------- reductions
+
+// DPP control codes (GFX9 encoding).
+constexpr int kDppQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+
+// All-reduce over aligned groups of `kWidth` lanes (kWidth in {1,2,4,8,16,32,64}).
+// Widths up to 16 stay inside a DPP row: quad xor-1, quad xor-2, half-row mirror and
+// row mirror each pair every lane with a distinct partner of the same group, so
+// after log2(kWidth) steps every lane of the group holds the group's total. Wider
+// groups finish with ds_swizzle-free xor shuffles across rows.
+template <int kWidth>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (kWidth >= 2) v += dpp<kDppQuadXor1>(v);
+  if constexpr (kWidth >= 4) v += dpp<kDppQuadXor2>(v);
+  if constexpr (kWidth >= 8) v += dpp<kDppRowHalfMirror>(v);
+  if constexpr (kWidth >= 16) v += dpp<kDppRowMirror>(v);
+  if constexpr (kWidth >= 32) v += __shfl_xor(v, 16, 64);
+  if constexpr (kWidth >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+template <int kWidth>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (kWidth >= 2) v = fmaxf(v, dpp<kDppQuadXor1>(v));
+  if constexpr (kWidth >= 4) v = fmaxf(v, dpp<kDppQuadXor2>(v));
+  if constexpr (kWidth >= 8) v = fmaxf(v, dpp<kDppRowHalfMirror>(v));
+  if constexpr (kWidth >= 16) v = fmaxf(v, dpp<kDppRowMirror>(v));
+  if constexpr (kWidth >= 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
+  if constexpr (kWidth >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+__device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
+
+// Sum over a workgroup of `kWaves` waves, through `kWaves` floats of LDS. Every
+// thread of the workgroup must call it.
+template <int kWaves>
+__device__ __forceinline__ float block_sum(float v, float* lds) {
+  v = wave_sum(v);
+  const int wave = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) lds[wave] = v;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) total += lds[w];
+  return total;
+}
+
+}  // namespace mvllm

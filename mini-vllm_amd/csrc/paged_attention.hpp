@@ -1,0 +1,68 @@
+// Internal launch interface of the paged-attention kernels (not part of the C ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mvllm {
+
+// Largest number of physical pages one decode split may span and still have its page
+// ids staged in LDS (4 KiB). The planner keeps splits at or below 1024 tokens, which is
+// at most 1025 pages even at a page size of 1; a caller that understates
+// max_context_len gets longer splits, which then read the table from global memory.
+constexpr int kMaxSplitPages = 1040;
+constexpr int kMaxSplitTokens = 1024;
+
+struct PagedParams {
+  const void* q;
+  const void* k_pool;
+  const void* v_pool;
+  const float* k_scales;  // [num_blocks, H_k], fp8 pools only
+  const float* v_scales;
+  void* out;
+  const int32_t* block_tables;
+  const int32_t* cu_seqlens_q;
+  const int32_t* context_lens;
+  const int32_t* seq_lens;
+  int num_seqs;
+  int num_tokens;
+  int hq;
+  int hk;
+  int max_blocks;
+  int block_shift;
+  int block_mask;
+  int split_tokens;   // decode: nominal keys per split
+  int max_splits;     // decode: grid extent along the split axis
+  int by_row;         // decode: 1 = one unit per query row (serves prefill rows too)
+  float scale;
+  float* part_o;      // [units, H_q, max_splits, D] fp32
+  float* part_ml;     // [units, H_q, max_splits, 2] fp32 (running max in log2 units, sum)
+};
+
+// Splits of one row: as many as its visible context needs at `split_tokens` keys
+// each, never more than the grid provides. Shared by the decode kernel, the merge
+// kernel and the host planner so that all three agree.
+__host__ __device__ inline int decode_num_splits(int visible, int split_tokens, int max_splits) {
+  int n = (visible + split_tokens - 1) / split_tokens;
+  n = n < max_splits ? n : max_splits;
+  return n < 1 ? 1 : n;
+}
+
+// Balanced split length: visible / n rounded up to a multiple of 16 keys.
+__host__ __device__ inline int decode_split_len(int visible, int nsplit) {
+  const int per = (visible + nsplit - 1) / nsplit;
+  return (per + 15) & ~15;
+}
+
+hipError_t launch_paged_decode(const PagedParams& p, int q_dtype, int kv_dtype, int head_dim,
+                               hipStream_t stream);
+
+hipError_t launch_paged_prefill(const PagedParams& p, int q_dtype, int kv_dtype, int head_dim,
+                                int max_query_len, hipStream_t stream);
+
+// Whether launch_paged_prefill has a kernel for this shape; if not, prefill rows are
+// served by the decode kernel in by-row mode.
+bool paged_prefill_supported(int q_dtype, int kv_dtype, int head_dim, int hq, int hk,
+                             int block_size);
+
+}  // namespace mvllm

@@ -1,0 +1,650 @@
+"""Build and load the MI355X kernel library, and bind it as the reference's extension.
+
+The reference JIT-compiles ``csrc/*.cu`` into a pybind11 module ``mini_vllm_C`` with
+``torch.utils.cpp_extension`` for sm_120 (mini_vllm/kernels/extension.py:266-298) and
+calls it with torch tensors. Here the kernels are HIP for gfx950 behind a plain C ABI
+(``include/minivllm_hip.h``), built with ``hipcc`` into ``libminivllm_hip.so`` and bound
+with :mod:`ctypes`. :func:`load_extension` returns an object exposing the reference
+module's functions -- ``paged_attention``, ``rmsnorm``, ``rope``, ``swiglu``, ``hello``
+-- with the same arguments and refusal messages, so ``ops.py`` and every caller above
+it are unchanged.
+
+Ownership follows the reference: each call returns a freshly allocated output tensor
+(torch's caching allocator), and the split-K workspace of ``paged_attention`` is also
+a torch allocation made here, so the library itself never allocates device memory.
+Work goes on torch's current stream and nothing synchronizes.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import subprocess
+import sys
+import threading
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+from typing import Any
+
+import torch
+
+PACKAGE_ROOT = Path(__file__).resolve().parents[2]  # .../mini-vllm_amd
+CSRC_DIR = PACKAGE_ROOT / "csrc"
+BUILD_DIR = PACKAGE_ROOT / "_build"
+LIB_DIR = PACKAGE_ROOT / "lib"
+LIB_PATH = LIB_DIR / "libminivllm_hip.so"
+REPO_ROOT = PACKAGE_ROOT.parent
+INCLUDE_DIR = REPO_ROOT / "include"
+
+ARCH = "gfx950"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+# Packed fp32 VALU ops are disabled for every kernel: the compiler emits them from
+# ordinary float code otherwise.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+]
+
+ABI_VERSION = 1
+
+DTYPE_CODES: dict[torch.dtype, int] = {
+    torch.float32: 0,
+    torch.float16: 1,
+    torch.bfloat16: 2,
+    torch.float8_e4m3fn: 3,
+}
+
+_lock = threading.Lock()
+_extension: "HipExtension | None" = None
+
+
+class ToolchainError(RuntimeError):
+    """Raised when the library cannot be built or loaded."""
+
+
+# ----------------------------------------------------------------------- build
+
+
+def sources() -> list[Path]:
+    found = sorted(CSRC_DIR.glob("*.hip"))
+    if not found:
+        raise ToolchainError(f"no HIP sources found in {CSRC_DIR}")
+    return found
+
+
+def build_library(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every ``csrc/*.hip`` for gfx950 and link ``lib/libminivllm_hip.so``.
+
+    Always compiles (this is the "does it build" check); objects go to ``_build/``
+    and the library is replaced atomically so a running process never maps a
+    half-written file.
+    """
+    if not Path(HIPCC).exists():
+        raise ToolchainError(f"hipcc not found at {HIPCC}")
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+
+    def compile_one(src: Path) -> Path:
+        obj = BUILD_DIR / (src.stem + ".o")
+        cmd = [HIPCC, *HIP_FLAGS, f"-I{INCLUDE_DIR}", "-c", str(src), "-o", str(obj)]
+        result = subprocess.run(cmd, capture_output=True, text=True)
+        noise = "'-packed-fp32-ops' is not a recognized feature"
+        log = "\n".join(l for l in (result.stderr + result.stdout).splitlines() if noise not in l)
+        if result.returncode != 0:
+            raise ToolchainError(f"hipcc failed on {src.name}:\n{log}")
+        if verbose and log.strip():
+            print(log, file=sys.stderr)
+        return obj
+
+    workers = jobs or min(8, os.cpu_count() or 4)
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        objects = list(pool.map(compile_one, sources()))
+
+    tmp = LIB_PATH.with_suffix(f".so.tmp{os.getpid()}")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise ToolchainError(f"link failed:\n{result.stderr}{result.stdout}")
+    os.replace(tmp, LIB_PATH)
+    if verbose:
+        print(f"built {LIB_PATH}", file=sys.stderr)
+    return LIB_PATH
+
+
+# ------------------------------------------------------------------- bindings
+
+
+class _Plan(ctypes.Structure):
+    _fields_ = [
+        ("split_tokens", ctypes.c_int32),
+        ("max_splits", ctypes.c_int32),
+        ("decode_by_row", ctypes.c_int32),
+        ("prefill_mfma", ctypes.c_int32),
+        ("workspace_bytes", ctypes.c_uint64),
+    ]
+
+
+def _bind(lib: ctypes.CDLL) -> None:
+    p, i32, i64, u64, f32 = (
+        ctypes.c_void_p,
+        ctypes.c_int32,
+        ctypes.c_int64,
+        ctypes.c_uint64,
+        ctypes.c_float,
+    )
+    lib.mvllm_last_error.restype = ctypes.c_char_p
+    lib.mvllm_last_error.argtypes = []
+    lib.mvllm_abi_version.restype = ctypes.c_int
+    lib.mvllm_abi_version.argtypes = []
+    lib.mvllm_paged_attention_plan.restype = ctypes.c_int
+    lib.mvllm_paged_attention_plan.argtypes = [i32] * 10 + [ctypes.POINTER(_Plan)]
+    lib.mvllm_paged_attention.restype = ctypes.c_int
+    lib.mvllm_paged_attention.argtypes = (
+        [p] * 10 + [i32] * 6 + [i64, i32, i32, i32, f32, i32, i32, p, u64, p]
+    )
+    lib.mvllm_rmsnorm.restype = ctypes.c_int
+    lib.mvllm_rmsnorm.argtypes = [p, p, p, i64, i64, f32, i32, p]
+    lib.mvllm_rope.restype = ctypes.c_int
+    lib.mvllm_rope.argtypes = [p, p, p, i32, p, p, i64, i64, i64, i64, i64, i32, p]
+    lib.mvllm_swiglu.restype = ctypes.c_int
+    lib.mvllm_swiglu.argtypes = [p, p, p, i64, i32, p]
+    lib.mvllm_axpby.restype = ctypes.c_int
+    lib.mvllm_axpby.argtypes = [p, p, f32, f32, i64, p]
+
+
+EXPORTED_SYMBOLS = (
+    "mvllm_last_error",
+    "mvllm_abi_version",
+    "mvllm_paged_attention_plan",
+    "mvllm_paged_attention",
+    "mvllm_rmsnorm",
+    "mvllm_rope",
+    "mvllm_swiglu",
+    "mvllm_axpby",
+)
+
+
+def open_library(path: Path = LIB_PATH) -> ctypes.CDLL:
+    """dlopen the library and declare its signatures (no GPU needed)."""
+    if not path.exists():
+        raise ToolchainError(
+            f"{path} is not built; run `python -m mini_vllm.kernels.extension --build` "
+            "or __graft_entry__.build()"
+        )
+    lib = ctypes.CDLL(str(path))
+    _bind(lib)
+    version = lib.mvllm_abi_version()
+    if version != ABI_VERSION:
+        raise ToolchainError(f"{path} has ABI version {version}, expected {ABI_VERSION}")
+    return lib
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class HipExtension:
+    """The reference's ``mini_vllm_C`` module surface, served by libminivllm_hip.so."""
+
+    def __init__(self, lib: ctypes.CDLL) -> None:
+        self.lib = lib
+        self.path = LIB_PATH
+
+    # -- plumbing
+    def _check(self, rc: int) -> None:
+        if rc != 0:
+            message = self.lib.mvllm_last_error().decode(errors="replace")
+            raise RuntimeError(message or f"libminivllm_hip call failed with code {rc}")
+
+    # -- ops
+    def hello(self, x: torch.Tensor, a: float, b: float) -> torch.Tensor:
+        """``a * x + b`` (reference csrc/hello.cu), the toolchain smoke test."""
+        if not x.is_cuda:
+            raise RuntimeError("hello: x must be a CUDA tensor")
+        if x.dtype != torch.float32:
+            raise RuntimeError("hello: x must be float32")
+        x = x.contiguous()
+        out = torch.empty_like(x)
+        self._check(self.lib.mvllm_axpby(out.data_ptr(), x.data_ptr(), a, b, x.numel(), _stream(x.device)))
+        return out
+
+    def rmsnorm(self, x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+        """RMSNorm over the last dim (reference csrc/rmsnorm.cu:121-169)."""
+        if not x.is_cuda:
+            raise RuntimeError("rmsnorm: x must be a CUDA tensor")
+        if not weight.is_cuda:
+            raise RuntimeError("rmsnorm: weight must be a CUDA tensor")
+        if x.dim() < 1:
+            raise RuntimeError("rmsnorm: x must have at least one dimension")
+        if weight.dim() != 1:
+            raise RuntimeError(f"rmsnorm: weight must be 1-D, got {weight.dim()} dimensions")
+        if x.shape[-1] != weight.shape[0]:
+            raise RuntimeError(
+                f"rmsnorm: x's last dimension is {x.shape[-1]} but weight has "
+                f"{weight.shape[0]} elements"
+            )
+        if x.dtype == torch.float64:
+            raise RuntimeError(
+                "rmsnorm: float64 is not supported; this kernel accumulates in fp32, which "
+                "would silently lose precision. Use the PyTorch path."
+            )
+        if x.dtype != weight.dtype:
+            raise RuntimeError(
+                f"rmsnorm: x is {x.dtype} but weight is {weight.dtype}; the PyTorch path "
+                "promotes mixed dtypes, this kernel does not"
+            )
+        code = DTYPE_CODES.get(x.dtype)
+        if code is None or code == 3:
+            raise RuntimeError(f"rmsnorm: dtype {x.dtype} is not supported")
+        x = x.contiguous()
+        weight = weight.contiguous()
+        out = torch.empty_like(x)
+        dim = x.shape[-1]
+        rows = 0 if dim == 0 else x.numel() // dim
+        self._check(
+            self.lib.mvllm_rmsnorm(
+                out.data_ptr(), x.data_ptr(), weight.data_ptr(), rows, dim, eps, code, _stream(x.device)
+            )
+        )
+        return out
+
+    def rope(
+        self, x: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor
+    ) -> torch.Tensor:
+        """Rotate-halves RoPE at explicit positions (reference csrc/rope.cu:115-195)."""
+        if not x.is_cuda:
+            raise RuntimeError("rope: x must be a CUDA tensor")
+        if not positions.is_cuda:
+            raise RuntimeError("rope: positions must be a CUDA tensor")
+        if not (cos.is_cuda and sin.is_cuda):
+            raise RuntimeError("rope: the cos/sin tables must be CUDA tensors")
+        if x.dtype == torch.float64:
+            raise RuntimeError(
+                "rope: float64 is not supported; this kernel computes the rotation in fp32. "
+                "Use the PyTorch path."
+            )
+        if x.dim() < 3:
+            raise RuntimeError(
+                "rope: x must be N.. x H x D — a head axis is required, since one position "
+                f"applies to every head of a token. Got {x.dim()} dimensions"
+            )
+        dim = x.shape[-1]
+        if dim % 2 != 0:
+            raise RuntimeError(f"rope: the head dimension must be even, got {dim}")
+        if cos.dim() != 2 or sin.dim() != 2:
+            raise RuntimeError("rope: the cos/sin tables must be 2-D")
+        if cos.shape != sin.shape:
+            raise RuntimeError(f"rope: cos is {tuple(cos.shape)} but sin is {tuple(sin.shape)}")
+        if cos.shape[1] != dim:
+            raise RuntimeError(
+                f"rope: the tables are {cos.shape[1]} wide but the head dimension is {dim}; "
+                "they are built as max_seq_len x D with the angles duplicated"
+            )
+        if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+            raise RuntimeError(
+                "rope: the cos/sin tables must be float32 even when x is bf16. "
+                f"Got {cos.dtype}"
+            )
+        if positions.dtype not in (torch.int32, torch.int64):
+            raise RuntimeError(f"rope: positions must be int32 or int64, got {positions.dtype}")
+        code = DTYPE_CODES.get(x.dtype)
+        if code is None or code == 3:
+            raise RuntimeError(f"rope: dtype {x.dtype} is not supported")
+        x = x.contiguous()
+        out = torch.empty_like(x)
+        rows = 0 if dim == 0 else x.numel() // dim
+        if rows == 0:
+            return out
+        positions = positions.contiguous()
+        cos = cos.contiguous()
+        sin = sin.contiguous()
+        heads = x.shape[-2]
+        tokens = rows // heads
+        count = positions.numel()
+        if count == 0:
+            raise RuntimeError("rope: positions is empty")
+        if tokens % count != 0:
+            raise RuntimeError(
+                f"rope: x holds {tokens} tokens, which is not a multiple of the {count} "
+                "positions given, so the positions cannot broadcast over it"
+            )
+        self._check(
+            self.lib.mvllm_rope(
+                out.data_ptr(),
+                x.data_ptr(),
+                positions.data_ptr(),
+                positions.element_size(),
+                cos.data_ptr(),
+                sin.data_ptr(),
+                rows,
+                heads,
+                dim,
+                count,
+                cos.shape[0],
+                code,
+                _stream(x.device),
+            )
+        )
+        return out
+
+    def swiglu(self, gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+        """``silu(gate) * up`` (reference csrc/swiglu.cu:87-120)."""
+        if not (gate.is_cuda and up.is_cuda):
+            raise RuntimeError("swiglu: gate and up must be CUDA tensors")
+        if gate.shape != up.shape:
+            raise RuntimeError(
+                f"swiglu: gate is {tuple(gate.shape)} but up is {tuple(up.shape)}; they are the "
+                "two projections of the same tokens and must match"
+            )
+        if gate.dtype != up.dtype:
+            raise RuntimeError(f"swiglu: gate is {gate.dtype} but up is {up.dtype}")
+        if gate.dtype == torch.float64:
+            raise RuntimeError(
+                "swiglu: float64 is not supported; this kernel evaluates the sigmoid in fp32. "
+                "Use the PyTorch path."
+            )
+        code = DTYPE_CODES.get(gate.dtype)
+        if code is None or code == 3:
+            raise RuntimeError(f"swiglu: dtype {gate.dtype} is not supported")
+        gate = gate.contiguous()
+        up = up.contiguous()
+        out = torch.empty_like(gate)
+        if gate.numel() == 0:
+            return out
+        self._check(
+            self.lib.mvllm_swiglu(
+                out.data_ptr(), gate.data_ptr(), up.data_ptr(), gate.numel(), code, _stream(gate.device)
+            )
+        )
+        return out
+
+    def paged_attention_plan(
+        self,
+        num_tokens: int,
+        num_seqs: int,
+        num_q_heads: int,
+        num_kv_heads: int,
+        head_dim: int,
+        block_size: int,
+        max_query_len: int,
+        max_context_len: int,
+        q_dtype: torch.dtype,
+        kv_dtype: torch.dtype,
+    ) -> dict[str, int]:
+        plan = _Plan()
+        self._check(
+            self.lib.mvllm_paged_attention_plan(
+                num_tokens,
+                num_seqs,
+                num_q_heads,
+                num_kv_heads,
+                head_dim,
+                block_size,
+                max_query_len,
+                max_context_len,
+                DTYPE_CODES.get(q_dtype, -1),
+                DTYPE_CODES.get(kv_dtype, -1),
+                ctypes.byref(plan),
+            )
+        )
+        return {name: getattr(plan, name) for name, _ in _Plan._fields_}
+
+    def paged_attention(
+        self,
+        q: torch.Tensor,
+        key_pool: torch.Tensor,
+        value_pool: torch.Tensor,
+        block_tables: torch.Tensor,
+        cu_seqlens_q: torch.Tensor,
+        context_lens: torch.Tensor,
+        seq_lens: torch.Tensor,
+        max_query_len: int,
+        max_context_len: int,
+        scale: float,
+        k_scale: torch.Tensor | None = None,
+        v_scale: torch.Tensor | None = None,
+        out: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """Ragged decode + prefill over a paged cache (reference csrc/paged_attention.cu:598-711).
+
+        Same positional arguments and refusals as the reference. Additions, all optional:
+        ``k_scale``/``v_scale`` (``num_blocks x H_k`` fp32) for a float8_e4m3fn pool, and
+        ``out`` to write into a caller-owned ``T x H_q x D`` tensor.
+        """
+        if not (q.is_cuda and key_pool.is_cuda and value_pool.is_cuda):
+            raise RuntimeError("paged_attention: q and the pools must be CUDA tensors")
+        if q.dim() != 3:
+            raise RuntimeError(
+                "paged_attention: expected q shaped T x H_q x D (the flattened token axis), "
+                f"got {list(q.shape)}"
+            )
+        if key_pool.dim() != 4 or key_pool.shape != value_pool.shape:
+            raise RuntimeError(
+                "paged_attention: expected matching pools shaped num_blocks x P x H_k x D, got "
+                f"{list(key_pool.shape)} and {list(value_pool.shape)}"
+            )
+        if not (q.is_contiguous() and key_pool.is_contiguous() and value_pool.is_contiguous()):
+            raise RuntimeError(
+                "paged_attention: q and the pools must be contiguous; the kernel walks them by "
+                "slot arithmetic rather than by stride"
+            )
+        fp8 = key_pool.dtype == torch.float8_e4m3fn
+        if q.dtype == torch.float64:
+            raise RuntimeError(
+                "paged_attention: float64 is not supported; the accumulators here are fp32"
+            )
+        if key_pool.dtype != value_pool.dtype or (q.dtype != key_pool.dtype and not fp8):
+            raise RuntimeError(
+                f"paged_attention: q and the pools must share a dtype, got {q.dtype}, "
+                f"{key_pool.dtype} and {value_pool.dtype}"
+            )
+        if q.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            raise RuntimeError(f"paged_attention: q dtype {q.dtype} is not supported")
+        if q.shape[2] != key_pool.shape[3]:
+            raise RuntimeError(
+                f"paged_attention: head dim mismatch, q has {q.shape[2]} and the pool has "
+                f"{key_pool.shape[3]}"
+            )
+        num_blocks, block_size, num_kv_heads, head_dim = key_pool.shape
+        if num_kv_heads == 0 or q.shape[1] % num_kv_heads != 0:
+            raise RuntimeError(
+                f"paged_attention: H_q ({q.shape[1]}) must be a multiple of H_k ({num_kv_heads})"
+            )
+        if block_size <= 0 or block_size & (block_size - 1):
+            raise RuntimeError(
+                f"paged_attention: the block size must be a power of two, got {block_size}"
+            )
+        num_sequences = seq_lens.shape[0]
+        if block_tables.dim() != 2 or block_tables.shape[0] != num_sequences:
+            raise RuntimeError(
+                f"paged_attention: expected a block table per sequence, got "
+                f"{list(block_tables.shape)} for {num_sequences} sequences"
+            )
+        if context_lens.shape[0] != num_sequences or cu_seqlens_q.shape[0] != num_sequences + 1:
+            raise RuntimeError("paged_attention: metadata disagrees on the sequence count")
+        if any(
+            t.dtype != torch.int32 for t in (block_tables, cu_seqlens_q, context_lens, seq_lens)
+        ):
+            raise RuntimeError("paged_attention: the metadata tensors must be int32")
+        if not block_tables.is_contiguous():
+            raise RuntimeError("paged_attention: block_tables must be contiguous")
+        if not all(
+            t.is_cuda and t.device == q.device
+            for t in (key_pool, value_pool, block_tables, cu_seqlens_q, context_lens, seq_lens)
+        ):
+            raise RuntimeError("paged_attention: every tensor must be on q's CUDA device")
+        if max_query_len < 1:
+            raise RuntimeError(f"paged_attention: max_query_len must be >= 1, got {max_query_len}")
+        if max_context_len < max_query_len:
+            raise RuntimeError(
+                f"paged_attention: max_context_len ({max_context_len}) must be at least "
+                f"max_query_len ({max_query_len}); a pass cannot compute more tokens than it "
+                "may attend over"
+            )
+        if fp8:
+            if k_scale is None or v_scale is None:
+                raise RuntimeError(
+                    "paged_attention: a float8_e4m3fn pool needs k_scale and v_scale "
+                    "(num_blocks x H_k float32)"
+                )
+            for name, s in (("k_scale", k_scale), ("v_scale", v_scale)):
+                if (
+                    s.dtype != torch.float32
+                    or tuple(s.shape) != (num_blocks, num_kv_heads)
+                    or not s.is_contiguous()
+                    or s.device != q.device
+                ):
+                    raise RuntimeError(
+                        f"paged_attention: {name} must be a contiguous float32 "
+                        f"{num_blocks} x {num_kv_heads} tensor on q's device"
+                    )
+        elif k_scale is not None or v_scale is not None:
+            raise RuntimeError("paged_attention: k_scale/v_scale apply only to a float8 pool")
+
+        # Make sure the metadata is readable by index arithmetic.
+        cu_seqlens_q = cu_seqlens_q.contiguous()
+        context_lens = context_lens.contiguous()
+        seq_lens = seq_lens.contiguous()
+
+        if out is None:
+            out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        elif out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous():
+            raise RuntimeError("paged_attention: out must be a contiguous tensor shaped like q")
+        num_tokens, num_q_heads, _ = q.shape
+        if num_tokens == 0 or num_sequences == 0:
+            return out
+
+        q_code = DTYPE_CODES[q.dtype]
+        kv_code = DTYPE_CODES[key_pool.dtype]
+        plan = _Plan()
+        self._check(
+            self.lib.mvllm_paged_attention_plan(
+                num_tokens,
+                num_sequences,
+                num_q_heads,
+                num_kv_heads,
+                head_dim,
+                block_size,
+                int(max_query_len),
+                int(max_context_len),
+                q_code,
+                kv_code,
+                ctypes.byref(plan),
+            )
+        )
+        workspace = None
+        if plan.workspace_bytes:
+            workspace = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=q.device)
+        self._check(
+            self.lib.mvllm_paged_attention(
+                out.data_ptr(),
+                q.data_ptr(),
+                key_pool.data_ptr(),
+                value_pool.data_ptr(),
+                _ptr(k_scale),
+                _ptr(v_scale),
+                block_tables.data_ptr(),
+                cu_seqlens_q.data_ptr(),
+                context_lens.data_ptr(),
+                seq_lens.data_ptr(),
+                num_tokens,
+                num_sequences,
+                num_q_heads,
+                num_kv_heads,
+                head_dim,
+                block_size,
+                num_blocks,
+                block_tables.shape[1],
+                int(max_query_len),
+                int(max_context_len),
+                float(scale),
+                q_code,
+                kv_code,
+                _ptr(workspace),
+                plan.workspace_bytes,
+                _stream(q.device),
+            )
+        )
+        return out
+
+
+def load_extension(verbose: bool = False) -> HipExtension:
+    """Return the bound library, building it first only if nothing is built yet.
+
+    Raises :class:`ToolchainError` when no GPU is visible: there is no CPU
+    implementation behind this object, by design.
+    """
+    global _extension
+    with _lock:
+        if _extension is not None:
+            return _extension
+        if not torch.cuda.is_available():
+            raise ToolchainError("no GPU visible; the HIP kernels need an MI355X (gfx950)")
+        if not LIB_PATH.exists():
+            build_library(verbose=verbose)
+        _extension = HipExtension(open_library())
+        return _extension
+
+
+def rebuild(verbose: bool = True) -> HipExtension:
+    """Compile from scratch and rebind (only valid before the old library was used)."""
+    global _extension
+    with _lock:
+        _extension = None
+    build_library(verbose=verbose)
+    return load_extension(verbose=verbose)
+
+
+def toolchain_report() -> dict[str, Any]:
+    report: dict[str, Any] = {
+        "python": sys.version.split()[0],
+        "torch": torch.__version__,
+        "torch_hip": getattr(torch.version, "hip", None),
+        "hipcc": HIPCC,
+        "arch": ARCH,
+        "library": str(LIB_PATH),
+        "library_built": LIB_PATH.exists(),
+        "sources": [p.name for p in sources()],
+        "gpu_available": torch.cuda.is_available(),
+    }
+    if torch.cuda.is_available():
+        props = torch.cuda.get_device_properties(0)
+        report["gpu"] = props.name
+        report["gcn_arch"] = getattr(props, "gcnArchName", None)
+        report["compute_units"] = props.multi_processor_count
+        report["vram_gb"] = round(props.total_memory / 1024**3, 2)
+    return report
+
+
+def main() -> int:
+    import argparse
+
+    parser = argparse.ArgumentParser(description="Build the Mini-vLLM MI355X kernel library.")
+    parser.add_argument("--build", action="store_true", help="compile before anything else")
+    args = parser.parse_args()
+    if args.build:
+        build_library(verbose=True)
+    for key, value in toolchain_report().items():
+        print(f"{key:>16}: {value}")
+    if not torch.cuda.is_available():
+        return 0
+    ext = load_extension(verbose=True)
+    x = torch.randn(1024, device="cuda")
+    ok = torch.allclose(ext.hello(x, 2.0, 3.0), 2.0 * x + 3.0)
+    print(f"\nhello(x, 2, 3) == 2x + 3 : {'ok' if ok else 'MISMATCH'}")
+    return 0 if ok else 1
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,215 @@
+"""The seam between the model and its kernels (reference mini_vllm/kernels/ops.py).
+
+Same op names, signatures and ``use_cuda`` switch as the reference, so the model,
+engine and tests above it run unchanged:
+
+    rmsnorm(x, weight, eps=1e-6, use_cuda=False)                       ops.py:117-131
+    rope(x, positions, cos, sin, use_cuda=False)                       ops.py:134-149
+    swiglu(gate, up, use_cuda=False)                                   ops.py:152-163
+    paged_attention(q, key_pool, value_pool, block_tables, cu_seqlens_q,
+                    context_lens, seq_lens, max_query_len, max_context_len,
+                    scale=None, use_cuda=False)                        ops.py:200-254
+
+The callee behind ``use_cuda=True`` is ``libminivllm_hip.so`` (HIP for gfx950).
+
+One deliberate difference: ``use_cuda=True`` never falls back. The reference routes a
+call its kernel cannot serve (CPU tensors, a non-contiguous pool, int64 tables ...)
+silently to the PyTorch path; here such a call raises ``RuntimeError`` naming the
+reason, because a silent fallback is exactly how a kernel that never ran ends up in
+a benchmark. ``use_cuda=False`` selects the PyTorch path (:mod:`mini_vllm.torch_path`)
+explicitly, as in the reference. Ops that have no kernel in this library yet
+(``attention``, the dense-cache decode/prefill) follow the reference's rule for
+unimplemented kernels and use the PyTorch path, which :func:`dispatch_report` states.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from mini_vllm import torch_path
+from mini_vllm.kernels.extension import load_extension
+
+__all__ = [
+    "CUDA_KERNELS",
+    "NOT_YET_FASTER",
+    "attention",
+    "cuda_kernel_names",
+    "dispatch_report",
+    "paged_attention",
+    "rmsnorm",
+    "rope",
+    "swiglu",
+]
+
+# op name -> (has a kernel in libminivllm_hip.so, source file). The keys are the
+# method names of the bound extension (`load_extension()`), kept from the reference.
+CUDA_KERNELS: dict[str, tuple[bool, str]] = {
+    "rmsnorm": (True, "csrc/elementwise.hip"),
+    "rope": (True, "csrc/elementwise.hip"),
+    "swiglu": (True, "csrc/elementwise.hip"),
+    "decode_attention": (False, "dense-cache decode (not in this library)"),
+    "flash_prefill": (False, "dense-cache prefill (not in this library)"),
+    "paged_attention": (True, "csrc/paged_decode.hip + csrc/paged_prefill.hip"),
+}
+
+# Kernels that exist but are deliberately not dispatched, with the reason.
+NOT_YET_FASTER: dict[str, str] = {}
+
+MAX_PAGED_HEAD_DIM = 256
+PAGED_HEAD_DIMS = (32, 64, 128, 256)
+
+
+def _use_kernel(name: str, use_cuda: bool, x: torch.Tensor) -> bool:
+    """Whether ``name`` runs on the HIP kernel; raises instead of falling back."""
+    if not use_cuda:
+        return False
+    implemented, _source = CUDA_KERNELS[name]
+    if not implemented or name in NOT_YET_FASTER:
+        return False
+    if not x.is_cuda:
+        raise RuntimeError(
+            f"{name}: use_cuda=True needs device tensors, got {x.device}; pass use_cuda=False "
+            "to run the PyTorch path"
+        )
+    return True
+
+
+def cuda_kernel_names() -> list[str]:
+    """The ops that currently have a working kernel."""
+    return [name for name, (implemented, _) in CUDA_KERNELS.items() if implemented]
+
+
+def dispatch_report(use_cuda: bool) -> str:
+    """One line per op saying which implementation a run would use."""
+    lines = []
+    for name, (implemented, source) in CUDA_KERNELS.items():
+        if not implemented:
+            note = f"no kernel yet — {source}"
+        elif name in NOT_YET_FASTER:
+            note = f"kernel from {source} is slower: {NOT_YET_FASTER[name]}"
+        elif not use_cuda:
+            note = f"kernel exists from {source}; use_cuda is off"
+        else:
+            lines.append(f"  {name:<18} hip     (kernel from {source})")
+            continue
+        lines.append(f"  {name:<18} torch   ({note})")
+    return "\n".join(lines)
+
+
+# ------------------------------------------------------------------------ ops
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
+            use_cuda: bool = False) -> torch.Tensor:
+    """RMSNorm over the last dimension (also QK-norm). Kernel: ``csrc/elementwise.hip``."""
+    if _use_kernel("rmsnorm", use_cuda, x):
+        return load_extension().rmsnorm(x, weight, eps)
+    return torch_path.rms_norm(x, weight, eps)
+
+
+def rope(x: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+         use_cuda: bool = False) -> torch.Tensor:
+    """Rotary embedding at explicit positions. Kernel: ``csrc/elementwise.hip``."""
+    if _use_kernel("rope", use_cuda, x):
+        return load_extension().rope(x, positions, cos, sin)
+    return torch_path.apply_rope(x, positions, cos, sin)
+
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor, use_cuda: bool = False) -> torch.Tensor:
+    """``silu(gate) * up``. Kernel: ``csrc/elementwise.hip``."""
+    if _use_kernel("swiglu", use_cuda, gate):
+        return load_extension().swiglu(gate, up)
+    return torch_path.silu(gate) * up
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+              mask: torch.Tensor | str | None = None, use_cuda: bool = False) -> torch.Tensor:
+    """Dense-cache grouped attention ``B x H x L x D`` (reference ops.py:166-197).
+
+    Not on the paged engine's path and without a kernel in this library: always the
+    PyTorch path (decode: every cached key visible; ``mask="causal"``: offset causal).
+    """
+    b, hq, L, d = q.shape
+    hk, S = k.shape[1], k.shape[2]
+    g = hq // hk
+    qs = q.reshape(b, hk, g, L, d)
+    scores = (qs @ k.unsqueeze(2).transpose(-2, -1).contiguous()) / math.sqrt(d)
+    if isinstance(mask, str):
+        if mask != "causal":
+            raise ValueError(f"unknown mask shorthand {mask!r}, expected 'causal'")
+        rows = torch.arange(L, device=q.device).unsqueeze(1)
+        cols = torch.arange(S, device=q.device).unsqueeze(0)
+        mask = torch.zeros(L, S, dtype=scores.dtype, device=q.device).masked_fill(
+            cols > rows + (S - L), float("-inf"))
+    if mask is not None:
+        scores = scores + mask
+    return (torch_path.softmax(scores, dim=-1) @ v.unsqueeze(2)).reshape(b, hq, L, d)
+
+
+def paged_attention(
+    q: torch.Tensor,
+    key_pool: torch.Tensor,
+    value_pool: torch.Tensor,
+    block_tables: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    context_lens: torch.Tensor,
+    seq_lens: torch.Tensor,
+    max_query_len: int,
+    max_context_len: int,
+    scale: float | None = None,
+    use_cuda: bool = False,
+    *,
+    k_scale: torch.Tensor | None = None,
+    v_scale: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Ragged attention over a paged cache. Kernels: ``csrc/paged_{decode,prefill}.hip``.
+
+    ::
+
+        q:    T x H_q x D              every scheduled token, sequences concatenated
+        pools num_blocks x P x H_k x D
+        out:  T x H_q x D
+
+    ``max_query_len``/``max_context_len`` are host integers (they size the grid without
+    a device read). ``k_scale``/``v_scale`` (``num_blocks x H_k`` fp32, keyword-only)
+    accompany a ``float8_e4m3fn`` pool: element = stored value x scale of its
+    (page, kv head).
+    """
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    if _use_kernel("paged_attention", use_cuda, q):
+        _check_kernel_can_page(q, key_pool, value_pool, block_tables)
+        return load_extension().paged_attention(
+            q, key_pool, value_pool, block_tables, cu_seqlens_q, context_lens, seq_lens,
+            int(max_query_len), int(max_context_len), scale, k_scale, v_scale,
+        )
+    return torch_path.paged_attention_gathered(
+        q, key_pool, value_pool, block_tables, cu_seqlens_q, context_lens, scale,
+        k_scale=k_scale, v_scale=v_scale,
+    )
+
+
+def _check_kernel_can_page(q: torch.Tensor, key_pool: torch.Tensor, value_pool: torch.Tensor,
+                           block_tables: torch.Tensor) -> None:
+    """The reference's ``_kernel_can_page`` gate (ops.py:257-275), raising instead of
+    declining, plus this library's head-dim set."""
+    if q.dim() != 3:
+        raise RuntimeError(f"paged_attention: expected q shaped T x H_q x D, got {list(q.shape)}")
+    if q.dtype == torch.float64:
+        raise RuntimeError("paged_attention: float64 is not supported; the accumulators here are fp32")
+    if q.shape[-1] not in PAGED_HEAD_DIMS:
+        raise RuntimeError(
+            f"paged_attention: head dim {q.shape[-1]} is not supported; this build serves "
+            f"{', '.join(map(str, PAGED_HEAD_DIMS))}"
+        )
+    if not (q.is_contiguous() and key_pool.is_contiguous() and value_pool.is_contiguous()):
+        raise RuntimeError(
+            "paged_attention: q and the pools must be contiguous; the kernel walks them by "
+            "slot arithmetic rather than by stride"
+        )
+    if block_tables.dtype != torch.int32:
+        raise RuntimeError("paged_attention: the metadata tensors must be int32")
+    if not block_tables.is_contiguous():
+        raise RuntimeError("paged_attention: block_tables must be contiguous")

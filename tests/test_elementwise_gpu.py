@@ -1,0 +1,204 @@
+"""RMSNorm / QK-norm, RoPE and SwiGLU kernels on the MI355X (``-m gpu``).
+
+Each kernel is compared with (a) the numpy oracle (oracle/elementwise.py) that rounds
+where the reference rounds, and (b) the reference's own PyTorch expression evaluated
+by PyTorch-ROCm on the same GPU, which is what the reference's kernel tests use
+(test_swiglu_cuda.py:43-56, test_rope_cuda.py:154-205, test_rmsnorm_cuda.py:117-224).
+RoPE and SwiGLU are expected bit-exact against (b); RMSNorm within one rounding of
+the storage type (its fp32 sum of squares is reduced in a different order).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from mini_vllm import torch_path
+from mini_vllm.kernels import ops
+from oracle import elementwise as ew
+
+pytestmark = pytest.mark.gpu
+
+NAMES = {torch.float32: "f32", torch.bfloat16: "bf16", torch.float16: "f16"}
+ULP = {torch.float32: 2**-23, torch.bfloat16: 2**-7, torch.float16: 2**-10}
+
+
+def within_ulps(got: torch.Tensor, want: np.ndarray, dtype, ulps: float = 1.0) -> None:
+    g = got.float().cpu().numpy()
+    tol = np.abs(want) * ULP[dtype] * ulps + 1e-30
+    bad = np.abs(g - want) > tol
+    assert not bad.any(), f"{bad.sum()} of {bad.size} elements beyond {ulps} ulp; max {np.abs(g - want).max()}"
+
+
+# -------------------------------------------------------------------- rmsnorm
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(7, 1024), (33, 16, 128), (5, 8, 128), (3, 96), (2, 4096), (4, 6000), (1, 13)])
+def test_rmsnorm_matches_the_oracle(extension, device, dtype, shape):
+    x = (torch.randn(shape) * 2).to(dtype)
+    w = (torch.rand(shape[-1]) + 0.5).to(dtype)
+    got = extension.rmsnorm(x.to(device), w.to(device), 1e-6)
+    want = ew.rms_norm(x.float().numpy(), w.float().numpy(), 1e-6, NAMES[dtype])
+    within_ulps(got, want, dtype, ulps=1.0 if dtype != torch.float32 else 8.0)
+    on_gpu = torch_path.rms_norm(x.to(device), w.to(device), 1e-6)
+    within_ulps(got, on_gpu.float().cpu().numpy(), dtype, ulps=1.0 if dtype != torch.float32 else 8.0)
+
+
+def test_rmsnorm_unit_weight_gives_unit_rms(extension, device):
+    x = torch.randn(64, 1024, device=device) * 5
+    out = extension.rmsnorm(x, torch.ones(1024, device=device), 1e-6)
+    rms = out.double().pow(2).mean(-1).sqrt()
+    assert torch.allclose(rms, torch.ones_like(rms), atol=1e-5)
+
+
+def test_rmsnorm_zero_row_stays_finite(extension, device):
+    out = extension.rmsnorm(torch.zeros(4, 128, device=device), torch.ones(128, device=device), 1e-6)
+    assert torch.equal(out, torch.zeros_like(out))
+
+
+def test_rmsnorm_reduces_in_fp32(extension, device):
+    """A row of large equal bf16 values: a bf16 accumulator would overflow the mean."""
+    x = torch.full((2, 1024), 3.0e4, dtype=torch.bfloat16, device=device)
+    out = extension.rmsnorm(x, torch.ones(1024, dtype=torch.bfloat16, device=device), 1e-6)
+    assert torch.allclose(out.float(), torch.ones(2, 1024, device=device), atol=1e-2)
+
+
+def test_rmsnorm_misaligned_and_strided_inputs(extension, device):
+    base = torch.randn(9, 129, dtype=torch.bfloat16, device=device)
+    x = base[:, 1:]                       # 2-byte offset rows, not 16-byte aligned
+    w = torch.rand(128, dtype=torch.bfloat16, device=device) + 0.5
+    got = extension.rmsnorm(x, w, 1e-6)
+    want = ew.rms_norm(x.float().cpu().numpy(), w.float().cpu().numpy(), 1e-6, "bf16")
+    within_ulps(got, want, torch.bfloat16)
+    xt = torch.randn(128, 6, dtype=torch.bfloat16, device=device).t()  # non-contiguous
+    got = extension.rmsnorm(xt, w, 1e-6)
+    within_ulps(got, ew.rms_norm(xt.float().cpu().numpy(), w.float().cpu().numpy(), 1e-6, "bf16"),
+                torch.bfloat16)
+
+
+def test_rmsnorm_refusals(extension, device):
+    x = torch.randn(4, 8, device=device)
+    with pytest.raises(RuntimeError, match="float64"):
+        extension.rmsnorm(x.double(), torch.ones(8, device=device).double())
+    with pytest.raises(RuntimeError, match="mixed dtypes"):
+        extension.rmsnorm(x, torch.ones(8, device=device, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="last dimension"):
+        extension.rmsnorm(x, torch.ones(9, device=device))
+
+
+# ----------------------------------------------------------------------- rope
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("pos_dtype", [torch.int64, torch.int32])
+def test_rope_matches_the_oracle_and_torch_bitwise(extension, device, dtype, pos_dtype):
+    cos, sin = torch_path.rope_tables(128, 4096)
+    x = torch.randn(1, 37, 16, 128).to(dtype)
+    positions = torch.randint(0, 4096, (37,), dtype=pos_dtype)
+    got = extension.rope(x.to(device), positions.to(device), cos.to(device), sin.to(device))
+    want = ew.apply_rope(x.float().numpy(), positions.numpy(), cos.numpy(), sin.numpy(),
+                         NAMES[dtype])
+    assert np.array_equal(got.float().cpu().numpy(), want)
+    on_gpu = torch_path.apply_rope(x.to(device), positions.to(device), cos.to(device), sin.to(device))
+    assert torch.equal(got, on_gpu)
+
+
+def test_rope_position_zero_is_identity_and_norms_are_kept(extension, device):
+    cos, sin = (t.to(device) for t in torch_path.rope_tables(128, 64))
+    x = torch.randn(1, 8, 4, 128, device=device)
+    assert torch.equal(extension.rope(x, torch.zeros(8, dtype=torch.long, device=device), cos, sin), x)
+    out = extension.rope(x, torch.arange(8, device=device), cos, sin)
+    n_in = x[..., :64] ** 2 + x[..., 64:] ** 2
+    n_out = out[..., :64] ** 2 + out[..., 64:] ** 2
+    assert torch.allclose(n_in, n_out, rtol=1e-5, atol=1e-6)
+
+
+def test_rope_decode_token_equals_its_prefill_position(extension, device):
+    cos, sin = (t.to(device) for t in torch_path.rope_tables(128, 512))
+    x = torch.randn(1, 50, 8, 128, dtype=torch.bfloat16, device=device)
+    full = extension.rope(x, torch.arange(50, device=device), cos, sin)
+    one = extension.rope(x[:, 37:38].contiguous(), torch.tensor([37], device=device), cos, sin)
+    assert torch.equal(full[:, 37:38], one)
+
+
+def test_rope_positions_broadcast_over_a_batch(extension, device):
+    cos, sin = (t.to(device) for t in torch_path.rope_tables(64, 128))
+    x = torch.randn(3, 10, 4, 64, device=device)
+    pos = torch.arange(5, 15, device=device)
+    got = extension.rope(x, pos, cos, sin)
+    assert torch.equal(got, torch_path.apply_rope(x, pos, cos, sin))
+
+
+def test_rope_out_of_range_position_is_nan_not_a_fault(extension, device):
+    cos, sin = (t.to(device) for t in torch_path.rope_tables(64, 16))
+    x = torch.randn(1, 3, 2, 64, device=device)
+    out = extension.rope(x, torch.tensor([1, 99, -3], device=device), cos, sin)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out[0, 0]).all()
+    assert torch.isnan(out[0, 1]).all() and torch.isnan(out[0, 2]).all()
+
+
+def test_rope_refusals(extension, device):
+    cos, sin = (t.to(device) for t in torch_path.rope_tables(64, 16))
+    x = torch.randn(4, 64, device=device)
+    with pytest.raises(RuntimeError, match="head axis"):
+        extension.rope(x, torch.arange(4, device=device), cos, sin)
+    with pytest.raises(RuntimeError, match="float32"):
+        extension.rope(x[None, :, None], torch.arange(4, device=device), cos.half(), sin.half())
+    with pytest.raises(RuntimeError, match="broadcast"):
+        extension.rope(torch.randn(1, 6, 2, 64, device=device), torch.arange(4, device=device), cos, sin)
+
+
+# --------------------------------------------------------------------- swiglu
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(64, 3072), (3, 1001), (1,)])
+def test_swiglu_is_bitwise_equal_to_torch(extension, device, dtype, shape):
+    g = (torch.randn(shape) * 4).to(dtype).to(device)
+    u = torch.randn(shape).to(dtype).to(device)
+    got = extension.swiglu(g, u)
+    assert torch.equal(got, torch_path.silu(g) * u)
+    want = ew.swiglu(g.float().cpu().numpy(), u.float().cpu().numpy(), NAMES[dtype])
+    within_ulps(got, want, dtype, ulps=1.0 if dtype != torch.float32 else 4.0)
+
+
+def test_swiglu_misaligned_views(extension, device):
+    g = torch.randn(1025, dtype=torch.bfloat16, device=device)[1:]
+    u = torch.randn(1025, dtype=torch.bfloat16, device=device)[1:]
+    assert torch.equal(extension.swiglu(g, u), torch_path.silu(g) * u)
+
+
+def test_swiglu_refusals(extension, device):
+    with pytest.raises(RuntimeError, match="must match"):
+        extension.swiglu(torch.randn(4, device=device), torch.randn(5, device=device))
+    with pytest.raises(RuntimeError, match="float64"):
+        extension.swiglu(torch.randn(4, device=device).double(), torch.randn(4, device=device).double())
+
+
+# ------------------------------------------------------------------ ops seam
+
+
+def test_ops_route_elementwise_to_the_kernels(extension, device, monkeypatch):
+    calls = []
+    for name in ("rmsnorm", "rope", "swiglu"):
+        original = getattr(extension, name)
+
+        def spy(*a, _orig=original, _name=name, **k):
+            calls.append(_name)
+            return _orig(*a, **k)
+
+        monkeypatch.setattr(extension, name, spy)
+    x = torch.randn(4, 128, device=device)
+    ops.rmsnorm(x, torch.ones(128, device=device), use_cuda=True)
+    cos, sin = (t.to(device) for t in torch_path.rope_tables(128, 16))
+    ops.rope(x[None, :, None], torch.arange(4, device=device), cos, sin, use_cuda=True)
+    ops.swiglu(x, x, use_cuda=True)
+    assert calls == ["rmsnorm", "rope", "swiglu"]
+
+
+def test_hello_axpby(extension, device):
+    x = torch.randn(1000, device=device)
+    assert torch.allclose(extension.hello(x, 2.0, 3.0), 2.0 * x + 3.0)

@@ -1,0 +1,111 @@
+"""The C-ABI library on the CPU: it loads, exports every declared symbol, and refuses
+bad arguments with the reference's messages before touching a GPU."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+
+import pytest
+import torch
+
+from mini_vllm.kernels import extension
+from mini_vllm.kernels.extension import EXPORTED_SYMBOLS, INCLUDE_DIR, open_library
+
+HEADER = INCLUDE_DIR / "minivllm_hip.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not extension.LIB_PATH.exists():
+        extension.build_library()
+    return open_library()
+
+
+def declared_functions() -> set[str]:
+    text = HEADER.read_text()
+    return set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(mvllm_\w+)\s*\(", text, re.M))
+
+
+def test_every_declared_symbol_is_exported(lib):
+    declared = declared_functions()
+    assert declared == set(EXPORTED_SYMBOLS), declared ^ set(EXPORTED_SYMBOLS)
+    for name in declared:
+        assert hasattr(lib, name), f"{name} is declared in {HEADER.name} but not exported"
+
+
+def test_abi_version(lib):
+    assert lib.mvllm_abi_version() == extension.ABI_VERSION
+    assert lib.mvllm_last_error() == b""
+
+
+def _paged(lib, **over):
+    args = dict(out=1, q=1, key_pool=1, value_pool=1, k_scales=None, v_scales=None,
+                block_tables=1, cu=1, ctx=1, seq=1, num_tokens=4, num_seqs=4, hq=16, hk=8,
+                d=128, p=16, num_blocks=512, max_blocks=63, max_q=1, max_ctx=1000, scale=0.088,
+                q_dtype=0, kv_dtype=0, ws=None, ws_bytes=0, stream=None)
+    args.update(over)
+    return lib.mvllm_paged_attention(*args.values())
+
+
+@pytest.mark.parametrize("over,code,message", [
+    (dict(p=3), 1, "power of two"),
+    (dict(hq=12), 1, "must be a multiple of H_k"),
+    (dict(max_q=8, max_ctx=4), 1, "at least max_query_len"),
+    (dict(max_q=0), 1, "max_query_len must be >= 1"),
+    (dict(d=96), 2, "head dim 96 is not supported"),
+    (dict(q_dtype=5), 1, "float64 is not supported"),
+    (dict(q_dtype=2, kv_dtype=0), 1, "must share a dtype"),
+    (dict(q_dtype=2, kv_dtype=3), 1, "k_scales and v_scales"),
+    (dict(out=None), 1, "NULL"),
+])
+def test_paged_attention_refusals(lib, over, code, message):
+    assert _paged(lib, **over) == code
+    assert message in lib.mvllm_last_error().decode()
+
+
+def test_split_workspace_is_required_when_planned(lib):
+    """A long decode needs split partials; a missing workspace is refused, not faulted."""
+    assert _paged(lib, num_tokens=1, num_seqs=1, max_ctx=8192) == 4
+    assert "workspace" in lib.mvllm_last_error().decode()
+
+
+def test_plan_is_host_only_and_consistent(lib):
+    plan = extension._Plan()
+    rc = lib.mvllm_paged_attention_plan(64, 64, 16, 8, 128, 16, 1, 4096, 2, 2, ctypes.byref(plan))
+    assert rc == 0
+    assert plan.prefill_mfma == 0 and plan.decode_by_row == 0
+    assert 64 <= plan.split_tokens <= 1024 and plan.split_tokens % 16 == 0
+    assert plan.max_splits == -(-4096 // plan.split_tokens)
+    if plan.max_splits > 1:
+        entries = 64 * 16 * plan.max_splits
+        assert plan.workspace_bytes >= entries * (128 + 2) * 4
+    rc = lib.mvllm_paged_attention_plan(4096, 8, 16, 8, 128, 16, 512, 2048, 2, 2, ctypes.byref(plan))
+    assert rc == 0 and plan.prefill_mfma == 1 and plan.decode_by_row == 0
+    rc = lib.mvllm_paged_attention_plan(100, 4, 16, 8, 128, 16, 40, 2048, 0, 0, ctypes.byref(plan))
+    assert rc == 0 and plan.prefill_mfma == 0 and plan.decode_by_row == 1
+
+
+@pytest.mark.parametrize("fn,args,message", [
+    ("mvllm_rmsnorm", (1, 1, 1, 4, 8, 1e-6, 7, None), "float64 is not supported"),
+    ("mvllm_rope", (1, 1, 1, 8, 1, 1, 4, 2, 7, 2, 16, 0, None), "must be even"),
+    ("mvllm_rope", (1, 1, 1, 8, 1, 1, 6, 2, 8, 2, 16, 0, None), "cannot broadcast"),
+    ("mvllm_rope", (1, 1, 1, 2, 1, 1, 4, 2, 8, 2, 16, 0, None), "int32 or int64"),
+    ("mvllm_swiglu", (1, 1, 1, 8, 9, None), "float64 is not supported"),
+])
+def test_elementwise_refusals(lib, fn, args, message):
+    assert getattr(lib, fn)(*args) != 0
+    assert message in lib.mvllm_last_error().decode()
+
+
+def test_empty_inputs_are_no_ops(lib):
+    assert lib.mvllm_rmsnorm(None, None, None, 0, 128, 1e-6, 2, None) == 0
+    assert lib.mvllm_swiglu(None, None, None, 0, 2, None) == 0
+    assert _paged(lib, num_tokens=0, num_seqs=0, out=None) == 0
+
+
+def test_load_extension_refuses_without_a_gpu():
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    with pytest.raises(extension.ToolchainError, match="no GPU"):
+        extension.load_extension()

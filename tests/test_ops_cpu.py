@@ -1,0 +1,76 @@
+"""The op seam on the CPU: routing rules and the explicit PyTorch path."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import assert_max_abs
+from mini_vllm import torch_path
+from mini_vllm.kernels import ops
+from mini_vllm.workloads import build_batch
+from oracle import elementwise as ew
+from oracle.paged_attention import paged_attention as oracle_paged
+
+
+def test_use_cuda_true_on_cpu_tensors_raises_instead_of_falling_back():
+    b = build_batch([20], [1], num_q_heads=4, num_kv_heads=2, head_dim=32)
+    with pytest.raises(RuntimeError, match="use_cuda=True needs device tensors"):
+        ops.paged_attention(*b.args(), use_cuda=True)
+    with pytest.raises(RuntimeError, match="needs device tensors"):
+        ops.rmsnorm(torch.randn(2, 8), torch.ones(8), use_cuda=True)
+    with pytest.raises(RuntimeError, match="needs device tensors"):
+        ops.swiglu(torch.randn(4), torch.randn(4), use_cuda=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_torch_path_paged_attention_matches_the_oracle(dtype):
+    b = build_batch([300, 1, 40, 64], [1, 1, 8, 64], dtype=dtype, num_q_heads=8,
+                    num_kv_heads=2, head_dim=64, seed=3)
+    got = ops.paged_attention(*b.args(), use_cuda=False)
+    want = oracle_paged(b.q, b.key_pool, b.value_pool, b.block_tables, b.cu_seqlens_q,
+                        b.context_lens, b.scale)
+    assert_max_abs(got, want, 1e-5 if dtype == torch.float32 else 3e-2)
+
+
+def test_torch_path_fp8_pool():
+    b = build_batch([100, 30], [1, 30], dtype=torch.bfloat16, kv_dtype=torch.float8_e4m3fn,
+                    num_q_heads=8, num_kv_heads=2, head_dim=64, seed=2)
+    got = ops.paged_attention(*b.args(), use_cuda=False, k_scale=b.k_scale, v_scale=b.v_scale)
+    want = oracle_paged(b.q, b.key_pool, b.value_pool, b.block_tables, b.cu_seqlens_q,
+                        b.context_lens, b.scale, b.k_scale, b.v_scale)
+    assert_max_abs(got, want, 3e-2)
+
+
+def test_torch_path_elementwise_matches_the_oracle():
+    x = torch.randn(6, 128).to(torch.bfloat16)
+    w = (torch.rand(128) + 0.5).to(torch.bfloat16)
+    got = ops.rmsnorm(x, w).float().numpy()
+    want = ew.rms_norm(x.float().numpy(), w.float().numpy(), 1e-6, "bf16")
+    assert (abs(got - want) <= abs(want) * 2**-7 + 1e-30).all()
+    cos, sin = torch_path.rope_tables(64, 32)
+    xr = torch.randn(1, 5, 3, 64)
+    pos = torch.tensor([0, 3, 9, 31, 2])
+    assert (ops.rope(xr, pos, cos, sin).numpy() ==
+            ew.apply_rope(xr.numpy(), pos.numpy(), cos.numpy(), sin.numpy())).all()
+
+
+def test_dispatch_report_names_every_op():
+    on = ops.dispatch_report(True)
+    off = ops.dispatch_report(False)
+    for name in ops.CUDA_KERNELS:
+        assert name in on and name in off
+    assert "paged_attention    hip" in on
+    assert "use_cuda is off" in off
+    assert set(ops.cuda_kernel_names()) == {"rmsnorm", "rope", "swiglu", "paged_attention"}
+
+
+def test_dense_attention_torch_path_decode_and_causal():
+    q = torch.randn(2, 8, 1, 32)
+    k = torch.randn(2, 4, 10, 32)
+    v = torch.randn(2, 4, 10, 32)
+    out = ops.attention(q, k, v, use_cuda=True)  # no dense kernel: PyTorch path
+    g = 2
+    ref = torch.softmax((q.reshape(2, 4, g, 1, 32) @ k.unsqueeze(2).transpose(-1, -2)) / 32**0.5, -1)
+    ref = (ref @ v.unsqueeze(2)).reshape(2, 8, 1, 32)
+    assert torch.allclose(out, ref, atol=1e-6)

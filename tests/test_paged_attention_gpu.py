@@ -1,0 +1,324 @@
+"""Paged attention on the MI355X against the CPU oracle (``-m gpu``).
+
+The case list follows the reference's kernel tests
+(tests/test_paged_attention_cuda.py:135-447): block/tile boundaries, the split path,
+ragged batches with empty splits, every GQA group size, head dim and block size,
+prefill lengths, the chunk's causal offset, known answers, mixed batches, the shuffle,
+dtypes, refusals and dispatch. BASELINE configs 1-4 are checked at full size.
+
+Tolerances (max-abs vs the fp32 oracle): fp32 2e-5, fp16 1e-2, bf16 2e-2, fp8 KV 6e-2.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import ATTN_ATOL, assert_max_abs
+from mini_vllm.kernels import ops
+from mini_vllm.workloads import build_batch, config_batch, prefill_flops
+from oracle.paged_attention import paged_attention as oracle_paged
+
+pytestmark = pytest.mark.gpu
+
+HQ, HK, D = 8, 4, 64
+
+
+def oracle(b):
+    return oracle_paged(b.q, b.key_pool, b.value_pool, b.block_tables, b.cu_seqlens_q,
+                        b.context_lens, b.scale, b.k_scale, b.v_scale)
+
+
+def kernel(ext, b):
+    out = ext.paged_attention(*b.args(), k_scale=b.k_scale, v_scale=b.v_scale)
+    torch.cuda.synchronize()
+    return out
+
+
+def case(contexts, query_lens, device, **kw):
+    kw.setdefault("num_q_heads", HQ)
+    kw.setdefault("num_kv_heads", HK)
+    kw.setdefault("head_dim", D)
+    kw.setdefault("seed", sum(contexts) + len(contexts))
+    return build_batch(contexts, query_lens, device=device, **kw)
+
+
+def check(ext, b, dtype=None, msg=""):
+    dtype = dtype or b.key_pool.dtype
+    got = kernel(ext, b)
+    assert got.dtype == b.q.dtype
+    assert_max_abs(got, oracle(b), ATTN_ATOL[dtype], msg)
+    return got
+
+
+# --------------------------------------------------------------------- decode
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("context", [1, 15, 16, 17, 63, 64, 65, 200, 1000])
+def test_decode_matches_the_oracle_at_every_boundary(extension, device, context, dtype):
+    check(extension, case([context], [1], device, dtype=dtype), msg=f"context {context}")
+
+
+def test_decode_over_a_long_context_uses_the_split_path(extension, device):
+    b = case([8192], [1], device)
+    plan = extension.paged_attention_plan(1, 1, HQ, HK, D, 16, 1, 8192, b.q.dtype, b.q.dtype)
+    assert plan["max_splits"] > 1
+    check(extension, b)
+
+
+def test_a_ragged_decode_batch_with_empty_splits(extension, device):
+    """Short sequences beside a long one get fewer splits than the grid holds."""
+    b = case([8192, 33, 4096, 17], [1, 1, 1, 1], device)
+    check(extension, b)
+
+
+@pytest.mark.parametrize("split_tokens", ["64", "1024"])
+def test_forced_split_sizes_agree(extension, device, monkeypatch, split_tokens):
+    monkeypatch.setenv("MVLLM_DECODE_SPLIT_TOKENS", split_tokens)
+    check(extension, case([3000, 129, 64, 1], [1, 1, 1, 1], device, dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("kv_heads", [1, 2, 8])
+def test_every_group_size(extension, device, kv_heads):
+    check(extension, case([100], [1], device, num_q_heads=8, num_kv_heads=kv_heads))
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(16, 1), (12, 4), (6, 2)])
+def test_wide_and_odd_groups(extension, device, heads, kv_heads):
+    check(extension, case([300, 7], [1, 1], device, num_q_heads=heads, num_kv_heads=kv_heads))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("head_dim", [32, 64, 128, 256])
+def test_every_head_dimension(extension, device, head_dim, dtype):
+    check(extension, case([100, 250], [1, 1], device, head_dim=head_dim, dtype=dtype))
+
+
+@pytest.mark.parametrize("block_size", [1, 2, 16, 64])
+def test_every_block_size(extension, device, block_size):
+    check(extension, case([100, 1100], [1, 1], device, block_size=block_size))
+
+
+# -------------------------------------------------------------------- prefill
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("length", [2, 8, 9, 16, 17, 64, 300])
+def test_prefill_matches_the_oracle(extension, device, length, dtype):
+    check(extension, case([length], [length], device, dtype=dtype), msg=f"length {length}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_a_chunk_sees_its_prefix_and_not_its_future(extension, device, dtype):
+    check(extension, case([40], [8], device, dtype=dtype))
+
+
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+@pytest.mark.parametrize("heads,kv_heads", [(16, 8), (8, 8), (16, 2), (12, 4)])
+def test_mfma_prefill_shapes(extension, device, head_dim, heads, kv_heads):
+    b = case([700, 130, 97], [200, 130, 33], device, dtype=torch.bfloat16, head_dim=head_dim,
+             num_q_heads=heads, num_kv_heads=kv_heads)
+    check(extension, b)
+
+
+@pytest.mark.parametrize("block_size", [1, 2, 64])
+def test_mfma_prefill_block_sizes(extension, device, block_size):
+    check(extension, case([180, 70], [100, 70], device, dtype=torch.bfloat16,
+                          block_size=block_size, num_q_heads=16, num_kv_heads=8, head_dim=128))
+
+
+def test_the_first_query_of_a_prompt_returns_its_own_value(extension, device):
+    for dtype in (torch.float32, torch.bfloat16):
+        b = case([12], [12], device, dtype=dtype)
+        got = kernel(extension, b)
+        first = b.value_pool[int(b.block_tables[0, 0]), 0]
+        for h in range(HQ):
+            assert torch.equal(got[0, h], first[h // (HQ // HK)]), f"{dtype} head {h}"
+
+
+def test_output_is_a_convex_combination_of_visible_values(extension, device):
+    b = case([64], [64], device)
+    got = kernel(extension, b)
+    visible = torch.stack([b.value_pool[int(x)] for x in b.block_tables[0]])
+    assert got.min() >= visible.min() - 1e-4 and got.max() <= visible.max() + 1e-4
+
+
+# ---------------------------------------------------------------- mixed batch
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_a_mixed_batch_gives_each_sequence_what_it_gets_alone(extension, device, dtype):
+    contexts, lens = [300, 700, 4096, 50], [300, 1, 1, 50]
+    b = case(contexts, lens, device, dtype=dtype)
+    together = kernel(extension, b)
+    for s in range(4):
+        lo, hi = int(b.cu_seqlens_q[s]), int(b.cu_seqlens_q[s + 1])
+        alone = extension.paged_attention(
+            b.q[lo:hi].contiguous(), b.key_pool, b.value_pool, b.block_tables[s:s + 1].contiguous(),
+            torch.tensor([0, hi - lo], dtype=torch.int32, device=device), b.context_lens[s:s + 1],
+            b.seq_lens[s:s + 1], hi - lo, contexts[s], b.scale)
+        torch.cuda.synchronize()
+        assert_max_abs(together[lo:hi], alone, 1e-6 if dtype == torch.float32 else 1e-2,
+                       f"sequence {s} changed in the batch")
+    assert_max_abs(together, oracle(b), ATTN_ATOL[dtype])
+
+
+def test_the_shuffle_is_what_is_being_tested(extension, device):
+    ordered = case([200], [1], device, shuffle=False, spare_blocks=0)
+    shuffled = case([200], [1], device, shuffle=True, spare_blocks=0)
+    assert not torch.equal(ordered.block_tables, shuffled.block_tables)
+    assert torch.equal(ordered.q, shuffled.q)
+    check(extension, ordered)
+    check(extension, shuffled)
+
+
+def test_padding_and_spare_blocks_are_never_read(extension, device):
+    b = case([33, 5, 100], [1, 1, 20], device, dtype=torch.bfloat16, spare_blocks=5)
+    used = {int(x) for x in b.block_tables.flatten().cpu() if int(x) >= 0}
+    for blk in range(b.key_pool.shape[0]):
+        if blk not in used:
+            b.key_pool[blk] = float("nan")
+            b.value_pool[blk] = float("nan")
+    assert torch.isfinite(kernel(extension, b)).all()
+
+
+# -------------------------------------------------------------------- dtypes / fp8
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_low_precision_stays_within_tolerance(extension, device, dtype):
+    check(extension, case([512, 77], [1, 1], device, dtype=dtype))
+
+
+@pytest.mark.parametrize("lens", [([100, 2048, 17], [1, 1, 1]), ([300, 64], [100, 64])])
+def test_fp8_kv_cache(extension, device, lens):
+    b = case(*lens, device, dtype=torch.bfloat16, kv_dtype=torch.float8_e4m3fn,
+             num_q_heads=16, num_kv_heads=8, head_dim=128)
+    check(extension, b, dtype=torch.float8_e4m3fn)
+
+
+def test_fp8_dequantisation_is_exact_for_one_visible_key(extension, device):
+    """With one visible key the output is that key's dequantised value, rounded once."""
+    b = case([12], [12], device, dtype=torch.bfloat16, kv_dtype=torch.float8_e4m3fn,
+             num_q_heads=16, num_kv_heads=8, head_dim=128)
+    got = kernel(extension, b)
+    blk = int(b.block_tables[0, 0])
+    want = (b.value_pool[blk, 0].float() * b.v_scale[blk][:, None]).to(torch.bfloat16)
+    for h in range(16):
+        assert torch.equal(got[0, h], want[h // 2])
+
+
+# ------------------------------------------------------------------- configs
+
+
+def test_config1_fp32_matches_golden_and_oracle(extension, device):
+    b = config_batch(1, device=device)
+    gold = np.load(__import__("pathlib").Path(__file__).parent / "golden" / "paged_cfg1.npz")
+    got = kernel(extension, b)
+    assert_max_abs(got, torch.from_numpy(gold["out"]), 2e-5, "config 1 vs golden")
+    assert_max_abs(got, oracle(b), 2e-5, "config 1 vs oracle")
+
+
+@pytest.mark.slow
+def test_config2_bf16_decode_full_size(extension, device):
+    b = config_batch(2, device=device)
+    check(extension, b, msg="config 2")
+
+
+@pytest.mark.slow
+def test_config3_chunked_prefill_full_size(extension, device):
+    b = config_batch(3, device=device)
+    assert prefill_flops(b) > 1e10
+    check(extension, b, msg="config 3")
+
+
+@pytest.mark.slow
+def test_config4_fp8_decode_subset_of_full_size(extension, device):
+    """Full config-4 batch on the GPU; every 8th sequence checked on the CPU oracle
+    (sequences are independent, so a subset of rows is a complete check of those rows)."""
+    b = config_batch(4, device=device)
+    got = kernel(extension, b)
+    picks = list(range(0, 128, 8))
+    rows = torch.tensor([int(b.cu_seqlens_q[s]) for s in picks])
+    sub = oracle_paged(b.q[rows], b.key_pool, b.value_pool, b.block_tables[picks],
+                       torch.arange(len(picks) + 1, dtype=torch.int32), b.context_lens[picks],
+                       b.scale, b.k_scale, b.v_scale)
+    assert_max_abs(got[rows.to(device)], sub, ATTN_ATOL[torch.float8_e4m3fn], "config 4")
+
+
+def test_repeated_calls_are_deterministic(extension, device):
+    b = case([3000, 40], [1, 40], device, dtype=torch.bfloat16, num_q_heads=16, num_kv_heads=8,
+             head_dim=128)
+    first = kernel(extension, b)
+    for _ in range(3):
+        assert torch.equal(kernel(extension, b), first)
+
+
+# ------------------------------------------------------------------- refusals
+
+
+def _call(ext, b, **over):
+    args = dict(q=b.q, key_pool=b.key_pool, value_pool=b.value_pool,
+                block_tables=b.block_tables, cu_seqlens_q=b.cu_seqlens_q,
+                context_lens=b.context_lens, seq_lens=b.seq_lens, max_query_len=1,
+                max_context_len=64, scale=b.scale)
+    args.update(over)
+    return ext.paged_attention(*args.values())
+
+
+@pytest.mark.parametrize("mutate,message", [
+    (lambda b: dict(key_pool=b.key_pool.narrow(0, 0, b.key_pool.shape[0] - 1)[::2],
+                    value_pool=b.key_pool.narrow(0, 0, b.key_pool.shape[0] - 1)[::2]), "contiguous"),
+    (lambda b: dict(key_pool=b.key_pool.repeat(1, 3, 1, 1)[:, :3].contiguous(),
+                    value_pool=b.key_pool.repeat(1, 3, 1, 1)[:, :3].contiguous()), "power of two"),
+    (lambda b: dict(block_tables=b.block_tables.long()), "int32"),
+    (lambda b: dict(q=b.q.unsqueeze(0)), "T x H_q x D"),
+    (lambda b: dict(max_query_len=8, max_context_len=4), "at least max_query_len"),
+    (lambda b: dict(q=b.q.double(), key_pool=b.key_pool.double(), value_pool=b.value_pool.double()),
+     "float64"),
+    (lambda b: dict(q=b.q.to(torch.bfloat16)), "must share a dtype"),
+])
+def test_refusals(extension, device, mutate, message):
+    b = case([64], [1], device)
+    with pytest.raises(RuntimeError, match=message):
+        _call(extension, b, **mutate(b))
+
+
+def test_fp8_pool_without_scales_is_refused(extension, device):
+    b = case([64], [1], device, dtype=torch.bfloat16, kv_dtype=torch.float8_e4m3fn)
+    with pytest.raises(RuntimeError, match="k_scale"):
+        extension.paged_attention(*b.args())
+
+
+# ------------------------------------------------------------------- dispatch
+
+
+def test_the_op_routes_to_the_kernel(extension, device, monkeypatch):
+    b = case([256], [1], device)
+    calls = []
+    original = extension.paged_attention
+
+    def spy(*args, **kwargs):
+        calls.append(args)
+        return original(*args, **kwargs)
+
+    monkeypatch.setattr(extension, "paged_attention", spy)
+    got = ops.paged_attention(*b.args(), use_cuda=True)
+    torch.cuda.synchronize()
+    assert len(calls) == 1, "use_cuda=True did not reach the kernel"
+    assert_max_abs(got, oracle(b), ATTN_ATOL[torch.float32])
+
+
+def test_use_cuda_never_falls_back(extension, device):
+    b = case([64], [1], device)
+    with pytest.raises(RuntimeError, match="contiguous"):
+        ops.paged_attention(b.q, b.key_pool[::2], b.value_pool[::2], *b.args()[3:],
+                            use_cuda=True)
+
+
+def test_the_torch_path_runs_on_device_without_cuda_requested(extension, device):
+    b = case([256, 30], [1, 30], device)
+    got = ops.paged_attention(*b.args(), use_cuda=False)
+    assert_max_abs(got, oracle(b), 1e-5)
