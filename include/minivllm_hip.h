@@ -47,13 +47,16 @@ int mvllm_abi_version(void);
 /* How one paged_attention call will be executed. Filled by mvllm_paged_attention_plan;
  * the caller allocates `workspace_bytes` of device memory (256-byte aligned) and passes
  * it to mvllm_paged_attention with the same arguments. */
+#define MVLLM_DECODE_NONE 0   /* no decode row: every sequence is a prefill chunk */
+#define MVLLM_DECODE_STREAM 1 /* persistent workgroups, equal shares of all decode keys */
+#define MVLLM_DECODE_GRID 2   /* one workgroup per (sequence, split) */
+#define MVLLM_DECODE_BY_ROW 3 /* one workgroup per (query row, split), prefill rows too */
 typedef struct mvllm_paged_plan {
-  int32_t split_tokens;     /* decode: keys per split (0 when nothing is split) */
-  int32_t max_splits;       /* decode: split-axis grid extent */
-  int32_t decode_by_row;    /* 1: the decode kernel serves every query row, prefill rows
-                               included (no MFMA prefill kernel for this shape/dtype) */
-  int32_t prefill_mfma;     /* 1: prefill rows go to the MFMA prefill kernel */
-  uint64_t workspace_bytes; /* split partials; 0 when no split is needed */
+  int32_t decode_mode;       /* MVLLM_DECODE_* */
+  int32_t decode_workgroups; /* stream: workgroups launched; grid modes: split-axis extent */
+  int32_t split_tokens;      /* grid modes: keys per split */
+  int32_t prefill_mfma;      /* 1: prefill rows go to the MFMA prefill kernel */
+  uint64_t workspace_bytes;  /* partials and metadata; 0 when none are needed */
 } mvllm_paged_plan;
 
 /* Plan a paged_attention call. Depends only on the host-side sizes below (never on

@@ -103,23 +103,64 @@ int check_paged_shape(int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t 
   return MVLLM_OK;
 }
 
-int decode_group_chunk(int group) { return group % 4 == 0 ? 4 : (group % 2 == 0 ? 2 : 1); }
+// A plan plus the workspace layout it implies.
+struct Plan {
+  mvllm_paged_plan pub;
+  int max_splits = 1;
+  uint64_t off_ml = 0;      // byte offsets into the workspace
+  uint64_t off_prefix = 0;
+};
 
-void make_plan(int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk, int32_t d,
+uint64_t align256(uint64_t v) { return (v + 255) / 256 * 256; }
+
+Plan make_plan(int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk, int32_t d,
                int32_t block_size, int32_t max_q, int32_t max_ctx, int32_t q_dtype,
-               int32_t kv_dtype, mvllm_paged_plan* plan) {
+               int32_t kv_dtype) {
+  Plan plan{};
   const bool has_prefill = max_q > 1;
   const bool mfma =
       has_prefill && mvllm::paged_prefill_supported(q_dtype, kv_dtype, d, hq, hk, block_size);
-  plan->prefill_mfma = mfma ? 1 : 0;
-  plan->decode_by_row = (has_prefill && !mfma) ? 1 : 0;
+  // Query lengths are at most max_q and sum to num_tokens, so num_tokens ==
+  // num_seqs * max_q (with max_q > 1) means every sequence is a prefill chunk.
+  const bool all_prefill =
+      has_prefill && static_cast<int64_t>(num_seqs) * max_q == static_cast<int64_t>(num_tokens);
+  const int64_t units = static_cast<int64_t>(hk) * (hq / hk / mvllm::decode_group_chunk(hq / hk));
+  plan.pub.prefill_mfma = mfma ? 1 : 0;
 
-  // Enough (row, kv head, head chunk) waves to keep every CU streaming: split each
-  // row's context until the grid holds ~16 waves per CU, in splits of 64..1024 keys.
-  const int64_t rows = plan->decode_by_row ? num_tokens : num_seqs;
-  const int64_t waves_per_row = static_cast<int64_t>(hk) * (hq / hk / decode_group_chunk(hq / hk));
+  if (has_prefill && !mfma) {
+    plan.pub.decode_mode = MVLLM_DECODE_BY_ROW;
+  } else if (all_prefill || num_seqs == 0) {
+    plan.pub.decode_mode = MVLLM_DECODE_NONE;
+  } else if (num_seqs <= mvllm::kMaxStreamSeqs && units <= 8 &&
+             static_cast<int64_t>(num_seqs) * max_ctx < (int64_t{1} << 31) &&
+             env_int("MVLLM_DECODE_SCHEDULE", 0) != 2) {
+    plan.pub.decode_mode = MVLLM_DECODE_STREAM;
+  } else {
+    plan.pub.decode_mode = MVLLM_DECODE_GRID;
+  }
+
+  if (plan.pub.decode_mode == MVLLM_DECODE_STREAM) {
+    // A few workgroups per CU, each streaming an equal share of all decode keys; no
+    // more workgroups than there are ~64-key shares in the largest possible batch.
+    const int64_t per_cu = env_int("MVLLM_DECODE_WGS_PER_CU", 1);
+    int64_t wgs = (per_cu > 0 ? per_cu : 1) * device_cus();
+    const int64_t by_size = (static_cast<int64_t>(num_seqs) * max_ctx + 63) / 64;
+    if (wgs > by_size) wgs = by_size;
+    if (wgs < 1) wgs = 1;
+    plan.pub.decode_workgroups = static_cast<int32_t>(wgs);
+    const uint64_t entries = static_cast<uint64_t>(wgs + num_seqs) * hq;
+    plan.off_ml = align256(entries * d * sizeof(float));
+    plan.off_prefix = plan.off_ml + align256(entries * 2 * sizeof(float));
+    plan.pub.workspace_bytes = plan.off_prefix + align256((num_seqs + 1) * sizeof(int));
+    return plan;
+  }
+  if (plan.pub.decode_mode == MVLLM_DECODE_NONE) return plan;
+
+  // Grid schedules: split each row's context until the grid holds ~16 waves per CU,
+  // in splits of 64..1024 keys.
+  const int64_t rows = plan.pub.decode_mode == MVLLM_DECODE_BY_ROW ? num_tokens : num_seqs;
   const int64_t target = static_cast<int64_t>(env_int("MVLLM_DECODE_WAVES_PER_CU", 16)) * device_cus();
-  const int64_t single = rows * waves_per_row > 0 ? rows * waves_per_row : 1;
+  const int64_t single = rows * units > 0 ? rows * units : 1;
   const int64_t wanted = (target + single - 1) / single;
   int64_t split = (max_ctx + wanted - 1) / wanted;
   split = (split + 63) / 64 * 64;
@@ -128,14 +169,15 @@ void make_plan(int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk, int
   if (split < 64) split = 64;
   if (split > mvllm::kMaxSplitTokens) split = mvllm::kMaxSplitTokens;
   const int64_t max_splits = (max_ctx + split - 1) / split;
-  plan->split_tokens = static_cast<int32_t>(split);
-  plan->max_splits = static_cast<int32_t>(max_splits < 1 ? 1 : max_splits);
-  plan->workspace_bytes = 0;
-  if (plan->max_splits > 1 && rows > 0) {
-    const uint64_t entries = static_cast<uint64_t>(rows) * hq * plan->max_splits;
-    const uint64_t o_bytes = (entries * d * sizeof(float) + 255) / 256 * 256;
-    plan->workspace_bytes = o_bytes + entries * 2 * sizeof(float);
+  plan.pub.split_tokens = static_cast<int32_t>(split);
+  plan.max_splits = static_cast<int>(max_splits < 1 ? 1 : max_splits);
+  plan.pub.decode_workgroups = plan.max_splits;
+  if (plan.max_splits > 1 && rows > 0) {
+    const uint64_t entries = static_cast<uint64_t>(rows) * hq * plan.max_splits;
+    plan.off_ml = align256(entries * d * sizeof(float));
+    plan.pub.workspace_bytes = plan.off_ml + align256(entries * 2 * sizeof(float));
   }
+  return plan;
 }
 
 }  // namespace
@@ -155,8 +197,9 @@ int mvllm_paged_attention_plan(int32_t num_tokens, int32_t num_seqs, int32_t num
   const int rc = check_paged_shape(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim,
                                    block_size, max_query_len, max_context_len, q_dtype, kv_dtype);
   if (rc != MVLLM_OK) return rc;
-  make_plan(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_query_len,
-            max_context_len, q_dtype, kv_dtype, plan);
+  *plan = make_plan(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
+                    max_query_len, max_context_len, q_dtype, kv_dtype)
+              .pub;
   return MVLLM_OK;
 }
 
@@ -189,15 +232,18 @@ int mvllm_paged_attention(void* out, const void* q, const void* key_pool,
                 "paged_attention: k_scales and v_scales are required for a float8 pool and "
                 "only for one");
   }
-  mvllm_paged_plan plan;
-  make_plan(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, max_query_len,
-            max_context_len, q_dtype, kv_dtype, &plan);
-  if (plan.workspace_bytes > 0 && (workspace == nullptr || workspace_bytes < plan.workspace_bytes)) {
+  const Plan plan = make_plan(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                              block_size, max_query_len, max_context_len, q_dtype, kv_dtype);
+  const uint64_t need = plan.pub.workspace_bytes;
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     return fail(MVLLM_ERR_WORKSPACE,
                 "paged_attention: workspace of %llu bytes is smaller than the %llu the plan "
                 "needs (call mvllm_paged_attention_plan)",
                 static_cast<unsigned long long>(workspace_bytes),
-                static_cast<unsigned long long>(plan.workspace_bytes));
+                static_cast<unsigned long long>(need));
+  }
+  if (need > 0 && reinterpret_cast<uintptr_t>(workspace) % 256 != 0) {
+    return fail(MVLLM_ERR_INVALID, "paged_attention: the workspace must be 256-byte aligned");
   }
 
   int shift = 0;
@@ -221,30 +267,25 @@ int mvllm_paged_attention(void* out, const void* q, const void* key_pool,
   p.max_blocks = max_blocks_per_seq;
   p.block_shift = shift;
   p.block_mask = block_size - 1;
-  p.split_tokens = plan.split_tokens;
+  p.stream_wgs = plan.pub.decode_mode == MVLLM_DECODE_STREAM ? plan.pub.decode_workgroups : 0;
+  p.split_tokens = plan.pub.split_tokens > 0 ? plan.pub.split_tokens : mvllm::kMaxSplitTokens;
   p.max_splits = plan.max_splits;
-  p.by_row = plan.decode_by_row;
+  p.by_row = plan.pub.decode_mode == MVLLM_DECODE_BY_ROW ? 1 : 0;
   p.scale = scale;
-  if (plan.workspace_bytes > 0) {
-    const uint64_t entries = static_cast<uint64_t>(plan.decode_by_row ? num_tokens : num_seqs) *
-                             num_q_heads * plan.max_splits;
-    const uint64_t o_bytes = (entries * head_dim * sizeof(float) + 255) / 256 * 256;
-    p.part_o = static_cast<float*>(workspace);
-    p.part_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) + o_bytes);
+  if (need > 0) {
+    char* ws = static_cast<char*>(workspace);
+    p.part_o = reinterpret_cast<float*>(ws);
+    p.part_ml = reinterpret_cast<float*>(ws + plan.off_ml);
+    if (plan.off_prefix > 0) p.seq_prefix = reinterpret_cast<int*>(ws + plan.off_prefix);
   }
 
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  // Every query length is at most max_query_len and they sum to num_tokens, so when
-  // num_tokens == num_seqs * max_query_len every sequence is a prefill chunk (if
-  // max_query_len > 1) and no decode row exists: skip that launch.
-  const bool all_prefill =
-      max_query_len > 1 && static_cast<int64_t>(num_seqs) * max_query_len == num_tokens;
-  if (plan.decode_by_row || !all_prefill) {
+  if (plan.pub.decode_mode != MVLLM_DECODE_NONE) {
     rc = hip_status(mvllm::launch_paged_decode(p, q_dtype, kv_dtype, head_dim, s),
                     "paged_attention: decode launch");
     if (rc != MVLLM_OK) return rc;
   }
-  if (plan.prefill_mfma) {
+  if (plan.pub.prefill_mfma) {
     rc = hip_status(mvllm::launch_paged_prefill(p, q_dtype, kv_dtype, head_dim, max_query_len, s),
                     "paged_attention: prefill launch");
     if (rc != MVLLM_OK) return rc;

@@ -8,9 +8,10 @@
 //            csrc/rmsnorm.cu:80-87): fp32 reduction, round before the weight multiply.
 //   rope     out = T(x*cos[pos] + rotate_half(x)*sin[pos]) in fp32 with the two
 //            products rounded separately (positional_encoding.py:58-62); products are
-//            computed with FMA contraction switched off (`#pragma clang fp contract(off)`
-//            in each kernel: HIP compiles device code with -ffp-contract=fast, which would
-//            otherwise fuse x*cos - y*sin into one FMA and round once instead of three times).
+//            rounded on their own: this file is compiled with -ffp-contract=off (the
+//            build sets it), since HIP's default contraction fuses x*cos - y*sin into one
+//            FMA that rounds once where the reference rounds three times. A pragma is not
+//            enough: the products come from inlined header functions.
 //   swiglu   out = T(T(g * T(sigmoid(g))) * u) (basics.py:39-41, csrc/swiglu.cu:48-51),
 //            sigmoid = 1 / (1 + expf(-g)).
 
@@ -28,7 +29,6 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const void* __restrict
                                                           const void* __restrict__ w,
                                                           void* __restrict__ out, int64_t rows,
                                                           int dim, float eps) {
-#pragma clang fp contract(off)
   constexpr int E = Chunk<T>::kN;
   const int lane = threadIdx.x % kWave;
   const int64_t row = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kR;
@@ -94,7 +94,6 @@ __global__ __launch_bounds__(256) void rmsnorm_scalar_kernel(const void* __restr
                                                              const void* __restrict__ w,
                                                              void* __restrict__ out, int64_t rows,
                                                              int dim, float eps) {
-#pragma clang fp contract(off)
   const int64_t row = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
   const int lane = threadIdx.x % kWave;
   if (row >= rows) return;  // whole wave leaves together
@@ -181,7 +180,6 @@ __global__ __launch_bounds__(256) void rope_kernel(const void* __restrict__ x,
                                                    void* __restrict__ out, int64_t pairs, int half,
                                                    int64_t heads, int64_t num_positions,
                                                    int64_t max_positions) {
-#pragma clang fp contract(off)
   const int64_t index = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (index >= pairs) return;
   const int64_t row = index / half;
@@ -241,7 +239,6 @@ hipError_t launch_rope(const void* x, const void* positions, int pos_bytes, cons
 
 template <typename T>
 __device__ __forceinline__ float swiglu_one(float g, float u) {
-#pragma clang fp contract(off)
   const float sig = Elem<T>::round(1.0f / (1.0f + expf(-g)));
   const float act = Elem<T>::round(__fmul_rn(g, sig));
   return __fmul_rn(act, u);

@@ -13,6 +13,14 @@ namespace mvllm {
 constexpr int kMaxSplitPages = 1040;
 constexpr int kMaxSplitTokens = 1024;
 
+// The stream schedule scans the context lengths of up to this many sequences in LDS.
+constexpr int kMaxStreamSeqs = 4096;
+
+// Query heads per decode wave for a GQA group of `group` heads.
+__host__ __device__ inline int decode_group_chunk(int group) {
+  return group % 4 == 0 ? 4 : (group % 2 == 0 ? 2 : 1);
+}
+
 struct PagedParams {
   const void* q;
   const void* k_pool;
@@ -31,12 +39,14 @@ struct PagedParams {
   int max_blocks;
   int block_shift;
   int block_mask;
-  int split_tokens;   // decode: nominal keys per split
-  int max_splits;     // decode: grid extent along the split axis
-  int by_row;         // decode: 1 = one unit per query row (serves prefill rows too)
+  int stream_wgs;     // decode: > 0 selects the stream schedule with this many workgroups
+  int split_tokens;   // grid decode: nominal keys per split
+  int max_splits;     // grid decode: grid extent along the split axis
+  int by_row;         // grid decode: 1 = one unit per query row (serves prefill rows too)
   float scale;
-  float* part_o;      // [units, H_q, max_splits, D] fp32
-  float* part_ml;     // [units, H_q, max_splits, 2] fp32 (running max in log2 units, sum)
+  float* part_o;      // split partials, D fp32 each
+  float* part_ml;     // split partials' (running max in log2 units, sum)
+  int* seq_prefix;    // stream decode: [num_seqs + 1] decode keys before each sequence
 };
 
 // Splits of one row: as many as its visible context needs at `split_tokens` keys

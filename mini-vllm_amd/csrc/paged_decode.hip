@@ -6,24 +6,36 @@
 // keys that the sequence's block table maps to physical slots
 // (slot = table[p >> shift] << shift | (p & mask), paged_attention.cu:87-93).
 //
-// The work decomposition is this library's own:
+// The work decomposition is this library's own.
 //
-//  * one workgroup per (sequence or row, split); one wave per (kv head, chunk of up
-//    to four query heads of that head's GQA group). The wave holds the queries of
-//    its whole group in registers, so each K/V byte is fetched from HBM exactly
-//    once however many query heads share it.
-//  * inside a wave, a token's (kv head) row is D elements = D / E lanes of 16 bytes
-//    (E = 8 for bf16/fp16, 4 for fp32, 16 for fp8). The 64 lanes split into
-//    64 / (D / E) row groups, each streaming its own tokens with its own online
-//    softmax state, so the main loop needs no cross-row-group traffic and no
-//    barrier: a dot product is reduced with 16-lane DPP all-reduces only.
-//  * the row groups, and then the splits, are merged with the same rescale
-//    exp(m_i - M) the reference uses one level up (paged_attention.cu:284-301).
-//  * the split's physical page ids are staged once into LDS and shared by all
-//    waves of the workgroup (every kv head of the split walks the same pages).
+// Inside a workgroup: one wave per (kv head, chunk of up to four query heads of that
+// head's GQA group). The wave holds the queries of its group in registers, so each
+// K/V byte is fetched from HBM exactly once however many query heads share it. A
+// token's (kv head) row is D elements = D / E lanes of 16 bytes (E = 8 for bf16/fp16,
+// 4 for fp32, 16 for fp8); the 64 lanes split into 64 / (D / E) row groups, each
+// streaming its own tokens with its own online-softmax state, so the main loop needs
+// no cross-row-group traffic and no barrier: a dot product is reduced with 16-lane DPP
+// all-reduces only. Row groups are merged once at the end with the reference's
+// rescale exp(m_i - M) (paged_attention.cu:284-301).
 //
-// Scores are kept in the log2 domain: s = (q.k) * scale * log2(e), p = 2^(s - m).
-// That is exp((q.k)*scale - max) exactly in real arithmetic and costs one v_exp_f32.
+// Across workgroups, two schedules:
+//
+//  * stream (the decode hot path): a persistent grid of a few workgroups per CU. The
+//    decode sequences' keys are laid end to end (an in-kernel prefix scan of
+//    context_lens, no host read) and every workgroup streams an equal share of that
+//    token axis, so every CU moves the same bytes whatever the length distribution.
+//    A share that covers a whole sequence writes its output directly; a sequence cut
+//    between workgroups leaves one (m, l, O) partial per piece, in slot
+//    (workgroup + sequence), which is unique because shares and sequences are both
+//    contiguous ranges of the same axis. A small merge kernel combines the pieces.
+//  * grid (fallback, and the by-row mode that also serves prefill rows when no MFMA
+//    prefill kernel fits the shape): one workgroup per (row, split) with splits of
+//    `split_tokens` keys, page ids staged in LDS, merged by a second kernel.
+//
+// K/V are read with nontemporal 16-byte loads (they are streamed once); page ids are
+// fetched one step ahead of the K/V loads that need them. Scores are kept in the
+// log2 domain: s = (q.k) * scale * log2(e), p = 2^(s - m), exactly
+// exp((q.k)*scale - max) in real arithmetic, at one v_exp_f32 per score.
 
 #include "common.hpp"
 #include "paged_attention.hpp"
@@ -33,17 +45,20 @@ namespace mvllm {
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kUnroll = 4;  // tokens in flight per row group per iteration
+constexpr int kUnroll = 4;  // tokens in flight per row group per step
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Which query row, sequence and visible context a decode workgroup serves.
+__device__ __forceinline__ u32x4 load16_stream(const char* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+// Which query row, sequence and visible context a grid-schedule workgroup serves.
 // Returns false when the workgroup has nothing to do in this pass.
 __device__ __forceinline__ bool resolve_row(const PagedParams& p, int index, int& seq, int& row,
                                             int& visible) {
   if (p.by_row) {
-    // Every query row is a unit (the fallback that also serves prefill rows):
-    // find its sequence by binary search over cu_seqlens_q.
+    // Every query row is a unit: find its sequence by binary search over cu_seqlens_q.
     row = index;
     int lo = 0, hi = p.num_seqs - 1;
     while (lo < hi) {
@@ -65,16 +80,366 @@ __device__ __forceinline__ bool resolve_row(const PagedParams& p, int index, int
   return visible > 0;
 }
 
+// Per-wave online-softmax state over a run of keys, for GC query heads.
+template <int GC, int E>
+struct WaveState {
+  float m[GC];
+  float l[GC];
+  float acc[GC][E];
+};
+
+template <typename TKV, int D, int GC>
+struct Decode {
+  static constexpr int E = Chunk<TKV>::kN;   // elements per 16-byte chunk
+  static constexpr int R = D / E;            // lanes per token row
+  static constexpr int RG = kWave / R;       // row groups per wave
+  static constexpr bool kFp8 = Elem<TKV>::kBytes == 1;
+  static_assert(R >= 1 && R <= kWave && (kWave % R) == 0, "head dim / dtype mismatch");
+  using State = WaveState<GC, E>;
+
+  template <typename TQ>
+  __device__ static void load_queries(const PagedParams& p, int row, int h0, int r,
+                                      float (&qf)[GC][E]) {
+#pragma unroll
+    for (int h = 0; h < GC; ++h) {
+      const int64_t base = (static_cast<int64_t>(row) * p.hq + h0 + h) * D + r * E;
+#pragma unroll
+      for (int e = 0; e < E; ++e) qf[h][e] = Elem<TQ>::load(p.q, base + e);
+    }
+  }
+
+  __device__ static void init(State& st) {
+#pragma unroll
+    for (int h = 0; h < GC; ++h) {
+      st.m[h] = -INFINITY;
+      st.l[h] = 0.0f;
+#pragma unroll
+      for (int e = 0; e < E; ++e) st.acc[h][e] = 0.0f;
+    }
+  }
+
+  // Stream keys [sb, se) of one sequence for kv head `kvh` into `st`. Page ids come
+  // from `lds_pages` (page i of the run at lds_pages[i - first_page]) when given,
+  // otherwise from the sequence's block table.
+  __device__ static void stream(const PagedParams& p, const int32_t* table, const int* lds_pages,
+                                int first_page, int kvh, int sb, int se, int g, int r,
+                                const float (&qf)[GC][E], float score_scale, State& st) {
+    const char* kbase = static_cast<const char*>(p.k_pool);
+    const char* vbase = static_cast<const char*>(p.v_pool);
+    constexpr int kElemBytes = Elem<TKV>::kBytes;
+    constexpr int kStep = RG * kUnroll;
+
+    auto page_of = [&](int tok) -> int {
+      const int pi = tok >> p.block_shift;
+      return lds_pages != nullptr ? lds_pages[pi - first_page] : table[pi];
+    };
+
+    int pg[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) pg[u] = page_of(min(sb + u * RG + g, se - 1));
+
+    for (int t0 = sb; t0 < se; t0 += kStep) {
+      u32x4 kw[kUnroll], vw[kUnroll];
+      bool valid[kUnroll];
+      float ks[kUnroll], vs[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        int tok = t0 + u * RG + g;
+        valid[u] = tok < se;
+        tok = valid[u] ? tok : se - 1;
+        const int64_t slot = (static_cast<int64_t>(pg[u]) << p.block_shift) | (tok & p.block_mask);
+        const int64_t off = ((slot * p.hk + kvh) * D + r * E) * kElemBytes;
+        kw[u] = load16_stream(kbase + off);
+        vw[u] = load16_stream(vbase + off);
+        if constexpr (kFp8) {
+          ks[u] = p.k_scales[static_cast<int64_t>(pg[u]) * p.hk + kvh];
+          vs[u] = p.v_scales[static_cast<int64_t>(pg[u]) * p.hk + kvh];
+        }
+      }
+      // Page ids of the next step, in flight while this step computes.
+      if (t0 + kStep < se) {
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) pg[u] = page_of(min(t0 + kStep + u * RG + g, se - 1));
+      }
+
+      float s[kUnroll][GC];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        float kf[E];
+        Chunk<TKV>::unpack(kw[u], kf);
+#pragma unroll
+        for (int h = 0; h < GC; ++h) {
+          float dot = 0.0f;
+#pragma unroll
+          for (int e = 0; e < E; ++e) dot = fmaf(qf[h][e], kf[e], dot);
+          dot = group_sum<R>(dot);
+          // The reference scales after the reduction (paged_attention.cu:181-183).
+          float sc = dot * score_scale;
+          if constexpr (kFp8) sc *= ks[u];
+          s[u][h] = valid[u] ? sc : -INFINITY;
+        }
+      }
+
+      float pr[kUnroll][GC];
+#pragma unroll
+      for (int h = 0; h < GC; ++h) {
+        float mx = st.m[h];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) mx = fmaxf(mx, s[u][h]);
+        // A row group that has seen no valid key yet keeps m = -inf; exponentiate
+        // against 0 then, so 2^(-inf - 0) = 0 instead of 2^(-inf + inf) = NaN
+        // (the empty-split rule of paged_attention.cu:210-213).
+        const float mu = mx == -INFINITY ? 0.0f : mx;
+        const float alpha = fast_exp2(st.m[h] - mu);
+        float sum = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          pr[u][h] = fast_exp2(s[u][h] - mu);
+          sum += pr[u][h];
+        }
+        st.l[h] = st.l[h] * alpha + sum;
+        st.m[h] = mx;
+#pragma unroll
+        for (int e = 0; e < E; ++e) st.acc[h][e] *= alpha;
+      }
+
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        float vf[E];
+        Chunk<TKV>::unpack(vw[u], vf);
+#pragma unroll
+        for (int h = 0; h < GC; ++h) {
+          float w = pr[u][h];
+          if constexpr (kFp8) w *= vs[u];
+#pragma unroll
+          for (int e = 0; e < E; ++e) st.acc[h][e] = fmaf(w, vf[e], st.acc[h][e]);
+        }
+      }
+    }
+  }
+
+  // Combine the wave's row groups: xor partners share r and differ in g. Afterwards
+  // every row group holds the totals.
+  __device__ static void merge_row_groups(State& st) {
+#pragma unroll
+    for (int off = R; off < kWave; off <<= 1) {
+#pragma unroll
+      for (int h = 0; h < GC; ++h) {
+        const float mo = __shfl_xor(st.m[h], off, kWave);
+        const float lo = __shfl_xor(st.l[h], off, kWave);
+        const float mx = fmaxf(st.m[h], mo);
+        const float mu = mx == -INFINITY ? 0.0f : mx;
+        const float a = fast_exp2(st.m[h] - mu);
+        const float b = fast_exp2(mo - mu);
+        st.l[h] = st.l[h] * a + lo * b;
+        st.m[h] = mx;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const float other = __shfl_xor(st.acc[h][e], off, kWave);
+          st.acc[h][e] = st.acc[h][e] * a + other * b;
+        }
+      }
+    }
+  }
+
+  template <typename TQ>
+  __device__ static void write_output(const PagedParams& p, int row, int h0, int r, const State& st) {
+#pragma unroll
+    for (int h = 0; h < GC; ++h) {
+      const float inv = st.l[h] > 0.0f ? 1.0f / st.l[h] : 0.0f;
+      const int64_t base = (static_cast<int64_t>(row) * p.hq + h0 + h) * D + r * E;
+#pragma unroll
+      for (int e = 0; e < E; ++e) Elem<TQ>::store(p.out, base + e, st.acc[h][e] * inv);
+    }
+  }
+
+  // Partial of head h0 + h at index (pidx0 + h * pstride).
+  __device__ static void write_partial(const PagedParams& p, int64_t pidx0, int64_t pstride, int r,
+                                       const State& st) {
+#pragma unroll
+    for (int h = 0; h < GC; ++h) {
+      const int64_t pidx = pidx0 + h * pstride;
+      float* po = p.part_o + pidx * D + r * E;
+#pragma unroll
+      for (int e = 0; e < E; e += 4) {
+        *reinterpret_cast<f32x4*>(po + e) =
+            f32x4{st.acc[h][e], st.acc[h][e + 1], st.acc[h][e + 2], st.acc[h][e + 3]};
+      }
+      if (r == 0) {
+        p.part_ml[pidx * 2] = st.m[h];
+        p.part_ml[pidx * 2 + 1] = st.l[h];
+      }
+    }
+  }
+};
+
+// The (kv head, head chunk) unit of a wave; false when the wave has none.
+template <int GC>
+__device__ __forceinline__ bool wave_unit(const PagedParams& p, int unit, int& kvh, int& h0) {
+  const int chunks = p.hq / p.hk / GC;
+  if (unit >= p.hk * chunks) return false;
+  kvh = unit / chunks;
+  h0 = kvh * (p.hq / p.hk) + (unit % chunks) * GC;
+  return true;
+}
+
 }  // namespace
 
-template <typename TQ, typename TKV, int D, int GC>
-__global__ __launch_bounds__(512) void paged_decode_kernel(const PagedParams p) {
-  constexpr int E = Chunk<TKV>::kN;        // elements per 16-byte chunk
-  constexpr int R = D / E;                 // lanes per token row
-  constexpr int RG = kWave / R;            // row groups per wave
-  static_assert(R >= 1 && R <= kWave && (kWave % R) == 0, "head dim / dtype mismatch");
-  constexpr bool kFp8 = Elem<TKV>::kBytes == 1;
+// ------------------------------------------------------------ stream schedule
 
+template <typename TQ, typename TKV, int D, int GC>
+__global__ __launch_bounds__(512) void paged_decode_stream_kernel(const PagedParams p) {
+  using K = Decode<TKV, D, GC>;
+  __shared__ int s_prefix[kMaxStreamSeqs + 1];  // decode keys before sequence s
+
+  const int n = p.num_seqs;
+  const int tid = threadIdx.x;
+  // Prefix scan of the decode sequences' context lengths (0 for prefill chunks), by
+  // wave 0: each lane sums a contiguous run, then a 64-lane inclusive scan.
+  if (tid < kWave) {
+    const int per = (n + kWave - 1) / kWave;
+    const int begin = min(tid * per, n);
+    const int end = min(begin + per, n);
+    int run = 0;
+    for (int s = begin; s < end; ++s) run += p.seq_lens[s] == 1 ? max(p.context_lens[s], 0) : 0;
+    int incl = run;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int other = __shfl_up(incl, off, kWave);
+      if (tid >= off) incl += other;
+    }
+    int acc = incl - run;
+    for (int s = begin; s < end; ++s) {
+      s_prefix[s] = acc;
+      acc += p.seq_lens[s] == 1 ? max(p.context_lens[s], 0) : 0;
+    }
+    if (tid == kWave - 1) s_prefix[n] = incl;
+  }
+  __syncthreads();
+
+  const int64_t total = s_prefix[n];
+  const int64_t wgs = gridDim.x;
+  if (blockIdx.x == 0) {
+    for (int s = tid; s <= n; s += blockDim.x) p.seq_prefix[s] = s_prefix[s];
+  }
+  const int64_t lo = static_cast<int64_t>(blockIdx.x) * total / wgs;
+  const int64_t hi = (static_cast<int64_t>(blockIdx.x) + 1) * total / wgs;
+  if (lo >= hi) return;
+
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+  const int g = lane / K::R;
+  const int r = lane % K::R;
+  int kvh, h0;
+  if (!wave_unit<GC>(p, wave, kvh, h0)) return;
+  const float score_scale = p.scale * kLog2e;
+
+  // First sequence whose keys include `lo`: the last s with prefix[s] <= lo.
+  int a = 0, b = n;  // invariant: prefix[a] <= lo < prefix[b]
+  while (b - a > 1) {
+    const int mid = (a + b) >> 1;
+    if (s_prefix[mid] <= lo) a = mid; else b = mid;
+  }
+  int seq = a;
+  int64_t pos = lo;
+  while (pos < hi) {
+    while (s_prefix[seq + 1] == s_prefix[seq]) ++seq;  // skip prefill / empty sequences
+    const int base = s_prefix[seq];
+    const int ctx = s_prefix[seq + 1] - base;
+    const int sb = static_cast<int>(pos - base);
+    const int se = static_cast<int>(min(hi, static_cast<int64_t>(s_prefix[seq + 1])) - base);
+    const int row = p.cu_seqlens_q[seq];
+
+    float qf[GC][K::E];
+    K::template load_queries<TQ>(p, row, h0, r, qf);
+    typename K::State st;
+    K::init(st);
+    const int32_t* table = p.block_tables + static_cast<int64_t>(seq) * p.max_blocks;
+    K::stream(p, table, nullptr, 0, kvh, sb, se, g, r, qf, score_scale, st);
+    K::merge_row_groups(st);
+    if (g == 0) {
+      if (sb == 0 && se == ctx) {
+        K::template write_output<TQ>(p, row, h0, r, st);
+      } else {
+        const int64_t slot = static_cast<int64_t>(blockIdx.x) + seq;
+        K::write_partial(p, slot * p.hq + h0, 1, r, st);
+      }
+    }
+    pos = base + se;
+    ++seq;
+  }
+}
+
+// Combine the pieces of every decode sequence that was cut between workgroups.
+// One wave per (sequence, query head); lanes cover the head dim.
+template <typename TQ, int D>
+__global__ __launch_bounds__(256) void paged_decode_stream_merge_kernel(const PagedParams p,
+                                                                        int wgs) {
+  constexpr int kPerLane = (D + kWave - 1) / kWave;
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int head = blockIdx.x * (blockDim.x / kWave) + wave;
+  const int seq = blockIdx.y;
+  if (head >= p.hq) return;
+  const int64_t total = p.seq_prefix[p.num_seqs];
+  const int64_t begin = p.seq_prefix[seq];
+  const int64_t end = p.seq_prefix[seq + 1];
+  if (end == begin || total == 0) return;
+  // Workgroup owning key x: the largest w with floor(w * total / wgs) <= x.
+  const int first = static_cast<int>(((begin + 1) * wgs - 1) / total);
+  const int last = static_cast<int>((end * wgs - 1) / total);
+  if (first == last) return;  // one piece: the decode kernel stored the output
+  const int pieces = last - first + 1;
+  const int64_t pidx0 = (static_cast<int64_t>(first) + seq) * p.hq + head;
+  const int64_t pstride = p.hq;
+
+  // A workgroup whose share is empty (only when there are fewer keys than workgroups)
+  // owns no key and wrote no partial: its slot is skipped.
+  auto live = [&](int i) {
+    const int64_t w = first + i;
+    return (w * total) / wgs < ((w + 1) * total) / wgs;
+  };
+  float mmax = -INFINITY;
+  for (int i = lane; i < pieces; i += kWave) {
+    if (live(i)) mmax = fmaxf(mmax, p.part_ml[(pidx0 + i * pstride) * 2]);
+  }
+  mmax = wave_max(mmax);
+  const float mu = mmax == -INFINITY ? 0.0f : mmax;
+  float total_l = 0.0f;
+  for (int i = lane; i < pieces; i += kWave) {
+    const int64_t pidx = pidx0 + i * pstride;
+    if (live(i)) total_l += __builtin_amdgcn_exp2f(p.part_ml[pidx * 2] - mu) * p.part_ml[pidx * 2 + 1];
+  }
+  total_l = wave_sum(total_l);
+  const float inv = total_l > 0.0f ? 1.0f / total_l : 0.0f;
+
+  float o[kPerLane];
+#pragma unroll
+  for (int i = 0; i < kPerLane; ++i) o[i] = 0.0f;
+  for (int i = 0; i < pieces; ++i) {
+    if (!live(i)) continue;
+    const int64_t pidx = pidx0 + i * pstride;
+    const float w = __builtin_amdgcn_exp2f(p.part_ml[pidx * 2] - mu);
+    const float* po = p.part_o + pidx * D;
+#pragma unroll
+    for (int k = 0; k < kPerLane; ++k) {
+      const int d = lane + k * kWave;
+      if (d < D) o[k] = fmaf(w, po[d], o[k]);
+    }
+  }
+  const int64_t base = (static_cast<int64_t>(p.cu_seqlens_q[seq]) * p.hq + head) * D;
+#pragma unroll
+  for (int k = 0; k < kPerLane; ++k) {
+    const int d = lane + k * kWave;
+    if (d < D) Elem<TQ>::store(p.out, base + d, o[k] * inv);
+  }
+}
+
+// -------------------------------------------------------------- grid schedule
+
+template <typename TQ, typename TKV, int D, int GC>
+__global__ __launch_bounds__(512) void paged_decode_grid_kernel(const PagedParams p) {
+  using K = Decode<TKV, D, GC>;
   __shared__ int s_pages[kMaxSplitPages];
 
   int seq, row, visible;
@@ -90,8 +455,8 @@ __global__ __launch_bounds__(512) void paged_decode_kernel(const PagedParams p) 
   const int partial_row = p.by_row ? row : seq;
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
-  const int g = lane / R;   // row group
-  const int r = lane % R;   // chunk within the row
+  const int g = lane / K::R;
+  const int r = lane % K::R;
 
   const int32_t* table = p.block_tables + static_cast<int64_t>(seq) * p.max_blocks;
   const int first_page = sb >> p.block_shift;
@@ -102,162 +467,29 @@ __global__ __launch_bounds__(512) void paged_decode_kernel(const PagedParams p) 
   }
   __syncthreads();
 
-  const int chunks = p.hq / p.hk / GC;                       // head chunks per kv head
-  const int unit = blockIdx.z * (blockDim.x / kWave) + wave;  // (kv head, chunk)
-  if (unit >= p.hk * chunks) return;
-  const int kvh = unit / chunks;
-  const int h0 = kvh * (p.hq / p.hk) + (unit % chunks) * GC;
+  int kvh, h0;
+  if (!wave_unit<GC>(p, blockIdx.z * (blockDim.x / kWave) + wave, kvh, h0)) return;
 
-  // Queries of the wave's heads, this lane's E dims, pre-scaled into log2 units.
-  float qf[GC][E];
-#pragma unroll
-  for (int h = 0; h < GC; ++h) {
-    const int64_t base = (static_cast<int64_t>(row) * p.hq + h0 + h) * D + r * E;
-#pragma unroll
-    for (int e = 0; e < E; ++e) qf[h][e] = Elem<TQ>::load(p.q, base + e);
-  }
-  const float score_scale = p.scale * kLog2e;
-
-  float m[GC], l[GC], acc[GC][E];
-#pragma unroll
-  for (int h = 0; h < GC; ++h) {
-    m[h] = -INFINITY;
-    l[h] = 0.0f;
-#pragma unroll
-    for (int e = 0; e < E; ++e) acc[h][e] = 0.0f;
-  }
-
-  const char* kbase = static_cast<const char*>(p.k_pool);
-  const char* vbase = static_cast<const char*>(p.v_pool);
-  constexpr int kElemBytes = Elem<TKV>::kBytes;
-
-  for (int t0 = sb; t0 < se; t0 += RG * kUnroll) {
-    u32x4 kw[kUnroll], vw[kUnroll];
-    bool valid[kUnroll];
-    float ks[kUnroll], vs[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      int tok = t0 + u * RG + g;
-      valid[u] = tok < se;
-      tok = valid[u] ? tok : se - 1;
-      const int pi = tok >> p.block_shift;
-      const int page = pages_in_lds ? s_pages[pi - first_page] : table[pi];
-      const int64_t slot = (static_cast<int64_t>(page) << p.block_shift) | (tok & p.block_mask);
-      const int64_t off = ((slot * p.hk + kvh) * D + r * E) * kElemBytes;
-      kw[u] = load16(kbase + off);
-      vw[u] = load16(vbase + off);
-      if constexpr (kFp8) {
-        ks[u] = p.k_scales[static_cast<int64_t>(page) * p.hk + kvh];
-        vs[u] = p.v_scales[static_cast<int64_t>(page) * p.hk + kvh];
-      }
-    }
-
-    float s[kUnroll][GC];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      float kf[E];
-      Chunk<TKV>::unpack(kw[u], kf);
-#pragma unroll
-      for (int h = 0; h < GC; ++h) {
-        float dot = 0.0f;
-#pragma unroll
-        for (int e = 0; e < E; ++e) dot = fmaf(qf[h][e], kf[e], dot);
-        dot = group_sum<R>(dot);
-        // The reference scales after the reduction (paged_attention.cu:181-183).
-        float sc = dot * score_scale;
-        if constexpr (kFp8) sc *= ks[u];
-        s[u][h] = valid[u] ? sc : -INFINITY;
-      }
-    }
-
-    float pr[kUnroll][GC];
-#pragma unroll
-    for (int h = 0; h < GC; ++h) {
-      float mx = m[h];
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) mx = fmaxf(mx, s[u][h]);
-      // A row group that has seen no valid key yet keeps m = -inf; exponentiate
-      // against 0 then, so 2^(-inf - 0) = 0 instead of 2^(-inf + inf) = NaN
-      // (the empty-split rule of paged_attention.cu:210-213).
-      const float mu = mx == -INFINITY ? 0.0f : mx;
-      const float alpha = fast_exp2(m[h] - mu);
-      float sum = 0.0f;
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        pr[u][h] = fast_exp2(s[u][h] - mu);
-        sum += pr[u][h];
-      }
-      l[h] = l[h] * alpha + sum;
-      m[h] = mx;
-#pragma unroll
-      for (int e = 0; e < E; ++e) acc[h][e] *= alpha;
-    }
-
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      float vf[E];
-      Chunk<TKV>::unpack(vw[u], vf);
-#pragma unroll
-      for (int h = 0; h < GC; ++h) {
-        float w = pr[u][h];
-        if constexpr (kFp8) w *= vs[u];
-#pragma unroll
-        for (int e = 0; e < E; ++e) acc[h][e] = fmaf(w, vf[e], acc[h][e]);
-      }
-    }
-  }
-
-  // Merge the wave's row groups: xor partners share r and differ in g.
-#pragma unroll
-  for (int off = R; off < kWave; off <<= 1) {
-#pragma unroll
-    for (int h = 0; h < GC; ++h) {
-      const float mo = __shfl_xor(m[h], off, kWave);
-      const float lo = __shfl_xor(l[h], off, kWave);
-      const float mx = fmaxf(m[h], mo);
-      const float mu = mx == -INFINITY ? 0.0f : mx;
-      const float a = fast_exp2(m[h] - mu);
-      const float b = fast_exp2(mo - mu);
-      l[h] = l[h] * a + lo * b;
-      m[h] = mx;
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        const float other = __shfl_xor(acc[h][e], off, kWave);
-        acc[h][e] = acc[h][e] * a + other * b;
-      }
-    }
-  }
-
-  if (g != 0) return;  // every row group now holds the same totals; one writes
+  float qf[GC][K::E];
+  K::template load_queries<TQ>(p, row, h0, r, qf);
+  typename K::State st;
+  K::init(st);
+  K::stream(p, table, pages_in_lds ? s_pages : nullptr, first_page, kvh, sb, se, g, r, qf,
+            p.scale * kLog2e, st);
+  K::merge_row_groups(st);
+  if (g != 0) return;
   if (nsplit == 1) {
-#pragma unroll
-    for (int h = 0; h < GC; ++h) {
-      const float inv = l[h] > 0.0f ? 1.0f / l[h] : 0.0f;
-      const int64_t base = (static_cast<int64_t>(row) * p.hq + h0 + h) * D + r * E;
-#pragma unroll
-      for (int e = 0; e < E; ++e) Elem<TQ>::store(p.out, base + e, acc[h][e] * inv);
-    }
+    K::template write_output<TQ>(p, row, h0, r, st);
   } else {
-#pragma unroll
-    for (int h = 0; h < GC; ++h) {
-      const int64_t prow = (static_cast<int64_t>(partial_row) * p.hq + h0 + h) * p.max_splits + split;
-      float* po = p.part_o + prow * D + r * E;
-#pragma unroll
-      for (int e = 0; e < E; e += 4) {
-        *reinterpret_cast<f32x4*>(po + e) = f32x4{acc[h][e], acc[h][e + 1], acc[h][e + 2], acc[h][e + 3]};
-      }
-      if (r == 0) {
-        p.part_ml[prow * 2] = m[h];
-        p.part_ml[prow * 2 + 1] = l[h];
-      }
-    }
+    K::write_partial(p, (static_cast<int64_t>(partial_row) * p.hq + h0) * p.max_splits + split,
+                     p.max_splits, r, st);
   }
 }
 
 // Combine the split partials of every (row, query head) that was split:
 // out = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s. One wave per (row, head).
 template <typename TQ, int D>
-__global__ __launch_bounds__(256) void paged_decode_merge_kernel(const PagedParams p) {
+__global__ __launch_bounds__(256) void paged_decode_grid_merge_kernel(const PagedParams p) {
   constexpr int kPerLane = (D + kWave - 1) / kWave;
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
@@ -311,33 +543,52 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(const PagedPara
 
 namespace {
 
-template <typename TQ, typename TKV, int D>
-hipError_t launch_decode_d(const PagedParams& p, int gc, hipStream_t stream) {
+int decode_waves(const PagedParams& p, int gc) {
   const int units = p.hk * (p.hq / p.hk / gc);
-  const int waves = units < 8 ? units : 8;
-  const dim3 grid(p.max_splits, p.by_row ? p.num_tokens : p.num_seqs, (units + waves - 1) / waves);
-  const dim3 block(waves * kWave);
-  switch (gc) {
-    case 4: paged_decode_kernel<TQ, TKV, D, 4><<<grid, block, 0, stream>>>(p); break;
-    case 2: paged_decode_kernel<TQ, TKV, D, 2><<<grid, block, 0, stream>>>(p); break;
-    default: paged_decode_kernel<TQ, TKV, D, 1><<<grid, block, 0, stream>>>(p); break;
+  return units < 8 ? units : 8;
+}
+
+template <typename TQ, typename TKV, int D, int GC>
+hipError_t launch_decode_g(const PagedParams& p, hipStream_t stream) {
+  const int units = p.hk * (p.hq / p.hk / GC);
+  const int waves = decode_waves(p, GC);
+  constexpr int kHeadsPerMergeBlock = 4;
+  if (p.stream_wgs > 0) {
+    if (units > 8) return hipErrorInvalidValue;  // planner keeps stream mode to <= 8 units
+    paged_decode_stream_kernel<TQ, TKV, D, GC><<<p.stream_wgs, waves * kWave, 0, stream>>>(p);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    const dim3 mgrid((p.hq + kHeadsPerMergeBlock - 1) / kHeadsPerMergeBlock, p.num_seqs);
+    paged_decode_stream_merge_kernel<TQ, D>
+        <<<mgrid, kHeadsPerMergeBlock * kWave, 0, stream>>>(p, p.stream_wgs);
+    return hipGetLastError();
   }
+  const dim3 grid(p.max_splits, p.by_row ? p.num_tokens : p.num_seqs, (units + waves - 1) / waves);
+  paged_decode_grid_kernel<TQ, TKV, D, GC><<<grid, waves * kWave, 0, stream>>>(p);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || p.max_splits == 1) return err;
-  const int heads_per_block = 4;
-  const dim3 mgrid((p.hq + heads_per_block - 1) / heads_per_block,
+  const dim3 mgrid((p.hq + kHeadsPerMergeBlock - 1) / kHeadsPerMergeBlock,
                    p.by_row ? p.num_tokens : p.num_seqs);
-  paged_decode_merge_kernel<TQ, D><<<mgrid, heads_per_block * kWave, 0, stream>>>(p);
+  paged_decode_grid_merge_kernel<TQ, D><<<mgrid, kHeadsPerMergeBlock * kWave, 0, stream>>>(p);
   return hipGetLastError();
 }
 
+template <typename TQ, typename TKV, int D>
+hipError_t launch_decode_d(const PagedParams& p, hipStream_t stream) {
+  switch (decode_group_chunk(p.hq / p.hk)) {
+    case 4: return launch_decode_g<TQ, TKV, D, 4>(p, stream);
+    case 2: return launch_decode_g<TQ, TKV, D, 2>(p, stream);
+    default: return launch_decode_g<TQ, TKV, D, 1>(p, stream);
+  }
+}
+
 template <typename TQ, typename TKV>
-hipError_t launch_decode_t(const PagedParams& p, int head_dim, int gc, hipStream_t stream) {
+hipError_t launch_decode_t(const PagedParams& p, int head_dim, hipStream_t stream) {
   switch (head_dim) {
-    case 32: return launch_decode_d<TQ, TKV, 32>(p, gc, stream);
-    case 64: return launch_decode_d<TQ, TKV, 64>(p, gc, stream);
-    case 128: return launch_decode_d<TQ, TKV, 128>(p, gc, stream);
-    case 256: return launch_decode_d<TQ, TKV, 256>(p, gc, stream);
+    case 32: return launch_decode_d<TQ, TKV, 32>(p, stream);
+    case 64: return launch_decode_d<TQ, TKV, 64>(p, stream);
+    case 128: return launch_decode_d<TQ, TKV, 128>(p, stream);
+    case 256: return launch_decode_d<TQ, TKV, 256>(p, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -346,19 +597,17 @@ hipError_t launch_decode_t(const PagedParams& p, int head_dim, int gc, hipStream
 
 hipError_t launch_paged_decode(const PagedParams& p, int q_dtype, int kv_dtype, int head_dim,
                                hipStream_t stream) {
-  const int group = p.hq / p.hk;
-  const int gc = group % 4 == 0 ? 4 : (group % 2 == 0 ? 2 : 1);
   if (kv_dtype == kFP8E4M3) {
-    if (q_dtype == kBF16) return launch_decode_t<bf16_t, fp8_t>(p, head_dim, gc, stream);
-    if (q_dtype == kF16) return launch_decode_t<f16_t, fp8_t>(p, head_dim, gc, stream);
-    if (q_dtype == kF32) return launch_decode_t<float, fp8_t>(p, head_dim, gc, stream);
+    if (q_dtype == kBF16) return launch_decode_t<bf16_t, fp8_t>(p, head_dim, stream);
+    if (q_dtype == kF16) return launch_decode_t<f16_t, fp8_t>(p, head_dim, stream);
+    if (q_dtype == kF32) return launch_decode_t<float, fp8_t>(p, head_dim, stream);
     return hipErrorInvalidValue;
   }
   if (q_dtype != kv_dtype) return hipErrorInvalidValue;
   switch (q_dtype) {
-    case kF32: return launch_decode_t<float, float>(p, head_dim, gc, stream);
-    case kF16: return launch_decode_t<f16_t, f16_t>(p, head_dim, gc, stream);
-    case kBF16: return launch_decode_t<bf16_t, bf16_t>(p, head_dim, gc, stream);
+    case kF32: return launch_decode_t<float, float>(p, head_dim, stream);
+    case kF16: return launch_decode_t<f16_t, f16_t>(p, head_dim, stream);
+    case kBF16: return launch_decode_t<bf16_t, bf16_t>(p, head_dim, stream);
     default: return hipErrorInvalidValue;
   }
 }

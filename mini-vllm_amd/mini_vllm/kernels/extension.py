@@ -52,6 +52,10 @@ HIP_FLAGS = [
     "-packed-fp32-ops",
 ]
 
+# Per-source extra flags. The elementwise kernels must round exactly where the
+# reference's PyTorch expressions round, so FMA contraction is off there.
+EXTRA_FLAGS = {"elementwise.hip": ["-ffp-contract=off"]}
+
 ABI_VERSION = 1
 
 DTYPE_CODES: dict[torch.dtype, int] = {
@@ -93,7 +97,8 @@ def build_library(verbose: bool = False, jobs: int | None = None) -> Path:
 
     def compile_one(src: Path) -> Path:
         obj = BUILD_DIR / (src.stem + ".o")
-        cmd = [HIPCC, *HIP_FLAGS, f"-I{INCLUDE_DIR}", "-c", str(src), "-o", str(obj)]
+        cmd = [HIPCC, *HIP_FLAGS, *EXTRA_FLAGS.get(src.name, []), f"-I{INCLUDE_DIR}", "-c",
+               str(src), "-o", str(obj)]
         result = subprocess.run(cmd, capture_output=True, text=True)
         noise = "'-packed-fp32-ops' is not a recognized feature"
         log = "\n".join(l for l in (result.stderr + result.stdout).splitlines() if noise not in l)
@@ -123,12 +128,15 @@ def build_library(verbose: bool = False, jobs: int | None = None) -> Path:
 
 class _Plan(ctypes.Structure):
     _fields_ = [
+        ("decode_mode", ctypes.c_int32),
+        ("decode_workgroups", ctypes.c_int32),
         ("split_tokens", ctypes.c_int32),
-        ("max_splits", ctypes.c_int32),
-        ("decode_by_row", ctypes.c_int32),
         ("prefill_mfma", ctypes.c_int32),
         ("workspace_bytes", ctypes.c_uint64),
     ]
+
+
+DECODE_MODES = {0: "none", 1: "stream", 2: "grid", 3: "by_row"}
 
 
 def _bind(lib: ctypes.CDLL) -> None:
@@ -398,7 +406,9 @@ class HipExtension:
                 ctypes.byref(plan),
             )
         )
-        return {name: getattr(plan, name) for name, _ in _Plan._fields_}
+        out = {name: getattr(plan, name) for name, _ in _Plan._fields_}
+        out["decode_mode"] = DECODE_MODES.get(out["decode_mode"], out["decode_mode"])
+        return out
 
     def paged_attention(
         self,

@@ -65,25 +65,38 @@ def test_paged_attention_refusals(lib, over, code, message):
 
 
 def test_split_workspace_is_required_when_planned(lib):
-    """A long decode needs split partials; a missing workspace is refused, not faulted."""
+    """Decode needs its partials workspace; a missing one is refused, not faulted."""
     assert _paged(lib, num_tokens=1, num_seqs=1, max_ctx=8192) == 4
     assert "workspace" in lib.mvllm_last_error().decode()
 
 
-def test_plan_is_host_only_and_consistent(lib):
+def _plan(lib, *args):
     plan = extension._Plan()
-    rc = lib.mvllm_paged_attention_plan(64, 64, 16, 8, 128, 16, 1, 4096, 2, 2, ctypes.byref(plan))
-    assert rc == 0
-    assert plan.prefill_mfma == 0 and plan.decode_by_row == 0
+    assert lib.mvllm_paged_attention_plan(*args, ctypes.byref(plan)) == 0
+    return plan
+
+
+def test_plan_is_host_only_and_consistent(lib):
+    # pure decode: the stream schedule, partial slots for (workgroups + sequences) x H_q
+    plan = _plan(lib, 64, 64, 16, 8, 128, 16, 1, 4096, 2, 2)
+    assert plan.decode_mode == 1 and plan.prefill_mfma == 0
+    assert 1 <= plan.decode_workgroups
+    entries = (plan.decode_workgroups + 64) * 16
+    assert plan.workspace_bytes >= entries * (128 + 2) * 4 + 65 * 4
+    # pure prefill chunks in bf16: no decode launch, MFMA prefill
+    plan = _plan(lib, 4096, 8, 16, 8, 128, 16, 512, 2048, 2, 2)
+    assert plan.decode_mode == 0 and plan.prefill_mfma == 1 and plan.workspace_bytes == 0
+    # mixed bf16 batch: stream decode + MFMA prefill
+    plan = _plan(lib, 101, 2, 16, 8, 128, 16, 100, 2048, 2, 2)
+    assert plan.decode_mode == 1 and plan.prefill_mfma == 1
+    # fp32 prefill has no MFMA kernel: the decode kernel serves every row
+    plan = _plan(lib, 100, 4, 16, 8, 128, 16, 40, 2048, 0, 0)
+    assert plan.decode_mode == 3 and plan.prefill_mfma == 0
     assert 64 <= plan.split_tokens <= 1024 and plan.split_tokens % 16 == 0
-    assert plan.max_splits == -(-4096 // plan.split_tokens)
-    if plan.max_splits > 1:
-        entries = 64 * 16 * plan.max_splits
-        assert plan.workspace_bytes >= entries * (128 + 2) * 4
-    rc = lib.mvllm_paged_attention_plan(4096, 8, 16, 8, 128, 16, 512, 2048, 2, 2, ctypes.byref(plan))
-    assert rc == 0 and plan.prefill_mfma == 1 and plan.decode_by_row == 0
-    rc = lib.mvllm_paged_attention_plan(100, 4, 16, 8, 128, 16, 40, 2048, 0, 0, ctypes.byref(plan))
-    assert rc == 0 and plan.prefill_mfma == 0 and plan.decode_by_row == 1
+    # more (kv head, head chunk) units than one workgroup's 8 waves: the split grid
+    plan = _plan(lib, 4, 4, 64, 8, 128, 16, 1, 4096, 2, 2)
+    assert plan.decode_mode == 2
+    assert plan.decode_workgroups == -(-4096 // plan.split_tokens)
 
 
 @pytest.mark.parametrize("fn,args,message", [

@@ -64,7 +64,29 @@ def test_decode_matches_the_oracle_at_every_boundary(extension, device, context,
 def test_decode_over_a_long_context_uses_the_split_path(extension, device):
     b = case([8192], [1], device)
     plan = extension.paged_attention_plan(1, 1, HQ, HK, D, 16, 1, 8192, b.q.dtype, b.q.dtype)
-    assert plan["max_splits"] > 1
+    assert plan["decode_mode"] == "stream" and plan["decode_workgroups"] > 1
+    check(extension, b)
+
+
+@pytest.mark.parametrize("schedule", ["stream", "grid"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_both_decode_schedules_agree_with_the_oracle(extension, device, monkeypatch, schedule, dtype):
+    """The stream schedule (default) and the split grid (forced) on a ragged batch,
+    including sequences shorter than one workgroup's share and longer than many."""
+    if schedule == "grid":
+        monkeypatch.setenv("MVLLM_DECODE_SCHEDULE", "2")
+    b = case([8192, 33, 4096, 17, 1, 700, 2], [1] * 7, device, dtype=dtype)
+    plan = extension.paged_attention_plan(7, 7, HQ, HK, D, 16, 1, 8192, dtype, dtype)
+    assert plan["decode_mode"] == schedule
+    check(extension, b)
+
+
+@pytest.mark.parametrize("wgs_per_cu", ["1", "4"])
+def test_stream_schedule_with_more_workgroups_than_keys(extension, device, monkeypatch, wgs_per_cu):
+    """Tiny batches leave most stream workgroups with empty shares; the merge must skip
+    their slots."""
+    monkeypatch.setenv("MVLLM_DECODE_WGS_PER_CU", wgs_per_cu)
+    b = case([3, 5, 2], [1, 1, 1], device, dtype=torch.bfloat16, block_size=1)
     check(extension, b)
 
 
@@ -76,6 +98,7 @@ def test_a_ragged_decode_batch_with_empty_splits(extension, device):
 
 @pytest.mark.parametrize("split_tokens", ["64", "1024"])
 def test_forced_split_sizes_agree(extension, device, monkeypatch, split_tokens):
+    monkeypatch.setenv("MVLLM_DECODE_SCHEDULE", "2")
     monkeypatch.setenv("MVLLM_DECODE_SPLIT_TOKENS", split_tokens)
     check(extension, case([3000, 129, 64, 1], [1, 1, 1, 1], device, dtype=torch.bfloat16))
 
