@@ -42,25 +42,26 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def time_steps(fn, steps: int, warmup: int) -> tuple[float, list[float]]:
-    """Mean ms per call over `steps` back-to-back calls, plus per-call event times."""
+def time_steps(fn, steps: int, warmup: int) -> float:
+    """Mean ms per call over `steps` back-to-back calls.
+
+    Two HIP events on the stream the kernels run on bracket the whole loop; no event
+    is recorded between calls, because a timed event record makes the GPU drain and
+    flush the previous kernel before dispatching the next one, which would add a gap
+    to every step that a real decode loop does not have.
+    """
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     first = torch.cuda.Event(enable_timing=True)
     last = torch.cuda.Event(enable_timing=True)
     first.record(stream)
     for i in range(steps):
-        starts[i].record(stream)
         fn(i)
-        ends[i].record(stream)
     last.record(stream)
     torch.cuda.synchronize()
-    per_call = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    return first.elapsed_time(last) / steps, per_call
+    return first.elapsed_time(last) / steps
 
 
 def rotated_batches(index: int, copies: int):
@@ -88,8 +89,6 @@ def rotated_batches(index: int, copies: int):
 def run_paged(batches, steps, warmup):
     from mini_vllm.kernels import ops
 
-    outs = [torch.empty_like(b.q) for b in batches]
-
     def step(i):
         b = batches[i % len(batches)]
         ops.paged_attention(*b.args(), use_cuda=True, k_scale=b.k_scale, v_scale=b.v_scale)
@@ -107,7 +106,7 @@ def copy_ceiling(nbytes: int, steps: int = 20) -> float:
     def step(i):
         dst[i % 2].copy_(src[i % 2])
 
-    ms, _ = time_steps(step, steps, 3)
+    ms = time_steps(step, steps, 3)
     return 2 * n * 2 / (ms * 1e-3) / 1e9
 
 
@@ -174,7 +173,7 @@ def main() -> int:
     plan = ext.paged_attention_plan(b.q.shape[0], len(b.contexts), 16, 8, 128, 16, 1,
                                     b.max_context_len, b.q.dtype, b.key_pool.dtype)
     log(f"config 2: K+V {kv_bytes / 1e6:.1f} MB per step, plan {plan}")
-    ms, per_call = run_paged(batches, args.steps, args.warmup)
+    ms = run_paged(batches, args.steps, args.warmup)
     gbs = kv_bytes / (ms * 1e-3) / 1e9
     log(f"config 2: {ms * 1e3:.1f} us/step, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of 8 TB/s)")
 
@@ -185,7 +184,7 @@ def main() -> int:
         log("config 3: building inputs")
         pf = rotated_batches(3, 2)
         flops = prefill_flops(pf[0])
-        pms, _ = run_paged(pf, max(10, args.steps // 2), 3)
+        pms = run_paged(pf, max(10, args.steps // 2), 3)
         tflops = flops / (pms * 1e-3) / 1e12
         extras["config3_prefill"] = {
             "ms_per_call": round(pms, 4), "gflop": round(flops / 1e9, 3),
@@ -196,7 +195,7 @@ def main() -> int:
         log("config 4: building inputs")
         f8 = rotated_batches(4, 2)
         f8_bytes = f8[0].kv_bytes() + f8[0].scale_bytes()
-        fms, _ = run_paged(f8, max(10, args.steps // 2), 3)
+        fms = run_paged(f8, max(10, args.steps // 2), 3)
         fgbs = f8_bytes / (fms * 1e-3) / 1e9
         extras["config4_fp8_decode"] = {
             "ms_per_call": round(fms, 4), "bytes": f8_bytes, "gbs": round(fgbs, 1),

@@ -45,8 +45,9 @@ const char* mvllm_last_error(void);
 int mvllm_abi_version(void);
 
 /* How one paged_attention call will be executed. Filled by mvllm_paged_attention_plan;
- * the caller allocates `workspace_bytes` of device memory (256-byte aligned) and passes
- * it to mvllm_paged_attention with the same arguments. */
+ * the caller provides `workspace_bytes` of device memory (256-byte aligned, contents
+ * irrelevant) and passes it to mvllm_paged_attention with the same arguments. Calls
+ * that overlap in time on one workspace race. */
 #define MVLLM_DECODE_NONE 0   /* no decode row: every sequence is a prefill chunk */
 #define MVLLM_DECODE_STREAM 1 /* persistent workgroups, equal shares of all decode keys */
 #define MVLLM_DECODE_GRID 2   /* one workgroup per (sequence, split) */
@@ -56,7 +57,7 @@ typedef struct mvllm_paged_plan {
   int32_t decode_workgroups; /* stream: workgroups launched; grid modes: split-axis extent */
   int32_t split_tokens;      /* grid modes: keys per split */
   int32_t prefill_mfma;      /* 1: prefill rows go to the MFMA prefill kernel */
-  uint64_t workspace_bytes;  /* partials and metadata; 0 when none are needed */
+  uint64_t workspace_bytes;  /* split partials and their index; 0 when none are needed */
 } mvllm_paged_plan;
 
 /* Plan a paged_attention call. Depends only on the host-side sizes below (never on

@@ -107,8 +107,8 @@ int check_paged_shape(int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t 
 struct Plan {
   mvllm_paged_plan pub;
   int max_splits = 1;
-  uint64_t off_ml = 0;      // byte offsets into the workspace
-  uint64_t off_prefix = 0;
+  uint64_t off_o = 0;       // byte offsets into the workspace
+  uint64_t off_ml = 0;
 };
 
 uint64_t align256(uint64_t v) { return (v + 255) / 256 * 256; }
@@ -148,10 +148,12 @@ Plan make_plan(int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk, int
     if (wgs > by_size) wgs = by_size;
     if (wgs < 1) wgs = 1;
     plan.pub.decode_workgroups = static_cast<int32_t>(wgs);
+    // [prefix: num_seqs + 1 int32][O partials][(m, l) partials]
     const uint64_t entries = static_cast<uint64_t>(wgs + num_seqs) * hq;
-    plan.off_ml = align256(entries * d * sizeof(float));
-    plan.off_prefix = plan.off_ml + align256(entries * 2 * sizeof(float));
-    plan.pub.workspace_bytes = plan.off_prefix + align256((num_seqs + 1) * sizeof(int));
+    const uint64_t head = align256(static_cast<uint64_t>(num_seqs + 1) * sizeof(int));
+    plan.off_o = head;
+    plan.off_ml = plan.off_o + align256(entries * d * sizeof(float));
+    plan.pub.workspace_bytes = plan.off_ml + align256(entries * 2 * sizeof(float));
     return plan;
   }
   if (plan.pub.decode_mode == MVLLM_DECODE_NONE) return plan;
@@ -274,9 +276,9 @@ int mvllm_paged_attention(void* out, const void* q, const void* key_pool,
   p.scale = scale;
   if (need > 0) {
     char* ws = static_cast<char*>(workspace);
-    p.part_o = reinterpret_cast<float*>(ws);
+    if (plan.pub.decode_mode == MVLLM_DECODE_STREAM) p.seq_prefix = reinterpret_cast<int*>(ws);
+    p.part_o = reinterpret_cast<float*>(ws + plan.off_o);
     p.part_ml = reinterpret_cast<float*>(ws + plan.off_ml);
-    if (plan.off_prefix > 0) p.seq_prefix = reinterpret_cast<int*>(ws + plan.off_prefix);
   }
 
   const hipStream_t s = static_cast<hipStream_t>(stream);

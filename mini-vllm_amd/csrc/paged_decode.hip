@@ -27,7 +27,10 @@
 //    A share that covers a whole sequence writes its output directly; a sequence cut
 //    between workgroups leaves one (m, l, O) partial per piece, in slot
 //    (workgroup + sequence), which is unique because shares and sequences are both
-//    contiguous ranges of the same axis. A small merge kernel combines the pieces.
+//    contiguous ranges of the same axis. A second small kernel merges the pieces.
+//    (Merging in the decode kernel instead -- the last workgroup to finish a piece
+//    merges, on an atomic counter -- measured slower: every merge then sits at the
+//    end of the launch behind a chain of dependent memory round trips.)
 //  * grid (fallback, and the by-row mode that also serves prefill rows when no MFMA
 //    prefill kernel fits the shape): one workgroup per (row, split) with splits of
 //    `split_tokens` keys, page ids staged in LDS, merged by a second kernel.
@@ -45,7 +48,11 @@ namespace mvllm {
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kUnroll = 4;  // tokens in flight per row group per step
+// Tokens per row group per step (each step's K/V rows are requested together).
+#ifndef MVLLM_DECODE_UNROLL
+#define MVLLM_DECODE_UNROLL 4
+#endif
+constexpr int kUnroll = MVLLM_DECODE_UNROLL;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -120,7 +127,10 @@ struct Decode {
 
   // Stream keys [sb, se) of one sequence for kv head `kvh` into `st`. Page ids come
   // from `lds_pages` (page i of the run at lds_pages[i - first_page]) when given,
-  // otherwise from the sequence's block table.
+  // otherwise from the sequence's block table; the next step's page ids are requested
+  // before this step is computed. (Requesting the next step's K/V rows early as well
+  // measured slower: on shuffled pages more requests in flight per CU cost DRAM
+  // efficiency.)
   __device__ static void stream(const PagedParams& p, const int32_t* table, const int* lds_pages,
                                 int first_page, int kvh, int sb, int se, int g, int r,
                                 const float (&qf)[GC][E], float score_scale, State& st) {
@@ -156,7 +166,6 @@ struct Decode {
           vs[u] = p.v_scales[static_cast<int64_t>(pg[u]) * p.hk + kvh];
         }
       }
-      // Page ids of the next step, in flight while this step computes.
       if (t0 + kStep < se) {
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) pg[u] = page_of(min(t0 + kStep + u * RG + g, se - 1));
@@ -287,6 +296,19 @@ __device__ __forceinline__ bool wave_unit(const PagedParams& p, int unit, int& k
 
 // ------------------------------------------------------------ stream schedule
 
+namespace {
+
+// Workgroup owning decode key x of `total` split over `wgs` equal shares
+// [floor(w*total/wgs), floor((w+1)*total/wgs)): the largest such w with start <= x.
+__device__ __forceinline__ int64_t share_owner(int64_t x, int64_t total, int64_t wgs) {
+  return ((x + 1) * wgs - 1) / total;
+}
+__device__ __forceinline__ bool share_nonempty(int64_t w, int64_t total, int64_t wgs) {
+  return (w * total) / wgs < ((w + 1) * total) / wgs;
+}
+
+}  // namespace
+
 template <typename TQ, typename TKV, int D, int GC>
 __global__ __launch_bounds__(512) void paged_decode_stream_kernel(const PagedParams p) {
   using K = Decode<TKV, D, GC>;
@@ -324,14 +346,14 @@ __global__ __launch_bounds__(512) void paged_decode_stream_kernel(const PagedPar
   }
   const int64_t lo = static_cast<int64_t>(blockIdx.x) * total / wgs;
   const int64_t hi = (static_cast<int64_t>(blockIdx.x) + 1) * total / wgs;
-  if (lo >= hi) return;
+  if (lo >= hi) return;  // whole workgroup: no barrier follows for it
 
   const int wave = tid / kWave;
   const int lane = tid % kWave;
   const int g = lane / K::R;
   const int r = lane % K::R;
-  int kvh, h0;
-  if (!wave_unit<GC>(p, wave, kvh, h0)) return;
+  int kvh = 0, h0 = 0;
+  const bool active = wave_unit<GC>(p, wave, kvh, h0);
   const float score_scale = p.scale * kLog2e;
 
   // First sequence whose keys include `lo`: the last s with prefix[s] <= lo.
@@ -349,20 +371,20 @@ __global__ __launch_bounds__(512) void paged_decode_stream_kernel(const PagedPar
     const int sb = static_cast<int>(pos - base);
     const int se = static_cast<int>(min(hi, static_cast<int64_t>(s_prefix[seq + 1])) - base);
     const int row = p.cu_seqlens_q[seq];
-
-    float qf[GC][K::E];
-    K::template load_queries<TQ>(p, row, h0, r, qf);
-    typename K::State st;
-    K::init(st);
-    const int32_t* table = p.block_tables + static_cast<int64_t>(seq) * p.max_blocks;
-    K::stream(p, table, nullptr, 0, kvh, sb, se, g, r, qf, score_scale, st);
-    K::merge_row_groups(st);
-    if (g == 0) {
-      if (sb == 0 && se == ctx) {
-        K::template write_output<TQ>(p, row, h0, r, st);
-      } else {
-        const int64_t slot = static_cast<int64_t>(blockIdx.x) + seq;
-        K::write_partial(p, slot * p.hq + h0, 1, r, st);
+    if (active) {
+      float qf[GC][K::E];
+      K::template load_queries<TQ>(p, row, h0, r, qf);
+      typename K::State st;
+      K::init(st);
+      const int32_t* table = p.block_tables + static_cast<int64_t>(seq) * p.max_blocks;
+      K::stream(p, table, nullptr, 0, kvh, sb, se, g, r, qf, score_scale, st);
+      K::merge_row_groups(st);
+      if (g == 0) {
+        if (sb == 0 && se == ctx) {
+          K::template write_output<TQ>(p, row, h0, r, st);
+        } else {
+          K::write_partial(p, (static_cast<int64_t>(blockIdx.x) + seq) * p.hq + h0, 1, r, st);
+        }
       }
     }
     pos = base + se;
@@ -370,68 +392,62 @@ __global__ __launch_bounds__(512) void paged_decode_stream_kernel(const PagedPar
   }
 }
 
-// Combine the pieces of every decode sequence that was cut between workgroups.
-// One wave per (sequence, query head); lanes cover the head dim.
+// Combine the pieces of every decode sequence cut between stream workgroups: one
+// workgroup per sequence, one float4 column of its H_q x D output per thread, the
+// pieces merged online (running max, rescaled sums) so their loads are in flight
+// together. Piece i of sequence s lives in slot (first + i + s), first/last being the
+// workgroups owning the sequence's first and last key.
 template <typename TQ, int D>
-__global__ __launch_bounds__(256) void paged_decode_stream_merge_kernel(const PagedParams p,
-                                                                        int wgs) {
-  constexpr int kPerLane = (D + kWave - 1) / kWave;
-  const int wave = threadIdx.x / kWave;
-  const int lane = threadIdx.x % kWave;
-  const int head = blockIdx.x * (blockDim.x / kWave) + wave;
-  const int seq = blockIdx.y;
-  if (head >= p.hq) return;
+__global__ __launch_bounds__(1024) void paged_decode_stream_merge_kernel(const PagedParams p,
+                                                                         int wgs_i) {
+  constexpr int kBatch = 8;  // pieces whose loads are issued together
+  const int seq = blockIdx.x;
+  const int64_t wgs = wgs_i;
   const int64_t total = p.seq_prefix[p.num_seqs];
   const int64_t begin = p.seq_prefix[seq];
   const int64_t end = p.seq_prefix[seq + 1];
   if (end == begin || total == 0) return;
-  // Workgroup owning key x: the largest w with floor(w * total / wgs) <= x.
-  const int first = static_cast<int>(((begin + 1) * wgs - 1) / total);
-  const int last = static_cast<int>((end * wgs - 1) / total);
+  const int64_t first = share_owner(begin, total, wgs);
+  const int64_t last = share_owner(end - 1, total, wgs);
   if (first == last) return;  // one piece: the decode kernel stored the output
-  const int pieces = last - first + 1;
-  const int64_t pidx0 = (static_cast<int64_t>(first) + seq) * p.hq + head;
-  const int64_t pstride = p.hq;
-
-  // A workgroup whose share is empty (only when there are fewer keys than workgroups)
-  // owns no key and wrote no partial: its slot is skipped.
-  auto live = [&](int i) {
-    const int64_t w = first + i;
-    return (w * total) / wgs < ((w + 1) * total) / wgs;
-  };
-  float mmax = -INFINITY;
-  for (int i = lane; i < pieces; i += kWave) {
-    if (live(i)) mmax = fmaxf(mmax, p.part_ml[(pidx0 + i * pstride) * 2]);
-  }
-  mmax = wave_max(mmax);
-  const float mu = mmax == -INFINITY ? 0.0f : mmax;
-  float total_l = 0.0f;
-  for (int i = lane; i < pieces; i += kWave) {
-    const int64_t pidx = pidx0 + i * pstride;
-    if (live(i)) total_l += __builtin_amdgcn_exp2f(p.part_ml[pidx * 2] - mu) * p.part_ml[pidx * 2 + 1];
-  }
-  total_l = wave_sum(total_l);
-  const float inv = total_l > 0.0f ? 1.0f / total_l : 0.0f;
-
-  float o[kPerLane];
+  const bool all_live = total >= wgs;
+  const int pieces = static_cast<int>(last - first + 1);
+  const int n4 = p.hq * D / 4;
+  const int row = p.cu_seqlens_q[seq];
+  for (int j = threadIdx.x; j < n4; j += blockDim.x) {
+    const int head = (4 * j) / D;
+    const int d = 4 * j - head * D;
+    float m = -INFINITY, l = 0.0f;
+    f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i0 = 0; i0 < pieces; i0 += kBatch) {
+      float mi[kBatch], li[kBatch];
+      f32x4 oi[kBatch];
 #pragma unroll
-  for (int i = 0; i < kPerLane; ++i) o[i] = 0.0f;
-  for (int i = 0; i < pieces; ++i) {
-    if (!live(i)) continue;
-    const int64_t pidx = pidx0 + i * pstride;
-    const float w = __builtin_amdgcn_exp2f(p.part_ml[pidx * 2] - mu);
-    const float* po = p.part_o + pidx * D;
+      for (int u = 0; u < kBatch; ++u) {
+        const int i = min(i0 + u, pieces - 1);
+        const int64_t pidx = (first + i + seq) * p.hq + head;
+        mi[u] = p.part_ml[pidx * 2];
+        li[u] = p.part_ml[pidx * 2 + 1];
+        oi[u] = *reinterpret_cast<const f32x4*>(p.part_o + pidx * D + d);
+      }
 #pragma unroll
-    for (int k = 0; k < kPerLane; ++k) {
-      const int d = lane + k * kWave;
-      if (d < D) o[k] = fmaf(w, po[d], o[k]);
+      for (int u = 0; u < kBatch; ++u) {
+        // Beyond the last piece, or a workgroup whose share was empty (fewer keys
+        // than workgroups): it wrote nothing and contributes nothing.
+        if (i0 + u >= pieces || !(all_live || share_nonempty(first + i0 + u, total, wgs))) continue;
+        const float mn = fmaxf(m, mi[u]);
+        const float mu = mn == -INFINITY ? 0.0f : mn;
+        const float a = fast_exp2(m - mu);
+        const float b = fast_exp2(mi[u] - mu);
+        l = l * a + li[u] * b;
+        o = o * a + oi[u] * b;
+        m = mn;
+      }
     }
-  }
-  const int64_t base = (static_cast<int64_t>(p.cu_seqlens_q[seq]) * p.hq + head) * D;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const int64_t obase = (static_cast<int64_t>(row) * p.hq + head) * D + d;
 #pragma unroll
-  for (int k = 0; k < kPerLane; ++k) {
-    const int d = lane + k * kWave;
-    if (d < D) Elem<TQ>::store(p.out, base + d, o[k] * inv);
+    for (int k = 0; k < 4; ++k) Elem<TQ>::store(p.out, obase + k, o[k] * inv);
   }
 }
 
@@ -558,9 +574,9 @@ hipError_t launch_decode_g(const PagedParams& p, hipStream_t stream) {
     paged_decode_stream_kernel<TQ, TKV, D, GC><<<p.stream_wgs, waves * kWave, 0, stream>>>(p);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
-    const dim3 mgrid((p.hq + kHeadsPerMergeBlock - 1) / kHeadsPerMergeBlock, p.num_seqs);
-    paged_decode_stream_merge_kernel<TQ, D>
-        <<<mgrid, kHeadsPerMergeBlock * kWave, 0, stream>>>(p, p.stream_wgs);
+    const int n4 = p.hq * D / 4;
+    const int threads = n4 >= 1024 ? 1024 : (n4 + kWave - 1) / kWave * kWave;
+    paged_decode_stream_merge_kernel<TQ, D><<<p.num_seqs, threads, 0, stream>>>(p, p.stream_wgs);
     return hipGetLastError();
   }
   const dim3 grid(p.max_splits, p.by_row ? p.num_tokens : p.num_seqs, (units + waves - 1) / waves);

@@ -10,9 +10,10 @@ module's functions -- ``paged_attention``, ``rmsnorm``, ``rope``, ``swiglu``, ``
 it are unchanged.
 
 Ownership follows the reference: each call returns a freshly allocated output tensor
-(torch's caching allocator), and the split-K workspace of ``paged_attention`` is also
-a torch allocation made here, so the library itself never allocates device memory.
-Work goes on torch's current stream and nothing synchronizes.
+(torch's caching allocator), so the library itself never allocates device memory. The
+split-K workspace of ``paged_attention`` is a torch allocation kept here, one per
+(device, stream), grown on demand. Work goes on torch's current stream and nothing
+synchronizes.
 """
 
 from __future__ import annotations
@@ -33,7 +34,9 @@ PACKAGE_ROOT = Path(__file__).resolve().parents[2]  # .../mini-vllm_amd
 CSRC_DIR = PACKAGE_ROOT / "csrc"
 BUILD_DIR = PACKAGE_ROOT / "_build"
 LIB_DIR = PACKAGE_ROOT / "lib"
-LIB_PATH = LIB_DIR / "libminivllm_hip.so"
+# MVLLM_LIBRARY points the loader at another build of the same library (variant builds
+# for measurements); the default is the in-tree build.
+LIB_PATH = Path(os.environ.get("MVLLM_LIBRARY") or LIB_DIR / "libminivllm_hip.so")
 REPO_ROOT = PACKAGE_ROOT.parent
 INCLUDE_DIR = REPO_ROOT / "include"
 
@@ -208,6 +211,23 @@ class HipExtension:
     def __init__(self, lib: ctypes.CDLL) -> None:
         self.lib = lib
         self.path = LIB_PATH
+        self._workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+    def workspace(self, device: torch.device, nbytes: int) -> torch.Tensor:
+        """The paged-attention workspace of (device, current stream), grown on demand.
+
+        Kept rather than allocated per call so a steady decode loop (or a captured
+        graph) reuses one buffer; calls on one stream are ordered, so they never race.
+        """
+        key = (device.index if device.index is not None else torch.cuda.current_device(),
+               _stream(device))
+        ws = self._workspaces.get(key)
+        if ws is None or ws.numel() < nbytes:
+            size = max(nbytes, 2 * ws.numel() if ws is not None else 0)
+            size = (size + (1 << 20) - 1) >> 20 << 20
+            ws = torch.empty(size, dtype=torch.uint8, device=device)
+            self._workspaces[key] = ws
+        return ws
 
     # -- plumbing
     def _check(self, rc: int) -> None:
@@ -555,7 +575,7 @@ class HipExtension:
         )
         workspace = None
         if plan.workspace_bytes:
-            workspace = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=q.device)
+            workspace = self.workspace(q.device, plan.workspace_bytes)
         self._check(
             self.lib.mvllm_paged_attention(
                 out.data_ptr(),
@@ -582,7 +602,7 @@ class HipExtension:
                 q_code,
                 kv_code,
                 _ptr(workspace),
-                plan.workspace_bytes,
+                0 if workspace is None else workspace.numel(),
                 _stream(q.device),
             )
         )
