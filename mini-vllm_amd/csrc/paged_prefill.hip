@@ -49,9 +49,7 @@ template <> struct Mma<bf16_t> {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                    __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
   }
-  __device__ static uint32_t pack2(float lo, float hi) {
-    return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
-  }
+  __device__ static uint32_t pack2(float lo, float hi) { return pack_bf16x2(lo, hi); }
 };
 template <> struct Mma<f16_t> {
   __device__ static f32x16 run(const u32x4& a, const u32x4& b, const f32x16& c) {
@@ -75,12 +73,11 @@ template <typename TQ> struct Stage<TQ, fp8_t> {
     const u32x2 w = *reinterpret_cast<const u32x2*>(src);
     u32x4 out;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t word = w[i / 2];
-      const int b = (i % 2) * 2;
-      const float lo = fp8e4m3_to_f32((word >> (8 * b)) & 0xffu) * scale;
-      const float hi = fp8e4m3_to_f32((word >> (8 * (b + 1))) & 0xffu) * scale;
-      out[i] = Mma<TQ>::pack2(lo, hi);
+    for (int i = 0; i < 2; ++i) {
+      const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w[i]), false);
+      const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w[i]), true);
+      out[2 * i] = Mma<TQ>::pack2(lo[0] * scale, lo[1] * scale);
+      out[2 * i + 1] = Mma<TQ>::pack2(hi[0] * scale, hi[1] * scale);
     }
     return out;
   }

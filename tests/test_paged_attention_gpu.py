@@ -233,6 +233,24 @@ def test_fp8_dequantisation_is_exact_for_one_visible_key(extension, device):
         assert torch.equal(got[0, h], want[h // 2])
 
 
+@pytest.mark.parametrize("query_len", [1, 12])
+def test_fp8_decodes_every_finite_code_exactly(extension, device, query_len):
+    """Key 0's values cover all 254 finite e4m3fn codes with scale 1; a query that sees
+    only key 0 (a decode over one key, or the first row of a prefill chunk) returns
+    them decoded exactly (both representable in bf16)."""
+    b = case([query_len], [query_len], device, dtype=torch.bfloat16,
+             kv_dtype=torch.float8_e4m3fn, num_q_heads=16, num_kv_heads=8, head_dim=128)
+    codes = torch.tensor([c for c in range(256) if c & 0x7F != 0x7F], dtype=torch.uint8)
+    blk = int(b.block_tables[0, 0])
+    row = codes.repeat(5)[: 8 * 128].reshape(8, 128).to(device)
+    b.value_pool.view(torch.uint8)[blk, 0] = row
+    b.v_scale[blk] = 1.0
+    got = kernel(extension, b)
+    want = row.view(torch.float8_e4m3fn).float().to(torch.bfloat16)
+    for h in range(16):
+        assert torch.equal(got[0, h], want[h // 2]), f"head {h}"
+
+
 # ------------------------------------------------------------------- configs
 
 
