@@ -38,6 +38,18 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 
 
+def measured_traffic() -> int | None:
+    """HBM bytes per decode launch from the committed counter summary (two rocprofv3
+    --pmc passes, calibrated on a copy of known size), or None if there is none."""
+    path = REPO / "profiles" / "paged_decode_cfg2_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1])
+    return None
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -147,7 +159,9 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--copies", type=int, default=3, help="rotated pool copies (defeat the MALL)")
-    parser.add_argument("--skip-extras", action="store_true")
+    parser.add_argument("--skip-extras", action="store_true", help="headline config 2 only")
+    parser.add_argument("--extras", default="3,4,copy",
+                        help="comma list of extras to run: 3 (prefill), 4 (fp8 decode), copy")
     parser.add_argument("--no-cpu", action="store_true")
     args = parser.parse_args()
 
@@ -178,9 +192,10 @@ def main() -> int:
     log(f"config 2: {ms * 1e3:.1f} us/step, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of 8 TB/s)")
 
     extras = {}
-    if not args.skip_extras:
-        del batches
-        torch.cuda.empty_cache()
+    wanted = set() if args.skip_extras else {e.strip() for e in args.extras.split(",") if e.strip()}
+    del batches
+    torch.cuda.empty_cache()
+    if "3" in wanted:
         log("config 3: building inputs")
         pf = rotated_batches(3, 2)
         flops = prefill_flops(pf[0])
@@ -192,6 +207,7 @@ def main() -> int:
         log(f"config 3: {pms * 1e3:.1f} us, {tflops:.1f} TFLOP/s")
         del pf
         torch.cuda.empty_cache()
+    if "4" in wanted:
         log("config 4: building inputs")
         f8 = rotated_batches(4, 2)
         f8_bytes = f8[0].kv_bytes() + f8[0].scale_bytes()
@@ -203,8 +219,9 @@ def main() -> int:
         log(f"config 4: {fms * 1e3:.1f} us, {fgbs:.0f} GB/s")
         del f8
         torch.cuda.empty_cache()
+    if "copy" in wanted:
         extras["copy_ceiling_gbs"] = round(copy_ceiling(1 << 30), 1)
-        log(f"copy_ ceiling {extras['copy_ceiling_gbs']} GB/s")
+        log(f"copy_ ceiling {extras['copy_ceiling_gbs']} GB/s (1 GiB device-to-device copies)")
 
     cpu = None
     if not args.no_cpu:
@@ -239,7 +256,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
         },
         "cpu_baseline": cpu,
         "extras": extras,
