@@ -1,0 +1,148 @@
+"""Qwen3 over a paged KV pool (reference model/qwen3_paged.py:40-228).
+
+The per-layer sequence is the reference's, op for op, because it is the caller the
+hot path has to serve unchanged:
+
+    attn_norm -> q/k/v projections -> QK-norm (rmsnorm over D) -> RoPE at
+    batch.positions -> write K/V to the pool -> paged attention -> wo -> residual ->
+    mlp_norm -> gate/up -> SwiGLU -> down -> residual
+
+and the forward returns one logits row per sequence (its last computed position),
+through the final norm and the tied embedding (reference qwen3_paged.py:211-228).
+Projections are plain ``x @ w.T`` matmuls (BLAS); every other op goes through
+``mini_vllm.kernels.ops`` with the model's ``use_cuda`` flag.
+
+Weights are random (there is no checkpoint download here): N(0, 0.02) for matrices
+and the embedding, ones for norm weights, seeded.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from mini_vllm import torch_path
+from mini_vllm.kernels import ops
+
+__all__ = ["ModelConfig", "Qwen3Paged", "random_weights"]
+
+
+@dataclass(frozen=True)
+class ModelConfig:
+    """Qwen3-0.6B's shape by default (reference model/loader.py:53-120 reads the same
+    fields from config.json)."""
+
+    vocab_size: int = 151936
+    hidden_size: int = 1024
+    num_hidden_layers: int = 28
+    num_attention_heads: int = 16
+    num_key_value_heads: int = 8
+    head_dim: int = 128
+    intermediate_size: int = 3072
+    max_position_embeddings: int = 40960
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1_000_000.0
+    dtype: torch.dtype = torch.bfloat16
+
+    @property
+    def q_size(self) -> int:
+        return self.num_attention_heads * self.head_dim
+
+    @property
+    def kv_size(self) -> int:
+        return self.num_key_value_heads * self.head_dim
+
+    def num_params(self) -> int:
+        e, i, v = self.hidden_size, self.intermediate_size, self.vocab_size
+        per_layer = e * (self.q_size + 2 * self.kv_size) + self.q_size * e + 3 * e * i
+        per_layer += 2 * e + 2 * self.head_dim
+        return v * e + self.num_hidden_layers * per_layer + e
+
+
+def random_weights(config: ModelConfig, seed: int = 0, device: torch.device | str = "cpu",
+                   std: float = 0.02) -> dict[str, torch.Tensor]:
+    """Seeded N(0, std) matrices (fp32 draws cast to the model dtype), unit norms."""
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    dt = config.dtype
+
+    def mat(rows: int, cols: int) -> torch.Tensor:
+        return (torch.randn(rows, cols, generator=gen) * std).to(dt).to(device)
+
+    def ones(n: int) -> torch.Tensor:
+        return torch.ones(n, dtype=dt, device=device)
+
+    e = config.hidden_size
+    w = {"embedding": mat(config.vocab_size, e), "final_norm": ones(e)}
+    for layer in range(config.num_hidden_layers):
+        pre = f"layers.{layer}."
+        w[pre + "wq"] = mat(config.q_size, e)
+        w[pre + "wk"] = mat(config.kv_size, e)
+        w[pre + "wv"] = mat(config.kv_size, e)
+        w[pre + "wo"] = mat(e, config.q_size)
+        w[pre + "q_norm"] = ones(config.head_dim)
+        w[pre + "k_norm"] = ones(config.head_dim)
+        w[pre + "attn_norm"] = ones(e)
+        w[pre + "mlp_norm"] = ones(e)
+        w[pre + "gate"] = mat(config.intermediate_size, e)
+        w[pre + "up"] = mat(config.intermediate_size, e)
+        w[pre + "down"] = mat(e, config.intermediate_size)
+    return w
+
+
+def _linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    return x @ w.t()
+
+
+class Qwen3Paged:
+    """``model(batch) -> N x V`` logits, one row per sequence of the ragged batch."""
+
+    def __init__(self, config: ModelConfig, weights: dict[str, torch.Tensor], manager,
+                 use_cuda: bool = True) -> None:
+        self.config = config
+        self.weights = weights
+        self.manager = manager
+        self.use_cuda = use_cuda
+        device = weights["embedding"].device
+        self.cos, self.sin = torch_path.rope_tables(config.head_dim,
+                                                    config.max_position_embeddings,
+                                                    config.rope_theta, device=device)
+        self.layers = []
+        for layer in range(config.num_hidden_layers):
+            pre = f"layers.{layer}."
+            self.layers.append({k[len(pre):]: v for k, v in weights.items() if k.startswith(pre)})
+
+    def _attention(self, layer: int, w: dict, x: torch.Tensor, batch) -> torch.Tensor:
+        c = self.config
+        t = x.shape[0]
+        u = self.use_cuda
+        q = _linear(x, w["wq"]).view(t, c.num_attention_heads, c.head_dim)
+        k = _linear(x, w["wk"]).view(t, c.num_key_value_heads, c.head_dim)
+        v = _linear(x, w["wv"]).view(t, c.num_key_value_heads, c.head_dim)
+        q = ops.rmsnorm(q, w["q_norm"], c.rms_norm_eps, use_cuda=u)
+        k = ops.rmsnorm(k, w["k_norm"], c.rms_norm_eps, use_cuda=u)
+        q = ops.rope(q.unsqueeze(0), batch.positions, self.cos, self.sin, use_cuda=u).squeeze(0)
+        k = ops.rope(k.unsqueeze(0), batch.positions, self.cos, self.sin, use_cuda=u).squeeze(0)
+        kv = self.manager.kv
+        kv.write(layer, batch.slot_mapping, k, v)
+        out = ops.paged_attention(
+            q.contiguous(), kv.layer_keys(layer), kv.layer_values(layer), batch.block_tables,
+            batch.cu_seqlens_q, batch.context_lens, batch.seq_lens, batch.max_query_len,
+            batch.max_context_len, 1.0 / math.sqrt(c.head_dim), use_cuda=u)
+        return _linear(out.view(t, c.q_size), w["wo"])
+
+    @torch.no_grad()
+    def __call__(self, batch) -> torch.Tensor:
+        c = self.config
+        u = self.use_cuda
+        h = self.weights["embedding"].index_select(0, batch.input_ids)
+        for layer, w in enumerate(self.layers):
+            normed = ops.rmsnorm(h, w["attn_norm"], c.rms_norm_eps, use_cuda=u)
+            h = h + self._attention(layer, w, normed, batch)
+            normed = ops.rmsnorm(h, w["mlp_norm"], c.rms_norm_eps, use_cuda=u)
+            gated = ops.swiglu(_linear(normed, w["gate"]), _linear(normed, w["up"]), use_cuda=u)
+            h = h + _linear(gated, w["down"])
+        h = h.index_select(0, batch.last_row_indices)
+        h = ops.rmsnorm(h, self.weights["final_norm"], c.rms_norm_eps, use_cuda=u)
+        return _linear(h, self.weights["embedding"])

@@ -1,0 +1,46 @@
+"""One request's tokens and progress (reference serve/sequence.py).
+
+``num_computed_tokens`` counts positions whose K/V are in the pool; the rest of
+``token_ids`` is what the next passes compute. A pass that reaches the end of the
+tokens yields a sampled token; a prefill chunk that stops mid-prompt yields none.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+__all__ = ["Sequence"]
+
+
+@dataclass(eq=False)
+class Sequence:
+    seq_id: int
+    prompt: list[int]
+    max_tokens: int
+    output: list[int] = field(default_factory=list)
+    num_computed_tokens: int = 0
+    preemptions: int = 0
+
+    @property
+    def token_ids(self) -> list[int]:
+        return self.prompt + self.output
+
+    def __len__(self) -> int:
+        return len(self.prompt) + len(self.output)
+
+    @property
+    def num_uncomputed_tokens(self) -> int:
+        return len(self) - self.num_computed_tokens
+
+    def is_decoding(self) -> bool:
+        """Past its prompt: one new token per pass."""
+        return self.num_computed_tokens > 0 and self.num_uncomputed_tokens == 1 and bool(self.output)
+
+    def is_done(self) -> bool:
+        return len(self.output) >= self.max_tokens
+
+    def reset_for_recompute(self) -> None:
+        """Preempted: its pages are gone, so everything (prompt and output so far) is
+        recomputed as a prefill when it is readmitted (reference sequence.py:198-217)."""
+        self.num_computed_tokens = 0
+        self.preemptions += 1

@@ -1,0 +1,92 @@
+"""The paged engine on the CPU (PyTorch path) against the dense float64 recompute.
+
+The reference's engine tests (tests/test_engine.py:56-350) in this form: chunked and
+unchunked prefill, many sequences sharing iterations, preemption under a pool too small
+for everyone, an impossible pool, and no block leaks afterwards.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from engine_helpers import assert_tokens_match, make_engine, prompts, tiny_config
+from mini_vllm.block import OutOfBlocks
+from mini_vllm.model import random_weights
+from mini_vllm.serve import SchedulerConfig
+from oracle.qwen3_dense import generate_greedy
+
+MAX_TOKENS = 8
+
+
+@pytest.fixture(scope="module")
+def model():
+    config = tiny_config()
+    return config, random_weights(config, seed=3)
+
+
+@pytest.fixture(scope="module")
+def reference(model):
+    config, weights = model
+    ps = prompts(6, 3, 40, config.vocab_size, seed=1)
+    return ps, [generate_greedy(config, weights, p, MAX_TOKENS) for p in ps]
+
+
+@pytest.mark.parametrize("sched", [
+    SchedulerConfig(),                                                 # everything in one pass
+    SchedulerConfig(max_batched_tokens=16, chunk_size=8),             # chunked, piggybacked
+    SchedulerConfig(max_batched_tokens=64, enable_chunked_prefill=False),
+    SchedulerConfig(max_sequences=2, max_batched_tokens=24, chunk_size=5),
+], ids=["one-pass", "chunked", "unchunked", "two-at-a-time"])
+def test_engine_matches_dense_recompute(model, reference, sched):
+    config, weights = model
+    ps, want = reference
+    engine = make_engine(config, weights, sched=sched)
+    got = engine.generate(ps, MAX_TOKENS)
+    for i, (g, (tok, logits)) in enumerate(zip(got, want)):
+        assert_tokens_match(g, tok, logits, tie_tol=1e-4, msg=f"prompt {i}")
+    engine.model.manager.check_no_leaks()
+    assert engine.model.manager.num_free_blocks == engine.model.manager.num_blocks
+
+
+def test_preemption_under_a_small_pool_still_matches(model, reference):
+    config, weights = model
+    ps, want = reference
+    engine = make_engine(config, weights, num_blocks=6, block_size=8,
+                         sched=SchedulerConfig(max_batched_tokens=32, chunk_size=16))
+    got = engine.generate(ps, MAX_TOKENS)
+    assert engine.stats.preemptions > 0, "the pool was meant to force preemption"
+    for i, (g, (tok, logits)) in enumerate(zip(got, want)):
+        assert_tokens_match(g, tok, logits, tie_tol=1e-4, msg=f"prompt {i}")
+    engine.model.manager.check_no_leaks()
+
+
+def test_a_pool_that_cannot_hold_one_sequence_raises(model):
+    config, weights = model
+    engine = make_engine(config, weights, num_blocks=2, block_size=4)
+    with pytest.raises(OutOfBlocks):
+        engine.generate([list(range(40))], 4)
+
+
+def test_stats_count_what_ran(model):
+    config, weights = model
+    engine = make_engine(config, weights, sched=SchedulerConfig(max_batched_tokens=16, chunk_size=8))
+    ps = prompts(3, 5, 20, config.vocab_size, seed=4)
+    engine.generate(ps, 5)
+    s = engine.stats
+    assert s.generated_tokens == 15
+    assert s.prefill_tokens == sum(len(p) for p in ps)
+    assert s.decode_tokens == 3 * 4
+    assert s.decode_only_tokens <= s.decode_tokens
+
+
+def test_logits_rows_are_each_sequences_last_position(model):
+    """One row per sequence, at its own last computed position (test_engine.py:154-179)."""
+    config, weights = model
+    engine = make_engine(config, weights)
+    ps = prompts(3, 4, 12, config.vocab_size, seed=7)
+    seqs = [engine.add_request(p, 1) for p in ps]
+    engine.step()
+    for seq, p in zip(seqs, ps):
+        tok, _ = generate_greedy(config, weights, p, 1)
+        assert seq.output == tok
