@@ -108,6 +108,45 @@ def run_paged(batches, steps, warmup):
     return time_steps(step, steps, warmup)
 
 
+def run_engine(requests: int = 256, max_tokens: int = 256, max_sequences: int = 32) -> dict:
+    """a Qwen3-0.6B-shaped model (random init, std 0.02, bf16) served
+    by the paged engine with the HIP kernels: `requests` prompts of U[64, 2048] random
+    token ids (seed 0), `max_tokens` greedy tokens each (EOS ignored), continuous
+    batching with a 2048-token budget, 512-token chunks, `max_sequences` in flight."""
+    from mini_vllm.block import BlockManager
+    from mini_vllm.model import ModelConfig, Qwen3Paged, random_weights
+    from mini_vllm.serve import LLMEngine, SchedulerConfig
+
+    config = ModelConfig()
+    weights = random_weights(config, seed=0, device="cuda")
+    gen = torch.Generator().manual_seed(0)
+    lens = torch.randint(64, 2049, (requests,), generator=gen).tolist()
+    prompts = [torch.randint(0, config.vocab_size, (n,), generator=gen).tolist() for n in lens]
+    blocks = max_sequences * -(-(2048 + max_tokens) // 16) + 64
+    sched = SchedulerConfig(max_batched_tokens=2048, max_sequences=max_sequences, chunk_size=512)
+
+    def engine():
+        manager = BlockManager(blocks, 16, config.num_hidden_layers, config.num_key_value_heads,
+                               config.head_dim, config.dtype, "cuda")
+        return LLMEngine(Qwen3Paged(config, weights, manager, use_cuda=True), sched, device="cuda")
+
+    engine().generate(prompts[:4], 4)  # warm up kernels and BLAS handles
+    torch.cuda.synchronize()
+    eng = engine()
+    eng.generate(prompts, max_tokens)
+    torch.cuda.synchronize()
+    st = eng.stats
+    return {
+        "requests": requests, "max_tokens": max_tokens, "max_sequences": max_sequences,
+        "prompt_tokens": sum(lens), "generated_tokens": st.generated_tokens,
+        "iterations": st.iterations, "preemptions": st.preemptions,
+        "elapsed_s": round(st.elapsed_s, 3),
+        "output_tok_s": round(st.output_tokens_per_s, 1),
+        "decode_tok_s": round(st.decode_tokens_per_s, 1),
+        "decode_only_iterations": st.decode_only_iterations,
+    }
+
+
 def copy_ceiling(nbytes: int, steps: int = 20) -> float:
     """GB/s of a device-to-device copy_ (read + write counted), the practical ceiling
     (method of the reference's mini_vllm/bench.py:448-466)."""
@@ -160,8 +199,9 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--copies", type=int, default=3, help="rotated pool copies (defeat the MALL)")
     parser.add_argument("--skip-extras", action="store_true", help="headline config 2 only")
-    parser.add_argument("--extras", default="3,4,copy",
-                        help="comma list of extras to run: 3 (prefill), 4 (fp8 decode), copy")
+    parser.add_argument("--extras", default="3,4,5,copy",
+                        help="comma list of extras to run: 3 (prefill), 4 (fp8 decode), "
+                             "5 (engine), copy")
     parser.add_argument("--no-cpu", action="store_true")
     args = parser.parse_args()
 
@@ -218,6 +258,11 @@ def main() -> int:
             "frac_of_hbm_peak": round(fgbs / HBM_PEAK_GBS, 4)}
         log(f"config 4: {fms * 1e3:.1f} us, {fgbs:.0f} GB/s")
         del f8
+        torch.cuda.empty_cache()
+    if "5" in wanted:
+        log("config 5: Qwen3-0.6B-shaped engine, 256 requests x 256 tokens")
+        extras["config5_engine"] = run_engine()
+        log(f"config 5: {extras['config5_engine']}")
         torch.cuda.empty_cache()
     if "copy" in wanted:
         extras["copy_ceiling_gbs"] = round(copy_ceiling(1 << 30), 1)
