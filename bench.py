@@ -108,7 +108,8 @@ def run_paged(batches, steps, warmup):
     return time_steps(step, steps, warmup)
 
 
-def run_engine(requests: int = 256, max_tokens: int = 256, max_sequences: int = 32) -> dict:
+def run_engine(requests: int = 256, max_tokens: int = 256, max_sequences: int = 32,
+               use_graphs: bool = True) -> dict:
     """a Qwen3-0.6B-shaped model (random init, std 0.02, bf16) served
     by the paged engine with the HIP kernels: `requests` prompts of U[64, 2048] random
     token ids (seed 0), `max_tokens` greedy tokens each (EOS ignored), continuous
@@ -122,13 +123,14 @@ def run_engine(requests: int = 256, max_tokens: int = 256, max_sequences: int = 
     gen = torch.Generator().manual_seed(0)
     lens = torch.randint(64, 2049, (requests,), generator=gen).tolist()
     prompts = [torch.randint(0, config.vocab_size, (n,), generator=gen).tolist() for n in lens]
-    blocks = max_sequences * -(-(2048 + max_tokens) // 16) + 64
+    blocks = max_sequences * -(-(2048 + max_tokens) // 16) + 64 + 1  # + the graphs' dummy page
     sched = SchedulerConfig(max_batched_tokens=2048, max_sequences=max_sequences, chunk_size=512)
 
     def engine():
         manager = BlockManager(blocks, 16, config.num_hidden_layers, config.num_key_value_heads,
                                config.head_dim, config.dtype, "cuda")
-        return LLMEngine(Qwen3Paged(config, weights, manager, use_cuda=True), sched, device="cuda")
+        return LLMEngine(Qwen3Paged(config, weights, manager, use_cuda=True), sched, device="cuda",
+                         use_graphs=use_graphs)
 
     engine().generate(prompts[:4], 4)  # warm up kernels and BLAS handles
     torch.cuda.synchronize()
@@ -144,6 +146,7 @@ def run_engine(requests: int = 256, max_tokens: int = 256, max_sequences: int = 
         "output_tok_s": round(st.output_tokens_per_s, 1),
         "decode_tok_s": round(st.decode_tokens_per_s, 1),
         "decode_only_iterations": st.decode_only_iterations,
+        "decode_graphs": use_graphs,
     }
 
 
@@ -262,6 +265,8 @@ def main() -> int:
     if "5" in wanted:
         log("config 5: Qwen3-0.6B-shaped engine, 256 requests x 256 tokens")
         extras["config5_engine"] = run_engine()
+        log(f"config 5 (graphs on): {extras['config5_engine']}")
+        extras["config5_engine_eager"] = run_engine(use_graphs=False)
         log(f"config 5: {extras['config5_engine']}")
         torch.cuda.empty_cache()
     if "copy" in wanted:

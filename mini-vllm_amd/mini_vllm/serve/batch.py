@@ -48,7 +48,7 @@ class ForwardBatch:
             start = seq.num_computed_tokens
             if count < 1 or start + count > len(seq):
                 raise ValueError(f"sequence {seq.seq_id}: cannot compute {count} tokens from {start}")
-            ids.extend(seq.token_ids[start:start + count])
+            ids.extend(seq.tokens(start, count))
             positions.extend(range(start, start + count))
             offsets.append(offsets[-1] + count)
             lens.append(count)

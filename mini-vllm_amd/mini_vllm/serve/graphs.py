@@ -1,0 +1,132 @@
+"""Pure-decode iterations replayed from captured HIP graphs.
+
+A decode iteration of the paged model is ~15 ops per layer; dispatched one by one from
+Python it costs several milliseconds of host time for about one millisecond of GPU work
+(the reference lists this as the engine's next bottleneck, serve/batch.py:286-347,
+runner.py:65-66). Every op of a decode step reads its per-iteration inputs from device
+tensors -- token ids, positions, slots, context lengths, block tables -- and the host
+integers the launches depend on (batch size, an upper bound on the context) can be held
+fixed, so one captured graph serves every decode step of a given shape:
+
+* graphs are keyed by (batch bucket, table width): the batch is padded up to a bucket
+  with dummy sequences (one token of context in a reserved page, rows discarded), and
+  the block-table width is rounded up to a multiple of 64 pages;
+* before a replay, the iteration's metadata is packed into one pinned host buffer and
+  copied into the graph's static input tensors with one host-to-device copy;
+* sampling (argmax) runs after the replay, outside the graph.
+
+The paged-attention plan in stream mode depends only on the batch size and the bound on
+max_context_len, so the kernels launched inside a graph stay valid for every replay;
+they read the real context lengths from the static buffers.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from mini_vllm.serve.batch import PADDING_BLOCK, ForwardBatch
+
+__all__ = ["DecodeGraphs"]
+
+BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128, 256)
+TABLE_QUANTUM = 64  # pages
+
+
+class _Captured:
+    def __init__(self, model, batch_size: int, width: int, dummy_block: int, device) -> None:
+        p = model.manager.block_size
+        self.batch_size, self.width = batch_size, width
+        b = batch_size
+        i32 = dict(dtype=torch.int32, device=device)
+        i64 = dict(dtype=torch.int64, device=device)
+        # Dynamic inputs: [ids | positions] int64 and [context | slots | tables] int32.
+        self.dyn64 = torch.zeros(2 * b, **i64)
+        self.dyn32 = torch.zeros(2 * b + b * width, **i32)
+        self.host64 = torch.zeros(2 * b, dtype=torch.int64, pin_memory=True)
+        self.host32 = torch.zeros(2 * b + b * width, dtype=torch.int32, pin_memory=True)
+        self.batch = ForwardBatch(
+            input_ids=self.dyn64[:b],
+            positions=self.dyn64[b:],
+            cu_seqlens_q=torch.arange(b + 1, **i32),
+            seq_lens=torch.ones(b, **i32),
+            context_lens=self.dyn32[:b],
+            slot_mapping=self.dyn32[b:2 * b],
+            block_tables=self.dyn32[2 * b:].view(b, width),
+            last_row_indices=torch.arange(b, **i64),
+            max_query_len=1,
+            max_context_len=width * p,
+            seq_ids=tuple(range(b)),
+        )
+        self.dummy_block = dummy_block
+        self.model = model
+        self.graph = None
+        self.logits = None
+
+    def fill(self, scheduled) -> None:
+        b, w, p = self.batch_size, self.width, self.model.manager.block_size
+        manager = self.model.manager
+        ids, pos, ctx, slots = [0] * b, [0] * b, [1] * b, [self.dummy_block * p] * b
+        tables = [[self.dummy_block] + [PADDING_BLOCK] * (w - 1) for _ in range(b)]
+        for i, (seq, _) in enumerate(scheduled):
+            start = seq.num_computed_tokens
+            ids[i] = seq.tokens(start, 1)[0]
+            pos[i] = start
+            ctx[i] = start + 1
+            slots[i] = manager.slots(seq.seq_id, start, 1)[0]
+            table = manager.table(seq.seq_id)
+            tables[i] = table + [PADDING_BLOCK] * (w - len(table))
+        self.host64[:b] = torch.tensor(ids)
+        self.host64[b:] = torch.tensor(pos)
+        flat = ctx + slots + [x for row in tables for x in row]
+        self.host32.copy_(torch.tensor(flat, dtype=torch.int32))
+        self.dyn64.copy_(self.host64, non_blocking=True)
+        self.dyn32.copy_(self.host32, non_blocking=True)
+
+    def capture(self) -> None:
+        # Warm up on a side stream (allocator pools, BLAS handles), then capture.
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                self.model(self.batch)
+        torch.cuda.current_stream().wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.logits = self.model(self.batch)
+
+
+class DecodeGraphs:
+    """Replays pure-decode iterations of ``model`` from captured graphs."""
+
+    def __init__(self, model, max_batch: int = 32) -> None:
+        self.model = model
+        self.max_batch = max_batch
+        self.device = model.weights["embedding"].device
+        manager = model.manager
+        # A page no sequence ever owns: the dummy rows of a padded batch write there.
+        self._dummy_id = -1
+        manager.allocate(self._dummy_id, 1)
+        self.dummy_block = manager.table(self._dummy_id)[0]
+        self.graphs: dict[tuple[int, int], _Captured] = {}
+        self.replays = 0
+
+    def supports(self, scheduled) -> bool:
+        return 0 < len(scheduled) <= self.max_batch and all(n == 1 for _, n in scheduled)
+
+    def run(self, scheduled) -> torch.Tensor:
+        """Logits ``len(scheduled) x V`` for a pure-decode iteration."""
+        n = len(scheduled)
+        bucket = next(b for b in BUCKETS if b >= n)
+        widest = max(len(self.model.manager.table(s.seq_id)) for s, _ in scheduled)
+        width = -(-widest // TABLE_QUANTUM) * TABLE_QUANTUM
+        key = (bucket, width)
+        entry = self.graphs.get(key)
+        if entry is None:
+            entry = _Captured(self.model, bucket, width, self.dummy_block, self.device)
+            entry.fill(scheduled)
+            entry.capture()
+            self.graphs[key] = entry
+        entry.fill(scheduled)
+        entry.graph.replay()
+        self.replays += 1
+        return entry.logits[:n]

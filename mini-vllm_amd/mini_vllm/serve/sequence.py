@@ -28,6 +28,15 @@ class Sequence:
     def __len__(self) -> int:
         return len(self.prompt) + len(self.output)
 
+    def tokens(self, start: int, count: int) -> list[int]:
+        """``token_ids[start:start + count]`` without building the whole list."""
+        n = len(self.prompt)
+        if start + count <= n:
+            return self.prompt[start:start + count]
+        if start >= n:
+            return self.output[start - n:start - n + count]
+        return self.prompt[start:] + self.output[:start + count - n]
+
     @property
     def num_uncomputed_tokens(self) -> int:
         return len(self) - self.num_computed_tokens

@@ -71,6 +71,48 @@ def test_bf16_kernels_match_up_to_ties(extension, device, head_dim):
         engine.model.manager.check_no_leaks()
 
 
+@pytest.mark.parametrize("dtype,head_dim", [(torch.float32, 32), (torch.bfloat16, 128)])
+def test_decode_graphs_match_eager(extension, device, dtype, head_dim):
+    """Graph-replayed decode iterations against eager ones on the same padded static
+    batch: each replay is checked after eager work and a synchronization in between, and
+    the static inputs change between replays (the positions advance), so a replay that
+    reused stale inputs or state would differ."""
+    from mini_vllm.serve.graphs import DecodeGraphs
+
+    config = tiny_config(dtype, head_dim=head_dim)
+    weights = random_weights(config, seed=4, device=device)
+    engine = make_engine(config, weights, use_cuda=True, device=device)
+    seqs = [engine.add_request(p, 100) for p in prompts(3, 5, 40, config.vocab_size, seed=6)]
+    engine.step()  # prefill; now every sequence decodes
+    graphs = DecodeGraphs(engine.model, max_batch=4)
+    for step in range(4):
+        out = engine.scheduler.schedule()
+        assert graphs.supports(out.scheduled)
+        replayed = graphs.run(out.scheduled).float().clone()
+        entry = next(iter(graphs.graphs.values()))
+        eager = engine.model(entry.batch)[: len(out.scheduled)].float()  # same static batch
+        torch.cuda.synchronize()
+        assert torch.allclose(replayed, eager, atol=1e-5 if dtype == torch.float32 else 2e-2,
+                              rtol=0), f"replay {step}: {(replayed - eager).abs().max()}"
+        engine.scheduler.commit(out, replayed.argmax(-1).tolist())
+    assert graphs.replays == 4 and len(graphs.graphs) == 1
+
+
+@pytest.mark.parametrize("sched", [SchedulerConfig(), SchedulerConfig(max_batched_tokens=24, chunk_size=8)],
+                         ids=["one-pass", "chunked"])
+def test_engine_with_decode_graphs_matches_dense_recompute(extension, device, sched):
+    config = tiny_config(torch.float32)
+    weights = random_weights(config, seed=5, device=device)
+    ps = prompts(6, 3, 60, config.vocab_size, seed=2)
+    want = _reference(config, weights, ps)
+    engine = make_engine(config, weights, use_cuda=True, device=device, sched=sched,
+                         use_graphs=True)
+    got = engine.generate(ps, MAX_TOKENS)
+    assert engine.graphs.replays > 0
+    for i, (g, (tok, logits)) in enumerate(zip(got, want)):
+        assert_tokens_match(g, tok, logits, tie_tol=1e-4, msg=f"prompt {i}")
+
+
 @pytest.mark.slow
 def test_qwen3_0_6b_shape_end_to_end(extension, device):
     """BASELINE config 5's model shape (28 layers, 16q/8kv, D=128, vocab 151936, bf16),
