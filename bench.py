@@ -150,6 +150,46 @@ def run_engine(requests: int = 256, max_tokens: int = 256, max_sequences: int = 
     }
 
 
+def run_elementwise(steps: int = 20) -> dict:
+    """RMSNorm (E=1024 and per-head D=128), RoPE (16 heads x 128) and SwiGLU (I=3072)
+    at bf16 on ~256 MB operands, three rotated copies each so every call reads HBM.
+    Bytes are algorithmic (the reference's rule, mini_vllm/bench.py:531-580): inputs
+    read once and outputs written once; RoPE also reads each token's cos/sin rows."""
+    from mini_vllm.kernels import ops
+    from mini_vllm.torch_path import rope_tables
+
+    bf = torch.bfloat16
+    out = {}
+
+    def measure(name, make, call, nbytes):
+        bufs = [make() for _ in range(3)]
+        ms = time_steps(lambda i: call(*bufs[i % 3]), steps, 3)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"us": round(ms * 1e3, 1), "gbs": round(gbs, 1),
+                     "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"elementwise {name}: {ms * 1e3:.1f} us, {gbs:.0f} GB/s")
+        del bufs
+        torch.cuda.empty_cache()
+
+    rows = 1 << 17
+    w = torch.ones(1024, device="cuda", dtype=bf)
+    measure("rmsnorm_E1024", lambda: (torch.randn(rows, 1024, device="cuda", dtype=bf),),
+            lambda x: ops.rmsnorm(x, w, 1e-6, use_cuda=True), 2 * rows * 1024 * 2 + 1024 * 2)
+    wq = torch.ones(128, device="cuda", dtype=bf)
+    tokens = 1 << 16
+    measure("qk_norm_16x128", lambda: (torch.randn(tokens, 16, 128, device="cuda", dtype=bf),),
+            lambda x: ops.rmsnorm(x, wq, 1e-6, use_cuda=True), 2 * tokens * 16 * 128 * 2 + 256)
+    cos, sin = rope_tables(128, tokens, device="cuda")
+    pos = torch.arange(tokens, device="cuda")
+    measure("rope_16x128", lambda: (torch.randn(1, tokens, 16, 128, device="cuda", dtype=bf),),
+            lambda x: ops.rope(x, pos, cos, sin, use_cuda=True),
+            2 * tokens * 16 * 128 * 2 + 2 * tokens * 128 * 4)
+    measure("swiglu_I3072", lambda: (torch.randn(tokens, 3072, device="cuda", dtype=bf),
+                                     torch.randn(tokens, 3072, device="cuda", dtype=bf)),
+            lambda g, u: ops.swiglu(g, u, use_cuda=True), 3 * tokens * 3072 * 2)
+    return out
+
+
 def copy_ceiling(nbytes: int, steps: int = 20) -> float:
     """GB/s of a device-to-device copy_ (read + write counted), the practical ceiling
     (method of the reference's mini_vllm/bench.py:448-466)."""
@@ -202,9 +242,9 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--copies", type=int, default=3, help="rotated pool copies (defeat the MALL)")
     parser.add_argument("--skip-extras", action="store_true", help="headline config 2 only")
-    parser.add_argument("--extras", default="3,4,5,copy",
+    parser.add_argument("--extras", default="3,4,5,ew,copy",
                         help="comma list of extras to run: 3 (prefill), 4 (fp8 decode), "
-                             "5 (engine), copy")
+                             "5 (engine), ew (elementwise kernels), copy")
     parser.add_argument("--no-cpu", action="store_true")
     args = parser.parse_args()
 
@@ -262,12 +302,12 @@ def main() -> int:
         log(f"config 4: {fms * 1e3:.1f} us, {fgbs:.0f} GB/s")
         del f8
         torch.cuda.empty_cache()
+    if "ew" in wanted:
+        extras["elementwise"] = run_elementwise()
     if "5" in wanted:
         log("config 5: Qwen3-0.6B-shaped engine, 256 requests x 256 tokens")
         extras["config5_engine"] = run_engine()
-        log(f"config 5 (graphs on): {extras['config5_engine']}")
-        extras["config5_engine_eager"] = run_engine(use_graphs=False)
-        log(f"config 5: {extras['config5_engine']}")
+        log(f"config 5 (decode graphs on): {extras['config5_engine']}")
         torch.cuda.empty_cache()
     if "copy" in wanted:
         extras["copy_ceiling_gbs"] = round(copy_ceiling(1 << 30), 1)

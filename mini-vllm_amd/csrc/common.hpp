@@ -154,6 +154,15 @@ __device__ __forceinline__ void store16(void* p, const u32x4& v) {
   *reinterpret_cast<u32x4*>(p) = v;
 }
 
+// Streaming variants: data touched once per call is loaded and stored nontemporally,
+// so it does not displace lines that other waves reuse (page tables, weights, tables).
+__device__ __forceinline__ u32x4 nt_load16(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ void nt_store16(void* p, const u32x4& v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
 // ------------------------------------------------------------------- reductions
 
 // DPP control codes (GFX9 encoding).

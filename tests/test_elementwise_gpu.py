@@ -105,6 +105,29 @@ def test_rope_matches_the_oracle_and_torch_bitwise(extension, device, dtype, pos
     assert torch.equal(got, on_gpu)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_dim", [64, 80, 12, 256])
+def test_rope_head_dims_vector_and_scalar_paths(extension, device, dtype, head_dim):
+    # 64/80/256 take the 16-byte-chunk kernel for every dtype; 12 (halves of 6) does not
+    # divide into chunks and takes the per-pair kernel.
+    cos, sin = torch_path.rope_tables(head_dim, 300)
+    x = torch.randn(2, 9, 3, head_dim).to(dtype)
+    positions = torch.randint(0, 300, (9,), dtype=torch.int64)
+    got = extension.rope(x.to(device), positions.to(device), cos.to(device), sin.to(device))
+    want = ew.apply_rope(x.float().numpy(), positions.numpy(), cos.numpy(),
+                         sin.numpy(), NAMES[dtype])
+    assert np.array_equal(got.float().cpu().numpy(), want.reshape(got.shape))
+
+
+def test_rope_misaligned_input_takes_the_pair_kernel(extension, device):
+    cos, sin = (t.to(device) for t in torch_path.rope_tables(128, 64))
+    base = torch.randn(1 + 5 * 2 * 128, dtype=torch.bfloat16, device=device)
+    x = base[1:].view(1, 5, 2, 128)
+    pos = torch.arange(5, device=device)
+    assert torch.equal(extension.rope(x, pos, cos, sin),
+                       torch_path.apply_rope(x.contiguous(), pos, cos, sin))
+
+
 def test_rope_position_zero_is_identity_and_norms_are_kept(extension, device):
     cos, sin = (t.to(device) for t in torch_path.rope_tables(128, 64))
     x = torch.randn(1, 8, 4, 128, device=device)
