@@ -58,6 +58,10 @@ typedef struct mvllm_paged_plan {
   int32_t split_tokens;      /* grid modes: keys per split */
   int32_t prefill_mfma;      /* 1: prefill rows go to the MFMA prefill kernel */
   uint64_t workspace_bytes;  /* split partials and their index; 0 when none are needed */
+  int32_t prefill_workgroups; /* MFMA prefill: > 0 persistent workgroups with balanced
+                                 shares of all key tiles (cut items merged after);
+                                 0 one workgroup per (sequence, heads, query tile) */
+  int32_t reserved;
 } mvllm_paged_plan;
 
 /* Plan a paged_attention call. Depends only on the host-side sizes below (never on

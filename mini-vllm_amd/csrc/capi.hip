@@ -109,14 +109,62 @@ struct Plan {
   int max_splits = 1;
   uint64_t off_o = 0;       // byte offsets into the workspace
   uint64_t off_ml = 0;
+  uint64_t off_pf = 0;      // stream prefill: [prefix][O partials][(m, l) partials]
+  uint64_t off_pf_o = 0;
+  uint64_t off_pf_ml = 0;
 };
 
 uint64_t align256(uint64_t v) { return (v + 255) / 256 * 256; }
+
+void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk,
+                 int32_t d, int32_t block_size, int32_t max_q, int32_t max_ctx, int32_t q_dtype,
+                 int32_t kv_dtype);
+
+// The MFMA prefill's schedule. The grid (one workgroup per 128-query item) is chosen
+// when there are at least as many items as CUs: the hardware dispatcher then balances
+// them, with no partials to merge. With fewer items (a chunk of a long prompt, a
+// prefill beside decodes) the grid would leave CUs idle behind a few long items, so
+// the stream schedule is used: one persistent workgroup per CU (times
+// MVLLM_PREFILL_WGS_PER_CU) with balanced shares of all key tiles, cut items merged
+// after (measured at 8K-16K contexts: 2.5-3x the grid). The item count is estimated
+// from host sizes: ceil(num_tokens / 128) query tiles per kv column.
+// MVLLM_PREFILL_SCHEDULE=1 / 2 forces stream / grid. The stream's workspace follows
+// the decode part's.
+void plan_prefill(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk,
+                  int32_t d) {
+  if (!plan.pub.prefill_mfma) return;
+  if (num_seqs > mvllm::kMaxStreamSeqs) return;
+  const int forced = env_int("MVLLM_PREFILL_SCHEDULE", 0);
+  if (forced == 2) return;
+  const int64_t items = static_cast<int64_t>((num_tokens + mvllm::kPrefillQueryTile - 1) /
+                                             mvllm::kPrefillQueryTile) *
+                        (hq / mvllm::prefill_item_heads(hq / hk));
+  if (forced != 1 && items >= device_cus()) return;
+  const int64_t per_cu = env_int("MVLLM_PREFILL_WGS_PER_CU", 1);
+  int64_t wgs = (per_cu > 0 ? per_cu : 1) * device_cus();
+  if (wgs > mvllm::kMaxPrefillWgs) wgs = mvllm::kMaxPrefillWgs;
+  const uint64_t rows = static_cast<uint64_t>(2 * wgs) * mvllm::prefill_item_heads(hq / hk) *
+                        mvllm::kPrefillQueryTile;
+  plan.pub.prefill_workgroups = static_cast<int32_t>(wgs);
+  plan.off_pf = align256(plan.pub.workspace_bytes);
+  plan.off_pf_o = plan.off_pf + align256(static_cast<uint64_t>(num_seqs + 1) * sizeof(int));
+  plan.off_pf_ml = plan.off_pf_o + align256(rows * d * sizeof(float));
+  plan.pub.workspace_bytes = plan.off_pf_ml + align256(rows * 2 * sizeof(float));
+}
 
 Plan make_plan(int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk, int32_t d,
                int32_t block_size, int32_t max_q, int32_t max_ctx, int32_t q_dtype,
                int32_t kv_dtype) {
   Plan plan{};
+  plan_decode(plan, num_tokens, num_seqs, hq, hk, d, block_size, max_q, max_ctx, q_dtype,
+              kv_dtype);
+  plan_prefill(plan, num_tokens, num_seqs, hq, hk, d);
+  return plan;
+}
+
+void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk,
+                 int32_t d, int32_t block_size, int32_t max_q, int32_t max_ctx, int32_t q_dtype,
+                 int32_t kv_dtype) {
   const bool has_prefill = max_q > 1;
   const bool mfma =
       has_prefill && mvllm::paged_prefill_supported(q_dtype, kv_dtype, d, hq, hk, block_size);
@@ -154,9 +202,9 @@ Plan make_plan(int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk, int
     plan.off_o = head;
     plan.off_ml = plan.off_o + align256(entries * d * sizeof(float));
     plan.pub.workspace_bytes = plan.off_ml + align256(entries * 2 * sizeof(float));
-    return plan;
+    return;
   }
-  if (plan.pub.decode_mode == MVLLM_DECODE_NONE) return plan;
+  if (plan.pub.decode_mode == MVLLM_DECODE_NONE) return;
 
   // Grid schedules: split each row's context until the grid holds ~16 waves per CU,
   // in splits of 64..1024 keys.
@@ -179,7 +227,6 @@ Plan make_plan(int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk, int
     plan.off_ml = align256(entries * d * sizeof(float));
     plan.pub.workspace_bytes = plan.off_ml + align256(entries * 2 * sizeof(float));
   }
-  return plan;
 }
 
 }  // namespace
@@ -188,7 +235,7 @@ extern "C" {
 
 const char* mvllm_last_error(void) { return g_error; }
 
-int mvllm_abi_version(void) { return 1; }
+int mvllm_abi_version(void) { return 2; }
 
 int mvllm_paged_attention_plan(int32_t num_tokens, int32_t num_seqs, int32_t num_q_heads,
                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
@@ -279,6 +326,12 @@ int mvllm_paged_attention(void* out, const void* q, const void* key_pool,
     if (plan.pub.decode_mode == MVLLM_DECODE_STREAM) p.seq_prefix = reinterpret_cast<int*>(ws);
     p.part_o = reinterpret_cast<float*>(ws + plan.off_o);
     p.part_ml = reinterpret_cast<float*>(ws + plan.off_ml);
+    if (plan.pub.prefill_workgroups > 0) {
+      p.pf_wgs = plan.pub.prefill_workgroups;
+      p.pf_prefix = reinterpret_cast<int*>(ws + plan.off_pf);
+      p.pf_o = reinterpret_cast<float*>(ws + plan.off_pf_o);
+      p.pf_ml = reinterpret_cast<float*>(ws + plan.off_pf_ml);
+    }
   }
 
   const hipStream_t s = static_cast<hipStream_t>(stream);

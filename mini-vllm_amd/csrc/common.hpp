@@ -163,6 +163,13 @@ __device__ __forceinline__ void nt_store16(void* p, const u32x4& v) {
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
 
+// A workgroup-uniform load of read-only metadata through the scalar cache (s_load): it
+// is waited for on its own counter, so it does not drain outstanding vector loads.
+typedef __attribute__((address_space(4))) const int32_t constant_i32;
+__device__ __forceinline__ int32_t sload(const int32_t* p) {
+  return *reinterpret_cast<constant_i32*>(reinterpret_cast<uintptr_t>(p));
+}
+
 // ------------------------------------------------------------------- reductions
 
 // DPP control codes (GFX9 encoding).

@@ -16,6 +16,38 @@ constexpr int kMaxSplitTokens = 1024;
 // The stream schedule scans the context lengths of up to this many sequences in LDS.
 constexpr int kMaxStreamSeqs = 4096;
 
+// Query positions per prefill work item (4 waves x 32 MFMA columns) and keys per tile.
+constexpr int kPrefillQueryTile = 128;
+// Most stream-prefill workgroups (the merge lists an item's pieces in LDS).
+constexpr int kMaxPrefillWgs = 2048;
+// XCDs (each with its own L2) that workgroups are dispatched to round robin on MI355X.
+constexpr int kXcds = 8;
+constexpr int kPrefillKeyTile = 64;
+
+// Query heads per prefill work item: two heads of a GQA group share every K/V tile
+// staged in LDS when the group size is even.
+__host__ __device__ inline int prefill_item_heads(int group) { return group % 2 == 0 ? 2 : 1; }
+
+// Key tiles the prefill workgroup of query tile q walks for a sequence of `context`
+// keys and `len` query tokens: keys [0, context - len + min((q + 1) * 128, len)).
+__host__ __device__ inline int prefill_item_tiles(int context, int len, int q) {
+  const int last = (q + 1) * kPrefillQueryTile < len ? (q + 1) * kPrefillQueryTile : len;
+  return (context - len + last + kPrefillKeyTile - 1) / kPrefillKeyTile;
+}
+
+// Equal shares of `total` work units over `wgs` workgroups: workgroup w owns
+// [floor(w * total / wgs), floor((w + 1) * total / wgs)).
+__host__ __device__ inline int64_t share_begin(int64_t w, int64_t total, int64_t wgs) {
+  return w * total / wgs;
+}
+// The workgroup owning unit x: the largest w whose share starts at or before x.
+__host__ __device__ inline int64_t share_owner(int64_t x, int64_t total, int64_t wgs) {
+  return ((x + 1) * wgs - 1) / total;
+}
+__host__ __device__ inline bool share_nonempty(int64_t w, int64_t total, int64_t wgs) {
+  return (w * total) / wgs < ((w + 1) * total) / wgs;
+}
+
 // Query heads per decode wave for a GQA group of `group` heads.
 __host__ __device__ inline int decode_group_chunk(int group) {
   return group % 4 == 0 ? 4 : (group % 2 == 0 ? 2 : 1);
@@ -47,6 +79,11 @@ struct PagedParams {
   float* part_o;      // split partials, D fp32 each
   float* part_ml;     // split partials' (running max in log2 units, sum)
   int* seq_prefix;    // stream decode: [num_seqs + 1] decode keys before each sequence
+  int pf_wgs;         // prefill: > 0 selects the stream schedule with this many workgroups
+  int* pf_prefix;     // stream prefill: [num_seqs + 1] work units before each sequence
+  float* pf_o;        // stream prefill partials: [2 * pf_wgs][heads][128][D] fp32, each
+                      // piece normalised by its own sum
+  float* pf_ml;       // their (max in log2 units, sum) per row: [2 * pf_wgs][heads][128][2]
 };
 
 // Splits of one row: as many as its visible context needs at `split_tokens` keys

@@ -296,19 +296,6 @@ __device__ __forceinline__ bool wave_unit(const PagedParams& p, int unit, int& k
 
 // ------------------------------------------------------------ stream schedule
 
-namespace {
-
-// Workgroup owning decode key x of `total` split over `wgs` equal shares
-// [floor(w*total/wgs), floor((w+1)*total/wgs)): the largest such w with start <= x.
-__device__ __forceinline__ int64_t share_owner(int64_t x, int64_t total, int64_t wgs) {
-  return ((x + 1) * wgs - 1) / total;
-}
-__device__ __forceinline__ bool share_nonempty(int64_t w, int64_t total, int64_t wgs) {
-  return (w * total) / wgs < ((w + 1) * total) / wgs;
-}
-
-}  // namespace
-
 template <typename TQ, typename TKV, int D, int GC>
 __global__ __launch_bounds__(512) void paged_decode_stream_kernel(const PagedParams p) {
   using K = Decode<TKV, D, GC>;

@@ -8,12 +8,24 @@
 //
 // Design (this library's own):
 //
-//  * workgroup = (128 query positions, kv head, HC = 2 (or 1) query heads of its GQA
-//    group); wave w owns 32 positions for all HC heads, so every K or V fragment read
-//    from LDS feeds HC MFMAs. The waves share the K/V tiles of their kv head,
-//    page-gathered from HBM into LDS 64 keys at a time, double buffered; page ids are
-//    fetched two tiles ahead and K/V one tile ahead, so the tile loop never waits on a
-//    block-table read.
+//  * work item = (sequence, column, query tile): 128 query positions of HW query heads
+//    (HW = 2 heads of one GQA group when the group is even) against one kv head. Its
+//    cost is the number of 64-key tiles it walks; items are laid end to end in
+//    (sequence, column, query tile) order.
+//  * stream schedule: one persistent workgroup per CU. An in-kernel prefix scan of the
+//    per-sequence costs (no host read of device data) gives every workgroup an equal
+//    share of all key tiles, whatever the spread of prefix lengths; an item cut
+//    between workgroups leaves (m, l, O) partials that paged_prefill_merge_kernel
+//    combines. A share's partial pieces are at most its first and its last, stored
+//    in slots 2w and 2w + 1. Shares are assigned XCD by XCD. Grid schedule (more than kMaxStreamSeqs sequences): one
+//    workgroup per item, whole.
+//  * workgroup = 4 x HS waves: wave (hs, w) owns query positions 32w .. 32w+31 of
+//    HCW = HW / HS heads. The launches use HS = HW (one head per wave): for a GQA
+//    pair, 8 waves, two per SIMD, one's softmax under the other's MFMAs.
+//  * K/V tiles of 64 keys are page-gathered from HBM into LDS, double buffered; page
+//    ids (and fp8 scales) are fetched four tiles ahead and K/V two tiles ahead (two
+//    register sets), across item boundaries, so each load has two loop iterations to
+//    arrive; per-sequence metadata comes through the scalar cache.
 //  * scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_{bf16,f16}:
 //    a lane then owns one query column and 16 keys per 32-key block, so the softmax
 //    row max is an in-lane max plus one xor-32 exchange.
@@ -21,8 +33,12 @@
 //    accumulators (converted to bf16/fp16); the MFMA's reduction axis is keys, so the
 //    accumulator's key order is used as-is and V^T is read with the same key
 //    permutation. V is transposed on its way into LDS.
-//  * online softmax in fp32, log2 domain; causal masking only on tiles that cross the
-//    diagonal; tiles past a wave's last visible key are skipped.
+//  * online softmax in fp32, log2 domain, the score scale folded into the exponent's
+//    FMA. The running max is raised only when a row's tile max exceeds it by more than
+//    8 (so exponentials stay <= 2^8): O is rescaled a handful of times per item rather
+//    than every tile, exactly (O and l always refer to the same max).
+//  * causal masking only on tiles that cross the diagonal; tiles past a wave's last
+//    visible key are skipped.
 //  * fp8-e4m3 pools are dequantised (x * per-(page, kv head) scale) while staging
 //    into LDS, and the MFMAs run in the query's 16-bit type.
 //
@@ -30,6 +46,10 @@
 //   A[m][k]: lane holds m = l32, k = 8h .. 8h+7
 //   B[k][n]: lane holds n = l32, k = 8h .. 8h+7
 //   C[m][n]: lane holds n = l32, m = 8j + 4h + i for j, i in 0..3 (register 4j + i)
+
+#include <climits>
+#include <cstdlib>
+#include <type_traits>
 
 #include "common.hpp"
 #include "paged_attention.hpp"
@@ -39,8 +59,8 @@ namespace mvllm {
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kTileKeys = 64;
-constexpr int kThreadsMax = 256;
+constexpr int kTileKeys = kPrefillKeyTile;
+constexpr float kRescaleSlack = 8.0f;  // log2 units: exponentials stay <= 2^8
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
@@ -87,193 +107,314 @@ template <typename TQ> struct Stage<TQ, fp8_t> {
 
 }  // namespace
 
-template <typename TQ, typename TKV, int D, int HC>
-__global__ __launch_bounds__(kThreadsMax) void paged_prefill_kernel(const PagedParams p) {
-  constexpr int kKStride = D + 8;            // K tile row, 16-bit elements (16 B pad)
-  constexpr int kVStride = kTileKeys + 4;    // V^T tile row, 16-bit elements (8 B pad)
-  constexpr int kKSteps = D / 16;            // MFMA k-steps over the head dim
-  constexpr int kDBlocks = D / 32;           // 32-row blocks of O^T
-  constexpr int kKUnits = kTileKeys * D / 8 / kThreadsMax;  // 8-element K units per thread
-  constexpr int kVPairs = 16 * (D / 8);                     // (key quad, dim octet) pairs
-  constexpr int kVUnits = (kVPairs + kThreadsMax - 1) / kThreadsMax;
+namespace {
+
+// A position in the stream of work: unit u = key tile t of item (s, c, q), which has
+// nt tiles; context / len of sequence s. Every field is workgroup-uniform.
+struct Cursor {
+  int u, s, c, q, t, nt, context, len;
+};
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Share index of workgroup `bid` of `n`: workgroups are dispatched to the XCDs round
+// robin, so this gives the workgroups of one XCD consecutive shares (the items one L2
+// serves are few, their K/V tiles reused from it).
+__device__ __forceinline__ int xcd_share(int bid, int n) {
+  return n % kXcds == 0 ? (bid % kXcds) * (n / kXcds) + bid / kXcds : bid;
+}
+
+// Work units of sequence s over all its items (0 for decode rows).
+__device__ __forceinline__ int prefill_seq_units(int context, int len, int cols) {
+  if (len <= 1) return 0;
+  const int qtiles = (len + kPrefillQueryTile - 1) / kPrefillQueryTile;
+  int units = 0;
+  for (int q = 0; q < qtiles; ++q) units += prefill_item_tiles(context, len, q);
+  return units * cols;
+}
+
+// Position `k` at unit u of the stream described by the prefix `pre` ([n + 1] work
+// units before each sequence, pre[n] > u).
+__device__ __forceinline__ void seek(Cursor& k, const PagedParams& p, const int* pre, int n,
+                                     int cols, int u) {
+  int a = 0, b = n;  // invariant: pre[a] <= u < pre[b]
+  while (b - a > 1) {
+    const int mid = (a + b) >> 1;
+    if (uniform(pre[mid]) <= u) a = mid; else b = mid;
+  }
+  k.u = u;
+  k.s = a;
+  k.context = sload(p.context_lens + a);
+  k.len = sload(p.seq_lens + a);
+  const int base = uniform(pre[a]);
+  const int per_col = (uniform(pre[a + 1]) - base) / cols;
+  int r = u - base;
+  k.c = r / per_col;
+  r -= k.c * per_col;
+  k.q = 0;
+  k.nt = prefill_item_tiles(k.context, k.len, 0);
+  while (r >= k.nt) {
+    r -= k.nt;
+    ++k.q;
+    k.nt = prefill_item_tiles(k.context, k.len, k.q);
+  }
+  k.t = r;
+}
+
+}  // namespace
+
+template <typename TQ, typename TKV, int D, int HCW, int HS>
+__global__ __launch_bounds__(256 * HS) void paged_prefill_kernel(const PagedParams p) {
+  constexpr int kThreads = 256 * HS;
+  constexpr int HW = HCW * HS;                  // query heads per work item
+  constexpr int kKStride = D + 8;               // K tile row, 16-bit elements (16 B pad)
+  constexpr int kVStride = kTileKeys + 4;       // V^T tile row, 16-bit elements (8 B pad)
+  constexpr int kKSteps = D / 16;               // MFMA k-steps over the head dim
+  constexpr int kDBlocks = D / 32;              // 32-row blocks of O^T
+  constexpr int kKUnits = kTileKeys * D / 8 / kThreads;  // 16-byte K pieces per thread
+  constexpr int kVKeys = kKUnits < 4 ? kKUnits : 4;       // keys per V staging unit
+  constexpr int kVGroups = kTileKeys / kVKeys;
+  constexpr int kVUnits = kVGroups * (D / 8) / kThreads;  // V units per thread
   constexpr int kElemBytes = Elem<TKV>::kBytes;
   constexpr bool kFp8 = kElemBytes == 1;
-  constexpr int kWaves = kThreadsMax / kWave;  // 4 waves x 32 query positions
-  static_assert(kKUnits >= 1, "head dim too small for the staging map");
+  static_assert(kKUnits >= 1 && kVUnits >= 1 && kVGroups * (D / 8) % kThreads == 0,
+                "staging map does not cover the tile");
+  static_assert(kTileKeys == kPrefillKeyTile && 32 * 4 == kPrefillQueryTile, "tile sizes");
 
   __shared__ __align__(16) uint16_t k_lds[2][kTileKeys * kKStride];
   __shared__ __align__(16) uint16_t v_lds[2][D * kVStride];
-
-  // Grid (head chunks, sequences, query tiles), the query tile slowest and reversed:
-  // workgroups are dispatched in index order, so the last (longest) query tiles of all
-  // sequences start first and the short ones fill in behind them.
-  const int seq = blockIdx.y;
-  const int query_len = p.seq_lens[seq];
-  if (query_len <= 1) return;  // a decode step: the decode kernel has it
-  const int qtiles = (query_len + 32 * kWaves - 1) / (32 * kWaves);
-  const int qt = static_cast<int>(gridDim.z) - 1 - static_cast<int>(blockIdx.z);
-  if (qt < 0 || qt >= qtiles) return;
-  const int qb = qt * 32 * kWaves;
-
-  const int group = p.hq / p.hk;
-  const int chunks = group / HC;
-  const int kvh = blockIdx.x / chunks;
-  const int head0 = kvh * group + (blockIdx.x % chunks) * HC;
-
-  const int context = p.context_lens[seq];
-  const int offset = context - query_len;  // causal offset S - L
-  const int row_base = p.cu_seqlens_q[seq];
-  const int32_t* table = p.block_tables + static_cast<int64_t>(seq) * p.max_blocks;
+  __shared__ int s_prefix[kMaxStreamSeqs + 1];
 
   const int tid = threadIdx.x;
-  const int wave = tid / kWave;
+  const int wave = uniform(tid / kWave);
   const int lane = tid % kWave;
   const int l32 = lane & 31;
   const int hsel = lane >> 5;
+  const int hs = wave / 4;   // head set
+  const int wq = wave % 4;   // 32-position query block
 
-  // Workgroup-wide key range, and this wave's.
-  const int wg_last = min(qb + 32 * kWaves, query_len);
-  const int kv_end = offset + wg_last;  // keys [0, kv_end) are visible to someone here
-  const int ntiles = (kv_end + kTileKeys - 1) / kTileKeys;
-  const int w_first = qb + 32 * wave;                  // first local query of this wave
-  const bool w_active = w_first < query_len;
-  const int w_kv_end = offset + min(w_first + 32, query_len);  // no query of the wave looks past
-  const int w_kv_full = offset + w_first + 1;          // below this, every query sees the key
+  const int n = p.num_seqs;
+  const int group = p.hq / p.hk;
+  const int chunks = group / HW;
+  const int cols = p.hk * chunks;
+  const bool stream = p.pf_wgs > 0;
+  const int share = xcd_share(blockIdx.x, gridDim.x);
 
-  // This lane's query (column l32 of the wave's tile), the same for its HC heads.
-  const int my_local = w_first + l32;
-  const bool my_valid = my_local < query_len;
-  const int my_visible = offset + my_local + 1;
-
-  // Q^T operands: lane holds q[row][head0 + h][16*ks + 8*hsel .. +7] for each k-step.
-  u32x4 qop[HC][kKSteps];
-  {
-    const int local = min(w_active ? (my_valid ? my_local : w_first) : 0, query_len - 1);
+  // ---- this workgroup's units [u0, u1) and the cursor at u0.
+  Cursor cur;
+  int u0, u1;
+  if (stream) {
+    // Prefix scan of the sequences' work units by wave 0: each lane sums a contiguous
+    // run, then a 64-lane inclusive scan.
+    if (tid < kWave) {
+      const int per = (n + kWave - 1) / kWave;
+      const int begin = min(tid * per, n);
+      const int end = min(begin + per, n);
+      int run = 0;
+      for (int s = begin; s < end; ++s) run += prefill_seq_units(p.context_lens[s], p.seq_lens[s], cols);
+      int incl = run;
 #pragma unroll
-    for (int h = 0; h < HC; ++h) {
-      const int64_t qrow = static_cast<int64_t>(row_base + local) * p.hq + head0 + h;
-      const char* qp = static_cast<const char*>(p.q) + (qrow * D + 8 * hsel) * 2;
-#pragma unroll
-      for (int ks = 0; ks < kKSteps; ++ks) qop[h][ks] = load16(qp + ks * 32);
+      for (int off = 1; off < kWave; off <<= 1) {
+        const int other = __shfl_up(incl, off, kWave);
+        if (tid >= off) incl += other;
+      }
+      int acc = incl - run;
+      for (int s = begin; s < end; ++s) {
+        s_prefix[s] = acc;
+        acc += prefill_seq_units(p.context_lens[s], p.seq_lens[s], cols);
+      }
+      if (tid == kWave - 1) s_prefix[n] = incl;
     }
+    __syncthreads();
+    const int total = uniform(s_prefix[n]);
+    if (blockIdx.x == 0) {
+      for (int s = tid; s <= n; s += kThreads) p.pf_prefix[s] = s_prefix[s];
+    }
+    u0 = static_cast<int>(share_begin(share, total, gridDim.x));
+    u1 = static_cast<int>(share_begin(share + 1, total, gridDim.x));
+    if (u0 >= u1) return;  // whole workgroup: no barrier follows for it
+    seek(cur, p, s_prefix, n, cols, u0);
+  } else {
+    cur.s = blockIdx.y;
+    cur.len = sload(p.seq_lens + cur.s);
+    cur.context = sload(p.context_lens + cur.s);
+    if (cur.len <= 1) return;  // a decode row: the decode kernel has it
+    const int qtiles = (cur.len + kPrefillQueryTile - 1) / kPrefillQueryTile;
+    // Query tile slowest and reversed: the longest tiles are dispatched first.
+    cur.q = static_cast<int>(gridDim.z) - 1 - static_cast<int>(blockIdx.z);
+    if (cur.q < 0 || cur.q >= qtiles) return;
+    cur.c = blockIdx.x;
+    cur.nt = prefill_item_tiles(cur.context, cur.len, cur.q);
+    cur.t = 0;
+    cur.u = 0;
+    u0 = 0;
+    u1 = cur.nt;
   }
+  auto advance = [&](Cursor& k) {
+    ++k.u;
+    if (++k.t < k.nt) return;
+    if (stream) {
+      seek(k, p, s_prefix, n, cols, k.u);
+    } else {
+      k.t = 0;  // grid items are never walked past their end
+    }
+  };
 
-  f32x16 o[HC][kDBlocks];
-  float m_run[HC], l_run[HC];
-#pragma unroll
-  for (int h = 0; h < HC; ++h) {
-#pragma unroll
-    for (int db = 0; db < kDBlocks; ++db) o[h][db] = f32x16{};
-    m_run[h] = -INFINITY;
-    l_run[h] = 0.0f;
-  }
-  const float score_scale = p.scale * kLog2e;
+  // c_eff = |scale| * log2(e), and the sign of a negative scale moved into Q (exact in
+  // 16-bit floats), so the max of raw scores is the max of scaled scores.
+  const float raw_c = p.scale * kLog2e;
+  const float score_c = fmaxf(fabsf(raw_c), 1e-30f);
+  const uint32_t q_sign = raw_c < 0.0f ? 0x80008000u : 0u;
 
   const char* kpool = static_cast<const char*>(p.k_pool);
   const char* vpool = static_cast<const char*>(p.v_pool);
+  const int64_t row_bytes = static_cast<int64_t>(p.hk) * D * kElemBytes;  // one token's K row
+  const int64_t page_bytes = row_bytes << p.block_shift;
 
-  // ---- staging. Each thread stages kKUnits 8-element K units and kVUnits (4 keys x 8
-  // dims) V units per tile. Their page ids (and fp8 scales) are fetched two tiles
-  // ahead, the K/V data one tile ahead, so neither latency sits on the tile loop.
-  auto k_key = [&](int u) { return (tid + u * kThreadsMax) / (D / 8); };
-  auto k_dim = [&](int u) { return ((tid + u * kThreadsMax) % (D / 8)) * 8; };
-  auto v_kq = [&](int u) { return (tid + u * kThreadsMax) % 16; };
-  auto v_dim = [&](int u) { return ((tid + u * kThreadsMax) / 16) * 8; };
-  auto v_live = [&](int u) { return tid + u * kThreadsMax < kVPairs; };
+  // ---- staging maps. K unit u: key (idx / (D/8)), dims 8 * (idx % (D/8)) .. +7, so 16
+  // lanes read one 16-byte-chunked key row. V unit u: keys kVKeys * (idx % kVGroups)
+  // .. + kVKeys - 1 at dims 8 * (idx / kVGroups) .. +7, transposed into V^T.
+  auto k_key = [&](int u) { return (tid + u * kThreads) / (D / 8); };
+  auto k_dim = [&](int u) { return ((tid + u * kThreads) % (D / 8)) * 8; };
+  auto v_grp = [&](int u) { return (tid + u * kThreads) % kVGroups; };
+  auto v_dim = [&](int u) { return ((tid + u * kThreads) / kVGroups) * 8; };
 
-  int kpg[kKUnits], vpg[kVUnits][4];
-  float ksc[kKUnits], vsc[kVUnits][4];
-  auto page_of = [&](int key) { return table[min(key, context - 1) >> p.block_shift]; };
-  auto fetch_pages = [&](int t) {
-    const int key0 = t * kTileKeys;
+  // Two register sets, by the parity of the step they serve (a compile-time index, so
+  // the sets stay in distinct registers): page ids are fetched four steps ahead and
+  // K/V two steps ahead, each consumed two loop iterations after it was issued.
+  int kpg[2][kKUnits], vpg[2][kVUnits][kVKeys];
+  float ksc[2][kKUnits], vsc[2][kVUnits][kVKeys];
+  auto fetch_pages = [&](const Cursor& k, auto set) {
+    constexpr int S = decltype(set)::value;
+    const int32_t* table = p.block_tables + static_cast<int64_t>(k.s) * p.max_blocks;
+    const int key0 = k.t * kTileKeys;
+    const int last = k.context - 1;
+    const int kvh = k.c / chunks;  // fp8 scales only
 #pragma unroll
-    for (int u = 0; u < kKUnits; ++u) kpg[u] = page_of(key0 + k_key(u));
+    for (int u = 0; u < kKUnits; ++u) kpg[S][u] = table[min(key0 + k_key(u), last) >> p.block_shift];
 #pragma unroll
     for (int u = 0; u < kVUnits; ++u) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) vpg[u][j] = v_live(u) ? page_of(key0 + 4 * v_kq(u) + j) : 0;
+      for (int j = 0; j < kVKeys; ++j) {
+        vpg[S][u][j] = table[min(key0 + kVKeys * v_grp(u) + j, last) >> p.block_shift];
+      }
     }
     if constexpr (kFp8) {
 #pragma unroll
-      for (int u = 0; u < kKUnits; ++u) ksc[u] = p.k_scales[static_cast<int64_t>(kpg[u]) * p.hk + kvh];
+      for (int u = 0; u < kKUnits; ++u) ksc[S][u] = p.k_scales[static_cast<int64_t>(kpg[S][u]) * p.hk + kvh];
 #pragma unroll
       for (int u = 0; u < kVUnits; ++u) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) vsc[u][j] = p.v_scales[static_cast<int64_t>(vpg[u][j]) * p.hk + kvh];
+        for (int j = 0; j < kVKeys; ++j) vsc[S][u][j] = p.v_scales[static_cast<int64_t>(vpg[S][u][j]) * p.hk + kvh];
       }
     }
-  };
-  auto addr = [&](int page, int key, int dim) -> int64_t {
-    const int k = min(key, context - 1);
-    const int64_t slot = (static_cast<int64_t>(page) << p.block_shift) | (k & p.block_mask);
-    return ((slot * p.hk + kvh) * D + dim) * kElemBytes;
   };
 
-  u32x4 kreg[kKUnits];
-  u32x4 vreg[kVUnits][4];
-  auto load_tile = [&](int t) {
-    const int key0 = t * kTileKeys;
+  u32x4 kreg[2][kKUnits];
+  u32x4 vreg[2][kVUnits][kVKeys];
+  // Byte offset of (page, key within the page, kv head, dims): the page's offset is one
+  // 32 x 32 -> 64-bit multiply-add, the rest fits 32 bits (a page is far below 4 GiB).
+  const uint32_t page_bytes32 = static_cast<uint32_t>(page_bytes);
+  auto pool_offset = [&](int page, int key, uint32_t inner) -> uint64_t {
+    return static_cast<uint64_t>(static_cast<uint32_t>(page)) * page_bytes32 +
+           (static_cast<uint32_t>(key & p.block_mask) * static_cast<uint32_t>(row_bytes) + inner);
+  };
+  auto load_tile = [&](const Cursor& k, auto set) {
+    constexpr int S = decltype(set)::value;
+    const int key0 = k.t * kTileKeys;
+    const int last = k.context - 1;
+    const uint32_t head_off = static_cast<uint32_t>((k.c / chunks) * D * kElemBytes);
 #pragma unroll
     for (int u = 0; u < kKUnits; ++u) {
-      kreg[u] = Stage<TQ, TKV>::load(kpool + addr(kpg[u], key0 + k_key(u), k_dim(u)),
-                                     kFp8 ? ksc[u] : 1.0f);
+      const int key = min(key0 + k_key(u), last);
+      const uint64_t off = pool_offset(kpg[S][u], key, head_off + k_dim(u) * kElemBytes);
+      kreg[S][u] = Stage<TQ, TKV>::load(kpool + off, kFp8 ? ksc[S][u] : 1.0f);
     }
 #pragma unroll
     for (int u = 0; u < kVUnits; ++u) {
-      if (!v_live(u)) continue;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        vreg[u][j] = Stage<TQ, TKV>::load(
-            vpool + addr(vpg[u][j], key0 + 4 * v_kq(u) + j, v_dim(u)), kFp8 ? vsc[u][j] : 1.0f);
+      for (int j = 0; j < kVKeys; ++j) {
+        const int key = min(key0 + kVKeys * v_grp(u) + j, last);
+        const uint64_t off = pool_offset(vpg[S][u][j], key, head_off + v_dim(u) * kElemBytes);
+        vreg[S][u][j] = Stage<TQ, TKV>::load(vpool + off, kFp8 ? vsc[S][u][j] : 1.0f);
       }
     }
   };
-  auto store_tile = [&](int buf) {
+  auto store_tile = [&](int buf, auto set) {
+    constexpr int S = decltype(set)::value;
 #pragma unroll
     for (int u = 0; u < kKUnits; ++u) {
-      *reinterpret_cast<u32x4*>(&k_lds[buf][k_key(u) * kKStride + k_dim(u)]) = kreg[u];
+      *reinterpret_cast<u32x4*>(&k_lds[buf][k_key(u) * kKStride + k_dim(u)]) = kreg[S][u];
     }
 #pragma unroll
     for (int u = 0; u < kVUnits; ++u) {
-      if (!v_live(u)) continue;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int sh = (e & 1) * 16;
-        const uint32_t a = (vreg[u][0][e >> 1] >> sh) & 0xffffu;
-        const uint32_t b = (vreg[u][1][e >> 1] >> sh) & 0xffffu;
-        const uint32_t c = (vreg[u][2][e >> 1] >> sh) & 0xffffu;
-        const uint32_t d = (vreg[u][3][e >> 1] >> sh) & 0xffffu;
-        *reinterpret_cast<u32x2*>(&v_lds[buf][(v_dim(u) + e) * kVStride + 4 * v_kq(u)]) =
-            u32x2{a | (b << 16), c | (d << 16)};
+        uint16_t* dst = &v_lds[buf][(v_dim(u) + e) * kVStride + kVKeys * v_grp(u)];
+        // v_perm_b32 selector: low halves (bytes 0,1 of each) or high halves (2,3) of
+        // two dwords, the first operand's in the upper half of the result.
+        const uint32_t sel = sh == 0 ? 0x05040100u : 0x07060302u;
+        if constexpr (kVKeys == 4) {
+          *reinterpret_cast<u32x2*>(dst) =
+              u32x2{__builtin_amdgcn_perm(vreg[S][u][1][e >> 1], vreg[S][u][0][e >> 1], sel),
+                    __builtin_amdgcn_perm(vreg[S][u][3][e >> 1], vreg[S][u][2][e >> 1], sel)};
+        } else if constexpr (kVKeys == 2) {
+          *reinterpret_cast<uint32_t*>(dst) =
+              __builtin_amdgcn_perm(vreg[S][u][1][e >> 1], vreg[S][u][0][e >> 1], sel);
+        } else {
+          *dst = static_cast<uint16_t>(vreg[S][u][0][e >> 1] >> sh);
+        }
       }
     }
   };
 
-  if (ntiles > 0) {
-    fetch_pages(0);
-    load_tile(0);
-    if (ntiles > 1) fetch_pages(1);
-  }
+  // ---- per-item state of this wave.
+  u32x4 qop[HCW][kKSteps];
+  f32x16 o[HCW][kDBlocks];
+  float m_run[HCW], l_run[HCW];
+  int w_first = 0, w_kv_end = 0, w_kv_full = 0, my_local = 0, my_visible = 0, head0 = 0;
+  int row_base = 0, piece_t0 = 0, piece_u0 = 0;
+  bool w_active = false, my_valid = false;
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    store_tile(buf);
-    __syncthreads();
-    if (t + 1 < ntiles) {
-      load_tile(t + 1);
-      if (t + 2 < ntiles) fetch_pages(t + 2);
+  auto begin_piece = [&]() {
+    const int offset = cur.context - cur.len;
+    const int qb = cur.q * kPrefillQueryTile;
+    w_first = qb + 32 * wq;
+    w_active = w_first < cur.len;
+    w_kv_end = offset + min(w_first + 32, cur.len);
+    w_kv_full = offset + w_first + 1;
+    my_local = w_first + l32;
+    my_valid = my_local < cur.len;
+    my_visible = offset + my_local + 1;
+    row_base = sload(p.cu_seqlens_q + cur.s);
+    head0 = (cur.c / chunks) * group + (cur.c % chunks) * HW + hs * HCW;
+    piece_t0 = cur.t;
+    piece_u0 = cur.u;
+    const int local = min(my_local, cur.len - 1);
+#pragma unroll
+    for (int h = 0; h < HCW; ++h) {
+      const int64_t qrow = static_cast<int64_t>(row_base + local) * p.hq + head0 + h;
+      const char* qp = static_cast<const char*>(p.q) + (qrow * D + 8 * hsel) * 2;
+#pragma unroll
+      for (int ks = 0; ks < kKSteps; ++ks) qop[h][ks] = load16(qp + ks * 32) ^ q_sign;
+#pragma unroll
+      for (int db = 0; db < kDBlocks; ++db) o[h][db] = f32x16{};
+      m_run[h] = -INFINITY;
+      l_run[h] = 0.0f;
     }
+  };
 
-    const int key0 = t * kTileKeys;
-    if (!w_active || key0 >= w_kv_end) continue;
-
+  auto compute = [&](int buf) {
+    const int key0 = cur.t * kTileKeys;
+    if (!w_active || key0 >= w_kv_end) return;
     const uint16_t* kt = k_lds[buf];
     const uint16_t* vt = v_lds[buf];
 
     // S^T = K Q^T for two 32-key blocks; one K fragment feeds every head's MFMA.
-    f32x16 s[HC][2];
+    f32x16 s[HCW][2];
 #pragma unroll
-    for (int h = 0; h < HC; ++h) {
+    for (int h = 0; h < HCW; ++h) {
       s[h][0] = f32x16{};
       s[h][1] = f32x16{};
     }
@@ -283,34 +424,47 @@ __global__ __launch_bounds__(kThreadsMax) void paged_prefill_kernel(const PagedP
       for (int kb = 0; kb < 2; ++kb) {
         const u32x4 a = *reinterpret_cast<const u32x4*>(kt + (kb * 32 + l32) * kKStride + 8 * hsel + ks * 16);
 #pragma unroll
-        for (int h = 0; h < HC; ++h) s[h][kb] = Mma<TQ>::run(a, qop[h][ks], s[h][kb]);
+        for (int h = 0; h < HCW; ++h) s[h][kb] = Mma<TQ>::run(a, qop[h][ks], s[h][kb]);
       }
     }
 
-    // Online softmax per head; P^T operands straight from the score registers.
-    const bool need_mask = key0 + kTileKeys > w_kv_full;
-    u32x4 pop[HC][4];
+    // Causal mask, on tiles crossing the diagonal only: score (kb, r) of this lane is
+    // key key0 + 4*hsel + (32kb + 8(r/4) + r%4); visible while below my_visible.
+    if (key0 + kTileKeys > w_kv_full) {
+      asm volatile("" ::: "memory");  // keep this a branch: most tiles need no mask
+      const int lim = my_valid ? my_visible - key0 - 4 * hsel : INT_MIN;
 #pragma unroll
-    for (int h = 0; h < HC; ++h) {
+      for (int h = 0; h < HCW; ++h) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            if (kb * 32 + 8 * (r >> 2) + (r & 3) >= lim) s[h][kb][r] = -INFINITY;
+          }
+        }
+      }
+    }
+
+    // Online softmax per head on raw scores; P^T operands straight from the registers.
+    u32x4 pop[HCW][4];
+#pragma unroll
+    for (int h = 0; h < HCW; ++h) {
       float tmax = -INFINITY;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float v = s[h][kb][r] * score_scale;
-          if (need_mask) {
-            const int key = key0 + kb * 32 + 8 * (r >> 2) + 4 * hsel + (r & 3);
-            v = (key < my_visible && my_valid) ? v : -INFINITY;
-          }
-          s[h][kb][r] = v;
-          tmax = fmaxf(tmax, v);
-        }
+        for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[h][kb][r]);
       }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
-      const float m_new = fmaxf(m_run[h], tmax);
-      const float mu = m_new == -INFINITY ? 0.0f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run[h] - mu);
-      m_run[h] = m_new;
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave)) * score_c;
+      if (__builtin_amdgcn_ballot_w64(tmax > m_run[h] + kRescaleSlack) != 0) {
+        const float m_new = fmaxf(m_run[h], tmax);
+        const float alpha = m_new == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run[h] - m_new);
+        m_run[h] = m_new;
+        l_run[h] *= alpha;
+#pragma unroll
+        for (int db = 0; db < kDBlocks; ++db) o[h][db] *= alpha;
+      }
+      const float neg_mu = m_run[h] == -INFINITY ? 0.0f : -m_run[h];
       float psum = 0.0f;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
@@ -319,7 +473,7 @@ __global__ __launch_bounds__(kThreadsMax) void paged_prefill_kernel(const PagedP
           float pv[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            pv[e] = __builtin_amdgcn_exp2f(s[h][kb][8 * half + e] - mu);
+            pv[e] = __builtin_amdgcn_exp2f(fmaf(s[h][kb][8 * half + e], score_c, neg_mu));
             psum += pv[e];
           }
           pop[h][2 * kb + half] =
@@ -327,9 +481,7 @@ __global__ __launch_bounds__(kThreadsMax) void paged_prefill_kernel(const PagedP
                     Mma<TQ>::pack2(pv[4], pv[5]), Mma<TQ>::pack2(pv[6], pv[7])};
         }
       }
-      l_run[h] = l_run[h] * alpha + psum;
-#pragma unroll
-      for (int db = 0; db < kDBlocks; ++db) o[h][db] *= alpha;
+      l_run[h] += psum;
     }
 
     // O^T += V^T P^T. For k-step ks = 2*kb + half, this lane's eight k-values are
@@ -344,28 +496,211 @@ __global__ __launch_bounds__(kThreadsMax) void paged_prefill_kernel(const PagedP
         const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 16 * ks + 8);
         const u32x4 a = u32x4{lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
-        for (int h = 0; h < HC; ++h) o[h][db] = Mma<TQ>::run(a, pop[h][ks], o[h][db]);
+        for (int h = 0; h < HCW; ++h) o[h][db] = Mma<TQ>::run(a, pop[h][ks], o[h][db]);
       }
     }
-  }
+  };
 
-  if (!w_active || !my_valid) return;
+  auto end_piece = [&]() {
+    if (!w_active || !my_valid) return;
+    const bool whole = piece_t0 == 0 && cur.t == cur.nt - 1;
+    const int64_t slot = 2 * static_cast<int64_t>(share) + (piece_u0 == u0 ? 0 : 1);
 #pragma unroll
-  for (int h = 0; h < HC; ++h) {
-    const float l_tot = l_run[h] + __shfl_xor(l_run[h], 32, kWave);
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    const int64_t orow = (static_cast<int64_t>(row_base + my_local) * p.hq + head0 + h) * D;
+    for (int h = 0; h < HCW; ++h) {
+      const float l_tot = l_run[h] + __shfl_xor(l_run[h], 32, kWave);
+      if (whole) {
+        const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        const int64_t orow = (static_cast<int64_t>(row_base + my_local) * p.hq + head0 + h) * D;
 #pragma unroll
-    for (int db = 0; db < kDBlocks; ++db) {
+        for (int db = 0; db < kDBlocks; ++db) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d = db * 32 + 8 * j + 4 * hsel;
-        float r[4];
+          for (int j = 0; j < 4; ++j) {
+            const int d = db * 32 + 8 * j + 4 * hsel;
+            float r[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) r[i] = o[h][db][4 * j + i] * inv;
-        *reinterpret_cast<u32x2*>(static_cast<char*>(p.out) + (orow + d) * 2) =
-            u32x2{Mma<TQ>::pack2(r[0], r[1]), Mma<TQ>::pack2(r[2], r[3])};
+            for (int i = 0; i < 4; ++i) r[i] = o[h][db][4 * j + i] * inv;
+            *reinterpret_cast<u32x2*>(static_cast<char*>(p.out) + (orow + d) * 2) =
+                u32x2{Mma<TQ>::pack2(r[0], r[1]), Mma<TQ>::pack2(r[2], r[3])};
+          }
+        }
+      } else {
+        // A piece's output normalised by its own sum, in fp32 (a 16-bit partial would
+        // round the result twice), plus its (max, sum) for the merge's weights.
+        const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+        const int64_t prow = (slot * HW + hs * HCW + h) * kPrefillQueryTile +
+                             (my_local - cur.q * kPrefillQueryTile);
+        float* po = p.pf_o + prow * D;
+#pragma unroll
+        for (int db = 0; db < kDBlocks; ++db) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int d = db * 32 + 8 * j + 4 * hsel;
+            *reinterpret_cast<f32x4*>(po + d) =
+                f32x4{o[h][db][4 * j] * inv, o[h][db][4 * j + 1] * inv,
+                      o[h][db][4 * j + 2] * inv, o[h][db][4 * j + 3] * inv};
+          }
+        }
+        if (hsel == 0) {
+          *reinterpret_cast<float2*>(p.pf_ml + prow * 2) = make_float2(m_run[h], l_tot);
+        }
       }
+    }
+  };
+
+  // ---- the tile loop over [u0, u1). Step x's page ids and K/V live in register set
+  // (x - u0) & 1; cursor `lc` is at the last step loaded, `fc` at the last fetched.
+  // sched_barrier keeps the scheduler from sinking the prefetches below the
+  // computation that is meant to hide their latency.
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  Cursor lc = cur;
+  fetch_pages(lc, I0{});
+  load_tile(lc, I0{});
+  if (u0 + 1 < u1) {
+    advance(lc);
+    fetch_pages(lc, I1{});
+    load_tile(lc, I1{});
+  }
+  Cursor fc = lc;
+  if (u0 + 2 < u1) {
+    advance(fc);
+    fetch_pages(fc, I0{});
+  }
+  if (u0 + 3 < u1) {
+    advance(fc);
+    fetch_pages(fc, I1{});
+  }
+  auto step_body = [&](int step, auto set) {
+    if (step == u0 || cur.t == 0) begin_piece();
+    store_tile(decltype(set)::value, set);
+    __syncthreads();
+    if (step + 2 < u1) {
+      advance(lc);
+      load_tile(lc, set);
+    }
+    if (step + 4 < u1) {
+      advance(fc);
+      fetch_pages(fc, set);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    compute(decltype(set)::value);
+    if (step + 1 == u1 || cur.t + 1 == cur.nt) end_piece();
+    if (step + 1 < u1) advance(cur);
+  };
+  for (int step = u0; step < u1; step += 2) {
+    step_body(step, I0{});
+    if (step + 1 < u1) step_body(step + 1, I1{});
+  }
+}
+
+// Combine the pieces of every prefill item cut between stream workgroups. Workgroup b
+// looks at the start of share b; if that falls inside an item and is the item's first
+// such boundary, it merges the item. The item's piece slots are listed once in LDS;
+// each of 1024 threads then owns kElems float4 columns of output rows and combines
+// the pieces kPieces at a time, with every load of a batch issued together (the
+// partials come from L2 / MALL, so latency, not bandwidth, sets this kernel's time).
+template <typename TQ, int D, int HW>
+__global__ __launch_bounds__(1024) void paged_prefill_merge_kernel(const PagedParams p) {
+  constexpr int kElems = 4;
+  constexpr int kPieces = 4;
+  __shared__ int s_slots[kMaxPrefillWgs];
+  __shared__ int s_pieces;
+  // Boundary b is the start of share b, merged on the XCD that computed share b.
+  const int b = xcd_share(blockIdx.x, gridDim.x);
+  if (b == 0) return;
+  const int64_t wgs = p.pf_wgs;
+  const int n = p.num_seqs;
+  const int total = sload(p.pf_prefix + n);
+  const int64_t x = share_begin(b, total, wgs);
+  if (x >= total) return;
+  const int group = p.hq / p.hk;
+  const int chunks = group / HW;
+  const int cols = p.hk * chunks;
+  Cursor k;
+  seek(k, p, p.pf_prefix, n, cols, static_cast<int>(x));
+  if (k.t == 0) return;  // the share starts an item: nothing is cut here
+  const int64_t start = x - k.t;
+  const int64_t end = start + k.nt;
+  if (share_begin(b - 1, total, wgs) > start) return;  // an earlier boundary merges it
+  if (threadIdx.x == 0) {
+    // Shares overlapping [start, end): the first holds the item as its last piece
+    // (slot 2w + 1) unless its share starts exactly there; later ones as their first
+    // (slot 2w). Empty shares hold nothing.
+    const int64_t first = share_owner(start, total, wgs);
+    int np = 0;
+    for (int64_t g = first; g < wgs; ++g) {
+      const int64_t gs = share_begin(g, total, wgs);
+      if (gs >= end) break;
+      if (gs == share_begin(g + 1, total, wgs)) continue;
+      s_slots[np++] = static_cast<int>(2 * g + (g == first && gs < start ? 1 : 0));
+    }
+    s_pieces = np;
+  }
+  __syncthreads();
+  const int pieces = s_pieces;
+  const int qb = k.q * kPrefillQueryTile;
+  const int rows = min(kPrefillQueryTile, k.len - qb);
+  const int head0 = (k.c / chunks) * group + (k.c % chunks) * HW;
+  const int row0 = sload(p.cu_seqlens_q + k.s) + qb;
+  constexpr int kD4 = D / 4;
+  const int n4 = HW * rows * kD4;
+  const int nthreads = static_cast<int>(blockDim.x);
+  for (int j0 = threadIdx.x; j0 < n4; j0 += kElems * nthreads) {
+    int64_t prow[kElems];
+    int dcol[kElems];
+    float m[kElems], l[kElems];
+    f32x4 acc[kElems];
+#pragma unroll
+    for (int e = 0; e < kElems; ++e) {
+      const int j = min(j0 + e * nthreads, n4 - 1);
+      const int hw = j / (rows * kD4);
+      const int rem = j - hw * rows * kD4;
+      const int row = rem / kD4;
+      dcol[e] = (rem - row * kD4) * 4;
+      prow[e] = static_cast<int64_t>(hw) * kPrefillQueryTile + row;
+      m[e] = -INFINITY;
+      l[e] = 0.0f;
+      acc[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    for (int i0 = 0; i0 < pieces; i0 += kPieces) {
+      float2 ml[kPieces][kElems];
+      f32x4 oi[kPieces][kElems];
+#pragma unroll
+      for (int i = 0; i < kPieces; ++i) {
+        const int64_t base =
+            static_cast<int64_t>(s_slots[min(i0 + i, pieces - 1)]) * HW * kPrefillQueryTile;
+#pragma unroll
+        for (int e = 0; e < kElems; ++e) {
+          ml[i][e] = *reinterpret_cast<const float2*>(p.pf_ml + (base + prow[e]) * 2);
+          oi[i][e] = *reinterpret_cast<const f32x4*>(p.pf_o + (base + prow[e]) * D + dcol[e]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kPieces; ++i) {
+        if (i0 + i >= pieces) break;
+#pragma unroll
+        for (int e = 0; e < kElems; ++e) {
+          // Piece rows are normalised: weight them by l_i * 2^(m_i - max).
+          const float mn = fmaxf(m[e], ml[i][e].x);
+          const float mu = mn == -INFINITY ? 0.0f : mn;
+          const float a = __builtin_amdgcn_exp2f(m[e] - mu);
+          const float c = ml[i][e].y * __builtin_amdgcn_exp2f(ml[i][e].x - mu);
+          l[e] = l[e] * a + c;
+          acc[e] = acc[e] * a + oi[i][e] * c;
+          m[e] = mn;
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < kElems; ++e) {
+      if (j0 + e * nthreads >= n4) continue;
+      const int hw = static_cast<int>(prow[e] / kPrefillQueryTile);
+      const int row = static_cast<int>(prow[e] - static_cast<int64_t>(hw) * kPrefillQueryTile);
+      const float inv = l[e] > 0.0f ? 1.0f / l[e] : 0.0f;
+      const int64_t obase = (static_cast<int64_t>(row0 + row) * p.hq + head0 + hw) * D + dcol[e];
+      *reinterpret_cast<u32x2*>(static_cast<char*>(p.out) + obase * 2) =
+          u32x2{Mma<TQ>::pack2(acc[e][0] * inv, acc[e][1] * inv),
+                Mma<TQ>::pack2(acc[e][2] * inv, acc[e][3] * inv)};
     }
   }
 }
@@ -374,19 +709,29 @@ __global__ __launch_bounds__(kThreadsMax) void paged_prefill_kernel(const PagedP
 
 namespace {
 
+template <typename TQ, typename TKV, int D, int HCW, int HS>
+void launch_prefill_cfg(const PagedParams& p, int max_query_len, hipStream_t stream) {
+  constexpr int HW = HCW * HS;
+  if (p.pf_wgs > 0) {
+    paged_prefill_kernel<TQ, TKV, D, HCW, HS><<<p.pf_wgs, 256 * HS, 0, stream>>>(p);
+    paged_prefill_merge_kernel<TQ, D, HW><<<p.pf_wgs, 1024, 0, stream>>>(p);
+  } else {
+    const int cols = p.hk * (p.hq / p.hk / HW);
+    const int qtiles = (max_query_len + kPrefillQueryTile - 1) / kPrefillQueryTile;
+    const dim3 grid(cols, p.num_seqs, qtiles);
+    paged_prefill_kernel<TQ, TKV, D, HCW, HS><<<grid, 256 * HS, 0, stream>>>(p);
+  }
+}
+
 template <typename TQ, typename TKV, int D>
 hipError_t launch_prefill_d(const PagedParams& p, int max_query_len, hipStream_t stream) {
-  const int group = p.hq / p.hk;
-  constexpr int kPositions = 32 * (kThreadsMax / kWave);
-  const int qtiles = (max_query_len + kPositions - 1) / kPositions;
-  // Two heads per wave fit the register file up to D = 128 (D = 256 would spill); at
-  // config 3 they measured 144 us against 157 us with one head per wave.
-  if (group % 2 == 0 && D <= 128) {
-    const dim3 grid(p.hk * (group / 2), p.num_seqs, qtiles);
-    paged_prefill_kernel<TQ, TKV, D, 2><<<grid, kThreadsMax, 0, stream>>>(p);
+  // Both heads of an even GQA group in one wave (HCW = 2) would share K/V fragments,
+  // but needs ~450 registers: one wave per SIMD and no softmax/MFMA overlap. Measured
+  // at config 3 it ran 25-40% slower than a wave per head, two waves per SIMD.
+  if (prefill_item_heads(p.hq / p.hk) == 1) {
+    launch_prefill_cfg<TQ, TKV, D, 1, 1>(p, max_query_len, stream);
   } else {
-    const dim3 grid(p.hk * group, p.num_seqs, qtiles);
-    paged_prefill_kernel<TQ, TKV, D, 1><<<grid, kThreadsMax, 0, stream>>>(p);
+    launch_prefill_cfg<TQ, TKV, D, 1, 2>(p, max_query_len, stream);
   }
   return hipGetLastError();
 }

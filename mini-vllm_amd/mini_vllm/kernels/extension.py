@@ -59,7 +59,7 @@ HIP_FLAGS = [
 # reference's PyTorch expressions round, so FMA contraction is off there.
 EXTRA_FLAGS = {"elementwise.hip": ["-ffp-contract=off"]}
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_CODES: dict[torch.dtype, int] = {
     torch.float32: 0,
@@ -136,6 +136,8 @@ class _Plan(ctypes.Structure):
         ("split_tokens", ctypes.c_int32),
         ("prefill_mfma", ctypes.c_int32),
         ("workspace_bytes", ctypes.c_uint64),
+        ("prefill_workgroups", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 

@@ -76,6 +76,18 @@ def _plan(lib, *args):
     return plan
 
 
+def test_prefill_grid_schedule_needs_no_workspace(lib, monkeypatch):
+    # enough 128-query items to fill the CUs: the grid schedule
+    plan = _plan(lib, 4096, 8, 16, 8, 128, 16, 512, 2048, 2, 2)
+    assert plan.prefill_mfma == 1 and plan.prefill_workgroups == 0 and plan.workspace_bytes == 0
+    monkeypatch.setenv("MVLLM_PREFILL_SCHEDULE", "2")
+    plan = _plan(lib, 512, 1, 16, 8, 128, 16, 512, 8192, 2, 2)
+    assert plan.prefill_workgroups == 0 and plan.workspace_bytes == 0
+    monkeypatch.setenv("MVLLM_PREFILL_SCHEDULE", "1")
+    plan = _plan(lib, 4096, 8, 16, 8, 128, 16, 512, 2048, 2, 2)
+    assert plan.prefill_workgroups > 0
+
+
 def test_plan_is_host_only_and_consistent(lib):
     # pure decode: the stream schedule, partial slots for (workgroups + sequences) x H_q
     plan = _plan(lib, 64, 64, 16, 8, 128, 16, 1, 4096, 2, 2)
@@ -83,12 +95,18 @@ def test_plan_is_host_only_and_consistent(lib):
     assert 1 <= plan.decode_workgroups
     entries = (plan.decode_workgroups + 64) * 16
     assert plan.workspace_bytes >= entries * (128 + 2) * 4 + 65 * 4
-    # pure prefill chunks in bf16: no decode launch, MFMA prefill
-    plan = _plan(lib, 4096, 8, 16, 8, 128, 16, 512, 2048, 2, 2)
-    assert plan.decode_mode == 0 and plan.prefill_mfma == 1 and plan.workspace_bytes == 0
-    # mixed bf16 batch: stream decode + MFMA prefill
+    # one prefill chunk in bf16 (fewer 128-query items than CUs): no decode launch,
+    # MFMA prefill on the stream schedule, whose partial slots (two per workgroup,
+    # 2 heads x 128 rows each) and per-sequence prefix make up the workspace
+    plan = _plan(lib, 512, 1, 16, 8, 128, 16, 512, 8192, 2, 2)
+    assert plan.decode_mode == 0 and plan.prefill_mfma == 1 and plan.prefill_workgroups >= 1
+    rows = 2 * plan.prefill_workgroups * 2 * 128
+    assert plan.workspace_bytes >= rows * (128 + 2) * 4 + 2 * 4
+    # mixed bf16 batch: stream decode + MFMA prefill, both workspaces
     plan = _plan(lib, 101, 2, 16, 8, 128, 16, 100, 2048, 2, 2)
-    assert plan.decode_mode == 1 and plan.prefill_mfma == 1
+    assert plan.decode_mode == 1 and plan.prefill_mfma == 1 and plan.prefill_workgroups >= 1
+    decode_part = (plan.decode_workgroups + 2) * 16 * (128 + 2) * 4
+    assert plan.workspace_bytes >= decode_part + 2 * plan.prefill_workgroups * 2 * 128 * 130 * 4
     # fp32 prefill has no MFMA kernel: the decode kernel serves every row
     plan = _plan(lib, 100, 4, 16, 8, 128, 16, 40, 2048, 0, 0)
     assert plan.decode_mode == 3 and plan.prefill_mfma == 0

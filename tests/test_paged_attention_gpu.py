@@ -146,6 +146,67 @@ def test_mfma_prefill_shapes(extension, device, head_dim, heads, kv_heads):
     check(extension, b)
 
 
+def _prefill_schedule(monkeypatch, schedule):
+    monkeypatch.setenv("MVLLM_PREFILL_SCHEDULE", "1" if schedule == "stream" else "2")
+
+
+@pytest.mark.parametrize("schedule", ["stream", "grid"])
+@pytest.mark.parametrize("heads,kv_heads", [(16, 8), (6, 2), (3, 3)])
+def test_prefill_schedules_on_a_ragged_batch(extension, device, monkeypatch, schedule, heads,
+                                             kv_heads):
+    """Balanced stream shares cut long items between workgroups (merged afterwards);
+    the grid runs every item whole. Prefixes from 0 to several thousand keys; GQA
+    pairs (two heads per work item, a wave each) and odd groups (one head)."""
+    _prefill_schedule(monkeypatch, schedule)
+    b = case([4000, 520, 17, 1300, 64], [512, 520, 9, 300, 2], device, dtype=torch.bfloat16,
+             num_q_heads=heads, num_kv_heads=kv_heads, head_dim=128)
+    plan = extension.paged_attention_plan(b.q.shape[0], 5, heads, kv_heads, 128, 16, 520, 4000,
+                                          torch.bfloat16, torch.bfloat16)
+    assert plan["prefill_mfma"] == 1
+    assert (plan["prefill_workgroups"] > 0) == (schedule == "stream")
+    check(extension, b)
+
+
+@pytest.mark.parametrize("wgs_per_cu", ["1", "3"])
+def test_prefill_stream_with_more_workgroups_than_tiles(extension, device, monkeypatch, wgs_per_cu):
+    """A two-tile prefill over hundreds of workgroups: most shares are empty, and each
+    tile of an item may sit in a different workgroup."""
+    monkeypatch.setenv("MVLLM_PREFILL_WGS_PER_CU", wgs_per_cu)
+    monkeypatch.setenv("MVLLM_PREFILL_SCHEDULE", "1")
+    b = case([70, 3], [70, 3], device, dtype=torch.bfloat16, num_q_heads=4, num_kv_heads=2,
+             head_dim=64)
+    check(extension, b)
+
+
+@pytest.mark.parametrize("schedule", ["stream", "grid"])
+def test_prefill_schedules_in_a_mixed_fp8_batch(extension, device, monkeypatch, schedule):
+    _prefill_schedule(monkeypatch, schedule)
+    b = case([900, 2500, 40, 700], [1, 400, 40, 1], device, dtype=torch.bfloat16,
+             kv_dtype=torch.float8_e4m3fn, num_q_heads=16, num_kv_heads=8, head_dim=128)
+    check(extension, b, dtype=torch.float8_e4m3fn)
+
+
+@pytest.mark.parametrize("schedule", ["stream", "grid"])
+@pytest.mark.parametrize("scale", [-0.3, 0.0, 2.0])
+def test_prefill_with_unusual_scales(extension, device, monkeypatch, scale, schedule):
+    """The softmax runs on raw scores with |scale| folded into the exponent and the sign
+    of a negative scale moved into Q; zero gives uniform weights."""
+    _prefill_schedule(monkeypatch, schedule)
+    b = case([300, 90], [150, 90], device, dtype=torch.bfloat16, num_q_heads=16,
+             num_kv_heads=8, head_dim=128)
+    b.scale = scale
+    check(extension, b)
+
+
+def test_prefill_schedule_choice(extension):
+    """Grid when the items fill the CUs; stream for a chunk of a long prompt."""
+    bf = torch.bfloat16
+    many = extension.paged_attention_plan(4096, 8, 16, 8, 128, 16, 512, 2048, bf, bf)
+    assert many["prefill_mfma"] == 1 and many["prefill_workgroups"] == 0
+    chunk = extension.paged_attention_plan(543, 32, 16, 8, 128, 16, 512, 8192, bf, bf)
+    assert chunk["prefill_mfma"] == 1 and chunk["prefill_workgroups"] > 0
+
+
 @pytest.mark.parametrize("block_size", [1, 2, 64])
 def test_mfma_prefill_block_sizes(extension, device, block_size):
     check(extension, case([180, 70], [100, 70], device, dtype=torch.bfloat16,
