@@ -109,7 +109,7 @@ def run_paged(batches, steps, warmup):
 
 
 def run_engine(requests: int = 256, max_tokens: int = 256, max_sequences: int = 32,
-               use_graphs: bool = True) -> dict:
+               use_graphs: bool = True, kv_dtype: torch.dtype | None = None) -> dict:
     """a Qwen3-0.6B-shaped model (random init, std 0.02, bf16) served
     by the paged engine with the HIP kernels: `requests` prompts of U[64, 2048] random
     token ids (seed 0), `max_tokens` greedy tokens each (EOS ignored), continuous
@@ -128,7 +128,7 @@ def run_engine(requests: int = 256, max_tokens: int = 256, max_sequences: int = 
 
     def engine():
         manager = BlockManager(blocks, 16, config.num_hidden_layers, config.num_key_value_heads,
-                               config.head_dim, config.dtype, "cuda")
+                               config.head_dim, kv_dtype or config.dtype, "cuda")
         return LLMEngine(Qwen3Paged(config, weights, manager, use_cuda=True), sched, device="cuda",
                          use_graphs=use_graphs)
 
@@ -147,7 +147,42 @@ def run_engine(requests: int = 256, max_tokens: int = 256, max_sequences: int = 
         "decode_tok_s": round(st.decode_tokens_per_s, 1),
         "decode_only_iterations": st.decode_only_iterations,
         "decode_graphs": use_graphs,
+        "kv_dtype": str(kv_dtype or config.dtype).replace("torch.", ""),
     }
+
+
+def run_kv_write(steps: int = 20) -> dict:
+    """The paged KV write (one layer, 8 kv heads x 128, 16-token pages): 2048 tokens (one
+    engine iteration's budget) and 65536 tokens (bandwidth), into shuffled slots of a
+    pool with 10% spare pages. Bytes = K and V read from the token rows + written to the
+    pool (bf16), or read (bf16) + written (fp8) + scales."""
+    from mini_vllm.kernels import ops
+
+    out = {}
+    hk, d, bs = 8, 128, 16
+    for tokens in (2048, 65536):
+        pages = -(-tokens // bs)
+        nb = int(pages * 1.1) + 1
+        gen = torch.Generator().manual_seed(tokens)
+        perm = torch.randperm(nb, generator=gen)[:pages]
+        slots = (perm[:, None] * bs + torch.arange(bs)).reshape(-1)[:tokens].to(torch.int32).cuda()
+        key = torch.randn(tokens, hk, d, device="cuda", dtype=torch.bfloat16)
+        value = torch.randn(tokens, hk, d, device="cuda", dtype=torch.bfloat16)
+        for kv in (torch.bfloat16, torch.float8_e4m3fn):
+            kp = torch.zeros(nb, bs, hk, d, device="cuda", dtype=kv)
+            vp = torch.zeros_like(kp)
+            sc = {}
+            if kv == torch.float8_e4m3fn:
+                sc = dict(k_scale=torch.zeros(nb, hk, device="cuda"),
+                          v_scale=torch.zeros(nb, hk, device="cuda"))
+            ms = time_steps(lambda i: ops.kv_write(kp, vp, key, value, slots, use_cuda=True, **sc),
+                            steps, 3)
+            elt = kp.element_size()
+            nbytes = 2 * tokens * hk * d * (2 + elt) + (2 * pages * hk * 4 * 2 if sc else 0)
+            name = f"T{tokens}_{'fp8' if sc else 'bf16'}"
+            out[name] = {"us": round(ms * 1e3, 1), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+            log(f"kv_write {name}: {ms * 1e3:.1f} us, {out[name]['gbs']:.0f} GB/s")
+    return out
 
 
 def run_elementwise(steps: int = 20) -> dict:
@@ -242,9 +277,10 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--copies", type=int, default=3, help="rotated pool copies (defeat the MALL)")
     parser.add_argument("--skip-extras", action="store_true", help="headline config 2 only")
-    parser.add_argument("--extras", default="3,4,5,ew,copy",
+    parser.add_argument("--extras", default="3,4,5,ew,kv,copy",
                         help="comma list of extras to run: 3 (prefill), 4 (fp8 decode), "
-                             "5 (engine), ew (elementwise kernels), copy")
+                             "5 (engine), 5fp8 (engine, fp8 KV cache), ew (elementwise "
+                             "kernels), kv (KV write), copy")
     parser.add_argument("--no-cpu", action="store_true")
     args = parser.parse_args()
 
@@ -304,10 +340,15 @@ def main() -> int:
         torch.cuda.empty_cache()
     if "ew" in wanted:
         extras["elementwise"] = run_elementwise()
+    if "kv" in wanted:
+        extras["kv_write"] = run_kv_write()
     if "5" in wanted:
         log("config 5: Qwen3-0.6B-shaped engine, 256 requests x 256 tokens")
         extras["config5_engine"] = run_engine()
         log(f"config 5 (decode graphs on): {extras['config5_engine']}")
+    if "5fp8" in wanted:
+        extras["config5_engine_fp8kv"] = run_engine(kv_dtype=torch.float8_e4m3fn)
+        log(f"config 5 with an fp8 KV cache: {extras['config5_engine_fp8kv']}")
         torch.cuda.empty_cache()
     if "copy" in wanted:
         extras["copy_ceiling_gbs"] = round(copy_ceiling(1 << 30), 1)

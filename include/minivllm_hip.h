@@ -130,6 +130,32 @@ int mvllm_rope(void* out, const void* x, const void* positions, int32_t position
 int mvllm_swiglu(void* out, const void* gate, const void* up, int64_t n, int32_t dtype,
                  void* stream);
 
+/* Scatter one iteration's keys and values into their pool slots, K and V in one
+ * launch. Replaces the two index_copy_ calls of PagedKvPool.write
+ * (mini_vllm/block/kv_pool.py:116-155; slot_mapping from mini_vllm/serve/batch.py:158-166).
+ *   key_pool,
+ *   value_pool   [num_blocks, block_size, num_kv_heads, head_dim] pool_dtype
+ *   k_scales,
+ *   v_scales     [num_blocks, num_kv_heads] float32, read and updated; required iff
+ *                pool_dtype is fp8, else NULL
+ *   key, value   [num_tokens, num_kv_heads, head_dim] src_dtype (f32, f16, bf16)
+ *   slot_mapping [num_tokens] int32 flat slot (block * block_size + offset); a negative
+ *                slot skips its token
+ * pool_dtype == src_dtype copies. An fp8 pool (head_dim 32, 64, 128 or 256; no
+ * counterpart in the reference) is quantised per (block, kv head): a call's tokens on
+ * consecutive rows of one block form
+ * a run (a block must get at most one run per call); a run starting at row 0 opens the
+ * block; scale s = max(old scale, least power of two >= max|x| / 448) over the run;
+ * rows already in the block are re-encoded as e4m3((code * old) / s) when s grew (an
+ * exponent shift: exact unless a value falls into e4m3's subnormals); new rows are
+ * e4m3(x / s), round to nearest even, 0 when s is 0. Slot values are not range-checked
+ * (the reference's write does not read them back either); shapes are. */
+int mvllm_kv_write(void* key_pool, void* value_pool, float* k_scales, float* v_scales,
+                   const void* key, const void* value, const int32_t* slot_mapping,
+                   int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+                   int32_t block_size, int64_t num_blocks, int32_t src_dtype,
+                   int32_t pool_dtype, void* stream);
+
 /* y = a * x + b over n floats: the toolchain smoke test, replacing `mini_vllm_C.hello`
  * (csrc/bindings.cpp:8,37-42 -> csrc/hello.cu:11-21; mini_vllm/kernels/extension.py:349-353). */
 int mvllm_axpby(float* y, const float* x, float a, float b, int64_t n, void* stream);

@@ -15,6 +15,7 @@
 #include "../../include/minivllm_hip.h"
 #include "common.hpp"
 #include "elementwise.hpp"
+#include "kv_write.hpp"
 #include "paged_attention.hpp"
 
 namespace {
@@ -425,6 +426,52 @@ int mvllm_swiglu(void* out, const void* gate, const void* up, int64_t n, int32_t
   return hip_status(
       mvllm::launch_swiglu(gate, up, out, n, dtype, static_cast<hipStream_t>(stream)),
       "swiglu: launch");
+}
+
+int mvllm_kv_write(void* key_pool, void* value_pool, float* k_scales, float* v_scales,
+                   const void* key, const void* value, const int32_t* slot_mapping,
+                   int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+                   int32_t block_size, int64_t num_blocks, int32_t src_dtype,
+                   int32_t pool_dtype, void* stream) {
+  g_error[0] = '\0';
+  if (src_dtype != mvllm::kF32 && src_dtype != mvllm::kF16 && src_dtype != mvllm::kBF16) {
+    return fail(MVLLM_ERR_INVALID,
+                "kv_write: key/value dtype code %d is not supported; float64 is not supported",
+                src_dtype);
+  }
+  if (!mvllm::kv_write_supported(src_dtype, pool_dtype, head_dim)) {
+    return fail(MVLLM_ERR_UNSUPPORTED,
+                "kv_write: a pool of dtype code %d cannot take keys of dtype code %d at head dim "
+                "%d; the pool must share the keys' dtype or be float8_e4m3fn (head dim 32, 64, "
+                "128 or 256)",
+                pool_dtype, src_dtype, head_dim);
+  }
+  if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || num_blocks <= 0) {
+    return fail(MVLLM_ERR_INVALID, "kv_write: bad shape");
+  }
+  if (block_size <= 0 || (block_size & (block_size - 1)) != 0) {
+    return fail(MVLLM_ERR_INVALID, "kv_write: block size %d is not a power of two", block_size);
+  }
+  if (num_blocks * block_size >= (int64_t{1} << 31)) {
+    return fail(MVLLM_ERR_INVALID, "kv_write: more slots than int32 slot_mapping addresses");
+  }
+  if (num_tokens == 0) return MVLLM_OK;
+  if (key_pool == nullptr || value_pool == nullptr || key == nullptr || value == nullptr ||
+      slot_mapping == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "kv_write: a required pointer is NULL");
+  }
+  const bool fp8 = pool_dtype == mvllm::kFP8E4M3;
+  if (fp8 != (k_scales != nullptr && v_scales != nullptr) || (!fp8 && (k_scales || v_scales))) {
+    return fail(MVLLM_ERR_INVALID,
+                "kv_write: k_scales and v_scales are required for a float8 pool and only for one");
+  }
+  int shift = 0;
+  while ((1 << shift) < block_size) ++shift;
+  return hip_status(mvllm::launch_kv_write(key_pool, value_pool, k_scales, v_scales, key, value,
+                                           slot_mapping, num_tokens, num_kv_heads, head_dim,
+                                           shift, src_dtype, pool_dtype,
+                                           static_cast<hipStream_t>(stream)),
+                    "kv_write: launch");
 }
 
 int mvllm_axpby(float* y, const float* x, float a, float b, int64_t n, void* stream) {

@@ -1,0 +1,342 @@
+// Paged KV write: scatter one iteration's keys and values into their pool slots.
+//
+// Replaces the two index_copy_ calls of the reference's PagedKvPool.write
+// (block/kv_pool.py:116-155): key/value [T, H_k, D] rows go to pool slot
+// slot_mapping[t] of the flat [num_blocks * P, H_k, D] view, for K and V in one launch.
+// A negative slot skips its token (padding rows of a captured decode graph).
+//
+// Same storage type: a copy, one thread per 16-byte chunk of K or V.
+//
+// fp8-e4m3 pools (no counterpart in the reference) carry one fp32 scale per (block, kv
+// head) for K and for V: stored code = e4m3(x / scale), read as code * scale. Writes
+// arrive a few tokens at a time, so the scale of a page grows as it fills. Scales are
+// powers of two, so re-encoding the rows already in a page under a grown scale only
+// shifts their exponents (exact, except where a value drops into e4m3's subnormals):
+//   * a run = consecutive tokens of this call that land on consecutive rows of one page
+//     (a page belongs to one sequence, whose new tokens are consecutive on the token
+//     axis and in the page, so a page gets one run per call: callers must keep it so);
+//     one wave per run;
+//   * a run that starts at offset 0 opens the page: the old scale and rows are dead;
+//   * new scale s = max(old scale, pow2ceil(max|x| / 448)) over the run's rows (0 when
+//     all are 0), pow2ceil = the least power of two >= its argument;
+//   * if s grew, the rows already in the page are re-encoded: e4m3((code * old) / s);
+//   * the run's rows are encoded as e4m3(clamp(x / s, -448, 448)), RNE (0 when s = 0).
+// Every step is an fp32 multiply / divide with one rounding, so the CPU restatement
+// (oracle/kv_write.py) reproduces the bytes exactly; since scales are powers of two the
+// kernel divides by multiplying with the exact reciprocal, which gives the same results.
+
+#include "common.hpp"
+#include "kv_write.hpp"
+
+namespace mvllm {
+
+namespace {
+
+// --------------------------------------------------------------------- copy
+
+__global__ __launch_bounds__(256) void kv_copy_kernel(void* __restrict__ k_pool,
+                                                      void* __restrict__ v_pool,
+                                                      const void* __restrict__ key,
+                                                      const void* __restrict__ value,
+                                                      const int32_t* __restrict__ slots,
+                                                      int64_t chunks_per_token, int64_t total) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= 2 * total) return;
+  const bool is_v = i >= total;
+  const int64_t j = is_v ? i - total : i;
+  const int64_t t = j / chunks_per_token;
+  const int64_t c = j - t * chunks_per_token;
+  const int32_t slot = slots[t];
+  if (slot < 0) return;
+  const char* src = static_cast<const char*>(is_v ? value : key) + j * 16;
+  char* dst = static_cast<char*>(is_v ? v_pool : k_pool) +
+              (static_cast<int64_t>(slot) * chunks_per_token + c) * 16;
+  store16(dst, nt_load16(src));
+}
+
+// Scalar fallback for row sizes that are not a multiple of 16 bytes.
+template <typename T>
+__global__ __launch_bounds__(256) void kv_copy_scalar_kernel(void* __restrict__ k_pool,
+                                                             void* __restrict__ v_pool,
+                                                             const void* __restrict__ key,
+                                                             const void* __restrict__ value,
+                                                             const int32_t* __restrict__ slots,
+                                                             int64_t row, int64_t total) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= 2 * total) return;
+  const bool is_v = i >= total;
+  const int64_t j = is_v ? i - total : i;
+  const int64_t t = j / row;
+  const int32_t slot = slots[t];
+  if (slot < 0) return;
+  static_cast<T*>(is_v ? v_pool : k_pool)[static_cast<int64_t>(slot) * row + (j - t * row)] =
+      static_cast<const T*>(is_v ? value : key)[j];
+}
+
+// ---------------------------------------------------------------------- fp8
+
+// Least power of two >= t (t >= 0 finite; 0 stays 0): clear the mantissa and, if it
+// was not already clear, step the exponent (a subnormal t gives 2^-126).
+__device__ __forceinline__ float pow2_ceil(float t) {
+  const uint32_t b = __float_as_uint(t);
+  if ((b & 0x7fffffu) == 0) return t;
+  return __uint_as_float((b & 0x7f800000u) + 0x800000u);
+}
+
+// Four values -> four e4m3 bytes (two packed conversions), each clamped to +-448.
+__device__ __forceinline__ uint32_t encode_fp8x4(float a, float b, float c, float d) {
+  auto cl = [](float v) { return fminf(fmaxf(v, -448.0f), 448.0f); };
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(cl(a), cl(b), 0, false);
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(cl(c), cl(d), lo, true));
+}
+
+// One wave per token (four tokens per workgroup); the wave of the token that starts a
+// run (its predecessor is not the row before it in the same page) handles the whole
+// run, the others exit at once. The run's length comes from a ballot over the following
+// slots. Lane task = (kv head, K or V, 8-element piece of a row), four per lane: pass 1
+// reduces max|x| over the run's rows (16 row pieces of loads in flight per lane), a
+// group all-reduce over the D/8 tasks of a (head, K/V) gives the scale, rows already in
+// the page are re-encoded if it grew, and pass 2 encodes the run's rows (reloaded from
+// L1/L2).
+template <typename TS, int D>
+__global__ __launch_bounds__(256) void kv_write_fp8_kernel(uint8_t* __restrict__ k_pool,
+                                                           uint8_t* __restrict__ v_pool,
+                                                           float* __restrict__ k_scales,
+                                                           float* __restrict__ v_scales,
+                                                           const void* __restrict__ key,
+                                                           const void* __restrict__ value,
+                                                           const int32_t* __restrict__ slots,
+                                                           int num_tokens, int hk,
+                                                           int block_shift) {
+  constexpr int E = 8;            // elements per task piece
+  constexpr int kPieces = D / E;  // tasks per (head, K/V)
+  constexpr int kUnroll = 4;      // rows whose loads are issued together
+  static_assert(D % E == 0 && kWave % kPieces == 0, "head dim");
+  const int lane = threadIdx.x % kWave;
+  const int t0 = static_cast<int>(blockIdx.x) * (blockDim.x / kWave) + static_cast<int>(threadIdx.x / kWave);
+  if (t0 >= num_tokens) return;
+  const int slot0 = slots[t0];
+  if (slot0 < 0) return;
+  const int page = slot0 >> block_shift;
+  const int rows_per_page = 1 << block_shift;
+  const int off0 = slot0 & (rows_per_page - 1);
+  if (t0 > 0) {
+    const int prev = slots[t0 - 1];
+    if (prev >= 0 && prev + 1 == slot0 && (prev >> block_shift) == page) return;  // mid-run
+  }
+  // Run length: the longest stretch of slot0 + i for i < min(rows left in the page,
+  // tokens left), 64 candidates per ballot.
+  const int limit = min(rows_per_page - off0, num_tokens - t0);
+  int len = limit;
+  for (int base = 1; base < limit; base += kWave) {
+    const int i = base + lane;
+    const bool stop = i < limit && slots[t0 + i] != slot0 + i;
+    const uint64_t mask = __builtin_amdgcn_ballot_w64(stop);
+    if (mask != 0) {
+      len = base + __builtin_ctzll(mask);
+      break;
+    }
+  }
+
+  // Lane tasks: task = tg + lane + 64k (k < kT) of the 2 * hk * D/8 (kv head, K or V,
+  // row piece) tasks; per batch kT tasks x kR rows of loads are in flight per lane.
+  const int ntasks = 2 * hk * kPieces;
+  constexpr int kT = 4;
+  constexpr int kR = 4;
+  constexpr int kChunks = Elem<TS>::kBytes == 4 ? 2 : 1;  // 16-byte loads per row piece
+  for (int tg = 0; tg < ntasks; tg += kWave * kT) {
+    int task[kT];
+    bool valid[kT];
+    float amax[kT], old[kT];
+#pragma unroll
+    for (int k = 0; k < kT; ++k) {
+      // A lane past the last task mirrors task `lane` (always valid): its loads and
+      // stores repeat that task's, so no memory access sits under a branch and the
+      // loads of a batch stay in flight together.
+      task[k] = tg + lane + kWave * k;
+      valid[k] = task[k] < ntasks;
+      if (!valid[k]) task[k] = lane % ntasks;
+      amax[k] = 0.0f;
+    }
+    auto pair_of = [&](int k) { return task[k] / kPieces; };
+    auto piece_of = [&](int k) { return (task[k] % kPieces) * E; };
+    auto src_row = [&](int k, int row) {
+      const int pr = pair_of(k);
+      const char* src = static_cast<const char*>(pr & 1 ? value : key);
+      return src + ((static_cast<int64_t>(t0 + row) * hk + (pr >> 1)) * D + piece_of(k)) *
+                       Elem<TS>::kBytes;
+    };
+    auto pool_piece = [&](int k, int row) {
+      const int pr = pair_of(k);
+      uint8_t* pool = pr & 1 ? v_pool : k_pool;
+      return pool + ((static_cast<int64_t>(page) << block_shift | row) * hk + (pr >> 1)) * D +
+             piece_of(k);
+    };
+    auto scale_ptr = [&](int k) {
+      const int pr = pair_of(k);
+      return (pr & 1 ? v_scales : k_scales) + static_cast<int64_t>(page) * hk + (pr >> 1);
+    };
+#pragma unroll
+    for (int k = 0; k < kT; ++k) old[k] = off0 > 0 ? *scale_ptr(k) : 0.0f;
+
+    // pass 1: max |x| over the run's rows, kT x kR row pieces in flight
+    for (int r0 = 0; r0 < len; r0 += kR) {
+      u32x4 raw[kT][kR][kChunks];
+#pragma unroll
+      for (int k = 0; k < kT; ++k) {
+#pragma unroll
+        for (int u = 0; u < kR; ++u) {
+          const int row = min(r0 + u, len - 1);  // rows past the run repeat its last
+#pragma unroll
+          for (int c = 0; c < kChunks; ++c) raw[k][u][c] = load16(src_row(k, row) + 16 * c);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kT; ++k) {
+#pragma unroll
+        for (int u = 0; u < kR; ++u) {
+          {
+            float x[E];
+#pragma unroll
+            for (int c = 0; c < kChunks; ++c) Chunk<TS>::unpack(raw[k][u][c], x + c * (E / kChunks));
+#pragma unroll
+            for (int e = 0; e < E; ++e) amax[k] = fmaxf(amax[k], fabsf(x[e]));
+          }
+        }
+      }
+    }
+    float sc[kT], inv[kT];
+#pragma unroll
+    for (int k = 0; k < kT; ++k) {
+      // tasks of one (head, K/V) are kPieces aligned lanes; invalid tasks form whole
+      // groups of their own
+      sc[k] = fmaxf(old[k], pow2_ceil(group_max<kPieces>(amax[k]) / 448.0f));
+      inv[k] = sc[k] > 0.0f ? 1.0f / sc[k] : 0.0f;  // exact: a power of two
+    }
+
+    // rows already in the page, re-encoded under a grown scale
+#pragma unroll
+    for (int k = 0; k < kT; ++k) {
+      if (!(valid[k] && old[k] > 0.0f && sc[k] > old[k])) continue;
+      for (int row = 0; row < off0; ++row) {
+        uint8_t* p = pool_piece(k, row);
+        const u32x2 w = *reinterpret_cast<const u32x2*>(p);
+        u32x2 out;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          float v[4];
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            // (code * old) / s: every factor a power of two or a 4-bit significand, so
+            // the products are exact and equal the correctly rounded quotient
+            v[b] = __fmul_rn(__fmul_rn(fp8e4m3_to_f32((w[i] >> (8 * b)) & 0xffu), old[k]), inv[k]);
+          }
+          out[i] = encode_fp8x4(v[0], v[1], v[2], v[3]);
+        }
+        *reinterpret_cast<u32x2*>(p) = out;
+      }
+    }
+
+    // pass 2: encode the run's rows (reloaded)
+    for (int r0 = 0; r0 < len; r0 += kR) {
+      u32x4 raw[kT][kR][kChunks];
+#pragma unroll
+      for (int k = 0; k < kT; ++k) {
+#pragma unroll
+        for (int u = 0; u < kR; ++u) {
+          const int row = min(r0 + u, len - 1);
+#pragma unroll
+          for (int c = 0; c < kChunks; ++c) raw[k][u][c] = load16(src_row(k, row) + 16 * c);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kT; ++k) {
+#pragma unroll
+        for (int u = 0; u < kR; ++u) {
+          // a repeated row or mirrored task stores the same bytes again
+          const int row = min(r0 + u, len - 1);
+          float x[E];
+#pragma unroll
+          for (int c = 0; c < kChunks; ++c) Chunk<TS>::unpack(raw[k][u][c], x + c * (E / kChunks));
+          u32x2 out;
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            // x / s == x * (1 / s) exactly: s is a power of two
+            out[i] = sc[k] > 0.0f ? encode_fp8x4(__fmul_rn(x[4 * i], inv[k]), __fmul_rn(x[4 * i + 1], inv[k]),
+                                                 __fmul_rn(x[4 * i + 2], inv[k]), __fmul_rn(x[4 * i + 3], inv[k]))
+                                  : 0u;
+          }
+          *reinterpret_cast<u32x2*>(pool_piece(k, off0 + row)) = out;
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kT; ++k) {
+      if (valid[k] && task[k] % kPieces == 0) *scale_ptr(k) = sc[k];
+    }
+  }
+}
+
+template <typename TS>
+hipError_t launch_fp8_t(void* k_pool, void* v_pool, float* k_scales, float* v_scales,
+                        const void* key, const void* value, const int32_t* slots, int num_tokens,
+                        int hk, int head_dim, int block_shift, hipStream_t stream) {
+#define MVLLM_KV_FP8(DIM)                                                                     \
+  kv_write_fp8_kernel<TS, DIM><<<(num_tokens + 3) / 4, 256, 0, stream>>>(                     \
+      static_cast<uint8_t*>(k_pool), static_cast<uint8_t*>(v_pool), k_scales, v_scales, key, \
+      value, slots, num_tokens, hk, block_shift)
+  switch (head_dim) {
+    case 32: MVLLM_KV_FP8(32); break;
+    case 64: MVLLM_KV_FP8(64); break;
+    case 128: MVLLM_KV_FP8(128); break;
+    case 256: MVLLM_KV_FP8(256); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef MVLLM_KV_FP8
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool kv_write_supported(int src_dtype, int pool_dtype, int head_dim) {
+  if (src_dtype != kF32 && src_dtype != kF16 && src_dtype != kBF16) return false;
+  if (pool_dtype == src_dtype) return true;
+  return pool_dtype == kFP8E4M3 &&
+         (head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256);
+}
+
+hipError_t launch_kv_write(void* k_pool, void* v_pool, float* k_scales, float* v_scales,
+                           const void* key, const void* value, const int32_t* slots,
+                           int num_tokens, int hk, int head_dim, int block_shift, int src_dtype,
+                           int pool_dtype, hipStream_t stream) {
+  if (pool_dtype == kFP8E4M3) {
+    switch (src_dtype) {
+      case kF32: return launch_fp8_t<float>(k_pool, v_pool, k_scales, v_scales, key, value, slots, num_tokens, hk, head_dim, block_shift, stream);
+      case kF16: return launch_fp8_t<f16_t>(k_pool, v_pool, k_scales, v_scales, key, value, slots, num_tokens, hk, head_dim, block_shift, stream);
+      case kBF16: return launch_fp8_t<bf16_t>(k_pool, v_pool, k_scales, v_scales, key, value, slots, num_tokens, hk, head_dim, block_shift, stream);
+      default: return hipErrorInvalidValue;
+    }
+  }
+  const int elt = src_dtype == kF32 ? 4 : 2;
+  const int64_t row_bytes = static_cast<int64_t>(hk) * head_dim * elt;
+  const bool aligned = (reinterpret_cast<uintptr_t>(k_pool) | reinterpret_cast<uintptr_t>(v_pool) |
+                        reinterpret_cast<uintptr_t>(key) | reinterpret_cast<uintptr_t>(value)) % 16 == 0;
+  if (aligned && row_bytes % 16 == 0) {
+    const int64_t per_token = row_bytes / 16;
+    const int64_t total = per_token * num_tokens;
+    kv_copy_kernel<<<static_cast<unsigned>((2 * total + 255) / 256), 256, 0, stream>>>(
+        k_pool, v_pool, key, value, slots, per_token, total);
+  } else {
+    const int64_t row = static_cast<int64_t>(hk) * head_dim;
+    const int64_t total = row * num_tokens;
+    const unsigned grid = static_cast<unsigned>((2 * total + 255) / 256);
+    if (elt == 4) {
+      kv_copy_scalar_kernel<float><<<grid, 256, 0, stream>>>(k_pool, v_pool, key, value, slots, row, total);
+    } else {
+      kv_copy_scalar_kernel<uint16_t><<<grid, 256, 0, stream>>>(k_pool, v_pool, key, value, slots, row, total);
+    }
+  }
+  return hipGetLastError();
+}
+
+}  // namespace mvllm

@@ -3,11 +3,15 @@
 One tensor per K and V shaped ``num_layers x num_blocks x P x H_k x D``, so one layer's
 view is exactly the ``num_blocks x P x H_k x D`` pool the paged-attention kernels walk
 (``slot = block * P + offset``), and a flat ``num_slots x H_k x D`` view of it is free.
+A ``float8_e4m3fn`` pool (not in the reference) also holds fp32 scales
+``num_layers x num_blocks x H_k`` for K and for V, maintained by the quantising write.
 """
 
 from __future__ import annotations
 
 import torch
+
+from mini_vllm.kernels import ops
 
 __all__ = ["PagedKvPool"]
 
@@ -25,12 +29,28 @@ class PagedKvPool:
         shape = (num_layers, num_blocks, block_size, num_kv_heads, head_dim)
         self.keys = torch.zeros(shape, dtype=dtype, device=device)
         self.values = torch.zeros(shape, dtype=dtype, device=device)
+        self.k_scales = self.v_scales = None
+        if dtype == torch.float8_e4m3fn:
+            scale_shape = (num_layers, num_blocks, num_kv_heads)
+            self.k_scales = torch.zeros(scale_shape, dtype=torch.float32, device=device)
+            self.v_scales = torch.zeros(scale_shape, dtype=torch.float32, device=device)
+
+    @property
+    def is_fp8(self) -> bool:
+        return self.k_scales is not None
+
+    def layer_scales(self, layer: int) -> tuple[torch.Tensor | None, torch.Tensor | None]:
+        """(k_scale, v_scale) of one layer for a float8 pool, else (None, None)."""
+        if not self.is_fp8:
+            return None, None
+        return self.k_scales[layer], self.v_scales[layer]
 
     @staticmethod
     def bytes_for(num_layers: int, num_blocks: int, block_size: int, num_kv_heads: int,
                   head_dim: int, dtype: torch.dtype) -> int:
         elt = torch.empty((), dtype=dtype).element_size()
-        return 2 * num_layers * num_blocks * block_size * num_kv_heads * head_dim * elt
+        scales = 2 * num_layers * num_blocks * num_kv_heads * 4 if dtype == torch.float8_e4m3fn else 0
+        return 2 * num_layers * num_blocks * block_size * num_kv_heads * head_dim * elt + scales
 
     def layer_keys(self, layer: int) -> torch.Tensor:
         return self.keys[layer]
@@ -39,17 +59,15 @@ class PagedKvPool:
         return self.values[layer]
 
     def write(self, layer: int, slot_mapping: torch.Tensor, key: torch.Tensor,
-              value: torch.Tensor) -> None:
-        """Scatter ``T x H_k x D`` keys/values to their slots. Slot values are not read
-        back (that would be a device-to-host sync per layer); the block manager bounded
-        them on the host."""
+              value: torch.Tensor, use_cuda: bool = False) -> None:
+        """Scatter ``T x H_k x D`` keys/values to their slots (``ops.kv_write``: one
+        kernel launch for K and V with ``use_cuda``, the reference's ``index_copy_``
+        pair otherwise). Slot values are not read back (that would be a device-to-host
+        sync per layer); the block manager bounded them on the host."""
         expected = (slot_mapping.shape[0], self.num_kv_heads, self.head_dim)
         if tuple(key.shape) != expected or key.shape != value.shape:
             raise ValueError(f"expected keys and values shaped {expected}, got "
                              f"{tuple(key.shape)} and {tuple(value.shape)}")
-        slots = self.num_blocks * self.block_size
-        flat_k = self.keys[layer].view(slots, self.num_kv_heads, self.head_dim)
-        flat_v = self.values[layer].view(slots, self.num_kv_heads, self.head_dim)
-        index = slot_mapping.to(device=flat_k.device, dtype=torch.int64)
-        flat_k.index_copy_(0, index, key.to(self.dtype))
-        flat_v.index_copy_(0, index, value.to(self.dtype))
+        k_scale, v_scale = self.layer_scales(layer)
+        ops.kv_write(self.keys[layer], self.values[layer], key, value, slot_mapping,
+                     use_cuda=use_cuda, k_scale=k_scale, v_scale=v_scale)

@@ -170,6 +170,8 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_swiglu.argtypes = [p, p, p, i64, i32, p]
     lib.mvllm_axpby.restype = ctypes.c_int
     lib.mvllm_axpby.argtypes = [p, p, f32, f32, i64, p]
+    lib.mvllm_kv_write.restype = ctypes.c_int
+    lib.mvllm_kv_write.argtypes = [p] * 7 + [i32] * 4 + [i64, i32, i32, p]
 
 
 EXPORTED_SYMBOLS = (
@@ -181,6 +183,7 @@ EXPORTED_SYMBOLS = (
     "mvllm_rope",
     "mvllm_swiglu",
     "mvllm_axpby",
+    "mvllm_kv_write",
 )
 
 
@@ -367,6 +370,51 @@ class HipExtension:
             )
         )
         return out
+
+    def kv_write(self, key_pool: torch.Tensor, value_pool: torch.Tensor, key: torch.Tensor,
+                 value: torch.Tensor, slot_mapping: torch.Tensor, *,
+                 k_scale: torch.Tensor | None = None,
+                 v_scale: torch.Tensor | None = None) -> None:
+        """Scatter ``T x H_k x D`` keys/values into one layer's pools at ``slot_mapping``
+        (replaces the reference's ``index_copy_`` pair, block/kv_pool.py:116-155). An
+        fp8 pool is quantised per (block, kv head) and its ``k_scale``/``v_scale``
+        (``num_blocks x H_k`` fp32) are updated in place; see include/minivllm_hip.h."""
+        tensors = (key_pool, value_pool, key, value, slot_mapping)
+        if not all(t.is_cuda for t in tensors):
+            raise RuntimeError("kv_write: pools, keys, values and slot_mapping must be CUDA tensors")
+        if key_pool.dim() != 4 or key_pool.shape != value_pool.shape:
+            raise RuntimeError("kv_write: the pools must be num_blocks x P x H_k x D and match")
+        nb, bs, hk, d = key_pool.shape
+        if key.shape != value.shape or key.dim() != 3 or tuple(key.shape[1:]) != (hk, d):
+            raise RuntimeError(
+                f"kv_write: expected keys and values shaped T x {hk} x {d}, got "
+                f"{tuple(key.shape)} and {tuple(value.shape)}")
+        if slot_mapping.dtype != torch.int32 or slot_mapping.shape != (key.shape[0],):
+            raise RuntimeError("kv_write: slot_mapping must be int32 with one slot per token")
+        if not (key_pool.is_contiguous() and value_pool.is_contiguous()):
+            raise RuntimeError("kv_write: the pools must be contiguous")
+        if key.dtype != value.dtype:
+            raise RuntimeError(f"kv_write: keys are {key.dtype} but values are {value.dtype}")
+        fp8 = key_pool.dtype == torch.float8_e4m3fn
+        if fp8:
+            for name, sc in (("k_scale", k_scale), ("v_scale", v_scale)):
+                if sc is None or sc.dtype != torch.float32 or tuple(sc.shape) != (nb, hk) \
+                        or not sc.is_contiguous() or not sc.is_cuda:
+                    raise RuntimeError(
+                        f"kv_write: a float8 pool needs {name} as a contiguous float32 "
+                        f"{nb} x {hk} CUDA tensor")
+        elif k_scale is not None or v_scale is not None:
+            raise RuntimeError("kv_write: k_scale / v_scale are for float8 pools only")
+        key = key.contiguous()
+        value = value.contiguous()
+        slot_mapping = slot_mapping.contiguous()
+        src = DTYPE_CODES.get(key.dtype, -1)
+        pool = DTYPE_CODES.get(key_pool.dtype, -1)
+        self._check(self.lib.mvllm_kv_write(
+            key_pool.data_ptr(), value_pool.data_ptr(),
+            k_scale.data_ptr() if fp8 else None, v_scale.data_ptr() if fp8 else None,
+            key.data_ptr(), value.data_ptr(), slot_mapping.data_ptr(),
+            key.shape[0], hk, d, bs, nb, src, pool, _stream(key.device)))
 
     def swiglu(self, gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
         """``silu(gate) * up`` (reference csrc/swiglu.cu:87-120)."""

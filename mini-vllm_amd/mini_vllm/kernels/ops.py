@@ -10,6 +10,12 @@ engine and tests above it run unchanged:
                     context_lens, seq_lens, max_query_len, max_context_len,
                     scale=None, use_cuda=False)                        ops.py:200-254
 
+plus one op the reference performs inline in ``PagedKvPool.write``
+(block/kv_pool.py:116-155, two ``index_copy_`` calls per layer):
+
+    kv_write(key_pool, value_pool, key, value, slot_mapping, use_cuda=False,
+             *, k_scale=None, v_scale=None)
+
 The callee behind ``use_cuda=True`` is ``libminivllm_hip.so`` (HIP for gfx950).
 
 One deliberate difference: ``use_cuda=True`` never falls back. The reference routes a
@@ -37,6 +43,7 @@ __all__ = [
     "attention",
     "cuda_kernel_names",
     "dispatch_report",
+    "kv_write",
     "paged_attention",
     "rmsnorm",
     "rope",
@@ -52,6 +59,7 @@ CUDA_KERNELS: dict[str, tuple[bool, str]] = {
     "decode_attention": (False, "dense-cache decode (not in this library)"),
     "flash_prefill": (False, "dense-cache prefill (not in this library)"),
     "paged_attention": (True, "csrc/paged_decode.hip + csrc/paged_prefill.hip"),
+    "kv_write": (True, "csrc/kv_write.hip"),
 }
 
 # Kernels that exist but are deliberately not dispatched, with the reason.
@@ -213,3 +221,19 @@ def _check_kernel_can_page(q: torch.Tensor, key_pool: torch.Tensor, value_pool: 
         raise RuntimeError("paged_attention: the metadata tensors must be int32")
     if not block_tables.is_contiguous():
         raise RuntimeError("paged_attention: block_tables must be contiguous")
+
+
+def kv_write(key_pool: torch.Tensor, value_pool: torch.Tensor, key: torch.Tensor,
+             value: torch.Tensor, slot_mapping: torch.Tensor, use_cuda: bool = False, *,
+             k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None) -> None:
+    """Scatter ``T x H_k x D`` keys/values into one layer's ``num_blocks x P x H_k x D``
+    pools at ``slot_mapping`` (int32, flat slot = block x P + offset; negative = skip).
+    Kernel: ``csrc/kv_write.hip``, K and V in one launch. A ``float8_e4m3fn`` pool is
+    quantised with per-(block, kv head) scales ``k_scale``/``v_scale`` updated in place
+    (policy: include/minivllm_hip.h)."""
+    if _use_kernel("kv_write", use_cuda, key):
+        load_extension().kv_write(key_pool, value_pool, key, value, slot_mapping,
+                                  k_scale=k_scale, v_scale=v_scale)
+        return
+    torch_path.kv_write(key_pool, value_pool, key, value, slot_mapping,
+                        k_scale=k_scale, v_scale=v_scale)

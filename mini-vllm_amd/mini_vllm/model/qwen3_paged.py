@@ -125,11 +125,13 @@ class Qwen3Paged:
         q = ops.rope(q.unsqueeze(0), batch.positions, self.cos, self.sin, use_cuda=u).squeeze(0)
         k = ops.rope(k.unsqueeze(0), batch.positions, self.cos, self.sin, use_cuda=u).squeeze(0)
         kv = self.manager.kv
-        kv.write(layer, batch.slot_mapping, k, v)
+        kv.write(layer, batch.slot_mapping, k, v, use_cuda=u)
+        k_scale, v_scale = kv.layer_scales(layer)
         out = ops.paged_attention(
             q.contiguous(), kv.layer_keys(layer), kv.layer_values(layer), batch.block_tables,
             batch.cu_seqlens_q, batch.context_lens, batch.seq_lens, batch.max_query_len,
-            batch.max_context_len, 1.0 / math.sqrt(c.head_dim), use_cuda=u)
+            batch.max_context_len, 1.0 / math.sqrt(c.head_dim), use_cuda=u,
+            k_scale=k_scale, v_scale=v_scale)
         return _linear(out.view(t, c.q_size), w["wo"])
 
     @torch.no_grad()

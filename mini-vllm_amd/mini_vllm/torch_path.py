@@ -21,6 +21,7 @@ import torch
 __all__ = [
     "apply_rope",
     "dequantize_fp8_pool",
+    "kv_write",
     "paged_attention_gathered",
     "rms_norm",
     "rope_tables",
@@ -69,6 +70,60 @@ def apply_rope(x: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor,
     half = x.shape[-1] // 2
     rotated = torch.cat((-x32[..., half:], x32[..., :half]), dim=-1)
     return (x32 * c + rotated * s).to(x.dtype)
+
+
+def _pow2_ceil(t: torch.Tensor) -> torch.Tensor:
+    """Least power of two >= t (float32, t >= 0; 0 stays 0)."""
+    b = t.float().contiguous().view(torch.int32)
+    up = torch.where((b & 0x7FFFFF) == 0, b, (b & 0x7F800000) + 0x800000)
+    return up.view(torch.float32)
+
+
+def kv_write(key_pool: torch.Tensor, value_pool: torch.Tensor, key: torch.Tensor,
+             value: torch.Tensor, slot_mapping: torch.Tensor, *,
+             k_scale: torch.Tensor | None = None, v_scale: torch.Tensor | None = None) -> None:
+    """Scatter ``T x H_k x D`` keys/values into one layer's pools at ``slot_mapping``.
+
+    Same dtype: the reference's ``index_copy_`` pair (block/kv_pool.py:148-155), with
+    negative slots skipped. A ``float8_e4m3fn`` pool follows the library's quantising
+    policy (include/minivllm_hip.h, ``mvllm_kv_write``) run by run in torch, reading
+    the slots on the host (this path syncs; the kernel does not).
+    """
+    nb, bs, hk, d = key_pool.shape
+    keep = slot_mapping >= 0
+    if key_pool.dtype != torch.float8_e4m3fn:
+        index = slot_mapping[keep].to(torch.int64)
+        key_pool.view(nb * bs, hk, d).index_copy_(0, index, key[keep].to(key_pool.dtype))
+        value_pool.view(nb * bs, hk, d).index_copy_(0, index, value[keep].to(value_pool.dtype))
+        return
+    slots = slot_mapping.tolist()
+    t = 0
+    while t < len(slots):
+        if slots[t] < 0:
+            t += 1
+            continue
+        block, row0 = divmod(slots[t], bs)
+        n = 1
+        while (t + n < len(slots) and slots[t + n] >= 0 and slots[t + n] // bs == block
+               and slots[t + n] % bs == row0 + n):
+            n += 1
+        for pool, scales, x in ((key_pool, k_scale, key), (value_pool, v_scale, value)):
+            rows = x[t:t + n].float()                                   # n x H_k x D
+            amax = rows.abs().amax(dim=(0, 2))                          # H_k
+            old = torch.zeros_like(amax) if row0 == 0 else scales[block].clone()
+            s = torch.maximum(old, _pow2_ceil(amax / 448.0))
+            grow = (old > 0) & (s > old)
+            if row0 > 0 and bool(grow.any()):
+                prev = pool[block, :row0].float()                       # row0 x H_k x D
+                re = ((prev * old[None, :, None]) / s[None, :, None]).clamp(-448.0, 448.0)
+                pool[block, :row0] = torch.where(grow[None, :, None],
+                                                 re.to(torch.float8_e4m3fn), pool[block, :row0])
+            safe = torch.where(s > 0, s, torch.ones_like(s))
+            enc = (rows / safe[None, :, None]).clamp(-448.0, 448.0)
+            enc = torch.where((s > 0)[None, :, None], enc, torch.zeros_like(enc))
+            pool[block, row0:row0 + n] = enc.to(torch.float8_e4m3fn)
+            scales[block] = s
+        t += n
 
 
 def dequantize_fp8_pool(pool: torch.Tensor, scales: torch.Tensor,

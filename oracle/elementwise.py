@@ -104,7 +104,8 @@ def fp8_e4m3_decode(codes: np.ndarray) -> np.ndarray:
 
 
 def fp8_e4m3_encode(x: np.ndarray) -> np.ndarray:
-    """Round-to-nearest-even encode with saturation to +-448 (finite inputs)."""
+    """Round-to-nearest-even encode with saturation to +-448 (finite inputs); the sign
+    bit is kept, so -0.0 encodes as 0x80 (as torch's cast and the GPU conversion do)."""
     table = fp8_e4m3_decode(np.arange(256, dtype=np.uint8))
     finite = np.array([i for i in range(128) if not np.isnan(table[i])])  # positive codes
     mags = table[finite].astype(np.float64)
@@ -116,4 +117,4 @@ def fp8_e4m3_encode(x: np.ndarray) -> np.ndarray:
     pick_hi = (a - lo > hi - a) | ((a - lo == hi - a) & (finite[idx] % 2 == 0))
     code = np.where(pick_hi, finite[idx], finite[idx - 1])
     code = np.where(a == mags[idx - 1], finite[idx - 1], code)
-    return (code | np.where(x < 0, 0x80, 0)).astype(np.uint8)
+    return (code | np.where(np.signbit(x), 0x80, 0)).astype(np.uint8)

@@ -20,9 +20,10 @@ def tiny_config(dtype=torch.float32, **over) -> ModelConfig:
 
 
 def make_engine(config, weights, *, num_blocks=64, block_size=16, use_cuda=False,
-                device="cpu", sched=None, use_graphs=False) -> LLMEngine:
+                device="cpu", sched=None, use_graphs=False, kv_dtype=None) -> LLMEngine:
     manager = BlockManager(num_blocks, block_size, config.num_hidden_layers,
-                           config.num_key_value_heads, config.head_dim, config.dtype, device)
+                           config.num_key_value_heads, config.head_dim,
+                           kv_dtype or config.dtype, device)
     model = Qwen3Paged(config, weights, manager, use_cuda=use_cuda)
     return LLMEngine(model, sched or SchedulerConfig(), device=device, use_graphs=use_graphs)
 

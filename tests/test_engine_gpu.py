@@ -126,3 +126,23 @@ def test_qwen3_0_6b_shape_end_to_end(extension, device):
     assert all(len(g) == 12 and all(0 <= t < config.vocab_size for t in g) for g in got)
     assert engine.stats.prefill_tokens == sum(len(p) for p in ps)
     engine.model.manager.check_no_leaks()
+
+
+@pytest.mark.parametrize("sched", [SchedulerConfig(), SchedulerConfig(max_batched_tokens=24, chunk_size=8)],
+                         ids=["one-pass", "chunked"])
+def test_fp8_kv_cache_engine_kernels_match_the_torch_path(extension, device, sched):
+    """An float8_e4m3fn KV pool end to end: the quantising write kernel and the fp8
+    attention kernels against the PyTorch path (the same write policy in torch, then
+    gather-dequantise-dense attention) on the same device, fp32 activations."""
+    config = tiny_config(torch.float32)
+    weights = random_weights(config, seed=7, device=device)
+    ps = prompts(6, 3, 60, config.vocab_size, seed=8)
+    runs = []
+    for use_cuda in (True, False):
+        engine = make_engine(config, weights, use_cuda=use_cuda, device=device, sched=sched,
+                             kv_dtype=torch.float8_e4m3fn)
+        runs.append(engine.generate(ps, MAX_TOKENS))
+        engine.model.manager.check_no_leaks()
+    kern, ref = runs
+    assert all(k[0] == r[0] for k, r in zip(kern, ref))
+    assert sum(k == r for k, r in zip(kern, ref)) >= len(ps) - 1

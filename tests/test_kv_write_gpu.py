@@ -1,0 +1,148 @@
+"""Paged KV write kernel (``csrc/kv_write.hip``) on the MI355X, through the C ABI, against
+the CPU oracle (oracle/kv_write.py): bit-exact bytes and scales (``-m gpu``)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from mini_vllm.kernels import ops
+from oracle import kv_write as ow
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand_slots(rng, num_blocks, bs, t, pad=0):
+    s = rng.choice(num_blocks * bs, size=t, replace=False).astype(np.int32)
+    s = np.concatenate([s, -np.ones(pad, dtype=np.int32)])
+    rng.shuffle(s)
+    return s
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("hk,d", [(8, 128), (2, 64), (3, 20)])
+def test_copy_is_the_reference_index_copy(extension, device, dtype, hk, d):
+    """Same-dtype pools: bit-exact scatter, padding slots (-1) skipped; (3, 20) rows are
+    not a multiple of 16 bytes in 16-bit types and take the per-element kernel."""
+    rng = np.random.default_rng(hk * d)
+    nb, bs, t = 40, 16, 300
+    pool_k = torch.randn(nb, bs, hk, d).to(dtype)
+    pool_v = torch.randn(nb, bs, hk, d).to(dtype)
+    slots = _rand_slots(rng, nb, bs, t, pad=7)
+    key = torch.randn(t + 7, hk, d).to(dtype)
+    value = torch.randn(t + 7, hk, d).to(dtype)
+    want_k = ow.kv_write_copy(pool_k.float().numpy(), slots, key.float().numpy())
+    want_v = ow.kv_write_copy(pool_v.float().numpy(), slots, value.float().numpy())
+    gk, gv = pool_k.to(device), pool_v.to(device)
+    extension.kv_write(gk, gv, key.to(device), value.to(device), torch.from_numpy(slots).to(device))
+    torch.cuda.synchronize()
+    assert np.array_equal(gk.float().cpu().numpy(), want_k)
+    assert np.array_equal(gv.float().cpu().numpy(), want_v)
+
+
+def _scenario(rng, hk, d, bs):
+    """A prefill chunk over 2.5 blocks of one sequence plus 5 rows of another, then decode
+    steps (with a padding row) whose magnitudes grow, so scales grow and rows already in
+    a block are re-encoded; the last step reopens a freed block at row 0."""
+    seq_a = [5 * bs + i for i in range(bs)] + [9 * bs + i for i in range(bs)] + \
+            [2 * bs + i for i in range(bs // 2)]
+    seq_b = [11 * bs + i for i in range(min(5, bs))]
+    steps = [np.array(seq_a + seq_b, np.int32)]
+    for k in range(6):
+        row_a = bs // 2 + k
+        a = 2 * bs + row_a if row_a < bs else 3 * bs + row_a - bs
+        row_b = min(5, bs) + k
+        b = 11 * bs + row_b if row_b < bs else 12 * bs + row_b - bs
+        steps.append(np.array([a, b, -1], np.int32))
+    steps.append(np.array([9 * bs, 9 * bs + 1], np.int32))
+    xs = [(rng.standard_normal((len(s), hk, d)) * (1.0 + 0.7 * i)).astype(np.float32)
+          for i, s in enumerate(steps)]
+    return steps, xs
+
+
+@pytest.mark.parametrize("src", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("hk,d,bs", [(8, 128, 16), (2, 64, 16), (4, 256, 4), (2, 128, 1), (2, 32, 16)])
+def test_fp8_write_matches_the_oracle_bytes(extension, device, src, hk, d, bs):
+    rng = np.random.default_rng(d + bs)
+    nb = 16
+    steps, xs = _scenario(rng, hk, d, bs) if bs > 1 else (
+        [np.array([3, 4, 9, -1, 12], np.int32), np.array([5, 3], np.int32)],
+        [rng.standard_normal((5, hk, d)).astype(np.float32),
+         rng.standard_normal((2, hk, d)).astype(np.float32) * 3])
+    codes_k = np.zeros((nb, bs, hk, d), np.uint8)
+    scales_k = np.zeros((nb, hk), np.float32)
+    codes_v, scales_v = codes_k.copy(), scales_k.copy()
+    kp = torch.zeros(nb, bs, hk, d, dtype=torch.float8_e4m3fn, device=device)
+    vp = torch.zeros_like(kp)
+    ks = torch.zeros(nb, hk, device=device)
+    vs = torch.zeros(nb, hk, device=device)
+    for sl, x in zip(steps, xs):
+        key = torch.from_numpy(x).to(src)
+        value = (torch.from_numpy(x) * 0.5 + 0.25).to(src)
+        codes_k, scales_k = ow.kv_write_fp8(codes_k, scales_k, sl, key.float().numpy())
+        codes_v, scales_v = ow.kv_write_fp8(codes_v, scales_v, sl, value.float().numpy())
+        extension.kv_write(kp, vp, key.to(device), value.to(device),
+                           torch.from_numpy(sl).to(device), k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    assert np.array_equal(ks.cpu().numpy(), scales_k)
+    assert np.array_equal(vs.cpu().numpy(), scales_v)
+    assert np.array_equal(kp.view(torch.uint8).cpu().numpy(), codes_k)
+    assert np.array_equal(vp.view(torch.uint8).cpu().numpy(), codes_v)
+
+
+def test_fp8_encoding_is_round_to_nearest_even(extension, device):
+    """Every e4m3 code's value and every midpoint between neighbours (ties go to the
+    even code), written at scale 1 (a block whose max is 448 -> scale pow2ceil(1) = 1)."""
+    from oracle.elementwise import fp8_e4m3_decode, fp8_e4m3_encode
+    vals = fp8_e4m3_decode(np.arange(0, 0x7F, dtype=np.uint8)).astype(np.float64)
+    mids = (vals[:-1] + vals[1:]) / 2
+    x = np.concatenate([vals, mids, -vals, -mids, [448.0]]).astype(np.float32)
+    n = x.size
+    d = 128
+    rows = -(-n // d)
+    flat = np.zeros(rows * d, np.float32)
+    flat[:n] = x
+    flat[n:] = 448.0
+    data = flat.reshape(rows, 1, d)
+    kp = torch.zeros(1, rows, 1, d, dtype=torch.float8_e4m3fn, device=device)
+    vp = torch.zeros_like(kp)
+    ks = torch.zeros(1, 1, device=device)
+    vs = torch.zeros(1, 1, device=device)
+    xt = torch.from_numpy(data).to(device)
+    extension.kv_write(kp, vp, xt, xt, torch.arange(rows, dtype=torch.int32, device=device),
+                       k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    assert float(ks[0, 0]) == 1.0
+    got = kp.view(torch.uint8).cpu().numpy().reshape(-1)[:n]
+    want = fp8_e4m3_encode(x)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, [(float(x[i]), int(got[i]), int(want[i])) for i in bad[:8]]
+
+
+def test_ops_route_kv_write_to_the_kernel(extension, device):
+    pool = torch.zeros(4, 16, 2, 64, dtype=torch.bfloat16, device=device)
+    pool_v = torch.zeros_like(pool)
+    x = torch.randn(3, 2, 64, dtype=torch.bfloat16, device=device)
+    slots = torch.tensor([17, 18, 40], dtype=torch.int32, device=device)
+    ops.kv_write(pool, pool_v, x, x, slots, use_cuda=True)
+    assert torch.equal(pool.view(-1, 2, 64)[17], x[0]) and torch.equal(pool.view(-1, 2, 64)[40], x[2])
+    with pytest.raises(RuntimeError, match="device tensors"):
+        ops.kv_write(pool.cpu(), pool_v.cpu(), x.cpu(), x.cpu(), slots.cpu(), use_cuda=True)
+
+
+def test_kv_write_refusals(extension, device):
+    pool = torch.zeros(4, 16, 2, 64, dtype=torch.bfloat16, device=device)
+    x = torch.randn(3, 2, 64, dtype=torch.bfloat16, device=device)
+    slots = torch.tensor([1, 2, 3], dtype=torch.int32, device=device)
+    with pytest.raises(RuntimeError, match="share the keys' dtype"):
+        extension.kv_write(pool.half(), pool.half(), x, x, slots)
+    with pytest.raises(RuntimeError, match="int32"):
+        extension.kv_write(pool, pool.clone(), x, x, slots.long())
+    with pytest.raises(RuntimeError, match="shaped"):
+        extension.kv_write(pool, pool.clone(), x[:, :1], x[:, :1], slots)
+    fp8 = pool.to(torch.float8_e4m3fn)
+    with pytest.raises(RuntimeError, match="k_scale"):
+        extension.kv_write(fp8, fp8.clone(), x, x, slots)
+    with pytest.raises(RuntimeError, match="float8 pools only"):
+        extension.kv_write(pool, pool.clone(), x, x, slots, k_scale=torch.zeros(4, 2, device=device))
