@@ -219,6 +219,12 @@ def run_elementwise(steps: int = 20) -> dict:
     measure("rope_16x128", lambda: (torch.randn(1, tokens, 16, 128, device="cuda", dtype=bf),),
             lambda x: ops.rope(x, pos, cos, sin, use_cuda=True),
             2 * tokens * 16 * 128 * 2 + 2 * tokens * 128 * 4)
+    wk = torch.ones(128, device="cuda", dtype=bf)
+    measure("qk_norm_rope_16q8k_x128",
+            lambda: (torch.randn(tokens, 16, 128, device="cuda", dtype=bf),
+                     torch.randn(tokens, 8, 128, device="cuda", dtype=bf)),
+            lambda q, k: ops.qk_norm_rope(q, k, wq, wk, pos, cos, sin, 1e-6, use_cuda=True),
+            2 * tokens * 24 * 128 * 2 + 2 * tokens * 128 * 4 + 512)
     measure("swiglu_I3072", lambda: (torch.randn(tokens, 3072, device="cuda", dtype=bf),
                                      torch.randn(tokens, 3072, device="cuda", dtype=bf)),
             lambda g, u: ops.swiglu(g, u, use_cuda=True), 3 * tokens * 3072 * 2)

@@ -124,6 +124,22 @@ int mvllm_rope(void* out, const void* x, const void* positions, int32_t position
                int64_t head_dim, int64_t num_positions, int64_t max_positions, int32_t dtype,
                void* stream);
 
+/* Qwen3's per-head QK-norm then RoPE, q and k in one launch: q_out = rope(rmsnorm(q,
+ * q_weight)), k_out = rope(rmsnorm(k, k_weight)), bitwise equal to mvllm_rmsnorm followed
+ * by mvllm_rope (same reduction order and rounding points). Replaces the four calls of
+ * the reference's Qwen3PagedAttention (model/qwen3_paged.py:73-78: ops.rmsnorm x 2,
+ * ops.rope x 2); no counterpart in mini_vllm_C.
+ *   q, q_out [num_tokens, num_q_heads, head_dim]; k, k_out [num_tokens, num_kv_heads,
+ *   head_dim]; q_weight, k_weight [head_dim]; all of `dtype` (f32/f16/bf16), 16-byte
+ *   aligned. positions, cos_table, sin_table as for mvllm_rope. head_dim: 16-byte chunks
+ *   per head a power of two from 2 to 64 (bf16: D = 16 .. 512). */
+int mvllm_qk_norm_rope(void* q_out, void* k_out, const void* q, const void* k,
+                       const void* q_weight, const void* k_weight, const void* positions,
+                       int32_t positions_bytes, const float* cos_table, const float* sin_table,
+                       int64_t num_tokens, int32_t num_q_heads, int32_t num_kv_heads,
+                       int32_t head_dim, int64_t num_positions, int64_t max_positions, float eps,
+                       int32_t dtype, void* stream);
+
 /* out = T(T(g * T(sigmoid(g))) * u) elementwise over n elements of `dtype`.
  * Replaces `mini_vllm_C.swiglu` (csrc/bindings.cpp:14,59-63 -> csrc/swiglu.cu:87-120),
  * called from mini_vllm/kernels/ops.py:161-162. */

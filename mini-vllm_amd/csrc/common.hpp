@@ -54,6 +54,11 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
   return static_cast<float>(v);
 }
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  // f is an fp32 value that must be rounded to fp16 as it stands. Without the empty asm
+  // the compiler may fold the multiply that produced f into the conversion
+  // (v_fma_mixlo_f16: one rounding of the exact product), which differs from PyTorch's
+  // fp32 multiply then .to(float16) whenever the fp32 result lands on an fp16 tie.
+  asm volatile("" : "+v"(f));
   const _Float16 v = static_cast<_Float16>(f);  // v_cvt_f16_f32, round to nearest even
   uint16_t b;
   __builtin_memcpy(&b, &v, 2);

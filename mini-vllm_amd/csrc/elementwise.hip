@@ -328,6 +328,163 @@ hipError_t launch_rope(const void* x, const void* positions, int pos_bytes, cons
   }
 }
 
+// -------------------------------------------------------------- qk_norm_rope
+
+// Qwen3's per-head QK-norm followed by RoPE, for q and k in one launch: what
+// rmsnorm(q, w_q) -> rope(q) and rmsnorm(k, w_k) -> rope(k) compute (reference
+// model/qwen3_paged.py:73-78), with the same rounding points, so the result is bitwise
+// equal to the two unfused kernels: the row's sum of squares is reduced in
+// rmsnorm_vec_kernel's order (kR lanes of one 16-byte chunk each, group_sum), the norm
+// output is rounded to T, and the rotation is rope_kernel's on those rounded values.
+// kR = D / N lanes per head row (one 16-byte chunk each); lane r's partner in the
+// rotation holds dims +-D/2, i.e. lane r ^ (kR / 2). Rows: the T * Hq rows of q, then
+// the T * Hk rows of k.
+template <typename T, typename TPos, int kR>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(
+    const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ wq,
+    const void* __restrict__ wk, const TPos* __restrict__ positions,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, void* __restrict__ q_out,
+    void* __restrict__ k_out, int64_t q_rows, int64_t k_rows, int hq, int hk,
+    int64_t num_positions, int64_t max_positions, float eps) {
+  constexpr int N = Chunk<T>::kN;
+  constexpr int D = kR * N;
+  const int lane = threadIdx.x % kWave;
+  const int r = lane % kR;
+  const int64_t row = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kR;
+  const bool live = row < q_rows + k_rows;
+  const bool is_k = row >= q_rows;
+  const int64_t local = is_k ? row - q_rows : row;
+  const int64_t token = live ? local / (is_k ? hk : hq) : 0;
+  const char* xr = static_cast<const char*>(is_k ? k : q) +
+                   (live ? local : 0) * static_cast<int64_t>(D) * Elem<T>::kBytes;
+
+  // rmsnorm, as rmsnorm_vec_kernel<T, kR, 1>
+  const u32x4 held = nt_load16(xr + r * 16);
+  float f[N];
+  Chunk<T>::unpack(held, f);
+  float sumsq = 0.0f;
+#pragma unroll
+  for (int e = 0; e < N; ++e) sumsq = fmaf(f[e], f[e], sumsq);
+  sumsq = group_sum<kR>(sumsq);
+  const float inv = rsqrtf(sumsq / static_cast<float>(D) + eps);
+  float wf[N];
+  Chunk<T>::unpack(load16(static_cast<const char*>(is_k ? wk : wq) + r * 16), wf);
+  float y[N];
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    if constexpr (N == 4) {
+      y[e] = __fmul_rn(__fmul_rn(f[e], inv), wf[e]);
+    } else {
+      y[e] = Elem<T>::round(__fmul_rn(Elem<T>::round(__fmul_rn(f[e], inv)), wf[e]));
+    }
+  }
+
+  // the rotation partner's values (dims +-D/2), across lanes: lane r ^ (kR / 2). For
+  // kR = 16 that is a rotation by 8 inside a 16-lane DPP row (one v_mov_dpp per value).
+  float py[N];
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    if constexpr (kR == 16) {
+      py[e] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(y[e]), 0x128, 0xF, 0xF, false));
+    } else {
+      py[e] = __shfl_xor(y[e], kR / 2, kWave);
+    }
+  }
+  if (!live) return;
+
+  const int64_t pos = static_cast<int64_t>(positions[token % num_positions]);
+  float out[N];
+  if (pos < 0 || pos >= max_positions) {
+#pragma unroll
+    for (int e = 0; e < N; ++e) out[e] = __int_as_float(0x7fc00000);
+  } else {
+    const float* cr = cos_t + pos * D + r * N;
+    const float* sr = sin_t + pos * D + r * N;
+    float c[N], sn[N];
+#pragma unroll
+    for (int e = 0; e < N; e += 4) {
+      Chunk<float>::unpack(load16(cr + e), c + e);
+      Chunk<float>::unpack(load16(sr + e), sn + e);
+    }
+    const bool lo = r < kR / 2;
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      // lo half: x_lo * cos - x_hi * sin; hi half: x_hi * cos + x_lo * sin
+      out[e] = lo ? __fsub_rn(__fmul_rn(y[e], c[e]), __fmul_rn(py[e], sn[e]))
+                  : __fadd_rn(__fmul_rn(y[e], c[e]), __fmul_rn(py[e], sn[e]));
+    }
+  }
+  char* orow = static_cast<char*>(is_k ? k_out : q_out) + local * static_cast<int64_t>(D) * Elem<T>::kBytes;
+  nt_store16(orow + r * 16, pack_chunk<T>(out));
+}
+
+namespace {
+template <typename T, typename TPos>
+hipError_t launch_qk_norm_rope_p(const void* q, const void* k, const void* wq, const void* wk,
+                                 const void* positions, const float* cos_t, const float* sin_t,
+                                 void* q_out, void* k_out, int64_t tokens, int hq, int hk, int dim,
+                                 int64_t num_positions, int64_t max_positions, float eps,
+                                 hipStream_t stream) {
+  constexpr int N = Chunk<T>::kN;
+  const int64_t q_rows = tokens * hq;
+  const int64_t k_rows = tokens * hk;
+  const TPos* pos = static_cast<const TPos*>(positions);
+#define MVLLM_QKNR(KR)                                                                          \
+  qk_norm_rope_kernel<T, TPos, KR><<<static_cast<unsigned>(((q_rows + k_rows) * KR + 255) / 256), \
+                                     256, 0, stream>>>(q, k, wq, wk, pos, cos_t, sin_t, q_out,    \
+                                                       k_out, q_rows, k_rows, hq, hk,            \
+                                                       num_positions, max_positions, eps)
+  switch (dim / N) {
+    case 2: MVLLM_QKNR(2); break;
+    case 4: MVLLM_QKNR(4); break;
+    case 8: MVLLM_QKNR(8); break;
+    case 16: MVLLM_QKNR(16); break;
+    case 32: MVLLM_QKNR(32); break;
+    case 64: MVLLM_QKNR(64); break;
+    default: return hipErrorInvalidValue;
+  }
+#undef MVLLM_QKNR
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_qk_norm_rope_t(const void* q, const void* k, const void* wq, const void* wk,
+                                 const void* positions, int pos_bytes, const float* cos_t,
+                                 const float* sin_t, void* q_out, void* k_out, int64_t tokens,
+                                 int hq, int hk, int dim, int64_t num_positions,
+                                 int64_t max_positions, float eps, hipStream_t stream) {
+  if (pos_bytes == 8) {
+    return launch_qk_norm_rope_p<T, int64_t>(q, k, wq, wk, positions, cos_t, sin_t, q_out, k_out,
+                                             tokens, hq, hk, dim, num_positions, max_positions,
+                                             eps, stream);
+  }
+  return launch_qk_norm_rope_p<T, int32_t>(q, k, wq, wk, positions, cos_t, sin_t, q_out, k_out,
+                                           tokens, hq, hk, dim, num_positions, max_positions, eps,
+                                           stream);
+}
+}  // namespace
+
+bool qk_norm_rope_supported(int dtype, int head_dim) {
+  const int n = dtype == kF32 ? 4 : 8;
+  if (dtype != kF32 && dtype != kF16 && dtype != kBF16) return false;
+  const int lanes = head_dim / n;
+  return head_dim % n == 0 && (lanes == 2 || lanes == 4 || lanes == 8 || lanes == 16 ||
+                                lanes == 32 || lanes == 64);
+}
+
+hipError_t launch_qk_norm_rope(const void* q, const void* k, const void* wq, const void* wk,
+                               const void* positions, int pos_bytes, const float* cos_t,
+                               const float* sin_t, void* q_out, void* k_out, int64_t tokens,
+                               int hq, int hk, int dim, int64_t num_positions,
+                               int64_t max_positions, float eps, int dtype, hipStream_t stream) {
+  switch (dtype) {
+    case kF32: return launch_qk_norm_rope_t<float>(q, k, wq, wk, positions, pos_bytes, cos_t, sin_t, q_out, k_out, tokens, hq, hk, dim, num_positions, max_positions, eps, stream);
+    case kF16: return launch_qk_norm_rope_t<f16_t>(q, k, wq, wk, positions, pos_bytes, cos_t, sin_t, q_out, k_out, tokens, hq, hk, dim, num_positions, max_positions, eps, stream);
+    case kBF16: return launch_qk_norm_rope_t<bf16_t>(q, k, wq, wk, positions, pos_bytes, cos_t, sin_t, q_out, k_out, tokens, hq, hk, dim, num_positions, max_positions, eps, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 // -------------------------------------------------------------------- swiglu
 
 template <typename T>

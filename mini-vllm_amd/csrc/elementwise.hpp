@@ -12,6 +12,14 @@ hipError_t launch_rope(const void* x, const void* positions, int pos_bytes, cons
                        const float* sin_t, void* out, int64_t rows, int64_t heads, int dim,
                        int64_t num_positions, int64_t max_positions, int dtype,
                        hipStream_t stream);
+// Whether launch_qk_norm_rope serves this dtype and head dim (D / (16 / elt) lanes
+// per head a power of two from 2 to 64).
+bool qk_norm_rope_supported(int dtype, int head_dim);
+hipError_t launch_qk_norm_rope(const void* q, const void* k, const void* wq, const void* wk,
+                               const void* positions, int pos_bytes, const float* cos_t,
+                               const float* sin_t, void* q_out, void* k_out, int64_t tokens,
+                               int hq, int hk, int dim, int64_t num_positions,
+                               int64_t max_positions, float eps, int dtype, hipStream_t stream);
 hipError_t launch_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype,
                          hipStream_t stream);
 hipError_t launch_axpby(const float* x, float* y, float a, float b, int64_t n,

@@ -170,6 +170,8 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_swiglu.argtypes = [p, p, p, i64, i32, p]
     lib.mvllm_axpby.restype = ctypes.c_int
     lib.mvllm_axpby.argtypes = [p, p, f32, f32, i64, p]
+    lib.mvllm_qk_norm_rope.restype = ctypes.c_int
+    lib.mvllm_qk_norm_rope.argtypes = [p] * 7 + [i32, p, p, i64, i32, i32, i32, i64, i64, f32, i32, p]
     lib.mvllm_kv_write.restype = ctypes.c_int
     lib.mvllm_kv_write.argtypes = [p] * 7 + [i32] * 4 + [i64, i32, i32, p]
 
@@ -184,6 +186,7 @@ EXPORTED_SYMBOLS = (
     "mvllm_swiglu",
     "mvllm_axpby",
     "mvllm_kv_write",
+    "mvllm_qk_norm_rope",
 )
 
 
@@ -415,6 +418,52 @@ class HipExtension:
             k_scale.data_ptr() if fp8 else None, v_scale.data_ptr() if fp8 else None,
             key.data_ptr(), value.data_ptr(), slot_mapping.data_ptr(),
             key.shape[0], hk, d, bs, nb, src, pool, _stream(key.device)))
+
+    def qk_norm_rope_supported(self, dtype: torch.dtype, head_dim: int) -> bool:
+        """Whether the fused kernel serves this dtype / head dim (16-byte chunks per head
+        a power of two from 2 to 64)."""
+        n = {torch.float32: 4, torch.float16: 8, torch.bfloat16: 8}.get(dtype)
+        if n is None or head_dim % n:
+            return False
+        return head_dim // n in (2, 4, 8, 16, 32, 64)
+
+    def qk_norm_rope(self, q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor,
+                     k_weight: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor,
+                     sin: torch.Tensor, eps: float = 1e-6) -> tuple[torch.Tensor, torch.Tensor]:
+        """Per-head RMSNorm then RoPE of q ``T x H_q x D`` and k ``T x H_k x D`` in one
+        launch, bitwise equal to ``rope(rmsnorm(x, w))`` with this library's kernels."""
+        tensors = (q, k, q_weight, k_weight, positions, cos, sin)
+        if not all(t.is_cuda for t in tensors):
+            raise RuntimeError("qk_norm_rope: every tensor must be a CUDA tensor")
+        if q.dim() != 3 or k.dim() != 3 or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
+            raise RuntimeError(
+                f"qk_norm_rope: q must be T x H_q x D and k T x H_k x D, got {tuple(q.shape)} "
+                f"and {tuple(k.shape)}")
+        d = q.shape[2]
+        if q.dtype != k.dtype or q_weight.dtype != q.dtype or k_weight.dtype != q.dtype:
+            raise RuntimeError("qk_norm_rope: q, k and both weights must share a dtype")
+        if q_weight.shape != (d,) or k_weight.shape != (d,):
+            raise RuntimeError(f"qk_norm_rope: the weights must be [{d}]")
+        if cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.shape != sin.shape \
+                or cos.dim() != 2 or cos.shape[1] != d:
+            raise RuntimeError(f"qk_norm_rope: the cos/sin tables must be float32 max_pos x {d}")
+        if positions.dtype not in (torch.int32, torch.int64):
+            raise RuntimeError("qk_norm_rope: positions must be int32 or int64")
+        code = DTYPE_CODES.get(q.dtype)
+        if code is None or code == 3:
+            raise RuntimeError(f"qk_norm_rope: dtype {q.dtype} is not supported")
+        q, k = q.contiguous(), k.contiguous()
+        q_out, k_out = torch.empty_like(q), torch.empty_like(k)
+        if q.shape[0] == 0:
+            return q_out, k_out
+        positions = positions.contiguous()
+        self._check(self.lib.mvllm_qk_norm_rope(
+            q_out.data_ptr(), k_out.data_ptr(), q.data_ptr(), k.data_ptr(),
+            q_weight.contiguous().data_ptr(), k_weight.contiguous().data_ptr(),
+            positions.data_ptr(), positions.element_size(), cos.contiguous().data_ptr(),
+            sin.contiguous().data_ptr(), q.shape[0], q.shape[1], k.shape[1], d,
+            positions.numel(), cos.shape[0], float(eps), code, _stream(q.device)))
+        return q_out, k_out
 
     def swiglu(self, gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
         """``silu(gate) * up`` (reference csrc/swiglu.cu:87-120)."""

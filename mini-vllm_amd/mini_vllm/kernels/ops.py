@@ -10,11 +10,12 @@ engine and tests above it run unchanged:
                     context_lens, seq_lens, max_query_len, max_context_len,
                     scale=None, use_cuda=False)                        ops.py:200-254
 
-plus one op the reference performs inline in ``PagedKvPool.write``
-(block/kv_pool.py:116-155, two ``index_copy_`` calls per layer):
+plus two ops that fuse what the reference's caller does in several calls:
 
     kv_write(key_pool, value_pool, key, value, slot_mapping, use_cuda=False,
-             *, k_scale=None, v_scale=None)
+             *, k_scale=None, v_scale=None)    PagedKvPool.write: kv_pool.py:116-155
+    qk_norm_rope(q, k, q_weight, k_weight, positions, cos, sin, eps=1e-6,
+                 use_cuda=False)               qwen3_paged.py:73-78 (2 rmsnorm + 2 rope)
 
 The callee behind ``use_cuda=True`` is ``libminivllm_hip.so`` (HIP for gfx950).
 
@@ -45,6 +46,7 @@ __all__ = [
     "dispatch_report",
     "kv_write",
     "paged_attention",
+    "qk_norm_rope",
     "rmsnorm",
     "rope",
     "swiglu",
@@ -60,6 +62,7 @@ CUDA_KERNELS: dict[str, tuple[bool, str]] = {
     "flash_prefill": (False, "dense-cache prefill (not in this library)"),
     "paged_attention": (True, "csrc/paged_decode.hip + csrc/paged_prefill.hip"),
     "kv_write": (True, "csrc/kv_write.hip"),
+    "qk_norm_rope": (True, "csrc/elementwise.hip"),
 }
 
 # Kernels that exist but are deliberately not dispatched, with the reason.
@@ -123,6 +126,28 @@ def rope(x: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, sin: torch
     if _use_kernel("rope", use_cuda, x):
         return load_extension().rope(x, positions, cos, sin)
     return torch_path.apply_rope(x, positions, cos, sin)
+
+
+def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor,
+                 k_weight: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor,
+                 sin: torch.Tensor, eps: float = 1e-6,
+                 use_cuda: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """Qwen3's QK-norm then RoPE for ``q`` (T x H_q x D) and ``k`` (T x H_k x D): the
+    reference caller's ``rmsnorm`` + ``rope`` on each (qwen3_paged.py:73-78). Kernel:
+    ``csrc/elementwise.hip`` (one launch, bitwise equal to the unfused kernels); a head
+    dim the fused kernel does not serve runs the unfused kernels."""
+    if _use_kernel("qk_norm_rope", use_cuda, q):
+        ext = load_extension()
+        if ext.qk_norm_rope_supported(q.dtype, q.shape[-1]):
+            return ext.qk_norm_rope(q, k, q_weight, k_weight, positions, cos, sin, eps)
+        q = ext.rope(ext.rmsnorm(q, q_weight, eps).unsqueeze(0), positions, cos, sin).squeeze(0)
+        k = ext.rope(ext.rmsnorm(k, k_weight, eps).unsqueeze(0), positions, cos, sin).squeeze(0)
+        return q, k
+    q = torch_path.apply_rope(torch_path.rms_norm(q, q_weight, eps).unsqueeze(0), positions,
+                              cos, sin).squeeze(0)
+    k = torch_path.apply_rope(torch_path.rms_norm(k, k_weight, eps).unsqueeze(0), positions,
+                              cos, sin).squeeze(0)
+    return q, k
 
 
 def swiglu(gate: torch.Tensor, up: torch.Tensor, use_cuda: bool = False) -> torch.Tensor:

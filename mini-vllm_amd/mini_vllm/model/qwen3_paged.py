@@ -7,6 +7,9 @@ hot path has to serve unchanged:
     batch.positions -> write K/V to the pool -> paged attention -> wo -> residual ->
     mlp_norm -> gate/up -> SwiGLU -> down -> residual
 
+(QK-norm + RoPE of q and k run as one fused op, bitwise equal to the unfused
+rmsnorm/rope pair; the K/V write is one op for K and V.)
+
 and the forward returns one logits row per sequence (its last computed position),
 through the final norm and the tied embedding (reference qwen3_paged.py:211-228).
 Projections are plain ``x @ w.T`` matmuls (BLAS); every other op goes through
@@ -120,10 +123,8 @@ class Qwen3Paged:
         q = _linear(x, w["wq"]).view(t, c.num_attention_heads, c.head_dim)
         k = _linear(x, w["wk"]).view(t, c.num_key_value_heads, c.head_dim)
         v = _linear(x, w["wv"]).view(t, c.num_key_value_heads, c.head_dim)
-        q = ops.rmsnorm(q, w["q_norm"], c.rms_norm_eps, use_cuda=u)
-        k = ops.rmsnorm(k, w["k_norm"], c.rms_norm_eps, use_cuda=u)
-        q = ops.rope(q.unsqueeze(0), batch.positions, self.cos, self.sin, use_cuda=u).squeeze(0)
-        k = ops.rope(k.unsqueeze(0), batch.positions, self.cos, self.sin, use_cuda=u).squeeze(0)
+        q, k = ops.qk_norm_rope(q, k, w["q_norm"], w["k_norm"], batch.positions, self.cos,
+                                self.sin, c.rms_norm_eps, use_cuda=u)
         kv = self.manager.kv
         kv.write(layer, batch.slot_mapping, k, v, use_cuda=u)
         k_scale, v_scale = kv.layer_scales(layer)

@@ -225,3 +225,75 @@ def test_ops_route_elementwise_to_the_kernels(extension, device, monkeypatch):
 def test_hello_axpby(extension, device):
     x = torch.randn(1000, device=device)
     assert torch.allclose(extension.hello(x, 2.0, 3.0), 2.0 * x + 3.0)
+
+
+# ---------------------------------------------------------------- qk_norm_rope
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_dim", [32, 64, 128, 256])
+@pytest.mark.parametrize("pos_dtype", [torch.int64, torch.int32])
+def test_qk_norm_rope_is_bitwise_the_unfused_kernels(extension, device, dtype, head_dim, pos_dtype):
+    t, hq, hk = 37, 16, 8
+    q = (torch.randn(t, hq, head_dim) * 2).to(dtype).to(device)
+    k = (torch.randn(t, hk, head_dim) * 2).to(dtype).to(device)
+    wq = (torch.rand(head_dim) + 0.5).to(dtype).to(device)
+    wk = (torch.rand(head_dim) + 0.5).to(dtype).to(device)
+    cos, sin = (x.to(device) for x in torch_path.rope_tables(head_dim, 512))
+    pos = torch.randint(0, 512, (t,), dtype=pos_dtype).to(device)
+    assert extension.qk_norm_rope_supported(dtype, head_dim)
+    fq, fk = extension.qk_norm_rope(q, k, wq, wk, pos, cos, sin, 1e-6)
+    uq = extension.rope(extension.rmsnorm(q, wq, 1e-6).unsqueeze(0), pos, cos, sin).squeeze(0)
+    uk = extension.rope(extension.rmsnorm(k, wk, 1e-6).unsqueeze(0), pos, cos, sin).squeeze(0)
+    torch.cuda.synchronize()
+    for got, want in ((fq, uq), (fk, uk)):
+        bad = (got != want).nonzero()
+        assert bad.numel() == 0, [(tuple(i.tolist()), float(got[tuple(i)]), float(want[tuple(i)]))
+                                  for i in bad[:6]]
+
+
+def test_qk_norm_rope_against_the_oracle(extension, device):
+    """Within two storage ulps of the numpy oracle's rms_norm -> apply_rope (the norm's
+    fp32 sum order may move one rounding by one ulp)."""
+    t, hq, hk, d = 20, 4, 2, 128
+    q = (torch.randn(t, hq, d) * 2).to(torch.bfloat16)
+    k = (torch.randn(t, hk, d) * 2).to(torch.bfloat16)
+    wq = (torch.rand(d) + 0.5).to(torch.bfloat16)
+    wk = (torch.rand(d) + 0.5).to(torch.bfloat16)
+    cos, sin = torch_path.rope_tables(d, 64)
+    pos = torch.randint(0, 64, (t,))
+    fq, fk = extension.qk_norm_rope(q.to(device), k.to(device), wq.to(device), wk.to(device),
+                                    pos.to(device), cos.to(device), sin.to(device), 1e-6)
+    for x, w, got in ((q, wq, fq), (k, wk, fk)):
+        n = ew.rms_norm(x.float().numpy(), w.float().numpy(), 1e-6, "bf16")
+        want = ew.apply_rope(n[None], pos.numpy(), cos.numpy(), sin.numpy(), "bf16")[0]
+        err = np.abs(got.float().cpu().numpy() - want)
+        assert np.all(err <= np.maximum(np.abs(want), 2.0**-6) * 2.0**-7 * 2), err.max()
+
+
+def test_qk_norm_rope_broadcast_positions_and_nan_for_out_of_range(extension, device):
+    cos, sin = (x.to(device) for x in torch_path.rope_tables(64, 16))
+    q = torch.randn(6, 2, 64, device=device)
+    k = torch.randn(6, 1, 64, device=device)
+    w = torch.ones(64, device=device)
+    fq, fk = extension.qk_norm_rope(q, k, w, w, torch.tensor([3, 99, 5], device=device), cos, sin)
+    torch.cuda.synchronize()
+    assert torch.isnan(fq[1]).all() and torch.isnan(fq[4]).all() and torch.isnan(fk[1]).all()
+    assert torch.isfinite(fq[[0, 2, 3, 5]]).all()
+    uq = extension.rope(extension.rmsnorm(q, w).unsqueeze(0), torch.tensor([3, 99, 5], device=device), cos, sin)
+    assert torch.equal(fq[0], uq[0, 0]) and torch.equal(fq[5], uq[0, 5])
+
+
+def test_ops_qk_norm_rope_routes_and_refuses(extension, device):
+    cos, sin = (x.to(device) for x in torch_path.rope_tables(128, 16))
+    q = torch.randn(3, 4, 128, dtype=torch.bfloat16, device=device)
+    k = torch.randn(3, 2, 128, dtype=torch.bfloat16, device=device)
+    w = torch.ones(128, dtype=torch.bfloat16, device=device)
+    pos = torch.arange(3, device=device)
+    kq, kk = ops.qk_norm_rope(q, k, w, w, pos, cos, sin, use_cuda=True)
+    tq, tk = ops.qk_norm_rope(q, k, w, w, pos, cos, sin, use_cuda=False)
+    assert (kq.float() - tq.float()).abs().max() <= 2 ** -5
+    with pytest.raises(RuntimeError, match="share a dtype"):
+        extension.qk_norm_rope(q, k.float(), w, w, pos, cos, sin)
+    with pytest.raises(RuntimeError, match="T x H_q x D"):
+        extension.qk_norm_rope(q[0], k, w, w, pos, cos, sin)

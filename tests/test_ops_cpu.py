@@ -62,7 +62,7 @@ def test_dispatch_report_names_every_op():
         assert name in on and name in off
     assert "paged_attention    hip" in on
     assert "use_cuda is off" in off
-    assert set(ops.cuda_kernel_names()) == {"rmsnorm", "rope", "swiglu", "paged_attention", "kv_write"}
+    assert set(ops.cuda_kernel_names()) == {"rmsnorm", "rope", "swiglu", "paged_attention", "kv_write", "qk_norm_rope"}
 
 
 def test_dense_attention_torch_path_decode_and_causal():
