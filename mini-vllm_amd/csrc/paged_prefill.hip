@@ -83,6 +83,45 @@ template <> struct Mma<f16_t> {
   }
 };
 
+// Scheduling order for a block of N MFMAs fed by N LDS fragment reads issued kLook
+// ahead: kLook reads, then (MFMA, read) pairs, then the last kLook MFMAs.
+template <int kLook, int N>
+__device__ __forceinline__ void lds_mfma_pipeline() {
+  constexpr int kMfma = 0x008, kDsRead = 0x100;
+  __builtin_amdgcn_sched_group_barrier(kDsRead, kLook, 0);
+#pragma unroll
+  for (int i = 0; i < N - kLook; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+  }
+  __builtin_amdgcn_sched_group_barrier(kMfma, kLook, 0);
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)(p)));
+}
+
+// 16 bytes per lane from global memory (base + voff, base wave-uniform) straight into
+// LDS: lane i's bytes land at LDS address lds + 16 i. Written as asm so that the
+// compiler's wait-count pass neither tracks it nor drains it: the callers wait for it
+// explicitly (vmcnt) before the data is read. M0 carries the LDS address; nothing else
+// in the kernels that use this sets M0.
+__device__ __forceinline__ void copy_to_lds(const char* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base),
+               "s"(lds)
+               : "memory");
+}
+
+// A 16-byte global load the compiler does not track either: the value must not be used
+// before an explicit vmcnt wait that names it as an operand.
+__device__ __forceinline__ u32x4 load16_untracked(const char* p) {
+  u32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+
 // Eight consecutive pool elements -> eight 16-bit elements of the compute type.
 template <typename TQ, typename TKV> struct Stage;
 template <typename TQ> struct Stage<TQ, TQ> {
@@ -113,6 +152,7 @@ namespace {
 // nt tiles; context / len of sequence s. Every field is workgroup-uniform.
 struct Cursor {
   int u, s, c, q, t, nt, context, len;
+  int kvh;  // kv head of column c
 };
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -150,6 +190,7 @@ __device__ __forceinline__ void seek(Cursor& k, const PagedParams& p, const int*
   const int per_col = (uniform(pre[a + 1]) - base) / cols;
   int r = u - base;
   k.c = r / per_col;
+  k.kvh = k.c / (cols / p.hk);
   r -= k.c * per_col;
   k.q = 0;
   k.nt = prefill_item_tiles(k.context, k.len, 0);
@@ -159,6 +200,64 @@ __device__ __forceinline__ void seek(Cursor& k, const PagedParams& p, const int*
     k.nt = prefill_item_tiles(k.context, k.len, k.q);
   }
   k.t = r;
+}
+
+// This workgroup's work units [u0, u1) and the cursor at u0; false when it has none.
+// Every thread must call it: the stream schedule's prefix scan ends in a barrier.
+template <int kThreads>
+__device__ __forceinline__ bool prefill_work(const PagedParams& p, int cols, int share,
+                                             int* s_prefix, Cursor& cur, int& u0, int& u1) {
+  const int tid = threadIdx.x;
+  const int n = p.num_seqs;
+  if (p.pf_wgs > 0) {
+    // Prefix scan of the sequences' work units by wave 0: each lane sums a contiguous
+    // run, then a 64-lane inclusive scan.
+    if (tid < kWave) {
+      const int per = (n + kWave - 1) / kWave;
+      const int begin = min(tid * per, n);
+      const int end = min(begin + per, n);
+      int run = 0;
+      for (int s = begin; s < end; ++s) run += prefill_seq_units(p.context_lens[s], p.seq_lens[s], cols);
+      int incl = run;
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) {
+        const int other = __shfl_up(incl, off, kWave);
+        if (tid >= off) incl += other;
+      }
+      int acc = incl - run;
+      for (int s = begin; s < end; ++s) {
+        s_prefix[s] = acc;
+        acc += prefill_seq_units(p.context_lens[s], p.seq_lens[s], cols);
+      }
+      if (tid == kWave - 1) s_prefix[n] = incl;
+    }
+    __syncthreads();
+    const int total = uniform(s_prefix[n]);
+    if (blockIdx.x == 0) {
+      for (int s = tid; s <= n; s += kThreads) p.pf_prefix[s] = s_prefix[s];
+    }
+    u0 = static_cast<int>(share_begin(share, total, gridDim.x));
+    u1 = static_cast<int>(share_begin(share + 1, total, gridDim.x));
+    if (u0 >= u1) return false;  // whole workgroup: no barrier follows for it
+    seek(cur, p, s_prefix, n, cols, u0);
+    return true;
+  }
+  cur.s = blockIdx.y;
+  cur.len = sload(p.seq_lens + cur.s);
+  cur.context = sload(p.context_lens + cur.s);
+  if (cur.len <= 1) return false;  // a decode row: the decode kernel has it
+  const int qtiles = (cur.len + kPrefillQueryTile - 1) / kPrefillQueryTile;
+  // Query tile slowest and reversed: the longest tiles are dispatched first.
+  cur.q = static_cast<int>(gridDim.z) - 1 - static_cast<int>(blockIdx.z);
+  if (cur.q < 0 || cur.q >= qtiles) return false;
+  cur.c = blockIdx.x;
+  cur.kvh = cur.c / (cols / p.hk);
+  cur.nt = prefill_item_tiles(cur.context, cur.len, cur.q);
+  cur.t = 0;
+  cur.u = 0;
+  u0 = 0;
+  u1 = cur.nt;
+  return true;
 }
 
 }  // namespace
@@ -203,54 +302,8 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_kernel(const PagedPara
   // ---- this workgroup's units [u0, u1) and the cursor at u0.
   Cursor cur;
   int u0, u1;
-  if (stream) {
-    // Prefix scan of the sequences' work units by wave 0: each lane sums a contiguous
-    // run, then a 64-lane inclusive scan.
-    if (tid < kWave) {
-      const int per = (n + kWave - 1) / kWave;
-      const int begin = min(tid * per, n);
-      const int end = min(begin + per, n);
-      int run = 0;
-      for (int s = begin; s < end; ++s) run += prefill_seq_units(p.context_lens[s], p.seq_lens[s], cols);
-      int incl = run;
-#pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) {
-        const int other = __shfl_up(incl, off, kWave);
-        if (tid >= off) incl += other;
-      }
-      int acc = incl - run;
-      for (int s = begin; s < end; ++s) {
-        s_prefix[s] = acc;
-        acc += prefill_seq_units(p.context_lens[s], p.seq_lens[s], cols);
-      }
-      if (tid == kWave - 1) s_prefix[n] = incl;
-    }
-    __syncthreads();
-    const int total = uniform(s_prefix[n]);
-    if (blockIdx.x == 0) {
-      for (int s = tid; s <= n; s += kThreads) p.pf_prefix[s] = s_prefix[s];
-    }
-    u0 = static_cast<int>(share_begin(share, total, gridDim.x));
-    u1 = static_cast<int>(share_begin(share + 1, total, gridDim.x));
-    if (u0 >= u1) return;  // whole workgroup: no barrier follows for it
-    seek(cur, p, s_prefix, n, cols, u0);
-  } else {
-    cur.s = blockIdx.y;
-    cur.len = sload(p.seq_lens + cur.s);
-    cur.context = sload(p.context_lens + cur.s);
-    if (cur.len <= 1) return;  // a decode row: the decode kernel has it
-    const int qtiles = (cur.len + kPrefillQueryTile - 1) / kPrefillQueryTile;
-    // Query tile slowest and reversed: the longest tiles are dispatched first.
-    cur.q = static_cast<int>(gridDim.z) - 1 - static_cast<int>(blockIdx.z);
-    if (cur.q < 0 || cur.q >= qtiles) return;
-    cur.c = blockIdx.x;
-    cur.nt = prefill_item_tiles(cur.context, cur.len, cur.q);
-    cur.t = 0;
-    cur.u = 0;
-    u0 = 0;
-    u1 = cur.nt;
-  }
-  auto advance = [&](Cursor& k) {
+  if (!prefill_work<kThreads>(p, cols, share, s_prefix, cur, u0, u1)) return;
+  auto advance = [&](Cursor& k) __attribute__((always_inline)) {
     ++k.u;
     if (++k.t < k.nt) return;
     if (stream) {
@@ -274,17 +327,17 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_kernel(const PagedPara
   // ---- staging maps. K unit u: key (idx / (D/8)), dims 8 * (idx % (D/8)) .. +7, so 16
   // lanes read one 16-byte-chunked key row. V unit u: keys kVKeys * (idx % kVGroups)
   // .. + kVKeys - 1 at dims 8 * (idx / kVGroups) .. +7, transposed into V^T.
-  auto k_key = [&](int u) { return (tid + u * kThreads) / (D / 8); };
-  auto k_dim = [&](int u) { return ((tid + u * kThreads) % (D / 8)) * 8; };
-  auto v_grp = [&](int u) { return (tid + u * kThreads) % kVGroups; };
-  auto v_dim = [&](int u) { return ((tid + u * kThreads) / kVGroups) * 8; };
+  auto k_key = [&](int u) __attribute__((always_inline)) { return (tid + u * kThreads) / (D / 8); };
+  auto k_dim = [&](int u) __attribute__((always_inline)) { return ((tid + u * kThreads) % (D / 8)) * 8; };
+  auto v_grp = [&](int u) __attribute__((always_inline)) { return (tid + u * kThreads) % kVGroups; };
+  auto v_dim = [&](int u) __attribute__((always_inline)) { return ((tid + u * kThreads) / kVGroups) * 8; };
 
   // Two register sets, by the parity of the step they serve (a compile-time index, so
   // the sets stay in distinct registers): page ids are fetched four steps ahead and
   // K/V two steps ahead, each consumed two loop iterations after it was issued.
   int kpg[2][kKUnits], vpg[2][kVUnits][kVKeys];
   float ksc[2][kKUnits], vsc[2][kVUnits][kVKeys];
-  auto fetch_pages = [&](const Cursor& k, auto set) {
+  auto fetch_pages = [&](const Cursor& k, auto set) __attribute__((always_inline)) {
     constexpr int S = decltype(set)::value;
     const int32_t* table = p.block_tables + static_cast<int64_t>(k.s) * p.max_blocks;
     const int key0 = k.t * kTileKeys;
@@ -315,11 +368,11 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_kernel(const PagedPara
   // Byte offset of (page, key within the page, kv head, dims): the page's offset is one
   // 32 x 32 -> 64-bit multiply-add, the rest fits 32 bits (a page is far below 4 GiB).
   const uint32_t page_bytes32 = static_cast<uint32_t>(page_bytes);
-  auto pool_offset = [&](int page, int key, uint32_t inner) -> uint64_t {
+  auto pool_offset = [&](int page, int key, uint32_t inner) __attribute__((always_inline)) -> uint64_t {
     return static_cast<uint64_t>(static_cast<uint32_t>(page)) * page_bytes32 +
            (static_cast<uint32_t>(key & p.block_mask) * static_cast<uint32_t>(row_bytes) + inner);
   };
-  auto load_tile = [&](const Cursor& k, auto set) {
+  auto load_tile = [&](const Cursor& k, auto set) __attribute__((always_inline)) {
     constexpr int S = decltype(set)::value;
     const int key0 = k.t * kTileKeys;
     const int last = k.context - 1;
@@ -340,7 +393,7 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_kernel(const PagedPara
       }
     }
   };
-  auto store_tile = [&](int buf, auto set) {
+  auto store_tile = [&](int buf, auto set) __attribute__((always_inline)) {
     constexpr int S = decltype(set)::value;
 #pragma unroll
     for (int u = 0; u < kKUnits; ++u) {
@@ -377,7 +430,7 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_kernel(const PagedPara
   int row_base = 0, piece_t0 = 0, piece_u0 = 0;
   bool w_active = false, my_valid = false;
 
-  auto begin_piece = [&]() {
+  auto begin_piece = [&]() __attribute__((always_inline)) {
     const int offset = cur.context - cur.len;
     const int qb = cur.q * kPrefillQueryTile;
     w_first = qb + 32 * wq;
@@ -405,7 +458,7 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_kernel(const PagedPara
     }
   };
 
-  auto compute = [&](int buf) {
+  auto compute = [&](int buf) __attribute__((always_inline)) {
     const int key0 = cur.t * kTileKeys;
     if (!w_active || key0 >= w_kv_end) return;
     const uint16_t* kt = k_lds[buf];
@@ -501,7 +554,7 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_kernel(const PagedPara
     }
   };
 
-  auto end_piece = [&]() {
+  auto end_piece = [&]() __attribute__((always_inline)) {
     if (!w_active || !my_valid) return;
     const bool whole = piece_t0 == 0 && cur.t == cur.nt - 1;
     const int64_t slot = 2 * static_cast<int64_t>(share) + (piece_u0 == u0 ? 0 : 1);
@@ -570,7 +623,7 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_kernel(const PagedPara
     advance(fc);
     fetch_pages(fc, I1{});
   }
-  auto step_body = [&](int step, auto set) {
+  auto step_body = [&](int step, auto set) __attribute__((always_inline)) {
     if (step == u0 || cur.t == 0) begin_piece();
     store_tile(decltype(set)::value, set);
     __syncthreads();
@@ -591,6 +644,424 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_kernel(const PagedPara
     step_body(step, I0{});
     if (step + 1 < u1) step_body(step + 1, I1{});
   }
+}
+
+// ------------------------------------------------------------- direct-to-LDS staging
+//
+// 16-bit pools, D = 128, pages of at least 16 keys, scale > 0. Same work items,
+// schedules, wave roles, softmax and partial slots as paged_prefill_kernel; what
+// differs is how a tile reaches LDS and how the waits are placed:
+//  * a wave stages KW = 64 / waves consecutive keys of every tile; they lie in one
+//    page, so the page id is a scalar load and every pool address is a scalar page
+//    base plus a per-lane constant (the key's row within the page, clamped to the
+//    sequence's last key on its last tile).
+//  * K goes from HBM straight into LDS with global_load_lds_dwordx4 (1 KB = 4 keys per
+//    instruction, lane i to byte 16 i): no registers, no LDS store instructions. Rows
+//    are 256 B; chunk c of key r is stored at chunk c ^ (r & 7), so the eight keys an
+//    MFMA fragment read serves per LDS cycle fall in distinct banks.
+//  * V is loaded into registers two tiles ahead and written transposed (v_perm pairs)
+//    into V^T rows of 64 keys, ordered as the P^T operand lists them (per 16 keys:
+//    4h..4h+3 then 8+4h..8+4h+3 in chunk 2ks + h), so a PV operand is one
+//    ds_read_b128; the chunks of row d are XOR-swizzled by (d ^ d >> 3) & 7.
+//  * three K buffers, three V^T buffers and three V register sets, each a separate
+//    array picked at compile time (the loop is unrolled by three): the compiler's
+//    wait-count pass then sees that the copies in flight write other arrays than
+//    the ones a step reads and writes, and does not drain them before every LDS
+//    access. Tiles t + 1 and t + 2 are in flight while t is computed.
+//  * before a tile's barrier each wave waits (vmcnt) for its own copies of that tile
+//    only, so the barrier publishes the whole tile.
+template <typename TQ, int HS>
+__global__ __launch_bounds__(256 * HS) void paged_prefill_lds_kernel(const PagedParams p) {
+  constexpr int D = 128;
+  constexpr int kThreads = 256 * HS;
+  constexpr int kWaves = 4 * HS;
+  constexpr int HW = HS;                  // query heads per work item, one per wave set
+  constexpr int KW = kTileKeys / kWaves;  // keys of a tile staged by one wave (16 or 8)
+  constexpr int kCopies = KW / 4;         // 1 KB direct loads per wave per tile
+  constexpr int KV = KW / 4;              // V keys per lane: 4 key groups x 16 dim chunks
+  constexpr int kKSteps = D / 16;
+  constexpr int kDBlocks = D / 32;
+  constexpr int kRow = D * 2;             // bytes of one key row in LDS
+  constexpr int kTileBytes = kTileKeys * kRow;
+  constexpr int kVRow = kTileKeys * 2;    // bytes of one V^T row
+  // Copies one tile's stage issues per lane (K and V). Every vector-memory load in the
+  // tile loop is untracked asm and the stages are issued in tile order, so waiting down
+  // to kStageOps outstanding completes everything but the newest stage.
+  constexpr int kStageOps = 2 * kCopies;
+  static_assert(KV == 2 || KV == 4, "V staging map");
+  static_assert(kTileKeys == kPrefillKeyTile && 32 * 4 == kPrefillQueryTile, "tile sizes");
+
+  __shared__ __align__(16) char k_lds0[kTileBytes];
+  __shared__ __align__(16) char k_lds1[kTileBytes];
+  __shared__ __align__(16) char k_lds2[kTileBytes];
+  __shared__ __align__(16) char r_lds0[kTileBytes];
+  __shared__ __align__(16) char r_lds1[kTileBytes];
+  __shared__ __align__(16) char r_lds2[kTileBytes];
+  __shared__ __align__(1024) char v_lds[2][kTileBytes];  // row addresses keep bits 4..6 clear
+  __shared__ int s_prefix[kMaxStreamSeqs + 1];
+  auto k_arr = [&](auto slot) __attribute__((always_inline)) -> char* {
+    constexpr int X = decltype(slot)::value;
+    if constexpr (X == 0) return k_lds0; else if constexpr (X == 1) return k_lds1; else return k_lds2;
+  };
+  auto r_arr = [&](auto slot) __attribute__((always_inline)) -> char* {
+    constexpr int X = decltype(slot)::value;
+    if constexpr (X == 0) return r_lds0; else if constexpr (X == 1) return r_lds1; else return r_lds2;
+  };
+
+  const int tid = threadIdx.x;
+  const int wave = uniform(tid / kWave);
+  const int lane = tid % kWave;
+  const int l32 = lane & 31;
+  const int hsel = lane >> 5;
+  const int hs = wave / 4;  // head of the pair
+  const int wq = wave % 4;  // 32-position query block
+
+  const int n = p.num_seqs;
+  const int group = p.hq / p.hk;
+  const int chunks = group / HW;
+  const int cols = p.hk * chunks;
+  const bool stream = p.pf_wgs > 0;
+  const int share = xcd_share(blockIdx.x, gridDim.x);
+
+  Cursor cur;
+  int u0, u1;
+  if (!prefill_work<kThreads>(p, cols, share, s_prefix, cur, u0, u1)) return;
+  auto advance = [&](Cursor& k) __attribute__((always_inline)) {
+    ++k.u;
+    if (++k.t < k.nt) return;
+    if (stream) {
+      seek(k, p, s_prefix, n, cols, k.u);
+    } else {
+      k.t = 0;  // grid items are never walked past their end
+    }
+  };
+
+  const float score_c = p.scale * kLog2e;  // > 0 (the dispatcher's condition)
+
+  const char* kpool = static_cast<const char*>(p.k_pool);
+  const char* vpool = static_cast<const char*>(p.v_pool);
+  const uint32_t row_bytes = static_cast<uint32_t>(p.hk * D * 2);  // one token's K row
+  const uint64_t page_bytes = static_cast<uint64_t>(row_bytes) << p.block_shift;
+
+  // ---- per-lane constants of the staging and fragment maps.
+  // K copy j: LDS chunk (lane % 16) of key KW*wave + 4j + lane/16 holds logical chunk
+  // (lane % 16) ^ (key & 7) (KW * wave is a multiple of 8).
+  uint32_t k_src_chunk[kCopies];
+#pragma unroll
+  for (int j = 0; j < kCopies; ++j) k_src_chunk[j] = (((lane & 15) ^ ((4 * j + (lane >> 4)) & 7)) * 16);
+  // V transpose: lane reads keys KW*wave + KV*(lane/16) + j at dims 8*(lane%16) .. +7.
+  const int v_chunk = lane & 15;
+  const int v_key = KW * wave + KV * (lane >> 4);  // tile-local, a multiple of KV
+  // Its V^T destination: row 8*v_chunk + e, logical chunk 2*(key>>4) + ((key>>2)&1),
+  // element 4*((key>>3)&1) + (key&3); row d's chunks are swizzled by (d ^ d>>3) & 7,
+  // which for d = 8*v_chunk + e is (v_chunk ^ e) & 7.
+  const int vt_chunk = (2 * (v_key >> 4) + ((v_key >> 2) & 1)) ^ (v_chunk & 7);
+  const uint32_t vt_dst = static_cast<uint32_t>(8 * v_chunk * kVRow + (4 * ((v_key >> 3) & 1) + (v_key & 3)) * 2);
+  // Fragment reads. K (kb, ks): key 32kb + l32, chunk 2ks + hsel.
+  uint32_t k_rd[kKSteps];
+#pragma unroll
+  for (int ks = 0; ks < kKSteps; ++ks) k_rd[ks] = l32 * kRow + (((2 * ks + hsel) ^ (l32 & 7)) * 16);
+  // V^T (db, ks): row d = 32db + l32, chunk 2ks + hsel; (d ^ d>>3) & 7 =
+  // ((l32 ^ l32>>3) & 7) ^ 4(db & 1).
+  uint32_t v_rd[2][4];
+  {
+    const int f0 = (l32 ^ (l32 >> 3)) & 7;
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) v_rd[par][ks] = l32 * kVRow + ((((2 * ks + hsel) ^ f0 ^ (4 * par)) & 7) * 16);
+    }
+  }
+
+  // Page id of this wave's keys of tile k (clamped to the sequence's last key).
+  auto page_of = [&](const Cursor& k) __attribute__((always_inline)) -> int {
+    const int key0 = min(k.t * kTileKeys + KW * wave, k.context - 1);
+    // An s_load result is already uniform; not reading it through readfirstlane lets
+    // its wait fall at the first use, a step later.
+    return sload(p.block_tables + static_cast<int64_t>(k.s) * p.max_blocks + (key0 >> p.block_shift));
+  };
+  // Issue tile k's K and V copies into slot `slot`: K rows swizzled, V rows as they are.
+  // Per-lane source offsets of copy j within the wave's first key row: key 4j + lane/16.
+  uint32_t k_src_off[kCopies], v_src_off[kCopies];
+#pragma unroll
+  for (int j = 0; j < kCopies; ++j) {
+    k_src_off[j] = static_cast<uint32_t>(4 * j + (lane >> 4)) * row_bytes + k_src_chunk[j];
+    v_src_off[j] = static_cast<uint32_t>(4 * j + (lane >> 4)) * row_bytes + (lane & 15) * 16;
+  }
+  auto stage = [&](const Cursor& k, int page, auto slot) __attribute__((always_inline)) {
+    const uint32_t kdst = lds_address(k_arr(slot) + KW * wave * kRow);
+    const uint32_t rdst = lds_address(r_arr(slot) + KW * wave * kRow);
+    const int key0 = k.t * kTileKeys + KW * wave;
+    const int last = k.context - 1;
+    const uint64_t head = static_cast<uint64_t>(static_cast<uint32_t>(page)) * page_bytes +
+                          static_cast<uint32_t>(k.kvh * D * 2);
+    if (key0 + KW - 1 <= last) {
+      // The wave's keys are whole: their first row joins the scalar base.
+      const uint64_t base = head + static_cast<uint32_t>(key0 & p.block_mask) * row_bytes;
+#pragma unroll
+      for (int j = 0; j < kCopies; ++j) {
+        copy_to_lds(kpool + base, k_src_off[j], kdst + 4 * j * kRow);
+        copy_to_lds(vpool + base, v_src_off[j], rdst + 4 * j * kRow);
+      }
+    } else {
+      // The sequence's last tile: rows past the last key repeat it.
+#pragma unroll
+      for (int j = 0; j < kCopies; ++j) {
+        const uint32_t row = static_cast<uint32_t>(min(key0 + 4 * j + (lane >> 4), last) & p.block_mask) * row_bytes;
+        copy_to_lds(kpool + head, row + k_src_chunk[j], kdst + 4 * j * kRow);
+        copy_to_lds(vpool + head, row + (lane & 15) * 16, rdst + 4 * j * kRow);
+      }
+    }
+  };
+  // Transpose this wave's V rows of slot `slot` (tile-local keys v_key .. v_key + KV - 1,
+  // dims 8 * v_chunk .. +7 per lane) into V^T buffer `vbuf`. Row 8 * v_chunk + e holds
+  // them in chunk vt_chunk ^ e: a V^T address has the chunk in bits 4..6 and nothing
+  // else there, so the swizzle is one XOR of the lane's row-0 address.
+  typedef __attribute__((address_space(3))) uint32_t lds_u32;
+  typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
+  auto store_v = [&](auto slot, int vbuf) __attribute__((always_inline)) {
+    const char* raw = r_arr(slot) + v_key * kRow + v_chunk * 16;
+    u32x4 vr[KV];
+#pragma unroll
+    for (int j = 0; j < KV; ++j) vr[j] = *reinterpret_cast<const u32x4*>(raw + j * kRow);
+    const uint32_t row0 = lds_address(v_lds[vbuf]) + vt_dst + (vt_chunk & 7) * 16;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      // v_perm_b32 selector: low halves (bytes 0,1 of each) or high halves (2,3) of two
+      // dwords, the first operand's in the upper half of the result.
+      const uint32_t sel = (e & 1) == 0 ? 0x05040100u : 0x07060302u;
+      const uint32_t addr = (row0 ^ (e * 16)) + e * kVRow;
+      if constexpr (KV == 2) {
+        *reinterpret_cast<lds_u32*>(addr) = __builtin_amdgcn_perm(vr[1][e >> 1], vr[0][e >> 1], sel);
+      } else {
+        *reinterpret_cast<lds_u32x2*>(addr) = u32x2{__builtin_amdgcn_perm(vr[1][e >> 1], vr[0][e >> 1], sel),
+                                                    __builtin_amdgcn_perm(vr[3][e >> 1], vr[2][e >> 1], sel)};
+      }
+    }
+  };
+
+  // ---- per-item state of this wave (one head, 32 query positions).
+  u32x4 qop[kKSteps];
+  f32x16 o[kDBlocks];
+  float m_run = -INFINITY, l_run = 0.0f;
+  int w_kv_end = 0, w_kv_full = 0, my_local = 0, my_visible = 0, head0 = 0;
+  int row_base = 0, piece_t0 = 0, piece_u0 = 0;
+  bool w_active = false, my_valid = false;
+
+  auto begin_piece = [&]() __attribute__((always_inline)) {
+    const int offset = cur.context - cur.len;
+    const int w_first = cur.q * kPrefillQueryTile + 32 * wq;
+    w_active = w_first < cur.len;
+    w_kv_end = offset + min(w_first + 32, cur.len);
+    w_kv_full = offset + w_first + 1;
+    my_local = w_first + l32;
+    my_valid = my_local < cur.len;
+    my_visible = offset + my_local + 1;
+    row_base = sload(p.cu_seqlens_q + cur.s);
+    head0 = (cur.c / chunks) * group + (cur.c % chunks) * HW + hs;
+    piece_t0 = cur.t;
+    piece_u0 = cur.u;
+    const int local = min(my_local, cur.len - 1);
+    const int64_t qrow = static_cast<int64_t>(row_base + local) * p.hq + head0;
+    const char* qp = static_cast<const char*>(p.q) + (qrow * D + 8 * hsel) * 2;
+#pragma unroll
+    for (int ks = 0; ks < kKSteps; ++ks) qop[ks] = load16_untracked(qp + ks * 32);
+#pragma unroll
+    for (int db = 0; db < kDBlocks; ++db) o[db] = f32x16{};
+    m_run = -INFINITY;
+    l_run = 0.0f;
+  };
+
+  auto compute = [&](auto slot, int vbuf) __attribute__((always_inline)) {
+    const int key0 = cur.t * kTileKeys;
+    if (!w_active || key0 >= w_kv_end) return;
+    const char* kt = k_arr(slot);
+    const char* vt = v_lds[vbuf];
+
+    // Fragments are read kLook MFMAs ahead of their use, so several LDS reads are in
+    // flight behind each MFMA (two in flight left the MFMAs waiting on LDS latency).
+    constexpr int kLook = 4;
+    f32x16 s[2] = {f32x16{}, f32x16{}};
+    {
+      auto k_frag = [&](int i) __attribute__((always_inline)) {
+        return *reinterpret_cast<const u32x4*>(kt + (i & 1) * 32 * kRow + k_rd[i >> 1]);
+      };
+      u32x4 fa[kLook];
+#pragma unroll
+      for (int i = 0; i < kLook; ++i) fa[i] = k_frag(i);
+#pragma unroll
+      for (int i = 0; i < 2 * kKSteps; ++i) {
+        const u32x4 a = fa[i % kLook];
+        if (i + kLook < 2 * kKSteps) fa[i % kLook] = k_frag(i + kLook);
+        s[i & 1] = Mma<TQ>::run(a, qop[i >> 1], s[i & 1]);
+      }
+      // Keep that order: the scheduler otherwise reuses one fragment register and
+      // waits for each read right before its MFMA.
+      lds_mfma_pipeline<kLook, 2 * kKSteps>();
+    }
+
+    // Causal mask on tiles crossing the diagonal: score (kb, r) of this lane is key
+    // key0 + 4*hsel + 32kb + 8(r/4) + r%4, visible while below my_visible.
+    if (key0 + kTileKeys > w_kv_full) {
+      asm volatile("" ::: "memory");  // keep this a branch: most tiles need no mask
+      const int lim = my_valid ? my_visible - key0 - 4 * hsel : INT_MIN;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          if (kb * 32 + 8 * (r >> 2) + (r & 3) >= lim) s[kb][r] = -INFINITY;
+        }
+      }
+    }
+
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[kb][r]);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave)) * score_c;
+    if (__builtin_amdgcn_ballot_w64(tmax > m_run + kRescaleSlack) != 0) {
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = m_new == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < kDBlocks; ++db) o[db] *= alpha;
+    }
+    const float neg_mu = m_run == -INFINITY ? 0.0f : -m_run;
+    float psum = 0.0f;
+    u32x4 pop[4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        float pv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          pv[e] = __builtin_amdgcn_exp2f(fmaf(s[kb][8 * half + e], score_c, neg_mu));
+          psum += pv[e];
+        }
+        pop[2 * kb + half] = u32x4{Mma<TQ>::pack2(pv[0], pv[1]), Mma<TQ>::pack2(pv[2], pv[3]),
+                                   Mma<TQ>::pack2(pv[4], pv[5]), Mma<TQ>::pack2(pv[6], pv[7])};
+      }
+    }
+    l_run += psum;
+
+    // O^T += V^T P^T: operand (db, ks) is row 32db + l32, logical chunk 2ks + hsel.
+    {
+      auto v_frag = [&](int i) __attribute__((always_inline)) {
+        const int db = i & 3, ks = i >> 2;
+        return *reinterpret_cast<const u32x4*>(vt + db * 32 * kVRow + v_rd[db & 1][ks]);
+      };
+      u32x4 fa[kLook];
+#pragma unroll
+      for (int i = 0; i < kLook; ++i) fa[i] = v_frag(i);
+#pragma unroll
+      for (int i = 0; i < kDBlocks * 4; ++i) {
+        const u32x4 a = fa[i % kLook];
+        if (i + kLook < kDBlocks * 4) fa[i % kLook] = v_frag(i + kLook);
+        o[i & 3] = Mma<TQ>::run(a, pop[i >> 2], o[i & 3]);
+      }
+      lds_mfma_pipeline<kLook, kDBlocks * 4>();
+    }
+  };
+
+  auto end_piece = [&]() __attribute__((always_inline)) {
+    if (!w_active || !my_valid) return;
+    const bool whole = piece_t0 == 0 && cur.t == cur.nt - 1;
+    const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (whole) {
+      const int64_t orow = (static_cast<int64_t>(row_base + my_local) * p.hq + head0) * D;
+#pragma unroll
+      for (int db = 0; db < kDBlocks; ++db) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int d = db * 32 + 8 * j + 4 * hsel;
+          float r[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) r[i] = o[db][4 * j + i] * inv;
+          *reinterpret_cast<u32x2*>(static_cast<char*>(p.out) + (orow + d) * 2) =
+              u32x2{Mma<TQ>::pack2(r[0], r[1]), Mma<TQ>::pack2(r[2], r[3])};
+        }
+      }
+    } else {
+      const int64_t slot = 2 * static_cast<int64_t>(share) + (piece_u0 == u0 ? 0 : 1);
+      const int64_t prow = (slot * HW + hs) * kPrefillQueryTile + (my_local - cur.q * kPrefillQueryTile);
+      float* po = p.pf_o + prow * D;
+#pragma unroll
+      for (int db = 0; db < kDBlocks; ++db) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int d = db * 32 + 8 * j + 4 * hsel;
+          *reinterpret_cast<f32x4*>(po + d) = f32x4{o[db][4 * j] * inv, o[db][4 * j + 1] * inv,
+                                                    o[db][4 * j + 2] * inv, o[db][4 * j + 3] * inv};
+        }
+      }
+      if (hsel == 0) *reinterpret_cast<float2*>(p.pf_ml + prow * 2) = make_float2(m_run, l_tot);
+    }
+  };
+
+  // ---- the tile loop. Tile x uses slot (x - u0) % 3 of every staging array. Every
+  // step issues the copies and loads of tile step + 2 (past the end, of the last tile
+  // again, so that every step issues the same instructions and the wait counts hold).
+  // Page ids are fetched three steps before their tile is staged: pg[slot] holds the
+  // page of the next tile staged into `slot`.
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  Cursor lc = cur;
+  stage(lc, page_of(lc), I0{});
+  if (u0 + 1 < u1) advance(lc);
+  stage(lc, page_of(lc), I1{});
+  Cursor fc = lc;
+  int pg[3];
+  if (u0 + 2 < u1) advance(fc);
+  pg[2] = page_of(fc);
+  if (u0 + 3 < u1) advance(fc);
+  pg[0] = page_of(fc);
+  if (u0 + 4 < u1) advance(fc);
+  pg[1] = page_of(fc);
+
+  int vbuf = 0;  // V^T buffer of the current tile: alternates
+  auto step_body = [&](int step, auto slot) __attribute__((always_inline)) {
+    constexpr int X = decltype(slot)::value;
+    constexpr int Y = (X + 2) % 3;  // slot of tile step + 2
+    using IY = std::integral_constant<int, Y>;
+    // This wave's copies of the tile have landed (only the next tile's stage may still
+    // be in flight): transpose its V rows, then all waves meet.
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kStageOps) : "memory");
+    store_v(slot, vbuf);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // Query loads of a new item. They are younger than the next tile's stage, so
+    // waiting for them (before the first MFMA) completes that stage too.
+    const bool fresh = step == u0 || cur.t == 0;
+    if (fresh) begin_piece();
+    if (step + 2 < u1) advance(lc);
+    stage(lc, pg[Y], IY{});
+    if (step + 5 < u1) advance(fc);
+    pg[Y] = page_of(fc);
+    if (fresh) {
+      asm volatile("s_waitcnt vmcnt(%8)"
+                   : "+v"(qop[0]), "+v"(qop[1]), "+v"(qop[2]), "+v"(qop[3]), "+v"(qop[4]),
+                     "+v"(qop[5]), "+v"(qop[6]), "+v"(qop[7])
+                   : "n"(kStageOps)
+                   : "memory");
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    compute(slot, vbuf);
+    if (step + 1 == u1 || cur.t + 1 == cur.nt) end_piece();
+    if (step + 1 < u1) advance(cur);
+    vbuf ^= 1;
+  };
+  for (int step = u0; step < u1; step += 3) {
+    step_body(step, I0{});
+    if (step + 1 < u1) step_body(step + 1, I1{});
+    if (step + 2 < u1) step_body(step + 2, I2{});
+  }
+  // No copy may still be writing LDS when the workgroup ends.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 // Combine the pieces of every prefill item cut between stream workgroups. Workgroup b
@@ -723,8 +1194,43 @@ void launch_prefill_cfg(const PagedParams& p, int max_query_len, hipStream_t str
   }
 }
 
+// MVLLM_PREFILL_STAGING=1 forces the register-staged kernel where the direct-to-LDS one
+// would run (for measurement); read once per process.
+bool lds_staging_enabled() {
+  static const bool enabled = [] {
+    const char* v = std::getenv("MVLLM_PREFILL_STAGING");
+    return v == nullptr || std::atoi(v) != 1;
+  }();
+  return enabled;
+}
+
+template <typename TQ, int HS>
+void launch_prefill_lds(const PagedParams& p, int max_query_len, hipStream_t stream) {
+  if (p.pf_wgs > 0) {
+    paged_prefill_lds_kernel<TQ, HS><<<p.pf_wgs, 256 * HS, 0, stream>>>(p);
+    paged_prefill_merge_kernel<TQ, 128, HS><<<p.pf_wgs, 1024, 0, stream>>>(p);
+  } else {
+    const int cols = p.hk * (p.hq / p.hk / HS);
+    const int qtiles = (max_query_len + kPrefillQueryTile - 1) / kPrefillQueryTile;
+    const dim3 grid(cols, p.num_seqs, qtiles);
+    paged_prefill_lds_kernel<TQ, HS><<<grid, 256 * HS, 0, stream>>>(p);
+  }
+}
+
 template <typename TQ, typename TKV, int D>
 hipError_t launch_prefill_d(const PagedParams& p, int max_query_len, hipStream_t stream) {
+  // 16-bit pools at D = 128 with pages of >= 16 keys and a positive scale: K copied
+  // straight into LDS.
+  if constexpr (std::is_same_v<TQ, TKV> && D == 128) {
+    if (p.block_shift >= 4 && p.scale > 0.0f && lds_staging_enabled()) {
+      if (prefill_item_heads(p.hq / p.hk) == 1) {
+        launch_prefill_lds<TQ, 1>(p, max_query_len, stream);
+      } else {
+        launch_prefill_lds<TQ, 2>(p, max_query_len, stream);
+      }
+      return hipGetLastError();
+    }
+  }
   // Both heads of an even GQA group in one wave (HCW = 2) would share K/V fragments,
   // but needs ~450 registers: one wave per SIMD and no softmax/MFMA overlap. Measured
   // at config 3 it ran 25-40% slower than a wave per head, two waves per SIMD.
