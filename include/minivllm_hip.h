@@ -172,6 +172,37 @@ int mvllm_kv_write(void* key_pool, void* value_pool, float* k_scales, float* v_s
                    int32_t block_size, int64_t num_blocks, int32_t src_dtype,
                    int32_t pool_dtype, void* stream);
 
+/* Skinny projection y[m, n] = x[m, k] w[n, k]^T (torch's x @ w.T, no bias), fp32
+ * accumulation, for the few rows of a decode step: m <= 64, k a multiple of 64, x and w
+ * 16-byte aligned, dtype f16 or bf16; anything else returns MVLLM_ERR_UNSUPPORTED (the
+ * caller's BLAS serves it). Replaces the projection matmuls of the caller
+ * (model/qwen3_paged.py:71-95,110 -> model/basics.py linear -> torch.matmul); no
+ * counterpart in mini_vllm_C. The result is the fp32 sum rounded once, but summed in
+ * a different order than a BLAS would, so it may differ from torch in the last bit. */
+int mvllm_linear(void* y, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
+                 int32_t dtype, void* stream);
+
+/* The same projection over w = [w0; w1; w2] (n0 + n1 + n2 rows) with its columns written
+ * to three outputs: y0 [m, n0], y1 [m, n1], y2 [m, n2]; n0 and n1 multiples of 32. One
+ * launch for the q, k and v projections of model/qwen3_paged.py:71-73. */
+int mvllm_linear_split(void* y0, void* y1, void* y2, const void* x, const void* w, int64_t m,
+                       int64_t n0, int64_t n1, int64_t n2, int64_t k, int32_t dtype,
+                       void* stream);
+
+/* y = residual + x w^T with residual [m, n]: the projection rounded to the dtype, then
+ * the add rounded again, as the two torch ops round them (model/qwen3_paged.py:136-138,
+ * `h + wo(...)` and `h + down(...)`). */
+int mvllm_linear_residual(void* y, const void* x, const void* w, const void* residual, int64_t m,
+                          int64_t n, int64_t k, int32_t dtype, void* stream);
+
+/* y [m, n_out] = swiglu(x gate^T, x up^T) in one launch (model/qwen3_paged.py:110, the
+ * gate and up projections then ops.swiglu), with w_gate_up [2 n_out, k] holding gate and
+ * up rows interleaved in groups of 16 (rows 32j .. 32j+15: gate rows 16j .. 16j+15; the
+ * next 16: the same up rows); n_out a multiple of 16. Gate and up are rounded to the
+ * dtype before the SwiGLU, which rounds as mvllm_swiglu does. */
+int mvllm_linear_swiglu(void* y, const void* x, const void* w_gate_up, int64_t m, int64_t n_out,
+                        int64_t k, int32_t dtype, void* stream);
+
 /* y = a * x + b over n floats: the toolchain smoke test, replacing `mini_vllm_C.hello`
  * (csrc/bindings.cpp:8,37-42 -> csrc/hello.cu:11-21; mini_vllm/kernels/extension.py:349-353). */
 int mvllm_axpby(float* y, const float* x, float a, float b, int64_t n, void* stream);

@@ -16,6 +16,7 @@
 #include "common.hpp"
 #include "elementwise.hpp"
 #include "kv_write.hpp"
+#include "linear.hpp"
 #include "paged_attention.hpp"
 
 namespace {
@@ -236,7 +237,7 @@ extern "C" {
 
 const char* mvllm_last_error(void) { return g_error; }
 
-int mvllm_abi_version(void) { return 2; }
+int mvllm_abi_version(void) { return 3; }
 
 int mvllm_paged_attention_plan(int32_t num_tokens, int32_t num_seqs, int32_t num_q_heads,
                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
@@ -479,6 +480,95 @@ int mvllm_swiglu(void* out, const void* gate, const void* up, int64_t n, int32_t
   return hip_status(
       mvllm::launch_swiglu(gate, up, out, n, dtype, static_cast<hipStream_t>(stream)),
       "swiglu: launch");
+}
+
+// Shared checks of the skinny projection entries: dtype, sizes, pointers, alignment.
+int check_linear(const char* name, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
+                 int32_t dtype) {
+  if (dtype != mvllm::kF16 && dtype != mvllm::kBF16) {
+    return fail(MVLLM_ERR_UNSUPPORTED,
+                "%s: dtype code %d is not served; the skinny kernel takes fp16 or bf16", name,
+                dtype);
+  }
+  if (m < 0 || n < 0 || k < 0) return fail(MVLLM_ERR_INVALID, "%s: negative size", name);
+  if (x == nullptr || w == nullptr) return fail(MVLLM_ERR_INVALID, "%s: a required pointer is NULL", name);
+  if (!mvllm::skinny_linear_supported(dtype, m, n, k)) {
+    return fail(MVLLM_ERR_UNSUPPORTED,
+                "%s: shape M=%lld N=%lld K=%lld is not served; the skinny kernel takes at most "
+                "%lld rows and K a multiple of 64",
+                name, static_cast<long long>(m), static_cast<long long>(n), static_cast<long long>(k),
+                static_cast<long long>(mvllm::kSkinnyMaxRows));
+  }
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) % 16 != 0) {
+    return fail(MVLLM_ERR_INVALID, "%s: x and w must be 16-byte aligned", name);
+  }
+  return MVLLM_OK;
+}
+
+int mvllm_linear(void* y, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
+                 int32_t dtype, void* stream) {
+  g_error[0] = '\0';
+  if (m == 0 || n == 0) return MVLLM_OK;
+  int rc = check_linear("linear", x, w, m, n, k, dtype);
+  if (rc != MVLLM_OK) return rc;
+  if (y == nullptr) return fail(MVLLM_ERR_INVALID, "linear: a required pointer is NULL");
+  return hip_status(
+      mvllm::launch_skinny_linear(y, x, w, m, n, k, dtype, static_cast<hipStream_t>(stream)),
+      "linear: launch");
+}
+
+int mvllm_linear_split(void* y0, void* y1, void* y2, const void* x, const void* w, int64_t m,
+                       int64_t n0, int64_t n1, int64_t n2, int64_t k, int32_t dtype,
+                       void* stream) {
+  g_error[0] = '\0';
+  if (n0 < 0 || n1 < 0 || n2 < 0) return fail(MVLLM_ERR_INVALID, "linear_split: negative size");
+  if (n0 % 32 != 0 || n1 % 32 != 0) {
+    return fail(MVLLM_ERR_INVALID,
+                "linear_split: the first two column groups (%lld, %lld) must be multiples of 32",
+                static_cast<long long>(n0), static_cast<long long>(n1));
+  }
+  const int64_t n = n0 + n1 + n2;
+  if (m == 0 || n == 0) return MVLLM_OK;
+  int rc = check_linear("linear_split", x, w, m, n, k, dtype);
+  if (rc != MVLLM_OK) return rc;
+  if ((n0 > 0 && y0 == nullptr) || (n1 > 0 && y1 == nullptr) || (n2 > 0 && y2 == nullptr)) {
+    return fail(MVLLM_ERR_INVALID, "linear_split: an output of a non-empty column group is NULL");
+  }
+  return hip_status(mvllm::launch_skinny_linear_split(y0, y1, y2, x, w, m, n0, n1, n2, k, dtype,
+                                                      static_cast<hipStream_t>(stream)),
+                    "linear_split: launch");
+}
+
+int mvllm_linear_residual(void* y, const void* x, const void* w, const void* residual, int64_t m,
+                          int64_t n, int64_t k, int32_t dtype, void* stream) {
+  g_error[0] = '\0';
+  if (m == 0 || n == 0) return MVLLM_OK;
+  int rc = check_linear("linear_residual", x, w, m, n, k, dtype);
+  if (rc != MVLLM_OK) return rc;
+  if (y == nullptr || residual == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "linear_residual: a required pointer is NULL");
+  }
+  return hip_status(mvllm::launch_skinny_linear_residual(y, x, w, residual, m, n, k, dtype,
+                                                         static_cast<hipStream_t>(stream)),
+                    "linear_residual: launch");
+}
+
+int mvllm_linear_swiglu(void* y, const void* x, const void* w_gate_up, int64_t m, int64_t n_out,
+                        int64_t k, int32_t dtype, void* stream) {
+  g_error[0] = '\0';
+  if (n_out < 0) return fail(MVLLM_ERR_INVALID, "linear_swiglu: negative size");
+  if (n_out % 16 != 0) {
+    return fail(MVLLM_ERR_INVALID,
+                "linear_swiglu: %lld output columns; the gate/up interleave needs a multiple of 16",
+                static_cast<long long>(n_out));
+  }
+  if (m == 0 || n_out == 0) return MVLLM_OK;
+  int rc = check_linear("linear_swiglu", x, w_gate_up, m, 2 * n_out, k, dtype);
+  if (rc != MVLLM_OK) return rc;
+  if (y == nullptr) return fail(MVLLM_ERR_INVALID, "linear_swiglu: a required pointer is NULL");
+  return hip_status(mvllm::launch_skinny_linear_swiglu(y, x, w_gate_up, m, n_out, k, dtype,
+                                                       static_cast<hipStream_t>(stream)),
+                    "linear_swiglu: launch");
 }
 
 int mvllm_kv_write(void* key_pool, void* value_pool, float* k_scales, float* v_scales,

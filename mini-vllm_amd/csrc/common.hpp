@@ -151,6 +151,17 @@ template <> struct Chunk<fp8_t> {
   }
 };
 
+// SwiGLU of one element with the reference's rounding points (basics.py:39-41,
+// csrc/swiglu.cu:48-51): T(T(g * T(sigmoid(g))) * u), sigmoid = 1 / (1 + expf(-g)); the
+// caller rounds the returned product to T. Shared by the elementwise kernel and the
+// fused gate/up projection so both give the same bits.
+template <typename T>
+__device__ __forceinline__ float swiglu_one(float g, float u) {
+  const float sig = Elem<T>::round(1.0f / (1.0f + expf(-g)));
+  const float act = Elem<T>::round(__fmul_rn(g, sig));
+  return __fmul_rn(act, u);
+}
+
 // 16-byte global load / store through the vector memory path.
 __device__ __forceinline__ u32x4 load16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);

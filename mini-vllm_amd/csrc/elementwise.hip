@@ -487,12 +487,6 @@ hipError_t launch_qk_norm_rope(const void* q, const void* k, const void* wq, con
 
 // -------------------------------------------------------------------- swiglu
 
-template <typename T>
-__device__ __forceinline__ float swiglu_one(float g, float u) {
-  const float sig = Elem<T>::round(1.0f / (1.0f + expf(-g)));
-  const float act = Elem<T>::round(__fmul_rn(g, sig));
-  return __fmul_rn(act, u);
-}
 
 template <typename T>
 __device__ __forceinline__ u32x4 swiglu_chunk(const u32x4& gw, const u32x4& uw) {

@@ -57,9 +57,9 @@ HIP_FLAGS = [
 
 # Per-source extra flags. The elementwise kernels must round exactly where the
 # reference's PyTorch expressions round, so FMA contraction is off there.
-EXTRA_FLAGS = {"elementwise.hip": ["-ffp-contract=off"]}
+EXTRA_FLAGS = {"elementwise.hip": ["-ffp-contract=off"], "linear.hip": ["-ffp-contract=off"]}
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_CODES: dict[torch.dtype, int] = {
     torch.float32: 0,
@@ -174,6 +174,14 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_qk_norm_rope.argtypes = [p] * 7 + [i32, p, p, i64, i32, i32, i32, i64, i64, f32, i32, p]
     lib.mvllm_kv_write.restype = ctypes.c_int
     lib.mvllm_kv_write.argtypes = [p] * 7 + [i32] * 4 + [i64, i32, i32, p]
+    lib.mvllm_linear.restype = ctypes.c_int
+    lib.mvllm_linear.argtypes = [p, p, p, i64, i64, i64, i32, p]
+    lib.mvllm_linear_split.restype = ctypes.c_int
+    lib.mvllm_linear_split.argtypes = [p, p, p, p, p, i64, i64, i64, i64, i64, i32, p]
+    lib.mvllm_linear_residual.restype = ctypes.c_int
+    lib.mvllm_linear_residual.argtypes = [p, p, p, p, i64, i64, i64, i32, p]
+    lib.mvllm_linear_swiglu.restype = ctypes.c_int
+    lib.mvllm_linear_swiglu.argtypes = [p, p, p, i64, i64, i64, i32, p]
 
 
 EXPORTED_SYMBOLS = (
@@ -187,6 +195,10 @@ EXPORTED_SYMBOLS = (
     "mvllm_axpby",
     "mvllm_kv_write",
     "mvllm_qk_norm_rope",
+    "mvllm_linear",
+    "mvllm_linear_split",
+    "mvllm_linear_residual",
+    "mvllm_linear_swiglu",
 )
 
 
@@ -418,6 +430,72 @@ class HipExtension:
             k_scale.data_ptr() if fp8 else None, v_scale.data_ptr() if fp8 else None,
             key.data_ptr(), value.data_ptr(), slot_mapping.data_ptr(),
             key.shape[0], hk, d, bs, nb, src, pool, _stream(key.device)))
+
+    def linear_supported(self, x: torch.Tensor, w: torch.Tensor) -> bool:
+        """Whether the skinny projection kernel serves ``x @ w.T`` (at most 64 rows of
+        f16/bf16, K a multiple of 64, contiguous 16-byte-aligned operands)."""
+        if x.dim() != 2 or w.dim() != 2 or x.dtype != w.dtype:
+            return False
+        if x.dtype not in (torch.float16, torch.bfloat16) or not (x.is_cuda and w.is_cuda):
+            return False
+        m, k = x.shape
+        return (1 <= m <= 64 and w.shape[1] == k and k % 64 == 0 and x.is_contiguous()
+                and w.is_contiguous() and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0)
+
+    def linear(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        """``x @ w.T`` for ``x`` M x K (M <= 64) and ``w`` N x K: the skinny projection
+        kernel (fp32 accumulation, one rounding)."""
+        if not self.linear_supported(x, w):
+            raise RuntimeError(
+                f"linear: x {tuple(x.shape)} {x.dtype} @ w {tuple(w.shape)}.T is not served by the "
+                "skinny kernel (at most 64 contiguous f16/bf16 rows, K a multiple of 64)")
+        y = torch.empty((x.shape[0], w.shape[0]), dtype=x.dtype, device=x.device)
+        self._check(self.lib.mvllm_linear(y.data_ptr(), x.data_ptr(), w.data_ptr(), x.shape[0],
+                                          w.shape[0], x.shape[1], DTYPE_CODES[x.dtype],
+                                          _stream(x.device)))
+        return y
+
+    def linear_split(self, x: torch.Tensor, w: torch.Tensor,
+                     sizes: tuple[int, ...]) -> tuple[torch.Tensor, ...]:
+        """``x @ w.T`` with its columns cut into contiguous outputs of ``sizes`` (up to
+        three; all but the last multiples of 32): the q, k, v projections in one launch."""
+        if not self.linear_supported(x, w):
+            raise RuntimeError("linear_split: shapes not served by the skinny kernel")
+        if not 1 <= len(sizes) <= 3 or sum(sizes) != w.shape[0] or any(s % 32 for s in sizes[:-1]):
+            raise RuntimeError(f"linear_split: column groups {sizes} must sum to {w.shape[0]}, "
+                               "all but the last multiples of 32")
+        outs = [torch.empty((x.shape[0], n), dtype=x.dtype, device=x.device) for n in sizes]
+        ptrs = [o.data_ptr() for o in outs] + [0] * (3 - len(outs))
+        ns = list(sizes) + [0] * (3 - len(sizes))
+        self._check(self.lib.mvllm_linear_split(*ptrs, x.data_ptr(), w.data_ptr(), x.shape[0], *ns,
+                                                x.shape[1], DTYPE_CODES[x.dtype], _stream(x.device)))
+        return tuple(outs)
+
+    def linear_residual(self, x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+        """``residual + x @ w.T`` in one launch, each step rounded as torch rounds it."""
+        if not self.linear_supported(x, w):
+            raise RuntimeError("linear_residual: shapes not served by the skinny kernel")
+        n = w.shape[0]
+        if residual.shape != (x.shape[0], n) or residual.dtype != x.dtype or not residual.is_contiguous():
+            raise RuntimeError(f"linear_residual: residual must be a contiguous {x.shape[0]} x {n} "
+                               f"{x.dtype} tensor, got {tuple(residual.shape)} {residual.dtype}")
+        y = torch.empty_like(residual)
+        self._check(self.lib.mvllm_linear_residual(y.data_ptr(), x.data_ptr(), w.data_ptr(),
+                                                   residual.data_ptr(), x.shape[0], n, x.shape[1],
+                                                   DTYPE_CODES[x.dtype], _stream(x.device)))
+        return y
+
+    def linear_swiglu(self, x: torch.Tensor, w_gate_up: torch.Tensor) -> torch.Tensor:
+        """``swiglu(x @ gate.T, x @ up.T)`` in one launch, ``w_gate_up`` interleaving gate
+        and up rows in groups of 16 (``torch_path.interleave_gate_up``)."""
+        if not self.linear_supported(x, w_gate_up) or w_gate_up.shape[0] % 32:
+            raise RuntimeError("linear_swiglu: shapes not served by the skinny kernel")
+        n_out = w_gate_up.shape[0] // 2
+        y = torch.empty((x.shape[0], n_out), dtype=x.dtype, device=x.device)
+        self._check(self.lib.mvllm_linear_swiglu(y.data_ptr(), x.data_ptr(), w_gate_up.data_ptr(),
+                                                 x.shape[0], n_out, x.shape[1], DTYPE_CODES[x.dtype],
+                                                 _stream(x.device)))
+        return y
 
     def qk_norm_rope_supported(self, dtype: torch.dtype, head_dim: int) -> bool:
         """Whether the fused kernel serves this dtype / head dim (16-byte chunks per head

@@ -45,6 +45,10 @@ __all__ = [
     "cuda_kernel_names",
     "dispatch_report",
     "kv_write",
+    "linear",
+    "linear_residual",
+    "linear_split",
+    "linear_swiglu",
     "paged_attention",
     "qk_norm_rope",
     "rmsnorm",
@@ -63,6 +67,7 @@ CUDA_KERNELS: dict[str, tuple[bool, str]] = {
     "paged_attention": (True, "csrc/paged_decode.hip + csrc/paged_prefill.hip"),
     "kv_write": (True, "csrc/kv_write.hip"),
     "qk_norm_rope": (True, "csrc/elementwise.hip"),
+    "linear": (True, "csrc/linear.hip (at most 64 rows; vendor BLAS above)"),
 }
 
 # Kernels that exist but are deliberately not dispatched, with the reason.
@@ -155,6 +160,64 @@ def swiglu(gate: torch.Tensor, up: torch.Tensor, use_cuda: bool = False) -> torc
     if _use_kernel("swiglu", use_cuda, gate):
         return load_extension().swiglu(gate, up)
     return torch_path.silu(gate) * up
+
+
+def linear(x: torch.Tensor, w: torch.Tensor, use_cuda: bool = False) -> torch.Tensor:
+    """``x @ w.T`` (no bias), the projections of model/basics.py ``linear``.
+
+    Kernel: ``csrc/linear.hip`` for decode-sized ``x`` (at most 64 rows of f16/bf16, K a
+    multiple of 64): a weight-bandwidth-bound skinny GEMM. Larger ``x`` (prefill chunks)
+    is a real GEMM and goes to the vendor BLAS through torch, as every projection does
+    in the reference; that is a dispatch by size, both paths on the device.
+    """
+    if _use_kernel("linear", use_cuda, x):
+        ext = load_extension()
+        if ext.linear_supported(x, w):
+            return ext.linear(x, w)
+    return x @ w.t()
+
+
+def skinny(x: torch.Tensor, use_cuda: bool) -> bool:
+    """Whether the projections of ``x`` (decode-sized: at most 64 rows) run on the
+    skinny projection kernels, fused with their neighbours (``linear_split``,
+    ``linear_residual``, ``linear_swiglu``)."""
+    if not _use_kernel("linear", use_cuda, x):
+        return False
+    return (x.dim() == 2 and 1 <= x.shape[0] <= 64 and x.dtype in (torch.float16, torch.bfloat16)
+            and x.shape[1] % 64 == 0)
+
+
+def linear_split(x: torch.Tensor, w: torch.Tensor, sizes: tuple[int, ...],
+                 use_cuda: bool = False) -> tuple[torch.Tensor, ...]:
+    """``x @ w.T`` cut column-wise into contiguous tensors of ``sizes`` (the q, k, v
+    projections over their concatenated weights). Kernel: ``csrc/linear.hip``."""
+    if _use_kernel("linear", use_cuda, x):
+        ext = load_extension()
+        if ext.linear_supported(x, w) and all(s % 32 == 0 for s in sizes[:-1]) and len(sizes) <= 3:
+            return ext.linear_split(x, w, tuple(sizes))
+    return tuple(t.contiguous() for t in (x @ w.t()).split(list(sizes), dim=-1))
+
+
+def linear_residual(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor,
+                    use_cuda: bool = False) -> torch.Tensor:
+    """``residual + x @ w.T``, the projection and the add each rounded as torch rounds
+    them. Kernel: ``csrc/linear.hip``."""
+    if _use_kernel("linear", use_cuda, x):
+        ext = load_extension()
+        if ext.linear_supported(x, w) and residual.is_contiguous() and residual.dtype == x.dtype:
+            return ext.linear_residual(x, w, residual)
+    return residual + x @ w.t()
+
+
+def linear_swiglu(x: torch.Tensor, w_gate_up: torch.Tensor, use_cuda: bool = False) -> torch.Tensor:
+    """``swiglu(x @ gate.T, x @ up.T)`` over ``torch_path.interleave_gate_up(gate, up)``.
+    Kernel: ``csrc/linear.hip``."""
+    if _use_kernel("linear", use_cuda, x):
+        ext = load_extension()
+        if ext.linear_supported(x, w_gate_up) and w_gate_up.shape[0] % 32 == 0:
+            return ext.linear_swiglu(x, w_gate_up)
+    gate, up = torch_path.split_gate_up(x @ w_gate_up.t())
+    return swiglu(gate, up, use_cuda=use_cuda)
 
 
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,

@@ -8,12 +8,16 @@ hot path has to serve unchanged:
     mlp_norm -> gate/up -> SwiGLU -> down -> residual
 
 (QK-norm + RoPE of q and k run as one fused op, bitwise equal to the unfused
-rmsnorm/rope pair; the K/V write is one op for K and V.)
+rmsnorm/rope pair; the K/V write is one op for K and V. Decode-sized steps, at most
+64 rows, also fuse the projections: q/k/v as one launch, gate/up with SwiGLU as one,
+and the o and down projections with their residual add, each rounded as the unfused
+ops round.)
 
 and the forward returns one logits row per sequence (its last computed position),
 through the final norm and the tied embedding (reference qwen3_paged.py:211-228).
-Projections are plain ``x @ w.T`` matmuls (BLAS); every other op goes through
-``mini_vllm.kernels.ops`` with the model's ``use_cuda`` flag.
+Every op, projections included (``ops.linear``: the skinny kernel for decode-sized
+inputs, BLAS otherwise), goes through ``mini_vllm.kernels.ops`` with the model's
+``use_cuda`` flag.
 
 Weights are random (there is no checkpoint download here): N(0, 0.02) for matrices
 and the embedding, ones for norm weights, seeded.
@@ -94,10 +98,6 @@ def random_weights(config: ModelConfig, seed: int = 0, device: torch.device | st
     return w
 
 
-def _linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-    return x @ w.t()
-
-
 class Qwen3Paged:
     """``model(batch) -> N x V`` logits, one row per sequence of the ragged batch."""
 
@@ -114,15 +114,31 @@ class Qwen3Paged:
         self.layers = []
         for layer in range(config.num_hidden_layers):
             pre = f"layers.{layer}."
-            self.layers.append({k[len(pre):]: v for k, v in weights.items() if k.startswith(pre)})
+            w = {k[len(pre):]: v for k, v in weights.items() if k.startswith(pre)}
+            if use_cuda:
+                # Decode-sized steps run q/k/v as one projection over the concatenated
+                # weights (wq, wk, wv become row views of it: no second copy) and gate/up
+                # as one projection over their 16-row interleave, fused with SwiGLU.
+                w["wqkv"] = torch.cat((w["wq"], w["wk"], w["wv"]))
+                w["wq"], w["wk"], w["wv"] = w["wqkv"].split(
+                    [config.q_size, config.kv_size, config.kv_size])
+                if config.intermediate_size % 16 == 0:
+                    w["gate_up"] = torch_path.interleave_gate_up(w["gate"], w["up"])
+            self.layers.append(w)
 
-    def _attention(self, layer: int, w: dict, x: torch.Tensor, batch) -> torch.Tensor:
+    def _attention(self, layer: int, w: dict, x: torch.Tensor, batch, h: torch.Tensor,
+                   fused: bool) -> torch.Tensor:
+        """``h + attention(x)``: the residual add rides in the o-projection when fused."""
         c = self.config
         t = x.shape[0]
         u = self.use_cuda
-        q = _linear(x, w["wq"]).view(t, c.num_attention_heads, c.head_dim)
-        k = _linear(x, w["wk"]).view(t, c.num_key_value_heads, c.head_dim)
-        v = _linear(x, w["wv"]).view(t, c.num_key_value_heads, c.head_dim)
+        if fused:
+            q, k, v = ops.linear_split(x, w["wqkv"], (c.q_size, c.kv_size, c.kv_size), use_cuda=u)
+        else:
+            q, k, v = (ops.linear(x, w[n], use_cuda=u) for n in ("wq", "wk", "wv"))
+        q = q.view(t, c.num_attention_heads, c.head_dim)
+        k = k.view(t, c.num_key_value_heads, c.head_dim)
+        v = v.view(t, c.num_key_value_heads, c.head_dim)
         q, k = ops.qk_norm_rope(q, k, w["q_norm"], w["k_norm"], batch.positions, self.cos,
                                 self.sin, c.rms_norm_eps, use_cuda=u)
         kv = self.manager.kv
@@ -133,19 +149,27 @@ class Qwen3Paged:
             batch.cu_seqlens_q, batch.context_lens, batch.seq_lens, batch.max_query_len,
             batch.max_context_len, 1.0 / math.sqrt(c.head_dim), use_cuda=u,
             k_scale=k_scale, v_scale=v_scale)
-        return _linear(out.view(t, c.q_size), w["wo"])
+        if fused:
+            return ops.linear_residual(out.view(t, c.q_size), w["wo"], h, use_cuda=u)
+        return h + ops.linear(out.view(t, c.q_size), w["wo"], use_cuda=u)
 
     @torch.no_grad()
     def __call__(self, batch) -> torch.Tensor:
         c = self.config
         u = self.use_cuda
         h = self.weights["embedding"].index_select(0, batch.input_ids)
+        fused = u and ops.skinny(h, use_cuda=u)
         for layer, w in enumerate(self.layers):
             normed = ops.rmsnorm(h, w["attn_norm"], c.rms_norm_eps, use_cuda=u)
-            h = h + self._attention(layer, w, normed, batch)
+            h = self._attention(layer, w, normed, batch, h, fused)
             normed = ops.rmsnorm(h, w["mlp_norm"], c.rms_norm_eps, use_cuda=u)
-            gated = ops.swiglu(_linear(normed, w["gate"]), _linear(normed, w["up"]), use_cuda=u)
-            h = h + _linear(gated, w["down"])
+            if fused and "gate_up" in w:
+                h = ops.linear_residual(ops.linear_swiglu(normed, w["gate_up"], use_cuda=u),
+                                        w["down"], h, use_cuda=u)
+            else:
+                gated = ops.swiglu(ops.linear(normed, w["gate"], use_cuda=u),
+                                   ops.linear(normed, w["up"], use_cuda=u), use_cuda=u)
+                h = h + ops.linear(gated, w["down"], use_cuda=u)
         h = h.index_select(0, batch.last_row_indices)
         h = ops.rmsnorm(h, self.weights["final_norm"], c.rms_norm_eps, use_cuda=u)
-        return _linear(h, self.weights["embedding"])
+        return ops.linear(h, self.weights["embedding"], use_cuda=u)

@@ -187,3 +187,20 @@ def paged_attention_gathered(q: torch.Tensor, key_pool: torch.Tensor, value_pool
         attended = (probs @ v).reshape(num_q_heads, L, head_dim)
         out[start:end] = attended.permute(1, 0, 2)
     return out
+
+
+def interleave_gate_up(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """Gate and up projection weights (``I x E`` each) as one ``2I x E`` matrix with their
+    rows interleaved in groups of 16: rows 32j .. 32j+15 are gate rows 16j .. 16j+15, the
+    next 16 the same up rows (the layout of ``linear_swiglu``)."""
+    i, e = gate.shape
+    if up.shape != gate.shape or i % 16:
+        raise ValueError("gate and up must share a shape with a multiple of 16 rows")
+    return torch.stack((gate.view(i // 16, 16, e), up.view(i // 16, 16, e)), dim=1).reshape(2 * i, e)
+
+
+def split_gate_up(y: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Undo the column interleave of ``x @ interleave_gate_up(gate, up).T``."""
+    m, n = y.shape
+    v = y.view(m, n // 32, 2, 16)
+    return v[:, :, 0, :].reshape(m, n // 2), v[:, :, 1, :].reshape(m, n // 2)

@@ -62,7 +62,8 @@ def test_dispatch_report_names_every_op():
         assert name in on and name in off
     assert "paged_attention    hip" in on
     assert "use_cuda is off" in off
-    assert set(ops.cuda_kernel_names()) == {"rmsnorm", "rope", "swiglu", "paged_attention", "kv_write", "qk_norm_rope"}
+    assert set(ops.cuda_kernel_names()) == {"rmsnorm", "rope", "swiglu", "paged_attention", "kv_write",
+                                            "qk_norm_rope", "linear"}
 
 
 def test_dense_attention_torch_path_decode_and_causal():
@@ -74,3 +75,49 @@ def test_dense_attention_torch_path_decode_and_causal():
     ref = torch.softmax((q.reshape(2, 4, g, 1, 32) @ k.unsqueeze(2).transpose(-1, -2)) / 32**0.5, -1)
     ref = (ref @ v.unsqueeze(2)).reshape(2, 8, 1, 32)
     assert torch.allclose(out, ref, atol=1e-6)
+
+
+def test_linear_torch_path_is_x_matmul_w_transposed():
+    x = torch.randn(5, 64)
+    w = torch.randn(7, 64)
+    torch.testing.assert_close(ops.linear(x, w), x @ w.t())
+    with pytest.raises(RuntimeError, match="device tensors"):
+        ops.linear(x, w, use_cuda=True)
+
+
+def test_gate_up_interleave_layout():
+    """Rows 32j .. 32j+15 of the interleave are gate rows 16j .. 16j+15 and the next 16
+    the same up rows; split_gate_up undoes it on the product's columns."""
+    gate = torch.arange(48 * 3, dtype=torch.float32).view(48, 3)
+    up = -gate - 1
+    w = torch_path.interleave_gate_up(gate, up)
+    assert w.shape == (96, 3)
+    for j in range(3):
+        assert torch.equal(w[32 * j:32 * j + 16], gate[16 * j:16 * j + 16])
+        assert torch.equal(w[32 * j + 16:32 * j + 32], up[16 * j:16 * j + 16])
+    x = torch.randn(5, 3)
+    g, u = torch_path.split_gate_up(x @ w.t())
+    torch.testing.assert_close(g, x @ gate.t(), rtol=0, atol=0)
+    torch.testing.assert_close(u, x @ up.t(), rtol=0, atol=0)
+    with pytest.raises(ValueError):
+        torch_path.interleave_gate_up(gate[:40], up[:40])
+
+
+def test_fused_projection_torch_paths():
+    """The fused projections' PyTorch paths equal the unfused ops they replace."""
+    x = torch.randn(6, 64)
+    wq, wk, wv = torch.randn(64, 64), torch.randn(32, 64), torch.randn(32, 64)
+    q, k, v = ops.linear_split(x, torch.cat((wq, wk, wv)), (64, 32, 32))
+    for got, w in ((q, wq), (k, wk), (v, wv)):
+        assert got.is_contiguous()
+        torch.testing.assert_close(got, x @ w.t())
+    r = torch.randn(6, 48)
+    wo = torch.randn(48, 64)
+    torch.testing.assert_close(ops.linear_residual(x, wo, r), r + x @ wo.t())
+    gate, up = torch.randn(32, 64), torch.randn(32, 64)
+    torch.testing.assert_close(
+        ops.linear_swiglu(x, torch_path.interleave_gate_up(gate, up)),
+        ops.swiglu(x @ gate.t(), x @ up.t()))
+    assert not ops.skinny(x, use_cuda=False)
+    with pytest.raises(RuntimeError, match="device tensors"):
+        ops.linear_residual(x, wo, r, use_cuda=True)
