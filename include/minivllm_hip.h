@@ -172,17 +172,30 @@ int mvllm_kv_write(void* key_pool, void* value_pool, float* k_scales, float* v_s
                    int32_t block_size, int64_t num_blocks, int32_t src_dtype,
                    int32_t pool_dtype, void* stream);
 
-/* Skinny projection y[m, n] = x[m, k] w[n, k]^T (torch's x @ w.T, no bias), fp32
- * accumulation, for the few rows of a decode step: m <= 64, k a multiple of 64, x and w
- * 16-byte aligned, dtype f16 or bf16; anything else returns MVLLM_ERR_UNSUPPORTED (the
- * caller's BLAS serves it). Replaces the projection matmuls of the caller
- * (model/qwen3_paged.py:71-95,110 -> model/basics.py linear -> torch.matmul); no
- * counterpart in mini_vllm_C. The result is the fp32 sum rounded once, but summed in
- * a different order than a BLAS would, so it may differ from torch in the last bit. */
+/* The skinny projections below read W pre-shuffled into MFMA fragment order ("packed"),
+ * made once when the weights are loaded: for each tile of 32 rows (t) and each k-step of
+ * 16 elements (s), the 64 x 16 bytes one wave loads for one matrix-core operand lie
+ * contiguously, 16 bytes l = 32 h + r holding W[32 t + r][16 s + 8 h .. 16 s + 8 h + 7]
+ * at byte offset ((t * k/16 + s) * 64 + l) * 16; rows past n are zeros. The packed
+ * buffer holds ceil(n / 32) * 32 * k elements. This packs row-major W [n, k] (fp16 or
+ * bf16, k a multiple of 64, both buffers 16-byte aligned) on `stream`. No counterpart in
+ * the reference: its projections read torch's row-major weights (model/loader.py). */
+int mvllm_linear_pack(void* w_packed, const void* w, int64_t n, int64_t k, int32_t dtype,
+                      void* stream);
+
+/* Skinny projection y[m, n] = x[m, k] w[n, k]^T (torch's x @ w.T, no bias) with w packed
+ * as above, fp32 accumulation, for the few rows of a decode step: m <= 64, k a multiple
+ * of 64 up to 65536, x and w 16-byte aligned, dtype f16 or bf16; anything else returns
+ * MVLLM_ERR_UNSUPPORTED (the caller's BLAS serves it). Replaces the projection matmuls
+ * of the caller (model/qwen3_paged.py:71-95,110 -> model/basics.py linear ->
+ * torch.matmul); no counterpart in mini_vllm_C. The result is the fp32 sum rounded
+ * once, but summed in a different order than a BLAS would, so it may differ from torch
+ * in the last bit. The order depends on k alone, so the fused variants below equal
+ * this entry bit for bit. */
 int mvllm_linear(void* y, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
                  int32_t dtype, void* stream);
 
-/* The same projection over w = [w0; w1; w2] (n0 + n1 + n2 rows) with its columns written
+/* The same projection over w = pack([w0; w1; w2]) (n0 + n1 + n2 rows) with its columns written
  * to three outputs: y0 [m, n0], y1 [m, n1], y2 [m, n2]; n0 and n1 multiples of 32. One
  * launch for the q, k and v projections of model/qwen3_paged.py:71-73. */
 int mvllm_linear_split(void* y0, void* y1, void* y2, const void* x, const void* w, int64_t m,
@@ -199,7 +212,7 @@ int mvllm_linear_residual(void* y, const void* x, const void* w, const void* res
  * gate and up projections then ops.swiglu), with w_gate_up [2 n_out, k] holding gate and
  * up rows interleaved in groups of 16 (rows 32j .. 32j+15: gate rows 16j .. 16j+15; the
  * next 16: the same up rows); n_out a multiple of 16. Gate and up are rounded to the
- * dtype before the SwiGLU, which rounds as mvllm_swiglu does. */
+ * dtype before the SwiGLU, which rounds as mvllm_swiglu does; w_gate_up is packed. */
 int mvllm_linear_swiglu(void* y, const void* x, const void* w_gate_up, int64_t m, int64_t n_out,
                         int64_t k, int32_t dtype, void* stream);
 

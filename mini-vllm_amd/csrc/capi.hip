@@ -237,7 +237,7 @@ extern "C" {
 
 const char* mvllm_last_error(void) { return g_error; }
 
-int mvllm_abi_version(void) { return 3; }
+int mvllm_abi_version(void) { return 4; }
 
 int mvllm_paged_attention_plan(int32_t num_tokens, int32_t num_seqs, int32_t num_q_heads,
                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
@@ -495,14 +495,40 @@ int check_linear(const char* name, const void* x, const void* w, int64_t m, int6
   if (!mvllm::skinny_linear_supported(dtype, m, n, k)) {
     return fail(MVLLM_ERR_UNSUPPORTED,
                 "%s: shape M=%lld N=%lld K=%lld is not served; the skinny kernel takes at most "
-                "%lld rows and K a multiple of 64",
+                "%lld rows and K a multiple of 64 up to %lld",
                 name, static_cast<long long>(m), static_cast<long long>(n), static_cast<long long>(k),
-                static_cast<long long>(mvllm::kSkinnyMaxRows));
+                static_cast<long long>(mvllm::kSkinnyMaxRows),
+                static_cast<long long>(mvllm::kSkinnyMaxK));
   }
   if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) % 16 != 0) {
     return fail(MVLLM_ERR_INVALID, "%s: x and w must be 16-byte aligned", name);
   }
   return MVLLM_OK;
+}
+
+int mvllm_linear_pack(void* w_packed, const void* w, int64_t n, int64_t k, int32_t dtype,
+                      void* stream) {
+  g_error[0] = '\0';
+  if (dtype != mvllm::kF16 && dtype != mvllm::kBF16) {
+    return fail(MVLLM_ERR_UNSUPPORTED, "linear_pack: dtype code %d is not served (fp16 or bf16)",
+                dtype);
+  }
+  if (n < 0 || k < 0) return fail(MVLLM_ERR_INVALID, "linear_pack: negative size");
+  if (n == 0) return MVLLM_OK;
+  if (!mvllm::skinny_linear_supported(dtype, 1, n, k)) {
+    return fail(MVLLM_ERR_UNSUPPORTED,
+                "linear_pack: N=%lld K=%lld is not served; K must be a multiple of 64 up to %lld",
+                static_cast<long long>(n), static_cast<long long>(k),
+                static_cast<long long>(mvllm::kSkinnyMaxK));
+  }
+  if (w_packed == nullptr || w == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "linear_pack: a required pointer is NULL");
+  }
+  if ((reinterpret_cast<uintptr_t>(w_packed) | reinterpret_cast<uintptr_t>(w)) % 16 != 0) {
+    return fail(MVLLM_ERR_INVALID, "linear_pack: both buffers must be 16-byte aligned");
+  }
+  return hip_status(mvllm::launch_skinny_linear_pack(w_packed, w, n, k, static_cast<hipStream_t>(stream)),
+                    "linear_pack: launch");
 }
 
 int mvllm_linear(void* y, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
@@ -514,7 +540,7 @@ int mvllm_linear(void* y, const void* x, const void* w, int64_t m, int64_t n, in
   if (y == nullptr) return fail(MVLLM_ERR_INVALID, "linear: a required pointer is NULL");
   return hip_status(
       mvllm::launch_skinny_linear(y, x, w, m, n, k, dtype, static_cast<hipStream_t>(stream)),
-      "linear: launch");
+                    "linear: launch");
 }
 
 int mvllm_linear_split(void* y0, void* y1, void* y2, const void* x, const void* w, int64_t m,

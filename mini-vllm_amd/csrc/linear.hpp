@@ -8,9 +8,17 @@ namespace mvllm {
 
 // Most rows (x rows, i.e. tokens) one skinny projection serves.
 constexpr int64_t kSkinnyMaxRows = 64;
+// Longest reduction (x columns) it serves.
+constexpr int64_t kSkinnyMaxK = 65536;
 
-// Whether launch_skinny_linear serves y[m, n] = x[m, k] w[n, k]^T in this dtype.
+// Whether launch_skinny_linear (over packed W) serves y[m, n] = x[m, k] w[n, k]^T in this dtype.
 bool skinny_linear_supported(int dtype, int64_t m, int64_t n, int64_t k);
+
+// Elements of W [n, k] packed into the kernel's fragment order (n rounded up to 32).
+int64_t skinny_linear_packed_elements(int64_t n, int64_t k);
+// Packs row-major W [n, k] (16-bit elements) into that order (rows past n zero).
+hipError_t launch_skinny_linear_pack(void* w_packed, const void* w, int64_t n, int64_t k,
+                                     hipStream_t stream);
 
 // Epilogues of the skinny projection kernel.
 enum LinearEpilogue : int { kLinearPlain = 0, kLinearSplit = 1, kLinearResidual = 2, kLinearSwiglu = 3 };

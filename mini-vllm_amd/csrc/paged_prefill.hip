@@ -97,24 +97,7 @@ __device__ __forceinline__ void lds_mfma_pipeline() {
   __builtin_amdgcn_sched_group_barrier(kMfma, kLook, 0);
 }
 
-// LDS byte address of a pointer into a __shared__ array.
-__device__ __forceinline__ uint32_t lds_address(const void* p) {
-  return static_cast<uint32_t>(
-      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)(p)));
-}
-
-// 16 bytes per lane from global memory (base + voff, base wave-uniform) straight into
-// LDS: lane i's bytes land at LDS address lds + 16 i. Written as asm so that the
-// compiler's wait-count pass neither tracks it nor drains it: the callers wait for it
-// explicitly (vmcnt) before the data is read. M0 carries the LDS address; nothing else
-// in the kernels that use this sets M0.
-__device__ __forceinline__ void copy_to_lds(const char* base, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base),
-               "s"(lds)
-               : "memory");
-}
-
-// A 16-byte global load the compiler does not track either: the value must not be used
+// A 16-byte global load the compiler does not track (like copy_to_lds): the value must not be used
 // before an explicit vmcnt wait that names it as an operand.
 __device__ __forceinline__ u32x4 load16_untracked(const char* p) {
   u32x4 v;

@@ -59,7 +59,7 @@ HIP_FLAGS = [
 # reference's PyTorch expressions round, so FMA contraction is off there.
 EXTRA_FLAGS = {"elementwise.hip": ["-ffp-contract=off"], "linear.hip": ["-ffp-contract=off"]}
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_CODES: dict[torch.dtype, int] = {
     torch.float32: 0,
@@ -174,6 +174,8 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_qk_norm_rope.argtypes = [p] * 7 + [i32, p, p, i64, i32, i32, i32, i64, i64, f32, i32, p]
     lib.mvllm_kv_write.restype = ctypes.c_int
     lib.mvllm_kv_write.argtypes = [p] * 7 + [i32] * 4 + [i64, i32, i32, p]
+    lib.mvllm_linear_pack.restype = ctypes.c_int
+    lib.mvllm_linear_pack.argtypes = [p, p, i64, i64, i32, p]
     lib.mvllm_linear.restype = ctypes.c_int
     lib.mvllm_linear.argtypes = [p, p, p, i64, i64, i64, i32, p]
     lib.mvllm_linear_split.restype = ctypes.c_int
@@ -195,6 +197,7 @@ EXPORTED_SYMBOLS = (
     "mvllm_axpby",
     "mvllm_kv_write",
     "mvllm_qk_norm_rope",
+    "mvllm_linear_pack",
     "mvllm_linear",
     "mvllm_linear_split",
     "mvllm_linear_residual",
@@ -431,68 +434,96 @@ class HipExtension:
             key.data_ptr(), value.data_ptr(), slot_mapping.data_ptr(),
             key.shape[0], hk, d, bs, nb, src, pool, _stream(key.device)))
 
-    def linear_supported(self, x: torch.Tensor, w: torch.Tensor) -> bool:
-        """Whether the skinny projection kernel serves ``x @ w.T`` (at most 64 rows of
-        f16/bf16, K a multiple of 64, contiguous 16-byte-aligned operands)."""
-        if x.dim() != 2 or w.dim() != 2 or x.dtype != w.dtype:
+    @staticmethod
+    def linear_packable(w: torch.Tensor) -> bool:
+        """Whether ``linear_pack`` takes ``w``: a contiguous f16/bf16 N x K device matrix,
+        K a multiple of 64 up to 65536, 16-byte aligned."""
+        return (w.dim() == 2 and w.is_cuda and w.dtype in (torch.float16, torch.bfloat16)
+                and w.shape[1] % 64 == 0 and 64 <= w.shape[1] <= 65536 and w.is_contiguous()
+                and w.data_ptr() % 16 == 0)
+
+    def linear_pack(self, w: torch.Tensor) -> torch.Tensor:
+        """``w`` (N x K) pre-shuffled into the skinny kernels' fragment order: a flat
+        tensor of ceil(N / 32) * 32 * K elements (``torch_path.pack_fragments``)."""
+        if not self.linear_packable(w):
+            raise RuntimeError(f"linear_pack: w {tuple(w.shape)} {w.dtype} is not packable (a "
+                               "contiguous f16/bf16 device matrix, K a multiple of 64 up to 65536)")
+        n, k = w.shape
+        packed = torch.empty(-(-n // 32) * 32 * k, dtype=w.dtype, device=w.device)
+        self._check(self.lib.mvllm_linear_pack(packed.data_ptr(), w.data_ptr(), n, k,
+                                               DTYPE_CODES[w.dtype], _stream(w.device)))
+        return packed
+
+    def linear_supported(self, x: torch.Tensor, w_packed: torch.Tensor, n: int) -> bool:
+        """Whether the skinny projection kernel serves ``x`` @ W.T for W (n x K) packed as
+        ``w_packed``: at most 64 contiguous rows of f16/bf16, K a multiple of 64 up to
+        65536, 16-byte-aligned operands."""
+        if x.dim() != 2 or x.dtype != w_packed.dtype or not (x.is_cuda and w_packed.is_cuda):
             return False
-        if x.dtype not in (torch.float16, torch.bfloat16) or not (x.is_cuda and w.is_cuda):
+        if x.dtype not in (torch.float16, torch.bfloat16):
             return False
         m, k = x.shape
-        return (1 <= m <= 64 and w.shape[1] == k and k % 64 == 0 and x.is_contiguous()
-                and w.is_contiguous() and x.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0)
+        return (1 <= m <= 64 and k % 64 == 0 and k <= 65536 and n >= 1
+                and w_packed.numel() == -(-n // 32) * 32 * k and x.is_contiguous()
+                and w_packed.is_contiguous() and x.data_ptr() % 16 == 0
+                and w_packed.data_ptr() % 16 == 0)
 
-    def linear(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-        """``x @ w.T`` for ``x`` M x K (M <= 64) and ``w`` N x K: the skinny projection
-        kernel (fp32 accumulation, one rounding)."""
-        if not self.linear_supported(x, w):
+    def _require(self, name: str, x: torch.Tensor, w_packed: torch.Tensor, n: int) -> None:
+        if not self.linear_supported(x, w_packed, n):
             raise RuntimeError(
-                f"linear: x {tuple(x.shape)} {x.dtype} @ w {tuple(w.shape)}.T is not served by the "
-                "skinny kernel (at most 64 contiguous f16/bf16 rows, K a multiple of 64)")
-        y = torch.empty((x.shape[0], w.shape[0]), dtype=x.dtype, device=x.device)
-        self._check(self.lib.mvllm_linear(y.data_ptr(), x.data_ptr(), w.data_ptr(), x.shape[0],
-                                          w.shape[0], x.shape[1], DTYPE_CODES[x.dtype],
+                f"{name}: x {tuple(x.shape)} {x.dtype} with a packed {n}-row weight of "
+                f"{w_packed.numel()} {w_packed.dtype} elements is not served by the skinny kernel "
+                "(at most 64 contiguous f16/bf16 rows, K a multiple of 64 up to 65536)")
+
+    def linear(self, x: torch.Tensor, w_packed: torch.Tensor, n: int) -> torch.Tensor:
+        """``x @ W.T`` for ``x`` M x K (M <= 64) and W (n x K) packed: the skinny projection
+        kernel (fp32 accumulation, one rounding)."""
+        self._require("linear", x, w_packed, n)
+        y = torch.empty((x.shape[0], n), dtype=x.dtype, device=x.device)
+        self._check(self.lib.mvllm_linear(y.data_ptr(), x.data_ptr(), w_packed.data_ptr(),
+                                          x.shape[0], n, x.shape[1], DTYPE_CODES[x.dtype],
                                           _stream(x.device)))
         return y
 
-    def linear_split(self, x: torch.Tensor, w: torch.Tensor,
+    def linear_split(self, x: torch.Tensor, w_packed: torch.Tensor,
                      sizes: tuple[int, ...]) -> tuple[torch.Tensor, ...]:
-        """``x @ w.T`` with its columns cut into contiguous outputs of ``sizes`` (up to
+        """``x @ W.T`` with its columns cut into contiguous outputs of ``sizes`` (up to
         three; all but the last multiples of 32): the q, k, v projections in one launch."""
-        if not self.linear_supported(x, w):
-            raise RuntimeError("linear_split: shapes not served by the skinny kernel")
-        if not 1 <= len(sizes) <= 3 or sum(sizes) != w.shape[0] or any(s % 32 for s in sizes[:-1]):
-            raise RuntimeError(f"linear_split: column groups {sizes} must sum to {w.shape[0]}, "
-                               "all but the last multiples of 32")
+        if not 1 <= len(sizes) <= 3 or any(s % 32 for s in sizes[:-1]) or min(sizes) < 0:
+            raise RuntimeError(f"linear_split: column groups {sizes}: one to three, all but the "
+                               "last multiples of 32")
+        self._require("linear_split", x, w_packed, sum(sizes))
         outs = [torch.empty((x.shape[0], n), dtype=x.dtype, device=x.device) for n in sizes]
         ptrs = [o.data_ptr() for o in outs] + [0] * (3 - len(outs))
         ns = list(sizes) + [0] * (3 - len(sizes))
-        self._check(self.lib.mvllm_linear_split(*ptrs, x.data_ptr(), w.data_ptr(), x.shape[0], *ns,
-                                                x.shape[1], DTYPE_CODES[x.dtype], _stream(x.device)))
+        self._check(self.lib.mvllm_linear_split(*ptrs, x.data_ptr(), w_packed.data_ptr(),
+                                                x.shape[0], *ns, x.shape[1], DTYPE_CODES[x.dtype],
+                                                _stream(x.device)))
         return tuple(outs)
 
-    def linear_residual(self, x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
-        """``residual + x @ w.T`` in one launch, each step rounded as torch rounds it."""
-        if not self.linear_supported(x, w):
-            raise RuntimeError("linear_residual: shapes not served by the skinny kernel")
-        n = w.shape[0]
+    def linear_residual(self, x: torch.Tensor, w_packed: torch.Tensor,
+                        residual: torch.Tensor) -> torch.Tensor:
+        """``residual + x @ W.T`` in one launch (W has ``residual.shape[1]`` rows), each
+        step rounded as torch rounds it."""
+        n = residual.shape[-1]
+        self._require("linear_residual", x, w_packed, n)
         if residual.shape != (x.shape[0], n) or residual.dtype != x.dtype or not residual.is_contiguous():
             raise RuntimeError(f"linear_residual: residual must be a contiguous {x.shape[0]} x {n} "
                                f"{x.dtype} tensor, got {tuple(residual.shape)} {residual.dtype}")
         y = torch.empty_like(residual)
-        self._check(self.lib.mvllm_linear_residual(y.data_ptr(), x.data_ptr(), w.data_ptr(),
+        self._check(self.lib.mvllm_linear_residual(y.data_ptr(), x.data_ptr(), w_packed.data_ptr(),
                                                    residual.data_ptr(), x.shape[0], n, x.shape[1],
                                                    DTYPE_CODES[x.dtype], _stream(x.device)))
         return y
 
-    def linear_swiglu(self, x: torch.Tensor, w_gate_up: torch.Tensor) -> torch.Tensor:
-        """``swiglu(x @ gate.T, x @ up.T)`` in one launch, ``w_gate_up`` interleaving gate
-        and up rows in groups of 16 (``torch_path.interleave_gate_up``)."""
-        if not self.linear_supported(x, w_gate_up) or w_gate_up.shape[0] % 32:
-            raise RuntimeError("linear_swiglu: shapes not served by the skinny kernel")
-        n_out = w_gate_up.shape[0] // 2
+    def linear_swiglu(self, x: torch.Tensor, w_packed: torch.Tensor, n_out: int) -> torch.Tensor:
+        """``swiglu(x @ gate.T, x @ up.T)`` in one launch, over
+        ``torch_path.interleave_gate_up(gate, up)`` (2 n_out rows) packed."""
+        if n_out % 16:
+            raise RuntimeError(f"linear_swiglu: {n_out} output columns, not a multiple of 16")
+        self._require("linear_swiglu", x, w_packed, 2 * n_out)
         y = torch.empty((x.shape[0], n_out), dtype=x.dtype, device=x.device)
-        self._check(self.lib.mvllm_linear_swiglu(y.data_ptr(), x.data_ptr(), w_gate_up.data_ptr(),
+        self._check(self.lib.mvllm_linear_swiglu(y.data_ptr(), x.data_ptr(), w_packed.data_ptr(),
                                                  x.shape[0], n_out, x.shape[1], DTYPE_CODES[x.dtype],
                                                  _stream(x.device)))
         return y

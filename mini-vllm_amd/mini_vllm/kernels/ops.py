@@ -32,6 +32,7 @@ unimplemented kernels and use the PyTorch path, which :func:`dispatch_report` st
 from __future__ import annotations
 
 import math
+from dataclasses import dataclass
 
 import torch
 
@@ -45,10 +46,12 @@ __all__ = [
     "cuda_kernel_names",
     "dispatch_report",
     "kv_write",
+    "PackedWeight",
     "linear",
     "linear_residual",
     "linear_split",
     "linear_swiglu",
+    "pack_weight",
     "paged_attention",
     "qk_norm_rope",
     "rmsnorm",
@@ -162,19 +165,54 @@ def swiglu(gate: torch.Tensor, up: torch.Tensor, use_cuda: bool = False) -> torc
     return torch_path.silu(gate) * up
 
 
-def linear(x: torch.Tensor, w: torch.Tensor, use_cuda: bool = False) -> torch.Tensor:
+@dataclass(frozen=True)
+class PackedWeight:
+    """A projection weight W (N x K) as the skinny kernels read it: ``packed`` in their
+    fragment order (``torch_path.pack_fragments``; None where no kernel serves it), with
+    the row-major ``dense`` kept beside it for the BLAS (prefill-sized inputs) and the
+    PyTorch path. Made once, when the weights are loaded, by :func:`pack_weight`."""
+
+    dense: torch.Tensor
+    packed: torch.Tensor | None
+
+    @property
+    def shape(self) -> torch.Size:
+        return self.dense.shape
+
+
+def pack_weight(w: torch.Tensor, use_cuda: bool = False) -> PackedWeight:
+    """``w`` with its fragment-order copy for the skinny kernels (``csrc/linear.hip``,
+    ``mvllm_linear_pack``) when they serve it; the dense matrix alone otherwise."""
+    packed = None
+    if _use_kernel("linear", use_cuda, w):
+        ext = load_extension()
+        if ext.linear_packable(w):
+            packed = ext.linear_pack(w)
+    return PackedWeight(w, packed)
+
+
+def _skinny_ext(x: torch.Tensor, w: PackedWeight, n: int, use_cuda: bool):
+    """The extension when the skinny kernel serves ``x`` against ``w``, else None."""
+    if not _use_kernel("linear", use_cuda, x) or not isinstance(w, PackedWeight) or w.packed is None:
+        return None
+    ext = load_extension()
+    return ext if ext.linear_supported(x, w.packed, n) else None
+
+
+def linear(x: torch.Tensor, w: torch.Tensor | PackedWeight, use_cuda: bool = False) -> torch.Tensor:
     """``x @ w.T`` (no bias), the projections of model/basics.py ``linear``.
 
     Kernel: ``csrc/linear.hip`` for decode-sized ``x`` (at most 64 rows of f16/bf16, K a
-    multiple of 64): a weight-bandwidth-bound skinny GEMM. Larger ``x`` (prefill chunks)
-    is a real GEMM and goes to the vendor BLAS through torch, as every projection does
-    in the reference; that is a dispatch by size, both paths on the device.
+    multiple of 64) against a :class:`PackedWeight`: a weight-bandwidth-bound skinny
+    GEMM. Larger ``x`` (prefill chunks) is a real GEMM and goes to the vendor BLAS
+    through torch, as every projection does in the reference; that is a dispatch by
+    size, both paths on the device. A plain tensor weight always takes the BLAS.
     """
-    if _use_kernel("linear", use_cuda, x):
-        ext = load_extension()
-        if ext.linear_supported(x, w):
-            return ext.linear(x, w)
-    return x @ w.t()
+    dense = w.dense if isinstance(w, PackedWeight) else w
+    ext = _skinny_ext(x, w, dense.shape[0], use_cuda)
+    if ext is not None:
+        return ext.linear(x, w.packed, dense.shape[0])
+    return x @ dense.t()
 
 
 def skinny(x: torch.Tensor, use_cuda: bool) -> bool:
@@ -184,39 +222,37 @@ def skinny(x: torch.Tensor, use_cuda: bool) -> bool:
     if not _use_kernel("linear", use_cuda, x):
         return False
     return (x.dim() == 2 and 1 <= x.shape[0] <= 64 and x.dtype in (torch.float16, torch.bfloat16)
-            and x.shape[1] % 64 == 0)
+            and x.shape[1] % 64 == 0 and x.shape[1] <= 65536)
 
 
-def linear_split(x: torch.Tensor, w: torch.Tensor, sizes: tuple[int, ...],
+def linear_split(x: torch.Tensor, w: PackedWeight, sizes: tuple[int, ...],
                  use_cuda: bool = False) -> tuple[torch.Tensor, ...]:
     """``x @ w.T`` cut column-wise into contiguous tensors of ``sizes`` (the q, k, v
     projections over their concatenated weights). Kernel: ``csrc/linear.hip``."""
-    if _use_kernel("linear", use_cuda, x):
-        ext = load_extension()
-        if ext.linear_supported(x, w) and all(s % 32 == 0 for s in sizes[:-1]) and len(sizes) <= 3:
-            return ext.linear_split(x, w, tuple(sizes))
-    return tuple(t.contiguous() for t in (x @ w.t()).split(list(sizes), dim=-1))
+    ext = _skinny_ext(x, w, w.shape[0], use_cuda)
+    if ext is not None and len(sizes) <= 3 and all(s % 32 == 0 for s in sizes[:-1]):
+        return ext.linear_split(x, w.packed, tuple(sizes))
+    return tuple(t.contiguous() for t in (x @ w.dense.t()).split(list(sizes), dim=-1))
 
 
-def linear_residual(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor,
+def linear_residual(x: torch.Tensor, w: PackedWeight, residual: torch.Tensor,
                     use_cuda: bool = False) -> torch.Tensor:
     """``residual + x @ w.T``, the projection and the add each rounded as torch rounds
     them. Kernel: ``csrc/linear.hip``."""
-    if _use_kernel("linear", use_cuda, x):
-        ext = load_extension()
-        if ext.linear_supported(x, w) and residual.is_contiguous() and residual.dtype == x.dtype:
-            return ext.linear_residual(x, w, residual)
-    return residual + x @ w.t()
+    ext = _skinny_ext(x, w, w.shape[0], use_cuda)
+    if ext is not None and residual.is_contiguous() and residual.dtype == x.dtype:
+        return ext.linear_residual(x, w.packed, residual)
+    return residual + x @ w.dense.t()
 
 
-def linear_swiglu(x: torch.Tensor, w_gate_up: torch.Tensor, use_cuda: bool = False) -> torch.Tensor:
+def linear_swiglu(x: torch.Tensor, w_gate_up: PackedWeight, use_cuda: bool = False) -> torch.Tensor:
     """``swiglu(x @ gate.T, x @ up.T)`` over ``torch_path.interleave_gate_up(gate, up)``.
     Kernel: ``csrc/linear.hip``."""
-    if _use_kernel("linear", use_cuda, x):
-        ext = load_extension()
-        if ext.linear_supported(x, w_gate_up) and w_gate_up.shape[0] % 32 == 0:
-            return ext.linear_swiglu(x, w_gate_up)
-    gate, up = torch_path.split_gate_up(x @ w_gate_up.t())
+    n = w_gate_up.shape[0]
+    ext = _skinny_ext(x, w_gate_up, n, use_cuda)
+    if ext is not None and n % 32 == 0:
+        return ext.linear_swiglu(x, w_gate_up.packed, n // 2)
+    gate, up = torch_path.split_gate_up(x @ w_gate_up.dense.t())
     return swiglu(gate, up, use_cuda=use_cuda)
 
 

@@ -16,8 +16,8 @@ ops round.)
 and the forward returns one logits row per sequence (its last computed position),
 through the final norm and the tied embedding (reference qwen3_paged.py:211-228).
 Every op, projections included (``ops.linear``: the skinny kernel for decode-sized
-inputs, BLAS otherwise), goes through ``mini_vllm.kernels.ops`` with the model's
-``use_cuda`` flag.
+inputs over weights packed at load, BLAS otherwise), goes through
+``mini_vllm.kernels.ops`` with the model's ``use_cuda`` flag.
 
 Weights are random (there is no checkpoint download here): N(0, 0.02) for matrices
 and the embedding, ones for norm weights, seeded.
@@ -112,28 +112,40 @@ class Qwen3Paged:
                                                     config.max_position_embeddings,
                                                     config.rope_theta, device=device)
         self.layers = []
+        self.packed = []
         for layer in range(config.num_hidden_layers):
             pre = f"layers.{layer}."
             w = {k[len(pre):]: v for k, v in weights.items() if k.startswith(pre)}
+            p = {}
             if use_cuda:
                 # Decode-sized steps run q/k/v as one projection over the concatenated
-                # weights (wq, wk, wv become row views of it: no second copy) and gate/up
-                # as one projection over their 16-row interleave, fused with SwiGLU.
-                w["wqkv"] = torch.cat((w["wq"], w["wk"], w["wv"]))
-                w["wq"], w["wk"], w["wv"] = w["wqkv"].split(
+                # weights (wq, wk, wv become row views of it: no second dense copy) and
+                # gate/up as one projection over their 16-row interleave, fused with
+                # SwiGLU; each decode weight also kept in the skinny kernels' packed order.
+                wqkv = torch.cat((w["wq"], w["wk"], w["wv"]))
+                w["wq"], w["wk"], w["wv"] = wqkv.split(
                     [config.q_size, config.kv_size, config.kv_size])
+                p["qkv"] = ops.pack_weight(wqkv, use_cuda=True)
+                p["o"] = ops.pack_weight(w["wo"], use_cuda=True)
+                p["down"] = ops.pack_weight(w["down"], use_cuda=True)
                 if config.intermediate_size % 16 == 0:
-                    w["gate_up"] = torch_path.interleave_gate_up(w["gate"], w["up"])
+                    p["gate_up"] = ops.pack_weight(
+                        torch_path.interleave_gate_up(w["gate"], w["up"]), use_cuda=True)
             self.layers.append(w)
+            self.packed.append(p)
+        # The logits projection over the tied embedding (its rows are also the token
+        # lookup table, so the dense matrix stays).
+        self.lm_head = (ops.pack_weight(weights["embedding"], use_cuda=True) if use_cuda
+                        else weights["embedding"])
 
-    def _attention(self, layer: int, w: dict, x: torch.Tensor, batch, h: torch.Tensor,
+    def _attention(self, layer: int, w: dict, p: dict, x: torch.Tensor, batch, h: torch.Tensor,
                    fused: bool) -> torch.Tensor:
         """``h + attention(x)``: the residual add rides in the o-projection when fused."""
         c = self.config
         t = x.shape[0]
         u = self.use_cuda
         if fused:
-            q, k, v = ops.linear_split(x, w["wqkv"], (c.q_size, c.kv_size, c.kv_size), use_cuda=u)
+            q, k, v = ops.linear_split(x, p["qkv"], (c.q_size, c.kv_size, c.kv_size), use_cuda=u)
         else:
             q, k, v = (ops.linear(x, w[n], use_cuda=u) for n in ("wq", "wk", "wv"))
         q = q.view(t, c.num_attention_heads, c.head_dim)
@@ -150,7 +162,7 @@ class Qwen3Paged:
             batch.max_context_len, 1.0 / math.sqrt(c.head_dim), use_cuda=u,
             k_scale=k_scale, v_scale=v_scale)
         if fused:
-            return ops.linear_residual(out.view(t, c.q_size), w["wo"], h, use_cuda=u)
+            return ops.linear_residual(out.view(t, c.q_size), p["o"], h, use_cuda=u)
         return h + ops.linear(out.view(t, c.q_size), w["wo"], use_cuda=u)
 
     @torch.no_grad()
@@ -159,17 +171,17 @@ class Qwen3Paged:
         u = self.use_cuda
         h = self.weights["embedding"].index_select(0, batch.input_ids)
         fused = u and ops.skinny(h, use_cuda=u)
-        for layer, w in enumerate(self.layers):
+        for layer, (w, p) in enumerate(zip(self.layers, self.packed)):
             normed = ops.rmsnorm(h, w["attn_norm"], c.rms_norm_eps, use_cuda=u)
-            h = self._attention(layer, w, normed, batch, h, fused)
+            h = self._attention(layer, w, p, normed, batch, h, fused)
             normed = ops.rmsnorm(h, w["mlp_norm"], c.rms_norm_eps, use_cuda=u)
-            if fused and "gate_up" in w:
-                h = ops.linear_residual(ops.linear_swiglu(normed, w["gate_up"], use_cuda=u),
-                                        w["down"], h, use_cuda=u)
+            if fused and "gate_up" in p:
+                h = ops.linear_residual(ops.linear_swiglu(normed, p["gate_up"], use_cuda=u),
+                                        p["down"], h, use_cuda=u)
             else:
                 gated = ops.swiglu(ops.linear(normed, w["gate"], use_cuda=u),
                                    ops.linear(normed, w["up"], use_cuda=u), use_cuda=u)
                 h = h + ops.linear(gated, w["down"], use_cuda=u)
         h = h.index_select(0, batch.last_row_indices)
         h = ops.rmsnorm(h, self.weights["final_norm"], c.rms_norm_eps, use_cuda=u)
-        return ops.linear(h, self.weights["embedding"], use_cuda=u)
+        return ops.linear(h, self.lm_head, use_cuda=u)

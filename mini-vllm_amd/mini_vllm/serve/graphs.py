@@ -83,7 +83,8 @@ class _Captured:
         self.dyn32.copy_(self.host32, non_blocking=True)
 
     def capture(self) -> None:
-        # Warm up on a side stream (allocator pools, BLAS handles), then capture.
+        # Warm up on a side stream (allocator pools, BLAS handles, the kernels' per-stream
+        # workspaces), then capture on that same stream.
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -91,7 +92,7 @@ class _Captured:
                 self.model(self.batch)
         torch.cuda.current_stream().wait_stream(side)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
+        with torch.cuda.graph(self.graph, stream=side):
             self.logits = self.model(self.batch)
 
 

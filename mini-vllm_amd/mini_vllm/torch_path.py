@@ -204,3 +204,17 @@ def split_gate_up(y: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     m, n = y.shape
     v = y.view(m, n // 32, 2, 16)
     return v[:, :, 0, :].reshape(m, n // 2), v[:, :, 1, :].reshape(m, n // 2)
+
+
+def pack_fragments(w: torch.Tensor) -> torch.Tensor:
+    """``w`` (N x K) in the skinny projection kernels' fragment order, flat: rows padded
+    with zeros to a multiple of 32, then for each 32-row tile t and 16-element k-step s
+    the 64 eight-element pieces l = 32 h + r holding w[32 t + r, 16 s + 8 h : 16 s + 8 h + 8]
+    (piece index (t * K/16 + s) * 64 + l). The layout of ``mvllm_linear_pack``."""
+    n, k = w.shape
+    if k % 16:
+        raise ValueError("K must be a multiple of 16")
+    tiles = -(-n // 32)
+    padded = torch.zeros((tiles * 32, k), dtype=w.dtype, device=w.device)
+    padded[:n] = w
+    return padded.view(tiles, 32, k // 16, 2, 8).permute(0, 2, 3, 1, 4).reshape(-1)

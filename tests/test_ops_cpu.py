@@ -107,17 +107,36 @@ def test_fused_projection_torch_paths():
     """The fused projections' PyTorch paths equal the unfused ops they replace."""
     x = torch.randn(6, 64)
     wq, wk, wv = torch.randn(64, 64), torch.randn(32, 64), torch.randn(32, 64)
-    q, k, v = ops.linear_split(x, torch.cat((wq, wk, wv)), (64, 32, 32))
+    qkv = ops.pack_weight(torch.cat((wq, wk, wv)))
+    assert qkv.packed is None  # no kernel on the PyTorch path
+    q, k, v = ops.linear_split(x, qkv, (64, 32, 32))
     for got, w in ((q, wq), (k, wk), (v, wv)):
         assert got.is_contiguous()
         torch.testing.assert_close(got, x @ w.t())
     r = torch.randn(6, 48)
-    wo = torch.randn(48, 64)
-    torch.testing.assert_close(ops.linear_residual(x, wo, r), r + x @ wo.t())
+    wo = ops.pack_weight(torch.randn(48, 64))
+    torch.testing.assert_close(ops.linear_residual(x, wo, r), r + x @ wo.dense.t())
+    torch.testing.assert_close(ops.linear(x, wo), x @ wo.dense.t())
     gate, up = torch.randn(32, 64), torch.randn(32, 64)
     torch.testing.assert_close(
-        ops.linear_swiglu(x, torch_path.interleave_gate_up(gate, up)),
+        ops.linear_swiglu(x, ops.pack_weight(torch_path.interleave_gate_up(gate, up))),
         ops.swiglu(x @ gate.t(), x @ up.t()))
     assert not ops.skinny(x, use_cuda=False)
     with pytest.raises(RuntimeError, match="device tensors"):
         ops.linear_residual(x, wo, r, use_cuda=True)
+
+
+def test_pack_fragments_layout():
+    """Piece (t, s, l = 32 h + r) of the packed weight is w[32 t + r, 16 s + 8 h : +8],
+    rows past N zero; checked element by element against that definition."""
+    n, k = 45, 64
+    w = torch.arange(n * k, dtype=torch.float32).view(n, k) + 1
+    packed = torch_path.pack_fragments(w).view(-1, 64, 8)
+    steps = k // 16
+    assert packed.shape[0] == 2 * steps
+    for t in range(2):
+        for s in range(steps):
+            for l in range(64):
+                r, h = 32 * t + l % 32, l // 32
+                want = w[r, 16 * s + 8 * h:16 * s + 8 * h + 8] if r < n else torch.zeros(8)
+                assert torch.equal(packed[t * steps + s, l], want), (t, s, l)
