@@ -185,6 +185,44 @@ def run_kv_write(steps: int = 20) -> dict:
     return out
 
 
+def run_dense(steps: int = 20) -> dict:
+    """Dense-cache attention (``ops.attention``, reference csrc/decode_attention.cu and
+    csrc/flash_prefill.cu) on the paged kernels, against the PyTorch path on the same
+    GPU: decode B=32 x S=2048 read in place from a cache preallocated for 4096 positions
+    (bytes = K + V read once), and causal prefill B=8 x L=512 after a 512-token prefix
+    (FLOPs over visible pairs), bf16, 16q/8kv heads, D=128."""
+    from mini_vllm.kernels import ops
+
+    bf = torch.bfloat16
+    out = {}
+    b, hq, hk, d = 32, 16, 8, 128
+    S, s_max = 2048, 4096
+    caches = [(torch.randn(b, hk, s_max, d, device="cuda", dtype=bf)[:, :, :S],
+               torch.randn(b, hk, s_max, d, device="cuda", dtype=bf)[:, :, :S]) for _ in range(3)]
+    q = torch.randn(b, hq, 1, d, device="cuda", dtype=bf)
+    nbytes = 2 * b * hk * S * d * 2
+    for name, use in (("kernel", True), ("torch", False)):
+        ms = time_steps(lambda i: ops.attention(q, *caches[i % 3], use_cuda=use), steps, 3)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[f"decode_{name}"] = {"us": round(ms * 1e3, 1), "gbs": round(gbs, 1)}
+        log(f"dense decode ({name}): {ms * 1e3:.1f} us, {gbs:.0f} GB/s")
+    del caches
+    b, L, S = 8, 512, 1024
+    qs = [torch.randn(b, hq, L, d, device="cuda", dtype=bf) for _ in range(3)]
+    kv = [(torch.randn(b, hk, S, d, device="cuda", dtype=bf),
+           torch.randn(b, hk, S, d, device="cuda", dtype=bf)) for _ in range(3)]
+    flops = 4 * hq * d * b * (L * (S - L) + L * (L + 1) // 2)
+    for name, use in (("kernel", True), ("torch", False)):
+        ms = time_steps(lambda i: ops.attention(qs[i % 3], *kv[i % 3], mask="causal", use_cuda=use),
+                        steps, 3)
+        tf = flops / (ms * 1e-3) / 1e12
+        out[f"prefill_{name}"] = {"us": round(ms * 1e3, 1), "tflops": round(tf, 1)}
+        log(f"dense prefill ({name}): {ms * 1e3:.1f} us, {tf:.0f} TFLOP/s")
+    del qs, kv
+    torch.cuda.empty_cache()
+    return out
+
+
 def run_elementwise(steps: int = 20) -> dict:
     """RMSNorm (E=1024 and per-head D=128), RoPE (16 heads x 128) and SwiGLU (I=3072)
     at bf16 on ~256 MB operands, three rotated copies each so every call reads HBM.
@@ -283,10 +321,10 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--copies", type=int, default=3, help="rotated pool copies (defeat the MALL)")
     parser.add_argument("--skip-extras", action="store_true", help="headline config 2 only")
-    parser.add_argument("--extras", default="3,4,5,ew,kv,copy",
+    parser.add_argument("--extras", default="3,4,5,ew,kv,dense,copy",
                         help="comma list of extras to run: 3 (prefill), 4 (fp8 decode), "
                              "5 (engine), 5fp8 (engine, fp8 KV cache), ew (elementwise "
-                             "kernels), kv (KV write), copy")
+                             "kernels), kv (KV write), dense (dense-cache attention), copy")
     parser.add_argument("--no-cpu", action="store_true")
     args = parser.parse_args()
 
@@ -348,6 +386,8 @@ def main() -> int:
         extras["elementwise"] = run_elementwise()
     if "kv" in wanted:
         extras["kv_write"] = run_kv_write()
+    if "dense" in wanted:
+        extras["dense_attention"] = run_dense()
     if "5" in wanted:
         log("config 5: Qwen3-0.6B-shaped engine, 256 requests x 256 tokens")
         extras["config5_engine"] = run_engine()

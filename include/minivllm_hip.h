@@ -105,6 +105,44 @@ int mvllm_paged_attention(void* out, const void* q, const void* key_pool,
                           int32_t kv_dtype, void* workspace, uint64_t workspace_bytes,
                           void* stream);
 
+/* Dense-cache attention: q, out [batch, query_len, num_q_heads, head_dim] contiguous
+ * (token-major); k, v [batch, num_kv_heads, kv_len, head_dim] read through the given
+ * element strides (head_dim contiguous), so a cache narrowed out of a larger buffer is
+ * read in place. Query i (0-based) attends keys 0 .. kv_len - query_len + i: with
+ * query_len == 1 every cached key (the reference's decode_attention), with query_len > 1
+ * causally with offset kv_len - query_len (its flash_prefill). Replaces
+ * `mini_vllm_C.decode_attention` / `mini_vllm_C.flash_prefill` (csrc/bindings.cpp:15-22,
+ * 65-80 -> csrc/decode_attention.cu:360-435, csrc/flash_prefill.cu:282-355), called from
+ * mini_vllm/kernels/ops.py:166-197. Served by the paged kernels over virtual 16-position
+ * pages of the cache. Requires: dtype f32/f16/bf16 for q, k, v and out; head_dim in {32,
+ * 64, 128, 256}; num_q_heads a multiple of num_kv_heads; kv_len >= query_len >= 1; k and
+ * v sharing strides, the position and head strides multiples of 16 bytes, the batch
+ * stride a multiple of the position stride, pointers 16-byte aligned (otherwise
+ * MVLLM_ERR_UNSUPPORTED: the caller's PyTorch path serves it). The workspace (size from
+ * mvllm_dense_attention_plan, 256-byte aligned, contents need not be initialised) holds
+ * the virtual page tables and the split partials; calls that overlap on one workspace
+ * race. */
+typedef struct mvllm_dense_args {
+  void* out;
+  const void* q;
+  const void* k;
+  const void* v;
+  int64_t k_stride_batch, k_stride_head, k_stride_pos; /* elements */
+  int64_t v_stride_batch, v_stride_head, v_stride_pos;
+  int32_t batch;
+  int32_t num_q_heads;
+  int32_t num_kv_heads;
+  int32_t query_len;
+  int32_t kv_len;
+  int32_t head_dim;
+  float scale;
+  int32_t dtype;
+} mvllm_dense_args;
+
+int mvllm_dense_attention_plan(const mvllm_dense_args* args, uint64_t* workspace_bytes);
+int mvllm_dense_attention(const mvllm_dense_args* args, void* workspace, uint64_t workspace_bytes,
+                          void* stream);
+
 /* RMSNorm over the last dimension: out = T(w * T(x * rsqrt(mean(x^2) + eps))), the sum
  * of squares in fp32. x, out [rows, dim]; weight [dim]; all of `dtype` (f32/f16/bf16).
  * Replaces `mini_vllm_C.rmsnorm` (csrc/bindings.cpp:9,44-49 -> csrc/rmsnorm.cu:121-169),

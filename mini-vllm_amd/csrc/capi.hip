@@ -14,6 +14,7 @@
 
 #include "../../include/minivllm_hip.h"
 #include "common.hpp"
+#include "dense.hpp"
 #include "elementwise.hpp"
 #include "kv_write.hpp"
 #include "linear.hpp"
@@ -231,6 +232,120 @@ void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, i
   }
 }
 
+// Fills the plan's schedule fields and workspace pointers into `p` and launches the
+// decode and prefill kernels the plan names (shared by the paged and dense entries).
+int launch_planned(const Plan& plan, mvllm::PagedParams& p, void* workspace, int32_t q_dtype,
+                   int32_t kv_dtype, int32_t head_dim, int32_t max_query_len, hipStream_t s,
+                   const char* name) {
+  p.stream_wgs = plan.pub.decode_mode == MVLLM_DECODE_STREAM ? plan.pub.decode_workgroups : 0;
+  p.split_tokens = plan.pub.split_tokens > 0 ? plan.pub.split_tokens : mvllm::kMaxSplitTokens;
+  p.max_splits = plan.max_splits;
+  p.by_row = plan.pub.decode_mode == MVLLM_DECODE_BY_ROW ? 1 : 0;
+  if (plan.pub.workspace_bytes > 0) {
+    char* ws = static_cast<char*>(workspace);
+    if (plan.pub.decode_mode == MVLLM_DECODE_STREAM) p.seq_prefix = reinterpret_cast<int*>(ws);
+    p.part_o = reinterpret_cast<float*>(ws + plan.off_o);
+    p.part_ml = reinterpret_cast<float*>(ws + plan.off_ml);
+    if (plan.pub.prefill_workgroups > 0) {
+      p.pf_wgs = plan.pub.prefill_workgroups;
+      p.pf_prefix = reinterpret_cast<int*>(ws + plan.off_pf);
+      p.pf_o = reinterpret_cast<float*>(ws + plan.off_pf_o);
+      p.pf_ml = reinterpret_cast<float*>(ws + plan.off_pf_ml);
+    }
+  }
+  if (plan.pub.decode_mode != MVLLM_DECODE_NONE) {
+    const int rc = hip_status(mvllm::launch_paged_decode(p, q_dtype, kv_dtype, head_dim, s),
+                              name);
+    if (rc != MVLLM_OK) return rc;
+  }
+  if (plan.pub.prefill_mfma) {
+    const int rc = hip_status(
+        mvllm::launch_paged_prefill(p, q_dtype, kv_dtype, head_dim, max_query_len, s), name);
+    if (rc != MVLLM_OK) return rc;
+  }
+  return MVLLM_OK;
+}
+
+// The dense entries' checks, their virtual-page geometry and their workspace layout:
+// the metadata first, then the paged plan's workspace.
+struct DensePlan {
+  Plan plan;
+  int max_blocks = 0;
+  int64_t slots_per_batch = 0;
+  uint64_t off_tables = 0, off_cu = 0, off_ctx = 0, off_len = 0, off_paged = 0;
+  uint64_t bytes = 0;
+};
+
+int dense_plan(const mvllm_dense_args* a, DensePlan& d) {
+  if (a == nullptr) return fail(MVLLM_ERR_INVALID, "dense_attention: args is NULL");
+  const char* name = a->query_len == 1 ? "decode_attention" : "flash_prefill";
+  if (a->dtype != mvllm::kF32 && a->dtype != mvllm::kF16 && a->dtype != mvllm::kBF16) {
+    return fail(MVLLM_ERR_INVALID,
+                "%s: dtype code %d is not supported (float32, float16, bfloat16); float64 is not "
+                "supported, the accumulators here are fp32",
+                name, a->dtype);
+  }
+  if (a->batch < 0 || a->num_q_heads <= 0 || a->num_kv_heads <= 0 ||
+      a->num_q_heads % a->num_kv_heads != 0) {
+    return fail(MVLLM_ERR_INVALID, "%s: H_q (%d) must be a multiple of H_k (%d)", name,
+                a->num_q_heads, a->num_kv_heads);
+  }
+  if (a->kv_len <= 0) {
+    return fail(MVLLM_ERR_INVALID,
+                "%s: the cache is empty, so there is nothing to attend to; softmax over zero "
+                "keys is undefined",
+                name);
+  }
+  if (a->query_len <= 0 || a->kv_len < a->query_len) {
+    return fail(MVLLM_ERR_INVALID,
+                "%s: %d queries against %d keys; this kernel masks causally, which needs S >= L "
+                "> 0",
+                name, a->query_len, a->kv_len);
+  }
+  const int esize = a->dtype == mvllm::kF32 ? 4 : 2;
+  const int64_t sp = a->k_stride_pos, sh = a->k_stride_head, sb = a->k_stride_batch;
+  if (sp != a->v_stride_pos || sh != a->v_stride_head || (a->batch > 1 && sb != a->v_stride_batch)) {
+    return fail(MVLLM_ERR_UNSUPPORTED, "%s: k and v must share their strides", name);
+  }
+  if (sp <= 0 || sh < 0 || sb < 0 || (sp * esize) % 16 != 0 || (sh * esize) % 16 != 0 ||
+      (reinterpret_cast<uintptr_t>(a->k) | reinterpret_cast<uintptr_t>(a->v) |
+       reinterpret_cast<uintptr_t>(a->q) | reinterpret_cast<uintptr_t>(a->out)) % 16 != 0) {
+    return fail(MVLLM_ERR_UNSUPPORTED,
+                "%s: the position and head strides of k and v must be positive multiples of 16 "
+                "bytes and every pointer 16-byte aligned",
+                name);
+  }
+  if (a->batch > 1 && sb % sp != 0) {
+    return fail(MVLLM_ERR_UNSUPPORTED,
+                "%s: the batch stride of k and v (%lld) must be a multiple of the position "
+                "stride (%lld)",
+                name, static_cast<long long>(sb), static_cast<long long>(sp));
+  }
+  d.max_blocks = (a->kv_len + 15) / 16;
+  d.slots_per_batch = a->batch > 1 ? sb / sp : 0;
+  if ((a->batch - 1) * d.slots_per_batch + 16 * static_cast<int64_t>(d.max_blocks) >=
+          (int64_t{1} << 31) ||
+      sh * esize * a->num_kv_heads >= (int64_t{1} << 32) || sp * esize * 16 >= (int64_t{1} << 32)) {
+    return fail(MVLLM_ERR_UNSUPPORTED, "%s: the cache is too large for 32-bit page ids", name);
+  }
+  const int64_t tokens = static_cast<int64_t>(a->batch) * a->query_len;
+  if (tokens >= (int64_t{1} << 31)) return fail(MVLLM_ERR_UNSUPPORTED, "%s: too many queries", name);
+  const int rc = check_paged_shape(static_cast<int32_t>(tokens), a->batch, a->num_q_heads,
+                                   a->num_kv_heads, a->head_dim, 16, a->query_len, a->kv_len,
+                                   a->dtype, a->dtype);
+  if (rc != MVLLM_OK) return rc;
+  d.plan = make_plan(static_cast<int32_t>(tokens), a->batch, a->num_q_heads, a->num_kv_heads,
+                     a->head_dim, 16, a->query_len, a->kv_len, a->dtype, a->dtype);
+  const uint64_t b = static_cast<uint64_t>(a->batch);
+  d.off_tables = 0;
+  d.off_cu = align256(b * d.max_blocks * 4);
+  d.off_ctx = d.off_cu + align256((b + 1) * 4);
+  d.off_len = d.off_ctx + align256(b * 4);
+  d.off_paged = d.off_len + align256(b * 4);
+  d.bytes = d.off_paged + d.plan.pub.workspace_bytes;
+  return MVLLM_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -318,36 +433,86 @@ int mvllm_paged_attention(void* out, const void* q, const void* key_pool,
   p.max_blocks = max_blocks_per_seq;
   p.block_shift = shift;
   p.block_mask = block_size - 1;
-  p.stream_wgs = plan.pub.decode_mode == MVLLM_DECODE_STREAM ? plan.pub.decode_workgroups : 0;
-  p.split_tokens = plan.pub.split_tokens > 0 ? plan.pub.split_tokens : mvllm::kMaxSplitTokens;
-  p.max_splits = plan.max_splits;
-  p.by_row = plan.pub.decode_mode == MVLLM_DECODE_BY_ROW ? 1 : 0;
+  p.table_shift = shift;
+  const int64_t kv_elem = kv_dtype == mvllm::kF32 ? 4 : (kv_dtype == mvllm::kFP8E4M3 ? 1 : 2);
+  p.kv_head_bytes = static_cast<int64_t>(head_dim) * kv_elem;
+  p.kv_row_bytes = p.kv_head_bytes * num_kv_heads;
   p.scale = scale;
-  if (need > 0) {
-    char* ws = static_cast<char*>(workspace);
-    if (plan.pub.decode_mode == MVLLM_DECODE_STREAM) p.seq_prefix = reinterpret_cast<int*>(ws);
-    p.part_o = reinterpret_cast<float*>(ws + plan.off_o);
-    p.part_ml = reinterpret_cast<float*>(ws + plan.off_ml);
-    if (plan.pub.prefill_workgroups > 0) {
-      p.pf_wgs = plan.pub.prefill_workgroups;
-      p.pf_prefix = reinterpret_cast<int*>(ws + plan.off_pf);
-      p.pf_o = reinterpret_cast<float*>(ws + plan.off_pf_o);
-      p.pf_ml = reinterpret_cast<float*>(ws + plan.off_pf_ml);
-    }
-  }
+  return launch_planned(plan, p, workspace, q_dtype, kv_dtype, head_dim, max_query_len,
+                        static_cast<hipStream_t>(stream), "paged_attention");
+}
 
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (plan.pub.decode_mode != MVLLM_DECODE_NONE) {
-    rc = hip_status(mvllm::launch_paged_decode(p, q_dtype, kv_dtype, head_dim, s),
-                    "paged_attention: decode launch");
-    if (rc != MVLLM_OK) return rc;
+int mvllm_dense_attention_plan(const mvllm_dense_args* args, uint64_t* workspace_bytes) {
+  g_error[0] = '\0';
+  if (workspace_bytes == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "dense_attention_plan: workspace_bytes is NULL");
   }
-  if (plan.pub.prefill_mfma) {
-    rc = hip_status(mvllm::launch_paged_prefill(p, q_dtype, kv_dtype, head_dim, max_query_len, s),
-                    "paged_attention: prefill launch");
-    if (rc != MVLLM_OK) return rc;
-  }
+  DensePlan d;
+  const int rc = dense_plan(args, d);
+  if (rc != MVLLM_OK) return rc;
+  *workspace_bytes = d.bytes;
   return MVLLM_OK;
+}
+
+int mvllm_dense_attention(const mvllm_dense_args* args, void* workspace, uint64_t workspace_bytes,
+                          void* stream) {
+  g_error[0] = '\0';
+  DensePlan d;
+  int rc = dense_plan(args, d);
+  if (rc != MVLLM_OK) return rc;
+  const char* name = args->query_len == 1 ? "decode_attention" : "flash_prefill";
+  if (args->batch == 0) return MVLLM_OK;
+  if (args->out == nullptr || args->q == nullptr || args->k == nullptr || args->v == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "%s: a required pointer is NULL", name);
+  }
+  if (workspace == nullptr || workspace_bytes < d.bytes) {
+    return fail(MVLLM_ERR_WORKSPACE,
+                "%s: workspace of %llu bytes is smaller than the %llu the call needs (call "
+                "mvllm_dense_attention_plan)",
+                name, static_cast<unsigned long long>(workspace_bytes),
+                static_cast<unsigned long long>(d.bytes));
+  }
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) {
+    return fail(MVLLM_ERR_INVALID, "%s: the workspace must be 256-byte aligned", name);
+  }
+  char* ws = static_cast<char*>(workspace);
+  mvllm::DenseMeta meta{};
+  meta.block_tables = reinterpret_cast<int32_t*>(ws + d.off_tables);
+  meta.cu_seqlens_q = reinterpret_cast<int32_t*>(ws + d.off_cu);
+  meta.context_lens = reinterpret_cast<int32_t*>(ws + d.off_ctx);
+  meta.seq_lens = reinterpret_cast<int32_t*>(ws + d.off_len);
+  meta.batch = args->batch;
+  meta.max_blocks = d.max_blocks;
+  meta.slots_per_batch = d.slots_per_batch;
+  meta.query_len = args->query_len;
+  meta.kv_len = args->kv_len;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  rc = hip_status(mvllm::launch_dense_meta(meta, s), name);
+  if (rc != MVLLM_OK) return rc;
+
+  const int esize = args->dtype == mvllm::kF32 ? 4 : 2;
+  mvllm::PagedParams p{};
+  p.q = args->q;
+  p.k_pool = args->k;
+  p.v_pool = args->v;
+  p.out = args->out;
+  p.block_tables = meta.block_tables;
+  p.cu_seqlens_q = meta.cu_seqlens_q;
+  p.context_lens = meta.context_lens;
+  p.seq_lens = meta.seq_lens;
+  p.num_seqs = args->batch;
+  p.num_tokens = args->batch * args->query_len;
+  p.hq = args->num_q_heads;
+  p.hk = args->num_kv_heads;
+  p.max_blocks = d.max_blocks;
+  p.block_shift = 4;
+  p.block_mask = 15;
+  p.table_shift = 0;
+  p.kv_row_bytes = args->k_stride_pos * esize;
+  p.kv_head_bytes = args->k_stride_head * esize;
+  p.scale = args->scale;
+  return launch_planned(d.plan, p, ws + d.off_paged, args->dtype, args->dtype, args->head_dim,
+                        args->query_len, s, name);
 }
 
 int mvllm_rmsnorm(void* out, const void* x, const void* weight, int64_t rows, int64_t dim,

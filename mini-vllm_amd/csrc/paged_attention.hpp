@@ -71,6 +71,11 @@ struct PagedParams {
   int max_blocks;
   int block_shift;
   int block_mask;
+  int table_shift;        // slot of a table entry's first row = entry << table_shift (a
+                          // paged pool: block_shift, entries are page ids; 0: entries
+                          // are slot ids themselves)
+  int64_t kv_row_bytes;   // pool bytes between consecutive slots (a paged pool: H_k D elements)
+  int64_t kv_head_bytes;  // pool bytes between kv heads of one slot (a paged pool: D elements)
   int stream_wgs;     // decode: > 0 selects the stream schedule with this many workgroups
   int split_tokens;   // grid decode: nominal keys per split
   int max_splits;     // grid decode: grid extent along the split axis

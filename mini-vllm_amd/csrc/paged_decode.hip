@@ -157,8 +157,8 @@ struct Decode {
         int tok = t0 + u * RG + g;
         valid[u] = tok < se;
         tok = valid[u] ? tok : se - 1;
-        const int64_t slot = (static_cast<int64_t>(pg[u]) << p.block_shift) | (tok & p.block_mask);
-        const int64_t off = ((slot * p.hk + kvh) * D + r * E) * kElemBytes;
+        const int64_t slot = (static_cast<int64_t>(pg[u]) << p.table_shift) + (tok & p.block_mask);
+        const int64_t off = slot * p.kv_row_bytes + kvh * p.kv_head_bytes + r * E * kElemBytes;
         kw[u] = load16_stream(kbase + off);
         vw[u] = load16_stream(vbase + off);
         if constexpr (kFp8) {

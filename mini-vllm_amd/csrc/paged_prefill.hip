@@ -304,8 +304,8 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_kernel(const PagedPara
 
   const char* kpool = static_cast<const char*>(p.k_pool);
   const char* vpool = static_cast<const char*>(p.v_pool);
-  const int64_t row_bytes = static_cast<int64_t>(p.hk) * D * kElemBytes;  // one token's K row
-  const int64_t page_bytes = row_bytes << p.block_shift;
+  const int64_t row_bytes = p.kv_row_bytes;  // one slot's K row
+  const int64_t page_bytes = row_bytes << p.table_shift;  // per unit of a table entry
 
   // ---- staging maps. K unit u: key (idx / (D/8)), dims 8 * (idx % (D/8)) .. +7, so 16
   // lanes read one 16-byte-chunked key row. V unit u: keys kVKeys * (idx % kVGroups)
@@ -359,7 +359,7 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_kernel(const PagedPara
     constexpr int S = decltype(set)::value;
     const int key0 = k.t * kTileKeys;
     const int last = k.context - 1;
-    const uint32_t head_off = static_cast<uint32_t>((k.c / chunks) * D * kElemBytes);
+    const uint32_t head_off = static_cast<uint32_t>((k.c / chunks) * p.kv_head_bytes);
 #pragma unroll
     for (int u = 0; u < kKUnits; ++u) {
       const int key = min(key0 + k_key(u), last);
@@ -723,8 +723,8 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_lds_kernel(const Paged
 
   const char* kpool = static_cast<const char*>(p.k_pool);
   const char* vpool = static_cast<const char*>(p.v_pool);
-  const uint32_t row_bytes = static_cast<uint32_t>(p.hk * D * 2);  // one token's K row
-  const uint64_t page_bytes = static_cast<uint64_t>(row_bytes) << p.block_shift;
+  const uint32_t row_bytes = static_cast<uint32_t>(p.kv_row_bytes);  // one slot's K row
+  const uint64_t page_bytes = static_cast<uint64_t>(row_bytes) << p.table_shift;  // per table unit
 
   // ---- per-lane constants of the staging and fragment maps.
   // K copy j: LDS chunk (lane % 16) of key KW*wave + 4j + lane/16 holds logical chunk
@@ -777,7 +777,7 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_lds_kernel(const Paged
     const int key0 = k.t * kTileKeys + KW * wave;
     const int last = k.context - 1;
     const uint64_t head = static_cast<uint64_t>(static_cast<uint32_t>(page)) * page_bytes +
-                          static_cast<uint32_t>(k.kvh * D * 2);
+                          static_cast<uint32_t>(k.kvh * static_cast<uint32_t>(p.kv_head_bytes));
     if (key0 + KW - 1 <= last) {
       // The wave's keys are whole: their first row joins the scalar base.
       const uint64_t base = head + static_cast<uint32_t>(key0 & p.block_mask) * row_bytes;

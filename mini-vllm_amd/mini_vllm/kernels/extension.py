@@ -129,6 +129,31 @@ def build_library(verbose: bool = False, jobs: int | None = None) -> Path:
 # ------------------------------------------------------------------- bindings
 
 
+class _DenseArgs(ctypes.Structure):
+    """``mvllm_dense_args`` of include/minivllm_hip.h."""
+
+    _fields_ = [
+        ("out", ctypes.c_void_p),
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("k_stride_batch", ctypes.c_int64),
+        ("k_stride_head", ctypes.c_int64),
+        ("k_stride_pos", ctypes.c_int64),
+        ("v_stride_batch", ctypes.c_int64),
+        ("v_stride_head", ctypes.c_int64),
+        ("v_stride_pos", ctypes.c_int64),
+        ("batch", ctypes.c_int32),
+        ("num_q_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("query_len", ctypes.c_int32),
+        ("kv_len", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("dtype", ctypes.c_int32),
+    ]
+
+
 class _Plan(ctypes.Structure):
     _fields_ = [
         ("decode_mode", ctypes.c_int32),
@@ -158,6 +183,10 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_abi_version.argtypes = []
     lib.mvllm_paged_attention_plan.restype = ctypes.c_int
     lib.mvllm_paged_attention_plan.argtypes = [i32] * 10 + [ctypes.POINTER(_Plan)]
+    lib.mvllm_dense_attention_plan.restype = ctypes.c_int
+    lib.mvllm_dense_attention_plan.argtypes = [ctypes.POINTER(_DenseArgs), ctypes.POINTER(ctypes.c_uint64)]
+    lib.mvllm_dense_attention.restype = ctypes.c_int
+    lib.mvllm_dense_attention.argtypes = [ctypes.POINTER(_DenseArgs), p, ctypes.c_uint64, p]
     lib.mvllm_paged_attention.restype = ctypes.c_int
     lib.mvllm_paged_attention.argtypes = (
         [p] * 10 + [i32] * 6 + [i64, i32, i32, i32, f32, i32, i32, p, u64, p]
@@ -197,6 +226,8 @@ EXPORTED_SYMBOLS = (
     "mvllm_axpby",
     "mvllm_kv_write",
     "mvllm_qk_norm_rope",
+    "mvllm_dense_attention_plan",
+    "mvllm_dense_attention",
     "mvllm_linear_pack",
     "mvllm_linear",
     "mvllm_linear_split",
@@ -604,6 +635,95 @@ class HipExtension:
             )
         )
         return out
+
+    # -- dense-cache attention (reference csrc/decode_attention.cu, csrc/flash_prefill.cu)
+    @staticmethod
+    def dense_supported(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
+        """Whether the library serves this dense call (after the reference's own checks):
+        head dim 32/64/128/256, k and v sharing strides that are multiples of 16 bytes
+        (the batch stride a multiple of the position stride), 16-byte aligned pointers.
+        Anything else is the PyTorch path's."""
+        if q.dim() != 4 or k.dim() != 4 or k.shape != v.shape or q.shape[-1] not in (32, 64, 128, 256):
+            return False
+        if q.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            return False
+        es = q.element_size()
+        sb, sh, sp, sd = k.stride()
+        if v.stride() != k.stride() and not (k.shape[0] == 1 and v.stride()[1:] == k.stride()[1:]):
+            return False
+        if sd != 1 or sp <= 0 or sh < 0 or (sp * es) % 16 or (sh * es) % 16:
+            return False
+        if k.shape[0] > 1 and sb % sp:
+            return False
+        return all(t.data_ptr() % 16 == 0 for t in (q, k, v))
+
+    def _dense_checks(self, name: str, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+        if not (q.is_cuda and k.is_cuda and v.is_cuda):
+            raise RuntimeError(f"{name}: q, k and v must be CUDA tensors")
+        if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+            raise RuntimeError(f"{name}: expected B x H x L x D tensors, got q.dim()={q.dim()}")
+        if name == "decode_attention" and q.shape[2] != 1:
+            raise RuntimeError(
+                f"decode_attention: this kernel is the L == 1 case, got a query length of "
+                f"{q.shape[2]}; use flash_prefill for longer queries")
+        if k.shape != v.shape:
+            raise RuntimeError(f"{name}: k is {list(k.shape)} but v is {list(v.shape)}")
+        if q.shape[0] != k.shape[0]:
+            raise RuntimeError(f"{name}: batch mismatch, q has {q.shape[0]} and k has {k.shape[0]}")
+        if q.shape[3] != k.shape[3]:
+            raise RuntimeError(f"{name}: head dim mismatch, q has {q.shape[3]} and k has {k.shape[3]}")
+        if k.shape[1] == 0 or q.shape[1] % k.shape[1] != 0:
+            raise RuntimeError(f"{name}: H_q ({q.shape[1]}) must be a multiple of H_k ({k.shape[1]})")
+        if name == "decode_attention" and k.shape[2] == 0:
+            raise RuntimeError(
+                "decode_attention: the cache is empty, so there is nothing to attend to; softmax "
+                "over zero keys is undefined")
+        if name == "flash_prefill" and not (q.shape[2] > 0 and k.shape[2] >= q.shape[2]):
+            raise RuntimeError(
+                f"flash_prefill: {q.shape[2]} queries against {k.shape[2]} keys; this kernel masks "
+                "causally, which needs S >= L > 0")
+        if q.dtype != k.dtype or q.dtype != v.dtype:
+            raise RuntimeError(f"{name}: q, k and v must share a dtype, got {q.dtype}, {k.dtype} "
+                               f"and {v.dtype}")
+        if q.dtype == torch.float64:
+            raise RuntimeError(f"{name}: float64 is not supported; the accumulators here are fp32. "
+                               "Use the PyTorch path.")
+        if q.stride(3) != 1 or k.stride(3) != 1 or v.stride(3) != 1:
+            raise RuntimeError(f"{name}: the head dimension must be contiguous")
+
+    def _dense(self, name: str, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+               scale: float) -> torch.Tensor:
+        self._dense_checks(name, q, k, v)
+        b, hq, L, d = q.shape
+        qt = q.transpose(1, 2)
+        if not qt.is_contiguous():
+            qt = qt.contiguous()
+        out = torch.empty((b, L, hq, d), dtype=q.dtype, device=q.device)
+        if b == 0:
+            return out.transpose(1, 2)
+        args = _DenseArgs(out.data_ptr(), qt.data_ptr(), k.data_ptr(), v.data_ptr(),
+                          *k.stride()[:3], *v.stride()[:3], b, hq, k.shape[1], L, k.shape[2], d,
+                          float(scale), DTYPE_CODES.get(q.dtype, -1))
+        need = ctypes.c_uint64()
+        self._check(self.lib.mvllm_dense_attention_plan(ctypes.byref(args), ctypes.byref(need)))
+        ws = self.workspace(q.device, need.value)
+        self._check(self.lib.mvllm_dense_attention(ctypes.byref(args), ws.data_ptr(), ws.numel(),
+                                                   _stream(q.device)))
+        return out.transpose(1, 2)
+
+    def decode_attention(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                         scale: float) -> torch.Tensor:
+        """One query token per sequence against its whole dense cache (reference
+        csrc/decode_attention.cu:360-435): q ``B x H_q x 1 x D``, k/v ``B x H_k x S x D``
+        read through their strides. The output is ``B x H_q x 1 x D``."""
+        return self._dense("decode_attention", q, k, v, scale)
+
+    def flash_prefill(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                      scale: float) -> torch.Tensor:
+        """L queries against S >= L cached keys, causal with offset S - L (reference
+        csrc/flash_prefill.cu:282-355). The output is ``B x H_q x L x D`` values, a
+        transposed view of a token-major buffer (its ``.transpose(1, 2)`` is contiguous)."""
+        return self._dense("flash_prefill", q, k, v, scale)
 
     def paged_attention_plan(
         self,

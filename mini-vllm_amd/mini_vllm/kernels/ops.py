@@ -65,8 +65,8 @@ CUDA_KERNELS: dict[str, tuple[bool, str]] = {
     "rmsnorm": (True, "csrc/elementwise.hip"),
     "rope": (True, "csrc/elementwise.hip"),
     "swiglu": (True, "csrc/elementwise.hip"),
-    "decode_attention": (False, "dense-cache decode (not in this library)"),
-    "flash_prefill": (False, "dense-cache prefill (not in this library)"),
+    "decode_attention": (True, "csrc/dense.hip over the paged decode kernels"),
+    "flash_prefill": (True, "csrc/dense.hip over the paged prefill kernels"),
     "paged_attention": (True, "csrc/paged_decode.hip + csrc/paged_prefill.hip"),
     "kv_write": (True, "csrc/kv_write.hip"),
     "qk_norm_rope": (True, "csrc/elementwise.hip"),
@@ -260,9 +260,21 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
               mask: torch.Tensor | str | None = None, use_cuda: bool = False) -> torch.Tensor:
     """Dense-cache grouped attention ``B x H x L x D`` (reference ops.py:166-197).
 
-    Not on the paged engine's path and without a kernel in this library: always the
-    PyTorch path (decode: every cached key visible; ``mask="causal"``: offset causal).
+    ``L == 1`` is decode (every cached key visible), ``L > 1`` prefill. Kernels:
+    ``decode_attention`` / ``flash_prefill`` of the extension (``csrc/dense.hip``: the
+    paged decode and MFMA prefill kernels over virtual 16-position pages of the cache,
+    read through its strides). They bake the causal structure in, so they serve decode
+    with ``mask`` None or "causal" and prefill with "causal" only (reference
+    ``_kernel_can_attend``, ops.py:278-305); an explicit mask tensor, fp64, or a shape
+    or stride layout the library refuses goes to the PyTorch path below.
     """
+    is_decode = q.shape[-2] == 1
+    name = "decode_attention" if is_decode else "flash_prefill"
+    if _use_kernel(name, use_cuda, q) and _kernel_can_attend(q, k, v, mask, is_decode):
+        ext = load_extension()
+        if ext.dense_supported(q, k, v):
+            scale = 1.0 / math.sqrt(q.shape[-1])
+            return getattr(ext, name)(q, k, v, scale)
     b, hq, L, d = q.shape
     hk, S = k.shape[1], k.shape[2]
     g = hq // hk
@@ -278,6 +290,24 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if mask is not None:
         scores = scores + mask
     return (torch_path.softmax(scores, dim=-1) @ v.unsqueeze(2)).reshape(b, hq, L, d)
+
+
+def _kernel_can_attend(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                       mask: torch.Tensor | str | None, is_decode: bool) -> bool:
+    """Whether the dense kernels may serve this call (reference ops.py:278-305): the
+    mask must be one they bake in, the dtypes shared and not fp64, S >= L, and the head
+    dimension contiguous."""
+    causal = isinstance(mask, str) and mask == "causal"
+    if is_decode:
+        if mask is not None and not causal:
+            return False
+    elif not causal:
+        return False
+    if q.dim() != 4 or q.dtype != k.dtype or q.dtype != v.dtype or q.dtype == torch.float64:
+        return False
+    if k.shape[-2] < q.shape[-2]:
+        return False
+    return k.shape[-2] > 0 and q.stride(-1) == 1 and k.stride(-1) == 1 and v.stride(-1) == 1
 
 
 def paged_attention(

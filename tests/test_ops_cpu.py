@@ -63,18 +63,37 @@ def test_dispatch_report_names_every_op():
     assert "paged_attention    hip" in on
     assert "use_cuda is off" in off
     assert set(ops.cuda_kernel_names()) == {"rmsnorm", "rope", "swiglu", "paged_attention", "kv_write",
-                                            "qk_norm_rope", "linear"}
+                                            "qk_norm_rope", "linear", "decode_attention",
+                                            "flash_prefill"}
 
 
 def test_dense_attention_torch_path_decode_and_causal():
     q = torch.randn(2, 8, 1, 32)
     k = torch.randn(2, 4, 10, 32)
     v = torch.randn(2, 4, 10, 32)
-    out = ops.attention(q, k, v, use_cuda=True)  # no dense kernel: PyTorch path
+    out = ops.attention(q, k, v)
     g = 2
     ref = torch.softmax((q.reshape(2, 4, g, 1, 32) @ k.unsqueeze(2).transpose(-1, -2)) / 32**0.5, -1)
     ref = (ref @ v.unsqueeze(2)).reshape(2, 8, 1, 32)
     assert torch.allclose(out, ref, atol=1e-6)
+    with pytest.raises(RuntimeError, match="device tensors"):
+        ops.attention(q, k, v, use_cuda=True)
+
+
+def test_dense_kernel_gate_follows_the_reference():
+    """``_kernel_can_attend`` (reference ops.py:278-305): decode takes None or "causal",
+    prefill only "causal"; explicit masks, fp64, S < L and a strided head dim go to the
+    PyTorch path."""
+    q1, qL = torch.randn(1, 4, 1, 32), torch.randn(1, 4, 6, 32)
+    k = torch.randn(1, 2, 9, 32)
+    can = ops._kernel_can_attend
+    assert can(q1, k, k, None, True) and can(q1, k, k, "causal", True)
+    assert not can(q1, k, k, torch.zeros(1, 9), True)
+    assert can(qL, k, k, "causal", False) and not can(qL, k, k, None, False)
+    assert not can(qL, k[:, :, :5], k[:, :, :5], "causal", False)  # S < L
+    assert not can(q1.double(), k.double(), k.double(), None, True)
+    strided = torch.randn(1, 2, 9, 64)[..., ::2]
+    assert not can(q1, strided, strided, None, True)
 
 
 def test_linear_torch_path_is_x_matmul_w_transposed():

@@ -276,3 +276,58 @@ def test_swiglu_matches_torch_cpu_within_a_rounding():
         tol = np.abs(want) * (2**-7 if name == "bf16" else 1e-6) + 1e-30
         assert (np.abs(got - want) <= tol).all()
     assert ew.swiglu(np.zeros(3, np.float32), np.ones(3, np.float32))[0] == 0.0
+
+
+# -- dense-cache attention oracle (oracle/dense_attention.py)
+
+def _as_pages(k: torch.Tensor, block: int = 16, seed: int = 0):
+    """k ``B x H_k x S x D`` laid out as a shuffled paged pool ``nb x P x H_k x D`` with
+    its block tables."""
+    b, hk, s, d = k.shape
+    pages = -(-s // block)
+    perm = torch.randperm(b * pages, generator=torch.Generator().manual_seed(seed))
+    pool = torch.zeros(b * pages, block, hk, d, dtype=k.dtype)
+    tables = perm.view(b, pages).to(torch.int32)
+    for i in range(b):
+        for j in range(s):
+            pool[tables[i, j // block], j % block] = k[i, :, j]
+    return pool, tables
+
+
+@pytest.mark.parametrize("L,S", [(1, 37), (5, 5), (7, 40)])
+def test_dense_oracle_equals_the_paged_oracle(L, S):
+    """The same keys as a dense cache and as shuffled pages give the same attention."""
+    from oracle.dense_attention import dense_attention
+
+    gen = torch.Generator().manual_seed(L * 100 + S)
+    b, hq, hk, d = 3, 8, 2, 32
+    q = torch.randn(b, hq, L, d, generator=gen)
+    k = torch.randn(b, hk, S, d, generator=gen)
+    v = torch.randn(b, hk, S, d, generator=gen)
+    dense = dense_attention(q, k, v, causal=True)
+    kp, tables = _as_pages(k)
+    vp, _ = _as_pages(v)
+    qt = q.transpose(1, 2).reshape(b * L, hq, d)
+    cu = torch.arange(0, (b + 1) * L, L, dtype=torch.int32)
+    ctx = torch.full((b,), S, dtype=torch.int32)
+    paged = oracle_paged(qt, kp, vp, tables, cu, ctx, 1 / math.sqrt(d), compute_dtype=torch.float64)
+    torch.testing.assert_close(dense.transpose(1, 2).reshape(b * L, hq, d), paged, rtol=0, atol=1e-12)
+
+
+def test_dense_oracle_known_answers():
+    """One visible key (S = 1) returns its value; q = 0 (equal scores) returns the mean
+    of the visible values, per query row under the causal offset."""
+    from oracle.dense_attention import dense_attention
+
+    gen = torch.Generator().manual_seed(5)
+    q = torch.randn(2, 4, 1, 16, generator=gen)
+    k = torch.randn(2, 2, 1, 16, generator=gen)
+    v = torch.randn(2, 2, 1, 16, generator=gen)
+    out = dense_attention(q, k, v)
+    assert torch.equal(out, v.double().repeat_interleave(2, dim=1))
+    L, S = 3, 6
+    v = torch.randn(1, 1, S, 8, generator=gen)
+    out = dense_attention(torch.zeros(1, 2, L, 8), torch.randn(1, 1, S, 8, generator=gen), v)
+    for i in range(L):
+        want = v[0, 0, : S - L + i + 1].double().mean(0)
+        torch.testing.assert_close(out[0, 1, i], want, rtol=0, atol=1e-12)
