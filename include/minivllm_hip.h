@@ -254,6 +254,15 @@ int mvllm_linear_residual(void* y, const void* x, const void* w, const void* res
 int mvllm_linear_swiglu(void* y, const void* x, const void* w_gate_up, int64_t m, int64_t n_out,
                         int64_t k, int32_t dtype, void* stream);
 
+/* Greedy sampling: out[r] (int64) = index of the maximum of logits row r, for `rows`
+ * rows of `vocab` logits each, `row_stride` elements apart, dtype f32/f16/bf16. The
+ * order is torch.argmax's: NaN above every number, -0 equal to +0, and among equal
+ * maxima the first index. Replaces `logits.argmax(dim=-1)` of the greedy sampler
+ * (mini_vllm/sampler.py:135-141; the engine's decode step, engine.py); no counterpart in
+ * mini_vllm_C. */
+int mvllm_argmax(int64_t* out, const void* logits, int64_t rows, int64_t vocab,
+                 int64_t row_stride, int32_t dtype, void* stream);
+
 /* y = a * x + b over n floats: the toolchain smoke test, replacing `mini_vllm_C.hello`
  * (csrc/bindings.cpp:8,37-42 -> csrc/hello.cu:11-21; mini_vllm/kernels/extension.py:349-353). */
 int mvllm_axpby(float* y, const float* x, float a, float b, int64_t n, void* stream);

@@ -18,6 +18,7 @@
 #include "elementwise.hpp"
 #include "kv_write.hpp"
 #include "linear.hpp"
+#include "sampler.hpp"
 #include "paged_attention.hpp"
 
 namespace {
@@ -513,6 +514,29 @@ int mvllm_dense_attention(const mvllm_dense_args* args, void* workspace, uint64_
   p.scale = args->scale;
   return launch_planned(d.plan, p, ws + d.off_paged, args->dtype, args->dtype, args->head_dim,
                         args->query_len, s, name);
+}
+
+int mvllm_argmax(int64_t* out, const void* logits, int64_t rows, int64_t vocab,
+                 int64_t row_stride, int32_t dtype, void* stream) {
+  g_error[0] = '\0';
+  if (dtype != mvllm::kF32 && dtype != mvllm::kF16 && dtype != mvllm::kBF16) {
+    return fail(MVLLM_ERR_UNSUPPORTED, "argmax: dtype code %d is not served (f32, f16, bf16)", dtype);
+  }
+  if (rows < 0 || rows >= (int64_t{1} << 31) || vocab <= 0 || vocab >= (int64_t{1} << 32) - 1 ||
+      row_stride < vocab) {
+    return fail(MVLLM_ERR_INVALID,
+                "argmax: %lld rows of %lld logits, %lld apart: rows must be < 2^31, the row "
+                "non-empty and shorter than 2^32 - 1, the stride at least the row",
+                static_cast<long long>(rows), static_cast<long long>(vocab),
+                static_cast<long long>(row_stride));
+  }
+  if (rows == 0) return MVLLM_OK;
+  if (out == nullptr || logits == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "argmax: a required pointer is NULL");
+  }
+  return hip_status(mvllm::launch_argmax(out, logits, rows, vocab, row_stride, dtype,
+                                         static_cast<hipStream_t>(stream)),
+                    "argmax: launch");
 }
 
 int mvllm_rmsnorm(void* out, const void* x, const void* weight, int64_t rows, int64_t dim,

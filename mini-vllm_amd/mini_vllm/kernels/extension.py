@@ -203,6 +203,8 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_qk_norm_rope.argtypes = [p] * 7 + [i32, p, p, i64, i32, i32, i32, i64, i64, f32, i32, p]
     lib.mvllm_kv_write.restype = ctypes.c_int
     lib.mvllm_kv_write.argtypes = [p] * 7 + [i32] * 4 + [i64, i32, i32, p]
+    lib.mvllm_argmax.restype = ctypes.c_int
+    lib.mvllm_argmax.argtypes = [p, p, i64, i64, i64, i32, p]
     lib.mvllm_linear_pack.restype = ctypes.c_int
     lib.mvllm_linear_pack.argtypes = [p, p, i64, i64, i32, p]
     lib.mvllm_linear.restype = ctypes.c_int
@@ -226,6 +228,7 @@ EXPORTED_SYMBOLS = (
     "mvllm_axpby",
     "mvllm_kv_write",
     "mvllm_qk_norm_rope",
+    "mvllm_argmax",
     "mvllm_dense_attention_plan",
     "mvllm_dense_attention",
     "mvllm_linear_pack",
@@ -634,6 +637,22 @@ class HipExtension:
                 out.data_ptr(), gate.data_ptr(), up.data_ptr(), gate.numel(), code, _stream(gate.device)
             )
         )
+        return out
+
+    def argmax(self, logits: torch.Tensor) -> torch.Tensor:
+        """``logits.argmax(dim=-1)`` (int64) for a 2-D f32/f16/bf16 device tensor whose
+        rows are contiguous: torch's order (NaN highest, -0 == +0, first index wins)."""
+        if not logits.is_cuda or logits.dim() != 2 or logits.stride(1) != 1:
+            raise RuntimeError("argmax: expected a 2-D CUDA tensor with contiguous rows, got "
+                               f"{tuple(logits.shape)} strides {logits.stride()}")
+        if logits.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            raise RuntimeError(f"argmax: dtype {logits.dtype} is not served (f32, f16, bf16)")
+        out = torch.empty(logits.shape[0], dtype=torch.int64, device=logits.device)
+        if logits.shape[0] == 0:
+            return out
+        self._check(self.lib.mvllm_argmax(out.data_ptr(), logits.data_ptr(), logits.shape[0],
+                                          logits.shape[1], max(logits.stride(0), logits.shape[1]),
+                                          DTYPE_CODES[logits.dtype], _stream(logits.device)))
         return out
 
     # -- dense-cache attention (reference csrc/decode_attention.cu, csrc/flash_prefill.cu)

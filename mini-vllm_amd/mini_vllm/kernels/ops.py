@@ -41,6 +41,7 @@ from mini_vllm.kernels.extension import load_extension
 
 __all__ = [
     "CUDA_KERNELS",
+    "argmax",
     "NOT_YET_FASTER",
     "attention",
     "cuda_kernel_names",
@@ -65,6 +66,7 @@ CUDA_KERNELS: dict[str, tuple[bool, str]] = {
     "rmsnorm": (True, "csrc/elementwise.hip"),
     "rope": (True, "csrc/elementwise.hip"),
     "swiglu": (True, "csrc/elementwise.hip"),
+    "argmax": (True, "csrc/sampler.hip"),
     "decode_attention": (True, "csrc/dense.hip over the paged decode kernels"),
     "flash_prefill": (True, "csrc/dense.hip over the paged prefill kernels"),
     "paged_attention": (True, "csrc/paged_decode.hip + csrc/paged_prefill.hip"),
@@ -163,6 +165,16 @@ def swiglu(gate: torch.Tensor, up: torch.Tensor, use_cuda: bool = False) -> torc
     if _use_kernel("swiglu", use_cuda, gate):
         return load_extension().swiglu(gate, up)
     return torch_path.silu(gate) * up
+
+
+def argmax(logits: torch.Tensor, use_cuda: bool = False) -> torch.Tensor:
+    """Greedy sampling, ``logits.argmax(dim=-1)`` over ``B x V`` logits (reference
+    sampler.py:135-141). Kernel: ``csrc/sampler.hip`` (one pass over each row, torch's
+    tie and NaN order); other shapes and dtypes take torch's reduction."""
+    if (_use_kernel("argmax", use_cuda, logits) and logits.dim() == 2 and logits.shape[1] > 0
+            and logits.stride(1) == 1 and logits.dtype in (torch.float32, torch.float16, torch.bfloat16)):
+        return load_extension().argmax(logits)
+    return logits.argmax(dim=-1)
 
 
 @dataclass(frozen=True)
