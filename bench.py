@@ -223,6 +223,82 @@ def run_dense(steps: int = 20) -> dict:
     return out
 
 
+def graph_time(fn, calls: int, replays: int = 5) -> float:
+    """Mean ms per call of ``fn(0) .. fn(calls - 1)`` captured in one HIP graph and
+    replayed: the GPU-side cost of a launch-sized op without the Python between calls
+    (what a captured decode step sees)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(calls):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for i in range(calls):
+            fn(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    first = torch.cuda.Event(enable_timing=True)
+    last = torch.cuda.Event(enable_timing=True)
+    first.record()
+    for _ in range(replays):
+        graph.replay()
+    last.record()
+    torch.cuda.synchronize()
+    del graph
+    return first.elapsed_time(last) / (replays * calls)
+
+
+def run_linear(steps: int = 20) -> dict:
+    """The decode step's projections (Qwen3-0.6B shapes, 32 rows = config 5's running
+    sequences, bf16) on the skinny kernels over packed weights against torch's BLAS on
+    the row-major ones, each call reading a different weight copy (> 1 GB rotated, so
+    the weights come from HBM as in a decode iteration). Bytes = weights + x + y. Timed
+    as replays of a captured graph of back-to-back calls (``graph_time``), as the decode
+    step runs them; the Python of an eager call costs more than these kernels."""
+    from mini_vllm import torch_path
+    from mini_vllm.kernels import ops
+
+    bf = torch.bfloat16
+    m = 32
+    shapes = {"qkv": (4096, 1024), "o": (1024, 2048), "gate_up_swiglu": (6144, 1024),
+              "down": (1024, 3072), "lm_head": (151936, 1024)}
+    out = {}
+    for name, (n, k) in shapes.items():
+        copies = max(3, int(1.2e9 // (n * k * 2)))
+        dense = [torch.randn(n, k, device="cuda", dtype=bf) * 0.02 for _ in range(copies)]
+        if name == "gate_up_swiglu":
+            dense = [torch_path.interleave_gate_up(w[: n // 2], w[n // 2:]) for w in dense]
+        packed = [ops.pack_weight(w, use_cuda=True) for w in dense]
+        x = torch.randn(m, k, device="cuda", dtype=bf)
+        r = torch.randn(m, n, device="cuda", dtype=bf)
+        if name == "qkv":
+            call = lambda i: ops.linear_split(x, packed[i % copies], (2048, 1024, 1024), use_cuda=True)
+        elif name in ("o", "down"):
+            call = lambda i: ops.linear_residual(x, packed[i % copies], r, use_cuda=True)
+        elif name == "gate_up_swiglu":
+            call = lambda i: ops.linear_swiglu(x, packed[i % copies], use_cuda=True)
+        else:
+            call = lambda i: ops.linear(x, packed[i % copies], use_cuda=True)
+        nbytes = 2 * n * k + 2 * m * k + 2 * m * n
+        ms = graph_time(call, min(steps, copies))
+        blas_ms = graph_time(lambda i: x @ dense[i % copies].t(), min(steps, copies))
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"n": n, "k": k, "us": round(ms * 1e3, 1), "gbs": round(gbs, 1),
+                     "blas_us": round(blas_ms * 1e3, 1)}
+        log(f"linear {name} ({m}x{n}x{k}): {ms * 1e3:.1f} us, {gbs:.0f} GB/s; BLAS {blas_ms * 1e3:.1f} us")
+        del dense, packed
+        torch.cuda.empty_cache()
+    logits = [torch.randn(m, 151936, device="cuda", dtype=bf) for _ in range(3)]
+    ms = graph_time(lambda i: ops.argmax(logits[i % 3], use_cuda=True), steps)
+    torch_ms = graph_time(lambda i: logits[i % 3].argmax(dim=-1), steps)
+    out["argmax_32x151936"] = {"us": round(ms * 1e3, 1), "torch_us": round(torch_ms * 1e3, 1)}
+    log(f"argmax 32x151936: {ms * 1e3:.1f} us; torch {torch_ms * 1e3:.1f} us")
+    return out
+
+
 def run_elementwise(steps: int = 20) -> dict:
     """RMSNorm (E=1024 and per-head D=128), RoPE (16 heads x 128) and SwiGLU (I=3072)
     at bf16 on ~256 MB operands, three rotated copies each so every call reads HBM.
@@ -321,10 +397,11 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--copies", type=int, default=3, help="rotated pool copies (defeat the MALL)")
     parser.add_argument("--skip-extras", action="store_true", help="headline config 2 only")
-    parser.add_argument("--extras", default="3,4,5,ew,kv,dense,copy",
+    parser.add_argument("--extras", default="3,4,5,ew,kv,dense,linear,copy",
                         help="comma list of extras to run: 3 (prefill), 4 (fp8 decode), "
                              "5 (engine), 5fp8 (engine, fp8 KV cache), ew (elementwise "
-                             "kernels), kv (KV write), dense (dense-cache attention), copy")
+                             "kernels), kv (KV write), dense (dense-cache attention), linear "
+                             "(decode projections and argmax), copy")
     parser.add_argument("--no-cpu", action="store_true")
     args = parser.parse_args()
 
@@ -388,6 +465,8 @@ def main() -> int:
         extras["kv_write"] = run_kv_write()
     if "dense" in wanted:
         extras["dense_attention"] = run_dense()
+    if "linear" in wanted:
+        extras["decode_projections"] = run_linear()
     if "5" in wanted:
         log("config 5: Qwen3-0.6B-shaped engine, 256 requests x 256 tokens")
         extras["config5_engine"] = run_engine()

@@ -221,6 +221,13 @@ int mvllm_kv_write(void* key_pool, void* value_pool, float* k_scales, float* v_s
 int mvllm_linear_pack(void* w_packed, const void* w, int64_t n, int64_t k, int32_t dtype,
                       void* stream);
 
+/* Device bytes of workspace the skinny projections below need for [m, k] x [n, k]^T (n =
+ * n0 + n1 + n2 for mvllm_linear_split, 2 n_out for mvllm_linear_swiglu): 0 for k <= 1024,
+ * else the fp32 partial sums of its k ranges (4 per 1024 of k, 4 KB (m <= 32) or 8 KB per
+ * 32 columns each). 256-byte aligned, contents need not be initialised; calls that
+ * overlap in time on one workspace race. */
+uint64_t mvllm_linear_workspace_bytes(int64_t m, int64_t n, int64_t k);
+
 /* Skinny projection y[m, n] = x[m, k] w[n, k]^T (torch's x @ w.T, no bias) with w packed
  * as above, fp32 accumulation, for the few rows of a decode step: m <= 64, k a multiple
  * of 64 up to 65536, x and w 16-byte aligned, dtype f16 or bf16; anything else returns
@@ -231,20 +238,21 @@ int mvllm_linear_pack(void* w_packed, const void* w, int64_t n, int64_t k, int32
  * in the last bit. The order depends on k alone, so the fused variants below equal
  * this entry bit for bit. */
 int mvllm_linear(void* y, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
-                 int32_t dtype, void* stream);
+                 int32_t dtype, void* workspace, uint64_t workspace_bytes, void* stream);
 
 /* The same projection over w = pack([w0; w1; w2]) (n0 + n1 + n2 rows) with its columns written
  * to three outputs: y0 [m, n0], y1 [m, n1], y2 [m, n2]; n0 and n1 multiples of 32. One
  * launch for the q, k and v projections of model/qwen3_paged.py:71-73. */
 int mvllm_linear_split(void* y0, void* y1, void* y2, const void* x, const void* w, int64_t m,
                        int64_t n0, int64_t n1, int64_t n2, int64_t k, int32_t dtype,
-                       void* stream);
+                       void* workspace, uint64_t workspace_bytes, void* stream);
 
 /* y = residual + x w^T with residual [m, n]: the projection rounded to the dtype, then
  * the add rounded again, as the two torch ops round them (model/qwen3_paged.py:136-138,
  * `h + wo(...)` and `h + down(...)`). */
 int mvllm_linear_residual(void* y, const void* x, const void* w, const void* residual, int64_t m,
-                          int64_t n, int64_t k, int32_t dtype, void* stream);
+                          int64_t n, int64_t k, int32_t dtype, void* workspace,
+                          uint64_t workspace_bytes, void* stream);
 
 /* y [m, n_out] = swiglu(x gate^T, x up^T) in one launch (model/qwen3_paged.py:110, the
  * gate and up projections then ops.swiglu), with w_gate_up [2 n_out, k] holding gate and
@@ -252,7 +260,20 @@ int mvllm_linear_residual(void* y, const void* x, const void* w, const void* res
  * next 16: the same up rows); n_out a multiple of 16. Gate and up are rounded to the
  * dtype before the SwiGLU, which rounds as mvllm_swiglu does; w_gate_up is packed. */
 int mvllm_linear_swiglu(void* y, const void* x, const void* w_gate_up, int64_t m, int64_t n_out,
-                        int64_t k, int32_t dtype, void* stream);
+                        int64_t k, int32_t dtype, void* workspace, uint64_t workspace_bytes,
+                        void* stream);
+
+/* h_out = residual + x w^T (rounded as mvllm_linear_residual) and normed = RMSNorm(h_out)
+ * with norm_weight and eps (rounded as mvllm_rmsnorm: bit for bit the two entries in
+ * sequence), h_out, normed, residual [m, n], norm_weight [n]: the o and down projections
+ * of model/qwen3_paged.py:97,111,136-138 with the RMSNorm that follows each (the MLP
+ * norm, the next layer's attention norm or the final norm), in two launches instead of
+ * three. k > 1024 (the split path), n a multiple of 512 up to 4096, other shapes return
+ * MVLLM_ERR_UNSUPPORTED; workspace as for mvllm_linear. */
+int mvllm_linear_residual_rmsnorm(void* h_out, void* normed, const void* x, const void* w,
+                                  const void* residual, const void* norm_weight, int64_t m,
+                                  int64_t n, int64_t k, float eps, int32_t dtype, void* workspace,
+                                  uint64_t workspace_bytes, void* stream);
 
 /* Greedy sampling: out[r] (int64) = index of the maximum of logits row r, for `rows`
  * rows of `vocab` logits each, `row_stride` elements apart, dtype f32/f16/bf16. The

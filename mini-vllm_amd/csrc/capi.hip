@@ -353,7 +353,7 @@ extern "C" {
 
 const char* mvllm_last_error(void) { return g_error; }
 
-int mvllm_abi_version(void) { return 4; }
+int mvllm_abi_version(void) { return 5; }
 
 int mvllm_paged_attention_plan(int32_t num_tokens, int32_t num_seqs, int32_t num_q_heads,
                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
@@ -695,6 +695,30 @@ int check_linear(const char* name, const void* x, const void* w, int64_t m, int6
   return MVLLM_OK;
 }
 
+// The partial-sum workspace a skinny projection with K > 1024 needs, checked against
+// what the caller gave.
+int check_linear_workspace(const char* name, int64_t m, int64_t n, int64_t k, const void* workspace,
+                           uint64_t workspace_bytes) {
+  const uint64_t need = mvllm::skinny_linear_workspace_bytes(m, n, k);
+  if (need == 0) return MVLLM_OK;
+  if (workspace == nullptr || workspace_bytes < need) {
+    return fail(MVLLM_ERR_WORKSPACE,
+                "%s: workspace of %llu bytes is smaller than the %llu this shape needs "
+                "(mvllm_linear_workspace_bytes)",
+                name, static_cast<unsigned long long>(workspace_bytes),
+                static_cast<unsigned long long>(need));
+  }
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) {
+    return fail(MVLLM_ERR_INVALID, "%s: the workspace must be 256-byte aligned", name);
+  }
+  return MVLLM_OK;
+}
+
+uint64_t mvllm_linear_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+  if (m < 1 || n < 1 || k < 64) return 0;
+  return mvllm::skinny_linear_workspace_bytes(m, n, k);
+}
+
 int mvllm_linear_pack(void* w_packed, const void* w, int64_t n, int64_t k, int32_t dtype,
                       void* stream) {
   g_error[0] = '\0';
@@ -721,20 +745,22 @@ int mvllm_linear_pack(void* w_packed, const void* w, int64_t n, int64_t k, int32
 }
 
 int mvllm_linear(void* y, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
-                 int32_t dtype, void* stream) {
+                 int32_t dtype, void* workspace, uint64_t workspace_bytes, void* stream) {
   g_error[0] = '\0';
   if (m == 0 || n == 0) return MVLLM_OK;
   int rc = check_linear("linear", x, w, m, n, k, dtype);
   if (rc != MVLLM_OK) return rc;
   if (y == nullptr) return fail(MVLLM_ERR_INVALID, "linear: a required pointer is NULL");
+  rc = check_linear_workspace("linear", m, n, k, workspace, workspace_bytes);
+  if (rc != MVLLM_OK) return rc;
   return hip_status(
-      mvllm::launch_skinny_linear(y, x, w, m, n, k, dtype, static_cast<hipStream_t>(stream)),
+      mvllm::launch_skinny_linear(y, x, w, m, n, k, dtype, workspace, static_cast<hipStream_t>(stream)),
                     "linear: launch");
 }
 
 int mvllm_linear_split(void* y0, void* y1, void* y2, const void* x, const void* w, int64_t m,
                        int64_t n0, int64_t n1, int64_t n2, int64_t k, int32_t dtype,
-                       void* stream) {
+                       void* workspace, uint64_t workspace_bytes, void* stream) {
   g_error[0] = '\0';
   if (n0 < 0 || n1 < 0 || n2 < 0) return fail(MVLLM_ERR_INVALID, "linear_split: negative size");
   if (n0 % 32 != 0 || n1 % 32 != 0) {
@@ -749,13 +775,16 @@ int mvllm_linear_split(void* y0, void* y1, void* y2, const void* x, const void* 
   if ((n0 > 0 && y0 == nullptr) || (n1 > 0 && y1 == nullptr) || (n2 > 0 && y2 == nullptr)) {
     return fail(MVLLM_ERR_INVALID, "linear_split: an output of a non-empty column group is NULL");
   }
+  rc = check_linear_workspace("linear_split", m, n, k, workspace, workspace_bytes);
+  if (rc != MVLLM_OK) return rc;
   return hip_status(mvllm::launch_skinny_linear_split(y0, y1, y2, x, w, m, n0, n1, n2, k, dtype,
-                                                      static_cast<hipStream_t>(stream)),
+                                                      workspace, static_cast<hipStream_t>(stream)),
                     "linear_split: launch");
 }
 
 int mvllm_linear_residual(void* y, const void* x, const void* w, const void* residual, int64_t m,
-                          int64_t n, int64_t k, int32_t dtype, void* stream) {
+                          int64_t n, int64_t k, int32_t dtype, void* workspace,
+                          uint64_t workspace_bytes, void* stream) {
   g_error[0] = '\0';
   if (m == 0 || n == 0) return MVLLM_OK;
   int rc = check_linear("linear_residual", x, w, m, n, k, dtype);
@@ -763,13 +792,16 @@ int mvllm_linear_residual(void* y, const void* x, const void* w, const void* res
   if (y == nullptr || residual == nullptr) {
     return fail(MVLLM_ERR_INVALID, "linear_residual: a required pointer is NULL");
   }
-  return hip_status(mvllm::launch_skinny_linear_residual(y, x, w, residual, m, n, k, dtype,
+  rc = check_linear_workspace("linear_residual", m, n, k, workspace, workspace_bytes);
+  if (rc != MVLLM_OK) return rc;
+  return hip_status(mvllm::launch_skinny_linear_residual(y, x, w, residual, m, n, k, dtype, workspace,
                                                          static_cast<hipStream_t>(stream)),
                     "linear_residual: launch");
 }
 
 int mvllm_linear_swiglu(void* y, const void* x, const void* w_gate_up, int64_t m, int64_t n_out,
-                        int64_t k, int32_t dtype, void* stream) {
+                        int64_t k, int32_t dtype, void* workspace, uint64_t workspace_bytes,
+                        void* stream) {
   g_error[0] = '\0';
   if (n_out < 0) return fail(MVLLM_ERR_INVALID, "linear_swiglu: negative size");
   if (n_out % 16 != 0) {
@@ -781,9 +813,40 @@ int mvllm_linear_swiglu(void* y, const void* x, const void* w_gate_up, int64_t m
   int rc = check_linear("linear_swiglu", x, w_gate_up, m, 2 * n_out, k, dtype);
   if (rc != MVLLM_OK) return rc;
   if (y == nullptr) return fail(MVLLM_ERR_INVALID, "linear_swiglu: a required pointer is NULL");
-  return hip_status(mvllm::launch_skinny_linear_swiglu(y, x, w_gate_up, m, n_out, k, dtype,
+  rc = check_linear_workspace("linear_swiglu", m, 2 * n_out, k, workspace, workspace_bytes);
+  if (rc != MVLLM_OK) return rc;
+  return hip_status(mvllm::launch_skinny_linear_swiglu(y, x, w_gate_up, m, n_out, k, dtype, workspace,
                                                        static_cast<hipStream_t>(stream)),
                     "linear_swiglu: launch");
+}
+
+int mvllm_linear_residual_rmsnorm(void* h_out, void* normed, const void* x, const void* w,
+                                  const void* residual, const void* norm_weight, int64_t m,
+                                  int64_t n, int64_t k, float eps, int32_t dtype, void* workspace,
+                                  uint64_t workspace_bytes, void* stream) {
+  g_error[0] = '\0';
+  if (m == 0 || n == 0) return MVLLM_OK;
+  int rc = check_linear("linear_residual_rmsnorm", x, w, m, n, k, dtype);
+  if (rc != MVLLM_OK) return rc;
+  if (!mvllm::skinny_residual_rmsnorm_supported(dtype, m, n, k)) {
+    return fail(MVLLM_ERR_UNSUPPORTED,
+                "linear_residual_rmsnorm: N=%lld K=%lld is not served; the fused norm takes K > "
+                "1024 and N a multiple of 512 up to 4096",
+                static_cast<long long>(n), static_cast<long long>(k));
+  }
+  if (h_out == nullptr || normed == nullptr || residual == nullptr || norm_weight == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "linear_residual_rmsnorm: a required pointer is NULL");
+  }
+  if ((reinterpret_cast<uintptr_t>(h_out) | reinterpret_cast<uintptr_t>(normed) |
+       reinterpret_cast<uintptr_t>(residual) | reinterpret_cast<uintptr_t>(norm_weight)) % 16 != 0) {
+    return fail(MVLLM_ERR_INVALID, "linear_residual_rmsnorm: every buffer must be 16-byte aligned");
+  }
+  rc = check_linear_workspace("linear_residual_rmsnorm", m, n, k, workspace, workspace_bytes);
+  if (rc != MVLLM_OK) return rc;
+  return hip_status(mvllm::launch_skinny_linear_residual_rmsnorm(
+                        h_out, normed, x, w, residual, norm_weight, m, n, k, eps, dtype, workspace,
+                        static_cast<hipStream_t>(stream)),
+                    "linear_residual_rmsnorm: launch");
 }
 
 int mvllm_kv_write(void* key_pool, void* value_pool, float* k_scales, float* v_scales,

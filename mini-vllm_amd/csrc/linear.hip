@@ -18,21 +18,27 @@
 //    A wave's load of a k-step is then one fully used 1 KB run (8 cache lines), where
 //    the row-major layout touches 32 lines for 32 bytes each (measured: ~2.5 us more per
 //    8 MB of cold weights). Rows past N are zero padding to the 32-row tile.
-//  * a workgroup is one tile of 32 output columns with all M rows, and 4 (K <= 1024) or
-//    8 waves that split K between them, in batches of at most 16 k-steps per wave; each
-//    wave issues every load of a batch before its first MFMA, so a projection's weights
-//    are requested up front. The waves' partial 32 x 32 sums meet in LDS. K is not split
-//    over workgroups: a cross-workgroup reduction needs device-scope release/acquire
-//    fences, which write back and invalidate L2 on this part (measured 2-3x slower).
-//    The split depends on K alone, so a column's sum is formed the same way whatever N,
-//    M or epilogue: the fused launches below equal the plain one bit for bit.
+//  * K is cut into T = 4 ceil(K / 1024) ranges of at most 16 k-steps (16 elements
+//    each), one per wave; a wave issues every load of its range before its first MFMA,
+//    so a projection's weights are requested up front. K <= 1024 (T = 4): one workgroup
+//    of 4 waves per tile of 32 output columns, the waves' 32 x 32 partial sums meeting in
+//    LDS, the epilogue in the same launch. K > 1024: T / 4 workgroups per tile (the
+//    N = 1024 projections of a decode step would otherwise run on 32 CUs), each wave
+//    writing its fp32 partial tile to a workspace, and a second launch adds the T
+//    partials and runs the epilogue - a kernel boundary, because a reduction inside one
+//    launch needs device-scope release/acquire fences, which write back and invalidate
+//    L2 on this part (measured 2-3x slower). The row-wise second launch also runs the
+//    RMSNorm that follows the o and down projections (`residual_rmsnorm`). Both add the
+//    T partials in wave order from zero, as the LDS reduction does, and the partition
+//    depends on K alone: a column's sum is formed the same way whatever N, M or
+//    epilogue, so every fused launch equals the plain one bit for bit.
 //  * B = x^T fragments (lane: row l32 of x, the same k): each wave copies its batch of
 //    x (32 or 64 rows x its k-steps) from global memory into LDS with the direct-to-LDS
 //    load (fully used 1 KB runs; x stays in L2), swizzled, and reads the fragments back
 //    from there - the same line-count argument as for W, measured ~2.5 us per projection
 //    against fragment loads straight from x. M > 32: a second 32-row block of x shares
 //    each W fragment.
-//  * epilogues, run by all threads over the LDS sums:
+//  * epilogues, over the summed tile:
 //      plain     y = T(x w^T)
 //      split     columns [0, n0) to y0, [n0, n0 + n1) to y1, the rest to y2 (the q, k
 //                and v projections as one launch over their concatenated weights)
@@ -46,6 +52,9 @@
 //    fusions save as much as the GEMM's inner loop.
 //  * rows of x past M read row M - 1 (discarded); k-steps past a wave's range re-read
 //    its last step (not summed). M0 is set only by the LDS copies.
+//  * residual_rmsnorm: h = T(r + T(x w^T)) and out = RMSNorm(h) (rounded as
+//    `rmsnorm_vec_kernel` rounds, with the same lane map and sum order, so bit for bit
+//    the unfused pair); one wave per row.
 
 #include <algorithm>
 
@@ -58,6 +67,7 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 template <typename T> struct LinMma;
 template <> struct LinMma<bf16_t> {
@@ -75,8 +85,18 @@ template <> struct LinMma<f16_t> {
   __device__ static uint16_t bits(float v) { return static_cast<uint16_t>(f32_to_f16_bits(v)); }
 };
 
-constexpr int kColTile = 32;    // output columns per workgroup (W rows)
-constexpr int kBatch = 16;      // k-steps (16 elements) a wave loads before its MFMAs
+constexpr int kColTile = 32;  // output columns per tile (W rows)
+constexpr int kSteps = 16;    // most k-steps (16 elements) of one wave, all loaded at once
+constexpr int kGroup = 4;     // waves per workgroup
+constexpr int kRowBytes = kSteps * 32;  // one x row of a wave's range in LDS
+
+// Waves over K (T): 4 per 1024 elements of K.
+int waves_of(int64_t k) { return static_cast<int>(4 * ((k / 16 + 4 * kSteps - 1) / (4 * kSteps))); }
+
+// A wave's partial 32 x 32 tile in LDS: [x row][W row], rows padded to 33 floats so
+// that both its writes (a lane's 16 values: one W row each, x row = lane) and its reads
+// (32 consecutive W rows of one x row) fall in distinct banks.
+constexpr int kPartRow = 33;
 
 struct Out {
   void* y0;
@@ -86,127 +106,75 @@ struct Out {
   int n0, n1;  // split: columns of y0 and y1
 };
 
-// Waves per workgroup for a K: 4 up to K = 1024 (one batch of 16 k-steps each), 8
-// above (two waves per SIMD still leave each 256 registers for a batch's 32 fragments).
-int waves_of(int64_t k) { return k <= 1024 ? 4 : 8; }
-
-// A wave's partial 32 x 32 tile in LDS: [x row][W row], rows padded to 33 floats so
-// that both its writes (a lane's 16 values: one W row each, x row = lane) and its reads
-// (32 consecutive W rows of one x row) fall in distinct banks.
-constexpr int kPartRow = 33;
-
-// k-steps per batch: 16, or 8 where 8 waves of two 32-row blocks of x would outgrow LDS.
-template <int MB, int WAVES> constexpr int batch_of() { return MB == 2 && WAVES == 8 ? 8 : 16; }
-
-template <typename T, int MB, int WAVES, int EPI>
-__global__ __launch_bounds__(WAVES * kWave) void skinny_linear_kernel(
-    Out out, const void* __restrict__ x, const void* __restrict__ w, int m, int n, int k) {
-  constexpr int kB = batch_of<MB, WAVES>();
-  constexpr int kRow = kB * 32;               // bytes of one x row in a batch
-  constexpr int kSlice = MB * 32 * kRow;      // one wave's x batch
-  constexpr int kPart = MB * 32 * kPartRow * 4;  // one wave's partial tile
-  constexpr int kLds = WAVES * (kSlice > kPart ? kSlice : kPart);
-  // Per wave: its batch of x rows (swizzled), then, after the K loop, its partial sums.
-  __shared__ __attribute__((aligned(1024))) char lds[kLds];
-
-  constexpr int waves = WAVES;
+// One wave's sum over its k-steps of the tile: acc[mb] is the MFMA accumulator of x rows
+// 32 mb .. 32 mb + 31. `slice` is the wave's LDS region (MB * 32 x rows of 512 bytes).
+template <typename T, int MB>
+__device__ __forceinline__ void wave_tile(f32x16 (&acc)[MB], const char* __restrict__ x,
+                                          const char* __restrict__ w, char* slice, int m, int k,
+                                          int tile, int g, int total_waves) {
   const int lane = threadIdx.x % kWave;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int l32 = lane & 31;
   const int hsel = lane >> 5;
-  const int tile = blockIdx.x;
-  const int n0 = tile * kColTile;
-
-  // This wave's k-steps [beg, beg + cnt): an even partition of the K / 16 over the waves.
+  // This wave's k-steps [beg, beg + cnt) of the K / 16, an even partition over the
+  // T waves (1 <= cnt <= 16).
   const int steps = k / 16;
-  const int beg = wave * steps / waves;
-  const int cnt = (wave + 1) * steps / waves - beg;
+  const int beg = g * steps / total_waves;
+  const int cnt = (g + 1) * steps / total_waves - beg;
 
   // The packed tile's k-step s is the 1 KB at (tile * steps + s) * 1024; this lane's
   // 16 bytes of it at lane * 16.
-  const char* wp = static_cast<const char*>(w) +
-                   (static_cast<int64_t>(tile) * steps + beg) * 1024 + lane * 16;
+  const char* wp = w + (static_cast<int64_t>(tile) * steps + beg) * 1024 + lane * 16;
+  u32x4 a[kSteps];
+#pragma unroll
+  for (int u = 0; u < kSteps; ++u) a[u] = load16(wp + static_cast<int64_t>(min(u, cnt - 1)) * 1024);
 
-  // x batches go to LDS with fully used 1 KB copies (lane i of copy j: x row
-  // j * 32/kB + i / (2 kB), 16-byte chunk c = (i % 2kB) ^ (row % 2kB), so the fragment
-  // reads below - 32 rows at one chunk each - spread over the banks) and are read back
-  // as MFMA fragments; x rows past M read row M - 1.
-  char* slice = lds + wave * kSlice;
+  // x goes to LDS with fully used 1 KB copies (lane i of copy j: x row 2 j + i / 32,
+  // 16-byte chunk c = (i % 32) ^ (row % 32), so the fragment reads below - 32 rows at
+  // one chunk each - spread over the banks) and is read back as MFMA fragments; x rows
+  // past M read row M - 1.
   const uint32_t slice_lds = lds_address(slice);
-  constexpr int kRowsPerCopy = 1024 / kRow;
-  constexpr int kCopies = MB * 32 / kRowsPerCopy;
-  const int copy_row = lane / (2 * kB);
-  const int copy_slot = lane % (2 * kB);
-
-  f32x16 acc[MB];
+  const char* xbase = x + static_cast<int64_t>(beg) * 32;
+#pragma unroll
+  for (int j = 0; j < MB * 16; ++j) {
+    const int row = 2 * j + (lane >> 5);
+    const int chunk = min(l32 ^ (row & 31), 2 * cnt - 1);
+    const uint32_t voff = static_cast<uint32_t>((min(row, m - 1) * k + 8 * chunk) * 2);
+    copy_to_lds(xbase, voff, slice_lds + j * 1024);
+  }
+  // Everything has landed (the weights from HBM arrive last anyway); the explicit wait
+  // covers the LDS copies, which the compiler does not count.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  // All fragment reads go out before the MFMAs, which then wait only for the weights.
+  u32x4 b[MB][kSteps];
+#pragma unroll
+  for (int u = 0; u < kSteps; ++u) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int c = (2 * u + hsel) ^ l32;
+      b[mb][u] = *reinterpret_cast<const u32x4*>(slice + (mb * 32 + l32) * kRowBytes + c * 16);
+    }
+  }
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x16{};
-  for (int b0 = 0; b0 < cnt; b0 += kB) {
-    const int nb = min(kB, cnt - b0);
-    const int st0 = beg + b0;
-    const char* xbase = static_cast<const char*>(x) + static_cast<int64_t>(st0) * 32;
-    u32x4 a[kB];
 #pragma unroll
-    for (int u = 0; u < kB; ++u) a[u] = load16(wp + static_cast<int64_t>(b0 + min(u, nb - 1)) * 1024);
-    // The previous batch's fragment reads are done before its slice is overwritten.
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  for (int u = 0; u < kSteps; ++u) {
+    if (u < cnt) {
 #pragma unroll
-    for (int j = 0; j < kCopies; ++j) {
-      const int row = j * kRowsPerCopy + copy_row;
-      const int chunk = min(copy_slot ^ (row & (2 * kB - 1)), 2 * nb - 1);
-      const uint32_t voff = static_cast<uint32_t>((min(row, m - 1) * k + 8 * chunk) * 2);
-      copy_to_lds(xbase, voff, slice_lds + j * 1024);
-    }
-    // Everything of the batch has landed (the weights from HBM arrive last anyway); the
-    // explicit wait covers the LDS copies, which the compiler does not count.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    // All fragment reads go out before the MFMAs, which then wait only for the weights.
-    u32x4 b[MB][kB];
-#pragma unroll
-    for (int u = 0; u < kB; ++u) {
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const int c = (2 * u + hsel) ^ (l32 & (2 * kB - 1));
-        b[mb][u] = *reinterpret_cast<const u32x4*>(slice + (mb * 32 + l32) * kRow + c * 16);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kB; ++u) {
-      if (u < nb) {
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) acc[mb] = LinMma<T>::run(a[u], b[mb][u], acc[mb]);
-      }
+      for (int mb = 0; mb < MB; ++mb) acc[mb] = LinMma<T>::run(a[u], b[mb][u], acc[mb]);
     }
   }
+}
 
-  // Every wave is past its last read of its x slice before the partial sums reuse LDS.
-  __syncthreads();
-  // Accumulator element r of lane (l32, hsel) is C[W row 8(r/4) + 4 hsel + r%4][x row
-  // l32]; it goes to part[wave][mb][x row][W row].
-  float* part = reinterpret_cast<float*>(lds);
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    float* dst = part + ((wave * MB + mb) * 32 + l32) * kPartRow + 4 * hsel;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) dst[8 * (r / 4) + r % 4] = acc[mb][r];
-  }
-  __syncthreads();
-
-  // The sum over the waves (in order) of C[col][row] of this tile.
-  auto total = [&](int row, int col) __attribute__((always_inline)) {
-    const float* src = part + ((row / 32) * 32 + row % 32) * kPartRow + col;
-    float sum = 0.0f;
-#pragma unroll
-    for (int wv = 0; wv < waves; ++wv) sum += src[wv * MB * 32 * kPartRow];
-    return sum;
-  };
-
+// The epilogue of one tile over `total(row, col)`, the summed x w^T (fp32).
+template <typename T, int MB, int EPI, typename Total>
+__device__ __forceinline__ void epilogue(const Out& out, int tile, int m, int n, Total total) {
+  const int nthreads = kGroup * kWave;
   if constexpr (EPI == kLinearSwiglu) {
     // 16 output columns per tile: gate col j pairs with up col 16 + j.
     const int nout = n / 2;
     uint16_t* yo = static_cast<uint16_t*>(out.y0);
-    for (int e = threadIdx.x; e < MB * 32 * 16; e += WAVES * kWave) {
+    for (int e = threadIdx.x; e < MB * 32 * 16; e += nthreads) {
       const int j = e % 16, row = e / 16;
       const int gcol = tile * 16 + j;
       if (row >= m || gcol >= nout) continue;
@@ -215,7 +183,8 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_linear_kernel(
       yo[static_cast<int64_t>(row) * nout + gcol] = LinMma<T>::bits(swiglu_one<T>(g, u));
     }
   } else {
-    for (int e = threadIdx.x; e < MB * 32 * kColTile; e += WAVES * kWave) {
+    const int n0 = tile * kColTile;
+    for (int e = threadIdx.x; e < MB * 32 * kColTile; e += nthreads) {
       const int col = e % kColTile, row = e / kColTile;
       const int gcol = n0 + col;
       if (row >= m || gcol >= n) continue;
@@ -240,32 +209,247 @@ __global__ __launch_bounds__(WAVES * kWave) void skinny_linear_kernel(
   }
 }
 
+// K <= 1024: one workgroup of 4 waves per tile, reduction in LDS, epilogue in place.
+template <typename T, int MB, int EPI>
+__global__ __launch_bounds__(kGroup * kWave) void skinny_linear_kernel(
+    Out out, const void* __restrict__ x, const void* __restrict__ w, int m, int n, int k) {
+  constexpr int kSlice = MB * 32 * kRowBytes;
+  __shared__ __attribute__((aligned(1024))) char lds[kGroup * kSlice];
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int l32 = lane & 31;
+  const int hsel = lane >> 5;
+  f32x16 acc[MB];
+  wave_tile<T, MB>(acc, static_cast<const char*>(x), static_cast<const char*>(w),
+                   lds + wave * kSlice, m, k, blockIdx.x, wave, kGroup);
+
+  // Every wave is past its last read of its x slice before the partial sums reuse LDS.
+  __syncthreads();
+  // Accumulator element r of lane (l32, hsel) is C[W row 8(r/4) + 4 hsel + r%4][x row
+  // l32]; it goes to part[wave][mb][x row][W row].
+  float* part = reinterpret_cast<float*>(lds);
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    float* dst = part + ((wave * MB + mb) * 32 + l32) * kPartRow + 4 * hsel;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dst[8 * (r / 4) + r % 4] = acc[mb][r];
+  }
+  __syncthreads();
+  // The sum over the waves (in order, from zero) of C[col][row] of this tile.
+  auto total = [&](int row, int col) __attribute__((always_inline)) {
+    const float* src = part + row * kPartRow + col;
+    float sum = 0.0f;
+#pragma unroll
+    for (int wv = 0; wv < kGroup; ++wv) sum += src[wv * MB * 32 * kPartRow];
+    return sum;
+  };
+  epilogue<T, MB, EPI>(out, blockIdx.x, m, n, total);
+}
+
+// K > 1024: wave g = 4 blockIdx.y + wave of the T writes its fp32 partial tile to
+// partials[tile][g][x row][col] (MB * 32 x rows).
+template <typename T, int MB>
+__global__ __launch_bounds__(kGroup * kWave) void skinny_partial_kernel(
+    float* __restrict__ partials, const void* __restrict__ x, const void* __restrict__ w, int m,
+    int k, int total_waves) {
+  constexpr int kSlice = MB * 32 * kRowBytes;
+  __shared__ __attribute__((aligned(1024))) char lds[kGroup * kSlice];
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int l32 = lane & 31;
+  const int hsel = lane >> 5;
+  const int g = blockIdx.y * kGroup + wave;
+  f32x16 acc[MB];
+  wave_tile<T, MB>(acc, static_cast<const char*>(x), static_cast<const char*>(w),
+                   lds + wave * kSlice, m, k, blockIdx.x, g, total_waves);
+  float* dst = partials + (static_cast<int64_t>(blockIdx.x) * total_waves + g) * (MB * 32 * kColTile);
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    float* row = dst + (mb * 32 + l32) * kColTile + 4 * hsel;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      *reinterpret_cast<f32x4*>(row + 8 * q) =
+          f32x4{acc[mb][4 * q], acc[mb][4 * q + 1], acc[mb][4 * q + 2], acc[mb][4 * q + 3]};
+    }
+  }
+}
+
+// Adds T partial float4s, `stride` floats apart, in order from zero: eight loads in
+// flight at a time, the additions sequential (the LDS reduction's order).
+__device__ __forceinline__ f32x4 sum_partials(const float* __restrict__ src, int64_t stride,
+                                              int total_waves) {
+  f32x4 sum = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  int g = 0;
+  for (; g + 8 <= total_waves; g += 8) {
+    f32x4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const f32x4*>(src + (g + i) * stride);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum[e] = sum[e] + v[i][e];
+    }
+  }
+  for (; g < total_waves; ++g) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(src + g * stride);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sum[e] = sum[e] + v[e];
+  }
+  return sum;
+}
+
+// K > 1024, tile epilogues: one workgroup per tile adds the T partials in wave order
+// (four columns per thread) into LDS, then runs the epilogue.
+template <typename T, int MB, int EPI>
+__global__ __launch_bounds__(kGroup * kWave) void skinny_reduce_kernel(
+    Out out, const float* __restrict__ partials, int m, int n, int total_waves) {
+  constexpr int kTile = MB * 32 * kColTile;
+  __shared__ float tot[kTile];
+  const float* base = partials + static_cast<int64_t>(blockIdx.x) * total_waves * kTile;
+  for (int e4 = threadIdx.x; e4 < kTile / 4; e4 += kGroup * kWave) {
+    *reinterpret_cast<f32x4*>(tot + 4 * e4) = sum_partials(base + 4 * e4, kTile, total_waves);
+  }
+  __syncthreads();
+  auto total = [&](int row, int col) __attribute__((always_inline)) {
+    return tot[row * kColTile + col];
+  };
+  epilogue<T, MB, EPI>(out, blockIdx.x, m, n, total);
+}
+
+// K > 1024, residual + RMSNorm: one wave per x row, lane r holding 8-column chunks
+// r, r + 64, ... (the lane map of rmsnorm_vec_kernel<T, 64, kCh>): h = T(r + T(sum)),
+// then out = T(T(h * inv) * weight) with inv from the lane-ordered fma sum of squares
+// reduced by group_sum<64>, as that kernel computes it.
+template <typename T, int MB, int kCh>
+__global__ __launch_bounds__(kGroup * kWave) void skinny_reduce_norm_kernel(
+    void* __restrict__ h_out, void* __restrict__ normed, const float* __restrict__ partials,
+    const void* __restrict__ residual, const void* __restrict__ norm_weight, int m, int n,
+    int total_waves, float eps) {
+  const int row = blockIdx.x * kGroup + threadIdx.x / kWave;
+  const int r = threadIdx.x % kWave;
+  if (row >= m) return;  // a whole wave: no barrier below
+  const int64_t tile_stride = static_cast<int64_t>(total_waves) * (MB * 32 * kColTile);
+  const int chunks = n / 8;
+  const char* res = static_cast<const char*>(residual) + static_cast<int64_t>(row) * n * 2;
+  char* hrow = static_cast<char*>(h_out) + static_cast<int64_t>(row) * n * 2;
+  u32x4 held[kCh];
+  float sumsq = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    const int chunk = r + c * kWave;
+    if (chunk < chunks) {
+      const int col = chunk * 8;
+      const float* src = partials + (col / kColTile) * tile_stride + row * kColTile + col % kColTile;
+      const f32x4 s0 = sum_partials(src, MB * 32 * kColTile, total_waves);
+      const f32x4 s1 = sum_partials(src + 4, MB * 32 * kColTile, total_waves);
+      float rf[8];
+      Chunk<T>::unpack(load16(res + col * 2), rf);
+      float f[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float sum = e < 4 ? s0[e] : s1[e - 4];
+        f[e] = Elem<T>::round(rf[e] + Elem<T>::round(sum));
+      }
+      u32x4 hv;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        hv[e / 2] = static_cast<uint32_t>(LinMma<T>::bits(f[e])) |
+                    (static_cast<uint32_t>(LinMma<T>::bits(f[e + 1])) << 16);
+      }
+      held[c] = hv;
+      store16(hrow + col * 2, hv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sumsq = fmaf(f[e], f[e], sumsq);
+    }
+  }
+  sumsq = group_sum<kWave>(sumsq);
+  const float inv = rsqrtf(sumsq / static_cast<float>(n) + eps);
+  char* orow = static_cast<char*>(normed) + static_cast<int64_t>(row) * n * 2;
+  const char* wr = static_cast<const char*>(norm_weight);
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    const int chunk = r + c * kWave;
+    if (chunk < chunks) {
+      float f[8], wf[8];
+      Chunk<T>::unpack(held[c], f);
+      Chunk<T>::unpack(load16(wr + chunk * 16), wf);
+      u32x4 res_v;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        float o2[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const float normalized = Elem<T>::round(__fmul_rn(f[e + q], inv));
+          o2[q] = __fmul_rn(normalized, wf[e + q]);
+        }
+        res_v[e / 2] = static_cast<uint32_t>(LinMma<T>::bits(o2[0])) |
+                       (static_cast<uint32_t>(LinMma<T>::bits(o2[1])) << 16);
+      }
+      store16(orow + chunk * 16, res_v);
+    }
+  }
+}
+
+int row_blocks(int64_t m) { return m <= 32 ? 1 : 2; }
+
 template <typename T, int MB, int EPI>
 hipError_t launch_m(const Out& out, const void* x, const void* w, int m, int n, int k,
-                    hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>((n + kColTile - 1) / kColTile));
-  if (waves_of(k) == 4) {
-    skinny_linear_kernel<T, MB, 4, EPI><<<grid, 4 * kWave, 0, stream>>>(out, x, w, m, n, k);
-  } else {
-    skinny_linear_kernel<T, MB, 8, EPI><<<grid, 8 * kWave, 0, stream>>>(out, x, w, m, n, k);
+                    void* workspace, hipStream_t stream) {
+  const unsigned tiles = static_cast<unsigned>((n + kColTile - 1) / kColTile);
+  const int t_waves = waves_of(k);
+  if (t_waves == kGroup) {
+    skinny_linear_kernel<T, MB, EPI><<<tiles, kGroup * kWave, 0, stream>>>(out, x, w, m, n, k);
+    return hipGetLastError();
   }
+  float* partials = static_cast<float*>(workspace);
+  skinny_partial_kernel<T, MB><<<dim3(tiles, t_waves / kGroup), kGroup * kWave, 0, stream>>>(
+      partials, x, w, m, k, t_waves);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  skinny_reduce_kernel<T, MB, EPI><<<tiles, kGroup * kWave, 0, stream>>>(out, partials, m, n, t_waves);
   return hipGetLastError();
 }
 
 template <typename T, int EPI>
 hipError_t launch_t(const Out& out, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
-                    hipStream_t stream) {
+                    void* workspace, hipStream_t stream) {
   const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
-  if (m <= 32) return launch_m<T, 1, EPI>(out, x, w, mi, ni, ki, stream);
-  return launch_m<T, 2, EPI>(out, x, w, mi, ni, ki, stream);
+  if (row_blocks(m) == 1) return launch_m<T, 1, EPI>(out, x, w, mi, ni, ki, workspace, stream);
+  return launch_m<T, 2, EPI>(out, x, w, mi, ni, ki, workspace, stream);
 }
 
 template <int EPI>
 hipError_t launch_e(const Out& out, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
-                    int dtype, hipStream_t stream) {
-  if (dtype == kBF16) return launch_t<bf16_t, EPI>(out, x, w, m, n, k, stream);
-  if (dtype == kF16) return launch_t<f16_t, EPI>(out, x, w, m, n, k, stream);
+                    int dtype, void* workspace, hipStream_t stream) {
+  if (dtype == kBF16) return launch_t<bf16_t, EPI>(out, x, w, m, n, k, workspace, stream);
+  if (dtype == kF16) return launch_t<f16_t, EPI>(out, x, w, m, n, k, workspace, stream);
   return hipErrorInvalidValue;
+}
+
+template <typename T, int MB>
+hipError_t launch_norm_m(void* h_out, void* normed, const void* x, const void* w, const void* residual,
+                         const void* norm_weight, int m, int n, int k, float eps, void* workspace,
+                         hipStream_t stream) {
+  const unsigned tiles = static_cast<unsigned>((n + kColTile - 1) / kColTile);
+  const int t_waves = waves_of(k);
+  float* partials = static_cast<float*>(workspace);
+  skinny_partial_kernel<T, MB><<<dim3(tiles, t_waves / kGroup), kGroup * kWave, 0, stream>>>(
+      partials, x, w, m, k, t_waves);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const unsigned rows = static_cast<unsigned>((m + kGroup - 1) / kGroup);
+  const int per_lane = n / 8 / kWave;
+  if (per_lane <= 2) {
+    skinny_reduce_norm_kernel<T, MB, 2><<<rows, kGroup * kWave, 0, stream>>>(
+        h_out, normed, partials, residual, norm_weight, m, n, t_waves, eps);
+  } else if (per_lane <= 4) {
+    skinny_reduce_norm_kernel<T, MB, 4><<<rows, kGroup * kWave, 0, stream>>>(
+        h_out, normed, partials, residual, norm_weight, m, n, t_waves, eps);
+  } else {
+    skinny_reduce_norm_kernel<T, MB, 8><<<rows, kGroup * kWave, 0, stream>>>(
+        h_out, normed, partials, residual, norm_weight, m, n, t_waves, eps);
+  }
+  return hipGetLastError();
 }
 
 // Packs W [n, k] (row-major) into the fragment order: one thread per 16 bytes.
@@ -293,6 +477,18 @@ bool skinny_linear_supported(int dtype, int64_t m, int64_t n, int64_t k) {
          k % 64 == 0 && k <= kSkinnyMaxK;
 }
 
+bool skinny_residual_rmsnorm_supported(int dtype, int64_t m, int64_t n, int64_t k) {
+  return skinny_linear_supported(dtype, m, n, k) && waves_of(k) > kGroup && n % 512 == 0 &&
+         n <= 4096;
+}
+
+uint64_t skinny_linear_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+  const int t_waves = waves_of(k);
+  if (t_waves == kGroup) return 0;
+  const uint64_t tiles = static_cast<uint64_t>((n + kColTile - 1) / kColTile);
+  return tiles * t_waves * row_blocks(m) * 32 * kColTile * sizeof(float);
+}
+
 int64_t skinny_linear_packed_elements(int64_t n, int64_t k) {
   return (n + kColTile - 1) / kColTile * kColTile * k;
 }
@@ -307,28 +503,49 @@ hipError_t launch_skinny_linear_pack(void* w_packed, const void* w, int64_t n, i
 }
 
 hipError_t launch_skinny_linear(void* y, const void* x, const void* w, int64_t m, int64_t n,
-                                int64_t k, int dtype, hipStream_t stream) {
-  return launch_e<kLinearPlain>(Out{y, nullptr, nullptr, nullptr, 0, 0}, x, w, m, n, k, dtype, stream);
+                                int64_t k, int dtype, void* workspace, hipStream_t stream) {
+  return launch_e<kLinearPlain>(Out{y, nullptr, nullptr, nullptr, 0, 0}, x, w, m, n, k, dtype,
+                                workspace, stream);
 }
 
 hipError_t launch_skinny_linear_split(void* y0, void* y1, void* y2, const void* x, const void* w,
                                       int64_t m, int64_t n0, int64_t n1, int64_t n2, int64_t k,
-                                      int dtype, hipStream_t stream) {
+                                      int dtype, void* workspace, hipStream_t stream) {
   return launch_e<kLinearSplit>(Out{y0, y1, y2, nullptr, static_cast<int>(n0), static_cast<int>(n1)},
-                                x, w, m, n0 + n1 + n2, k, dtype, stream);
+                                x, w, m, n0 + n1 + n2, k, dtype, workspace, stream);
 }
 
 hipError_t launch_skinny_linear_residual(void* y, const void* x, const void* w, const void* residual,
                                          int64_t m, int64_t n, int64_t k, int dtype,
-                                         hipStream_t stream) {
+                                         void* workspace, hipStream_t stream) {
   return launch_e<kLinearResidual>(Out{y, nullptr, nullptr, residual, 0, 0}, x, w, m, n, k, dtype,
-                                   stream);
+                                   workspace, stream);
 }
 
 hipError_t launch_skinny_linear_swiglu(void* y, const void* x, const void* w_gate_up, int64_t m,
-                                       int64_t n_out, int64_t k, int dtype, hipStream_t stream) {
+                                       int64_t n_out, int64_t k, int dtype, void* workspace,
+                                       hipStream_t stream) {
   return launch_e<kLinearSwiglu>(Out{y, nullptr, nullptr, nullptr, 0, 0}, x, w_gate_up, m, 2 * n_out,
-                                 k, dtype, stream);
+                                 k, dtype, workspace, stream);
+}
+
+hipError_t launch_skinny_linear_residual_rmsnorm(void* h_out, void* normed, const void* x,
+                                                 const void* w, const void* residual,
+                                                 const void* norm_weight, int64_t m, int64_t n,
+                                                 int64_t k, float eps, int dtype, void* workspace,
+                                                 hipStream_t stream) {
+  const int mi = static_cast<int>(m), ni = static_cast<int>(n), ki = static_cast<int>(k);
+  if (dtype == kBF16) {
+    return row_blocks(m) == 1
+               ? launch_norm_m<bf16_t, 1>(h_out, normed, x, w, residual, norm_weight, mi, ni, ki, eps, workspace, stream)
+               : launch_norm_m<bf16_t, 2>(h_out, normed, x, w, residual, norm_weight, mi, ni, ki, eps, workspace, stream);
+  }
+  if (dtype == kF16) {
+    return row_blocks(m) == 1
+               ? launch_norm_m<f16_t, 1>(h_out, normed, x, w, residual, norm_weight, mi, ni, ki, eps, workspace, stream)
+               : launch_norm_m<f16_t, 2>(h_out, normed, x, w, residual, norm_weight, mi, ni, ki, eps, workspace, stream);
+  }
+  return hipErrorInvalidValue;
 }
 
 }  // namespace mvllm

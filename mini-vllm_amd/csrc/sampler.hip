@@ -55,7 +55,7 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(int64_t* __restr
   if (vec) {
     // 16-byte chunks: 16 / sizeof(T) elements each, all loads of the thread first.
     constexpr int kPer = 16 / sizeof(T);
-    constexpr int kAhead = 8;
+    constexpr int kAhead = 24;  // a 196608-element bf16 row in one batch
     const int64_t chunks = v / kPer;
     for (int64_t c0 = threadIdx.x; c0 < chunks; c0 += kAhead * kArgmaxThreads) {
       u32x4 w[kAhead];

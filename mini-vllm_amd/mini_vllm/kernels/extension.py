@@ -59,7 +59,7 @@ HIP_FLAGS = [
 # reference's PyTorch expressions round, so FMA contraction is off there.
 EXTRA_FLAGS = {"elementwise.hip": ["-ffp-contract=off"], "linear.hip": ["-ffp-contract=off"]}
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_CODES: dict[torch.dtype, int] = {
     torch.float32: 0,
@@ -207,14 +207,18 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_argmax.argtypes = [p, p, i64, i64, i64, i32, p]
     lib.mvllm_linear_pack.restype = ctypes.c_int
     lib.mvllm_linear_pack.argtypes = [p, p, i64, i64, i32, p]
+    lib.mvllm_linear_workspace_bytes.restype = u64
+    lib.mvllm_linear_workspace_bytes.argtypes = [i64, i64, i64]
     lib.mvllm_linear.restype = ctypes.c_int
-    lib.mvllm_linear.argtypes = [p, p, p, i64, i64, i64, i32, p]
+    lib.mvllm_linear.argtypes = [p, p, p, i64, i64, i64, i32, p, u64, p]
     lib.mvllm_linear_split.restype = ctypes.c_int
-    lib.mvllm_linear_split.argtypes = [p, p, p, p, p, i64, i64, i64, i64, i64, i32, p]
+    lib.mvllm_linear_split.argtypes = [p, p, p, p, p, i64, i64, i64, i64, i64, i32, p, u64, p]
     lib.mvllm_linear_residual.restype = ctypes.c_int
-    lib.mvllm_linear_residual.argtypes = [p, p, p, p, i64, i64, i64, i32, p]
+    lib.mvllm_linear_residual.argtypes = [p, p, p, p, i64, i64, i64, i32, p, u64, p]
     lib.mvllm_linear_swiglu.restype = ctypes.c_int
-    lib.mvllm_linear_swiglu.argtypes = [p, p, p, i64, i64, i64, i32, p]
+    lib.mvllm_linear_swiglu.argtypes = [p, p, p, i64, i64, i64, i32, p, u64, p]
+    lib.mvllm_linear_residual_rmsnorm.restype = ctypes.c_int
+    lib.mvllm_linear_residual_rmsnorm.argtypes = [p, p, p, p, p, p, i64, i64, i64, f32, i32, p, u64, p]
 
 
 EXPORTED_SYMBOLS = (
@@ -232,6 +236,8 @@ EXPORTED_SYMBOLS = (
     "mvllm_dense_attention_plan",
     "mvllm_dense_attention",
     "mvllm_linear_pack",
+    "mvllm_linear_workspace_bytes",
+    "mvllm_linear_residual_rmsnorm",
     "mvllm_linear",
     "mvllm_linear_split",
     "mvllm_linear_residual",
@@ -269,9 +275,11 @@ class HipExtension:
         self.lib = lib
         self.path = LIB_PATH
         self._workspaces: dict[tuple[int, int], torch.Tensor] = {}
+        self._retired: list[torch.Tensor] = []
 
     def workspace(self, device: torch.device, nbytes: int) -> torch.Tensor:
-        """The paged-attention workspace of (device, current stream), grown on demand.
+        """The kernels' workspace of (device, current stream), grown on demand (paged and
+        dense attention, split projections).
 
         Kept rather than allocated per call so a steady decode loop (or a captured
         graph) reuses one buffer; calls on one stream are ordered, so they never race.
@@ -282,6 +290,8 @@ class HipExtension:
         if ws is None or ws.numel() < nbytes:
             size = max(nbytes, 2 * ws.numel() if ws is not None else 0)
             size = (size + (1 << 20) - 1) >> 20 << 20
+            if ws is not None:
+                self._retired.append(ws)  # a captured graph may still name it
             ws = torch.empty(size, dtype=torch.uint8, device=device)
             self._workspaces[key] = ws
         return ws
@@ -509,6 +519,15 @@ class HipExtension:
                 f"{w_packed.numel()} {w_packed.dtype} elements is not served by the skinny kernel "
                 "(at most 64 contiguous f16/bf16 rows, K a multiple of 64 up to 65536)")
 
+    def _linear_ws(self, x: torch.Tensor, n: int) -> tuple[int, int]:
+        """(pointer, bytes) of the partial-sum workspace of x (M x K) against n rows of
+        weights: none for K <= 1024, else the stream's shared workspace."""
+        need = int(self.lib.mvllm_linear_workspace_bytes(x.shape[0], n, x.shape[1]))
+        if need == 0:
+            return 0, 0
+        ws = self.workspace(x.device, need)
+        return ws.data_ptr(), ws.numel()
+
     def linear(self, x: torch.Tensor, w_packed: torch.Tensor, n: int) -> torch.Tensor:
         """``x @ W.T`` for ``x`` M x K (M <= 64) and W (n x K) packed: the skinny projection
         kernel (fp32 accumulation, one rounding)."""
@@ -516,7 +535,7 @@ class HipExtension:
         y = torch.empty((x.shape[0], n), dtype=x.dtype, device=x.device)
         self._check(self.lib.mvllm_linear(y.data_ptr(), x.data_ptr(), w_packed.data_ptr(),
                                           x.shape[0], n, x.shape[1], DTYPE_CODES[x.dtype],
-                                          _stream(x.device)))
+                                          *self._linear_ws(x, n), _stream(x.device)))
         return y
 
     def linear_split(self, x: torch.Tensor, w_packed: torch.Tensor,
@@ -532,7 +551,7 @@ class HipExtension:
         ns = list(sizes) + [0] * (3 - len(sizes))
         self._check(self.lib.mvllm_linear_split(*ptrs, x.data_ptr(), w_packed.data_ptr(),
                                                 x.shape[0], *ns, x.shape[1], DTYPE_CODES[x.dtype],
-                                                _stream(x.device)))
+                                                *self._linear_ws(x, sum(sizes)), _stream(x.device)))
         return tuple(outs)
 
     def linear_residual(self, x: torch.Tensor, w_packed: torch.Tensor,
@@ -547,7 +566,8 @@ class HipExtension:
         y = torch.empty_like(residual)
         self._check(self.lib.mvllm_linear_residual(y.data_ptr(), x.data_ptr(), w_packed.data_ptr(),
                                                    residual.data_ptr(), x.shape[0], n, x.shape[1],
-                                                   DTYPE_CODES[x.dtype], _stream(x.device)))
+                                                   DTYPE_CODES[x.dtype], *self._linear_ws(x, n),
+                                                   _stream(x.device)))
         return y
 
     def linear_swiglu(self, x: torch.Tensor, w_packed: torch.Tensor, n_out: int) -> torch.Tensor:
@@ -559,8 +579,37 @@ class HipExtension:
         y = torch.empty((x.shape[0], n_out), dtype=x.dtype, device=x.device)
         self._check(self.lib.mvllm_linear_swiglu(y.data_ptr(), x.data_ptr(), w_packed.data_ptr(),
                                                  x.shape[0], n_out, x.shape[1], DTYPE_CODES[x.dtype],
-                                                 _stream(x.device)))
+                                                 *self._linear_ws(x, 2 * n_out), _stream(x.device)))
         return y
+
+    @staticmethod
+    def linear_residual_rmsnorm_supported(x: torch.Tensor, n: int) -> bool:
+        """Whether ``linear_residual_rmsnorm`` serves x (M x K) against n weight rows:
+        K > 1024 and n a multiple of 512 up to 4096 (beyond ``linear_supported``)."""
+        return x.dim() == 2 and x.shape[1] > 1024 and n % 512 == 0 and n <= 4096
+
+    def linear_residual_rmsnorm(self, x: torch.Tensor, w_packed: torch.Tensor,
+                                residual: torch.Tensor, norm_weight: torch.Tensor,
+                                eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+        """(h, normed): h = residual + x @ W.T and normed = rmsnorm(h, norm_weight, eps),
+        each bit for bit its unfused op, in two launches."""
+        n = residual.shape[-1]
+        self._require("linear_residual_rmsnorm", x, w_packed, n)
+        if not self.linear_residual_rmsnorm_supported(x, n):
+            raise RuntimeError(f"linear_residual_rmsnorm: N={n} K={x.shape[1]} is not served "
+                               "(K > 1024, N a multiple of 512 up to 4096)")
+        if (residual.shape != (x.shape[0], n) or residual.dtype != x.dtype or not residual.is_contiguous()
+                or norm_weight.shape != (n,) or norm_weight.dtype != x.dtype
+                or not norm_weight.is_contiguous()):
+            raise RuntimeError("linear_residual_rmsnorm: residual must be a contiguous M x N tensor "
+                               "and norm_weight a contiguous N vector, both of x's dtype")
+        h = torch.empty_like(residual)
+        normed = torch.empty_like(residual)
+        self._check(self.lib.mvllm_linear_residual_rmsnorm(
+            h.data_ptr(), normed.data_ptr(), x.data_ptr(), w_packed.data_ptr(), residual.data_ptr(),
+            norm_weight.data_ptr(), x.shape[0], n, x.shape[1], float(eps), DTYPE_CODES[x.dtype],
+            *self._linear_ws(x, n), _stream(x.device)))
+        return h, normed
 
     def qk_norm_rope_supported(self, dtype: torch.dtype, head_dim: int) -> bool:
         """Whether the fused kernel serves this dtype / head dim (16-byte chunks per head

@@ -50,6 +50,7 @@ __all__ = [
     "PackedWeight",
     "linear",
     "linear_residual",
+    "linear_residual_rmsnorm",
     "linear_split",
     "linear_swiglu",
     "pack_weight",
@@ -255,6 +256,22 @@ def linear_residual(x: torch.Tensor, w: PackedWeight, residual: torch.Tensor,
     if ext is not None and residual.is_contiguous() and residual.dtype == x.dtype:
         return ext.linear_residual(x, w.packed, residual)
     return residual + x @ w.dense.t()
+
+
+def linear_residual_rmsnorm(x: torch.Tensor, w: PackedWeight, residual: torch.Tensor,
+                            norm_weight: torch.Tensor, eps: float = 1e-6,
+                            use_cuda: bool = False) -> tuple[torch.Tensor, torch.Tensor] | None:
+    """(h, rmsnorm(h)) for h = residual + x @ w.T, bit for bit ``linear_residual`` then
+    ``rmsnorm``, in two launches (``csrc/linear.hip``: split partial sums, then a row
+    reduction that adds the residual and normalises). None where the kernel does not
+    serve the shape (K <= 1024, N not a multiple of 512, ...): the caller runs the two
+    ops. Not dispatched on the PyTorch path either (None)."""
+    ext = _skinny_ext(x, w, w.shape[0], use_cuda)
+    if (ext is None or not ext.linear_residual_rmsnorm_supported(x, w.shape[0])
+            or not residual.is_contiguous() or residual.dtype != x.dtype
+            or norm_weight.dtype != x.dtype or not norm_weight.is_contiguous()):
+        return None
+    return ext.linear_residual_rmsnorm(x, w.packed, residual, norm_weight, eps)
 
 
 def linear_swiglu(x: torch.Tensor, w_gate_up: PackedWeight, use_cuda: bool = False) -> torch.Tensor:

@@ -138,9 +138,9 @@ class Qwen3Paged:
         self.lm_head = (ops.pack_weight(weights["embedding"], use_cuda=True) if use_cuda
                         else weights["embedding"])
 
-    def _attention(self, layer: int, w: dict, p: dict, x: torch.Tensor, batch, h: torch.Tensor,
+    def _attention(self, layer: int, w: dict, p: dict, x: torch.Tensor, batch,
                    fused: bool) -> torch.Tensor:
-        """``h + attention(x)``: the residual add rides in the o-projection when fused."""
+        """The attention output (``T x H_q D``) of normed input x, before ``wo``."""
         c = self.config
         t = x.shape[0]
         u = self.use_cuda
@@ -161,9 +161,22 @@ class Qwen3Paged:
             batch.cu_seqlens_q, batch.context_lens, batch.seq_lens, batch.max_query_len,
             batch.max_context_len, 1.0 / math.sqrt(c.head_dim), use_cuda=u,
             k_scale=k_scale, v_scale=v_scale)
+        return out.view(t, c.q_size)
+
+    def _residual_norm(self, x: torch.Tensor, pw, dense_w: torch.Tensor, h: torch.Tensor,
+                       norm_w: torch.Tensor, fused: bool) -> tuple[torch.Tensor, torch.Tensor]:
+        """(h + x w^T, rmsnorm of that): the o and down projections with the norm that
+        follows each, fused into the projection's reduction when the kernels serve it."""
+        c = self.config
+        u = self.use_cuda
         if fused:
-            return ops.linear_residual(out.view(t, c.q_size), p["o"], h, use_cuda=u)
-        return h + ops.linear(out.view(t, c.q_size), w["wo"], use_cuda=u)
+            both = ops.linear_residual_rmsnorm(x, pw, h, norm_w, c.rms_norm_eps, use_cuda=u)
+            if both is not None:
+                return both
+            h = ops.linear_residual(x, pw, h, use_cuda=u)
+        else:
+            h = h + ops.linear(x, dense_w, use_cuda=u)
+        return h, ops.rmsnorm(h, norm_w, c.rms_norm_eps, use_cuda=u)
 
     @torch.no_grad()
     def __call__(self, batch) -> torch.Tensor:
@@ -171,17 +184,22 @@ class Qwen3Paged:
         u = self.use_cuda
         h = self.weights["embedding"].index_select(0, batch.input_ids)
         fused = u and ops.skinny(h, use_cuda=u)
+        n_layers = len(self.layers)
+        normed = ops.rmsnorm(h, self.layers[0]["attn_norm"], c.rms_norm_eps, use_cuda=u)
         for layer, (w, p) in enumerate(zip(self.layers, self.packed)):
-            normed = ops.rmsnorm(h, w["attn_norm"], c.rms_norm_eps, use_cuda=u)
-            h = self._attention(layer, w, p, normed, batch, h, fused)
-            normed = ops.rmsnorm(h, w["mlp_norm"], c.rms_norm_eps, use_cuda=u)
+            # normed = attn_norm(h) of this layer, computed by the previous layer's
+            # down projection (or above, for the first layer).
+            out = self._attention(layer, w, p, normed, batch, fused)
+            h, normed = self._residual_norm(out, p.get("o"), w["wo"], h, w["mlp_norm"], fused)
             if fused and "gate_up" in p:
-                h = ops.linear_residual(ops.linear_swiglu(normed, p["gate_up"], use_cuda=u),
-                                        p["down"], h, use_cuda=u)
+                gated = ops.linear_swiglu(normed, p["gate_up"], use_cuda=u)
             else:
                 gated = ops.swiglu(ops.linear(normed, w["gate"], use_cuda=u),
                                    ops.linear(normed, w["up"], use_cuda=u), use_cuda=u)
-                h = h + ops.linear(gated, w["down"], use_cuda=u)
-        h = h.index_select(0, batch.last_row_indices)
-        h = ops.rmsnorm(h, self.weights["final_norm"], c.rms_norm_eps, use_cuda=u)
-        return ops.linear(h, self.lm_head, use_cuda=u)
+            next_norm = (self.layers[layer + 1]["attn_norm"] if layer + 1 < n_layers
+                         else self.weights["final_norm"])
+            h, normed = self._residual_norm(gated, p.get("down"), w["down"], h, next_norm, fused)
+        # normed is now final_norm(h) of every row; RMSNorm is row-wise, so selecting the
+        # last rows after it equals normalising them after the selection.
+        normed = normed.index_select(0, batch.last_row_indices)
+        return ops.linear(normed, self.lm_head, use_cuda=u)

@@ -134,23 +134,36 @@ def test_known_answer_identity(extension, device):
 
 
 def test_c_abi_refusals(extension, device):
-    """Shapes and dtypes the kernel does not serve are refused by the library, not run."""
+    """Shapes and dtypes the kernel does not serve are refused by the library, not run,
+    and so is a K > 1024 call without its partial-sum workspace."""
     x, w, _ = _operands(4, 64, 128, torch.bfloat16, 6)
     packed = extension.linear_pack(w)
     y = torch.empty(4, 64, dtype=torch.bfloat16, device="cuda")
     stream = torch.cuda.current_stream().cuda_stream
     bf16 = DTYPE_CODES[torch.bfloat16]
     lib = extension.lib
-    assert lib.mvllm_linear(y.data_ptr(), x.data_ptr(), packed.data_ptr(), 65, 64, 128, bf16, stream) == 2
-    assert lib.mvllm_linear(y.data_ptr(), x.data_ptr(), packed.data_ptr(), 4, 64, 96, bf16, stream) == 2
-    assert lib.mvllm_linear(y.data_ptr(), x.data_ptr(), packed.data_ptr(), 4, 64, 128,
-                            DTYPE_CODES[torch.float32], stream) == 2
-    assert lib.mvllm_linear(0, x.data_ptr(), packed.data_ptr(), 4, 64, 128, bf16, stream) == 1
+    call = lambda m, k, dtype=bf16, out=y.data_ptr(): lib.mvllm_linear(
+        out, x.data_ptr(), packed.data_ptr(), m, 64, k, dtype, 0, 0, stream)
+    assert call(65, 128) == 2
+    assert call(4, 96) == 2
+    assert call(4, 128, DTYPE_CODES[torch.float32]) == 2
+    assert call(4, 128, out=0) == 1
     assert lib.mvllm_linear_split(y.data_ptr(), y.data_ptr(), 0, x.data_ptr(), packed.data_ptr(),
-                                  4, 40, 24, 0, 128, bf16, stream) == 1
+                                  4, 40, 24, 0, 128, bf16, 0, 0, stream) == 1
     assert lib.mvllm_linear_pack(packed.data_ptr(), w.data_ptr(), 64, 96, bf16, stream) == 2
-    assert lib.mvllm_linear(y.data_ptr(), x.data_ptr(), packed.data_ptr(), 4, 64, 128, bf16, stream) == 0
+    assert call(4, 128) == 0
     assert torch.equal(y, extension.linear(x, packed, 64))
+    assert lib.mvllm_linear_workspace_bytes(4, 64, 1024) == 0
+    need = lib.mvllm_linear_workspace_bytes(4, 64, 2048)
+    assert need == 2 * 8 * 32 * 32 * 4  # 2 tiles x 8 waves x one 32 x 32 fp32 tile
+    x2, w2, _ = _operands(4, 64, 2048, torch.bfloat16, 7)
+    p2 = extension.linear_pack(w2)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    args = (y.data_ptr(), x2.data_ptr(), p2.data_ptr(), 4, 64, 2048, bf16)
+    assert lib.mvllm_linear(*args, 0, 0, stream) == 4  # MVLLM_ERR_WORKSPACE
+    assert lib.mvllm_linear(*args, ws.data_ptr(), need - 1, stream) == 4
+    assert lib.mvllm_linear(*args, ws.data_ptr(), need, stream) == 0
+    assert torch.equal(y, extension.linear(x2, p2, 64))
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -201,3 +214,37 @@ def test_swiglu_equals_gate_up_then_swiglu(extension, device, m, i, dtype):
     want = ops.swiglu(_lin(extension, x, gate), _lin(extension, x, up), use_cuda=True)
     assert got.shape == (m, i) and torch.equal(got, want)
     assert torch.equal(ops.linear_swiglu(x, pw, use_cuda=True), got)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,n,k", [(1, 1024, 2048), (32, 1024, 3072), (33, 1024, 2048),
+                                   (64, 2048, 1088), (7, 4096, 4096)])
+def test_residual_rmsnorm_equals_the_unfused_pair(extension, device, m, n, k, dtype):
+    """(h, normed) of the fused launch pair, bitwise linear_residual then the RMSNorm
+    kernel (random norm weight, eps 1e-6)."""
+    x, w, gen = _operands(m, n, k, dtype, 41 + m + k)
+    r = torch.randn(m, n, generator=gen).to(dtype).cuda()
+    nw = (torch.rand(n, generator=gen) + 0.5).to(dtype).cuda()
+    pw = ops.pack_weight(w, use_cuda=True)
+    h, normed = extension.linear_residual_rmsnorm(x, pw.packed, r, nw, 1e-6)
+    want_h = extension.linear_residual(x, pw.packed, r)
+    assert torch.equal(h, want_h)
+    assert torch.equal(normed, ops.rmsnorm(want_h, nw, 1e-6, use_cuda=True))
+    got = ops.linear_residual_rmsnorm(x, pw, r, nw, 1e-6, use_cuda=True)
+    assert got is not None and torch.equal(got[0], h) and torch.equal(got[1], normed)
+
+
+def test_residual_rmsnorm_refuses_what_it_does_not_serve(extension, device):
+    """K <= 1024 or N not a multiple of 512: ops returns None (the caller runs the two
+    ops), the extension raises."""
+    x, w, gen = _operands(4, 1024, 1024, torch.bfloat16, 3)
+    r = torch.randn(4, 1024, generator=gen).to(torch.bfloat16).cuda()
+    nw = torch.ones(1024, dtype=torch.bfloat16, device="cuda")
+    pw = ops.pack_weight(w, use_cuda=True)
+    assert ops.linear_residual_rmsnorm(x, pw, r, nw, use_cuda=True) is None
+    with pytest.raises(RuntimeError, match="not served"):
+        extension.linear_residual_rmsnorm(x, pw.packed, r, nw, 1e-6)
+    x, w, gen = _operands(4, 1000, 2048, torch.bfloat16, 4)
+    pw = ops.pack_weight(w, use_cuda=True)
+    r = torch.randn(4, 1000, generator=gen).to(torch.bfloat16).cuda()
+    assert ops.linear_residual_rmsnorm(x, pw, r, nw[:1000], use_cuda=True) is None
