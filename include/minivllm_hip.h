@@ -280,9 +280,15 @@ int mvllm_linear_residual_rmsnorm(void* h_out, void* normed, const void* x, cons
  * order is torch.argmax's: NaN above every number, -0 equal to +0, and among equal
  * maxima the first index. Replaces `logits.argmax(dim=-1)` of the greedy sampler
  * (mini_vllm/sampler.py:135-141; the engine's decode step, engine.py); no counterpart in
- * mini_vllm_C. */
+ * mini_vllm_C. Two launches for rows longer than 16384 logits (segments per workgroup,
+ * then one wave per row), one otherwise. */
 int mvllm_argmax(int64_t* out, const void* logits, int64_t rows, int64_t vocab,
-                 int64_t row_stride, int32_t dtype, void* stream);
+                 int64_t row_stride, int32_t dtype, void* workspace, uint64_t workspace_bytes,
+                 void* stream);
+/* Workspace of mvllm_argmax (8-byte aligned, contents need not be initialised): one
+ * 8-byte key per 16384-logit segment of each row; 0 for rows of at most 16384 logits.
+ * Rows may hold up to 64 segments (1048576 logits). */
+uint64_t mvllm_argmax_workspace_bytes(int64_t rows, int64_t vocab);
 
 /* y = a * x + b over n floats: the toolchain smoke test, replacing `mini_vllm_C.hello`
  * (csrc/bindings.cpp:8,37-42 -> csrc/hello.cu:11-21; mini_vllm/kernels/extension.py:349-353). */

@@ -353,7 +353,7 @@ extern "C" {
 
 const char* mvllm_last_error(void) { return g_error; }
 
-int mvllm_abi_version(void) { return 5; }
+int mvllm_abi_version(void) { return 6; }
 
 int mvllm_paged_attention_plan(int32_t num_tokens, int32_t num_seqs, int32_t num_q_heads,
                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
@@ -516,25 +516,40 @@ int mvllm_dense_attention(const mvllm_dense_args* args, void* workspace, uint64_
                         args->query_len, s, name);
 }
 
+uint64_t mvllm_argmax_workspace_bytes(int64_t rows, int64_t vocab) {
+  if (rows < 1 || vocab < 1) return 0;
+  return mvllm::argmax_workspace_bytes(rows, vocab);
+}
+
 int mvllm_argmax(int64_t* out, const void* logits, int64_t rows, int64_t vocab,
-                 int64_t row_stride, int32_t dtype, void* stream) {
+                 int64_t row_stride, int32_t dtype, void* workspace, uint64_t workspace_bytes,
+                 void* stream) {
   g_error[0] = '\0';
   if (dtype != mvllm::kF32 && dtype != mvllm::kF16 && dtype != mvllm::kBF16) {
     return fail(MVLLM_ERR_UNSUPPORTED, "argmax: dtype code %d is not served (f32, f16, bf16)", dtype);
   }
-  if (rows < 0 || rows >= (int64_t{1} << 31) || vocab <= 0 || vocab >= (int64_t{1} << 32) - 1 ||
+  if (rows < 0 || rows >= (int64_t{1} << 31) || vocab <= 0 || vocab > mvllm::argmax_max_vocab() ||
       row_stride < vocab) {
     return fail(MVLLM_ERR_INVALID,
                 "argmax: %lld rows of %lld logits, %lld apart: rows must be < 2^31, the row "
-                "non-empty and shorter than 2^32 - 1, the stride at least the row",
+                "non-empty and at most %lld long, the stride at least the row",
                 static_cast<long long>(rows), static_cast<long long>(vocab),
-                static_cast<long long>(row_stride));
+                static_cast<long long>(row_stride),
+                static_cast<long long>(mvllm::argmax_max_vocab()));
   }
   if (rows == 0) return MVLLM_OK;
   if (out == nullptr || logits == nullptr) {
     return fail(MVLLM_ERR_INVALID, "argmax: a required pointer is NULL");
   }
-  return hip_status(mvllm::launch_argmax(out, logits, rows, vocab, row_stride, dtype,
+  const uint64_t need = mvllm::argmax_workspace_bytes(rows, vocab);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need ||
+                   reinterpret_cast<uintptr_t>(workspace) % 8 != 0)) {
+    return fail(MVLLM_ERR_WORKSPACE,
+                "argmax: needs %llu bytes of 8-byte aligned workspace "
+                "(mvllm_argmax_workspace_bytes), got %llu",
+                static_cast<unsigned long long>(need), static_cast<unsigned long long>(workspace_bytes));
+  }
+  return hip_status(mvllm::launch_argmax(out, logits, rows, vocab, row_stride, dtype, workspace,
                                          static_cast<hipStream_t>(stream)),
                     "argmax: launch");
 }

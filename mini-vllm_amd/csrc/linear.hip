@@ -54,7 +54,7 @@
 //    its last step (not summed). M0 is set only by the LDS copies.
 //  * residual_rmsnorm: h = T(r + T(x w^T)) and out = RMSNorm(h) (rounded as
 //    `rmsnorm_vec_kernel` rounds, with the same lane map and sum order, so bit for bit
-//    the unfused pair); one wave per row.
+//    the unfused pair); one wave (workgroup) per row.
 
 #include <algorithm>
 
@@ -316,22 +316,60 @@ __global__ __launch_bounds__(kGroup * kWave) void skinny_reduce_kernel(
   epilogue<T, MB, EPI>(out, blockIdx.x, m, n, total);
 }
 
-// K > 1024, residual + RMSNorm: one wave per x row, lane r holding 8-column chunks
-// r, r + 64, ... (the lane map of rmsnorm_vec_kernel<T, 64, kCh>): h = T(r + T(sum)),
-// then out = T(T(h * inv) * weight) with inv from the lane-ordered fma sum of squares
-// reduced by group_sum<64>, as that kernel computes it.
+// K > 1024, residual + RMSNorm: one wave (workgroup) per x row, lane r holding 8-column
+// chunks r, r + 64, ... (the lane map of rmsnorm_vec_kernel<T, 64, kCh>): h = T(r +
+// T(sum)), then out = T(T(h * inv) * weight) with inv from the lane-ordered fma sum of
+// squares reduced by group_sum<64>, as that kernel computes it. All of a lane's partial
+// loads for kB waves at a time go out together (kCh x 2 x kB float4s).
 template <typename T, int MB, int kCh>
-__global__ __launch_bounds__(kGroup * kWave) void skinny_reduce_norm_kernel(
+__global__ __launch_bounds__(kWave) void skinny_reduce_norm_kernel(
     void* __restrict__ h_out, void* __restrict__ normed, const float* __restrict__ partials,
     const void* __restrict__ residual, const void* __restrict__ norm_weight, int m, int n,
     int total_waves, float eps) {
-  const int row = blockIdx.x * kGroup + threadIdx.x / kWave;
-  const int r = threadIdx.x % kWave;
-  if (row >= m) return;  // a whole wave: no barrier below
-  const int64_t tile_stride = static_cast<int64_t>(total_waves) * (MB * 32 * kColTile);
+  constexpr int kB = 32 / kCh;
+  constexpr int64_t kTile = MB * 32 * kColTile;
+  const int row = blockIdx.x;
+  const int r = threadIdx.x;
+  const int64_t tile_stride = static_cast<int64_t>(total_waves) * kTile;
   const int chunks = n / 8;
   const char* res = static_cast<const char*>(residual) + static_cast<int64_t>(row) * n * 2;
   char* hrow = static_cast<char*>(h_out) + static_cast<int64_t>(row) * n * 2;
+
+  const float* src[kCh];
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    const int col = min(r + c * kWave, chunks - 1) * 8;
+    src[c] = partials + (col / kColTile) * tile_stride + row * kColTile + col % kColTile;
+  }
+  f32x4 sum[kCh][2];
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) sum[c][0] = sum[c][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int g0 = 0; g0 < total_waves; g0 += kB) {
+    f32x4 v[kCh][2][kB];
+#pragma unroll
+    for (int i = 0; i < kB; ++i) {
+      const int64_t off = static_cast<int64_t>(min(g0 + i, total_waves - 1)) * kTile;
+#pragma unroll
+      for (int c = 0; c < kCh; ++c) {
+        v[c][0][i] = *reinterpret_cast<const f32x4*>(src[c] + off);
+        v[c][1][i] = *reinterpret_cast<const f32x4*>(src[c] + off + 4);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kB; ++i) {
+      if (g0 + i < total_waves) {
+#pragma unroll
+        for (int c = 0; c < kCh; ++c) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            sum[c][0][e] = sum[c][0][e] + v[c][0][i][e];
+            sum[c][1][e] = sum[c][1][e] + v[c][1][i][e];
+          }
+        }
+      }
+    }
+  }
+
   u32x4 held[kCh];
   float sumsq = 0.0f;
 #pragma unroll
@@ -339,17 +377,11 @@ __global__ __launch_bounds__(kGroup * kWave) void skinny_reduce_norm_kernel(
     const int chunk = r + c * kWave;
     if (chunk < chunks) {
       const int col = chunk * 8;
-      const float* src = partials + (col / kColTile) * tile_stride + row * kColTile + col % kColTile;
-      const f32x4 s0 = sum_partials(src, MB * 32 * kColTile, total_waves);
-      const f32x4 s1 = sum_partials(src + 4, MB * 32 * kColTile, total_waves);
       float rf[8];
       Chunk<T>::unpack(load16(res + col * 2), rf);
       float f[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float sum = e < 4 ? s0[e] : s1[e - 4];
-        f[e] = Elem<T>::round(rf[e] + Elem<T>::round(sum));
-      }
+      for (int e = 0; e < 8; ++e) f[e] = Elem<T>::round(rf[e] + Elem<T>::round(sum[c][e / 4][e % 4]));
       u32x4 hv;
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
@@ -437,16 +469,16 @@ hipError_t launch_norm_m(void* h_out, void* normed, const void* x, const void* w
       partials, x, w, m, k, t_waves);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const unsigned rows = static_cast<unsigned>((m + kGroup - 1) / kGroup);
+  const unsigned rows = static_cast<unsigned>(m);
   const int per_lane = n / 8 / kWave;
   if (per_lane <= 2) {
-    skinny_reduce_norm_kernel<T, MB, 2><<<rows, kGroup * kWave, 0, stream>>>(
+    skinny_reduce_norm_kernel<T, MB, 2><<<rows, kWave, 0, stream>>>(
         h_out, normed, partials, residual, norm_weight, m, n, t_waves, eps);
   } else if (per_lane <= 4) {
-    skinny_reduce_norm_kernel<T, MB, 4><<<rows, kGroup * kWave, 0, stream>>>(
+    skinny_reduce_norm_kernel<T, MB, 4><<<rows, kWave, 0, stream>>>(
         h_out, normed, partials, residual, norm_weight, m, n, t_waves, eps);
   } else {
-    skinny_reduce_norm_kernel<T, MB, 8><<<rows, kGroup * kWave, 0, stream>>>(
+    skinny_reduce_norm_kernel<T, MB, 8><<<rows, kWave, 0, stream>>>(
         h_out, normed, partials, residual, norm_weight, m, n, t_waves, eps);
   }
   return hipGetLastError();

@@ -59,7 +59,7 @@ HIP_FLAGS = [
 # reference's PyTorch expressions round, so FMA contraction is off there.
 EXTRA_FLAGS = {"elementwise.hip": ["-ffp-contract=off"], "linear.hip": ["-ffp-contract=off"]}
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_CODES: dict[torch.dtype, int] = {
     torch.float32: 0,
@@ -204,7 +204,9 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_kv_write.restype = ctypes.c_int
     lib.mvllm_kv_write.argtypes = [p] * 7 + [i32] * 4 + [i64, i32, i32, p]
     lib.mvllm_argmax.restype = ctypes.c_int
-    lib.mvllm_argmax.argtypes = [p, p, i64, i64, i64, i32, p]
+    lib.mvllm_argmax.argtypes = [p, p, i64, i64, i64, i32, p, u64, p]
+    lib.mvllm_argmax_workspace_bytes.restype = u64
+    lib.mvllm_argmax_workspace_bytes.argtypes = [i64, i64]
     lib.mvllm_linear_pack.restype = ctypes.c_int
     lib.mvllm_linear_pack.argtypes = [p, p, i64, i64, i32, p]
     lib.mvllm_linear_workspace_bytes.restype = u64
@@ -233,6 +235,7 @@ EXPORTED_SYMBOLS = (
     "mvllm_kv_write",
     "mvllm_qk_norm_rope",
     "mvllm_argmax",
+    "mvllm_argmax_workspace_bytes",
     "mvllm_dense_attention_plan",
     "mvllm_dense_attention",
     "mvllm_linear_pack",
@@ -699,9 +702,13 @@ class HipExtension:
         out = torch.empty(logits.shape[0], dtype=torch.int64, device=logits.device)
         if logits.shape[0] == 0:
             return out
-        self._check(self.lib.mvllm_argmax(out.data_ptr(), logits.data_ptr(), logits.shape[0],
-                                          logits.shape[1], max(logits.stride(0), logits.shape[1]),
-                                          DTYPE_CODES[logits.dtype], _stream(logits.device)))
+        rows, vocab = logits.shape
+        need = int(self.lib.mvllm_argmax_workspace_bytes(rows, vocab))
+        ws = self.workspace(logits.device, need) if need else None
+        self._check(self.lib.mvllm_argmax(out.data_ptr(), logits.data_ptr(), rows, vocab,
+                                          max(logits.stride(0), vocab), DTYPE_CODES[logits.dtype],
+                                          ws.data_ptr() if ws is not None else 0, need,
+                                          _stream(logits.device)))
         return out
 
     # -- dense-cache attention (reference csrc/decode_attention.cu, csrc/flash_prefill.cu)

@@ -16,8 +16,8 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("rows,vocab", [(1, 1), (3, 7), (32, 151936), (65, 1000), (5, 8193),
-                                        (2, 300001)])
+@pytest.mark.parametrize("rows,vocab", [(1, 1), (3, 7), (4, 8), (32, 151936), (65, 1000),
+                                        (5, 16385), (2, 300001), (1, 1048576)])
 def test_matches_torch_argmax(extension, device, rows, vocab, dtype):
     gen = torch.Generator().manual_seed(rows * 31 + vocab)
     logits = torch.randn(rows, vocab, generator=gen).to(dtype).cuda()
