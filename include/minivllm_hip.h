@@ -178,6 +178,23 @@ int mvllm_qk_norm_rope(void* q_out, void* k_out, const void* q, const void* k,
                        int32_t head_dim, int64_t num_positions, int64_t max_positions, float eps,
                        int32_t dtype, void* stream);
 
+/* mvllm_qk_norm_rope that also writes the paged KV pools of the layer, in the same
+ * launch: each rotated k head row goes to key_pool at slot slot_mapping[token] (pool
+ * [slots, num_kv_heads, head_dim], i.e. num_blocks x block_size slots, of `dtype`) and v
+ * [num_tokens, num_kv_heads, head_dim] is copied to value_pool at the same slot; a
+ * negative slot writes nothing. The rotated k is not returned otherwise. Replaces the
+ * rmsnorm/rope calls plus PagedKvPool.write's two index_copy_ (model/qwen3_paged.py:
+ * 73-80 -> block/kv_pool.py:116-155) for a pool of q's dtype (an fp8 pool takes
+ * mvllm_qk_norm_rope then mvllm_kv_write); no counterpart in mini_vllm_C. */
+int mvllm_qk_norm_rope_kv_write(void* q_out, void* key_pool, void* value_pool, const void* q,
+                                const void* k, const void* v, const void* q_weight,
+                                const void* k_weight, const void* positions,
+                                int32_t positions_bytes, const float* cos_table,
+                                const float* sin_table, const int32_t* slot_mapping,
+                                int64_t num_tokens, int32_t num_q_heads, int32_t num_kv_heads,
+                                int32_t head_dim, int64_t num_positions, int64_t max_positions,
+                                float eps, int32_t dtype, void* stream);
+
 /* out = T(T(g * T(sigmoid(g))) * u) elementwise over n elements of `dtype`.
  * Replaces `mini_vllm_C.swiglu` (csrc/bindings.cpp:14,59-63 -> csrc/swiglu.cu:87-120),
  * called from mini_vllm/kernels/ops.py:161-162. */

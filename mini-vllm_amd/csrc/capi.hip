@@ -347,6 +347,60 @@ int dense_plan(const mvllm_dense_args* a, DensePlan& d) {
   return MVLLM_OK;
 }
 
+// Checks and launch of the fused QK-norm + RoPE, optionally writing the KV pools.
+int qk_norm_rope_entry(void* q_out, void* k_out, const void* q, const void* k,
+                       const void* q_weight, const void* k_weight, const void* positions,
+                       int32_t positions_bytes, const float* cos_table, const float* sin_table,
+                       int64_t num_tokens, int32_t num_q_heads, int32_t num_kv_heads,
+                       int32_t head_dim, int64_t num_positions, int64_t max_positions, float eps,
+                       int32_t dtype, void* stream, const void* v, void* k_pool, void* v_pool,
+                       const int32_t* slots) {
+  if (dtype != mvllm::kF32 && dtype != mvllm::kF16 && dtype != mvllm::kBF16) {
+    return fail(MVLLM_ERR_INVALID,
+                "qk_norm_rope: dtype code %d is not supported; float64 is not supported", dtype);
+  }
+  if (!mvllm::qk_norm_rope_supported(dtype, head_dim)) {
+    return fail(MVLLM_ERR_UNSUPPORTED,
+                "qk_norm_rope: head dim %d is not supported (16-byte chunks per head must be "
+                "a power of two from 2 to 64); call rmsnorm and rope",
+                head_dim);
+  }
+  if (num_tokens < 0 || num_q_heads <= 0 || num_kv_heads <= 0) {
+    return fail(MVLLM_ERR_INVALID, "qk_norm_rope: bad shape");
+  }
+  if (positions_bytes != 4 && positions_bytes != 8) {
+    return fail(MVLLM_ERR_INVALID, "qk_norm_rope: positions must be int32 or int64");
+  }
+  if (num_tokens == 0) return MVLLM_OK;
+  if (num_positions <= 0 || num_tokens % num_positions != 0) {
+    return fail(MVLLM_ERR_INVALID,
+                "qk_norm_rope: %lld tokens is not a multiple of the %lld positions given, so the "
+                "positions cannot broadcast over them",
+                static_cast<long long>(num_tokens), static_cast<long long>(num_positions));
+  }
+  if (max_positions <= 0) return fail(MVLLM_ERR_INVALID, "qk_norm_rope: empty cos/sin tables");
+  if (q_out == nullptr || (k_out == nullptr && k_pool == nullptr) || q == nullptr || k == nullptr ||
+      q_weight == nullptr || k_weight == nullptr || positions == nullptr ||
+      cos_table == nullptr || sin_table == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "qk_norm_rope: a required pointer is NULL");
+  }
+  const uintptr_t bits = reinterpret_cast<uintptr_t>(q_out) | reinterpret_cast<uintptr_t>(k_out) |
+                         reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                         reinterpret_cast<uintptr_t>(q_weight) |
+                         reinterpret_cast<uintptr_t>(k_weight) |
+                         reinterpret_cast<uintptr_t>(cos_table) |
+                         reinterpret_cast<uintptr_t>(sin_table);
+  if (bits % 16 != 0) {
+    return fail(MVLLM_ERR_INVALID, "qk_norm_rope: every tensor must be 16-byte aligned");
+  }
+  return hip_status(
+      mvllm::launch_qk_norm_rope(q, k, q_weight, k_weight, positions, positions_bytes, cos_table,
+                                 sin_table, q_out, k_out, num_tokens, num_q_heads, num_kv_heads,
+                                 head_dim, num_positions, max_positions, eps, dtype,
+                                 static_cast<hipStream_t>(stream), v, k_pool, v_pool, slots),
+      "qk_norm_rope: launch");
+}
+
 }  // namespace
 
 extern "C" {
@@ -621,50 +675,33 @@ int mvllm_qk_norm_rope(void* q_out, void* k_out, const void* q, const void* k,
                        int32_t head_dim, int64_t num_positions, int64_t max_positions, float eps,
                        int32_t dtype, void* stream) {
   g_error[0] = '\0';
-  if (dtype != mvllm::kF32 && dtype != mvllm::kF16 && dtype != mvllm::kBF16) {
-    return fail(MVLLM_ERR_INVALID,
-                "qk_norm_rope: dtype code %d is not supported; float64 is not supported", dtype);
+  return qk_norm_rope_entry(q_out, k_out, q, k, q_weight, k_weight, positions, positions_bytes,
+                            cos_table, sin_table, num_tokens, num_q_heads, num_kv_heads, head_dim,
+                            num_positions, max_positions, eps, dtype, stream, nullptr, nullptr,
+                            nullptr, nullptr);
+}
+
+int mvllm_qk_norm_rope_kv_write(void* q_out, void* key_pool, void* value_pool, const void* q,
+                                const void* k, const void* v, const void* q_weight,
+                                const void* k_weight, const void* positions,
+                                int32_t positions_bytes, const float* cos_table,
+                                const float* sin_table, const int32_t* slot_mapping,
+                                int64_t num_tokens, int32_t num_q_heads, int32_t num_kv_heads,
+                                int32_t head_dim, int64_t num_positions, int64_t max_positions,
+                                float eps, int32_t dtype, void* stream) {
+  g_error[0] = '\0';
+  if (num_tokens > 0 && (key_pool == nullptr || value_pool == nullptr || v == nullptr ||
+                         slot_mapping == nullptr)) {
+    return fail(MVLLM_ERR_INVALID, "qk_norm_rope_kv_write: a required pointer is NULL");
   }
-  if (!mvllm::qk_norm_rope_supported(dtype, head_dim)) {
-    return fail(MVLLM_ERR_UNSUPPORTED,
-                "qk_norm_rope: head dim %d is not supported (16-byte chunks per head must be "
-                "a power of two from 2 to 64); call rmsnorm and rope",
-                head_dim);
+  if ((reinterpret_cast<uintptr_t>(key_pool) | reinterpret_cast<uintptr_t>(value_pool) |
+       reinterpret_cast<uintptr_t>(v)) % 16 != 0) {
+    return fail(MVLLM_ERR_INVALID, "qk_norm_rope_kv_write: every tensor must be 16-byte aligned");
   }
-  if (num_tokens < 0 || num_q_heads <= 0 || num_kv_heads <= 0) {
-    return fail(MVLLM_ERR_INVALID, "qk_norm_rope: bad shape");
-  }
-  if (positions_bytes != 4 && positions_bytes != 8) {
-    return fail(MVLLM_ERR_INVALID, "qk_norm_rope: positions must be int32 or int64");
-  }
-  if (num_tokens == 0) return MVLLM_OK;
-  if (num_positions <= 0 || num_tokens % num_positions != 0) {
-    return fail(MVLLM_ERR_INVALID,
-                "qk_norm_rope: %lld tokens is not a multiple of the %lld positions given, so the "
-                "positions cannot broadcast over them",
-                static_cast<long long>(num_tokens), static_cast<long long>(num_positions));
-  }
-  if (max_positions <= 0) return fail(MVLLM_ERR_INVALID, "qk_norm_rope: empty cos/sin tables");
-  if (q_out == nullptr || k_out == nullptr || q == nullptr || k == nullptr ||
-      q_weight == nullptr || k_weight == nullptr || positions == nullptr ||
-      cos_table == nullptr || sin_table == nullptr) {
-    return fail(MVLLM_ERR_INVALID, "qk_norm_rope: a required pointer is NULL");
-  }
-  const uintptr_t bits = reinterpret_cast<uintptr_t>(q_out) | reinterpret_cast<uintptr_t>(k_out) |
-                         reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
-                         reinterpret_cast<uintptr_t>(q_weight) |
-                         reinterpret_cast<uintptr_t>(k_weight) |
-                         reinterpret_cast<uintptr_t>(cos_table) |
-                         reinterpret_cast<uintptr_t>(sin_table);
-  if (bits % 16 != 0) {
-    return fail(MVLLM_ERR_INVALID, "qk_norm_rope: every tensor must be 16-byte aligned");
-  }
-  return hip_status(
-      mvllm::launch_qk_norm_rope(q, k, q_weight, k_weight, positions, positions_bytes, cos_table,
-                                 sin_table, q_out, k_out, num_tokens, num_q_heads, num_kv_heads,
-                                 head_dim, num_positions, max_positions, eps, dtype,
-                                 static_cast<hipStream_t>(stream)),
-      "qk_norm_rope: launch");
+  return qk_norm_rope_entry(q_out, nullptr, q, k, q_weight, k_weight, positions, positions_bytes,
+                            cos_table, sin_table, num_tokens, num_q_heads, num_kv_heads, head_dim,
+                            num_positions, max_positions, eps, dtype, stream, v, key_pool,
+                            value_pool, slot_mapping);
 }
 
 int mvllm_swiglu(void* out, const void* gate, const void* up, int64_t n, int32_t dtype,

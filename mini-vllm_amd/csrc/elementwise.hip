@@ -339,18 +339,42 @@ hipError_t launch_rope(const void* x, const void* positions, int pos_bytes, cons
 // kR = D / N lanes per head row (one 16-byte chunk each); lane r's partner in the
 // rotation holds dims +-D/2, i.e. lane r ^ (kR / 2). Rows: the T * Hq rows of q, then
 // the T * Hk rows of k.
-template <typename T, typename TPos, int kR>
+// With KV, the same launch also writes the paged KV pool (the reference's two
+// index_copy_ calls, block/kv_pool.py:116-155): each rotated k head row goes to slot
+// slots[token] of k_pool as it is stored, and v rows (appended after the k rows) are
+// copied to v_pool; a negative slot writes nothing. k_out may then be null.
+struct KvSink {
+  const void* v;
+  void* k_pool;
+  void* v_pool;
+  const int32_t* slots;
+  int64_t v_rows;
+};
+
+template <typename T, typename TPos, int kR, bool KV>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ wq,
     const void* __restrict__ wk, const TPos* __restrict__ positions,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t, void* __restrict__ q_out,
     void* __restrict__ k_out, int64_t q_rows, int64_t k_rows, int hq, int hk,
-    int64_t num_positions, int64_t max_positions, float eps) {
+    int64_t num_positions, int64_t max_positions, float eps, KvSink kv) {
   constexpr int N = Chunk<T>::kN;
   constexpr int D = kR * N;
   const int lane = threadIdx.x % kWave;
   const int r = lane % kR;
   const int64_t row = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kR;
+  if constexpr (KV) {
+    if (row >= q_rows + k_rows) {  // a whole kR-lane group: a v row to copy
+      const int64_t local = row - q_rows - k_rows;
+      if (local >= kv.v_rows) return;
+      const int32_t slot = kv.slots[local / hk];
+      if (slot < 0) return;
+      const int64_t dst = (static_cast<int64_t>(slot) * hk + local % hk) * D * Elem<T>::kBytes;
+      store16(static_cast<char*>(kv.v_pool) + dst + r * 16,
+              nt_load16(static_cast<const char*>(kv.v) + local * D * Elem<T>::kBytes + r * 16));
+      return;
+    }
+  }
   const bool live = row < q_rows + k_rows;
   const bool is_k = row >= q_rows;
   const int64_t local = is_k ? row - q_rows : row;
@@ -414,8 +438,20 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
                   : __fadd_rn(__fmul_rn(y[e], c[e]), __fmul_rn(py[e], sn[e]));
     }
   }
-  char* orow = static_cast<char*>(is_k ? k_out : q_out) + local * static_cast<int64_t>(D) * Elem<T>::kBytes;
-  nt_store16(orow + r * 16, pack_chunk<T>(out));
+  const u32x4 packed = pack_chunk<T>(out);
+  if (!KV || !is_k || k_out != nullptr) {
+    char* orow = static_cast<char*>(is_k ? k_out : q_out) + local * static_cast<int64_t>(D) * Elem<T>::kBytes;
+    nt_store16(orow + r * 16, packed);
+  }
+  if constexpr (KV) {
+    if (is_k) {
+      const int32_t slot = kv.slots[token];
+      if (slot >= 0) {
+        const int64_t dst = (static_cast<int64_t>(slot) * hk + local % hk) * D * Elem<T>::kBytes;
+        store16(static_cast<char*>(kv.k_pool) + dst + r * 16, packed);
+      }
+    }
+  }
 }
 
 namespace {
@@ -424,16 +460,24 @@ hipError_t launch_qk_norm_rope_p(const void* q, const void* k, const void* wq, c
                                  const void* positions, const float* cos_t, const float* sin_t,
                                  void* q_out, void* k_out, int64_t tokens, int hq, int hk, int dim,
                                  int64_t num_positions, int64_t max_positions, float eps,
-                                 hipStream_t stream) {
+                                 const KvSink& kv, hipStream_t stream) {
   constexpr int N = Chunk<T>::kN;
   const int64_t q_rows = tokens * hq;
   const int64_t k_rows = tokens * hk;
+  const int64_t rows = q_rows + k_rows + kv.v_rows;
   const TPos* pos = static_cast<const TPos*>(positions);
 #define MVLLM_QKNR(KR)                                                                          \
-  qk_norm_rope_kernel<T, TPos, KR><<<static_cast<unsigned>(((q_rows + k_rows) * KR + 255) / 256), \
-                                     256, 0, stream>>>(q, k, wq, wk, pos, cos_t, sin_t, q_out,    \
-                                                       k_out, q_rows, k_rows, hq, hk,            \
-                                                       num_positions, max_positions, eps)
+  if (kv.k_pool != nullptr) {                                                                   \
+    qk_norm_rope_kernel<T, TPos, KR, true><<<static_cast<unsigned>((rows * KR + 255) / 256),   \
+                                             256, 0, stream>>>(                                 \
+        q, k, wq, wk, pos, cos_t, sin_t, q_out, k_out, q_rows, k_rows, hq, hk, num_positions,  \
+        max_positions, eps, kv);                                                                \
+  } else {                                                                                      \
+    qk_norm_rope_kernel<T, TPos, KR, false><<<static_cast<unsigned>((rows * KR + 255) / 256),  \
+                                              256, 0, stream>>>(                                \
+        q, k, wq, wk, pos, cos_t, sin_t, q_out, k_out, q_rows, k_rows, hq, hk, num_positions,  \
+        max_positions, eps, kv);                                                                \
+  }
   switch (dim / N) {
     case 2: MVLLM_QKNR(2); break;
     case 4: MVLLM_QKNR(4); break;
@@ -452,15 +496,16 @@ hipError_t launch_qk_norm_rope_t(const void* q, const void* k, const void* wq, c
                                  const void* positions, int pos_bytes, const float* cos_t,
                                  const float* sin_t, void* q_out, void* k_out, int64_t tokens,
                                  int hq, int hk, int dim, int64_t num_positions,
-                                 int64_t max_positions, float eps, hipStream_t stream) {
+                                 int64_t max_positions, float eps, const KvSink& kv,
+                                 hipStream_t stream) {
   if (pos_bytes == 8) {
     return launch_qk_norm_rope_p<T, int64_t>(q, k, wq, wk, positions, cos_t, sin_t, q_out, k_out,
                                              tokens, hq, hk, dim, num_positions, max_positions,
-                                             eps, stream);
+                                             eps, kv, stream);
   }
   return launch_qk_norm_rope_p<T, int32_t>(q, k, wq, wk, positions, cos_t, sin_t, q_out, k_out,
                                            tokens, hq, hk, dim, num_positions, max_positions, eps,
-                                           stream);
+                                           kv, stream);
 }
 }  // namespace
 
@@ -476,11 +521,13 @@ hipError_t launch_qk_norm_rope(const void* q, const void* k, const void* wq, con
                                const void* positions, int pos_bytes, const float* cos_t,
                                const float* sin_t, void* q_out, void* k_out, int64_t tokens,
                                int hq, int hk, int dim, int64_t num_positions,
-                               int64_t max_positions, float eps, int dtype, hipStream_t stream) {
+                               int64_t max_positions, float eps, int dtype, hipStream_t stream,
+                               const void* v, void* k_pool, void* v_pool, const int32_t* slots) {
+  const KvSink kv{v, k_pool, v_pool, slots, k_pool != nullptr ? tokens * hk : 0};
   switch (dtype) {
-    case kF32: return launch_qk_norm_rope_t<float>(q, k, wq, wk, positions, pos_bytes, cos_t, sin_t, q_out, k_out, tokens, hq, hk, dim, num_positions, max_positions, eps, stream);
-    case kF16: return launch_qk_norm_rope_t<f16_t>(q, k, wq, wk, positions, pos_bytes, cos_t, sin_t, q_out, k_out, tokens, hq, hk, dim, num_positions, max_positions, eps, stream);
-    case kBF16: return launch_qk_norm_rope_t<bf16_t>(q, k, wq, wk, positions, pos_bytes, cos_t, sin_t, q_out, k_out, tokens, hq, hk, dim, num_positions, max_positions, eps, stream);
+    case kF32: return launch_qk_norm_rope_t<float>(q, k, wq, wk, positions, pos_bytes, cos_t, sin_t, q_out, k_out, tokens, hq, hk, dim, num_positions, max_positions, eps, kv, stream);
+    case kF16: return launch_qk_norm_rope_t<f16_t>(q, k, wq, wk, positions, pos_bytes, cos_t, sin_t, q_out, k_out, tokens, hq, hk, dim, num_positions, max_positions, eps, kv, stream);
+    case kBF16: return launch_qk_norm_rope_t<bf16_t>(q, k, wq, wk, positions, pos_bytes, cos_t, sin_t, q_out, k_out, tokens, hq, hk, dim, num_positions, max_positions, eps, kv, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -15,11 +15,16 @@ hipError_t launch_rope(const void* x, const void* positions, int pos_bytes, cons
 // Whether launch_qk_norm_rope serves this dtype and head dim (D / (16 / elt) lanes
 // per head a power of two from 2 to 64).
 bool qk_norm_rope_supported(int dtype, int head_dim);
+// With k_pool non-null the launch also writes k (as rotated) and v to the paged pools
+// [slots, hk, dim] of the same dtype at slots[token] (negative: skipped); k_out may
+// then be null.
 hipError_t launch_qk_norm_rope(const void* q, const void* k, const void* wq, const void* wk,
                                const void* positions, int pos_bytes, const float* cos_t,
                                const float* sin_t, void* q_out, void* k_out, int64_t tokens,
                                int hq, int hk, int dim, int64_t num_positions,
-                               int64_t max_positions, float eps, int dtype, hipStream_t stream);
+                               int64_t max_positions, float eps, int dtype, hipStream_t stream,
+                               const void* v = nullptr, void* k_pool = nullptr,
+                               void* v_pool = nullptr, const int32_t* slots = nullptr);
 hipError_t launch_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype,
                          hipStream_t stream);
 hipError_t launch_axpby(const float* x, float* y, float a, float b, int64_t n,

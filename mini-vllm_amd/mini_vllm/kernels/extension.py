@@ -201,6 +201,9 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_axpby.argtypes = [p, p, f32, f32, i64, p]
     lib.mvllm_qk_norm_rope.restype = ctypes.c_int
     lib.mvllm_qk_norm_rope.argtypes = [p] * 7 + [i32, p, p, i64, i32, i32, i32, i64, i64, f32, i32, p]
+    lib.mvllm_qk_norm_rope_kv_write.restype = ctypes.c_int
+    lib.mvllm_qk_norm_rope_kv_write.argtypes = (
+        [p] * 9 + [i32, p, p, p, i64, i32, i32, i32, i64, i64, f32, i32, p])
     lib.mvllm_kv_write.restype = ctypes.c_int
     lib.mvllm_kv_write.argtypes = [p] * 7 + [i32] * 4 + [i64, i32, i32, p]
     lib.mvllm_argmax.restype = ctypes.c_int
@@ -235,6 +238,7 @@ EXPORTED_SYMBOLS = (
     "mvllm_kv_write",
     "mvllm_qk_norm_rope",
     "mvllm_argmax",
+    "mvllm_qk_norm_rope_kv_write",
     "mvllm_argmax_workspace_bytes",
     "mvllm_dense_attention_plan",
     "mvllm_dense_attention",
@@ -659,6 +663,48 @@ class HipExtension:
             sin.contiguous().data_ptr(), q.shape[0], q.shape[1], k.shape[1], d,
             positions.numel(), cos.shape[0], float(eps), code, _stream(q.device)))
         return q_out, k_out
+
+    def qk_norm_rope_kv_write(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                              q_weight: torch.Tensor, k_weight: torch.Tensor,
+                              positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                              eps: float, key_pool: torch.Tensor, value_pool: torch.Tensor,
+                              slot_mapping: torch.Tensor) -> torch.Tensor:
+        """``qk_norm_rope`` whose rotated k, and v, go straight to their slots of the
+        layer's paged pools (``num_blocks x P x H_k x D`` of q's dtype) in the same
+        launch; returns the rotated q."""
+        if not (key_pool.is_cuda and value_pool.is_cuda and v.is_cuda and slot_mapping.is_cuda):
+            raise RuntimeError("qk_norm_rope_kv_write: every tensor must be a CUDA tensor")
+        if (key_pool.dtype != q.dtype or value_pool.dtype != q.dtype or v.dtype != q.dtype
+                or key_pool.shape != value_pool.shape or key_pool.dim() != 4
+                or tuple(key_pool.shape[2:]) != tuple(k.shape[1:]) or v.shape != k.shape
+                or not (key_pool.is_contiguous() and value_pool.is_contiguous())):
+            raise RuntimeError(
+                "qk_norm_rope_kv_write: the pools must be contiguous num_blocks x P x H_k x D "
+                f"tensors of q's dtype matching k and v, got {tuple(key_pool.shape)} "
+                f"{key_pool.dtype} for k {tuple(k.shape)}")
+        if slot_mapping.dtype != torch.int32 or slot_mapping.shape != (k.shape[0],):
+            raise RuntimeError("qk_norm_rope_kv_write: slot_mapping must be int32 [T]")
+        tensors = (q, k, q_weight, k_weight, positions, cos, sin)
+        if not all(t.is_cuda for t in tensors):
+            raise RuntimeError("qk_norm_rope_kv_write: every tensor must be a CUDA tensor")
+        d = q.shape[2]
+        code = DTYPE_CODES.get(q.dtype)
+        if code is None or code == 3 or positions.dtype not in (torch.int32, torch.int64):
+            raise RuntimeError(f"qk_norm_rope_kv_write: dtype {q.dtype} / positions "
+                               f"{positions.dtype} not supported")
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        q_out = torch.empty_like(q)
+        if q.shape[0] == 0:
+            return q_out
+        positions = positions.contiguous()
+        self._check(self.lib.mvllm_qk_norm_rope_kv_write(
+            q_out.data_ptr(), key_pool.data_ptr(), value_pool.data_ptr(), q.data_ptr(),
+            k.data_ptr(), v.data_ptr(), q_weight.contiguous().data_ptr(),
+            k_weight.contiguous().data_ptr(), positions.data_ptr(), positions.element_size(),
+            cos.contiguous().data_ptr(), sin.contiguous().data_ptr(), slot_mapping.data_ptr(),
+            q.shape[0], q.shape[1], k.shape[1], d, positions.numel(), cos.shape[0], float(eps),
+            code, _stream(q.device)))
+        return q_out
 
     def swiglu(self, gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
         """``silu(gate) * up`` (reference csrc/swiglu.cu:87-120)."""

@@ -56,6 +56,7 @@ __all__ = [
     "pack_weight",
     "paged_attention",
     "qk_norm_rope",
+    "qk_norm_rope_kv_write",
     "rmsnorm",
     "rope",
     "swiglu",
@@ -159,6 +160,26 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor,
     k = torch_path.apply_rope(torch_path.rms_norm(k, k_weight, eps).unsqueeze(0), positions,
                               cos, sin).squeeze(0)
     return q, k
+
+
+def qk_norm_rope_kv_write(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                          q_weight: torch.Tensor, k_weight: torch.Tensor, positions: torch.Tensor,
+                          cos: torch.Tensor, sin: torch.Tensor, eps: float,
+                          key_pool: torch.Tensor, value_pool: torch.Tensor,
+                          slot_mapping: torch.Tensor, use_cuda: bool = False) -> torch.Tensor | None:
+    """``qk_norm_rope`` plus the KV-pool write of the rotated k and of v (reference
+    qwen3_paged.py:73-80 -> block/kv_pool.py:116-155) in one launch, returning the
+    rotated q. Kernel: ``csrc/elementwise.hip``. None where it does not serve the call
+    (the PyTorch path, an fp8 pool, a head dim the fused kernel does not take): the
+    caller then runs ``qk_norm_rope`` and ``kv_write``."""
+    if not _use_kernel("qk_norm_rope", use_cuda, q):
+        return None
+    ext = load_extension()
+    if (not ext.qk_norm_rope_supported(q.dtype, q.shape[-1]) or key_pool.dtype != q.dtype
+            or value_pool.dtype != q.dtype or v.dtype != q.dtype):
+        return None
+    return ext.qk_norm_rope_kv_write(q, k, v, q_weight, k_weight, positions, cos, sin, eps,
+                                     key_pool, value_pool, slot_mapping)
 
 
 def swiglu(gate: torch.Tensor, up: torch.Tensor, use_cuda: bool = False) -> torch.Tensor:

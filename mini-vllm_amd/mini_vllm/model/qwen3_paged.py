@@ -8,7 +8,8 @@ hot path has to serve unchanged:
     mlp_norm -> gate/up -> SwiGLU -> down -> residual
 
 (QK-norm + RoPE of q and k run as one fused op, bitwise equal to the unfused
-rmsnorm/rope pair; the K/V write is one op for K and V. Decode-sized steps, at most
+rmsnorm/rope pair, which with a 16-bit pool also writes K and V to their slots; the
+K/V write is otherwise one op for K and V. Decode-sized steps, at most
 64 rows, also fuse the projections: q/k/v as one launch, gate/up with SwiGLU as one,
 and the o and down projections with their residual add, each rounded as the unfused
 ops round.)
@@ -151,10 +152,16 @@ class Qwen3Paged:
         q = q.view(t, c.num_attention_heads, c.head_dim)
         k = k.view(t, c.num_key_value_heads, c.head_dim)
         v = v.view(t, c.num_key_value_heads, c.head_dim)
-        q, k = ops.qk_norm_rope(q, k, w["q_norm"], w["k_norm"], batch.positions, self.cos,
-                                self.sin, c.rms_norm_eps, use_cuda=u)
         kv = self.manager.kv
-        kv.write(layer, batch.slot_mapping, k, v, use_cuda=u)
+        qr = ops.qk_norm_rope_kv_write(q, k, v, w["q_norm"], w["k_norm"], batch.positions,
+                                       self.cos, self.sin, c.rms_norm_eps, kv.layer_keys(layer),
+                                       kv.layer_values(layer), batch.slot_mapping, use_cuda=u)
+        if qr is not None:
+            q = qr
+        else:
+            q, k = ops.qk_norm_rope(q, k, w["q_norm"], w["k_norm"], batch.positions, self.cos,
+                                    self.sin, c.rms_norm_eps, use_cuda=u)
+            kv.write(layer, batch.slot_mapping, k, v, use_cuda=u)
         k_scale, v_scale = kv.layer_scales(layer)
         out = ops.paged_attention(
             q.contiguous(), kv.layer_keys(layer), kv.layer_values(layer), batch.block_tables,

@@ -146,3 +146,52 @@ def test_kv_write_refusals(extension, device):
         extension.kv_write(fp8, fp8.clone(), x, x, slots)
     with pytest.raises(RuntimeError, match="float8 pools only"):
         extension.kv_write(pool, pool.clone(), x, x, slots, k_scale=torch.zeros(4, 2, device=device))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("hq,hk,d", [(16, 8, 128), (4, 2, 64), (8, 1, 256)])
+def test_qk_norm_rope_kv_write_is_the_unfused_sequence(extension, device, dtype, hq, hk, d):
+    """QK-norm + RoPE with the pool write in one launch: q bitwise the fused
+    qk_norm_rope's, and both pools bitwise what qk_norm_rope then kv_write leave (the
+    rotated k and the raw v at their slots, -1 slots and the rest of the pool untouched)."""
+    from mini_vllm.torch_path import rope_tables
+
+    rng = np.random.default_rng(hq * d)
+    nb, bs, t = 30, 16, 200
+    gen = torch.Generator().manual_seed(hq + d)
+    q = torch.randn(t + 5, hq, d, generator=gen).to(dtype).to(device)
+    k = torch.randn(t + 5, hk, d, generator=gen).to(dtype).to(device)
+    v = torch.randn(t + 5, hk, d, generator=gen).to(dtype).to(device)
+    wq = (torch.rand(d, generator=gen) + 0.5).to(dtype).to(device)
+    wk = (torch.rand(d, generator=gen) + 0.5).to(dtype).to(device)
+    cos, sin = rope_tables(d, 4096, device=device)
+    pos = torch.from_numpy(rng.integers(0, 4096, size=t + 5)).to(device)
+    slots = torch.from_numpy(_rand_slots(rng, nb, bs, t, pad=5)).to(device)
+    pool_k = torch.randn(nb, bs, hk, d, generator=gen).to(dtype).to(device)
+    pool_v = torch.randn(nb, bs, hk, d, generator=gen).to(dtype).to(device)
+    want_k, want_v = pool_k.clone(), pool_v.clone()
+    q_ref, k_ref = extension.qk_norm_rope(q, k, wq, wk, pos, cos, sin, 1e-6)
+    extension.kv_write(want_k, want_v, k_ref, v, slots)
+    q_got = extension.qk_norm_rope_kv_write(q, k, v, wq, wk, pos, cos, sin, 1e-6, pool_k, pool_v, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(q_got, q_ref)
+    assert torch.equal(pool_k, want_k) and torch.equal(pool_v, want_v)
+    q_ops = ops.qk_norm_rope_kv_write(q, k, v, wq, wk, pos, cos, sin, 1e-6, pool_k, pool_v, slots,
+                                      use_cuda=True)
+    assert q_ops is not None and torch.equal(q_ops, q_ref)
+
+
+def test_qk_norm_rope_kv_write_leaves_fp8_pools_to_the_two_ops(extension, device):
+    """An fp8 pool (quantised with per-block scales) is not written by the fused launch:
+    ops returns None and the caller runs qk_norm_rope then kv_write."""
+    from mini_vllm.torch_path import rope_tables
+
+    q = torch.randn(4, 16, 128, dtype=torch.bfloat16, device=device)
+    k = torch.randn(4, 8, 128, dtype=torch.bfloat16, device=device)
+    w = torch.ones(128, dtype=torch.bfloat16, device=device)
+    cos, sin = rope_tables(128, 64, device=device)
+    pool = torch.zeros(4, 16, 8, 128, dtype=torch.float8_e4m3fn, device=device)
+    slots = torch.arange(4, dtype=torch.int32, device=device)
+    pos = torch.arange(4, device=device)
+    assert ops.qk_norm_rope_kv_write(q, k, k, w, w, pos, cos, sin, 1e-6, pool, pool, slots,
+                                     use_cuda=True) is None
