@@ -399,7 +399,8 @@ def main() -> int:
     parser.add_argument("--skip-extras", action="store_true", help="headline config 2 only")
     parser.add_argument("--extras", default="3,4,5,ew,kv,dense,linear,copy",
                         help="comma list of extras to run: 3 (prefill), 4 (fp8 decode), "
-                             "5 (engine), 5fp8 (engine, fp8 KV cache), ew (elementwise "
+                             "5 (engine), 5small (engine, 64 x 128 tokens), 5fp8 (engine, fp8 "
+                             "KV cache), ew (elementwise "
                              "kernels), kv (KV write), dense (dense-cache attention), linear "
                              "(decode projections and argmax), copy")
     parser.add_argument("--no-cpu", action="store_true")
@@ -471,6 +472,10 @@ def main() -> int:
         log("config 5: Qwen3-0.6B-shaped engine, 256 requests x 256 tokens")
         extras["config5_engine"] = run_engine()
         log(f"config 5 (decode graphs on): {extras['config5_engine']}")
+    if "5small" in wanted:
+        # A shorter engine run (64 requests x 128 tokens), sized for a kernel trace.
+        extras["config5_engine_small"] = run_engine(requests=64, max_tokens=128)
+        log(f"config 5 small: {extras['config5_engine_small']}")
     if "5fp8" in wanted:
         extras["config5_engine_fp8kv"] = run_engine(kv_dtype=torch.float8_e4m3fn)
         log(f"config 5 with an fp8 KV cache: {extras['config5_engine_fp8kv']}")
