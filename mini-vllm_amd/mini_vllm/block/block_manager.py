@@ -32,6 +32,8 @@ class BlockManager:
                               dtype, device)
         self._free: deque[int] = deque(range(num_blocks))
         self._tables: dict[int, list[int]] = {}
+        self._changes = 0  # bumped on every table change: (seq_id, version) names a table
+        self._versions: dict[int, int] = {}
 
     @property
     def num_free_blocks(self) -> int:
@@ -53,6 +55,17 @@ class BlockManager:
         table = self._tables.setdefault(seq_id, [])
         for _ in range(need):
             table.append(self._free.popleft())
+        if need:
+            self._bump(seq_id)
+
+    def _bump(self, seq_id: int) -> None:
+        self._changes += 1
+        self._versions[seq_id] = self._changes
+
+    def version(self, seq_id: int) -> int:
+        """A number that changes whenever the sequence's block table does (never reused),
+        so a copy of the table can be kept until it changes."""
+        return self._versions.get(seq_id, 0)
 
     def slots(self, seq_id: int, start: int, count: int) -> list[int]:
         """Physical slots of logical positions ``start .. start + count - 1``."""
@@ -65,6 +78,7 @@ class BlockManager:
 
     def free(self, seq_id: int) -> None:
         self._free.extend(self._tables.pop(seq_id, []))
+        self._bump(seq_id)
 
     def check_no_leaks(self) -> None:
         held = sum(len(t) for t in self._tables.values())

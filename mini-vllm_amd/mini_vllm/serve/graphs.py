@@ -61,24 +61,37 @@ class _Captured:
         self.model = model
         self.graph = None
         self.logits = None
+        # numpy views of the pinned buffers, written in place; each table row is
+        # rewritten only when the block manager reports a change of that sequence's
+        # table (row_keys: (seq_id, version), or None for a dummy row).
+        self.np64 = self.host64.numpy()
+        self.np32 = self.host32.numpy()
+        self.row_keys: list = [()] * b
 
     def fill(self, scheduled) -> None:
         b, w, p = self.batch_size, self.width, self.model.manager.block_size
         manager = self.model.manager
-        ids, pos, ctx, slots = [0] * b, [0] * b, [1] * b, [self.dummy_block * p] * b
-        tables = [[self.dummy_block] + [PADDING_BLOCK] * (w - 1) for _ in range(b)]
+        ids, pos = self.np64[:b], self.np64[b:]
+        ctx, slots = self.np32[:b], self.np32[b:2 * b]
+        tables = self.np32[2 * b:].reshape(b, w)
         for i, (seq, _) in enumerate(scheduled):
             start = seq.num_computed_tokens
             ids[i] = seq.tokens(start, 1)[0]
             pos[i] = start
             ctx[i] = start + 1
-            slots[i] = manager.slots(seq.seq_id, start, 1)[0]
             table = manager.table(seq.seq_id)
-            tables[i] = table + [PADDING_BLOCK] * (w - len(table))
-        self.host64[:b] = torch.tensor(ids)
-        self.host64[b:] = torch.tensor(pos)
-        flat = ctx + slots + [x for row in tables for x in row]
-        self.host32.copy_(torch.tensor(flat, dtype=torch.int32))
+            slots[i] = table[start // p] * p + start % p
+            key = (seq.seq_id, manager.version(seq.seq_id))
+            if self.row_keys[i] != key:
+                tables[i, :len(table)] = table
+                tables[i, len(table):] = PADDING_BLOCK
+                self.row_keys[i] = key
+        for i in range(len(scheduled), b):
+            if self.row_keys[i] is not None:
+                ids[i], pos[i], ctx[i], slots[i] = 0, 0, 1, self.dummy_block * p
+                tables[i, 0] = self.dummy_block
+                tables[i, 1:] = PADDING_BLOCK
+                self.row_keys[i] = None
         self.dyn64.copy_(self.host64, non_blocking=True)
         self.dyn32.copy_(self.host32, non_blocking=True)
 
