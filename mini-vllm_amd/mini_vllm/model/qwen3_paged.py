@@ -12,7 +12,8 @@ rmsnorm/rope pair, which with a 16-bit pool also writes K and V to their slots; 
 K/V write is otherwise one op for K and V. Decode-sized steps, at most
 64 rows, also fuse the projections: q/k/v as one launch, gate/up with SwiGLU as one,
 and the o and down projections with their residual add, each rounded as the unfused
-ops round.)
+ops round; larger steps run the same ops as one BLAS call each over the concatenated
+weights.)
 
 and the forward returns one logits row per sequence (its last computed position),
 through the final norm and the tied embedding (reference qwen3_paged.py:211-228).
@@ -190,7 +191,10 @@ class Qwen3Paged:
         c = self.config
         u = self.use_cuda
         h = self.weights["embedding"].index_select(0, batch.input_ids)
-        fused = u and ops.skinny(h, use_cuda=u)
+        # With the kernels on, every step takes the fused ops: decode-sized ones run the
+        # skinny kernels, larger ones (prefill chunks) one BLAS call over the
+        # concatenated weights instead of three (q/k/v) or two (gate/up).
+        fused = u
         n_layers = len(self.layers)
         normed = ops.rmsnorm(h, self.layers[0]["attn_norm"], c.rms_norm_eps, use_cuda=u)
         for layer, (w, p) in enumerate(zip(self.layers, self.packed)):
