@@ -187,12 +187,12 @@ __device__ __forceinline__ void seek(Cursor& k, const PagedParams& p, const int*
 
 // This workgroup's work units [u0, u1) and the cursor at u0; false when it has none.
 // Every thread must call it: the stream schedule's prefix scan ends in a barrier.
-template <int kThreads>
+template <int kThreads, bool kGridOnly = false>
 __device__ __forceinline__ bool prefill_work(const PagedParams& p, int cols, int share,
                                              int* s_prefix, Cursor& cur, int& u0, int& u1) {
   const int tid = threadIdx.x;
   const int n = p.num_seqs;
-  if (p.pf_wgs > 0) {
+  if (!kGridOnly && p.pf_wgs > 0) {
     // Prefix scan of the sequences' work units by wave 0: each lane sums a contiguous
     // run, then a 64-lane inclusive scan.
     if (tid < kWave) {
@@ -653,7 +653,7 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_kernel(const PagedPara
 //    access. Tiles t + 1 and t + 2 are in flight while t is computed.
 //  * before a tile's barrier each wave waits (vmcnt) for its own copies of that tile
 //    only, so the barrier publishes the whole tile.
-template <typename TQ, int HS>
+template <typename TQ, int HS, bool kStream>
 __global__ __launch_bounds__(256 * HS) void paged_prefill_lds_kernel(const PagedParams p) {
   constexpr int D = 128;
   constexpr int kThreads = 256 * HS;
@@ -703,12 +703,14 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_lds_kernel(const Paged
   const int group = p.hq / p.hk;
   const int chunks = group / HW;
   const int cols = p.hk * chunks;
-  const bool stream = p.pf_wgs > 0;
+  // Compiled per schedule: the grid's kernel carries none of the stream's cursor
+  // seeking (whose registers otherwise spill into the tile loop).
+  constexpr bool stream = kStream;
   const int share = xcd_share(blockIdx.x, gridDim.x);
 
   Cursor cur;
   int u0, u1;
-  if (!prefill_work<kThreads>(p, cols, share, s_prefix, cur, u0, u1)) return;
+  if (!prefill_work<kThreads, !kStream>(p, cols, share, s_prefix, cur, u0, u1)) return;
   auto advance = [&](Cursor& k) __attribute__((always_inline)) {
     ++k.u;
     if (++k.t < k.nt) return;
@@ -1190,13 +1192,13 @@ bool lds_staging_enabled() {
 template <typename TQ, int HS>
 void launch_prefill_lds(const PagedParams& p, int max_query_len, hipStream_t stream) {
   if (p.pf_wgs > 0) {
-    paged_prefill_lds_kernel<TQ, HS><<<p.pf_wgs, 256 * HS, 0, stream>>>(p);
+    paged_prefill_lds_kernel<TQ, HS, true><<<p.pf_wgs, 256 * HS, 0, stream>>>(p);
     paged_prefill_merge_kernel<TQ, 128, HS><<<p.pf_wgs, 1024, 0, stream>>>(p);
   } else {
     const int cols = p.hk * (p.hq / p.hk / HS);
     const int qtiles = (max_query_len + kPrefillQueryTile - 1) / kPrefillQueryTile;
     const dim3 grid(cols, p.num_seqs, qtiles);
-    paged_prefill_lds_kernel<TQ, HS><<<grid, 256 * HS, 0, stream>>>(p);
+    paged_prefill_lds_kernel<TQ, HS, false><<<grid, 256 * HS, 0, stream>>>(p);
   }
 }
 
