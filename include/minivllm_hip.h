@@ -193,13 +193,27 @@ int mvllm_qk_norm_rope_kv_write(void* q_out, void* key_pool, void* value_pool, c
                                 const float* sin_table, const int32_t* slot_mapping,
                                 int64_t num_tokens, int32_t num_q_heads, int32_t num_kv_heads,
                                 int32_t head_dim, int64_t num_positions, int64_t max_positions,
-                                float eps, int32_t dtype, void* stream);
+                                float eps, int64_t q_token_stride, int64_t kv_token_stride,
+                                int32_t dtype, void* stream);
+/* (q_token_stride / kv_token_stride: elements between consecutive tokens of q and of k
+ * and v, whose heads are contiguous within a token; 0 means contiguous tensors. Column
+ * views of the fused q/k/v projection's output pass its width, so the prefill path
+ * needs no copies.) */
 
 /* out = T(T(g * T(sigmoid(g))) * u) elementwise over n elements of `dtype`.
  * Replaces `mini_vllm_C.swiglu` (csrc/bindings.cpp:14,59-63 -> csrc/swiglu.cu:87-120),
  * called from mini_vllm/kernels/ops.py:161-162. */
 int mvllm_swiglu(void* out, const void* gate, const void* up, int64_t n, int32_t dtype,
                  void* stream);
+
+/* mvllm_swiglu over the fused gate/up projection's output: gate_up [rows, 2 cols] in
+ * the 16-column interleave of mvllm_linear_swiglu's weight (columns 32j .. 32j+15: gate
+ * columns 16j .. 16j+15; the next 16: the same up columns), out [rows, cols] contiguous;
+ * cols a multiple of 16. Rounds as mvllm_swiglu. The prefill-sized MLP of
+ * model/qwen3_paged.py:101-111 after one BLAS call over the interleaved weight; no
+ * counterpart in mini_vllm_C. */
+int mvllm_swiglu_interleaved(void* out, const void* gate_up, int64_t rows, int64_t cols,
+                             int32_t dtype, void* stream);
 
 /* Scatter one iteration's keys and values into their pool slots, K and V in one
  * launch. Replaces the two index_copy_ calls of PagedKvPool.write

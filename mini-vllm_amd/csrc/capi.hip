@@ -354,7 +354,8 @@ int qk_norm_rope_entry(void* q_out, void* k_out, const void* q, const void* k,
                        int64_t num_tokens, int32_t num_q_heads, int32_t num_kv_heads,
                        int32_t head_dim, int64_t num_positions, int64_t max_positions, float eps,
                        int32_t dtype, void* stream, const void* v, void* k_pool, void* v_pool,
-                       const int32_t* slots) {
+                       const int32_t* slots, int64_t q_token_stride = 0,
+                       int64_t kv_token_stride = 0) {
   if (dtype != mvllm::kF32 && dtype != mvllm::kF16 && dtype != mvllm::kBF16) {
     return fail(MVLLM_ERR_INVALID,
                 "qk_norm_rope: dtype code %d is not supported; float64 is not supported", dtype);
@@ -393,11 +394,25 @@ int qk_norm_rope_entry(void* q_out, void* k_out, const void* q, const void* k,
   if (bits % 16 != 0) {
     return fail(MVLLM_ERR_INVALID, "qk_norm_rope: every tensor must be 16-byte aligned");
   }
+  // Token strides: whole head vectors per token, each token's rows 16-byte aligned.
+  const int64_t elem = dtype == mvllm::kF32 ? 4 : 2;
+  const int64_t q_row = static_cast<int64_t>(num_q_heads) * head_dim;
+  const int64_t kv_row = static_cast<int64_t>(num_kv_heads) * head_dim;
+  const int64_t qs = q_token_stride > 0 ? q_token_stride : q_row;
+  const int64_t kvs = kv_token_stride > 0 ? kv_token_stride : kv_row;
+  if (qs < q_row || kvs < kv_row || (qs * elem) % 16 != 0 || (kvs * elem) % 16 != 0) {
+    return fail(MVLLM_ERR_INVALID,
+                "qk_norm_rope: token strides %lld (q) and %lld (k, v) must cover the token's "
+                "heads (%lld, %lld elements) and keep every token 16-byte aligned",
+                static_cast<long long>(qs), static_cast<long long>(kvs),
+                static_cast<long long>(q_row), static_cast<long long>(kv_row));
+  }
   return hip_status(
       mvllm::launch_qk_norm_rope(q, k, q_weight, k_weight, positions, positions_bytes, cos_table,
                                  sin_table, q_out, k_out, num_tokens, num_q_heads, num_kv_heads,
                                  head_dim, num_positions, max_positions, eps, dtype,
-                                 static_cast<hipStream_t>(stream), v, k_pool, v_pool, slots),
+                                 static_cast<hipStream_t>(stream), v, k_pool, v_pool, slots, qs,
+                                 kvs),
       "qk_norm_rope: launch");
 }
 
@@ -407,7 +422,7 @@ extern "C" {
 
 const char* mvllm_last_error(void) { return g_error; }
 
-int mvllm_abi_version(void) { return 6; }
+int mvllm_abi_version(void) { return 7; }
 
 int mvllm_paged_attention_plan(int32_t num_tokens, int32_t num_seqs, int32_t num_q_heads,
                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
@@ -688,7 +703,8 @@ int mvllm_qk_norm_rope_kv_write(void* q_out, void* key_pool, void* value_pool, c
                                 const float* sin_table, const int32_t* slot_mapping,
                                 int64_t num_tokens, int32_t num_q_heads, int32_t num_kv_heads,
                                 int32_t head_dim, int64_t num_positions, int64_t max_positions,
-                                float eps, int32_t dtype, void* stream) {
+                                float eps, int64_t q_token_stride, int64_t kv_token_stride,
+                                int32_t dtype, void* stream) {
   g_error[0] = '\0';
   if (num_tokens > 0 && (key_pool == nullptr || value_pool == nullptr || v == nullptr ||
                          slot_mapping == nullptr)) {
@@ -701,7 +717,7 @@ int mvllm_qk_norm_rope_kv_write(void* q_out, void* key_pool, void* value_pool, c
   return qk_norm_rope_entry(q_out, nullptr, q, k, q_weight, k_weight, positions, positions_bytes,
                             cos_table, sin_table, num_tokens, num_q_heads, num_kv_heads, head_dim,
                             num_positions, max_positions, eps, dtype, stream, v, key_pool,
-                            value_pool, slot_mapping);
+                            value_pool, slot_mapping, q_token_stride, kv_token_stride);
 }
 
 int mvllm_swiglu(void* out, const void* gate, const void* up, int64_t n, int32_t dtype,
@@ -721,6 +737,32 @@ int mvllm_swiglu(void* out, const void* gate, const void* up, int64_t n, int32_t
   return hip_status(
       mvllm::launch_swiglu(gate, up, out, n, dtype, static_cast<hipStream_t>(stream)),
       "swiglu: launch");
+}
+
+int mvllm_swiglu_interleaved(void* out, const void* gate_up, int64_t rows, int64_t cols,
+                             int32_t dtype, void* stream) {
+  g_error[0] = '\0';
+  if (dtype != mvllm::kF32 && dtype != mvllm::kF16 && dtype != mvllm::kBF16) {
+    return fail(MVLLM_ERR_INVALID,
+                "swiglu_interleaved: dtype code %d is not supported; float64 is not supported",
+                dtype);
+  }
+  if (rows < 0 || cols < 0 || cols % 16 != 0) {
+    return fail(MVLLM_ERR_INVALID,
+                "swiglu_interleaved: cols (%lld) must be a multiple of 16 (the interleave's "
+                "group) and rows non-negative",
+                static_cast<long long>(cols));
+  }
+  if (rows == 0 || cols == 0) return MVLLM_OK;
+  if (out == nullptr || gate_up == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "swiglu_interleaved: a required pointer is NULL");
+  }
+  if ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(gate_up)) % 16 != 0) {
+    return fail(MVLLM_ERR_INVALID, "swiglu_interleaved: every tensor must be 16-byte aligned");
+  }
+  return hip_status(mvllm::launch_swiglu_interleaved(gate_up, out, rows, cols, dtype,
+                                                     static_cast<hipStream_t>(stream)),
+                    "swiglu_interleaved: launch");
 }
 
 // Shared checks of the skinny projection entries: dtype, sizes, pointers, alignment.

@@ -350,6 +350,12 @@ struct KvSink {
   const int32_t* slots;
   int64_t v_rows;
 };
+// Elements between consecutive tokens of the q input and of the k and v inputs (the
+// rows of one token are contiguous head vectors): hq D and hk D when each is its own
+// tensor, the fused projection's width when they are column views of its output.
+struct TokenStrides {
+  int64_t q, kv;
+};
 
 template <typename T, typename TPos, int kR, bool KV>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
@@ -357,7 +363,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const void* __restrict__ wk, const TPos* __restrict__ positions,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t, void* __restrict__ q_out,
     void* __restrict__ k_out, int64_t q_rows, int64_t k_rows, int hq, int hk,
-    int64_t num_positions, int64_t max_positions, float eps, KvSink kv) {
+    int64_t num_positions, int64_t max_positions, float eps, KvSink kv, TokenStrides ts) {
   constexpr int N = Chunk<T>::kN;
   constexpr int D = kR * N;
   const int lane = threadIdx.x % kWave;
@@ -367,20 +373,24 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     if (row >= q_rows + k_rows) {  // a whole kR-lane group: a v row to copy
       const int64_t local = row - q_rows - k_rows;
       if (local >= kv.v_rows) return;
-      const int32_t slot = kv.slots[local / hk];
+      const int64_t vt = local / hk;
+      const int32_t slot = kv.slots[vt];
       if (slot < 0) return;
       const int64_t dst = (static_cast<int64_t>(slot) * hk + local % hk) * D * Elem<T>::kBytes;
+      const int64_t src = (vt * ts.kv + (local - vt * hk) * D) * Elem<T>::kBytes;
       store16(static_cast<char*>(kv.v_pool) + dst + r * 16,
-              nt_load16(static_cast<const char*>(kv.v) + local * D * Elem<T>::kBytes + r * 16));
+              nt_load16(static_cast<const char*>(kv.v) + src + r * 16));
       return;
     }
   }
   const bool live = row < q_rows + k_rows;
   const bool is_k = row >= q_rows;
   const int64_t local = is_k ? row - q_rows : row;
-  const int64_t token = live ? local / (is_k ? hk : hq) : 0;
+  const int heads = is_k ? hk : hq;
+  const int64_t token = live ? local / heads : 0;
+  const int64_t head = live ? local - token * heads : 0;
   const char* xr = static_cast<const char*>(is_k ? k : q) +
-                   (live ? local : 0) * static_cast<int64_t>(D) * Elem<T>::kBytes;
+                   (token * (is_k ? ts.kv : ts.q) + head * D) * Elem<T>::kBytes;
 
   // rmsnorm, as rmsnorm_vec_kernel<T, kR, 1>
   const u32x4 held = nt_load16(xr + r * 16);
@@ -460,7 +470,7 @@ hipError_t launch_qk_norm_rope_p(const void* q, const void* k, const void* wq, c
                                  const void* positions, const float* cos_t, const float* sin_t,
                                  void* q_out, void* k_out, int64_t tokens, int hq, int hk, int dim,
                                  int64_t num_positions, int64_t max_positions, float eps,
-                                 const KvSink& kv, hipStream_t stream) {
+                                 const KvSink& kv, TokenStrides ts, hipStream_t stream) {
   constexpr int N = Chunk<T>::kN;
   const int64_t q_rows = tokens * hq;
   const int64_t k_rows = tokens * hk;
@@ -471,12 +481,12 @@ hipError_t launch_qk_norm_rope_p(const void* q, const void* k, const void* wq, c
     qk_norm_rope_kernel<T, TPos, KR, true><<<static_cast<unsigned>((rows * KR + 255) / 256),   \
                                              256, 0, stream>>>(                                 \
         q, k, wq, wk, pos, cos_t, sin_t, q_out, k_out, q_rows, k_rows, hq, hk, num_positions,  \
-        max_positions, eps, kv);                                                                \
+        max_positions, eps, kv, ts);                                                            \
   } else {                                                                                      \
     qk_norm_rope_kernel<T, TPos, KR, false><<<static_cast<unsigned>((rows * KR + 255) / 256),  \
                                               256, 0, stream>>>(                                \
         q, k, wq, wk, pos, cos_t, sin_t, q_out, k_out, q_rows, k_rows, hq, hk, num_positions,  \
-        max_positions, eps, kv);                                                                \
+        max_positions, eps, kv, ts);                                                            \
   }
   switch (dim / N) {
     case 2: MVLLM_QKNR(2); break;
@@ -497,15 +507,15 @@ hipError_t launch_qk_norm_rope_t(const void* q, const void* k, const void* wq, c
                                  const float* sin_t, void* q_out, void* k_out, int64_t tokens,
                                  int hq, int hk, int dim, int64_t num_positions,
                                  int64_t max_positions, float eps, const KvSink& kv,
-                                 hipStream_t stream) {
+                                 TokenStrides ts, hipStream_t stream) {
   if (pos_bytes == 8) {
     return launch_qk_norm_rope_p<T, int64_t>(q, k, wq, wk, positions, cos_t, sin_t, q_out, k_out,
                                              tokens, hq, hk, dim, num_positions, max_positions,
-                                             eps, kv, stream);
+                                             eps, kv, ts, stream);
   }
   return launch_qk_norm_rope_p<T, int32_t>(q, k, wq, wk, positions, cos_t, sin_t, q_out, k_out,
                                            tokens, hq, hk, dim, num_positions, max_positions, eps,
-                                           kv, stream);
+                                           kv, ts, stream);
 }
 }  // namespace
 
@@ -522,12 +532,15 @@ hipError_t launch_qk_norm_rope(const void* q, const void* k, const void* wq, con
                                const float* sin_t, void* q_out, void* k_out, int64_t tokens,
                                int hq, int hk, int dim, int64_t num_positions,
                                int64_t max_positions, float eps, int dtype, hipStream_t stream,
-                               const void* v, void* k_pool, void* v_pool, const int32_t* slots) {
+                               const void* v, void* k_pool, void* v_pool, const int32_t* slots,
+                               int64_t q_token_stride, int64_t kv_token_stride) {
   const KvSink kv{v, k_pool, v_pool, slots, k_pool != nullptr ? tokens * hk : 0};
+  const TokenStrides ts{q_token_stride > 0 ? q_token_stride : static_cast<int64_t>(hq) * dim,
+                        kv_token_stride > 0 ? kv_token_stride : static_cast<int64_t>(hk) * dim};
   switch (dtype) {
-    case kF32: return launch_qk_norm_rope_t<float>(q, k, wq, wk, positions, pos_bytes, cos_t, sin_t, q_out, k_out, tokens, hq, hk, dim, num_positions, max_positions, eps, kv, stream);
-    case kF16: return launch_qk_norm_rope_t<f16_t>(q, k, wq, wk, positions, pos_bytes, cos_t, sin_t, q_out, k_out, tokens, hq, hk, dim, num_positions, max_positions, eps, kv, stream);
-    case kBF16: return launch_qk_norm_rope_t<bf16_t>(q, k, wq, wk, positions, pos_bytes, cos_t, sin_t, q_out, k_out, tokens, hq, hk, dim, num_positions, max_positions, eps, kv, stream);
+    case kF32: return launch_qk_norm_rope_t<float>(q, k, wq, wk, positions, pos_bytes, cos_t, sin_t, q_out, k_out, tokens, hq, hk, dim, num_positions, max_positions, eps, kv, ts, stream);
+    case kF16: return launch_qk_norm_rope_t<f16_t>(q, k, wq, wk, positions, pos_bytes, cos_t, sin_t, q_out, k_out, tokens, hq, hk, dim, num_positions, max_positions, eps, kv, ts, stream);
+    case kBF16: return launch_qk_norm_rope_t<bf16_t>(q, k, wq, wk, positions, pos_bytes, cos_t, sin_t, q_out, k_out, tokens, hq, hk, dim, num_positions, max_positions, eps, kv, ts, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -568,6 +581,27 @@ __global__ __launch_bounds__(256) void swiglu_scalar_kernel(const void* __restri
   Elem<T>::store(out, index, swiglu_one<T>(Elem<T>::load(gate, index), Elem<T>::load(up, index)));
 }
 
+// SwiGLU over the fused gate/up projection's output [rows][2 cols] in its 16-column
+// interleave (gate columns 16j .. 16j + 15 at 32j .., the same up columns at 32j + 16 ..):
+// out [rows][cols] = swiglu(gate, up) with the same roundings as swiglu_vec_kernel.
+// One 16-byte chunk of output per thread; cols a multiple of 16.
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu_interleaved_kernel(const void* __restrict__ gate_up,
+                                                                 void* __restrict__ out,
+                                                                 int64_t chunks, int64_t row_chunks) {
+  constexpr int E = Chunk<T>::kN;
+  constexpr int G = 16 / E;  // output chunks per 16-column group
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= chunks) return;
+  const int64_t row = i / row_chunks;
+  const int64_t c = i - row * row_chunks;
+  const int64_t src = row * 2 * row_chunks * E + 32 * (c / G) + E * (c % G);
+  const char* base = static_cast<const char*>(gate_up) + src * Elem<T>::kBytes;
+  const u32x4 g = nt_load16(base);
+  const u32x4 u = nt_load16(base + 16 * Elem<T>::kBytes);
+  nt_store16(static_cast<char*>(out) + i * 16, swiglu_chunk<T>(g, u));
+}
+
 namespace {
 template <typename T>
 hipError_t launch_swiglu_t(const void* gate, const void* up, void* out, int64_t n,
@@ -584,6 +618,22 @@ hipError_t launch_swiglu_t(const void* gate, const void* up, void* out, int64_t 
   return hipGetLastError();
 }
 }  // namespace
+
+hipError_t launch_swiglu_interleaved(const void* gate_up, void* out, int64_t rows, int64_t cols,
+                                     int dtype, hipStream_t stream) {
+  const int e = dtype == kF32 ? 4 : 8;
+  const int64_t row_chunks = cols / e;
+  const int64_t chunks = rows * row_chunks;
+  if (chunks == 0) return hipSuccess;
+  const unsigned grid = static_cast<unsigned>((chunks + 255) / 256);
+  switch (dtype) {
+    case kF32: swiglu_interleaved_kernel<float><<<grid, 256, 0, stream>>>(gate_up, out, chunks, row_chunks); break;
+    case kF16: swiglu_interleaved_kernel<f16_t><<<grid, 256, 0, stream>>>(gate_up, out, chunks, row_chunks); break;
+    case kBF16: swiglu_interleaved_kernel<bf16_t><<<grid, 256, 0, stream>>>(gate_up, out, chunks, row_chunks); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
 
 hipError_t launch_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype,
                          hipStream_t stream) {

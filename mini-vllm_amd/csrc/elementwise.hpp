@@ -24,7 +24,14 @@ hipError_t launch_qk_norm_rope(const void* q, const void* k, const void* wq, con
                                int hq, int hk, int dim, int64_t num_positions,
                                int64_t max_positions, float eps, int dtype, hipStream_t stream,
                                const void* v = nullptr, void* k_pool = nullptr,
-                               void* v_pool = nullptr, const int32_t* slots = nullptr);
+                               void* v_pool = nullptr, const int32_t* slots = nullptr,
+                               int64_t q_token_stride = 0, int64_t kv_token_stride = 0);
+// (Token strides in elements between consecutive tokens of q and of k and v; 0 means
+// contiguous, hq * dim and hk * dim.)
+// out [rows][cols] = swiglu of the 16-column gate/up interleave [rows][2 cols]; cols a
+// multiple of 16, every pointer 16-byte aligned.
+hipError_t launch_swiglu_interleaved(const void* gate_up, void* out, int64_t rows, int64_t cols,
+                                     int dtype, hipStream_t stream);
 hipError_t launch_swiglu(const void* gate, const void* up, void* out, int64_t n, int dtype,
                          hipStream_t stream);
 hipError_t launch_axpby(const float* x, float* y, float a, float b, int64_t n,

@@ -59,7 +59,7 @@ HIP_FLAGS = [
 # reference's PyTorch expressions round, so FMA contraction is off there.
 EXTRA_FLAGS = {"elementwise.hip": ["-ffp-contract=off"], "linear.hip": ["-ffp-contract=off"]}
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 DTYPE_CODES: dict[torch.dtype, int] = {
     torch.float32: 0,
@@ -197,13 +197,15 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_rope.argtypes = [p, p, p, i32, p, p, i64, i64, i64, i64, i64, i32, p]
     lib.mvllm_swiglu.restype = ctypes.c_int
     lib.mvllm_swiglu.argtypes = [p, p, p, i64, i32, p]
+    lib.mvllm_swiglu_interleaved.restype = ctypes.c_int
+    lib.mvllm_swiglu_interleaved.argtypes = [p, p, i64, i64, i32, p]
     lib.mvllm_axpby.restype = ctypes.c_int
     lib.mvllm_axpby.argtypes = [p, p, f32, f32, i64, p]
     lib.mvllm_qk_norm_rope.restype = ctypes.c_int
     lib.mvllm_qk_norm_rope.argtypes = [p] * 7 + [i32, p, p, i64, i32, i32, i32, i64, i64, f32, i32, p]
     lib.mvllm_qk_norm_rope_kv_write.restype = ctypes.c_int
     lib.mvllm_qk_norm_rope_kv_write.argtypes = (
-        [p] * 9 + [i32, p, p, p, i64, i32, i32, i32, i64, i64, f32, i32, p])
+        [p] * 9 + [i32, p, p, p, i64, i32, i32, i32, i64, i64, f32, i64, i64, i32, p])
     lib.mvllm_kv_write.restype = ctypes.c_int
     lib.mvllm_kv_write.argtypes = [p] * 7 + [i32] * 4 + [i64, i32, i32, p]
     lib.mvllm_argmax.restype = ctypes.c_int
@@ -234,6 +236,7 @@ EXPORTED_SYMBOLS = (
     "mvllm_rmsnorm",
     "mvllm_rope",
     "mvllm_swiglu",
+    "mvllm_swiglu_interleaved",
     "mvllm_axpby",
     "mvllm_kv_write",
     "mvllm_qk_norm_rope",
@@ -675,7 +678,9 @@ class HipExtension:
                               slot_mapping: torch.Tensor) -> torch.Tensor:
         """``qk_norm_rope`` whose rotated k, and v, go straight to their slots of the
         layer's paged pools (``num_blocks x P x H_k x D`` of q's dtype) in the same
-        launch; returns the rotated q."""
+        launch; returns the rotated q. q, k and v may be column views of one fused
+        projection's output: heads contiguous within a token, any 16-byte-aligned token
+        stride (k and v sharing theirs)."""
         if not (key_pool.is_cuda and value_pool.is_cuda and v.is_cuda and slot_mapping.is_cuda):
             raise RuntimeError("qk_norm_rope_kv_write: every tensor must be a CUDA tensor")
         if (key_pool.dtype != q.dtype or value_pool.dtype != q.dtype or v.dtype != q.dtype
@@ -696,8 +701,11 @@ class HipExtension:
         if code is None or code == 3 or positions.dtype not in (torch.int32, torch.int64):
             raise RuntimeError(f"qk_norm_rope_kv_write: dtype {q.dtype} / positions "
                                f"{positions.dtype} not supported")
-        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-        q_out = torch.empty_like(q)
+        def rows_ok(t):  # heads contiguous within each token
+            return t.stride(2) == 1 and t.stride(1) == d
+        if not (rows_ok(q) and rows_ok(k) and rows_ok(v)) or k.stride(0) != v.stride(0):
+            q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        q_out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
         if q.shape[0] == 0:
             return q_out
         positions = positions.contiguous()
@@ -707,8 +715,24 @@ class HipExtension:
             k_weight.contiguous().data_ptr(), positions.data_ptr(), positions.element_size(),
             cos.contiguous().data_ptr(), sin.contiguous().data_ptr(), slot_mapping.data_ptr(),
             q.shape[0], q.shape[1], k.shape[1], d, positions.numel(), cos.shape[0], float(eps),
-            code, _stream(q.device)))
+            q.stride(0), k.stride(0), code, _stream(q.device)))
         return q_out
+
+    def swiglu_interleaved(self, gate_up: torch.Tensor) -> torch.Tensor:
+        """``swiglu`` over ``gate_up`` [T, 2 I], the fused gate/up projection's output in
+        the 16-column interleave of ``torch_path.interleave_gate_up``; returns [T, I]."""
+        if not gate_up.is_cuda or gate_up.dim() != 2 or gate_up.shape[1] % 32 != 0:
+            raise RuntimeError("swiglu_interleaved: gate_up must be a CUDA [T, 2 I] tensor, "
+                               "I a multiple of 16")
+        code = DTYPE_CODES.get(gate_up.dtype)
+        if code is None or code == 3:
+            raise RuntimeError(f"swiglu_interleaved: dtype {gate_up.dtype} is not supported")
+        gate_up = gate_up.contiguous()
+        rows, cols = gate_up.shape[0], gate_up.shape[1] // 2
+        out = torch.empty(rows, cols, dtype=gate_up.dtype, device=gate_up.device)
+        self._check(self.lib.mvllm_swiglu_interleaved(out.data_ptr(), gate_up.data_ptr(), rows,
+                                                      cols, code, _stream(gate_up.device)))
+        return out
 
     def swiglu(self, gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
         """``silu(gate) * up`` (reference csrc/swiglu.cu:87-120)."""

@@ -260,13 +260,16 @@ def skinny(x: torch.Tensor, use_cuda: bool) -> bool:
 
 
 def linear_split(x: torch.Tensor, w: PackedWeight, sizes: tuple[int, ...],
-                 use_cuda: bool = False) -> tuple[torch.Tensor, ...]:
+                 use_cuda: bool = False, views: bool = False) -> tuple[torch.Tensor, ...]:
     """``x @ w.T`` cut column-wise into contiguous tensors of ``sizes`` (the q, k, v
-    projections over their concatenated weights). Kernel: ``csrc/linear.hip``."""
+    projections over their concatenated weights). Kernel: ``csrc/linear.hip``. With
+    ``views`` the BLAS path (prefill-sized inputs) returns column views of its one
+    output instead of copies, for a consumer that reads strided tokens."""
     ext = _skinny_ext(x, w, w.shape[0], use_cuda)
     if ext is not None and len(sizes) <= 3 and all(s % 32 == 0 for s in sizes[:-1]):
         return ext.linear_split(x, w.packed, tuple(sizes))
-    return tuple(t.contiguous() for t in (x @ w.dense.t()).split(list(sizes), dim=-1))
+    parts = (x @ w.dense.t()).split(list(sizes), dim=-1)
+    return parts if views else tuple(t.contiguous() for t in parts)
 
 
 def linear_residual(x: torch.Tensor, w: PackedWeight, residual: torch.Tensor,
@@ -302,7 +305,11 @@ def linear_swiglu(x: torch.Tensor, w_gate_up: PackedWeight, use_cuda: bool = Fal
     ext = _skinny_ext(x, w_gate_up, n, use_cuda)
     if ext is not None and n % 32 == 0:
         return ext.linear_swiglu(x, w_gate_up.packed, n // 2)
-    gate, up = torch_path.split_gate_up(x @ w_gate_up.dense.t())
+    y = x @ w_gate_up.dense.t()
+    if _use_kernel("swiglu", use_cuda, y) and y.dim() == 2 and n % 32 == 0:
+        # prefill-sized: SwiGLU straight off the interleaved product, no gate/up copies
+        return load_extension().swiglu_interleaved(y)
+    gate, up = torch_path.split_gate_up(y)
     return swiglu(gate, up, use_cuda=use_cuda)
 
 

@@ -147,7 +147,8 @@ class Qwen3Paged:
         t = x.shape[0]
         u = self.use_cuda
         if fused:
-            q, k, v = ops.linear_split(x, p["qkv"], (c.q_size, c.kv_size, c.kv_size), use_cuda=u)
+            q, k, v = ops.linear_split(x, p["qkv"], (c.q_size, c.kv_size, c.kv_size), use_cuda=u,
+                                       views=True)
         else:
             q, k, v = (ops.linear(x, w[n], use_cuda=u) for n in ("wq", "wk", "wv"))
         q = q.view(t, c.num_attention_heads, c.head_dim)
@@ -160,9 +161,9 @@ class Qwen3Paged:
         if qr is not None:
             q = qr
         else:
-            q, k = ops.qk_norm_rope(q, k, w["q_norm"], w["k_norm"], batch.positions, self.cos,
-                                    self.sin, c.rms_norm_eps, use_cuda=u)
-            kv.write(layer, batch.slot_mapping, k, v, use_cuda=u)
+            q, k = ops.qk_norm_rope(q.contiguous(), k.contiguous(), w["q_norm"], w["k_norm"],
+                                    batch.positions, self.cos, self.sin, c.rms_norm_eps, use_cuda=u)
+            kv.write(layer, batch.slot_mapping, k, v.contiguous(), use_cuda=u)
         k_scale, v_scale = kv.layer_scales(layer)
         out = ops.paged_attention(
             q.contiguous(), kv.layer_keys(layer), kv.layer_values(layer), batch.block_tables,

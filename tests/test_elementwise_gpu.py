@@ -188,6 +188,21 @@ def test_swiglu_is_bitwise_equal_to_torch(extension, device, dtype, shape):
     within_ulps(got, want, dtype, ulps=1.0 if dtype != torch.float32 else 4.0)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("rows,cols", [(1, 16), (7, 48), (300, 3072)])
+def test_swiglu_interleaved_is_split_then_swiglu(extension, device, dtype, rows, cols):
+    """SwiGLU read straight off the 16-column gate/up interleave equals splitting it
+    (torch_path.split_gate_up) and calling swiglu, bit for bit."""
+    gen = torch.Generator().manual_seed(rows + cols)
+    y = (torch.randn(rows, 2 * cols, generator=gen) * 3).to(dtype).to(device)
+    gate, up = torch_path.split_gate_up(y)
+    want = extension.swiglu(gate.contiguous(), up.contiguous())
+    got = extension.swiglu_interleaved(y)
+    assert got.shape == (rows, cols) and torch.equal(got, want)
+    with pytest.raises(RuntimeError, match="multiple of 16"):
+        extension.swiglu_interleaved(y[:, : 2 * cols - 16])
+
+
 def test_swiglu_misaligned_views(extension, device):
     g = torch.randn(1025, dtype=torch.bfloat16, device=device)[1:]
     u = torch.randn(1025, dtype=torch.bfloat16, device=device)[1:]

@@ -181,6 +181,39 @@ def test_qk_norm_rope_kv_write_is_the_unfused_sequence(extension, device, dtype,
     assert q_ops is not None and torch.equal(q_ops, q_ref)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("hq,hk,d", [(16, 8, 128), (6, 2, 64)])
+def test_qk_norm_rope_kv_write_reads_column_views(extension, device, dtype, hq, hk, d):
+    """q, k, v as column views of one fused q/k/v projection output (token stride the
+    projection's width, the prefill path): every output bitwise the call on contiguous
+    copies, with no copy made."""
+    from mini_vllm.torch_path import rope_tables
+
+    rng = np.random.default_rng(7 * hq + d)
+    nb, bs, t = 20, 16, 150
+    gen = torch.Generator().manual_seed(3 * hq + d)
+    width = (hq + 2 * hk) * d
+    fused = torch.randn(t, width, generator=gen).to(dtype).to(device)
+    q, k, v = fused.split([hq * d, hk * d, hk * d], dim=-1)
+    q, k, v = q.view(t, hq, d), k.view(t, hk, d), v.view(t, hk, d)
+    assert not q.is_contiguous() and q.stride(0) == width
+    wq = (torch.rand(d, generator=gen) + 0.5).to(dtype).to(device)
+    wk = (torch.rand(d, generator=gen) + 0.5).to(dtype).to(device)
+    cos, sin = rope_tables(d, 2048, device=device)
+    pos = torch.from_numpy(rng.integers(0, 2048, size=t)).to(device)
+    slots = torch.from_numpy(_rand_slots(rng, nb, bs, t - 4, pad=4)).to(device)
+    pool_k = torch.randn(nb, bs, hk, d, generator=gen).to(dtype).to(device)
+    pool_v = torch.randn(nb, bs, hk, d, generator=gen).to(dtype).to(device)
+    want_k, want_v = pool_k.clone(), pool_v.clone()
+    q_want = extension.qk_norm_rope_kv_write(q.contiguous(), k.contiguous(), v.contiguous(), wq,
+                                             wk, pos, cos, sin, 1e-6, want_k, want_v, slots)
+    q_got = extension.qk_norm_rope_kv_write(q, k, v, wq, wk, pos, cos, sin, 1e-6, pool_k, pool_v,
+                                            slots)
+    torch.cuda.synchronize()
+    assert torch.equal(q_got, q_want)
+    assert torch.equal(pool_k, want_k) and torch.equal(pool_v, want_v)
+
+
 def test_qk_norm_rope_kv_write_leaves_fp8_pools_to_the_two_ops(extension, device):
     """An fp8 pool (quantised with per-block scales) is not written by the fused launch:
     ops returns None and the caller runs qk_norm_rope then kv_write."""
