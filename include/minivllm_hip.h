@@ -206,6 +206,16 @@ int mvllm_qk_norm_rope_kv_write(void* q_out, void* key_pool, void* value_pool, c
 int mvllm_swiglu(void* out, const void* gate, const void* up, int64_t n, int32_t dtype,
                  void* stream);
 
+/* h_out = x + residual (rounded to dtype as torch's add rounds) and out = RMSNorm(h_out)
+ * with weight and eps (rounded as mvllm_rmsnorm), all [rows, dim] contiguous: the
+ * residual add and the norm after the o and down projections of prefill-sized steps
+ * (model/qwen3_paged.py:97-99,111-113) in one pass. Dims beyond 512 16-byte chunks, or
+ * not a whole number of chunks, return MVLLM_ERR_UNSUPPORTED; no counterpart in
+ * mini_vllm_C. */
+int mvllm_add_rmsnorm(void* h_out, void* out, const void* x, const void* residual,
+                      const void* weight, int64_t rows, int32_t dim, float eps, int32_t dtype,
+                      void* stream);
+
 /* mvllm_swiglu over the fused gate/up projection's output: gate_up [rows, 2 cols] in
  * the 16-column interleave of mvllm_linear_swiglu's weight (columns 32j .. 32j+15: gate
  * columns 16j .. 16j+15; the next 16: the same up columns), out [rows, cols] contiguous;

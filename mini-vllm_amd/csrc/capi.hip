@@ -739,6 +739,32 @@ int mvllm_swiglu(void* out, const void* gate, const void* up, int64_t n, int32_t
       "swiglu: launch");
 }
 
+int mvllm_add_rmsnorm(void* h_out, void* out, const void* x, const void* residual,
+                      const void* weight, int64_t rows, int32_t dim, float eps, int32_t dtype,
+                      void* stream) {
+  g_error[0] = '\0';
+  if (!mvllm::add_rmsnorm_supported(dtype, dim)) {
+    return fail(MVLLM_ERR_UNSUPPORTED,
+                "add_rmsnorm: dtype code %d with dim %d is not served (f32/f16/bf16, dim a "
+                "multiple of one 16-byte chunk, at most 512 chunks); add then call rmsnorm",
+                dtype, dim);
+  }
+  if (rows < 0) return fail(MVLLM_ERR_INVALID, "add_rmsnorm: negative row count");
+  if (rows == 0) return MVLLM_OK;
+  if (h_out == nullptr || out == nullptr || x == nullptr || residual == nullptr ||
+      weight == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "add_rmsnorm: a required pointer is NULL");
+  }
+  if ((reinterpret_cast<uintptr_t>(h_out) | reinterpret_cast<uintptr_t>(out) |
+       reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(residual) |
+       reinterpret_cast<uintptr_t>(weight)) % 16 != 0) {
+    return fail(MVLLM_ERR_INVALID, "add_rmsnorm: every tensor must be 16-byte aligned");
+  }
+  return hip_status(mvllm::launch_add_rmsnorm(x, residual, weight, h_out, out, rows, dim, eps,
+                                              dtype, static_cast<hipStream_t>(stream)),
+                    "add_rmsnorm: launch");
+}
+
 int mvllm_swiglu_interleaved(void* out, const void* gate_up, int64_t rows, int64_t cols,
                              int32_t dtype, void* stream) {
   g_error[0] = '\0';

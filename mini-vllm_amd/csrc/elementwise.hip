@@ -25,11 +25,16 @@ namespace mvllm {
 // kR lanes per row (a power of two <= 64), each holding up to kMaxCh 16-byte chunks of
 // the row in registers between the reduction and the scale pass; 64 / kR rows per wave.
 // x and out are streamed nontemporally, the weight row (shared by every row) is cached.
-template <typename T, int kR, int kMaxCh>
+// With kAdd the row is first h = T(x + residual) (torch's add: an fp32 sum rounded to
+// T), stored to h_out, and the norm runs on h: the residual add of a transformer block
+// and the RMSNorm after it in one pass.
+template <typename T, int kR, int kMaxCh, bool kAdd = false>
 __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const void* __restrict__ x,
                                                           const void* __restrict__ w,
                                                           void* __restrict__ out, int64_t rows,
-                                                          int dim, float eps) {
+                                                          int dim, float eps,
+                                                          const void* __restrict__ residual = nullptr,
+                                                          void* __restrict__ h_out = nullptr) {
   constexpr int E = Chunk<T>::kN;
   const int lane = threadIdx.x % kWave;
   const int64_t row = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kR;
@@ -45,6 +50,28 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const void* __restrict
     const int chunk = r + c * kR;
     if (chunk < chunks) {
       held[c] = nt_load16(xr + chunk * 16);
+      if constexpr (kAdd) {
+        const int64_t off = (live ? row : 0) * static_cast<int64_t>(dim) * Elem<T>::kBytes + chunk * 16;
+        float a[E], b[E];
+        Chunk<T>::unpack(held[c], a);
+        Chunk<T>::unpack(nt_load16(static_cast<const char*>(residual) + off), b);
+        u32x4 h;
+        if constexpr (E == 4) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = __float_as_uint(a[e] + b[e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < E; e += 2) {
+            if constexpr (__is_same(T, bf16_t)) {
+              h[e / 2] = f32_to_bf16_bits(a[e] + b[e]) | (f32_to_bf16_bits(a[e + 1] + b[e + 1]) << 16);
+            } else {
+              h[e / 2] = f32_to_f16_bits(a[e] + b[e]) | (f32_to_f16_bits(a[e + 1] + b[e + 1]) << 16);
+            }
+          }
+        }
+        held[c] = h;
+        if (live) nt_store16(static_cast<char*>(h_out) + off, h);
+      }
       float f[E];
       Chunk<T>::unpack(held[c], f);
 #pragma unroll
@@ -114,48 +141,78 @@ __global__ __launch_bounds__(256) void rmsnorm_scalar_kernel(const void* __restr
 
 namespace {
 
-template <typename T, int kR>
-hipError_t launch_rmsnorm_r(const void* x, const void* w, void* out, int64_t rows, int dim,
-                            float eps, hipStream_t stream) {
+template <typename T, int kR, bool kAdd>
+hipError_t launch_rmsnorm_rk(const void* x, const void* w, void* out, int64_t rows, int dim,
+                             float eps, const void* residual, void* h_out, hipStream_t stream) {
   constexpr int E = Chunk<T>::kN;
   const int chunks = dim / E;
   const int per_lane = (chunks + kR - 1) / kR;
   const int64_t threads = rows * kR;
   const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
   if (per_lane <= 1) {
-    rmsnorm_vec_kernel<T, kR, 1><<<grid, 256, 0, stream>>>(x, w, out, rows, dim, eps);
+    rmsnorm_vec_kernel<T, kR, 1, kAdd><<<grid, 256, 0, stream>>>(x, w, out, rows, dim, eps, residual, h_out);
   } else if (per_lane <= 2) {
-    rmsnorm_vec_kernel<T, kR, 2><<<grid, 256, 0, stream>>>(x, w, out, rows, dim, eps);
+    rmsnorm_vec_kernel<T, kR, 2, kAdd><<<grid, 256, 0, stream>>>(x, w, out, rows, dim, eps, residual, h_out);
   } else if (per_lane <= 4) {
-    rmsnorm_vec_kernel<T, kR, 4><<<grid, 256, 0, stream>>>(x, w, out, rows, dim, eps);
+    rmsnorm_vec_kernel<T, kR, 4, kAdd><<<grid, 256, 0, stream>>>(x, w, out, rows, dim, eps, residual, h_out);
   } else {
-    rmsnorm_vec_kernel<T, kR, 8><<<grid, 256, 0, stream>>>(x, w, out, rows, dim, eps);
+    rmsnorm_vec_kernel<T, kR, 8, kAdd><<<grid, 256, 0, stream>>>(x, w, out, rows, dim, eps, residual, h_out);
   }
   return hipGetLastError();
 }
 
+template <typename T, int kR>
+hipError_t launch_rmsnorm_r(const void* x, const void* w, void* out, int64_t rows, int dim,
+                            float eps, hipStream_t stream, const void* residual = nullptr,
+                            void* h_out = nullptr) {
+  if (residual != nullptr) {
+    return launch_rmsnorm_rk<T, kR, true>(x, w, out, rows, dim, eps, residual, h_out, stream);
+  }
+  return launch_rmsnorm_rk<T, kR, false>(x, w, out, rows, dim, eps, nullptr, nullptr, stream);
+}
+
 template <typename T>
 hipError_t launch_rmsnorm_t(const void* x, const void* w, void* out, int64_t rows, int dim,
-                            float eps, hipStream_t stream) {
+                            float eps, hipStream_t stream, const void* res = nullptr,
+                            void* h_out = nullptr) {
   constexpr int E = Chunk<T>::kN;
   const bool aligned = (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
-                        reinterpret_cast<uintptr_t>(out)) % 16 == 0;
+                        reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(res) |
+                        reinterpret_cast<uintptr_t>(h_out)) % 16 == 0;
   const int chunks = dim / E;
   if (!aligned || dim % E != 0 || chunks > 64 * 8) {
+    if (res != nullptr) return hipErrorInvalidValue;  // the add has the vector kernel only
     const dim3 grid(static_cast<unsigned>((rows * kWave + 255) / 256));
     rmsnorm_scalar_kernel<T><<<grid, 256, 0, stream>>>(x, w, out, rows, dim, eps);
     return hipGetLastError();
   }
-  if (chunks <= 1) return launch_rmsnorm_r<T, 1>(x, w, out, rows, dim, eps, stream);
-  if (chunks <= 2) return launch_rmsnorm_r<T, 2>(x, w, out, rows, dim, eps, stream);
-  if (chunks <= 4) return launch_rmsnorm_r<T, 4>(x, w, out, rows, dim, eps, stream);
-  if (chunks <= 8) return launch_rmsnorm_r<T, 8>(x, w, out, rows, dim, eps, stream);
-  if (chunks <= 16) return launch_rmsnorm_r<T, 16>(x, w, out, rows, dim, eps, stream);
-  if (chunks <= 32) return launch_rmsnorm_r<T, 32>(x, w, out, rows, dim, eps, stream);
-  return launch_rmsnorm_r<T, 64>(x, w, out, rows, dim, eps, stream);
+  if (chunks <= 1) return launch_rmsnorm_r<T, 1>(x, w, out, rows, dim, eps, stream, res, h_out);
+  if (chunks <= 2) return launch_rmsnorm_r<T, 2>(x, w, out, rows, dim, eps, stream, res, h_out);
+  if (chunks <= 4) return launch_rmsnorm_r<T, 4>(x, w, out, rows, dim, eps, stream, res, h_out);
+  if (chunks <= 8) return launch_rmsnorm_r<T, 8>(x, w, out, rows, dim, eps, stream, res, h_out);
+  if (chunks <= 16) return launch_rmsnorm_r<T, 16>(x, w, out, rows, dim, eps, stream, res, h_out);
+  if (chunks <= 32) return launch_rmsnorm_r<T, 32>(x, w, out, rows, dim, eps, stream, res, h_out);
+  return launch_rmsnorm_r<T, 64>(x, w, out, rows, dim, eps, stream, res, h_out);
 }
 
 }  // namespace
+
+bool add_rmsnorm_supported(int dtype, int dim) {
+  const int e = dtype == kF32 ? 4 : 8;
+  return (dtype == kF32 || dtype == kF16 || dtype == kBF16) && dim > 0 && dim % e == 0 &&
+         dim / e <= 64 * 8;
+}
+
+hipError_t launch_add_rmsnorm(const void* x, const void* residual, const void* w, void* h_out,
+                              void* out, int64_t rows, int dim, float eps, int dtype,
+                              hipStream_t stream) {
+  switch (dtype) {
+    case kF32: return launch_rmsnorm_t<float>(x, w, out, rows, dim, eps, stream, residual, h_out);
+    case kF16: return launch_rmsnorm_t<f16_t>(x, w, out, rows, dim, eps, stream, residual, h_out);
+    case kBF16: return launch_rmsnorm_t<bf16_t>(x, w, out, rows, dim, eps, stream, residual, h_out);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 hipError_t launch_rmsnorm(const void* x, const void* w, void* out, int64_t rows, int dim,
                           float eps, int dtype, hipStream_t stream) {

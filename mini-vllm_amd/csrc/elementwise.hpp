@@ -8,6 +8,12 @@ namespace mvllm {
 
 hipError_t launch_rmsnorm(const void* x, const void* w, void* out, int64_t rows, int dim,
                           float eps, int dtype, hipStream_t stream);
+// h_out = T(x + residual) and out = RMSNorm(h_out) in one pass (rows of dim elements,
+// every pointer 16-byte aligned); add_rmsnorm_supported says which dims it takes.
+bool add_rmsnorm_supported(int dtype, int dim);
+hipError_t launch_add_rmsnorm(const void* x, const void* residual, const void* w, void* h_out,
+                              void* out, int64_t rows, int dim, float eps, int dtype,
+                              hipStream_t stream);
 hipError_t launch_rope(const void* x, const void* positions, int pos_bytes, const float* cos_t,
                        const float* sin_t, void* out, int64_t rows, int64_t heads, int dim,
                        int64_t num_positions, int64_t max_positions, int dtype,

@@ -193,6 +193,8 @@ def _bind(lib: ctypes.CDLL) -> None:
     )
     lib.mvllm_rmsnorm.restype = ctypes.c_int
     lib.mvllm_rmsnorm.argtypes = [p, p, p, i64, i64, f32, i32, p]
+    lib.mvllm_add_rmsnorm.restype = ctypes.c_int
+    lib.mvllm_add_rmsnorm.argtypes = [p, p, p, p, p, i64, i32, f32, i32, p]
     lib.mvllm_rope.restype = ctypes.c_int
     lib.mvllm_rope.argtypes = [p, p, p, i32, p, p, i64, i64, i64, i64, i64, i32, p]
     lib.mvllm_swiglu.restype = ctypes.c_int
@@ -237,6 +239,7 @@ EXPORTED_SYMBOLS = (
     "mvllm_rope",
     "mvllm_swiglu",
     "mvllm_swiglu_interleaved",
+    "mvllm_add_rmsnorm",
     "mvllm_axpby",
     "mvllm_kv_write",
     "mvllm_qk_norm_rope",
@@ -327,6 +330,35 @@ class HipExtension:
         out = torch.empty_like(x)
         self._check(self.lib.mvllm_axpby(out.data_ptr(), x.data_ptr(), a, b, x.numel(), _stream(x.device)))
         return out
+
+    @staticmethod
+    def add_rmsnorm_supported(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor) -> bool:
+        """Whether ``add_rmsnorm`` serves these tensors (the library's own rule: f32, f16
+        or bf16 alike, CUDA, rows of whole 16-byte chunks, at most 512 of them)."""
+        e = 4 if x.dtype == torch.float32 else 8
+        dim = x.shape[-1] if x.dim() else 0
+        return (x.dtype in (torch.float32, torch.float16, torch.bfloat16) and x.is_cuda
+                and residual.dtype == x.dtype and weight.dtype == x.dtype
+                and residual.shape == x.shape and weight.shape == (dim,)
+                and dim > 0 and dim % e == 0 and dim // e <= 512)
+
+    def add_rmsnorm(self, x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                    eps: float = 1e-6) -> tuple[torch.Tensor, torch.Tensor]:
+        """``h = residual + x`` (torch's rounding) and ``rmsnorm(h)`` in one launch;
+        returns (h, normed)."""
+        if not (residual.is_cuda and weight.is_cuda) or not self.add_rmsnorm_supported(x, residual, weight):
+            raise RuntimeError("add_rmsnorm: x, residual and weight must be CUDA tensors of one "
+                               "dtype (f32, f16, bf16), x and residual alike, rows of whole "
+                               "16-byte chunks (at most 512)")
+        x, residual, weight = x.contiguous(), residual.contiguous(), weight.contiguous()
+        h = torch.empty_like(x)
+        out = torch.empty_like(x)
+        dim = x.shape[-1]
+        self._check(self.lib.mvllm_add_rmsnorm(h.data_ptr(), out.data_ptr(), x.data_ptr(),
+                                               residual.data_ptr(), weight.data_ptr(),
+                                               x.numel() // dim, dim, float(eps),
+                                               DTYPE_CODES[x.dtype], _stream(x.device)))
+        return h, out
 
     def rmsnorm(self, x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
         """RMSNorm over the last dim (reference csrc/rmsnorm.cu:121-169)."""

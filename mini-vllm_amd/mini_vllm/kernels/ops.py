@@ -132,6 +132,20 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
     return torch_path.rms_norm(x, weight, eps)
 
 
+def add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                eps: float = 1e-6, use_cuda: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(h, rmsnorm(h))`` for ``h = residual + x``: a block's residual add and the norm
+    after it (reference qwen3_paged.py:97-99,111-113 run them as two ops). Kernel:
+    ``csrc/elementwise.hip``, one launch, bit for bit the add then ``rmsnorm``; shapes it
+    does not take run the two ops."""
+    if _use_kernel("rmsnorm", use_cuda, x):
+        ext = load_extension()
+        if ext.add_rmsnorm_supported(x, residual, weight):
+            return ext.add_rmsnorm(x, residual, weight, eps)
+    h = residual + x
+    return h, rmsnorm(h, weight, eps, use_cuda=use_cuda)
+
+
 def rope(x: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
          use_cuda: bool = False) -> torch.Tensor:
     """Rotary embedding at explicit positions. Kernel: ``csrc/elementwise.hip``."""

@@ -182,6 +182,10 @@ class Qwen3Paged:
             both = ops.linear_residual_rmsnorm(x, pw, h, norm_w, c.rms_norm_eps, use_cuda=u)
             if both is not None:
                 return both
+            if not ops.skinny(x, use_cuda=u):
+                # prefill-sized: the BLAS product, then the add and the norm in one pass
+                return ops.add_rmsnorm(ops.linear(x, pw, use_cuda=u), h, norm_w,
+                                       c.rms_norm_eps, use_cuda=u)
             h = ops.linear_residual(x, pw, h, use_cuda=u)
         else:
             h = h + ops.linear(x, dense_w, use_cuda=u)

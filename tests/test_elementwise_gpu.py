@@ -189,6 +189,33 @@ def test_swiglu_is_bitwise_equal_to_torch(extension, device, dtype, shape):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("rows,dim", [(1, 128), (37, 1024), (2048, 1024), (5, 2048)])
+def test_add_rmsnorm_is_the_add_then_rmsnorm(extension, device, dtype, rows, dim):
+    """One pass for a block's residual add and the RMSNorm after it: h bitwise torch's
+    add, the normed rows bitwise the rmsnorm kernel on that h; ops routes to it."""
+    gen = torch.Generator().manual_seed(rows * 3 + dim)
+    x = (torch.randn(rows, dim, generator=gen) * 2).to(dtype).to(device)
+    r = torch.randn(rows, dim, generator=gen).to(dtype).to(device)
+    w = (torch.rand(dim, generator=gen) + 0.5).to(dtype).to(device)
+    h, normed = extension.add_rmsnorm(x, r, w, 1e-6)
+    want_h = r + x
+    assert torch.equal(h, want_h)
+    assert torch.equal(normed, extension.rmsnorm(want_h, w, 1e-6))
+    h2, n2 = ops.add_rmsnorm(x, r, w, 1e-6, use_cuda=True)
+    assert torch.equal(h2, h) and torch.equal(n2, normed)
+
+
+def test_add_rmsnorm_refusals_and_fallback(extension, device):
+    x = torch.randn(4, 100, dtype=torch.bfloat16, device=device)  # 100 not a whole chunk count
+    w = torch.ones(100, dtype=torch.bfloat16, device=device)
+    assert not extension.add_rmsnorm_supported(x, x, w)
+    with pytest.raises(RuntimeError, match="16-byte chunks"):
+        extension.add_rmsnorm(x, x, w)
+    h, n = ops.add_rmsnorm(x, x, w, use_cuda=True)  # the two ops instead
+    assert torch.equal(h, x + x) and torch.equal(n, extension.rmsnorm(x + x, w))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("rows,cols", [(1, 16), (7, 48), (300, 3072)])
 def test_swiglu_interleaved_is_split_then_swiglu(extension, device, dtype, rows, cols):
     """SwiGLU read straight off the 16-column gate/up interleave equals splitting it

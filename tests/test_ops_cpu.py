@@ -159,3 +159,13 @@ def test_pack_fragments_layout():
                 r, h = 32 * t + l % 32, l // 32
                 want = w[r, 16 * s + 8 * h:16 * s + 8 * h + 8] if r < n else torch.zeros(8)
                 assert torch.equal(packed[t * steps + s, l], want), (t, s, l)
+
+
+def test_add_rmsnorm_torch_path():
+    x, r = torch.randn(3, 64), torch.randn(3, 64)
+    w = torch.rand(64) + 0.5
+    h, n = ops.add_rmsnorm(x, r, w)
+    torch.testing.assert_close(h, r + x, rtol=0, atol=0)
+    torch.testing.assert_close(n, ops.rmsnorm(r + x, w), rtol=0, atol=0)
+    with pytest.raises(RuntimeError, match="needs device tensors"):
+        ops.add_rmsnorm(x, r, w, use_cuda=True)
