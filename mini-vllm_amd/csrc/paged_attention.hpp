@@ -35,6 +35,17 @@ __host__ __device__ inline int prefill_item_tiles(int context, int len, int q) {
   return (context - len + last + kPrefillKeyTile - 1) / kPrefillKeyTile;
 }
 
+// Stream decode: the workgroups that take a share. Shares of at least
+// kMinDecodeShareKeys keys: with few decode keys (a prefill step carrying a handful of
+// decode rows) equal shares over every CU would cut each sequence into dozens of
+// pieces, whose merge then costs more than the keys. Shared by the decode kernel and
+// its merge.
+constexpr int64_t kMinDecodeShareKeys = 128;
+__host__ __device__ inline int64_t decode_stream_shares(int64_t total_keys, int64_t wgs) {
+  const int64_t cap = (total_keys + kMinDecodeShareKeys - 1) / kMinDecodeShareKeys;
+  return cap < 1 ? 1 : (cap < wgs ? cap : wgs);
+}
+
 // Equal shares of `total` work units over `wgs` workgroups: workgroup w owns
 // [floor(w * total / wgs), floor((w + 1) * total / wgs)).
 __host__ __device__ inline int64_t share_begin(int64_t w, int64_t total, int64_t wgs) {

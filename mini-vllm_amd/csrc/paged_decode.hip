@@ -327,10 +327,11 @@ __global__ __launch_bounds__(512) void paged_decode_stream_kernel(const PagedPar
   __syncthreads();
 
   const int64_t total = s_prefix[n];
-  const int64_t wgs = gridDim.x;
+  const int64_t wgs = decode_stream_shares(total, gridDim.x);
   if (blockIdx.x == 0) {
     for (int s = tid; s <= n; s += blockDim.x) p.seq_prefix[s] = s_prefix[s];
   }
+  if (blockIdx.x >= wgs) return;  // whole workgroup: no barrier follows for it
   const int64_t lo = static_cast<int64_t>(blockIdx.x) * total / wgs;
   const int64_t hi = (static_cast<int64_t>(blockIdx.x) + 1) * total / wgs;
   if (lo >= hi) return;  // whole workgroup: no barrier follows for it
@@ -389,8 +390,8 @@ __global__ __launch_bounds__(1024) void paged_decode_stream_merge_kernel(const P
                                                                          int wgs_i) {
   constexpr int kBatch = 8;  // pieces whose loads are issued together
   const int seq = blockIdx.x;
-  const int64_t wgs = wgs_i;
   const int64_t total = p.seq_prefix[p.num_seqs];
+  const int64_t wgs = decode_stream_shares(total, wgs_i);
   const int64_t begin = p.seq_prefix[seq];
   const int64_t end = p.seq_prefix[seq + 1];
   if (end == begin || total == 0) return;
