@@ -123,6 +123,14 @@ def test_plan_is_host_only_and_consistent(lib):
     ("mvllm_rope", (1, 1, 1, 8, 1, 1, 6, 2, 8, 2, 16, 0, None), "cannot broadcast"),
     ("mvllm_rope", (1, 1, 1, 2, 1, 1, 4, 2, 8, 2, 16, 0, None), "int32 or int64"),
     ("mvllm_swiglu", (1, 1, 1, 8, 9, None), "float64 is not supported"),
+    ("mvllm_swiglu_interleaved", (16, 16, 4, 40, 2, None), "multiple of 16"),
+    ("mvllm_add_rmsnorm", (16, 16, 16, 16, 16, 4, 100, 1e-6, 2, None), "is not served"),
+    # a q token stride shorter than the token's heads (16 x 128)
+    ("mvllm_qk_norm_rope_kv_write", (16,) * 9 + (4, 16, 16, 16, 4, 16, 8, 128, 4, 64, 1e-6,
+                                     100, 0, 2, None), "token strides"),
+    # a k/v token stride that breaks 16-byte alignment (bf16: a multiple of 8 elements)
+    ("mvllm_qk_norm_rope_kv_write", (16,) * 9 + (4, 16, 16, 16, 4, 16, 8, 128, 4, 64, 1e-6,
+                                     0, 1028, 2, None), "16-byte aligned"),
 ])
 def test_elementwise_refusals(lib, fn, args, message):
     assert getattr(lib, fn)(*args) != 0
