@@ -117,14 +117,16 @@ def run_engine(requests: int = 256, max_tokens: int = 256, max_sequences: int = 
     from mini_vllm.block import BlockManager
     from mini_vllm.model import ModelConfig, Qwen3Paged, random_weights
     from mini_vllm.serve import LLMEngine, SchedulerConfig
+    from mini_vllm.workloads import (CONFIG5_BUDGET, CONFIG5_CHUNK, config5_pool_blocks,
+                                     config5_prompts)
 
     config = ModelConfig()
     weights = random_weights(config, seed=0, device="cuda")
-    gen = torch.Generator().manual_seed(0)
-    lens = torch.randint(64, 2049, (requests,), generator=gen).tolist()
-    prompts = [torch.randint(0, config.vocab_size, (n,), generator=gen).tolist() for n in lens]
-    blocks = max_sequences * -(-(2048 + max_tokens) // 16) + 64 + 1  # + the graphs' dummy page
-    sched = SchedulerConfig(max_batched_tokens=2048, max_sequences=max_sequences, chunk_size=512)
+    prompts = config5_prompts(requests, config.vocab_size)
+    lens = [len(p) for p in prompts]
+    blocks = config5_pool_blocks(max_sequences, max_tokens)
+    sched = SchedulerConfig(max_batched_tokens=CONFIG5_BUDGET, max_sequences=max_sequences,
+                            chunk_size=CONFIG5_CHUNK)
 
     def engine():
         manager = BlockManager(blocks, 16, config.num_hidden_layers, config.num_key_value_heads,
@@ -415,9 +417,13 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
 
+    from mini_vllm.kernels import ops
     from mini_vllm.kernels.extension import load_extension
     from mini_vllm.workloads import prefill_flops
 
+    # Every measured call must run on the kernels: a decline raises instead of timing
+    # the PyTorch path.
+    ops.set_strict(True)
     ext = load_extension()
     log(f"library {ext.path}; device {torch.cuda.get_device_name(0)}")
 

@@ -44,6 +44,12 @@ const char* mvllm_last_error(void);
 /* ABI version of this library (bumped on any signature change). */
 int mvllm_abi_version(void);
 
+/* Identity of the sources this library was built from: 16 hex digits of a SHA-256 over
+ * the kernel sources, their headers and the compiler flags, stamped in by the build
+ * ("unstamped" for a build that did not pass one). A loader compares it with the
+ * sources beside it and refuses a stale library. */
+const char* mvllm_build_id(void);
+
 /* How one paged_attention call will be executed. Filled by mvllm_paged_attention_plan;
  * the caller provides `workspace_bytes` of device memory (256-byte aligned, contents
  * irrelevant) and passes it to mvllm_paged_attention with the same arguments. Calls
@@ -64,14 +70,31 @@ typedef struct mvllm_paged_plan {
   int32_t reserved;
 } mvllm_paged_plan;
 
-/* Plan a paged_attention call. Depends only on the host-side sizes below (never on
- * device data), so it is free to call every iteration. Replaces the grid/split
- * selection of the reference's launch_paged_attention / splits_for
- * (csrc/paged_attention.cu:477-521). */
+/* Explicit overrides of the planner's schedule choices, for measurement and for tests
+ * that force one schedule; a zero field (or a NULL pointer for all of them) keeps the
+ * planner's own choice. The library reads no environment: the schedule depends on
+ * the sizes, the device's CU count and these options only. */
+typedef struct mvllm_plan_options {
+  int32_t decode_schedule;     /* 0 auto; MVLLM_DECODE_STREAM or MVLLM_DECODE_GRID forces one */
+  int32_t decode_wgs_per_cu;   /* stream decode: workgroups per CU (default 1) */
+  int32_t decode_waves_per_cu; /* grid decode: waves per CU the splits aim for (default 16) */
+  int32_t decode_split_tokens; /* grid decode: keys per split (default from the wave target) */
+  int32_t prefill_schedule;    /* 0 auto; 1 forces the stream schedule, 2 the grid */
+  int32_t prefill_wgs_per_cu;  /* stream prefill: workgroups per CU (default 1) */
+  int32_t prefill_staging;     /* 0 auto (direct-to-LDS copies where served); 1 forces the
+                                  register-staged prefill kernel */
+  int32_t reserved;            /* must be 0 */
+} mvllm_plan_options;
+
+/* Plan a paged_attention call. Depends only on the host-side sizes below and the
+ * options (never on device data), so it is free to call every iteration. Replaces the
+ * grid/split selection of the reference's launch_paged_attention / splits_for
+ * (csrc/paged_attention.cu:477-521). `options` may be NULL. */
 int mvllm_paged_attention_plan(int32_t num_tokens, int32_t num_seqs, int32_t num_q_heads,
                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                                int32_t max_query_len, int32_t max_context_len, int32_t q_dtype,
-                               int32_t kv_dtype, mvllm_paged_plan* plan);
+                               int32_t kv_dtype, const mvllm_plan_options* options,
+                               mvllm_paged_plan* plan);
 
 /* Ragged attention over a paged KV cache: every scheduled token of every sequence in
  * one call. Replaces `mini_vllm_C.paged_attention` (csrc/bindings.cpp:23-32,81-94 ->
@@ -93,7 +116,7 @@ int mvllm_paged_attention_plan(int32_t num_tokens, int32_t num_seqs, int32_t num
  * grid; no device read). scale multiplies q.k (the reference default is 1/sqrt(D)).
  * head_dim in {32, 64, 128, 256}; block_size a power of two; num_q_heads a multiple
  * of num_kv_heads; q_dtype in {f32, f16, bf16}; kv_dtype equals q_dtype, or is fp8
- * (with any q_dtype). */
+ * (with any q_dtype). `options` (may be NULL) must be the ones the plan was made with. */
 int mvllm_paged_attention(void* out, const void* q, const void* key_pool,
                           const void* value_pool, const float* k_scales, const float* v_scales,
                           const int32_t* block_tables, const int32_t* cu_seqlens_q,
@@ -102,8 +125,8 @@ int mvllm_paged_attention(void* out, const void* q, const void* key_pool,
                           int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                           int64_t num_blocks, int32_t max_blocks_per_seq, int32_t max_query_len,
                           int32_t max_context_len, float scale, int32_t q_dtype,
-                          int32_t kv_dtype, void* workspace, uint64_t workspace_bytes,
-                          void* stream);
+                          int32_t kv_dtype, const mvllm_plan_options* options, void* workspace,
+                          uint64_t workspace_bytes, void* stream);
 
 /* Dense-cache attention: q, out [batch, query_len, num_q_heads, head_dim] contiguous
  * (token-major); k, v [batch, num_kv_heads, kv_len, head_dim] read through the given
@@ -180,9 +203,10 @@ int mvllm_qk_norm_rope(void* q_out, void* k_out, const void* q, const void* k,
 
 /* mvllm_qk_norm_rope that also writes the paged KV pools of the layer, in the same
  * launch: each rotated k head row goes to key_pool at slot slot_mapping[token] (pool
- * [slots, num_kv_heads, head_dim], i.e. num_blocks x block_size slots, of `dtype`) and v
- * [num_tokens, num_kv_heads, head_dim] is copied to value_pool at the same slot; a
- * negative slot writes nothing. The rotated k is not returned otherwise. Replaces the
+ * [num_slots, num_kv_heads, head_dim], i.e. num_blocks x block_size slots, of `dtype`)
+ * and v [num_tokens, num_kv_heads, head_dim] is copied to value_pool at the same slot; a
+ * slot outside [0, num_slots) writes nothing (negative: padding rows of a captured
+ * decode graph). The rotated k is not returned otherwise. Replaces the
  * rmsnorm/rope calls plus PagedKvPool.write's two index_copy_ (model/qwen3_paged.py:
  * 73-80 -> block/kv_pool.py:116-155) for a pool of q's dtype (an fp8 pool takes
  * mvllm_qk_norm_rope then mvllm_kv_write); no counterpart in mini_vllm_C. */
@@ -191,7 +215,8 @@ int mvllm_qk_norm_rope_kv_write(void* q_out, void* key_pool, void* value_pool, c
                                 const void* k_weight, const void* positions,
                                 int32_t positions_bytes, const float* cos_table,
                                 const float* sin_table, const int32_t* slot_mapping,
-                                int64_t num_tokens, int32_t num_q_heads, int32_t num_kv_heads,
+                                int64_t num_slots, int64_t num_tokens, int32_t num_q_heads,
+                                int32_t num_kv_heads,
                                 int32_t head_dim, int64_t num_positions, int64_t max_positions,
                                 float eps, int64_t q_token_stride, int64_t kv_token_stride,
                                 int32_t dtype, void* stream);
@@ -234,8 +259,9 @@ int mvllm_swiglu_interleaved(void* out, const void* gate_up, int64_t rows, int64
  *   v_scales     [num_blocks, num_kv_heads] float32, read and updated; required iff
  *                pool_dtype is fp8, else NULL
  *   key, value   [num_tokens, num_kv_heads, head_dim] src_dtype (f32, f16, bf16)
- *   slot_mapping [num_tokens] int32 flat slot (block * block_size + offset); a negative
- *                slot skips its token
+ *   slot_mapping [num_tokens] int32 flat slot (block * block_size + offset); a slot
+ *                outside [0, num_blocks * block_size) skips its token (negative:
+ *                padding rows of a captured decode graph)
  * pool_dtype == src_dtype copies. An fp8 pool (head_dim 32, 64, 128 or 256; no
  * counterpart in the reference) is quantised per (block, kv head): a call's tokens on
  * consecutive rows of one block form
@@ -243,8 +269,7 @@ int mvllm_swiglu_interleaved(void* out, const void* gate_up, int64_t rows, int64
  * block; scale s = max(old scale, least power of two >= max|x| / 448) over the run;
  * rows already in the block are re-encoded as e4m3((code * old) / s) when s grew (an
  * exponent shift: exact unless a value falls into e4m3's subnormals); new rows are
- * e4m3(x / s), round to nearest even, 0 when s is 0. Slot values are not range-checked
- * (the reference's write does not read them back either); shapes are. */
+ * e4m3(x / s), round to nearest even, 0 when s is 0. */
 int mvllm_kv_write(void* key_pool, void* value_pool, float* k_scales, float* v_scales,
                    const void* key, const void* value, const int32_t* slot_mapping,
                    int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim,

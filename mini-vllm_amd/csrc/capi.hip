@@ -57,10 +57,34 @@ int device_cus() {
   return cus;
 }
 
-int env_int(const char* name, int fallback) {
-  const char* v = getenv(name);
-  if (v == nullptr || *v == '\0') return fallback;
-  return atoi(v);
+// The planner's options with the defaults filled in (mvllm_plan_options: 0 = default).
+struct Options {
+  int decode_schedule = 0;
+  int decode_wgs_per_cu = 1;
+  int decode_waves_per_cu = 16;
+  int decode_split_tokens = 0;
+  int prefill_schedule = 0;
+  int prefill_wgs_per_cu = 1;
+  int prefill_staging = 0;
+};
+
+int read_options(const mvllm_plan_options* o, Options& out) {
+  out = Options{};
+  if (o == nullptr) return MVLLM_OK;
+  if (o->decode_schedule < 0 || o->decode_schedule > MVLLM_DECODE_GRID ||
+      o->prefill_schedule < 0 || o->prefill_schedule > 2 || o->prefill_staging < 0 ||
+      o->prefill_staging > 1 || o->decode_wgs_per_cu < 0 || o->decode_waves_per_cu < 0 ||
+      o->decode_split_tokens < 0 || o->prefill_wgs_per_cu < 0 || o->reserved != 0) {
+    return fail(MVLLM_ERR_INVALID, "paged_attention: plan options out of range");
+  }
+  out.decode_schedule = o->decode_schedule;
+  if (o->decode_wgs_per_cu > 0) out.decode_wgs_per_cu = o->decode_wgs_per_cu;
+  if (o->decode_waves_per_cu > 0) out.decode_waves_per_cu = o->decode_waves_per_cu;
+  out.decode_split_tokens = o->decode_split_tokens;
+  out.prefill_schedule = o->prefill_schedule;
+  if (o->prefill_wgs_per_cu > 0) out.prefill_wgs_per_cu = o->prefill_wgs_per_cu;
+  out.prefill_staging = o->prefill_staging;
+  return MVLLM_OK;
 }
 
 int check_paged_shape(int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk, int32_t d,
@@ -111,6 +135,7 @@ int check_paged_shape(int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t 
 struct Plan {
   mvllm_paged_plan pub;
   int max_splits = 1;
+  int register_staging = 0;  // prefill: the register-staged kernel even where direct-to-LDS serves
   uint64_t off_o = 0;       // byte offsets into the workspace
   uint64_t off_ml = 0;
   uint64_t off_pf = 0;      // stream prefill: [prefix][O partials][(m, l) partials]
@@ -122,30 +147,30 @@ uint64_t align256(uint64_t v) { return (v + 255) / 256 * 256; }
 
 void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk,
                  int32_t d, int32_t block_size, int32_t max_q, int32_t max_ctx, int32_t q_dtype,
-                 int32_t kv_dtype);
+                 int32_t kv_dtype, const Options& o);
 
 // The MFMA prefill's schedule. The grid (one workgroup per 128-query item) is chosen
 // when there are at least as many items as CUs: the hardware dispatcher then balances
 // them, with no partials to merge. With fewer items (a chunk of a long prompt, a
 // prefill beside decodes) the grid would leave CUs idle behind a few long items, so
-// the stream schedule is used: one persistent workgroup per CU (times
-// MVLLM_PREFILL_WGS_PER_CU) with balanced shares of all key tiles, cut items merged
+// the stream schedule is used: one persistent workgroup per CU (times the
+// prefill_wgs_per_cu option) with balanced shares of all key tiles, cut items merged
 // after (measured at 8K-16K contexts: 2.5-3x the grid). The item count is estimated
-// from host sizes: ceil(num_tokens / 128) query tiles per kv column.
-// MVLLM_PREFILL_SCHEDULE=1 / 2 forces stream / grid. The stream's workspace follows
+// from host sizes: ceil(num_tokens / 128) query tiles per kv column. The
+// prefill_schedule option 1 / 2 forces stream / grid. The stream's workspace follows
 // the decode part's.
 void plan_prefill(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk,
-                  int32_t d) {
+                  int32_t d, const Options& o) {
   if (!plan.pub.prefill_mfma) return;
+  plan.register_staging = o.prefill_staging;
   if (num_seqs > mvllm::kMaxStreamSeqs) return;
-  const int forced = env_int("MVLLM_PREFILL_SCHEDULE", 0);
+  const int forced = o.prefill_schedule;
   if (forced == 2) return;
   const int64_t items = static_cast<int64_t>((num_tokens + mvllm::kPrefillQueryTile - 1) /
                                              mvllm::kPrefillQueryTile) *
                         (hq / mvllm::prefill_item_heads(hq / hk));
   if (forced != 1 && items >= device_cus()) return;
-  const int64_t per_cu = env_int("MVLLM_PREFILL_WGS_PER_CU", 1);
-  int64_t wgs = (per_cu > 0 ? per_cu : 1) * device_cus();
+  int64_t wgs = static_cast<int64_t>(o.prefill_wgs_per_cu) * device_cus();
   if (wgs > mvllm::kMaxPrefillWgs) wgs = mvllm::kMaxPrefillWgs;
   const uint64_t rows = static_cast<uint64_t>(2 * wgs) * mvllm::prefill_item_heads(hq / hk) *
                         mvllm::kPrefillQueryTile;
@@ -158,17 +183,17 @@ void plan_prefill(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, 
 
 Plan make_plan(int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk, int32_t d,
                int32_t block_size, int32_t max_q, int32_t max_ctx, int32_t q_dtype,
-               int32_t kv_dtype) {
+               int32_t kv_dtype, const Options& o = Options{}) {
   Plan plan{};
   plan_decode(plan, num_tokens, num_seqs, hq, hk, d, block_size, max_q, max_ctx, q_dtype,
-              kv_dtype);
-  plan_prefill(plan, num_tokens, num_seqs, hq, hk, d);
+              kv_dtype, o);
+  plan_prefill(plan, num_tokens, num_seqs, hq, hk, d, o);
   return plan;
 }
 
 void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk,
                  int32_t d, int32_t block_size, int32_t max_q, int32_t max_ctx, int32_t q_dtype,
-                 int32_t kv_dtype) {
+                 int32_t kv_dtype, const Options& o) {
   const bool has_prefill = max_q > 1;
   const bool mfma =
       has_prefill && mvllm::paged_prefill_supported(q_dtype, kv_dtype, d, hq, hk, block_size);
@@ -185,7 +210,7 @@ void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, i
     plan.pub.decode_mode = MVLLM_DECODE_NONE;
   } else if (num_seqs <= mvllm::kMaxStreamSeqs && units <= 8 &&
              static_cast<int64_t>(num_seqs) * max_ctx < (int64_t{1} << 31) &&
-             env_int("MVLLM_DECODE_SCHEDULE", 0) != 2) {
+             o.decode_schedule != MVLLM_DECODE_GRID) {
     plan.pub.decode_mode = MVLLM_DECODE_STREAM;
   } else {
     plan.pub.decode_mode = MVLLM_DECODE_GRID;
@@ -194,8 +219,7 @@ void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, i
   if (plan.pub.decode_mode == MVLLM_DECODE_STREAM) {
     // A few workgroups per CU, each streaming an equal share of all decode keys; no
     // more workgroups than there are ~64-key shares in the largest possible batch.
-    const int64_t per_cu = env_int("MVLLM_DECODE_WGS_PER_CU", 1);
-    int64_t wgs = (per_cu > 0 ? per_cu : 1) * device_cus();
+    int64_t wgs = static_cast<int64_t>(o.decode_wgs_per_cu) * device_cus();
     const int64_t by_size = (static_cast<int64_t>(num_seqs) * max_ctx + 63) / 64;
     if (wgs > by_size) wgs = by_size;
     if (wgs < 1) wgs = 1;
@@ -213,12 +237,12 @@ void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, i
   // Grid schedules: split each row's context until the grid holds ~16 waves per CU,
   // in splits of 64..1024 keys.
   const int64_t rows = plan.pub.decode_mode == MVLLM_DECODE_BY_ROW ? num_tokens : num_seqs;
-  const int64_t target = static_cast<int64_t>(env_int("MVLLM_DECODE_WAVES_PER_CU", 16)) * device_cus();
+  const int64_t target = static_cast<int64_t>(o.decode_waves_per_cu) * device_cus();
   const int64_t single = rows * units > 0 ? rows * units : 1;
   const int64_t wanted = (target + single - 1) / single;
   int64_t split = (max_ctx + wanted - 1) / wanted;
   split = (split + 63) / 64 * 64;
-  const int override_split = env_int("MVLLM_DECODE_SPLIT_TOKENS", 0);
+  const int override_split = o.decode_split_tokens;
   if (override_split > 0) split = (override_split + 15) / 16 * 16;
   if (split < 64) split = 64;
   if (split > mvllm::kMaxSplitTokens) split = mvllm::kMaxSplitTokens;
@@ -242,6 +266,7 @@ int launch_planned(const Plan& plan, mvllm::PagedParams& p, void* workspace, int
   p.split_tokens = plan.pub.split_tokens > 0 ? plan.pub.split_tokens : mvllm::kMaxSplitTokens;
   p.max_splits = plan.max_splits;
   p.by_row = plan.pub.decode_mode == MVLLM_DECODE_BY_ROW ? 1 : 0;
+  p.pf_register_staging = plan.register_staging;
   if (plan.pub.workspace_bytes > 0) {
     char* ws = static_cast<char*>(workspace);
     if (plan.pub.decode_mode == MVLLM_DECODE_STREAM) p.seq_prefix = reinterpret_cast<int*>(ws);
@@ -354,7 +379,7 @@ int qk_norm_rope_entry(void* q_out, void* k_out, const void* q, const void* k,
                        int64_t num_tokens, int32_t num_q_heads, int32_t num_kv_heads,
                        int32_t head_dim, int64_t num_positions, int64_t max_positions, float eps,
                        int32_t dtype, void* stream, const void* v, void* k_pool, void* v_pool,
-                       const int32_t* slots, int64_t q_token_stride = 0,
+                       const int32_t* slots, int64_t num_slots = 0, int64_t q_token_stride = 0,
                        int64_t kv_token_stride = 0) {
   if (dtype != mvllm::kF32 && dtype != mvllm::kF16 && dtype != mvllm::kBF16) {
     return fail(MVLLM_ERR_INVALID,
@@ -411,8 +436,8 @@ int qk_norm_rope_entry(void* q_out, void* k_out, const void* q, const void* k,
       mvllm::launch_qk_norm_rope(q, k, q_weight, k_weight, positions, positions_bytes, cos_table,
                                  sin_table, q_out, k_out, num_tokens, num_q_heads, num_kv_heads,
                                  head_dim, num_positions, max_positions, eps, dtype,
-                                 static_cast<hipStream_t>(stream), v, k_pool, v_pool, slots, qs,
-                                 kvs),
+                                 static_cast<hipStream_t>(stream), v, k_pool, v_pool, slots,
+                                 num_slots, qs, kvs),
       "qk_norm_rope: launch");
 }
 
@@ -422,19 +447,28 @@ extern "C" {
 
 const char* mvllm_last_error(void) { return g_error; }
 
-int mvllm_abi_version(void) { return 7; }
+int mvllm_abi_version(void) { return 8; }
+
+#ifndef MVLLM_SOURCE_HASH
+#define MVLLM_SOURCE_HASH "unstamped"
+#endif
+const char* mvllm_build_id(void) { return MVLLM_SOURCE_HASH; }
 
 int mvllm_paged_attention_plan(int32_t num_tokens, int32_t num_seqs, int32_t num_q_heads,
                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                                int32_t max_query_len, int32_t max_context_len, int32_t q_dtype,
-                               int32_t kv_dtype, mvllm_paged_plan* plan) {
+                               int32_t kv_dtype, const mvllm_plan_options* options,
+                               mvllm_paged_plan* plan) {
   g_error[0] = '\0';
   if (plan == nullptr) return fail(MVLLM_ERR_INVALID, "paged_attention_plan: plan is NULL");
-  const int rc = check_paged_shape(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim,
-                                   block_size, max_query_len, max_context_len, q_dtype, kv_dtype);
+  int rc = check_paged_shape(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                             block_size, max_query_len, max_context_len, q_dtype, kv_dtype);
+  if (rc != MVLLM_OK) return rc;
+  Options o;
+  rc = read_options(options, o);
   if (rc != MVLLM_OK) return rc;
   *plan = make_plan(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
-                    max_query_len, max_context_len, q_dtype, kv_dtype)
+                    max_query_len, max_context_len, q_dtype, kv_dtype, o)
               .pub;
   return MVLLM_OK;
 }
@@ -447,11 +481,14 @@ int mvllm_paged_attention(void* out, const void* q, const void* key_pool,
                           int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                           int64_t num_blocks, int32_t max_blocks_per_seq, int32_t max_query_len,
                           int32_t max_context_len, float scale, int32_t q_dtype,
-                          int32_t kv_dtype, void* workspace, uint64_t workspace_bytes,
-                          void* stream) {
+                          int32_t kv_dtype, const mvllm_plan_options* options, void* workspace,
+                          uint64_t workspace_bytes, void* stream) {
   g_error[0] = '\0';
   int rc = check_paged_shape(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim,
                              block_size, max_query_len, max_context_len, q_dtype, kv_dtype);
+  if (rc != MVLLM_OK) return rc;
+  Options o;
+  rc = read_options(options, o);
   if (rc != MVLLM_OK) return rc;
   if (num_tokens == 0 || num_seqs == 0) return MVLLM_OK;
   if (out == nullptr || q == nullptr || key_pool == nullptr || value_pool == nullptr ||
@@ -469,7 +506,7 @@ int mvllm_paged_attention(void* out, const void* q, const void* key_pool,
                 "only for one");
   }
   const Plan plan = make_plan(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim,
-                              block_size, max_query_len, max_context_len, q_dtype, kv_dtype);
+                              block_size, max_query_len, max_context_len, q_dtype, kv_dtype, o);
   const uint64_t need = plan.pub.workspace_bytes;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     return fail(MVLLM_ERR_WORKSPACE,
@@ -693,7 +730,7 @@ int mvllm_qk_norm_rope(void* q_out, void* k_out, const void* q, const void* k,
   return qk_norm_rope_entry(q_out, k_out, q, k, q_weight, k_weight, positions, positions_bytes,
                             cos_table, sin_table, num_tokens, num_q_heads, num_kv_heads, head_dim,
                             num_positions, max_positions, eps, dtype, stream, nullptr, nullptr,
-                            nullptr, nullptr);
+                            nullptr, nullptr, 0);
 }
 
 int mvllm_qk_norm_rope_kv_write(void* q_out, void* key_pool, void* value_pool, const void* q,
@@ -701,11 +738,12 @@ int mvllm_qk_norm_rope_kv_write(void* q_out, void* key_pool, void* value_pool, c
                                 const void* k_weight, const void* positions,
                                 int32_t positions_bytes, const float* cos_table,
                                 const float* sin_table, const int32_t* slot_mapping,
-                                int64_t num_tokens, int32_t num_q_heads, int32_t num_kv_heads,
-                                int32_t head_dim, int64_t num_positions, int64_t max_positions,
-                                float eps, int64_t q_token_stride, int64_t kv_token_stride,
-                                int32_t dtype, void* stream) {
+                                int64_t num_slots, int64_t num_tokens, int32_t num_q_heads,
+                                int32_t num_kv_heads, int32_t head_dim, int64_t num_positions,
+                                int64_t max_positions, float eps, int64_t q_token_stride,
+                                int64_t kv_token_stride, int32_t dtype, void* stream) {
   g_error[0] = '\0';
+  if (num_slots < 0) return fail(MVLLM_ERR_INVALID, "qk_norm_rope_kv_write: negative num_slots");
   if (num_tokens > 0 && (key_pool == nullptr || value_pool == nullptr || v == nullptr ||
                          slot_mapping == nullptr)) {
     return fail(MVLLM_ERR_INVALID, "qk_norm_rope_kv_write: a required pointer is NULL");
@@ -717,7 +755,7 @@ int mvllm_qk_norm_rope_kv_write(void* q_out, void* key_pool, void* value_pool, c
   return qk_norm_rope_entry(q_out, nullptr, q, k, q_weight, k_weight, positions, positions_bytes,
                             cos_table, sin_table, num_tokens, num_q_heads, num_kv_heads, head_dim,
                             num_positions, max_positions, eps, dtype, stream, v, key_pool,
-                            value_pool, slot_mapping, q_token_stride, kv_token_stride);
+                            value_pool, slot_mapping, num_slots, q_token_stride, kv_token_stride);
 }
 
 int mvllm_swiglu(void* out, const void* gate, const void* up, int64_t n, int32_t dtype,
@@ -1010,7 +1048,7 @@ int mvllm_kv_write(void* key_pool, void* value_pool, float* k_scales, float* v_s
   while ((1 << shift) < block_size) ++shift;
   return hip_status(mvllm::launch_kv_write(key_pool, value_pool, k_scales, v_scales, key, value,
                                            slot_mapping, num_tokens, num_kv_heads, head_dim,
-                                           shift, src_dtype, pool_dtype,
+                                           shift, num_blocks, src_dtype, pool_dtype,
                                            static_cast<hipStream_t>(stream)),
                     "kv_write: launch");
 }

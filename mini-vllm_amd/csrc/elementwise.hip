@@ -406,6 +406,7 @@ struct KvSink {
   void* v_pool;
   const int32_t* slots;
   int64_t v_rows;
+  int64_t num_slots;  // slots outside [0, num_slots) are skipped
 };
 // Elements between consecutive tokens of the q input and of the k and v inputs (the
 // rows of one token are contiguous head vectors): hq D and hk D when each is its own
@@ -432,7 +433,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
       if (local >= kv.v_rows) return;
       const int64_t vt = local / hk;
       const int32_t slot = kv.slots[vt];
-      if (slot < 0) return;
+      if (slot < 0 || slot >= kv.num_slots) return;
       const int64_t dst = (static_cast<int64_t>(slot) * hk + local % hk) * D * Elem<T>::kBytes;
       const int64_t src = (vt * ts.kv + (local - vt * hk) * D) * Elem<T>::kBytes;
       store16(static_cast<char*>(kv.v_pool) + dst + r * 16,
@@ -513,7 +514,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   if constexpr (KV) {
     if (is_k) {
       const int32_t slot = kv.slots[token];
-      if (slot >= 0) {
+      if (slot >= 0 && slot < kv.num_slots) {
         const int64_t dst = (static_cast<int64_t>(slot) * hk + local % hk) * D * Elem<T>::kBytes;
         store16(static_cast<char*>(kv.k_pool) + dst + r * 16, packed);
       }
@@ -590,8 +591,9 @@ hipError_t launch_qk_norm_rope(const void* q, const void* k, const void* wq, con
                                int hq, int hk, int dim, int64_t num_positions,
                                int64_t max_positions, float eps, int dtype, hipStream_t stream,
                                const void* v, void* k_pool, void* v_pool, const int32_t* slots,
-                               int64_t q_token_stride, int64_t kv_token_stride) {
-  const KvSink kv{v, k_pool, v_pool, slots, k_pool != nullptr ? tokens * hk : 0};
+                               int64_t num_slots, int64_t q_token_stride,
+                               int64_t kv_token_stride) {
+  const KvSink kv{v, k_pool, v_pool, slots, k_pool != nullptr ? tokens * hk : 0, num_slots};
   const TokenStrides ts{q_token_stride > 0 ? q_token_stride : static_cast<int64_t>(hq) * dim,
                         kv_token_stride > 0 ? kv_token_stride : static_cast<int64_t>(hk) * dim};
   switch (dtype) {

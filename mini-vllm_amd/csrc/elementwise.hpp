@@ -22,8 +22,8 @@ hipError_t launch_rope(const void* x, const void* positions, int pos_bytes, cons
 // per head a power of two from 2 to 64).
 bool qk_norm_rope_supported(int dtype, int head_dim);
 // With k_pool non-null the launch also writes k (as rotated) and v to the paged pools
-// [slots, hk, dim] of the same dtype at slots[token] (negative: skipped); k_out may
-// then be null.
+// [num_slots, hk, dim] of the same dtype at slots[token] (outside [0, num_slots):
+// skipped); k_out may then be null.
 hipError_t launch_qk_norm_rope(const void* q, const void* k, const void* wq, const void* wk,
                                const void* positions, int pos_bytes, const float* cos_t,
                                const float* sin_t, void* q_out, void* k_out, int64_t tokens,
@@ -31,7 +31,8 @@ hipError_t launch_qk_norm_rope(const void* q, const void* k, const void* wq, con
                                int64_t max_positions, float eps, int dtype, hipStream_t stream,
                                const void* v = nullptr, void* k_pool = nullptr,
                                void* v_pool = nullptr, const int32_t* slots = nullptr,
-                               int64_t q_token_stride = 0, int64_t kv_token_stride = 0);
+                               int64_t num_slots = 0, int64_t q_token_stride = 0,
+                               int64_t kv_token_stride = 0);
 // (Token strides in elements between consecutive tokens of q and of k and v; 0 means
 // contiguous, hq * dim and hk * dim.)
 // out [rows][cols] = swiglu of the 16-column gate/up interleave [rows][2 cols]; cols a

@@ -39,7 +39,8 @@ __global__ __launch_bounds__(256) void kv_copy_kernel(void* __restrict__ k_pool,
                                                       const void* __restrict__ key,
                                                       const void* __restrict__ value,
                                                       const int32_t* __restrict__ slots,
-                                                      int64_t chunks_per_token, int64_t total) {
+                                                      int64_t chunks_per_token, int64_t total,
+                                                      int64_t num_slots) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= 2 * total) return;
   const bool is_v = i >= total;
@@ -47,7 +48,7 @@ __global__ __launch_bounds__(256) void kv_copy_kernel(void* __restrict__ k_pool,
   const int64_t t = j / chunks_per_token;
   const int64_t c = j - t * chunks_per_token;
   const int32_t slot = slots[t];
-  if (slot < 0) return;
+  if (slot < 0 || slot >= num_slots) return;
   const char* src = static_cast<const char*>(is_v ? value : key) + j * 16;
   char* dst = static_cast<char*>(is_v ? v_pool : k_pool) +
               (static_cast<int64_t>(slot) * chunks_per_token + c) * 16;
@@ -61,14 +62,15 @@ __global__ __launch_bounds__(256) void kv_copy_scalar_kernel(void* __restrict__ 
                                                              const void* __restrict__ key,
                                                              const void* __restrict__ value,
                                                              const int32_t* __restrict__ slots,
-                                                             int64_t row, int64_t total) {
+                                                             int64_t row, int64_t total,
+                                                             int64_t num_slots) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= 2 * total) return;
   const bool is_v = i >= total;
   const int64_t j = is_v ? i - total : i;
   const int64_t t = j / row;
   const int32_t slot = slots[t];
-  if (slot < 0) return;
+  if (slot < 0 || slot >= num_slots) return;
   static_cast<T*>(is_v ? v_pool : k_pool)[static_cast<int64_t>(slot) * row + (j - t * row)] =
       static_cast<const T*>(is_v ? value : key)[j];
 }
@@ -107,7 +109,7 @@ __global__ __launch_bounds__(256) void kv_write_fp8_kernel(uint8_t* __restrict__
                                                            const void* __restrict__ value,
                                                            const int32_t* __restrict__ slots,
                                                            int num_tokens, int hk,
-                                                           int block_shift) {
+                                                           int block_shift, int64_t num_blocks) {
   constexpr int E = 8;            // elements per task piece
   constexpr int kPieces = D / E;  // tasks per (head, K/V)
   constexpr int kUnroll = 4;      // rows whose loads are issued together
@@ -118,6 +120,7 @@ __global__ __launch_bounds__(256) void kv_write_fp8_kernel(uint8_t* __restrict__
   const int slot0 = slots[t0];
   if (slot0 < 0) return;
   const int page = slot0 >> block_shift;
+  if (page >= num_blocks) return;  // out of the pool: skipped, like a negative slot
   const int rows_per_page = 1 << block_shift;
   const int off0 = slot0 & (rows_per_page - 1);
   if (t0 > 0) {
@@ -280,11 +283,12 @@ __global__ __launch_bounds__(256) void kv_write_fp8_kernel(uint8_t* __restrict__
 template <typename TS>
 hipError_t launch_fp8_t(void* k_pool, void* v_pool, float* k_scales, float* v_scales,
                         const void* key, const void* value, const int32_t* slots, int num_tokens,
-                        int hk, int head_dim, int block_shift, hipStream_t stream) {
+                        int hk, int head_dim, int block_shift, int64_t num_blocks,
+                        hipStream_t stream) {
 #define MVLLM_KV_FP8(DIM)                                                                     \
   kv_write_fp8_kernel<TS, DIM><<<(num_tokens + 3) / 4, 256, 0, stream>>>(                     \
       static_cast<uint8_t*>(k_pool), static_cast<uint8_t*>(v_pool), k_scales, v_scales, key, \
-      value, slots, num_tokens, hk, block_shift)
+      value, slots, num_tokens, hk, block_shift, num_blocks)
   switch (head_dim) {
     case 32: MVLLM_KV_FP8(32); break;
     case 64: MVLLM_KV_FP8(64); break;
@@ -307,17 +311,18 @@ bool kv_write_supported(int src_dtype, int pool_dtype, int head_dim) {
 
 hipError_t launch_kv_write(void* k_pool, void* v_pool, float* k_scales, float* v_scales,
                            const void* key, const void* value, const int32_t* slots,
-                           int num_tokens, int hk, int head_dim, int block_shift, int src_dtype,
-                           int pool_dtype, hipStream_t stream) {
+                           int num_tokens, int hk, int head_dim, int block_shift,
+                           int64_t num_blocks, int src_dtype, int pool_dtype, hipStream_t stream) {
   if (pool_dtype == kFP8E4M3) {
     switch (src_dtype) {
-      case kF32: return launch_fp8_t<float>(k_pool, v_pool, k_scales, v_scales, key, value, slots, num_tokens, hk, head_dim, block_shift, stream);
-      case kF16: return launch_fp8_t<f16_t>(k_pool, v_pool, k_scales, v_scales, key, value, slots, num_tokens, hk, head_dim, block_shift, stream);
-      case kBF16: return launch_fp8_t<bf16_t>(k_pool, v_pool, k_scales, v_scales, key, value, slots, num_tokens, hk, head_dim, block_shift, stream);
+      case kF32: return launch_fp8_t<float>(k_pool, v_pool, k_scales, v_scales, key, value, slots, num_tokens, hk, head_dim, block_shift, num_blocks, stream);
+      case kF16: return launch_fp8_t<f16_t>(k_pool, v_pool, k_scales, v_scales, key, value, slots, num_tokens, hk, head_dim, block_shift, num_blocks, stream);
+      case kBF16: return launch_fp8_t<bf16_t>(k_pool, v_pool, k_scales, v_scales, key, value, slots, num_tokens, hk, head_dim, block_shift, num_blocks, stream);
       default: return hipErrorInvalidValue;
     }
   }
   const int elt = src_dtype == kF32 ? 4 : 2;
+  const int64_t num_slots = num_blocks << block_shift;
   const int64_t row_bytes = static_cast<int64_t>(hk) * head_dim * elt;
   const bool aligned = (reinterpret_cast<uintptr_t>(k_pool) | reinterpret_cast<uintptr_t>(v_pool) |
                         reinterpret_cast<uintptr_t>(key) | reinterpret_cast<uintptr_t>(value)) % 16 == 0;
@@ -325,15 +330,15 @@ hipError_t launch_kv_write(void* k_pool, void* v_pool, float* k_scales, float* v
     const int64_t per_token = row_bytes / 16;
     const int64_t total = per_token * num_tokens;
     kv_copy_kernel<<<static_cast<unsigned>((2 * total + 255) / 256), 256, 0, stream>>>(
-        k_pool, v_pool, key, value, slots, per_token, total);
+        k_pool, v_pool, key, value, slots, per_token, total, num_slots);
   } else {
     const int64_t row = static_cast<int64_t>(hk) * head_dim;
     const int64_t total = row * num_tokens;
     const unsigned grid = static_cast<unsigned>((2 * total + 255) / 256);
     if (elt == 4) {
-      kv_copy_scalar_kernel<float><<<grid, 256, 0, stream>>>(k_pool, v_pool, key, value, slots, row, total);
+      kv_copy_scalar_kernel<float><<<grid, 256, 0, stream>>>(k_pool, v_pool, key, value, slots, row, total, num_slots);
     } else {
-      kv_copy_scalar_kernel<uint16_t><<<grid, 256, 0, stream>>>(k_pool, v_pool, key, value, slots, row, total);
+      kv_copy_scalar_kernel<uint16_t><<<grid, 256, 0, stream>>>(k_pool, v_pool, key, value, slots, row, total, num_slots);
     }
   }
   return hipGetLastError();

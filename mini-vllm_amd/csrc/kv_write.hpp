@@ -11,7 +11,7 @@ bool kv_write_supported(int src_dtype, int pool_dtype, int head_dim);
 
 hipError_t launch_kv_write(void* k_pool, void* v_pool, float* k_scales, float* v_scales,
                            const void* key, const void* value, const int32_t* slots,
-                           int num_tokens, int hk, int head_dim, int block_shift, int src_dtype,
-                           int pool_dtype, hipStream_t stream);
+                           int num_tokens, int hk, int head_dim, int block_shift,
+                           int64_t num_blocks, int src_dtype, int pool_dtype, hipStream_t stream);
 
 }  // namespace mvllm

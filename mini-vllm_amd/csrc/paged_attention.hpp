@@ -100,6 +100,8 @@ struct PagedParams {
   float* pf_o;        // stream prefill partials: [2 * pf_wgs][heads][128][D] fp32, each
                       // piece normalised by its own sum
   float* pf_ml;       // their (max in log2 units, sum) per row: [2 * pf_wgs][heads][128][2]
+  int pf_register_staging;  // 1: the register-staged prefill kernel even where the
+                            // direct-to-LDS one serves (a plan option, for measurement)
 };
 
 // Splits of one row: as many as its visible context needs at `split_tokens` keys

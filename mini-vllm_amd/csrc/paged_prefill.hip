@@ -1179,16 +1179,6 @@ void launch_prefill_cfg(const PagedParams& p, int max_query_len, hipStream_t str
   }
 }
 
-// MVLLM_PREFILL_STAGING=1 forces the register-staged kernel where the direct-to-LDS one
-// would run (for measurement); read once per process.
-bool lds_staging_enabled() {
-  static const bool enabled = [] {
-    const char* v = std::getenv("MVLLM_PREFILL_STAGING");
-    return v == nullptr || std::atoi(v) != 1;
-  }();
-  return enabled;
-}
-
 template <typename TQ, int HS>
 void launch_prefill_lds(const PagedParams& p, int max_query_len, hipStream_t stream) {
   if (p.pf_wgs > 0) {
@@ -1207,7 +1197,7 @@ hipError_t launch_prefill_d(const PagedParams& p, int max_query_len, hipStream_t
   // 16-bit pools at D = 128 with pages of >= 16 keys and a positive scale: K copied
   // straight into LDS.
   if constexpr (std::is_same_v<TQ, TKV> && D == 128) {
-    if (p.block_shift >= 4 && p.scale > 0.0f && lds_staging_enabled()) {
+    if (p.block_shift >= 4 && p.scale > 0.0f && !p.pf_register_staging) {
       if (prefill_item_heads(p.hq / p.hk) == 1) {
         launch_prefill_lds<TQ, 1>(p, max_query_len, stream);
       } else {

@@ -19,6 +19,7 @@ synchronizes.
 from __future__ import annotations
 
 import ctypes
+import hashlib
 import math
 import os
 import subprocess
@@ -59,7 +60,7 @@ HIP_FLAGS = [
 # reference's PyTorch expressions round, so FMA contraction is off there.
 EXTRA_FLAGS = {"elementwise.hip": ["-ffp-contract=off"], "linear.hip": ["-ffp-contract=off"]}
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 DTYPE_CODES: dict[torch.dtype, int] = {
     torch.float32: 0,
@@ -86,6 +87,21 @@ def sources() -> list[Path]:
     return found
 
 
+def source_hash() -> str | None:
+    """16 hex digits of a SHA-256 over the kernel sources, their headers and the build
+    flags: the identity the build stamps into the library (``mvllm_build_id``). None
+    when the sources are not beside the package (an installed library)."""
+    files = sorted(CSRC_DIR.glob("*.hip")) + sorted(CSRC_DIR.glob("*.hpp")) + sorted(
+        INCLUDE_DIR.glob("*.h"))
+    if not any(f.suffix == ".hip" for f in files):
+        return None
+    h = hashlib.sha256()
+    h.update(repr((HIP_FLAGS, sorted(EXTRA_FLAGS.items()))).encode())
+    for f in files:
+        h.update(f.name.encode() + b"\0" + f.read_bytes() + b"\0")
+    return h.hexdigest()[:16]
+
+
 def build_library(verbose: bool = False, jobs: int | None = None) -> Path:
     """Compile every ``csrc/*.hip`` for gfx950 and link ``lib/libminivllm_hip.so``.
 
@@ -97,10 +113,12 @@ def build_library(verbose: bool = False, jobs: int | None = None) -> Path:
         raise ToolchainError(f"hipcc not found at {HIPCC}")
     BUILD_DIR.mkdir(parents=True, exist_ok=True)
     LIB_DIR.mkdir(parents=True, exist_ok=True)
+    stamp = f'-DMVLLM_SOURCE_HASH="{source_hash()}"'
 
     def compile_one(src: Path) -> Path:
         obj = BUILD_DIR / (src.stem + ".o")
-        cmd = [HIPCC, *HIP_FLAGS, *EXTRA_FLAGS.get(src.name, []), f"-I{INCLUDE_DIR}", "-c",
+        extra = [*EXTRA_FLAGS.get(src.name, []), *([stamp] if src.name == "capi.hip" else [])]
+        cmd = [HIPCC, *HIP_FLAGS, *extra, f"-I{INCLUDE_DIR}", "-c",
                str(src), "-o", str(obj)]
         result = subprocess.run(cmd, capture_output=True, text=True)
         noise = "'-packed-fp32-ops' is not a recognized feature"
@@ -154,6 +172,38 @@ class _DenseArgs(ctypes.Structure):
     ]
 
 
+class _PlanOptions(ctypes.Structure):
+    """``mvllm_plan_options`` of include/minivllm_hip.h (0 = the planner's choice)."""
+
+    _fields_ = [
+        ("decode_schedule", ctypes.c_int32),
+        ("decode_wgs_per_cu", ctypes.c_int32),
+        ("decode_waves_per_cu", ctypes.c_int32),
+        ("decode_split_tokens", ctypes.c_int32),
+        ("prefill_schedule", ctypes.c_int32),
+        ("prefill_wgs_per_cu", ctypes.c_int32),
+        ("prefill_staging", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+SCHEDULES = {"stream": 1, "grid": 2}
+
+
+def make_plan_options(options: dict[str, Any] | None) -> "_PlanOptions | None":
+    """``mvllm_plan_options`` from a dict of its field names (schedules may be given as
+    "stream" / "grid"); None for the planner's defaults."""
+    if not options:
+        return None
+    fields = {name for name, _ in _PlanOptions._fields_} - {"reserved"}
+    unknown = set(options) - fields
+    if unknown:
+        raise ValueError(f"unknown plan options {sorted(unknown)}; known: {sorted(fields)}")
+    values = {k: SCHEDULES.get(v, v) if k.endswith("schedule") else int(v)
+              for k, v in options.items()}
+    return _PlanOptions(**values)
+
+
 class _Plan(ctypes.Structure):
     _fields_ = [
         ("decode_mode", ctypes.c_int32),
@@ -181,15 +231,18 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_last_error.argtypes = []
     lib.mvllm_abi_version.restype = ctypes.c_int
     lib.mvllm_abi_version.argtypes = []
+    lib.mvllm_build_id.restype = ctypes.c_char_p
+    lib.mvllm_build_id.argtypes = []
+    opts = ctypes.POINTER(_PlanOptions)
     lib.mvllm_paged_attention_plan.restype = ctypes.c_int
-    lib.mvllm_paged_attention_plan.argtypes = [i32] * 10 + [ctypes.POINTER(_Plan)]
+    lib.mvllm_paged_attention_plan.argtypes = [i32] * 10 + [opts, ctypes.POINTER(_Plan)]
     lib.mvllm_dense_attention_plan.restype = ctypes.c_int
     lib.mvllm_dense_attention_plan.argtypes = [ctypes.POINTER(_DenseArgs), ctypes.POINTER(ctypes.c_uint64)]
     lib.mvllm_dense_attention.restype = ctypes.c_int
     lib.mvllm_dense_attention.argtypes = [ctypes.POINTER(_DenseArgs), p, ctypes.c_uint64, p]
     lib.mvllm_paged_attention.restype = ctypes.c_int
     lib.mvllm_paged_attention.argtypes = (
-        [p] * 10 + [i32] * 6 + [i64, i32, i32, i32, f32, i32, i32, p, u64, p]
+        [p] * 10 + [i32] * 6 + [i64, i32, i32, i32, f32, i32, i32, opts, p, u64, p]
     )
     lib.mvllm_rmsnorm.restype = ctypes.c_int
     lib.mvllm_rmsnorm.argtypes = [p, p, p, i64, i64, f32, i32, p]
@@ -207,7 +260,7 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_qk_norm_rope.argtypes = [p] * 7 + [i32, p, p, i64, i32, i32, i32, i64, i64, f32, i32, p]
     lib.mvllm_qk_norm_rope_kv_write.restype = ctypes.c_int
     lib.mvllm_qk_norm_rope_kv_write.argtypes = (
-        [p] * 9 + [i32, p, p, p, i64, i32, i32, i32, i64, i64, f32, i64, i64, i32, p])
+        [p] * 9 + [i32, p, p, p, i64, i64, i32, i32, i32, i64, i64, f32, i64, i64, i32, p])
     lib.mvllm_kv_write.restype = ctypes.c_int
     lib.mvllm_kv_write.argtypes = [p] * 7 + [i32] * 4 + [i64, i32, i32, p]
     lib.mvllm_argmax.restype = ctypes.c_int
@@ -233,6 +286,7 @@ def _bind(lib: ctypes.CDLL) -> None:
 EXPORTED_SYMBOLS = (
     "mvllm_last_error",
     "mvllm_abi_version",
+    "mvllm_build_id",
     "mvllm_paged_attention_plan",
     "mvllm_paged_attention",
     "mvllm_rmsnorm",
@@ -259,7 +313,12 @@ EXPORTED_SYMBOLS = (
 
 
 def open_library(path: Path = LIB_PATH) -> ctypes.CDLL:
-    """dlopen the library and declare its signatures (no GPU needed)."""
+    """dlopen the library and declare its signatures (no GPU needed).
+
+    The in-tree library must have been built from the sources beside it: its stamped
+    build id is compared with :func:`source_hash` and a stale build is refused (a
+    library named by ``MVLLM_LIBRARY`` is the caller's choice and only warned about).
+    """
     if not path.exists():
         raise ToolchainError(
             f"{path} is not built; run `python -m mini_vllm.kernels.extension --build` "
@@ -270,6 +329,13 @@ def open_library(path: Path = LIB_PATH) -> ctypes.CDLL:
     version = lib.mvllm_abi_version()
     if version != ABI_VERSION:
         raise ToolchainError(f"{path} has ABI version {version}, expected {ABI_VERSION}")
+    built, current = lib.mvllm_build_id().decode(), source_hash()
+    if current is not None and built != current:
+        message = (f"{path} was built from other sources (build id {built}, sources "
+                   f"{current}); rebuild it: __graft_entry__.build()")
+        if path == LIB_DIR / "libminivllm_hip.so":
+            raise ToolchainError(message)
+        print(f"warning: {message}", file=sys.stderr)
     return lib
 
 
@@ -292,7 +358,7 @@ class HipExtension:
         self.lib = lib
         self.path = LIB_PATH
         self._workspaces: dict[tuple[int, int], torch.Tensor] = {}
-        self._retired: list[torch.Tensor] = []
+        self._recording: list[torch.Tensor] | None = None
 
     def workspace(self, device: torch.device, nbytes: int) -> torch.Tensor:
         """The kernels' workspace of (device, current stream), grown on demand (paged and
@@ -300,6 +366,9 @@ class HipExtension:
 
         Kept rather than allocated per call so a steady decode loop (or a captured
         graph) reuses one buffer; calls on one stream are ordered, so they never race.
+        A buffer outgrown is dropped (torch's allocator frees it in stream order); a
+        captured graph keeps the buffers its launches name alive itself, through
+        :meth:`recording_workspaces`.
         """
         key = (device.index if device.index is not None else torch.cuda.current_device(),
                _stream(device))
@@ -307,11 +376,28 @@ class HipExtension:
         if ws is None or ws.numel() < nbytes:
             size = max(nbytes, 2 * ws.numel() if ws is not None else 0)
             size = (size + (1 << 20) - 1) >> 20 << 20
-            if ws is not None:
-                self._retired.append(ws)  # a captured graph may still name it
             ws = torch.empty(size, dtype=torch.uint8, device=device)
             self._workspaces[key] = ws
+        if self._recording is not None:
+            self._recording.append(ws)
         return ws
+
+    def recording_workspaces(self):
+        """Context manager yielding the list of every workspace handed out inside it:
+        a graph capture holds that list for as long as the graph lives, since its
+        launches name those buffers."""
+        ext = self
+
+        class _Recorder:
+            def __enter__(self):
+                self.previous, ext._recording = ext._recording, []
+                return ext._recording
+
+            def __exit__(self, *exc):
+                ext._recording = self.previous
+                return False
+
+        return _Recorder()
 
     # -- plumbing
     def _check(self, rc: int) -> None:
@@ -665,31 +751,43 @@ class HipExtension:
             return False
         return head_dim // n in (2, 4, 8, 16, 32, 64)
 
+    @staticmethod
+    def _qk_norm_rope_checks(name: str, q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor,
+                             k_weight: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor,
+                             sin: torch.Tensor) -> int:
+        """The shape, dtype and device rules both fused QK-norm + RoPE entries share
+        (the kernel takes q's token count for k, v and the slots, and reads the tables
+        at pos x D); returns q's dtype code."""
+        tensors = (q, k, q_weight, k_weight, positions, cos, sin)
+        if not all(t.is_cuda for t in tensors):
+            raise RuntimeError(f"{name}: every tensor must be a CUDA tensor")
+        if q.dim() != 3 or k.dim() != 3 or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
+            raise RuntimeError(
+                f"{name}: q must be T x H_q x D and k T x H_k x D, got {tuple(q.shape)} "
+                f"and {tuple(k.shape)}")
+        d = q.shape[2]
+        if q.dtype != k.dtype or q_weight.dtype != q.dtype or k_weight.dtype != q.dtype:
+            raise RuntimeError(f"{name}: q, k and both weights must share a dtype")
+        if q_weight.shape != (d,) or k_weight.shape != (d,):
+            raise RuntimeError(f"{name}: the weights must be [{d}]")
+        if cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.shape != sin.shape \
+                or cos.dim() != 2 or cos.shape[1] != d:
+            raise RuntimeError(f"{name}: the cos/sin tables must be float32 max_pos x {d}")
+        if positions.dtype not in (torch.int32, torch.int64) or positions.dim() != 1:
+            raise RuntimeError(f"{name}: positions must be a 1-D int32 or int64 tensor")
+        code = DTYPE_CODES.get(q.dtype)
+        if code is None or code == 3:
+            raise RuntimeError(f"{name}: dtype {q.dtype} is not supported")
+        return code
+
     def qk_norm_rope(self, q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor,
                      k_weight: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor,
                      sin: torch.Tensor, eps: float = 1e-6) -> tuple[torch.Tensor, torch.Tensor]:
         """Per-head RMSNorm then RoPE of q ``T x H_q x D`` and k ``T x H_k x D`` in one
         launch, bitwise equal to ``rope(rmsnorm(x, w))`` with this library's kernels."""
-        tensors = (q, k, q_weight, k_weight, positions, cos, sin)
-        if not all(t.is_cuda for t in tensors):
-            raise RuntimeError("qk_norm_rope: every tensor must be a CUDA tensor")
-        if q.dim() != 3 or k.dim() != 3 or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
-            raise RuntimeError(
-                f"qk_norm_rope: q must be T x H_q x D and k T x H_k x D, got {tuple(q.shape)} "
-                f"and {tuple(k.shape)}")
+        code = self._qk_norm_rope_checks("qk_norm_rope", q, k, q_weight, k_weight, positions,
+                                         cos, sin)
         d = q.shape[2]
-        if q.dtype != k.dtype or q_weight.dtype != q.dtype or k_weight.dtype != q.dtype:
-            raise RuntimeError("qk_norm_rope: q, k and both weights must share a dtype")
-        if q_weight.shape != (d,) or k_weight.shape != (d,):
-            raise RuntimeError(f"qk_norm_rope: the weights must be [{d}]")
-        if cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.shape != sin.shape \
-                or cos.dim() != 2 or cos.shape[1] != d:
-            raise RuntimeError(f"qk_norm_rope: the cos/sin tables must be float32 max_pos x {d}")
-        if positions.dtype not in (torch.int32, torch.int64):
-            raise RuntimeError("qk_norm_rope: positions must be int32 or int64")
-        code = DTYPE_CODES.get(q.dtype)
-        if code is None or code == 3:
-            raise RuntimeError(f"qk_norm_rope: dtype {q.dtype} is not supported")
         q, k = q.contiguous(), k.contiguous()
         q_out, k_out = torch.empty_like(q), torch.empty_like(k)
         if q.shape[0] == 0:
@@ -713,6 +811,8 @@ class HipExtension:
         launch; returns the rotated q. q, k and v may be column views of one fused
         projection's output: heads contiguous within a token, any 16-byte-aligned token
         stride (k and v sharing theirs)."""
+        name = "qk_norm_rope_kv_write"
+        code = self._qk_norm_rope_checks(name, q, k, q_weight, k_weight, positions, cos, sin)
         if not (key_pool.is_cuda and value_pool.is_cuda and v.is_cuda and slot_mapping.is_cuda):
             raise RuntimeError("qk_norm_rope_kv_write: every tensor must be a CUDA tensor")
         if (key_pool.dtype != q.dtype or value_pool.dtype != q.dtype or v.dtype != q.dtype
@@ -723,16 +823,11 @@ class HipExtension:
                 "qk_norm_rope_kv_write: the pools must be contiguous num_blocks x P x H_k x D "
                 f"tensors of q's dtype matching k and v, got {tuple(key_pool.shape)} "
                 f"{key_pool.dtype} for k {tuple(k.shape)}")
-        if slot_mapping.dtype != torch.int32 or slot_mapping.shape != (k.shape[0],):
-            raise RuntimeError("qk_norm_rope_kv_write: slot_mapping must be int32 [T]")
-        tensors = (q, k, q_weight, k_weight, positions, cos, sin)
-        if not all(t.is_cuda for t in tensors):
-            raise RuntimeError("qk_norm_rope_kv_write: every tensor must be a CUDA tensor")
+        if slot_mapping.dtype != torch.int32 or slot_mapping.shape != (k.shape[0],) \
+                or not slot_mapping.is_contiguous():
+            raise RuntimeError(f"{name}: slot_mapping must be a contiguous int32 [T]")
         d = q.shape[2]
-        code = DTYPE_CODES.get(q.dtype)
-        if code is None or code == 3 or positions.dtype not in (torch.int32, torch.int64):
-            raise RuntimeError(f"qk_norm_rope_kv_write: dtype {q.dtype} / positions "
-                               f"{positions.dtype} not supported")
+
         def rows_ok(t):  # heads contiguous within each token
             return t.stride(2) == 1 and t.stride(1) == d
         if not (rows_ok(q) and rows_ok(k) and rows_ok(v)) or k.stride(0) != v.stride(0):
@@ -746,6 +841,7 @@ class HipExtension:
             k.data_ptr(), v.data_ptr(), q_weight.contiguous().data_ptr(),
             k_weight.contiguous().data_ptr(), positions.data_ptr(), positions.element_size(),
             cos.contiguous().data_ptr(), sin.contiguous().data_ptr(), slot_mapping.data_ptr(),
+            key_pool.shape[0] * key_pool.shape[1],
             q.shape[0], q.shape[1], k.shape[1], d, positions.numel(), cos.shape[0], float(eps),
             q.stride(0), k.stride(0), code, _stream(q.device)))
         return q_out
@@ -918,8 +1014,12 @@ class HipExtension:
         max_context_len: int,
         q_dtype: torch.dtype,
         kv_dtype: torch.dtype,
+        plan_options: dict[str, Any] | None = None,
     ) -> dict[str, int]:
+        """The library's plan for a call of these sizes (``mvllm_paged_attention_plan``);
+        ``plan_options`` are ``mvllm_plan_options`` fields by name."""
         plan = _Plan()
+        opts = make_plan_options(plan_options)
         self._check(
             self.lib.mvllm_paged_attention_plan(
                 num_tokens,
@@ -932,6 +1032,7 @@ class HipExtension:
                 max_context_len,
                 DTYPE_CODES.get(q_dtype, -1),
                 DTYPE_CODES.get(kv_dtype, -1),
+                None if opts is None else ctypes.byref(opts),
                 ctypes.byref(plan),
             )
         )
@@ -954,12 +1055,14 @@ class HipExtension:
         k_scale: torch.Tensor | None = None,
         v_scale: torch.Tensor | None = None,
         out: torch.Tensor | None = None,
+        plan_options: dict[str, Any] | None = None,
     ) -> torch.Tensor:
         """Ragged decode + prefill over a paged cache (reference csrc/paged_attention.cu:598-711).
 
         Same positional arguments and refusals as the reference. Additions, all optional:
-        ``k_scale``/``v_scale`` (``num_blocks x H_k`` fp32) for a float8_e4m3fn pool, and
-        ``out`` to write into a caller-owned ``T x H_q x D`` tensor.
+        ``k_scale``/``v_scale`` (``num_blocks x H_k`` fp32) for a float8_e4m3fn pool,
+        ``out`` to write into a caller-owned ``T x H_q x D`` tensor, and ``plan_options``
+        (``mvllm_plan_options`` fields by name) to force a schedule.
         """
         if not (q.is_cuda and key_pool.is_cuda and value_pool.is_cuda):
             raise RuntimeError("paged_attention: q and the pools must be CUDA tensors")
@@ -1066,6 +1169,8 @@ class HipExtension:
 
         q_code = DTYPE_CODES[q.dtype]
         kv_code = DTYPE_CODES[key_pool.dtype]
+        opts = make_plan_options(plan_options)
+        opts_ref = None if opts is None else ctypes.byref(opts)
         plan = _Plan()
         self._check(
             self.lib.mvllm_paged_attention_plan(
@@ -1079,6 +1184,7 @@ class HipExtension:
                 int(max_context_len),
                 q_code,
                 kv_code,
+                opts_ref,
                 ctypes.byref(plan),
             )
         )
@@ -1110,6 +1216,7 @@ class HipExtension:
                 float(scale),
                 q_code,
                 kv_code,
+                opts_ref,
                 _ptr(workspace),
                 0 if workspace is None else workspace.numel(),
                 _stream(q.device),

@@ -19,19 +19,24 @@ plus two ops that fuse what the reference's caller does in several calls:
 
 The callee behind ``use_cuda=True`` is ``libminivllm_hip.so`` (HIP for gfx950).
 
-One deliberate difference: ``use_cuda=True`` never falls back. The reference routes a
-call its kernel cannot serve (CPU tensors, a non-contiguous pool, int64 tables ...)
-silently to the PyTorch path; here such a call raises ``RuntimeError`` naming the
-reason, because a silent fallback is exactly how a kernel that never ran ends up in
-a benchmark. ``use_cuda=False`` selects the PyTorch path (:mod:`mini_vllm.torch_path`)
-explicitly, as in the reference. Ops that have no kernel in this library yet
-(``attention``, the dense-cache decode/prefill) follow the reference's rule for
-unimplemented kernels and use the PyTorch path, which :func:`dispatch_report` states.
+Routing follows the reference (ops.py:82-89): ``use_cuda=True`` means "use a kernel
+where one applies". A call the kernels cannot serve -- CPU tensors (the same model
+object serves CPU tests and GPU serving), a head dim or dtype mix the library does not
+take, a non-contiguous pool, int64 tables -- runs the PyTorch path
+(:mod:`mini_vllm.torch_path`) instead, and :func:`dispatch_report` lists every such
+decline of the process with its reason. Because a silent fallback is also how a kernel
+that never ran ends up in a benchmark, :func:`set_strict` (or the environment variable
+``MINIVLLM_STRICT_KERNELS=1`` at import, or the :func:`strict_kernels` context) turns
+every decline into a ``RuntimeError`` naming the reason; ``bench.py`` and the GPU
+tests run strict. Ops that route by size rather than by capability (projections of
+prefill-sized inputs go to the vendor BLAS) are not declines.
 """
 
 from __future__ import annotations
 
 import math
+import os
+from contextlib import contextmanager
 from dataclasses import dataclass
 
 import torch
@@ -59,6 +64,8 @@ __all__ = [
     "qk_norm_rope_kv_write",
     "rmsnorm",
     "rope",
+    "set_strict",
+    "strict_kernels",
     "swiglu",
 ]
 
@@ -84,18 +91,59 @@ MAX_PAGED_HEAD_DIM = 256
 PAGED_HEAD_DIMS = (32, 64, 128, 256)
 
 
+# Declines of this process: op name -> {reason: count}.
+FALLBACKS: dict[str, dict[str, int]] = {}
+
+_strict = os.environ.get("MINIVLLM_STRICT_KERNELS", "").strip() not in ("", "0")
+
+
+def set_strict(flag: bool) -> bool:
+    """Make every decline raise (True) or fall back to the PyTorch path (False, the
+    reference's behaviour and the default); returns the previous setting."""
+    global _strict
+    previous, _strict = _strict, bool(flag)
+    return previous
+
+
+def is_strict() -> bool:
+    return _strict
+
+
+@contextmanager
+def strict_kernels(flag: bool = True):
+    """``with strict_kernels():`` -- :func:`set_strict` for the duration of a block."""
+    previous = set_strict(flag)
+    try:
+        yield
+    finally:
+        set_strict(previous)
+
+
+def _decline(name: str, reason: str) -> bool:
+    """A ``use_cuda=True`` call the kernel cannot serve: recorded and routed to the
+    PyTorch path (returns False), or raised in strict mode."""
+    if _strict:
+        raise RuntimeError(f"{name}: {reason} (strict kernel mode: no PyTorch fallback)")
+    counts = FALLBACKS.setdefault(name, {})
+    counts[reason] = counts.get(reason, 0) + 1
+    return False
+
+
+def _served(name: str, reason: str | None) -> bool:
+    """True when the op's own gate found nothing (``reason`` None), else a decline."""
+    return True if reason is None else _decline(name, reason)
+
+
 def _use_kernel(name: str, use_cuda: bool, x: torch.Tensor) -> bool:
-    """Whether ``name`` runs on the HIP kernel; raises instead of falling back."""
+    """Whether ``name`` runs on the HIP kernel for this call (reference ops.py:82-89):
+    ``use_cuda`` set, the op implemented and not held back, and device tensors."""
     if not use_cuda:
         return False
     implemented, _source = CUDA_KERNELS[name]
     if not implemented or name in NOT_YET_FASTER:
         return False
     if not x.is_cuda:
-        raise RuntimeError(
-            f"{name}: use_cuda=True needs device tensors, got {x.device}; pass use_cuda=False "
-            "to run the PyTorch path"
-        )
+        return _decline(name, f"use_cuda=True needs device tensors, got {x.device}")
     return True
 
 
@@ -105,7 +153,8 @@ def cuda_kernel_names() -> list[str]:
 
 
 def dispatch_report(use_cuda: bool) -> str:
-    """One line per op saying which implementation a run would use."""
+    """One line per op saying which implementation a run would use, then the calls of
+    this process that the kernels declined (and so ran on the PyTorch path)."""
     lines = []
     for name, (implemented, source) in CUDA_KERNELS.items():
         if not implemented:
@@ -118,6 +167,11 @@ def dispatch_report(use_cuda: bool) -> str:
             lines.append(f"  {name:<18} hip     (kernel from {source})")
             continue
         lines.append(f"  {name:<18} torch   ({note})")
+    if FALLBACKS:
+        lines.append("  declined calls that ran on the PyTorch path:")
+        for name, reasons in FALLBACKS.items():
+            for reason, count in reasons.items():
+                lines.append(f"    {name:<16} x{count}: {reason}")
     return "\n".join(lines)
 
 
@@ -126,10 +180,21 @@ def dispatch_report(use_cuda: bool) -> str:
 
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
             use_cuda: bool = False) -> torch.Tensor:
-    """RMSNorm over the last dimension (also QK-norm). Kernel: ``csrc/elementwise.hip``."""
-    if _use_kernel("rmsnorm", use_cuda, x):
+    """RMSNorm over the last dimension (also QK-norm). Kernel: ``csrc/elementwise.hip``.
+    The kernel needs ``weight`` in x's dtype (reference ops.py:129); PyTorch would
+    promote instead, so a mixed call runs the PyTorch path."""
+    if _use_kernel("rmsnorm", use_cuda, x) and _served(
+            "rmsnorm", _same_dtype_reason(x, weight, "weight")):
         return load_extension().rmsnorm(x, weight, eps)
     return torch_path.rms_norm(x, weight, eps)
+
+
+def _same_dtype_reason(x: torch.Tensor, other: torch.Tensor, what: str) -> str | None:
+    if other.dtype != x.dtype:
+        return f"{what} is {other.dtype} but x is {x.dtype}; the kernel does not promote"
+    if not other.is_cuda:
+        return f"{what} is on {other.device}"
+    return None
 
 
 def add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
@@ -148,10 +213,19 @@ def add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
 
 def rope(x: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
          use_cuda: bool = False) -> torch.Tensor:
-    """Rotary embedding at explicit positions. Kernel: ``csrc/elementwise.hip``."""
-    if _use_kernel("rope", use_cuda, x):
+    """Rotary embedding at explicit positions. Kernel: ``csrc/elementwise.hip``. The
+    kernel takes fp32 tables and a head axis (reference ops.py:147)."""
+    if _use_kernel("rope", use_cuda, x) and _served("rope", _rope_reason(x, cos, sin)):
         return load_extension().rope(x, positions, cos, sin)
     return torch_path.apply_rope(x, positions, cos, sin)
+
+
+def _rope_reason(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> str | None:
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32:
+        return f"the cos/sin tables are {cos.dtype}/{sin.dtype}, the kernel takes float32"
+    if x.dim() < 3:
+        return f"x has {x.dim()} dimensions; the kernel needs a head axis"
+    return None
 
 
 def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor,
@@ -161,13 +235,17 @@ def qk_norm_rope(q: torch.Tensor, k: torch.Tensor, q_weight: torch.Tensor,
     """Qwen3's QK-norm then RoPE for ``q`` (T x H_q x D) and ``k`` (T x H_k x D): the
     reference caller's ``rmsnorm`` + ``rope`` on each (qwen3_paged.py:73-78). Kernel:
     ``csrc/elementwise.hip`` (one launch, bitwise equal to the unfused kernels); a head
-    dim the fused kernel does not serve runs the unfused kernels."""
+    dim or dtype mix the fused kernel does not serve runs the unfused ops."""
     if _use_kernel("qk_norm_rope", use_cuda, q):
         ext = load_extension()
-        if ext.qk_norm_rope_supported(q.dtype, q.shape[-1]):
+        if (ext.qk_norm_rope_supported(q.dtype, q.shape[-1]) and k.dtype == q.dtype
+                and q_weight.dtype == q.dtype and k_weight.dtype == q.dtype
+                and _rope_reason(q, cos, sin) is None):
             return ext.qk_norm_rope(q, k, q_weight, k_weight, positions, cos, sin, eps)
-        q = ext.rope(ext.rmsnorm(q, q_weight, eps).unsqueeze(0), positions, cos, sin).squeeze(0)
-        k = ext.rope(ext.rmsnorm(k, k_weight, eps).unsqueeze(0), positions, cos, sin).squeeze(0)
+        q = rope(rmsnorm(q, q_weight, eps, use_cuda).unsqueeze(0), positions, cos, sin,
+                 use_cuda).squeeze(0)
+        k = rope(rmsnorm(k, k_weight, eps, use_cuda).unsqueeze(0), positions, cos, sin,
+                 use_cuda).squeeze(0)
         return q, k
     q = torch_path.apply_rope(torch_path.rms_norm(q, q_weight, eps).unsqueeze(0), positions,
                               cos, sin).squeeze(0)
@@ -190,15 +268,20 @@ def qk_norm_rope_kv_write(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         return None
     ext = load_extension()
     if (not ext.qk_norm_rope_supported(q.dtype, q.shape[-1]) or key_pool.dtype != q.dtype
-            or value_pool.dtype != q.dtype or v.dtype != q.dtype):
+            or value_pool.dtype != q.dtype or v.dtype != q.dtype or k.dtype != q.dtype
+            or q_weight.dtype != q.dtype or k_weight.dtype != q.dtype
+            or _rope_reason(q, cos, sin) is not None or not key_pool.is_contiguous()
+            or not value_pool.is_contiguous() or slot_mapping.dtype != torch.int32):
         return None
     return ext.qk_norm_rope_kv_write(q, k, v, q_weight, k_weight, positions, cos, sin, eps,
                                      key_pool, value_pool, slot_mapping)
 
 
 def swiglu(gate: torch.Tensor, up: torch.Tensor, use_cuda: bool = False) -> torch.Tensor:
-    """``silu(gate) * up``. Kernel: ``csrc/elementwise.hip``."""
-    if _use_kernel("swiglu", use_cuda, gate):
+    """``silu(gate) * up``. Kernel: ``csrc/elementwise.hip``; gate and up of one dtype
+    (reference ops.py:161)."""
+    if _use_kernel("swiglu", use_cuda, gate) and _served(
+            "swiglu", _same_dtype_reason(gate, up, "up")):
         return load_extension().swiglu(gate, up)
     return torch_path.silu(gate) * up
 
@@ -341,9 +424,11 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     """
     is_decode = q.shape[-2] == 1
     name = "decode_attention" if is_decode else "flash_prefill"
-    if _use_kernel(name, use_cuda, q) and _kernel_can_attend(q, k, v, mask, is_decode):
+    if _use_kernel(name, use_cuda, q) and _served(name, None if _kernel_can_attend(
+            q, k, v, mask, is_decode) else "a mask, dtype mix or layout the kernel does not bake in"):
         ext = load_extension()
-        if ext.dense_supported(q, k, v):
+        if _served(name, None if ext.dense_supported(q, k, v) else
+                   "a head dim or cache stride layout the library does not take"):
             scale = 1.0 / math.sqrt(q.shape[-1])
             return getattr(ext, name)(q, k, v, scale)
     b, hq, L, d = q.shape
@@ -412,8 +497,9 @@ def paged_attention(
     """
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
-    if _use_kernel("paged_attention", use_cuda, q):
-        _check_kernel_can_page(q, key_pool, value_pool, block_tables)
+    if _use_kernel("paged_attention", use_cuda, q) and _served(
+            "paged_attention", _kernel_can_page(q, key_pool, value_pool, block_tables,
+                                                (cu_seqlens_q, context_lens, seq_lens))):
         return load_extension().paged_attention(
             q, key_pool, value_pool, block_tables, cu_seqlens_q, context_lens, seq_lens,
             int(max_query_len), int(max_context_len), scale, k_scale, v_scale,
@@ -424,28 +510,30 @@ def paged_attention(
     )
 
 
-def _check_kernel_can_page(q: torch.Tensor, key_pool: torch.Tensor, value_pool: torch.Tensor,
-                           block_tables: torch.Tensor) -> None:
-    """The reference's ``_kernel_can_page`` gate (ops.py:257-275), raising instead of
-    declining, plus this library's head-dim set."""
+def _kernel_can_page(q: torch.Tensor, key_pool: torch.Tensor, value_pool: torch.Tensor,
+                     block_tables: torch.Tensor, metadata: tuple[torch.Tensor, ...] = ()) -> str | None:
+    """Why the paged kernels cannot serve this call, or None when they can: the
+    reference's ``_kernel_can_page`` (ops.py:257-275) with this library's head-dim set
+    (32, 64, 128, 256 where the reference takes any D <= 256) and float8 pools."""
     if q.dim() != 3:
-        raise RuntimeError(f"paged_attention: expected q shaped T x H_q x D, got {list(q.shape)}")
+        return f"q is {list(q.shape)}, not T x H_q x D"
     if q.dtype == torch.float64:
-        raise RuntimeError("paged_attention: float64 is not supported; the accumulators here are fp32")
+        return "float64 is not supported; the accumulators here are fp32"
+    fp8 = key_pool.dtype == torch.float8_e4m3fn and value_pool.dtype == torch.float8_e4m3fn
+    if not fp8 and (key_pool.dtype != q.dtype or value_pool.dtype != q.dtype):
+        return f"q ({q.dtype}) and the pools ({key_pool.dtype}, {value_pool.dtype}) must share a dtype"
     if q.shape[-1] not in PAGED_HEAD_DIMS:
-        raise RuntimeError(
-            f"paged_attention: head dim {q.shape[-1]} is not supported; this build serves "
-            f"{', '.join(map(str, PAGED_HEAD_DIMS))}"
-        )
+        return (f"head dim {q.shape[-1]} is not served; this build takes "
+                f"{', '.join(map(str, PAGED_HEAD_DIMS))}")
     if not (q.is_contiguous() and key_pool.is_contiguous() and value_pool.is_contiguous()):
-        raise RuntimeError(
-            "paged_attention: q and the pools must be contiguous; the kernel walks them by "
-            "slot arithmetic rather than by stride"
-        )
-    if block_tables.dtype != torch.int32:
-        raise RuntimeError("paged_attention: the metadata tensors must be int32")
-    if not block_tables.is_contiguous():
-        raise RuntimeError("paged_attention: block_tables must be contiguous")
+        return "q and the pools must be contiguous; the kernel walks them by slot arithmetic"
+    if block_tables.dtype != torch.int32 or not block_tables.is_contiguous():
+        return "block_tables must be contiguous int32"
+    if any(t.dtype != torch.int32 for t in metadata):
+        return "cu_seqlens_q, context_lens and seq_lens must be int32"
+    if not all(t.is_cuda for t in (key_pool, value_pool, block_tables, *metadata)):
+        return "the pools and the metadata must be device tensors"
+    return None
 
 
 def kv_write(key_pool: torch.Tensor, value_pool: torch.Tensor, key: torch.Tensor,
@@ -456,9 +544,25 @@ def kv_write(key_pool: torch.Tensor, value_pool: torch.Tensor, key: torch.Tensor
     Kernel: ``csrc/kv_write.hip``, K and V in one launch. A ``float8_e4m3fn`` pool is
     quantised with per-(block, kv head) scales ``k_scale``/``v_scale`` updated in place
     (policy: include/minivllm_hip.h)."""
-    if _use_kernel("kv_write", use_cuda, key):
+    if _use_kernel("kv_write", use_cuda, key) and _served("kv_write", _kv_write_reason(
+            key_pool, value_pool, key, value, slot_mapping)):
         load_extension().kv_write(key_pool, value_pool, key, value, slot_mapping,
                                   k_scale=k_scale, v_scale=v_scale)
         return
     torch_path.kv_write(key_pool, value_pool, key, value, slot_mapping,
                         k_scale=k_scale, v_scale=v_scale)
+
+
+def _kv_write_reason(key_pool: torch.Tensor, value_pool: torch.Tensor, key: torch.Tensor,
+                     value: torch.Tensor, slot_mapping: torch.Tensor) -> str | None:
+    if not (key_pool.is_cuda and value_pool.is_cuda and value.is_cuda and slot_mapping.is_cuda):
+        return "the pools, values and slot_mapping must be device tensors"
+    if not (key_pool.is_contiguous() and value_pool.is_contiguous()):
+        return "the pools must be contiguous"
+    if slot_mapping.dtype != torch.int32:
+        return f"slot_mapping is {slot_mapping.dtype}, the kernel takes int32"
+    if key.dtype in (torch.float64, torch.float8_e4m3fn) or key.dtype != value.dtype:
+        return f"keys/values of {key.dtype}/{value.dtype} are not served"
+    if key_pool.dtype != key.dtype and key_pool.dtype != torch.float8_e4m3fn:
+        return f"a {key_pool.dtype} pool with {key.dtype} keys is not served"
+    return None

@@ -212,10 +212,15 @@ class Qwen3Paged:
             else:
                 gated = ops.swiglu(ops.linear(normed, w["gate"], use_cuda=u),
                                    ops.linear(normed, w["up"], use_cuda=u), use_cuda=u)
-            next_norm = (self.layers[layer + 1]["attn_norm"] if layer + 1 < n_layers
-                         else self.weights["final_norm"])
+            last = layer + 1 == n_layers
+            next_norm = self.weights["final_norm"] if last else self.layers[layer + 1]["attn_norm"]
+            if last and batch.total_tokens > batch.num_sequences:
+                # Only each sequence's last row reaches the logits (reference
+                # qwen3_paged.py:211-228), and everything after the attention is
+                # row-wise: the last down projection, its residual and the final norm
+                # run on those rows alone.
+                rows = batch.last_row_indices
+                gated, h = gated.index_select(0, rows), h.index_select(0, rows)
             h, normed = self._residual_norm(gated, p.get("down"), w["down"], h, next_norm, fused)
-        # normed is now final_norm(h) of every row; RMSNorm is row-wise, so selecting the
-        # last rows after it equals normalising them after the selection.
-        normed = normed.index_select(0, batch.last_row_indices)
+        # normed is now final_norm(h) of each sequence's last row.
         return ops.linear(normed, self.lm_head, use_cuda=u)

@@ -61,6 +61,7 @@ class _Captured:
         self.model = model
         self.graph = None
         self.logits = None
+        self.workspaces: list[torch.Tensor] = []  # kernel workspaces the graph names
         # numpy views of the pinned buffers, written in place; each table row is
         # rewritten only when the block manager reports a change of that sequence's
         # table (row_keys: (seq_id, version), or None for a dummy row).
@@ -105,8 +106,28 @@ class _Captured:
                 self.model(self.batch)
         torch.cuda.current_stream().wait_stream(side)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph, stream=side):
+        recorder = _workspace_recorder(self.model)
+        with recorder as workspaces, torch.cuda.graph(self.graph, stream=side):
             self.logits = self.model(self.batch)
+        self.workspaces = list(workspaces)
+
+
+class _NoRecorder:
+    def __enter__(self):
+        return []
+
+    def __exit__(self, *exc):
+        return False
+
+
+def _workspace_recorder(model):
+    """Records the kernel library's workspaces a capture names (nothing to record on
+    the PyTorch path), so the graph keeps them alive."""
+    if not model.use_cuda:
+        return _NoRecorder()
+    from mini_vllm.kernels.extension import load_extension
+
+    return load_extension().recording_workspaces()
 
 
 class DecodeGraphs:

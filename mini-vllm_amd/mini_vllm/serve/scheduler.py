@@ -109,6 +109,11 @@ class Scheduler:
                 budget -= n
         while self.waiting and len(self.running) < self.config.max_sequences and budget > 0:
             seq = self.waiting[0]
+            if seq in out.preempted:
+                # Readmitting a victim in the iteration that evicted it lets two long
+                # prompts evict each other forever (each restarting from token zero);
+                # it waits one iteration while the sequence that evicted it advances.
+                break
             n = self._chunk(seq, budget)
             if n == 0:
                 break

@@ -190,3 +190,25 @@ def prefill_flops(batch: PagedBatch) -> int:
     for S, L in zip(batch.contexts, batch.query_lens):
         pairs += L * (S - L) + L * (L + 1) // 2
     return 4 * hq * d * pairs
+
+
+# ----------------------------------------------------------------- config 5
+
+CONFIG5_PROMPT_LEN = (64, 2048)   # inclusive bounds of the uniform prompt lengths
+CONFIG5_BUDGET = 2048             # scheduled tokens per iteration
+CONFIG5_CHUNK = 512               # prefill chunk
+
+
+def config5_prompts(requests: int = 256, vocab_size: int = 151936, seed: int = 0) -> list[list[int]]:
+    """BASELINE config 5's requests: prompt lengths U[64, 2048], token ids uniform in
+    [0, vocab), drawn from one seeded CPU generator (lengths first, then each prompt)."""
+    gen = torch.Generator().manual_seed(seed)
+    lo, hi = CONFIG5_PROMPT_LEN
+    lens = torch.randint(lo, hi + 1, (requests,), generator=gen).tolist()
+    return [torch.randint(0, vocab_size, (n,), generator=gen).tolist() for n in lens]
+
+
+def config5_pool_blocks(max_sequences: int = 32, max_tokens: int = 256, block_size: int = 16) -> int:
+    """Pages for config 5's pool: every in-flight sequence at its longest, a margin, and
+    the decode graphs' reserved dummy page (no preemption at this size)."""
+    return max_sequences * -(-(CONFIG5_PROMPT_LEN[1] + max_tokens) // block_size) + 64 + 1

@@ -43,6 +43,23 @@ def seeded():
     random.seed(SEED)
 
 
+@pytest.fixture(autouse=True)
+def strict_kernels_on_gpu(request):
+    """GPU tests run the seam in strict mode: a ``use_cuda=True`` call the kernels
+    decline raises instead of passing on the PyTorch path, so no GPU test can pass on
+    a fallback. Tests of the fallback itself switch it off for their block."""
+    if request.node.get_closest_marker("gpu") is None:
+        yield
+        return
+    from mini_vllm.kernels import ops
+
+    previous = ops.set_strict(True)
+    try:
+        yield
+    finally:
+        ops.set_strict(previous)
+
+
 @pytest.fixture(scope="session")
 def device() -> torch.device:
     if not torch.cuda.is_available():

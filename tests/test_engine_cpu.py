@@ -90,3 +90,70 @@ def test_logits_rows_are_each_sequences_last_position(model):
     for seq, p in zip(seqs, ps):
         tok, _ = generate_greedy(config, weights, p, 1)
         assert seq.output == tok
+
+
+def test_use_cuda_model_on_cpu_tensors_equals_the_pytorch_path(model):
+    """Port of the reference's tests/test_qwen3_cached.py:335-350 to the paged model:
+    a model built with ``use_cuda=True`` on CPU tensors falls back op by op and gives
+    exactly the ``use_cuda=False`` model's logits and tokens (the same model object
+    serves CPU tests and GPU serving)."""
+    from mini_vllm.kernels import ops
+    from mini_vllm.serve.batch import ForwardBatch
+
+    config, weights = model
+    ps = prompts(3, 4, 20, config.vocab_size, seed=11)
+    logits = {}
+    for use_cuda in (False, True):
+        engine = make_engine(config, weights, use_cuda=use_cuda)
+        seqs = [engine.add_request(p, 4) for p in ps]
+        out = engine.scheduler.schedule()
+        batch = ForwardBatch.from_scheduled(out.scheduled, engine.model.manager)
+        logits[use_cuda] = engine.model(batch)
+        engine.scheduler.commit(out, ops.argmax(logits[use_cuda]).tolist())
+        while engine.scheduler.has_work:
+            engine.step()
+        logits[use_cuda, "tokens"] = [s.output for s in seqs]
+    assert torch.equal(logits[True], logits[False])
+    assert logits[True, "tokens"] == logits[False, "tokens"]
+    assert "declined calls" in ops.dispatch_report(True)
+
+
+def test_cached_dense_recompute_equals_the_full_recompute(model):
+    """The oracle's KV-cached greedy loop (used at the 0.6B shape, where recomputing
+    every step is too slow) against its full recompute: same tokens, logits to 1e-12."""
+    from oracle.qwen3_dense import generate_greedy_cached
+
+    config, weights = model
+    for p in prompts(3, 1, 30, config.vocab_size, seed=12):
+        tok, logits = generate_greedy(config, weights, p, 6)
+        tok_c, logits_c = generate_greedy_cached(config, weights, p, 6)
+        assert tok == tok_c
+        for a, b in zip(logits, logits_c):
+            assert (a - b).abs().max() < 1e-12
+
+
+@pytest.mark.parametrize("num_blocks", [7, 8])
+def test_two_long_prompts_do_not_evict_each_other_forever(num_blocks):
+    """Regression: with a victim readmitted in the iteration that evicted it, two long
+    prompts in a 7- or 8-page pool kept evicting each other, each restarting from token
+    zero, and the engine never finished. A victim now waits one iteration."""
+    from mini_vllm.block import BlockManager
+    from mini_vllm.serve import Scheduler
+    from mini_vllm.serve.sequence import Sequence
+
+    manager = BlockManager(num_blocks, 8, 1, 1, 8, torch.float32)
+    sched = Scheduler(SchedulerConfig(max_batched_tokens=32, chunk_size=16), manager)
+    lens = [36, 21, 29, 35, 12, 10]
+    seqs = [Sequence(i, list(range(n)), 8) for i, n in enumerate(lens)]
+    for s in seqs:
+        sched.add(s)
+    preempted = 0
+    for _ in range(500):
+        if not sched.has_work:
+            break
+        out = sched.schedule()
+        preempted += len(out.preempted)
+        sched.commit(out, [0] * len(out.scheduled))
+    assert not sched.has_work, "the scheduler did not finish"
+    assert preempted > 0 and all(len(s.output) == 8 for s in seqs)
+    manager.check_no_leaks()

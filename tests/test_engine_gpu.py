@@ -113,12 +113,79 @@ def test_engine_with_decode_graphs_matches_dense_recompute(extension, device, sc
         assert_tokens_match(g, tok, logits, tie_tol=1e-4, msg=f"prompt {i}")
 
 
-@pytest.mark.slow
-def test_qwen3_0_6b_shape_end_to_end(extension, device):
-    """BASELINE config 5's model shape (28 layers, 16q/8kv, D=128, vocab 151936, bf16),
-    a few requests with chunked prefill and piggybacked decodes, kernels on."""
+@pytest.fixture(scope="module")
+def qwen3_06b(device):
+    """BASELINE config 5's model: Qwen3-0.6B's shape (28 layers, 16q/8kv, D=128, vocab
+    151936), bf16, random init (seed 0, std 0.02)."""
     config = ModelConfig()
-    weights = random_weights(config, seed=0, device=device)
+    return config, random_weights(config, seed=0, device=device)
+
+
+def _config5_engine(config, weights, device, max_sequences=32, max_tokens=256, **kw):
+    from mini_vllm.workloads import CONFIG5_BUDGET, CONFIG5_CHUNK, config5_pool_blocks
+
+    sched = SchedulerConfig(max_batched_tokens=CONFIG5_BUDGET, max_sequences=max_sequences,
+                            chunk_size=CONFIG5_CHUNK)
+    return make_engine(config, weights, num_blocks=config5_pool_blocks(max_sequences, max_tokens),
+                       use_cuda=True, device=device, sched=sched, use_graphs=True, **kw)
+
+
+@pytest.mark.slow
+@pytest.mark.timeout(600)
+def test_config5_exact_workload(extension, device, qwen3_06b):
+    """BASELINE config 5 exactly as bench.py runs it: 256 requests of U[64, 2048] prompt
+    tokens (seed 0), 256 greedy tokens each, a 2048-token budget, 512-token chunks, 32
+    sequences in flight, decode graphs on. Every token is generated, inside the vocab,
+    every prompt token prefilled once, and no page leaks."""
+    from mini_vllm.workloads import config5_prompts
+
+    config, weights = qwen3_06b
+    ps = config5_prompts(256, config.vocab_size)
+    engine = _config5_engine(config, weights, device)
+    got = engine.generate(ps, 256)
+    st = engine.stats
+    assert st.generated_tokens == 65536 == sum(len(g) for g in got)
+    assert all(len(g) == 256 for g in got)
+    assert st.prefill_tokens == 257310 == sum(len(p) for p in ps)
+    assert st.preemptions == 0 and engine.graphs.replays > 0
+    flat = torch.tensor([t for g in got for t in g])
+    assert int(flat.min()) >= 0 and int(flat.max()) < config.vocab_size
+    manager = engine.model.manager
+    manager.check_no_leaks()
+    assert manager.num_free_blocks == manager.num_blocks - 1  # the graphs' reserved page
+
+
+@pytest.mark.slow
+@pytest.mark.timeout(600)
+def test_qwen3_0_6b_bf16_greedy_tokens_match_the_float64_recompute(extension, device, qwen3_06b):
+    """Config-5 prompts trimmed to 256 tokens through the config-5 engine (bf16, decode
+    graphs, chunked budget), 8 greedy tokens each, against the dense float64 recompute
+    of the same weights (oracle/qwen3_dense.py, KV-cached). The reference's bf16 rule
+    (tests/test_engine.py:471-524): where a prompt first diverges, the engine's token
+    must be the recompute's top-2 at that step, and at least half the prompts agree
+    exactly."""
+    from mini_vllm.workloads import config5_prompts
+    from oracle.qwen3_dense import DenseQwen3
+
+    config, weights = qwen3_06b
+    ps = [p[:256] for p in config5_prompts(6, config.vocab_size)]
+    engine = _config5_engine(config, weights, device)
+    got = engine.generate(ps, MAX_TOKENS)
+    dense = DenseQwen3(config, weights)
+    agree = 0
+    for i, (g, p) in enumerate(zip(got, ps)):
+        tok, logits = dense.generate(p, MAX_TOKENS)
+        ok, step = _first_divergence_is_a_tie(g, tok, logits)
+        assert ok, f"prompt {i} diverges at step {step} outside the recompute's top 2"
+        agree += step is None
+    assert agree >= len(ps) // 2, f"only {agree} of {len(ps)} prompts agree exactly"
+
+
+@pytest.mark.slow
+@pytest.mark.timeout(300)
+def test_qwen3_0_6b_shape_end_to_end(extension, device, qwen3_06b):
+    """A few requests at the model's shape with a smaller budget, kernels on."""
+    config, weights = qwen3_06b
     ps = prompts(6, 64, 700, config.vocab_size, seed=0)
     engine = make_engine(config, weights, num_blocks=512, use_cuda=True, device=device,
                          sched=SchedulerConfig(max_batched_tokens=512, chunk_size=256))
@@ -126,6 +193,44 @@ def test_qwen3_0_6b_shape_end_to_end(extension, device):
     assert all(len(g) == 12 and all(0 <= t < config.vocab_size for t in g) for g in got)
     assert engine.stats.prefill_tokens == sum(len(p) for p in ps)
     engine.model.manager.check_no_leaks()
+
+
+@pytest.mark.parametrize("kv_dtype", [None, torch.float8_e4m3fn], ids=["bf16", "fp8"])
+def test_decode_graphs_under_preemption(extension, device, kv_dtype):
+    """A pool too small for every sequence at once: sequences are preempted (by
+    recompute) and come back with new block tables while decode graphs replay, so a
+    graph row that kept a stale table would read the wrong pages. Tokens against the
+    float64 recompute (bf16, top-2 rule) or the eager engine of the same pool (fp8);
+    no page leaks."""
+    config = tiny_config(torch.bfloat16, head_dim=128, num_attention_heads=4,
+                         num_key_value_heads=2)
+    weights = random_weights(config, seed=13, device=device)
+    ps = prompts(6, 3, 40, config.vocab_size, seed=14)
+    sched = SchedulerConfig(max_batched_tokens=32, chunk_size=16, max_sequences=6)
+    runs = {}
+    for graphs in (True, False):
+        # 8 free pages of 8 tokens either way (the graphs reserve one more)
+        engine = make_engine(config, weights, num_blocks=8 + graphs, block_size=8, use_cuda=True,
+                             device=device, sched=sched, use_graphs=graphs, kv_dtype=kv_dtype)
+        runs[graphs] = engine.generate(ps, MAX_TOKENS)
+        assert engine.stats.preemptions > 0, "the pool was meant to force preemption"
+        if graphs:
+            assert engine.graphs.replays > 0
+        engine.model.manager.check_no_leaks()
+    if kv_dtype is None:
+        # graphs pad the batch, which changes the kernels' work split (and so the sum
+        # order): both runs answer to the float64 recompute's top-2 rule instead
+        want = _reference(config, weights, ps)
+        for graphs, run in runs.items():
+            agree = 0
+            for i, (g, (tok, logits)) in enumerate(zip(run, want)):
+                ok, step = _first_divergence_is_a_tie(g, tok, logits)
+                assert ok, f"graphs={graphs} prompt {i} diverges at step {step} outside the top 2"
+                agree += step is None
+            assert agree >= len(ps) // 2
+    else:
+        assert all(a[0] == b[0] for a, b in zip(runs[True], runs[False]))
+        assert sum(a == b for a, b in zip(runs[True], runs[False])) >= len(ps) - 1
 
 
 @pytest.mark.parametrize("sched", [SchedulerConfig(), SchedulerConfig(max_batched_tokens=24, chunk_size=8)],

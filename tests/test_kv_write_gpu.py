@@ -228,3 +228,64 @@ def test_qk_norm_rope_kv_write_leaves_fp8_pools_to_the_two_ops(extension, device
     pos = torch.arange(4, device=device)
     assert ops.qk_norm_rope_kv_write(q, k, k, w, w, pos, cos, sin, 1e-6, pool, pool, slots,
                                      use_cuda=True) is None
+
+
+def test_qk_norm_rope_kv_write_refuses_mismatched_shapes_before_launch(extension, device):
+    """The fused write takes q's token count for k, v and the slots and reads the tables
+    at pos x D, so every shape it relies on is checked on the host (no launch)."""
+    from mini_vllm.torch_path import rope_tables
+
+    bf = dict(dtype=torch.bfloat16, device=device)
+    q, k, v = (torch.randn(6, h, 128, **bf) for h in (16, 8, 8))
+    w = torch.ones(128, **bf)
+    cos, sin = rope_tables(128, 64, device=device)
+    pool = torch.zeros(4, 16, 8, 128, **bf)
+    slots = torch.arange(6, dtype=torch.int32, device=device)
+    pos = torch.arange(6, device=device)
+    before = pool.clone()
+    call = extension.qk_norm_rope_kv_write
+    with pytest.raises(RuntimeError, match="T x H_q x D"):
+        call(q, k[:4], v[:4], w, w, pos, cos, sin, 1e-6, pool, pool.clone(), slots)
+    with pytest.raises(RuntimeError, match="cos/sin tables"):
+        call(q, k, v, w, w, pos, cos[:, :64], sin[:, :64], 1e-6, pool, pool.clone(), slots)
+    with pytest.raises(RuntimeError, match="weights must be"):
+        call(q, k, v, w[:64], w, pos, cos, sin, 1e-6, pool, pool.clone(), slots)
+    with pytest.raises(RuntimeError, match="T x H_q x D"):
+        call(q.view(6, 16 * 128), k, v, w, w, pos, cos, sin, 1e-6, pool, pool.clone(), slots)
+    with pytest.raises(RuntimeError, match="slot_mapping"):
+        call(q, k, v, w, w, pos, cos, sin, 1e-6, pool, pool.clone(), slots[:5])
+    with pytest.raises(RuntimeError, match="matching k and v"):
+        call(q, k, v[:, :4], w, w, pos, cos, sin, 1e-6, pool, pool.clone(), slots)
+    torch.cuda.synchronize()
+    assert torch.equal(pool, before)
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_slots_outside_the_pool_are_skipped(extension, device, fused):
+    """A slot at or past num_blocks x P writes nothing (as a negative one), in the plain
+    KV write and in the fused QK-norm + RoPE write: the rest of the pool is exactly what
+    the in-range tokens leave."""
+    from mini_vllm.torch_path import rope_tables
+
+    nb, bs, hk, d = 4, 16, 2, 64
+    bf = dict(dtype=torch.bfloat16, device=device)
+    k = torch.randn(5, hk, d, **bf)
+    v = torch.randn(5, hk, d, **bf)
+    good = torch.tensor([3, 17, -1, 40, 63], dtype=torch.int32, device=device)
+    bad = torch.tensor([3, 17, nb * bs, 40, nb * bs + 1000], dtype=torch.int32, device=device)
+    keep = torch.tensor([3, 17, -1, 40, -1], dtype=torch.int32, device=device)
+    pools = []
+    for slots in (bad, keep):
+        pk, pv = torch.zeros(nb, bs, hk, d, **bf), torch.zeros(nb, bs, hk, d, **bf)
+        if fused:
+            q = torch.randn(5, 4, d, **bf)
+            w = torch.ones(d, **bf)
+            cos, sin = rope_tables(d, 64, device=device)
+            extension.qk_norm_rope_kv_write(q, k, v, w, w, torch.arange(5, device=device), cos,
+                                            sin, 1e-6, pk, pv, slots)
+        else:
+            extension.kv_write(pk, pv, k, v, slots)
+        pools.append((pk, pv))
+    torch.cuda.synchronize()
+    assert torch.equal(pools[0][0], pools[1][0]) and torch.equal(pools[0][1], pools[1][1])
+    assert pools[1][1].view(-1, hk, d)[17].equal(v[1]) and good.numel() == 5

@@ -43,7 +43,7 @@ def _paged(lib, **over):
     args = dict(out=1, q=1, key_pool=1, value_pool=1, k_scales=None, v_scales=None,
                 block_tables=1, cu=1, ctx=1, seq=1, num_tokens=4, num_seqs=4, hq=16, hk=8,
                 d=128, p=16, num_blocks=512, max_blocks=63, max_q=1, max_ctx=1000, scale=0.088,
-                q_dtype=0, kv_dtype=0, ws=None, ws_bytes=0, stream=None)
+                q_dtype=0, kv_dtype=0, options=None, ws=None, ws_bytes=0, stream=None)
     args.update(over)
     return lib.mvllm_paged_attention(*args.values())
 
@@ -70,22 +70,45 @@ def test_split_workspace_is_required_when_planned(lib):
     assert "workspace" in lib.mvllm_last_error().decode()
 
 
-def _plan(lib, *args):
+def _plan(lib, *args, options=None):
     plan = extension._Plan()
-    assert lib.mvllm_paged_attention_plan(*args, ctypes.byref(plan)) == 0
+    opts = extension.make_plan_options(options)
+    assert lib.mvllm_paged_attention_plan(*args, None if opts is None else ctypes.byref(opts),
+                                          ctypes.byref(plan)) == 0
     return plan
 
 
-def test_prefill_grid_schedule_needs_no_workspace(lib, monkeypatch):
+def test_prefill_grid_schedule_needs_no_workspace(lib):
     # enough 128-query items to fill the CUs: the grid schedule
     plan = _plan(lib, 4096, 8, 16, 8, 128, 16, 512, 2048, 2, 2)
     assert plan.prefill_mfma == 1 and plan.prefill_workgroups == 0 and plan.workspace_bytes == 0
-    monkeypatch.setenv("MVLLM_PREFILL_SCHEDULE", "2")
-    plan = _plan(lib, 512, 1, 16, 8, 128, 16, 512, 8192, 2, 2)
+    plan = _plan(lib, 512, 1, 16, 8, 128, 16, 512, 8192, 2, 2, options={"prefill_schedule": "grid"})
     assert plan.prefill_workgroups == 0 and plan.workspace_bytes == 0
-    monkeypatch.setenv("MVLLM_PREFILL_SCHEDULE", "1")
-    plan = _plan(lib, 4096, 8, 16, 8, 128, 16, 512, 2048, 2, 2)
+    plan = _plan(lib, 4096, 8, 16, 8, 128, 16, 512, 2048, 2, 2,
+                 options={"prefill_schedule": "stream"})
     assert plan.prefill_workgroups > 0
+
+
+def test_plan_options_are_explicit_and_checked(lib, monkeypatch):
+    """The schedule depends on the sizes and the options only: no environment knob."""
+    monkeypatch.setenv("MVLLM_DECODE_SCHEDULE", "2")
+    monkeypatch.setenv("MVLLM_PREFILL_SCHEDULE", "1")
+    assert _plan(lib, 64, 64, 16, 8, 128, 16, 1, 4096, 2, 2).decode_mode == 1
+    assert _plan(lib, 4096, 8, 16, 8, 128, 16, 512, 2048, 2, 2).prefill_workgroups == 0
+    grid = _plan(lib, 64, 64, 16, 8, 128, 16, 1, 4096, 2, 2,
+                 options={"decode_schedule": "grid", "decode_split_tokens": 1024})
+    assert grid.decode_mode == 2 and grid.split_tokens == 1024
+    bad = extension.make_plan_options({"prefill_staging": 2})
+    plan = extension._Plan()
+    assert lib.mvllm_paged_attention_plan(64, 64, 16, 8, 128, 16, 1, 4096, 2, 2,
+                                          ctypes.byref(bad), ctypes.byref(plan)) == 1
+    assert "plan options" in lib.mvllm_last_error().decode()
+    with pytest.raises(ValueError, match="unknown plan options"):
+        extension.make_plan_options({"decode_sched": 1})
+
+
+def test_the_library_carries_the_id_of_its_sources(lib):
+    assert lib.mvllm_build_id().decode() == extension.source_hash()
 
 
 def test_plan_is_host_only_and_consistent(lib):
@@ -126,10 +149,10 @@ def test_plan_is_host_only_and_consistent(lib):
     ("mvllm_swiglu_interleaved", (16, 16, 4, 40, 2, None), "multiple of 16"),
     ("mvllm_add_rmsnorm", (16, 16, 16, 16, 16, 4, 100, 1e-6, 2, None), "is not served"),
     # a q token stride shorter than the token's heads (16 x 128)
-    ("mvllm_qk_norm_rope_kv_write", (16,) * 9 + (4, 16, 16, 16, 4, 16, 8, 128, 4, 64, 1e-6,
+    ("mvllm_qk_norm_rope_kv_write", (16,) * 9 + (4, 16, 16, 16, 64, 4, 16, 8, 128, 4, 64, 1e-6,
                                      100, 0, 2, None), "token strides"),
     # a k/v token stride that breaks 16-byte alignment (bf16: a multiple of 8 elements)
-    ("mvllm_qk_norm_rope_kv_write", (16,) * 9 + (4, 16, 16, 16, 4, 16, 8, 128, 4, 64, 1e-6,
+    ("mvllm_qk_norm_rope_kv_write", (16,) * 9 + (4, 16, 16, 16, 64, 4, 16, 8, 128, 4, 64, 1e-6,
                                      0, 1028, 2, None), "16-byte aligned"),
 ])
 def test_elementwise_refusals(lib, fn, args, message):

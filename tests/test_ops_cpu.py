@@ -13,14 +13,63 @@ from oracle import elementwise as ew
 from oracle.paged_attention import paged_attention as oracle_paged
 
 
-def test_use_cuda_true_on_cpu_tensors_raises_instead_of_falling_back():
+def test_use_cuda_true_on_cpu_tensors_falls_back_to_the_pytorch_path():
+    """The reference's contract (ops.py:82-89, tests/test_qwen3_cached.py:335-350): the
+    flag means "use kernels where they apply", so CPU tensors take the PyTorch path and
+    give exactly its result; the decline is reported by dispatch_report."""
+    ops.FALLBACKS.clear()
     b = build_batch([20], [1], num_q_heads=4, num_kv_heads=2, head_dim=32)
-    with pytest.raises(RuntimeError, match="use_cuda=True needs device tensors"):
-        ops.paged_attention(*b.args(), use_cuda=True)
-    with pytest.raises(RuntimeError, match="needs device tensors"):
-        ops.rmsnorm(torch.randn(2, 8), torch.ones(8), use_cuda=True)
-    with pytest.raises(RuntimeError, match="needs device tensors"):
-        ops.swiglu(torch.randn(4), torch.randn(4), use_cuda=True)
+    assert torch.equal(ops.paged_attention(*b.args(), use_cuda=True),
+                       ops.paged_attention(*b.args(), use_cuda=False))
+    x, w = torch.randn(2, 8), torch.rand(8) + 0.5
+    assert torch.equal(ops.rmsnorm(x, w, use_cuda=True), ops.rmsnorm(x, w))
+    g, u = torch.randn(4), torch.randn(4)
+    assert torch.equal(ops.swiglu(g, u, use_cuda=True), ops.swiglu(g, u))
+    report = ops.dispatch_report(True)
+    assert "declined calls" in report and "needs device tensors" in report
+    assert ops.FALLBACKS["paged_attention"] and ops.FALLBACKS["rmsnorm"]
+
+
+def test_strict_mode_raises_on_every_decline():
+    b = build_batch([20], [1], num_q_heads=4, num_kv_heads=2, head_dim=32)
+    with ops.strict_kernels():
+        with pytest.raises(RuntimeError, match="use_cuda=True needs device tensors"):
+            ops.paged_attention(*b.args(), use_cuda=True)
+        with pytest.raises(RuntimeError, match="strict kernel mode"):
+            ops.rmsnorm(torch.randn(2, 8), torch.ones(8), use_cuda=True)
+        with pytest.raises(RuntimeError, match="needs device tensors"):
+            ops.swiglu(torch.randn(4), torch.randn(4), use_cuda=True)
+        # use_cuda=False is an explicit choice of the PyTorch path, never a decline
+        ops.rmsnorm(torch.randn(2, 8), torch.ones(8), use_cuda=False)
+    assert not ops.is_strict()
+
+
+def test_paged_gate_reasons_follow_the_reference():
+    """``_kernel_can_page`` (reference ops.py:257-275) plus this library's head dims:
+    each unserved shape names its reason; a served one has none. Checked on
+    meta tensors for the layout rules, device placement aside."""
+    b = build_batch([20], [1], num_q_heads=4, num_kv_heads=2, head_dim=32)
+    can = ops._kernel_can_page
+    assert "device tensors" in can(b.q, b.key_pool, b.value_pool, b.block_tables)
+    assert "T x H_q x D" in can(b.q.unsqueeze(0), b.key_pool, b.value_pool, b.block_tables)
+    assert "float64" in can(b.q.double(), b.key_pool, b.value_pool, b.block_tables)
+    assert "share a dtype" in can(b.q.half(), b.key_pool, b.value_pool, b.block_tables)
+    q96 = torch.randn(1, 4, 96)
+    pool96 = torch.randn(4, 16, 2, 96)
+    assert "head dim 96" in can(q96, pool96, pool96, b.block_tables)
+    assert "contiguous" in can(b.q, b.key_pool.transpose(1, 2), b.value_pool, b.block_tables)
+    assert "int32" in can(b.q, b.key_pool, b.value_pool, b.block_tables.long())
+    assert "int32" in can(b.q, b.key_pool, b.value_pool, b.block_tables,
+                          (b.cu_seqlens_q.long(),))
+
+
+def test_a_head_dim_the_kernels_do_not_serve_runs_the_pytorch_path():
+    """Reference behaviour for D <= 256 outside this build's set: the PyTorch path."""
+    b = build_batch([30, 5], [1, 5], num_q_heads=4, num_kv_heads=2, head_dim=48, seed=5)
+    got = ops.paged_attention(*b.args(), use_cuda=True)
+    want = oracle_paged(b.q, b.key_pool, b.value_pool, b.block_tables, b.cu_seqlens_q,
+                        b.context_lens, b.scale)
+    assert_max_abs(got, want, 1e-5)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -76,7 +125,8 @@ def test_dense_attention_torch_path_decode_and_causal():
     ref = torch.softmax((q.reshape(2, 4, g, 1, 32) @ k.unsqueeze(2).transpose(-1, -2)) / 32**0.5, -1)
     ref = (ref @ v.unsqueeze(2)).reshape(2, 8, 1, 32)
     assert torch.allclose(out, ref, atol=1e-6)
-    with pytest.raises(RuntimeError, match="device tensors"):
+    assert torch.equal(ops.attention(q, k, v, use_cuda=True), out)
+    with ops.strict_kernels(), pytest.raises(RuntimeError, match="device tensors"):
         ops.attention(q, k, v, use_cuda=True)
 
 
@@ -100,7 +150,8 @@ def test_linear_torch_path_is_x_matmul_w_transposed():
     x = torch.randn(5, 64)
     w = torch.randn(7, 64)
     torch.testing.assert_close(ops.linear(x, w), x @ w.t())
-    with pytest.raises(RuntimeError, match="device tensors"):
+    assert torch.equal(ops.linear(x, w, use_cuda=True), x @ w.t())
+    with ops.strict_kernels(), pytest.raises(RuntimeError, match="device tensors"):
         ops.linear(x, w, use_cuda=True)
 
 
@@ -141,7 +192,8 @@ def test_fused_projection_torch_paths():
         ops.linear_swiglu(x, ops.pack_weight(torch_path.interleave_gate_up(gate, up))),
         ops.swiglu(x @ gate.t(), x @ up.t()))
     assert not ops.skinny(x, use_cuda=False)
-    with pytest.raises(RuntimeError, match="device tensors"):
+    assert torch.equal(ops.linear_residual(x, wo, r, use_cuda=True), r + x @ wo.dense.t())
+    with ops.strict_kernels(), pytest.raises(RuntimeError, match="device tensors"):
         ops.linear_residual(x, wo, r, use_cuda=True)
 
 
@@ -167,5 +219,7 @@ def test_add_rmsnorm_torch_path():
     h, n = ops.add_rmsnorm(x, r, w)
     torch.testing.assert_close(h, r + x, rtol=0, atol=0)
     torch.testing.assert_close(n, ops.rmsnorm(r + x, w), rtol=0, atol=0)
-    with pytest.raises(RuntimeError, match="needs device tensors"):
+    h2, n2 = ops.add_rmsnorm(x, r, w, use_cuda=True)
+    assert torch.equal(h2, h) and torch.equal(n2, n)
+    with ops.strict_kernels(), pytest.raises(RuntimeError, match="needs device tensors"):
         ops.add_rmsnorm(x, r, w, use_cuda=True)

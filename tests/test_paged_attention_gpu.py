@@ -30,8 +30,9 @@ def oracle(b):
                         b.context_lens, b.scale, b.k_scale, b.v_scale)
 
 
-def kernel(ext, b):
-    out = ext.paged_attention(*b.args(), k_scale=b.k_scale, v_scale=b.v_scale)
+def kernel(ext, b, options=None):
+    out = ext.paged_attention(*b.args(), k_scale=b.k_scale, v_scale=b.v_scale,
+                              plan_options=options)
     torch.cuda.synchronize()
     return out
 
@@ -44,9 +45,9 @@ def case(contexts, query_lens, device, **kw):
     return build_batch(contexts, query_lens, device=device, **kw)
 
 
-def check(ext, b, dtype=None, msg=""):
+def check(ext, b, dtype=None, msg="", options=None):
     dtype = dtype or b.key_pool.dtype
-    got = kernel(ext, b)
+    got = kernel(ext, b, options)
     assert got.dtype == b.q.dtype
     assert_max_abs(got, oracle(b), ATTN_ATOL[dtype], msg)
     return got
@@ -70,24 +71,23 @@ def test_decode_over_a_long_context_uses_the_split_path(extension, device):
 
 @pytest.mark.parametrize("schedule", ["stream", "grid"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_both_decode_schedules_agree_with_the_oracle(extension, device, monkeypatch, schedule, dtype):
+def test_both_decode_schedules_agree_with_the_oracle(extension, device, schedule, dtype):
     """The stream schedule (default) and the split grid (forced) on a ragged batch,
     including sequences shorter than one workgroup's share and longer than many."""
-    if schedule == "grid":
-        monkeypatch.setenv("MVLLM_DECODE_SCHEDULE", "2")
+    options = {"decode_schedule": "grid"} if schedule == "grid" else None
     b = case([8192, 33, 4096, 17, 1, 700, 2], [1] * 7, device, dtype=dtype)
-    plan = extension.paged_attention_plan(7, 7, HQ, HK, D, 16, 1, 8192, dtype, dtype)
+    plan = extension.paged_attention_plan(7, 7, HQ, HK, D, 16, 1, 8192, dtype, dtype,
+                                          plan_options=options)
     assert plan["decode_mode"] == schedule
-    check(extension, b)
+    check(extension, b, options=options)
 
 
 @pytest.mark.parametrize("wgs_per_cu", ["1", "4"])
-def test_stream_schedule_with_more_workgroups_than_keys(extension, device, monkeypatch, wgs_per_cu):
+def test_stream_schedule_with_more_workgroups_than_keys(extension, device, wgs_per_cu):
     """Tiny batches leave most stream workgroups with empty shares; the merge must skip
     their slots."""
-    monkeypatch.setenv("MVLLM_DECODE_WGS_PER_CU", wgs_per_cu)
     b = case([3, 5, 2], [1, 1, 1], device, dtype=torch.bfloat16, block_size=1)
-    check(extension, b)
+    check(extension, b, options={"decode_wgs_per_cu": wgs_per_cu})
 
 
 def test_a_ragged_decode_batch_with_empty_splits(extension, device):
@@ -97,10 +97,9 @@ def test_a_ragged_decode_batch_with_empty_splits(extension, device):
 
 
 @pytest.mark.parametrize("split_tokens", ["64", "1024"])
-def test_forced_split_sizes_agree(extension, device, monkeypatch, split_tokens):
-    monkeypatch.setenv("MVLLM_DECODE_SCHEDULE", "2")
-    monkeypatch.setenv("MVLLM_DECODE_SPLIT_TOKENS", split_tokens)
-    check(extension, case([3000, 129, 64, 1], [1, 1, 1, 1], device, dtype=torch.bfloat16))
+def test_forced_split_sizes_agree(extension, device, split_tokens):
+    check(extension, case([3000, 129, 64, 1], [1, 1, 1, 1], device, dtype=torch.bfloat16),
+          options={"decode_schedule": "grid", "decode_split_tokens": split_tokens})
 
 
 @pytest.mark.parametrize("kv_heads", [1, 2, 8])
@@ -146,56 +145,51 @@ def test_mfma_prefill_shapes(extension, device, head_dim, heads, kv_heads):
     check(extension, b)
 
 
-def _prefill_schedule(monkeypatch, schedule):
-    monkeypatch.setenv("MVLLM_PREFILL_SCHEDULE", "1" if schedule == "stream" else "2")
+def _prefill_schedule(schedule):
+    return {"prefill_schedule": schedule}
 
 
 @pytest.mark.parametrize("schedule", ["stream", "grid"])
 @pytest.mark.parametrize("heads,kv_heads", [(16, 8), (6, 2), (3, 3)])
-def test_prefill_schedules_on_a_ragged_batch(extension, device, monkeypatch, schedule, heads,
-                                             kv_heads):
+def test_prefill_schedules_on_a_ragged_batch(extension, device, schedule, heads, kv_heads):
     """Balanced stream shares cut long items between workgroups (merged afterwards);
     the grid runs every item whole. Prefixes from 0 to several thousand keys; GQA
     pairs (two heads per work item, a wave each) and odd groups (one head)."""
-    _prefill_schedule(monkeypatch, schedule)
+    options = _prefill_schedule(schedule)
     b = case([4000, 520, 17, 1300, 64], [512, 520, 9, 300, 2], device, dtype=torch.bfloat16,
              num_q_heads=heads, num_kv_heads=kv_heads, head_dim=128)
     plan = extension.paged_attention_plan(b.q.shape[0], 5, heads, kv_heads, 128, 16, 520, 4000,
-                                          torch.bfloat16, torch.bfloat16)
+                                          torch.bfloat16, torch.bfloat16, plan_options=options)
     assert plan["prefill_mfma"] == 1
     assert (plan["prefill_workgroups"] > 0) == (schedule == "stream")
-    check(extension, b)
+    check(extension, b, options=options)
 
 
 @pytest.mark.parametrize("wgs_per_cu", ["1", "3"])
-def test_prefill_stream_with_more_workgroups_than_tiles(extension, device, monkeypatch, wgs_per_cu):
+def test_prefill_stream_with_more_workgroups_than_tiles(extension, device, wgs_per_cu):
     """A two-tile prefill over hundreds of workgroups: most shares are empty, and each
     tile of an item may sit in a different workgroup."""
-    monkeypatch.setenv("MVLLM_PREFILL_WGS_PER_CU", wgs_per_cu)
-    monkeypatch.setenv("MVLLM_PREFILL_SCHEDULE", "1")
     b = case([70, 3], [70, 3], device, dtype=torch.bfloat16, num_q_heads=4, num_kv_heads=2,
              head_dim=64)
-    check(extension, b)
+    check(extension, b, options={"prefill_wgs_per_cu": wgs_per_cu, "prefill_schedule": "stream"})
 
 
 @pytest.mark.parametrize("schedule", ["stream", "grid"])
-def test_prefill_schedules_in_a_mixed_fp8_batch(extension, device, monkeypatch, schedule):
-    _prefill_schedule(monkeypatch, schedule)
+def test_prefill_schedules_in_a_mixed_fp8_batch(extension, device, schedule):
     b = case([900, 2500, 40, 700], [1, 400, 40, 1], device, dtype=torch.bfloat16,
              kv_dtype=torch.float8_e4m3fn, num_q_heads=16, num_kv_heads=8, head_dim=128)
-    check(extension, b, dtype=torch.float8_e4m3fn)
+    check(extension, b, dtype=torch.float8_e4m3fn, options=_prefill_schedule(schedule))
 
 
 @pytest.mark.parametrize("schedule", ["stream", "grid"])
 @pytest.mark.parametrize("scale", [-0.3, 0.0, 2.0])
-def test_prefill_with_unusual_scales(extension, device, monkeypatch, scale, schedule):
+def test_prefill_with_unusual_scales(extension, device, scale, schedule):
     """The softmax runs on raw scores with |scale| folded into the exponent and the sign
     of a negative scale moved into Q; zero gives uniform weights."""
-    _prefill_schedule(monkeypatch, schedule)
     b = case([300, 90], [150, 90], device, dtype=torch.bfloat16, num_q_heads=16,
              num_kv_heads=8, head_dim=128)
     b.scale = scale
-    check(extension, b)
+    check(extension, b, options=_prefill_schedule(schedule))
 
 
 def test_prefill_schedule_choice(extension):
@@ -337,17 +331,20 @@ def test_config3_chunked_prefill_full_size(extension, device):
 
 
 @pytest.mark.slow
-def test_config4_fp8_decode_subset_of_full_size(extension, device):
-    """Full config-4 batch on the GPU; every 8th sequence checked on the CPU oracle
-    (sequences are independent, so a subset of rows is a complete check of those rows)."""
+def test_config4_fp8_decode_full_size(extension, device):
+    """The full config-4 batch (128 sequences of 2048-8192 fp8 keys) on the GPU, every
+    row checked against the CPU oracle, 32 sequences per oracle call (sequences are
+    independent, so the groups together are the whole check)."""
     b = config_batch(4, device=device)
-    got = kernel(extension, b)
-    picks = list(range(0, 128, 8))
-    rows = torch.tensor([int(b.cu_seqlens_q[s]) for s in picks])
-    sub = oracle_paged(b.q[rows], b.key_pool, b.value_pool, b.block_tables[picks],
-                       torch.arange(len(picks) + 1, dtype=torch.int32), b.context_lens[picks],
-                       b.scale, b.k_scale, b.v_scale)
-    assert_max_abs(got[rows.to(device)], sub, ATTN_ATOL[torch.float8_e4m3fn], "config 4")
+    got = kernel(extension, b).cpu()
+    pools = (b.key_pool.cpu(), b.value_pool.cpu(), b.k_scale.cpu(), b.v_scale.cpu())
+    for lo in range(0, 128, 32):
+        picks = list(range(lo, lo + 32))
+        rows = torch.tensor([int(b.cu_seqlens_q[s]) for s in picks])
+        sub = oracle_paged(b.q[rows].cpu(), pools[0], pools[1], b.block_tables[picks].cpu(),
+                           torch.arange(len(picks) + 1, dtype=torch.int32),
+                           b.context_lens[picks].cpu(), b.scale, pools[2], pools[3])
+        assert_max_abs(got[rows], sub, ATTN_ATOL[torch.float8_e4m3fn], f"config 4 rows {lo}+")
 
 
 def test_repeated_calls_are_deterministic(extension, device):
@@ -413,11 +410,35 @@ def test_the_op_routes_to_the_kernel(extension, device, monkeypatch):
     assert_max_abs(got, oracle(b), ATTN_ATOL[torch.float32])
 
 
-def test_use_cuda_never_falls_back(extension, device):
+def test_strict_mode_refuses_what_the_kernel_cannot_serve(extension, device):
     b = case([64], [1], device)
     with pytest.raises(RuntimeError, match="contiguous"):
         ops.paged_attention(b.q, b.key_pool[::2], b.value_pool[::2], *b.args()[3:],
                             use_cuda=True)
+
+
+def test_declined_calls_fall_back_to_the_pytorch_path_on_device(extension, device):
+    """Outside strict mode a call the kernel cannot serve (a strided pool, a head dim
+    outside 32/64/128/256) runs the PyTorch path on the device, as the reference's
+    ``_kernel_can_page`` routes it (ops.py:257-275), and is reported."""
+    ops.FALLBACKS.clear()
+    with ops.strict_kernels(False):
+        b = case([64, 9], [1, 9], device)
+
+        def strided(pool):  # the same pool as a non-contiguous view
+            wide = torch.zeros(*pool.shape[:-1], 2 * pool.shape[-1], dtype=pool.dtype,
+                               device=pool.device)
+            wide[..., :pool.shape[-1]] = pool
+            return wide[..., :pool.shape[-1]]
+
+        kp, vp = strided(b.key_pool), strided(b.value_pool)
+        got = ops.paged_attention(b.q, kp, vp, *b.args()[3:], use_cuda=True)
+        want = ops.paged_attention(b.q, kp, vp, *b.args()[3:], use_cuda=False)
+        assert torch.equal(got, want)
+        assert_max_abs(got, oracle(b), ATTN_ATOL[torch.float32])
+        b48 = case([40, 7], [1, 7], device, head_dim=48)
+        assert_max_abs(ops.paged_attention(*b48.args(), use_cuda=True), oracle(b48), 1e-5)
+    assert "contiguous" in ops.dispatch_report(True) and "head dim 48" in ops.dispatch_report(True)
 
 
 def test_the_torch_path_runs_on_device_without_cuda_requested(extension, device):
