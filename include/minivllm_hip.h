@@ -128,6 +128,29 @@ int mvllm_paged_attention(void* out, const void* q, const void* key_pool,
                           int32_t kv_dtype, const mvllm_plan_options* options, void* workspace,
                           uint64_t workspace_bytes, void* stream);
 
+/* mvllm_paged_attention for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc); no
+ * counterpart in the reference. The same arguments without the workspace: the split
+ * partials go to a static device array of MVLLM_NOALLOC_SCRATCH_BYTES that the library
+ * holds on each GPU it runs on (the current device's) until the process ends, and the
+ * call allocates nothing. A call whose plan needs more scratch than that returns
+ * MVLLM_ERR_UNSUPPORTED (a prefill on the stream schedule needs up to ~66 MB at
+ * H_q 16, D 128: plan options prefill_schedule = 2 put it on the grid, which needs
+ * none). Nothing in the scratch needs to start at zero. Every call on one GPU shares
+ * its array: calls that overlap in time on one GPU (two streams, two threads) race. */
+#define MVLLM_NOALLOC_SCRATCH_BYTES (16u << 20)
+int mvllm_paged_attention_noalloc(void* out, const void* q, const void* key_pool,
+                                  const void* value_pool, const float* k_scales,
+                                  const float* v_scales, const int32_t* block_tables,
+                                  const int32_t* cu_seqlens_q, const int32_t* context_lens,
+                                  const int32_t* seq_lens, int32_t num_tokens, int32_t num_seqs,
+                                  int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                  int32_t block_size, int64_t num_blocks,
+                                  int32_t max_blocks_per_seq, int32_t max_query_len,
+                                  int32_t max_context_len, float scale, int32_t q_dtype,
+                                  int32_t kv_dtype, const mvllm_plan_options* options,
+                                  void* stream);
+
 /* Dense-cache attention: q, out [batch, query_len, num_q_heads, head_dim] contiguous
  * (token-major); k, v [batch, num_kv_heads, kv_len, head_dim] read through the given
  * element strides (head_dim contiguous), so a cache narrowed out of a larger buffer is

@@ -11,6 +11,7 @@
 
 #include <atomic>
 #include <cstdarg>
+#include <mutex>
 
 #include "../../include/minivllm_hip.h"
 #include "common.hpp"
@@ -473,7 +474,14 @@ int mvllm_paged_attention_plan(int32_t num_tokens, int32_t num_seqs, int32_t num
   return MVLLM_OK;
 }
 
-int mvllm_paged_attention(void* out, const void* q, const void* key_pool,
+}  // extern "C"
+
+namespace {
+
+// The paged entry behind mvllm_paged_attention and mvllm_paged_attention_noalloc: the
+// scratch pointer is the caller's workspace for the first and this library's static
+// device array for the second (`name` prefixes the errors).
+int paged_attention_entry(const char* name, void* out, const void* q, const void* key_pool,
                           const void* value_pool, const float* k_scales, const float* v_scales,
                           const int32_t* block_tables, const int32_t* cu_seqlens_q,
                           const int32_t* context_lens, const int32_t* seq_lens,
@@ -482,8 +490,7 @@ int mvllm_paged_attention(void* out, const void* q, const void* key_pool,
                           int64_t num_blocks, int32_t max_blocks_per_seq, int32_t max_query_len,
                           int32_t max_context_len, float scale, int32_t q_dtype,
                           int32_t kv_dtype, const mvllm_plan_options* options, void* workspace,
-                          uint64_t workspace_bytes, void* stream) {
-  g_error[0] = '\0';
+                          uint64_t workspace_bytes, void* stream, bool static_scratch) {
   int rc = check_paged_shape(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim,
                              block_size, max_query_len, max_context_len, q_dtype, kv_dtype);
   if (rc != MVLLM_OK) return rc;
@@ -508,6 +515,14 @@ int mvllm_paged_attention(void* out, const void* q, const void* key_pool,
   const Plan plan = make_plan(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim,
                               block_size, max_query_len, max_context_len, q_dtype, kv_dtype, o);
   const uint64_t need = plan.pub.workspace_bytes;
+  if (static_scratch && need > workspace_bytes) {
+    return fail(MVLLM_ERR_UNSUPPORTED,
+                "%s: this call needs %llu bytes of scratch, more than the library's static "
+                "%llu (a prefill on the stream schedule is the usual cause: plan options "
+                "prefill_schedule = 2 run it on the grid, which needs none)",
+                name, static_cast<unsigned long long>(need),
+                static_cast<unsigned long long>(workspace_bytes));
+  }
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     return fail(MVLLM_ERR_WORKSPACE,
                 "paged_attention: workspace of %llu bytes is smaller than the %llu the plan "
@@ -546,7 +561,89 @@ int mvllm_paged_attention(void* out, const void* q, const void* key_pool,
   p.kv_row_bytes = p.kv_head_bytes * num_kv_heads;
   p.scale = scale;
   return launch_planned(plan, p, workspace, q_dtype, kv_dtype, head_dim, max_query_len,
-                        static_cast<hipStream_t>(stream), "paged_attention");
+                        static_cast<hipStream_t>(stream), name);
+}
+
+// The allocation-free entry's scratch: one array per device, held from the library's
+// load until the process ends. Host code never names it directly (its host-side name
+// is a stand-in, not a device address); each device's address comes from
+// hipGetSymbolAddress once, with that device current, and is kept here.
+constexpr uint64_t kNoallocScratchBytes = MVLLM_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address (resolved on the device's first call).
+int scratch_for_current_device(void** ptr) {
+  int dev = 0;
+  int rc = hip_status(hipGetDevice(&dev), "paged_attention_noalloc: hipGetDevice");
+  if (rc != MVLLM_OK) return rc;
+  if (dev < 0 || dev >= kMaxDevices) {
+    return fail(MVLLM_ERR_UNSUPPORTED, "paged_attention_noalloc: device %d out of range", dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    rc = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+                    "paged_attention_noalloc: hipGetSymbolAddress");
+    if (rc != MVLLM_OK) return rc;
+    if (p == nullptr || reinterpret_cast<uintptr_t>(p) % 256 != 0) {
+      return fail(MVLLM_ERR_HIP, "paged_attention_noalloc: bad scratch address");
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return MVLLM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mvllm_paged_attention(void* out, const void* q, const void* key_pool,
+                          const void* value_pool, const float* k_scales, const float* v_scales,
+                          const int32_t* block_tables, const int32_t* cu_seqlens_q,
+                          const int32_t* context_lens, const int32_t* seq_lens,
+                          int32_t num_tokens, int32_t num_seqs, int32_t num_q_heads,
+                          int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                          int64_t num_blocks, int32_t max_blocks_per_seq, int32_t max_query_len,
+                          int32_t max_context_len, float scale, int32_t q_dtype,
+                          int32_t kv_dtype, const mvllm_plan_options* options, void* workspace,
+                          uint64_t workspace_bytes, void* stream) {
+  g_error[0] = '\0';
+  return paged_attention_entry("paged_attention", out, q, key_pool, value_pool, k_scales,
+                               v_scales, block_tables, cu_seqlens_q, context_lens, seq_lens,
+                               num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                               block_size, num_blocks, max_blocks_per_seq, max_query_len,
+                               max_context_len, scale, q_dtype, kv_dtype, options, workspace,
+                               workspace_bytes, stream, false);
+}
+
+int mvllm_paged_attention_noalloc(void* out, const void* q, const void* key_pool,
+                                  const void* value_pool, const float* k_scales,
+                                  const float* v_scales, const int32_t* block_tables,
+                                  const int32_t* cu_seqlens_q, const int32_t* context_lens,
+                                  const int32_t* seq_lens, int32_t num_tokens, int32_t num_seqs,
+                                  int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                  int32_t block_size, int64_t num_blocks,
+                                  int32_t max_blocks_per_seq, int32_t max_query_len,
+                                  int32_t max_context_len, float scale, int32_t q_dtype,
+                                  int32_t kv_dtype, const mvllm_plan_options* options,
+                                  void* stream) {
+  g_error[0] = '\0';
+  void* ws = nullptr;
+  if (num_tokens > 0 && num_seqs > 0) {
+    const int rc = scratch_for_current_device(&ws);
+    if (rc != MVLLM_OK) return rc;
+  }
+  return paged_attention_entry("paged_attention_noalloc", out, q, key_pool, value_pool,
+                               k_scales, v_scales, block_tables, cu_seqlens_q, context_lens,
+                               seq_lens, num_tokens, num_seqs, num_q_heads, num_kv_heads,
+                               head_dim, block_size, num_blocks, max_blocks_per_seq,
+                               max_query_len, max_context_len, scale, q_dtype, kv_dtype,
+                               options, ws, kNoallocScratchBytes, stream, true);
 }
 
 int mvllm_dense_attention_plan(const mvllm_dense_args* args, uint64_t* workspace_bytes) {

@@ -244,6 +244,10 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_paged_attention.argtypes = (
         [p] * 10 + [i32] * 6 + [i64, i32, i32, i32, f32, i32, i32, opts, p, u64, p]
     )
+    lib.mvllm_paged_attention_noalloc.restype = ctypes.c_int
+    lib.mvllm_paged_attention_noalloc.argtypes = (
+        [p] * 10 + [i32] * 6 + [i64, i32, i32, i32, f32, i32, i32, opts, p]
+    )
     lib.mvllm_rmsnorm.restype = ctypes.c_int
     lib.mvllm_rmsnorm.argtypes = [p, p, p, i64, i64, f32, i32, p]
     lib.mvllm_add_rmsnorm.restype = ctypes.c_int
@@ -289,6 +293,7 @@ EXPORTED_SYMBOLS = (
     "mvllm_build_id",
     "mvllm_paged_attention_plan",
     "mvllm_paged_attention",
+    "mvllm_paged_attention_noalloc",
     "mvllm_rmsnorm",
     "mvllm_rope",
     "mvllm_swiglu",
