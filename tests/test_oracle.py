@@ -11,6 +11,7 @@ head mapping, wrong slot arithmetic) fails at least one of them.
 from __future__ import annotations
 
 import math
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -331,3 +332,33 @@ def test_dense_oracle_known_answers():
     for i in range(L):
         want = v[0, 0, : S - L + i + 1].double().mean(0)
         torch.testing.assert_close(out[0, 1, i], want, rtol=0, atol=1e-12)
+
+
+def test_dense_model_oracle_matches_transformers_qwen3():
+    """oracle/qwen3_dense.py (and its KV-cached loop) against Hugging Face's Qwen3 in
+    float64 on the tiny shape with non-unit norm weights (fixture made by
+    tests/golden/make_qwen3_golden.py, transformers 5.15.0): the same greedy tokens and
+    next-token logits to 1e-6 at every step (Hugging Face computes the RoPE frequencies
+    and the RMSNorm statistics in float32 even in a float64 model: ~1e-7 here, against
+    O(0.1) for any wiring mistake). This pins the layer wiring (norm order,
+    QK-norm per head, rotate-half RoPE at theta 1e6, GQA, SwiGLU, tied embedding)
+    independently of this repository's engine."""
+    import sys
+
+    from oracle.qwen3_dense import DenseQwen3, generate_greedy
+
+    sys.path.insert(0, str(Path(__file__).resolve().parent / "golden"))
+    from make_qwen3_golden import golden_weights, weights_digest
+
+    fx = np.load(Path(__file__).resolve().parent / "golden" / "qwen3_tiny_hf.npz")
+    config, weights = golden_weights()
+    assert weights_digest(weights) == str(fx["weights_sha256"]), "the weight generator changed"
+    dense = DenseQwen3(config, weights)
+    for i in range(int(fx["num_prompts"])):
+        prompt = fx[f"prompt_{i}"].tolist()
+        want_tokens, want_logits = fx[f"tokens_{i}"].tolist(), fx[f"step_logits_{i}"]
+        for tokens, logits in (generate_greedy(config, weights, prompt, len(want_tokens)),
+                               dense.generate(prompt, len(want_tokens))):
+            assert tokens == want_tokens, f"prompt {i}"
+            got = np.stack([l.numpy() for l in logits])
+            assert np.abs(got - want_logits).max() < 1e-6, f"prompt {i}"
