@@ -361,35 +361,125 @@ def copy_ceiling(nbytes: int, steps: int = 20) -> float:
     return 2 * n * 2 / (ms * 1e-3) / 1e9
 
 
-def cpu_baseline(seconds_budget: float = 15.0) -> dict:
-    """The CPU oracle on the first sequences of config 2 (bf16 inputs, fp32 math)."""
-    from mini_vllm.workloads import config_batch
-    from oracle.paged_attention import paged_attention as oracle_paged
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _sub_batch(b, seqs: list[int]):
+    """The rows of sequences ``seqs`` of a PagedBatch (same pools), for a bounded CPU
+    sample: sequences are independent, so a subset is the same work per sequence."""
+    from mini_vllm.workloads import PagedBatch
+
+    cu = [int(v) for v in b.cu_seqlens_q]
+    rows = torch.cat([torch.arange(cu[s], cu[s + 1]) for s in seqs])
+    lens = [cu[s + 1] - cu[s] for s in seqs]
+    new_cu = torch.tensor([0] + lens, dtype=torch.int32).cumsum(0, dtype=torch.int32)
+    return PagedBatch(b.q[rows], b.key_pool, b.value_pool, b.block_tables[seqs].contiguous(), new_cu,
+                      b.context_lens[seqs], b.seq_lens[seqs], max(lens),
+                      max(b.contexts[s] for s in seqs), b.scale, b.k_scale, b.v_scale,
+                      [b.contexts[s] for s in seqs], lens)
+
+
+def _median_time(fn, runs: int = 5) -> tuple[float, int]:
+    fn()  # warmup
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline() -> dict:
+    """The reference's CPU path (its gather-then-dense PyTorch attention,
+    ``ops.paged_attention(use_cuda=False)``, mini_vllm/paged_attention.py:36-110) on the
+    host cores, for BASELINE configs 1-4 in their own dtype and in fp32 (median of 5 runs
+    after a warmup, on the same seeded inputs; configs 2 and 4 on a stated sample of
+    their sequences), and a stated subset of config 5 through the engine with the
+    kernels off. The headline entry is config 2 in bf16; ``configs`` holds the rest."""
+    from mini_vllm.kernels import ops
+    from mini_vllm.workloads import config_batch, prefill_flops
 
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
-    full = config_batch(2, device="cpu")
-    n = 8
-    rows = torch.arange(n)
-    args = (full.q[rows], full.key_pool, full.value_pool, full.block_tables[:n],
-            torch.arange(n + 1, dtype=torch.int32), full.context_lens[:n], full.scale)
-    kv = 2 * sum(full.contexts[:n]) * 8 * 128 * 2
-    oracle_paged(*args)  # warmup
-    times = []
-    start = time.perf_counter()
-    while len(times) < 5 or (time.perf_counter() - start < seconds_budget and len(times) < 50):
-        t0 = time.perf_counter()
-        oracle_paged(*args)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+    configs = {}
+
+    def attention_leg(name, b, work, unit, sample):
+        for leg in ("native", "fp32") if b.q.dtype != torch.float32 else ("native",):
+            q = b.q if leg == "native" else b.q.float()
+            fp8 = b.key_pool.dtype == torch.float8_e4m3fn
+            kp = b.key_pool if leg == "native" or fp8 else b.key_pool.float()
+            vp = b.value_pool if leg == "native" or fp8 else b.value_pool.float()
+            args = (q, kp, vp, b.block_tables, b.cu_seqlens_q, b.context_lens, b.seq_lens,
+                    b.max_query_len, b.max_context_len, b.scale)
+            med, runs = _median_time(lambda: ops.paged_attention(
+                *args, use_cuda=False, k_scale=b.k_scale, v_scale=b.v_scale))
+            dtype = str(q.dtype).replace("torch.", "")
+            configs[f"{name}_{dtype}"] = {
+                "value": round(work / med / (1e9 if unit == "GB/s" else 1e12), 4), "unit": unit,
+                "ms": round(med * 1e3, 2), "runs": runs, "sample": sample}
+            log(f"cpu {name} {dtype}: {med * 1e3:.1f} ms, {configs[f'{name}_{dtype}']['value']} {unit}")
+
+    b1 = config_batch(1)
+    attention_leg("config1", b1, b1.kv_bytes(), "GB/s", "all 4 sequences (fp32 inputs)")
+    b2 = config_batch(2)
+    s2 = _sub_batch(b2, list(range(8)))
+    attention_leg("config2", s2, s2.kv_bytes(), "GB/s",
+                  f"sequences 0-7 of 64 (ctx {s2.contexts})")
+    b3 = config_batch(3)
+    attention_leg("config3", b3, prefill_flops(b3), "TFLOP/s", "all 8 sequences x 512 queries")
+    b4 = config_batch(4)
+    s4 = _sub_batch(b4, list(range(4)))
+    attention_leg("config4", s4, s4.kv_bytes() + s4.scale_bytes(), "GB/s",
+                  f"sequences 0-3 of 128 (ctx {s4.contexts}), fp8 pool dequantised")
+    del b2, b3, b4
+    configs["config5_subset"] = _cpu_engine_subset()
+
+    head = configs["config2_bfloat16"]
     return {
-        "value": round(kv / med / 1e9, 3),
+        "value": head["value"],
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"config 2 sequences 0-{n - 1} (ctx {full.contexts[:n]}), oracle/paged_attention.py "
-                  f"gather-then-dense in fp32, median of {len(times)} runs, {med * 1e3:.1f} ms",
+        "sample": f"config 2 in bf16: {head['sample']}; ops.paged_attention(use_cuda=False), the "
+                  f"reference's gather-then-dense path; median of {head['runs']} runs, {head['ms']} ms",
+        "cpu_model": _cpu_model(),
+        "configs": configs,
     }
+
+
+def _cpu_engine_subset(requests: int = 8, prompt_tokens: int = 128, max_tokens: int = 32) -> dict:
+    """Config 5 on the host cores, kernels off: the first ``requests`` config-5 prompts
+    trimmed to ``prompt_tokens`` tokens, ``max_tokens`` greedy tokens each, through the
+    same engine (bf16 Qwen3-0.6B shape, random init seed 0, 2048-token budget, 512-token
+    chunks). A subset: the whole workload would take hours on a CPU."""
+    from mini_vllm.block import BlockManager
+    from mini_vllm.model import ModelConfig, Qwen3Paged, random_weights
+    from mini_vllm.serve import LLMEngine, SchedulerConfig
+    from mini_vllm.workloads import CONFIG5_BUDGET, CONFIG5_CHUNK, config5_prompts
+
+    config = ModelConfig()
+    weights = random_weights(config, seed=0)
+    prompts = [p[:prompt_tokens] for p in config5_prompts(requests, config.vocab_size)]
+    blocks = requests * -(-(prompt_tokens + max_tokens) // 16) + 1
+    manager = BlockManager(blocks, 16, config.num_hidden_layers, config.num_key_value_heads,
+                           config.head_dim, config.dtype, "cpu")
+    engine = LLMEngine(Qwen3Paged(config, weights, manager, use_cuda=False),
+                       SchedulerConfig(max_batched_tokens=CONFIG5_BUDGET, chunk_size=CONFIG5_CHUNK))
+    engine.generate(prompts, max_tokens)
+    st = engine.stats
+    log(f"cpu config 5 subset: {st.output_tokens_per_s:.1f} output tok/s")
+    return {"value": round(st.output_tokens_per_s, 2), "unit": "output tok/s",
+            "decode_tok_s": round(st.decode_tokens_per_s, 2), "elapsed_s": round(st.elapsed_s, 2),
+            "sample": f"{requests} requests: config-5 prompts 0-{requests - 1} trimmed to "
+                      f"{prompt_tokens} tokens, {max_tokens} greedy tokens each, bf16, "
+                      "use_cuda=False (one run)"}
 
 
 def main() -> int:

@@ -145,9 +145,7 @@ def paged_attention_gathered(q: torch.Tensor, key_pool: torch.Tensor, value_pool
             "expected matching pools shaped num_blocks x P x H_k x D, got "
             f"{tuple(key_pool.shape)} and {tuple(value_pool.shape)}"
         )
-    if key_pool.dtype == torch.float8_e4m3fn:
-        key_pool = dequantize_fp8_pool(key_pool, k_scale, q.dtype)
-        value_pool = dequantize_fp8_pool(value_pool, v_scale, q.dtype)
+    fp8 = key_pool.dtype == torch.float8_e4m3fn
     num_seqs = context_lens.shape[0]
     if block_tables.shape[0] != num_seqs or cu_seqlens_q.shape[0] != num_seqs + 1:
         raise ValueError("metadata disagrees on the sequence count")
@@ -173,8 +171,13 @@ def paged_attention_gathered(q: torch.Tensor, key_pool: torch.Tensor, value_pool
                 f"sequence {s} needs {used} blocks for {S} tokens but its table is padded there"
             )
         ids = table.to(dtype=torch.int64, device=key_pool.device)
-        k = key_pool.index_select(0, ids).reshape(-1, num_kv_heads, head_dim)[:S]
-        v = value_pool.index_select(0, ids).reshape(-1, num_kv_heads, head_dim)[:S]
+        k = key_pool.index_select(0, ids)
+        v = value_pool.index_select(0, ids)
+        if fp8:  # dequantised after the gather: only this sequence's pages
+            k = dequantize_fp8_pool(k, k_scale.index_select(0, ids), q.dtype)
+            v = dequantize_fp8_pool(v, v_scale.index_select(0, ids), q.dtype)
+        k = k.reshape(-1, num_kv_heads, head_dim)[:S]
+        v = v.reshape(-1, num_kv_heads, head_dim)[:S]
         k = k.permute(1, 0, 2).unsqueeze(1)                       # H_k x 1 x S x D
         v = v.permute(1, 0, 2).unsqueeze(1)
         qs = q[start:end].permute(1, 0, 2).reshape(num_kv_heads, group, L, head_dim)
