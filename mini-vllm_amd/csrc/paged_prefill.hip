@@ -1049,6 +1049,400 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_lds_kernel(const Paged
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// The grid schedule's kernel for 16-bit pools at D = 128, a GQA pair per work item and
+// pages of >= 16 keys, software pipelined: the scores of tile t + 1 are computed
+// (S^T = K Q^T) while the softmax of tile t runs, so one wave keeps its MFMAs and its
+// vector work in flight together instead of alternating between them (with the two
+// waves of a SIMD meeting at every tile's barrier, both used to reach their softmax at
+// the same time and leave the matrix core idle). Per tile t, in order:
+//   wait for this wave's copies of tile t + 1; barrier (tile t + 1's K and raw V rows,
+//   and every wave's V^T rows of tile t, are then visible, and every wave is done with
+//   tile t - 1); transpose this wave's V rows of tile t + 1 into V^T buffer (t + 1) & 1;
+//   stage tile t + 3 into the slots tile t used (K read by S(t) one step earlier);
+//   S(t + 1) = K(t + 1) Q^T  ||  softmax of S(t) -> P(t); O^T += V^T(t) P^T(t).
+// Staging maps and the softmax are those of paged_prefill_lds_kernel, except that K
+// rows are swizzled over 16 chunks (key & 15) instead of 8; K/V slots rotate by three and the score accumulators by two, so the loop is unrolled by
+// six with every buffer named at compile time.
+template <typename TQ>
+__global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedParams p) {
+  constexpr int D = 128;
+  constexpr int kWaves = 8;
+  constexpr int HW = 2;                   // query heads per work item, one per wave set
+  constexpr int KW = kTileKeys / kWaves;  // keys of a tile staged by one wave
+  constexpr int kCopies = KW / 4;         // 1 KB direct loads per wave per tile (K and V each)
+  constexpr int KV = KW / 4;              // V keys per lane in the transpose
+  constexpr int kKSteps = D / 16;
+  constexpr int kDBlocks = D / 32;
+  constexpr int kRow = D * 2;
+  constexpr int kTileBytes = kTileKeys * kRow;
+  constexpr int kVRow = kTileKeys * 2;
+  constexpr int kStageOps = 2 * kCopies;  // vector-memory ops of one tile's stage per lane
+  static_assert(KV == 2 && kTileKeys == 64 && 32 * 4 == kPrefillQueryTile, "tile sizes");
+
+  __shared__ __align__(16) char k_lds0[kTileBytes];
+  __shared__ __align__(16) char k_lds1[kTileBytes];
+  __shared__ __align__(16) char k_lds2[kTileBytes];
+  __shared__ __align__(16) char r_lds0[kTileBytes];
+  __shared__ __align__(16) char r_lds1[kTileBytes];
+  __shared__ __align__(16) char r_lds2[kTileBytes];
+  __shared__ __align__(1024) char v_lds0[kTileBytes];  // V^T of even tiles
+  __shared__ __align__(1024) char v_lds1[kTileBytes];  // V^T of odd tiles
+  auto k_arr = [&](auto slot) __attribute__((always_inline)) -> char* {
+    constexpr int X = decltype(slot)::value;
+    if constexpr (X == 0) return k_lds0; else if constexpr (X == 1) return k_lds1; else return k_lds2;
+  };
+  auto r_arr = [&](auto slot) __attribute__((always_inline)) -> char* {
+    constexpr int X = decltype(slot)::value;
+    if constexpr (X == 0) return r_lds0; else if constexpr (X == 1) return r_lds1; else return r_lds2;
+  };
+  auto v_arr = [&](auto par) __attribute__((always_inline)) -> char* {
+    if constexpr (decltype(par)::value == 0) return v_lds0; else return v_lds1;
+  };
+
+  const int tid = threadIdx.x;
+  const int wave = uniform(tid / kWave);
+  const int lane = tid % kWave;
+  const int l32 = lane & 31;
+  const int hsel = lane >> 5;
+  const int hs = wave / 4;  // head of the pair
+  const int wq = wave % 4;  // 32-position query block
+
+  // ---- the work item: (sequence blockIdx.y, column blockIdx.x, query tile), query
+  // tiles dispatched longest first.
+  const int group = p.hq / p.hk;
+  const int chunks = group / HW;
+  const int s = blockIdx.y;
+  const int len = sload(p.seq_lens + s);
+  const int context = sload(p.context_lens + s);
+  if (len <= 1) return;  // a decode row: the decode kernel has it
+  const int qtiles = (len + kPrefillQueryTile - 1) / kPrefillQueryTile;
+  const int qt = static_cast<int>(gridDim.z) - 1 - static_cast<int>(blockIdx.z);
+  if (qt >= qtiles) return;
+  const int c = blockIdx.x;
+  const int kvh = c / chunks;
+  const int nt = prefill_item_tiles(context, len, qt);
+
+  const float score_c = p.scale * kLog2e;  // > 0 (the dispatcher's condition)
+  const char* kpool = static_cast<const char*>(p.k_pool);
+  const char* vpool = static_cast<const char*>(p.v_pool);
+  const uint32_t row_bytes = static_cast<uint32_t>(p.kv_row_bytes);
+  const uint64_t page_bytes = static_cast<uint64_t>(row_bytes) << p.table_shift;
+  const int32_t* table = p.block_tables + static_cast<int64_t>(s) * p.max_blocks;
+  const uint32_t head_off = static_cast<uint32_t>(kvh * static_cast<uint32_t>(p.kv_head_bytes));
+
+  // ---- this wave's rows: one head, 32 query positions.
+  const int offset = context - len;
+  const int w_first = qt * kPrefillQueryTile + 32 * wq;
+  const bool w_active = w_first < len;
+  const int w_kv_end = offset + min(w_first + 32, len);  // keys its last query sees
+  const int w_kv_full = offset + w_first + 1;            // keys all its queries see
+  const int w_nt = w_active ? (w_kv_end + kTileKeys - 1) / kTileKeys : 0;  // its tiles
+  const int my_local = w_first + l32;
+  const bool my_valid = my_local < len;
+  const int my_visible = offset + my_local + 1;
+  const int row_base = sload(p.cu_seqlens_q + s);
+  const int head0 = (c / chunks) * group + (c % chunks) * HW + hs;
+
+  // ---- per-lane constants of the staging and fragment maps (as paged_prefill_lds_kernel).
+  uint32_t k_src_off[kCopies], v_src_off[kCopies], k_src_chunk[kCopies];
+#pragma unroll
+  for (int j = 0; j < kCopies; ++j) {
+    // K rows: chunk c of key r at chunk c ^ (r & 15), so the 16 lanes of a fragment
+    // read that one LDS cycle serves (16 keys, one chunk) fall in distinct banks.
+    k_src_chunk[j] = (((lane & 15) ^ ((KW * wave + 4 * j + (lane >> 4)) & 15)) * 16);
+    k_src_off[j] = static_cast<uint32_t>(4 * j + (lane >> 4)) * row_bytes + k_src_chunk[j];
+    v_src_off[j] = static_cast<uint32_t>(4 * j + (lane >> 4)) * row_bytes + (lane & 15) * 16;
+  }
+  const int v_chunk = lane & 15;
+  const int v_key = KW * wave + KV * (lane >> 4);
+  const int vt_chunk = (2 * (v_key >> 4) + ((v_key >> 2) & 1)) ^ (v_chunk & 7);
+  const uint32_t vt_dst = static_cast<uint32_t>(8 * v_chunk * kVRow + (4 * ((v_key >> 3) & 1) + (v_key & 3)) * 2);
+  uint32_t k_rd[kKSteps];
+#pragma unroll
+  for (int ks = 0; ks < kKSteps; ++ks) k_rd[ks] = l32 * kRow + (((2 * ks + hsel) ^ (l32 & 15)) * 16);
+  uint32_t v_rd[2][4];
+  {
+    const int f0 = (l32 ^ (l32 >> 3)) & 7;
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) v_rd[par][ks] = l32 * kVRow + ((((2 * ks + hsel) ^ f0 ^ (4 * par)) & 7) * 16);
+    }
+  }
+
+  // Page id of this wave's keys of tile t (past the last tile: the last tile again).
+  auto page_of = [&](int t) __attribute__((always_inline)) -> int {
+    const int key0 = min(min(t, nt - 1) * kTileKeys + KW * wave, context - 1);
+    return sload(table + (key0 >> p.block_shift));
+  };
+  auto stage = [&](int t, int page, auto slot) __attribute__((always_inline)) {
+    t = min(t, nt - 1);
+    const uint32_t kdst = lds_address(k_arr(slot) + KW * wave * kRow);
+    const uint32_t rdst = lds_address(r_arr(slot) + KW * wave * kRow);
+    const int key0 = t * kTileKeys + KW * wave;
+    const int last = context - 1;
+    const uint64_t head = static_cast<uint64_t>(static_cast<uint32_t>(page)) * page_bytes + head_off;
+    if (key0 + KW - 1 <= last) {
+      const uint64_t base = head + static_cast<uint32_t>(key0 & p.block_mask) * row_bytes;
+#pragma unroll
+      for (int j = 0; j < kCopies; ++j) {
+        copy_to_lds(kpool + base, k_src_off[j], kdst + 4 * j * kRow);
+        copy_to_lds(vpool + base, v_src_off[j], rdst + 4 * j * kRow);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kCopies; ++j) {
+        const uint32_t row = static_cast<uint32_t>(min(key0 + 4 * j + (lane >> 4), last) & p.block_mask) * row_bytes;
+        copy_to_lds(kpool + head, row + k_src_chunk[j], kdst + 4 * j * kRow);
+        copy_to_lds(vpool + head, row + (lane & 15) * 16, rdst + 4 * j * kRow);
+      }
+    }
+  };
+  typedef __attribute__((address_space(3))) uint32_t lds_u32;
+  auto store_v = [&](auto slot, auto par) __attribute__((always_inline)) {
+    const char* raw = r_arr(slot) + v_key * kRow + v_chunk * 16;
+    u32x4 vr[KV];
+#pragma unroll
+    for (int j = 0; j < KV; ++j) vr[j] = *reinterpret_cast<const u32x4*>(raw + j * kRow);
+    const uint32_t row0 = lds_address(v_arr(par)) + vt_dst + (vt_chunk & 7) * 16;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t sel = (e & 1) == 0 ? 0x05040100u : 0x07060302u;
+      const uint32_t addr = (row0 ^ (e * 16)) + e * kVRow;
+      *reinterpret_cast<lds_u32*>(addr) = __builtin_amdgcn_perm(vr[1][e >> 1], vr[0][e >> 1], sel);
+    }
+  };
+
+  // ---- per-wave state.
+  u32x4 qop[kKSteps];
+  {
+    const int local = min(my_local, len - 1);
+    const int64_t qrow = static_cast<int64_t>(row_base + local) * p.hq + head0;
+    const char* qp = static_cast<const char*>(p.q) + (qrow * D + 8 * hsel) * 2;
+#pragma unroll
+    for (int ks = 0; ks < kKSteps; ++ks) qop[ks] = load16(qp + ks * 32);
+  }
+  f32x16 o[kDBlocks];
+#pragma unroll
+  for (int db = 0; db < kDBlocks; ++db) o[db] = f32x16{};
+  float m_run = -INFINITY, l_run = 0.0f;
+  f32x16 sc0[2], sc1[2];  // scores of even / odd tiles
+
+  // S(t) = K(t) Q^T from K slot `slot`, fragments read four MFMAs ahead.
+  auto qk = [&](auto slot, f32x16 (&sc)[2]) __attribute__((always_inline)) {
+    constexpr int kLook = 4;
+    const char* kt = k_arr(slot);
+    auto k_frag = [&](int i) __attribute__((always_inline)) {
+      return *reinterpret_cast<const u32x4*>(kt + (i & 1) * 32 * kRow + k_rd[i >> 1]);
+    };
+    sc[0] = f32x16{};
+    sc[1] = f32x16{};
+    u32x4 fa[kLook];
+#pragma unroll
+    for (int i = 0; i < kLook; ++i) fa[i] = k_frag(i);
+#pragma unroll
+    for (int i = 0; i < 2 * kKSteps; ++i) {
+      const u32x4 a = fa[i % kLook];
+      if (i + kLook < 2 * kKSteps) fa[i % kLook] = k_frag(i + kLook);
+      sc[i & 1] = Mma<TQ>::run(a, qop[i >> 1], sc[i & 1]);
+    }
+  };
+  // Causal mask of tile t's scores (tiles crossing this wave's diagonal only).
+  auto mask = [&](int t, f32x16 (&sc)[2]) __attribute__((always_inline)) {
+    const int key0 = t * kTileKeys;
+    if (key0 + kTileKeys > w_kv_full) {
+      const int lim = my_valid ? my_visible - key0 - 4 * hsel : INT_MIN;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          if (kb * 32 + 8 * (r >> 2) + (r & 3) >= lim) sc[kb][r] = -INFINITY;
+        }
+      }
+    }
+  };
+  // Running max of a tile's scores (raised only past the slack, O and l rescaled with
+  // it); returns -max in log2 units, the exponent's offset.
+  auto tile_max = [&](const f32x16 (&sc)[2]) __attribute__((always_inline)) -> float {
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sc[kb][r]);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave)) * score_c;
+    if (__builtin_amdgcn_ballot_w64(tmax > m_run + kRescaleSlack) != 0) {
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = m_new == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < kDBlocks; ++db) o[db] *= alpha;
+    }
+    return m_run == -INFINITY ? 0.0f : -m_run;
+  };
+  // Score element r of key block kb -> probability: exp2(s * c - max), summed into
+  // ps[r % 4] and packed in pairs into the P^T operand pop[2 kb + r / 8].
+  auto prob = [&](const f32x16 (&sc)[2], int kb, int r, float neg_mu, float (&pf)[2][16],
+                  float (&ps)[4]) __attribute__((always_inline)) {
+    pf[kb][r] = __builtin_amdgcn_exp2f(fmaf(sc[kb][r], score_c, neg_mu));
+    ps[r & 3] += pf[kb][r];
+  };
+  auto pack = [&](const float (&pf)[2][16], int kb, int half, u32x4 (&pop)[4]) __attribute__((always_inline)) {
+    const float* v = &pf[kb][8 * half];
+    pop[2 * kb + half] = u32x4{Mma<TQ>::pack2(v[0], v[1]), Mma<TQ>::pack2(v[2], v[3]),
+                               Mma<TQ>::pack2(v[4], v[5]), Mma<TQ>::pack2(v[6], v[7])};
+  };
+  constexpr int kMfma = 0x008, kDsRead = 0x100, kVec = 0x002 | 0x400;  // VALU and TRANS
+  // Phase A of tile t: S(t + 1) = K(t + 1) Q^T from K slot `slot`, each MFMA paired with
+  // one K fragment read (four ahead) and one probability of key block 0 of tile t.
+  auto phase_a = [&](auto slot, f32x16 (&nxt)[2], const f32x16 (&cur)[2], float neg_mu,
+                     float (&pf)[2][16], float (&ps)[4], u32x4 (&pop)[4]) __attribute__((always_inline)) {
+    constexpr int kLook = 4;
+    const char* kt = k_arr(slot);
+    auto k_frag = [&](int i) __attribute__((always_inline)) {
+      return *reinterpret_cast<const u32x4*>(kt + (i & 1) * 32 * kRow + k_rd[i >> 1]);
+    };
+    nxt[0] = f32x16{};
+    nxt[1] = f32x16{};
+    u32x4 fa[kLook];
+#pragma unroll
+    for (int i = 0; i < kLook; ++i) fa[i] = k_frag(i);
+#pragma unroll
+    for (int i = 0; i < 2 * kKSteps; ++i) {
+      const u32x4 a = fa[i % kLook];
+      if (i + kLook < 2 * kKSteps) fa[i % kLook] = k_frag(i + kLook);
+      nxt[i & 1] = Mma<TQ>::run(a, qop[i >> 1], nxt[i & 1]);
+      prob(cur, 0, i, neg_mu, pf, ps);
+      if (i == 7) pack(pf, 0, 0, pop);
+      if (i == 15) pack(pf, 0, 1, pop);
+    }
+    __builtin_amdgcn_sched_group_barrier(kDsRead, kLook, 0);
+#pragma unroll
+    for (int i = 0; i < 2 * kKSteps; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+      if (i + kLook < 2 * kKSteps) __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+      if (i == 7 || i == 15) {
+        __builtin_amdgcn_sched_group_barrier(kVec, 7, 0);
+      } else {
+        __builtin_amdgcn_sched_group_barrier(kVec, 3, 0);
+      }
+    }
+  };
+  // Phase B of tile t: O^T += V^T(t) P^T(t) from V^T buffer `par`; the first eight MFMAs
+  // (keys 0-31) each paired with two probabilities of key block 1, which the last
+  // eight consume.
+  auto phase_b = [&](auto par, const f32x16 (&cur)[2], float neg_mu, float (&pf)[2][16],
+                     float (&ps)[4], u32x4 (&pop)[4]) __attribute__((always_inline)) {
+    constexpr int kLook = 4;
+    const char* vt = v_arr(par);
+    auto v_frag = [&](int i) __attribute__((always_inline)) {
+      const int db = i & 3, ks = i >> 2;
+      return *reinterpret_cast<const u32x4*>(vt + db * 32 * kVRow + v_rd[db & 1][ks]);
+    };
+    u32x4 fa[kLook];
+#pragma unroll
+    for (int i = 0; i < kLook; ++i) fa[i] = v_frag(i);
+#pragma unroll
+    for (int i = 0; i < kDBlocks * 4; ++i) {
+      const u32x4 a = fa[i % kLook];
+      if (i + kLook < kDBlocks * 4) fa[i % kLook] = v_frag(i + kLook);
+      o[i & 3] = Mma<TQ>::run(a, pop[i >> 2], o[i & 3]);
+      if (i < 8) {
+        prob(cur, 1, 2 * i, neg_mu, pf, ps);
+        prob(cur, 1, 2 * i + 1, neg_mu, pf, ps);
+      }
+      if (i == 3) pack(pf, 1, 0, pop);
+      if (i == 7) pack(pf, 1, 1, pop);
+    }
+    __builtin_amdgcn_sched_group_barrier(kDsRead, kLook, 0);
+#pragma unroll
+    for (int i = 0; i < kDBlocks * 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+      if (i + kLook < kDBlocks * 4) __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+      if (i == 3 || i == 7) {
+        __builtin_amdgcn_sched_group_barrier(kVec, 10, 0);
+      } else if (i < 8) {
+        __builtin_amdgcn_sched_group_barrier(kVec, 6, 0);
+      }
+    }
+  };
+
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+
+  // ---- prologue: tiles 0-2 staged, page ids of tiles 3-5 fetched; tile 0's V^T built
+  // and its scores computed.
+  stage(0, page_of(0), I0{});
+  stage(1, page_of(1), I1{});
+  stage(2, page_of(2), I2{});
+  int pg[3] = {page_of(3), page_of(4), page_of(5)};  // pg[x]: next tile staged into slot x
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kStageOps) : "memory");
+  store_v(I0{}, I0{});
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  if (w_nt > 0) qk(I0{}, sc0);
+
+  // Step for tile t: X = t % 3 (the slots tile t used, restaged with tile t + 3), Y =
+  // (t + 1) % 3 (tile t + 1's slots), P = t & 1 (tile t's score and V^T buffers).
+  auto step = [&](int t, auto xs, auto par) __attribute__((always_inline)) {
+    constexpr int X = decltype(xs)::value;
+    constexpr int Y = (X + 1) % 3;
+    constexpr int P = decltype(par)::value;
+    using IY = std::integral_constant<int, Y>;
+    using IQ = std::integral_constant<int, 1 - P>;
+    f32x16(&cur)[2] = P == 0 ? sc0 : sc1;
+    f32x16(&nxt)[2] = P == 0 ? sc1 : sc0;
+    // Tile t + 1 has landed for this wave (tiles t + 2 may still be in flight); the
+    // barrier publishes it and tile t's V^T, and retires tile t - 1.
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kStageOps) : "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    store_v(IY{}, IQ{});
+    stage(t + 3, pg[X], xs);
+    pg[X] = page_of(t + 6);
+    __builtin_amdgcn_sched_barrier(0);
+    if (t < w_nt) {
+      mask(t, cur);
+      const float neg_mu = tile_max(cur);
+      float pf[2][16];
+      float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      u32x4 pop[4];
+      // Scores of tile t + 1 even past this wave's last tile (the slot then holds a
+      // staged copy of a valid tile; the result goes unused): no branch, so the
+      // probabilities stay interleaved with these MFMAs.
+      phase_a(IY{}, nxt, cur, neg_mu, pf, ps, pop);
+      phase_b(par, cur, neg_mu, pf, ps, pop);
+      l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+    }
+  };
+  for (int t = 0; t < nt; t += 6) {
+    step(t, I0{}, I0{});
+    if (t + 1 < nt) step(t + 1, I1{}, I1{});
+    if (t + 2 < nt) step(t + 2, I2{}, I0{});
+    if (t + 3 < nt) step(t + 3, I0{}, I1{});
+    if (t + 4 < nt) step(t + 4, I1{}, I0{});
+    if (t + 5 < nt) step(t + 5, I2{}, I1{});
+  }
+  // No copy may still be writing LDS when the workgroup ends.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (!w_active || !my_valid) return;
+  const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  const int64_t orow = (static_cast<int64_t>(row_base + my_local) * p.hq + head0) * D;
+#pragma unroll
+  for (int db = 0; db < kDBlocks; ++db) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = db * 32 + 8 * j + 4 * hsel;
+      float r[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r[i] = o[db][4 * j + i] * inv;
+      *reinterpret_cast<u32x2*>(static_cast<char*>(p.out) + (orow + d) * 2) =
+          u32x2{Mma<TQ>::pack2(r[0], r[1]), Mma<TQ>::pack2(r[2], r[3])};
+    }
+  }
+}
+
 // Combine the pieces of every prefill item cut between stream workgroups. Workgroup b
 // looks at the start of share b; if that falls inside an item and is the item's first
 // such boundary, it merges the item. The item's piece slots are listed once in LDS;
@@ -1188,6 +1582,12 @@ void launch_prefill_lds(const PagedParams& p, int max_query_len, hipStream_t str
     const int cols = p.hk * (p.hq / p.hk / HS);
     const int qtiles = (max_query_len + kPrefillQueryTile - 1) / kPrefillQueryTile;
     const dim3 grid(cols, p.num_seqs, qtiles);
+    if constexpr (HS == 2) {
+      if (!p.pf_register_staging) {
+        paged_prefill_pipe_kernel<TQ><<<grid, 512, 0, stream>>>(p);
+        return;
+      }
+    }
     paged_prefill_lds_kernel<TQ, HS, false><<<grid, 256 * HS, 0, stream>>>(p);
   }
 }
