@@ -151,9 +151,11 @@ void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, i
                  int32_t kv_dtype, const Options& o);
 
 // The MFMA prefill's schedule. The grid (one workgroup per 128-query item) is chosen
-// when there are at least as many items as CUs: the hardware dispatcher then balances
-// them, with no partials to merge. With fewer items (a chunk of a long prompt, a
-// prefill beside decodes) the grid would leave CUs idle behind a few long items, so
+// when there are at least half as many items as CUs: the hardware dispatcher then
+// balances them, with no partials to merge (four 512-query chunks beside 28 decodes,
+// 136 items: grid 102 us, stream 110 us). With fewer items (one chunk of a long
+// prompt, 40 items: stream 104 us, grid 109 us) the grid would leave CUs idle behind a
+// few long items, so
 // the stream schedule is used: one persistent workgroup per CU (times the
 // prefill_wgs_per_cu option) with balanced shares of all key tiles, cut items merged
 // after (measured at 8K-16K contexts: 2.5-3x the grid). The item count is estimated
@@ -170,7 +172,7 @@ void plan_prefill(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, 
   const int64_t items = static_cast<int64_t>((num_tokens + mvllm::kPrefillQueryTile - 1) /
                                              mvllm::kPrefillQueryTile) *
                         (hq / mvllm::prefill_item_heads(hq / hk));
-  if (forced != 1 && items >= device_cus()) return;
+  if (forced != 1 && 2 * items >= device_cus()) return;
   int64_t wgs = static_cast<int64_t>(o.prefill_wgs_per_cu) * device_cus();
   if (wgs > mvllm::kMaxPrefillWgs) wgs = mvllm::kMaxPrefillWgs;
   const uint64_t rows = static_cast<uint64_t>(2 * wgs) * mvllm::prefill_item_heads(hq / hk) *
