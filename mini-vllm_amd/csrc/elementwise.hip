@@ -415,7 +415,12 @@ struct TokenStrides {
   int64_t q, kv;
 };
 
-template <typename T, typename TPos, int kR, bool KV>
+// G rows per kR-lane group: G consecutive heads of one token (q heads, k heads or, with
+// KV, v heads), so the token's position, its cos/sin rows and the norm weight are loaded
+// once per group, and the G row loads are in flight together (one 16-byte load per lane
+// and a position-dependent table read behind it, per row, left most of HBM's bandwidth
+// unused at G = 1). G divides hq and hk; G = 1 is one row per group.
+template <typename T, typename TPos, int kR, int G, bool KV>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ wq,
     const void* __restrict__ wk, const TPos* __restrict__ positions,
@@ -424,98 +429,131 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     int64_t num_positions, int64_t max_positions, float eps, KvSink kv, TokenStrides ts) {
   constexpr int N = Chunk<T>::kN;
   constexpr int D = kR * N;
+  constexpr int64_t kRowBytes = static_cast<int64_t>(D) * Elem<T>::kBytes;
   const int lane = threadIdx.x % kWave;
   const int r = lane % kR;
-  const int64_t row = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kR;
+  const int64_t group = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kR;
+  const int64_t qk_groups = (q_rows + k_rows) / G;
   if constexpr (KV) {
-    if (row >= q_rows + k_rows) {  // a whole kR-lane group: a v row to copy
-      const int64_t local = row - q_rows - k_rows;
+    if (group >= qk_groups) {  // a whole kR-lane group: G v rows to copy
+      const int64_t local = (group - qk_groups) * G;
       if (local >= kv.v_rows) return;
       const int64_t vt = local / hk;
       const int32_t slot = kv.slots[vt];
       if (slot < 0 || slot >= kv.num_slots) return;
-      const int64_t dst = (static_cast<int64_t>(slot) * hk + local % hk) * D * Elem<T>::kBytes;
-      const int64_t src = (vt * ts.kv + (local - vt * hk) * D) * Elem<T>::kBytes;
-      store16(static_cast<char*>(kv.v_pool) + dst + r * 16,
-              nt_load16(static_cast<const char*>(kv.v) + src + r * 16));
+      const int64_t h0 = local - vt * hk;
+      const char* src = static_cast<const char*>(kv.v) + (vt * ts.kv + h0 * D) * Elem<T>::kBytes + r * 16;
+      char* dst = static_cast<char*>(kv.v_pool) + (static_cast<int64_t>(slot) * hk + h0) * kRowBytes + r * 16;
+      u32x4 rows[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) rows[g] = nt_load16(src + g * kRowBytes);
+#pragma unroll
+      for (int g = 0; g < G; ++g) store16(dst + g * kRowBytes, rows[g]);
       return;
     }
   }
-  const bool live = row < q_rows + k_rows;
-  const bool is_k = row >= q_rows;
-  const int64_t local = is_k ? row - q_rows : row;
+  const bool live = group < qk_groups;
+  const int64_t first = live ? group * G : 0;  // first row of the group
+  const bool is_k = first >= q_rows;
+  const int64_t local = is_k ? first - q_rows : first;
   const int heads = is_k ? hk : hq;
-  const int64_t token = live ? local / heads : 0;
-  const int64_t head = live ? local - token * heads : 0;
+  // 32-bit division when the row index fits (always, short of 2^31 rows)
+  const int64_t token = local < (int64_t{1} << 31)
+                            ? static_cast<int64_t>(static_cast<uint32_t>(local) / static_cast<uint32_t>(heads))
+                            : local / heads;
+  const int64_t head0 = local - token * heads;
   const char* xr = static_cast<const char*>(is_k ? k : q) +
-                   (token * (is_k ? ts.kv : ts.q) + head * D) * Elem<T>::kBytes;
-
-  // rmsnorm, as rmsnorm_vec_kernel<T, kR, 1>
-  const u32x4 held = nt_load16(xr + r * 16);
-  float f[N];
-  Chunk<T>::unpack(held, f);
-  float sumsq = 0.0f;
+                   (token * (is_k ? ts.kv : ts.q) + head0 * D) * Elem<T>::kBytes + r * 16;
+  u32x4 held[G];
 #pragma unroll
-  for (int e = 0; e < N; ++e) sumsq = fmaf(f[e], f[e], sumsq);
-  sumsq = group_sum<kR>(sumsq);
-  const float inv = rsqrtf(sumsq / static_cast<float>(D) + eps);
+  for (int g = 0; g < G; ++g) held[g] = nt_load16(xr + g * kRowBytes);
+  const int64_t pidx = token < num_positions ? token
+                       : (num_positions < (int64_t{1} << 31) && token < (int64_t{1} << 31)
+                              ? static_cast<int64_t>(static_cast<uint32_t>(token) %
+                                                     static_cast<uint32_t>(num_positions))
+                              : token % num_positions);
+  const int64_t pos = static_cast<int64_t>(positions[pidx]);
+  const bool pos_ok = pos >= 0 && pos < max_positions;
   float wf[N];
   Chunk<T>::unpack(load16(static_cast<const char*>(is_k ? wk : wq) + r * 16), wf);
-  float y[N];
-#pragma unroll
-  for (int e = 0; e < N; ++e) {
-    if constexpr (N == 4) {
-      y[e] = __fmul_rn(__fmul_rn(f[e], inv), wf[e]);
-    } else {
-      y[e] = Elem<T>::round(__fmul_rn(Elem<T>::round(__fmul_rn(f[e], inv)), wf[e]));
-    }
-  }
-
-  // the rotation partner's values (dims +-D/2), across lanes: lane r ^ (kR / 2). For
-  // kR = 16 that is a rotation by 8 inside a 16-lane DPP row (one v_mov_dpp per value).
-  float py[N];
-#pragma unroll
-  for (int e = 0; e < N; ++e) {
-    if constexpr (kR == 16) {
-      py[e] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(y[e]), 0x128, 0xF, 0xF, false));
-    } else {
-      py[e] = __shfl_xor(y[e], kR / 2, kWave);
-    }
-  }
-  if (!live) return;
-
-  const int64_t pos = static_cast<int64_t>(positions[token % num_positions]);
-  float out[N];
-  if (pos < 0 || pos >= max_positions) {
-#pragma unroll
-    for (int e = 0; e < N; ++e) out[e] = __int_as_float(0x7fc00000);
-  } else {
-    const float* cr = cos_t + pos * D + r * N;
-    const float* sr = sin_t + pos * D + r * N;
-    float c[N], sn[N];
+  float c[N], sn[N];
+  {
+    // an out-of-range position reads row 0 (its outputs are NaN below)
+    const int64_t row = pos_ok ? pos : 0;
+    const float* cr = cos_t + row * D + r * N;
+    const float* sr = sin_t + row * D + r * N;
 #pragma unroll
     for (int e = 0; e < N; e += 4) {
       Chunk<float>::unpack(load16(cr + e), c + e);
       Chunk<float>::unpack(load16(sr + e), sn + e);
     }
-    const bool lo = r < kR / 2;
+  }
+  // lo half: x_lo * cos - x_hi * sin = x_lo * cos + x_hi * (-sin), exactly (negation
+  // commutes with rounding); hi half: x_hi * cos + x_lo * sin. The sign is folded into
+  // the sine once per group.
+  if (r < kR / 2) {
+#pragma unroll
+    for (int e = 0; e < N; ++e) sn[e] = -sn[e];
+  }
+  if (!pos_ok) {
+    // every output of a row at an out-of-range position is NaN
+#pragma unroll
+    for (int e = 0; e < N; ++e) c[e] = sn[e] = __int_as_float(0x7fc00000);
+  }
+  int32_t slot = -1;
+  if constexpr (KV) {
+    if (is_k && live) slot = kv.slots[token];
+  }
+
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    // rmsnorm, as rmsnorm_vec_kernel<T, kR, 1>
+    float f[N];
+    Chunk<T>::unpack(held[g], f);
+    float sumsq = 0.0f;
+#pragma unroll
+    for (int e = 0; e < N; ++e) sumsq = fmaf(f[e], f[e], sumsq);
+    sumsq = group_sum<kR>(sumsq);
+    const float inv = rsqrtf(sumsq / static_cast<float>(D) + eps);
+    float y[N];
+#pragma unroll
+    for (int e = 0; e < N; e += 2) {
+      if constexpr (N == 4) {
+        y[e] = __fmul_rn(__fmul_rn(f[e], inv), wf[e]);
+        y[e + 1] = __fmul_rn(__fmul_rn(f[e + 1], inv), wf[e + 1]);
+      } else {
+        float n0 = __fmul_rn(f[e], inv), n1 = __fmul_rn(f[e + 1], inv);
+        round_pair<T>(n0, n1);
+        y[e] = __fmul_rn(n0, wf[e]);
+        y[e + 1] = __fmul_rn(n1, wf[e + 1]);
+        round_pair<T>(y[e], y[e + 1]);
+      }
+    }
+
+    // the rotation partner's values (dims +-D/2), across lanes: lane r ^ (kR / 2). For
+    // kR = 16 that is a rotation by 8 inside a 16-lane DPP row (one v_mov_dpp per value).
+    float py[N];
 #pragma unroll
     for (int e = 0; e < N; ++e) {
-      // lo half: x_lo * cos - x_hi * sin; hi half: x_hi * cos + x_lo * sin
-      out[e] = lo ? __fsub_rn(__fmul_rn(y[e], c[e]), __fmul_rn(py[e], sn[e]))
-                  : __fadd_rn(__fmul_rn(y[e], c[e]), __fmul_rn(py[e], sn[e]));
+      if constexpr (kR == 16) {
+        py[e] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(y[e]), 0x128, 0xF, 0xF, false));
+      } else {
+        py[e] = __shfl_xor(y[e], kR / 2, kWave);
+      }
     }
-  }
-  const u32x4 packed = pack_chunk<T>(out);
-  if (!KV || !is_k || k_out != nullptr) {
-    char* orow = static_cast<char*>(is_k ? k_out : q_out) + local * static_cast<int64_t>(D) * Elem<T>::kBytes;
-    nt_store16(orow + r * 16, packed);
-  }
-  if constexpr (KV) {
-    if (is_k) {
-      const int32_t slot = kv.slots[token];
-      if (slot >= 0 && slot < kv.num_slots) {
-        const int64_t dst = (static_cast<int64_t>(slot) * hk + local % hk) * D * Elem<T>::kBytes;
+    if (!live) continue;
+
+    float out[N];
+#pragma unroll
+    for (int e = 0; e < N; ++e) out[e] = __fadd_rn(__fmul_rn(y[e], c[e]), __fmul_rn(py[e], sn[e]));
+    const u32x4 packed = pack_chunk<T>(out);
+    if (!KV || !is_k || k_out != nullptr) {
+      char* orow = static_cast<char*>(is_k ? k_out : q_out) + (local + g) * kRowBytes;
+      nt_store16(orow + r * 16, packed);
+    }
+    if constexpr (KV) {
+      if (is_k && slot >= 0 && slot < kv.num_slots) {
+        const int64_t dst = (static_cast<int64_t>(slot) * hk + head0 + g) * kRowBytes;
         store16(static_cast<char*>(kv.k_pool) + dst + r * 16, packed);
       }
     }
@@ -523,6 +561,43 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
 }
 
 namespace {
+// Rows per lane group: the largest G in {8, 4, 2} dividing both head counts that still
+// leaves two waves per SIMD of a 256-CU device (2^17 lanes), else 1.
+int qk_rows_per_group(int64_t rows, int kr, int hq, int hk) {
+  for (int g = 8; g > 1; g /= 2) {
+    if (hq % g == 0 && hk % g == 0 && rows / g * kr >= (int64_t{1} << 17)) return g;
+  }
+  return 1;
+}
+
+template <typename T, typename TPos, int KR>
+void launch_qk_norm_rope_r(const void* q, const void* k, const void* wq, const void* wk,
+                           const TPos* pos, const float* cos_t, const float* sin_t, void* q_out,
+                           void* k_out, int64_t q_rows, int64_t k_rows, int hq, int hk,
+                           int64_t num_positions, int64_t max_positions, float eps,
+                           const KvSink& kv, TokenStrides ts, hipStream_t stream) {
+  const int64_t rows = q_rows + k_rows + kv.v_rows;
+  const int g = qk_rows_per_group(rows, KR, hq, hk);
+  const unsigned grid = static_cast<unsigned>((rows / g * KR + 255) / 256);
+#define MVLLM_QKNR(G)                                                                         \
+  if (kv.k_pool != nullptr) {                                                                 \
+    qk_norm_rope_kernel<T, TPos, KR, G, true><<<grid, 256, 0, stream>>>(                      \
+        q, k, wq, wk, pos, cos_t, sin_t, q_out, k_out, q_rows, k_rows, hq, hk, num_positions, \
+        max_positions, eps, kv, ts);                                                          \
+  } else {                                                                                    \
+    qk_norm_rope_kernel<T, TPos, KR, G, false><<<grid, 256, 0, stream>>>(                     \
+        q, k, wq, wk, pos, cos_t, sin_t, q_out, k_out, q_rows, k_rows, hq, hk, num_positions, \
+        max_positions, eps, kv, ts);                                                          \
+  }
+  switch (g) {
+    case 8: MVLLM_QKNR(8); break;
+    case 4: MVLLM_QKNR(4); break;
+    case 2: MVLLM_QKNR(2); break;
+    default: MVLLM_QKNR(1); break;
+  }
+#undef MVLLM_QKNR
+}
+
 template <typename T, typename TPos>
 hipError_t launch_qk_norm_rope_p(const void* q, const void* k, const void* wq, const void* wk,
                                  const void* positions, const float* cos_t, const float* sin_t,
@@ -532,30 +607,23 @@ hipError_t launch_qk_norm_rope_p(const void* q, const void* k, const void* wq, c
   constexpr int N = Chunk<T>::kN;
   const int64_t q_rows = tokens * hq;
   const int64_t k_rows = tokens * hk;
-  const int64_t rows = q_rows + k_rows + kv.v_rows;
   const TPos* pos = static_cast<const TPos*>(positions);
-#define MVLLM_QKNR(KR)                                                                          \
-  if (kv.k_pool != nullptr) {                                                                   \
-    qk_norm_rope_kernel<T, TPos, KR, true><<<static_cast<unsigned>((rows * KR + 255) / 256),   \
-                                             256, 0, stream>>>(                                 \
-        q, k, wq, wk, pos, cos_t, sin_t, q_out, k_out, q_rows, k_rows, hq, hk, num_positions,  \
-        max_positions, eps, kv, ts);                                                            \
-  } else {                                                                                      \
-    qk_norm_rope_kernel<T, TPos, KR, false><<<static_cast<unsigned>((rows * KR + 255) / 256),  \
-                                              256, 0, stream>>>(                                \
-        q, k, wq, wk, pos, cos_t, sin_t, q_out, k_out, q_rows, k_rows, hq, hk, num_positions,  \
-        max_positions, eps, kv, ts);                                                            \
-  }
   switch (dim / N) {
-    case 2: MVLLM_QKNR(2); break;
-    case 4: MVLLM_QKNR(4); break;
-    case 8: MVLLM_QKNR(8); break;
-    case 16: MVLLM_QKNR(16); break;
-    case 32: MVLLM_QKNR(32); break;
-    case 64: MVLLM_QKNR(64); break;
+#define MVLLM_QKNR_R(KR)                                                                        \
+  case KR:                                                                                      \
+    launch_qk_norm_rope_r<T, TPos, KR>(q, k, wq, wk, pos, cos_t, sin_t, q_out, k_out, q_rows,   \
+                                       k_rows, hq, hk, num_positions, max_positions, eps, kv, ts, \
+                                       stream);                                                 \
+    break;
+    MVLLM_QKNR_R(2)
+    MVLLM_QKNR_R(4)
+    MVLLM_QKNR_R(8)
+    MVLLM_QKNR_R(16)
+    MVLLM_QKNR_R(32)
+    MVLLM_QKNR_R(64)
+#undef MVLLM_QKNR_R
     default: return hipErrorInvalidValue;
   }
-#undef MVLLM_QKNR
   return hipGetLastError();
 }
 
@@ -613,6 +681,16 @@ __device__ __forceinline__ u32x4 swiglu_chunk(const u32x4& gw, const u32x4& uw) 
   float g[E], u[E], r[E];
   Chunk<T>::unpack(gw, g);
   Chunk<T>::unpack(uw, u);
+  if constexpr (Elem<T>::kBytes == 2) {
+    bool small = true;
+#pragma unroll
+    for (int e = 0; e < E; ++e) small = small && fabsf(g[e]) < 32.0f;  // false for NaN
+    if (__all(small)) {  // wave-uniform: both paths give the same bits
+#pragma unroll
+      for (int e = 0; e < E; e += 2) swiglu_two_small<T>(g[e], g[e + 1], u[e], u[e + 1], r[e], r[e + 1]);
+      return pack_chunk<T>(r);
+    }
+  }
 #pragma unroll
   for (int e = 0; e < E; ++e) r[e] = swiglu_one<T>(g[e], u[e]);
   return pack_chunk<T>(r);

@@ -92,41 +92,38 @@ __device__ __forceinline__ uint32_t encode_fp8x4(float a, float b, float c, floa
   return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(cl(c), cl(d), lo, true));
 }
 
-// One wave per token (four tokens per workgroup); the wave of the token that starts a
-// run (its predecessor is not the row before it in the same page) handles the whole
-// run, the others exit at once. The run's length comes from a ballot over the following
-// slots. Lane task = (kv head, K or V, 8-element piece of a row), four per lane: pass 1
-// reduces max|x| over the run's rows (16 row pieces of loads in flight per lane), a
-// group all-reduce over the D/8 tasks of a (head, K/V) gives the scale, rows already in
-// the page are re-encoded if it grew, and pass 2 encodes the run's rows (reloaded from
-// L1/L2).
+// One workgroup per `tokens_per_wg` consecutive tokens (at most 64; one for small
+// calls, so that decode steps spread over workgroups, up to 64 for large ones, so that
+// no workgroup is launched only to find that its token continues a run): a ballot over
+// those tokens finds the runs that start among them, and the workgroup writes them one
+// after another, each whole. The run's length comes from a ballot over the following
+// slots (every wave takes the same ballots). Thread task = (kv head, K or V, 8-element
+// piece of a row), kPieces consecutive lanes per (head, K/V), a workgroup's worth of
+// tasks at a time (all of them for 8 kv heads at D = 128). Each thread loads its piece
+// of up to kRows run rows at once (one round trip), reduces max|x| over them, the
+// kPieces lanes of a (head, K/V) combine theirs into the page's scale, rows already in
+// the page are re-encoded if it grew, and the rows still in registers are encoded and
+// stored. Longer runs (pages of more than kRows tokens) are read kRows rows at a time
+// for the scale and read again to encode, except the last batch, still held.
 template <typename TS, int D>
-__global__ __launch_bounds__(256) void kv_write_fp8_kernel(uint8_t* __restrict__ k_pool,
-                                                           uint8_t* __restrict__ v_pool,
-                                                           float* __restrict__ k_scales,
-                                                           float* __restrict__ v_scales,
-                                                           const void* __restrict__ key,
-                                                           const void* __restrict__ value,
-                                                           const int32_t* __restrict__ slots,
-                                                           int num_tokens, int hk,
-                                                           int block_shift, int64_t num_blocks) {
+__device__ __forceinline__ void kv_write_fp8_run(uint8_t* __restrict__ k_pool,
+                                                 uint8_t* __restrict__ v_pool,
+                                                 float* __restrict__ k_scales,
+                                                 float* __restrict__ v_scales,
+                                                 const void* __restrict__ key,
+                                                 const void* __restrict__ value,
+                                                 const int32_t* __restrict__ slots, int num_tokens,
+                                                 int hk, int block_shift, int t0) {
   constexpr int E = 8;            // elements per task piece
   constexpr int kPieces = D / E;  // tasks per (head, K/V)
-  constexpr int kUnroll = 4;      // rows whose loads are issued together
+  constexpr int kChunks = Elem<TS>::kBytes == 4 ? 2 : 1;  // 16-byte loads per row piece
+  constexpr int kRows = 16 / kChunks;                     // rows held per task
   static_assert(D % E == 0 && kWave % kPieces == 0, "head dim");
   const int lane = threadIdx.x % kWave;
-  const int t0 = static_cast<int>(blockIdx.x) * (blockDim.x / kWave) + static_cast<int>(threadIdx.x / kWave);
-  if (t0 >= num_tokens) return;
   const int slot0 = slots[t0];
-  if (slot0 < 0) return;
   const int page = slot0 >> block_shift;
-  if (page >= num_blocks) return;  // out of the pool: skipped, like a negative slot
   const int rows_per_page = 1 << block_shift;
   const int off0 = slot0 & (rows_per_page - 1);
-  if (t0 > 0) {
-    const int prev = slots[t0 - 1];
-    if (prev >= 0 && prev + 1 == slot0 && (prev >> block_shift) == page) return;  // mid-run
-  }
   // Run length: the longest stretch of slot0 + i for i < min(rows left in the page,
   // tokens left), 64 candidates per ballot.
   const int limit = min(rows_per_page - off0, num_tokens - t0);
@@ -141,88 +138,55 @@ __global__ __launch_bounds__(256) void kv_write_fp8_kernel(uint8_t* __restrict__
     }
   }
 
-  // Lane tasks: task = tg + lane + 64k (k < kT) of the 2 * hk * D/8 (kv head, K or V,
-  // row piece) tasks; per batch kT tasks x kR rows of loads are in flight per lane.
   const int ntasks = 2 * hk * kPieces;
-  constexpr int kT = 4;
-  constexpr int kR = 4;
-  constexpr int kChunks = Elem<TS>::kBytes == 4 ? 2 : 1;  // 16-byte loads per row piece
-  for (int tg = 0; tg < ntasks; tg += kWave * kT) {
-    int task[kT];
-    bool valid[kT];
-    float amax[kT], old[kT];
-#pragma unroll
-    for (int k = 0; k < kT; ++k) {
-      // A lane past the last task mirrors task `lane` (always valid): its loads and
-      // stores repeat that task's, so no memory access sits under a branch and the
-      // loads of a batch stay in flight together.
-      task[k] = tg + lane + kWave * k;
-      valid[k] = task[k] < ntasks;
-      if (!valid[k]) task[k] = lane % ntasks;
-      amax[k] = 0.0f;
-    }
-    auto pair_of = [&](int k) { return task[k] / kPieces; };
-    auto piece_of = [&](int k) { return (task[k] % kPieces) * E; };
-    auto src_row = [&](int k, int row) {
-      const int pr = pair_of(k);
-      const char* src = static_cast<const char*>(pr & 1 ? value : key);
-      return src + ((static_cast<int64_t>(t0 + row) * hk + (pr >> 1)) * D + piece_of(k)) *
-                       Elem<TS>::kBytes;
-    };
-    auto pool_piece = [&](int k, int row) {
-      const int pr = pair_of(k);
-      uint8_t* pool = pr & 1 ? v_pool : k_pool;
-      return pool + ((static_cast<int64_t>(page) << block_shift | row) * hk + (pr >> 1)) * D +
-             piece_of(k);
-    };
-    auto scale_ptr = [&](int k) {
-      const int pr = pair_of(k);
-      return (pr & 1 ? v_scales : k_scales) + static_cast<int64_t>(page) * hk + (pr >> 1);
-    };
-#pragma unroll
-    for (int k = 0; k < kT; ++k) old[k] = off0 > 0 ? *scale_ptr(k) : 0.0f;
+  const int64_t src_stride = static_cast<int64_t>(hk) * D * Elem<TS>::kBytes;  // bytes per token
+  const int64_t pool_stride = static_cast<int64_t>(hk) * D;                    // bytes per slot
+  const int last = (len - 1) / kRows * kRows;  // first row of the last batch
+  for (int base = 0; base < ntasks; base += blockDim.x) {
+    // A thread past the last task mirrors a valid one (its group of kPieces lanes is
+    // all past it): loads stay in bounds and no store is made.
+    const int task = base + static_cast<int>(threadIdx.x);
+    const bool valid = task < ntasks;
+    const int tk = valid ? task : task % ntasks;
+    const int pair = tk / kPieces;
+    const int piece = (tk % kPieces) * E;
+    const bool is_v = pair & 1;
+    const int head = pair >> 1;
+    const char* src = static_cast<const char*>(is_v ? value : key) +
+                      (static_cast<int64_t>(t0) * hk * D + head * D + piece) * Elem<TS>::kBytes;
+    uint8_t* pool = (is_v ? v_pool : k_pool) +
+                    (static_cast<int64_t>(page) << block_shift) * pool_stride + head * D + piece;
+    float* scale_p = (is_v ? v_scales : k_scales) + static_cast<int64_t>(page) * hk + head;
+    const float old = off0 > 0 ? *scale_p : 0.0f;
 
-    // pass 1: max |x| over the run's rows, kT x kR row pieces in flight
-    for (int r0 = 0; r0 < len; r0 += kR) {
-      u32x4 raw[kT][kR][kChunks];
+    u32x4 raw[kRows][kChunks];
+    auto load_rows = [&](int r0) {
 #pragma unroll
-      for (int k = 0; k < kT; ++k) {
+      for (int i = 0; i < kRows; ++i) {
+        const int row = min(r0 + i, len - 1);  // rows past the run repeat its last
 #pragma unroll
-        for (int u = 0; u < kR; ++u) {
-          const int row = min(r0 + u, len - 1);  // rows past the run repeat its last
-#pragma unroll
-          for (int c = 0; c < kChunks; ++c) raw[k][u][c] = load16(src_row(k, row) + 16 * c);
-        }
+        for (int c = 0; c < kChunks; ++c) raw[i][c] = load16(src + row * src_stride + 16 * c);
       }
+    };
+    float amax = 0.0f;
+    for (int r0 = 0; r0 < len; r0 += kRows) {
+      load_rows(r0);
 #pragma unroll
-      for (int k = 0; k < kT; ++k) {
+      for (int i = 0; i < kRows; ++i) {
+        float x[E];
 #pragma unroll
-        for (int u = 0; u < kR; ++u) {
-          {
-            float x[E];
+        for (int c = 0; c < kChunks; ++c) Chunk<TS>::unpack(raw[i][c], x + c * (E / kChunks));
 #pragma unroll
-            for (int c = 0; c < kChunks; ++c) Chunk<TS>::unpack(raw[k][u][c], x + c * (E / kChunks));
-#pragma unroll
-            for (int e = 0; e < E; ++e) amax[k] = fmaxf(amax[k], fabsf(x[e]));
-          }
-        }
+        for (int e = 0; e < E; ++e) amax = fmaxf(amax, fabsf(x[e]));
       }
     }
-    float sc[kT], inv[kT];
-#pragma unroll
-    for (int k = 0; k < kT; ++k) {
-      // tasks of one (head, K/V) are kPieces aligned lanes; invalid tasks form whole
-      // groups of their own
-      sc[k] = fmaxf(old[k], pow2_ceil(group_max<kPieces>(amax[k]) / 448.0f));
-      inv[k] = sc[k] > 0.0f ? 1.0f / sc[k] : 0.0f;  // exact: a power of two
-    }
+    const float sc = fmaxf(old, pow2_ceil(group_max<kPieces>(amax) / 448.0f));
+    const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;  // exact: a power of two
 
     // rows already in the page, re-encoded under a grown scale
-#pragma unroll
-    for (int k = 0; k < kT; ++k) {
-      if (!(valid[k] && old[k] > 0.0f && sc[k] > old[k])) continue;
+    if (valid && old > 0.0f && sc > old) {
       for (int row = 0; row < off0; ++row) {
-        uint8_t* p = pool_piece(k, row);
+        uint8_t* p = pool + row * pool_stride;
         const u32x2 w = *reinterpret_cast<const u32x2*>(p);
         u32x2 out;
 #pragma unroll
@@ -232,7 +196,7 @@ __global__ __launch_bounds__(256) void kv_write_fp8_kernel(uint8_t* __restrict__
           for (int b = 0; b < 4; ++b) {
             // (code * old) / s: every factor a power of two or a 4-bit significand, so
             // the products are exact and equal the correctly rounded quotient
-            v[b] = __fmul_rn(__fmul_rn(fp8e4m3_to_f32((w[i] >> (8 * b)) & 0xffu), old[k]), inv[k]);
+            v[b] = __fmul_rn(__fmul_rn(fp8e4m3_to_f32((w[i] >> (8 * b)) & 0xffu), old), inv);
           }
           out[i] = encode_fp8x4(v[0], v[1], v[2], v[3]);
         }
@@ -240,43 +204,62 @@ __global__ __launch_bounds__(256) void kv_write_fp8_kernel(uint8_t* __restrict__
       }
     }
 
-    // pass 2: encode the run's rows (reloaded)
-    for (int r0 = 0; r0 < len; r0 += kR) {
-      u32x4 raw[kT][kR][kChunks];
+    // the run's rows, the last batch first (it is still in registers)
+    for (int r0 = last; r0 >= 0; r0 -= kRows) {
+      if (r0 != last) load_rows(r0);
+      if (valid) {
 #pragma unroll
-      for (int k = 0; k < kT; ++k) {
-#pragma unroll
-        for (int u = 0; u < kR; ++u) {
-          const int row = min(r0 + u, len - 1);
-#pragma unroll
-          for (int c = 0; c < kChunks; ++c) raw[k][u][c] = load16(src_row(k, row) + 16 * c);
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < kT; ++k) {
-#pragma unroll
-        for (int u = 0; u < kR; ++u) {
-          // a repeated row or mirrored task stores the same bytes again
-          const int row = min(r0 + u, len - 1);
+        for (int i = 0; i < kRows; ++i) {
           float x[E];
 #pragma unroll
-          for (int c = 0; c < kChunks; ++c) Chunk<TS>::unpack(raw[k][u][c], x + c * (E / kChunks));
+          for (int c = 0; c < kChunks; ++c) Chunk<TS>::unpack(raw[i][c], x + c * (E / kChunks));
           u32x2 out;
 #pragma unroll
-          for (int i = 0; i < 2; ++i) {
+          for (int h = 0; h < 2; ++h) {
             // x / s == x * (1 / s) exactly: s is a power of two
-            out[i] = sc[k] > 0.0f ? encode_fp8x4(__fmul_rn(x[4 * i], inv[k]), __fmul_rn(x[4 * i + 1], inv[k]),
-                                                 __fmul_rn(x[4 * i + 2], inv[k]), __fmul_rn(x[4 * i + 3], inv[k]))
-                                  : 0u;
+            out[h] = sc > 0.0f ? encode_fp8x4(__fmul_rn(x[4 * h], inv), __fmul_rn(x[4 * h + 1], inv),
+                                              __fmul_rn(x[4 * h + 2], inv), __fmul_rn(x[4 * h + 3], inv))
+                               : 0u;
           }
-          *reinterpret_cast<u32x2*>(pool_piece(k, off0 + row)) = out;
+          if (r0 + i < len) *reinterpret_cast<u32x2*>(pool + (off0 + r0 + i) * pool_stride) = out;
         }
       }
     }
-#pragma unroll
-    for (int k = 0; k < kT; ++k) {
-      if (valid[k] && task[k] % kPieces == 0) *scale_ptr(k) = sc[k];
+    if (valid && tk % kPieces == 0) *scale_p = sc;
+  }
+}
+
+template <typename TS, int D>
+__global__ __launch_bounds__(256) void kv_write_fp8_kernel(uint8_t* __restrict__ k_pool,
+                                                           uint8_t* __restrict__ v_pool,
+                                                           float* __restrict__ k_scales,
+                                                           float* __restrict__ v_scales,
+                                                           const void* __restrict__ key,
+                                                           const void* __restrict__ value,
+                                                           const int32_t* __restrict__ slots,
+                                                           int num_tokens, int hk, int block_shift,
+                                                           int64_t num_blocks, int tokens_per_wg) {
+  // Token t starts a run when its slot is in the pool and does not continue the slot of
+  // token t - 1 on the same page.
+  const int lane = threadIdx.x % kWave;
+  const int t = static_cast<int>(blockIdx.x) * tokens_per_wg + lane;
+  bool start = false;
+  if (lane < tokens_per_wg && t < num_tokens) {
+    const int slot = slots[t];
+    if (slot >= 0 && (slot >> block_shift) < num_blocks) {
+      start = true;
+      if (t > 0) {
+        const int prev = slots[t - 1];
+        if (prev >= 0 && prev + 1 == slot && (prev >> block_shift) == (slot >> block_shift)) start = false;
+      }
     }
+  }
+  uint64_t starts = __builtin_amdgcn_ballot_w64(start);
+  while (starts != 0) {
+    const int t0 = static_cast<int>(blockIdx.x) * tokens_per_wg + __builtin_ctzll(starts);
+    starts &= starts - 1;
+    kv_write_fp8_run<TS, D>(k_pool, v_pool, k_scales, v_scales, key, value, slots, num_tokens,
+                            hk, block_shift, t0);
   }
 }
 
@@ -285,10 +268,19 @@ hipError_t launch_fp8_t(void* k_pool, void* v_pool, float* k_scales, float* v_sc
                         const void* key, const void* value, const int32_t* slots, int num_tokens,
                         int hk, int head_dim, int block_shift, int64_t num_blocks,
                         hipStream_t stream) {
+  if (num_tokens <= 0) return hipSuccess;
+  // tokens per workgroup: about 1024 workgroups, 1 to 64 tokens each
+  const int tpw = num_tokens >= 64 * 1024 ? 64 : (num_tokens >= 2048 ? num_tokens / 1024 : 1);
+  const unsigned grid = static_cast<unsigned>((num_tokens + tpw - 1) / tpw);
+  // threads per workgroup: the 2 * hk * D / 8 tasks, in whole waves, at most 256
+  auto threads = [hk](int dim) {
+    const int tasks = 2 * hk * dim / 8;
+    return tasks >= 256 ? 256 : (tasks + kWave - 1) / kWave * kWave;
+  };
 #define MVLLM_KV_FP8(DIM)                                                                     \
-  kv_write_fp8_kernel<TS, DIM><<<(num_tokens + 3) / 4, 256, 0, stream>>>(                     \
+  kv_write_fp8_kernel<TS, DIM><<<grid, threads(DIM), 0, stream>>>(                             \
       static_cast<uint8_t*>(k_pool), static_cast<uint8_t*>(v_pool), k_scales, v_scales, key, \
-      value, slots, num_tokens, hk, block_shift, num_blocks)
+      value, slots, num_tokens, hk, block_shift, num_blocks, tpw)
   switch (head_dim) {
     case 32: MVLLM_KV_FP8(32); break;
     case 64: MVLLM_KV_FP8(64); break;

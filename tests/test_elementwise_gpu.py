@@ -188,6 +188,26 @@ def test_swiglu_is_bitwise_equal_to_torch(extension, device, dtype, shape):
     within_ulps(got, want, dtype, ulps=1.0 if dtype != torch.float32 else 4.0)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_swiglu_over_every_16_bit_input(extension, device, dtype):
+    """Every finite 16-bit gate value against torch's expression, bit for bit (sign of
+    zero included). In bit order, whole waves fall inside |g| < 32 (the short
+    instruction path) or outside it (the general one); shuffled, most waves mix both
+    and take the general path; a run of one magnitude exercises each path alone."""
+    bits = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16)
+    g = bits.view(dtype)
+    g = g[torch.isfinite(g.float())]
+    gen = torch.Generator().manual_seed(5)
+    u = (torch.randn(g.numel(), generator=gen) * 2).to(dtype).to(device)
+    small = g[g.float().abs() < 32]
+    for gate in (g, g[torch.randperm(g.numel(), generator=gen)], small.repeat(2)[: g.numel()]):
+        gate = gate.to(device)
+        up = u[: gate.numel()]
+        got = extension.swiglu(gate, up)
+        want = torch_path.silu(gate) * up
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("rows,dim", [(1, 128), (37, 1024), (2048, 1024), (5, 2048)])
 def test_add_rmsnorm_is_the_add_then_rmsnorm(extension, device, dtype, rows, dim):
@@ -292,6 +312,32 @@ def test_qk_norm_rope_is_bitwise_the_unfused_kernels(extension, device, dtype, h
         bad = (got != want).nonzero()
         assert bad.numel() == 0, [(tuple(i.tolist()), float(got[tuple(i)]), float(want[tuple(i)]))
                                   for i in bad[:6]]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("t,hq,hk", [(4096, 16, 8), (1500, 16, 8), (3000, 6, 2)])
+def test_qk_norm_rope_row_groups_are_bitwise_the_unfused_kernels(extension, device, dtype, t, hq, hk):
+    """Large calls, where one lane group takes 8, 4 or 2 heads of a token (the head
+    counts and the token count pick it), bitwise the unfused kernels, including rows at
+    out-of-range positions (NaN) among in-range ones."""
+    d = 128
+    gen = torch.Generator().manual_seed(t + hq)
+    q = (torch.randn(t, hq, d, generator=gen) * 2).to(dtype).to(device)
+    k = (torch.randn(t, hk, d, generator=gen) * 2).to(dtype).to(device)
+    wq = (torch.rand(d, generator=gen) + 0.5).to(dtype).to(device)
+    wk = (torch.rand(d, generator=gen) + 0.5).to(dtype).to(device)
+    cos, sin = (x.to(device) for x in torch_path.rope_tables(d, 8192))
+    pos = torch.randint(0, 8192, (t,), generator=gen)
+    pos[::97] = 8192  # out of range: NaN rows
+    pos = pos.to(device)
+    fq, fk = extension.qk_norm_rope(q, k, wq, wk, pos, cos, sin, 1e-6)
+    uq = extension.rope(extension.rmsnorm(q, wq, 1e-6).unsqueeze(0), pos, cos, sin).squeeze(0)
+    uk = extension.rope(extension.rmsnorm(k, wk, 1e-6).unsqueeze(0), pos, cos, sin).squeeze(0)
+    torch.cuda.synchronize()
+    for got, want in ((fq, uq), (fk, uk)):
+        assert torch.equal(torch.isnan(got), torch.isnan(want))
+        assert torch.equal(got.nan_to_num(0.0), want.nan_to_num(0.0))
+    assert torch.isnan(fq[97]).all() and torch.isfinite(fq[1]).all()
 
 
 def test_qk_norm_rope_against_the_oracle(extension, device):

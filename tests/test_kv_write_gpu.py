@@ -91,6 +91,74 @@ def test_fp8_write_matches_the_oracle_bytes(extension, device, src, hk, d, bs):
     assert np.array_equal(vp.view(torch.uint8).cpu().numpy(), codes_v)
 
 
+def _large_fp8_call(rng, nb, bs, t):
+    """Slots of one large call: sequences of 1..300 tokens (single-token ones are decode
+    steps) on consecutive rows of their own pages, each starting at the row its page's
+    history ends on (or at row 0 of a fresh page), with -1 padding between some; and
+    the history call that partly filled those pages."""
+    pages = rng.permutation(nb).tolist()
+    hist, slots = [], []
+    while len(slots) < t:
+        n = int(rng.integers(1, 4)) if rng.random() < 0.3 else int(rng.integers(5, 300))
+        n = min(n, t - len(slots))
+        need = -(-(n + bs) // bs)
+        if len(pages) < need:
+            break
+        own = [pages.pop() for _ in range(need)]
+        start = int(rng.integers(0, bs))  # rows already written by the history call
+        hist += [own[0] * bs + r for r in range(start)]
+        rows = [own[(start + i) // bs] * bs + (start + i) % bs for i in range(n)]
+        slots += rows
+        if rng.random() < 0.2 and len(slots) < t:
+            slots.append(-1)
+    slots = slots[:t] + [-1] * (t - len(slots[:t]))
+    return np.array(hist, np.int32), np.array(slots, np.int32)
+
+
+@pytest.mark.parametrize("t", [3000, 70000])
+def test_fp8_write_large_calls_match_the_oracle_bytes(extension, device, t):
+    """Calls large enough that a workgroup takes several tokens (2 at 3000, 64 at 70000):
+    runs start anywhere in a workgroup's tokens and cross into the next one's, pages are
+    continued mid-way under a grown or kept scale, decode-like single tokens sit among
+    long chunks; bytes and scales equal the oracle's. The same call with padding slots
+    replaced by slots past the pool leaves the same pool."""
+    rng = np.random.default_rng(t)
+    hk, d, bs = 2, 32, 16
+    nb = t // bs * 3
+    hist, slots = _large_fp8_call(rng, nb, bs, t)
+    codes_k = np.zeros((nb, bs, hk, d), np.uint8)
+    scales_k = np.zeros((nb, hk), np.float32)
+    codes_v, scales_v = codes_k.copy(), scales_k.copy()
+    kp = torch.zeros(nb, bs, hk, d, dtype=torch.float8_e4m3fn, device=device)
+    vp = torch.zeros_like(kp)
+    ks = torch.zeros(nb, hk, device=device)
+    vs = torch.zeros(nb, hk, device=device)
+    for step, sl in enumerate((hist, slots)):
+        x = (rng.standard_normal((len(sl), hk, d)) * (1.0 + step)).astype(np.float32)
+        key = torch.from_numpy(x).to(torch.bfloat16)
+        value = (torch.from_numpy(x) * 0.5 + 0.25).to(torch.bfloat16)
+        codes_k, scales_k = ow.kv_write_fp8(codes_k, scales_k, sl, key.float().numpy())
+        codes_v, scales_v = ow.kv_write_fp8(codes_v, scales_v, sl, value.float().numpy())
+        if step == 1:
+            before = [a.clone() for a in (kp, vp, ks, vs)]
+        extension.kv_write(kp, vp, key.to(device), value.to(device),
+                           torch.from_numpy(sl).to(device), k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    assert np.array_equal(ks.cpu().numpy(), scales_k)
+    assert np.array_equal(vs.cpu().numpy(), scales_v)
+    assert np.array_equal(kp.view(torch.uint8).cpu().numpy(), codes_k)
+    assert np.array_equal(vp.view(torch.uint8).cpu().numpy(), codes_v)
+    bad = slots.copy()
+    bad[bad < 0] = nb * bs + np.arange((bad < 0).sum(), dtype=np.int32)
+    kp2, vp2, ks2, vs2 = before
+    extension.kv_write(kp2, vp2, key.to(device), value.to(device),
+                       torch.from_numpy(bad).to(device), k_scale=ks2, v_scale=vs2)
+    torch.cuda.synchronize()
+    assert torch.equal(kp2.view(torch.uint8), kp.view(torch.uint8))
+    assert torch.equal(vp2.view(torch.uint8), vp.view(torch.uint8))
+    assert torch.equal(ks2, ks) and torch.equal(vs2, vs)
+
+
 def test_fp8_encoding_is_round_to_nearest_even(extension, device):
     """Every e4m3 code's value and every midpoint between neighbours (ties go to the
     even code), written at scale 1 (a block whose max is 448 -> scale pow2ceil(1) = 1)."""
@@ -149,15 +217,18 @@ def test_kv_write_refusals(extension, device):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("hq,hk,d", [(16, 8, 128), (4, 2, 64), (8, 1, 256)])
-def test_qk_norm_rope_kv_write_is_the_unfused_sequence(extension, device, dtype, hq, hk, d):
+@pytest.mark.parametrize("hq,hk,d,t", [(16, 8, 128, 200), (4, 2, 64, 200), (8, 1, 256, 200),
+                                       (16, 8, 128, 3000), (6, 2, 128, 2500)])
+def test_qk_norm_rope_kv_write_is_the_unfused_sequence(extension, device, dtype, hq, hk, d, t):
     """QK-norm + RoPE with the pool write in one launch: q bitwise the fused
     qk_norm_rope's, and both pools bitwise what qk_norm_rope then kv_write leave (the
-    rotated k and the raw v at their slots, -1 slots and the rest of the pool untouched)."""
+    rotated k and the raw v at their slots, -1 slots and the rest of the pool untouched).
+    The larger calls take several heads of a token per lane group."""
     from mini_vllm.torch_path import rope_tables
 
-    rng = np.random.default_rng(hq * d)
-    nb, bs, t = 30, 16, 200
+    rng = np.random.default_rng(hq * d + t)
+    bs = 16
+    nb = max(30, t // bs + 40)
     gen = torch.Generator().manual_seed(hq + d)
     q = torch.randn(t + 5, hq, d, generator=gen).to(dtype).to(device)
     k = torch.randn(t + 5, hk, d, generator=gen).to(dtype).to(device)
