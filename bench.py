@@ -76,14 +76,14 @@ def time_steps(fn, steps: int, warmup: int) -> float:
     return first.elapsed_time(last) / steps
 
 
-def rotated_batches(index: int, copies: int):
+def rotated_batches(index: int, copies: int, kv_dtype=None):
     """`copies` batches sharing shapes and tables, each with its own K/V pools."""
     from mini_vllm.workloads import config_batch
 
-    base = config_batch(index, device="cuda", generator_device="cuda")
+    base = config_batch(index, device="cuda", generator_device="cuda", kv_dtype=kv_dtype)
     batches = [base]
     for c in range(1, copies):
-        other = config_batch(index, device="cuda", seed=0, generator_device="cuda")
+        other = config_batch(index, device="cuda", seed=0, generator_device="cuda", kv_dtype=kv_dtype)
         gen = torch.Generator(device="cuda").manual_seed(1000 + c)
         if other.key_pool.dtype == torch.float8_e4m3fn:
             # fresh fp8 codes with the same scales: any finite code pattern is valid data
@@ -489,8 +489,9 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--copies", type=int, default=3, help="rotated pool copies (defeat the MALL)")
     parser.add_argument("--skip-extras", action="store_true", help="headline config 2 only")
-    parser.add_argument("--extras", default="3,4,5,ew,kv,dense,linear,copy",
-                        help="comma list of extras to run: 3 (prefill), 4 (fp8 decode), "
+    parser.add_argument("--extras", default="3,3fp8,4,5,ew,kv,dense,linear,copy",
+                        help="comma list of extras to run: 3 (prefill), 3fp8 (prefill over an "
+                             "fp8 pool), 4 (fp8 decode), "
                              "5 (engine), 5small (engine, 64 x 128 tokens), 5fp8 (engine, fp8 "
                              "KV cache), ew (elementwise "
                              "kernels), kv (KV write), dense (dense-cache attention), linear "
@@ -542,6 +543,18 @@ def main() -> int:
             "ms_per_call": round(pms, 4), "gflop": round(flops / 1e9, 3),
             "tflops": round(tflops, 2), "frac_of_bf16_mfma_peak": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4)}
         log(f"config 3: {pms * 1e3:.1f} us, {tflops:.1f} TFLOP/s")
+        del pf
+        torch.cuda.empty_cache()
+    if "3fp8" in wanted:
+        log("config 3 over an fp8 pool: building inputs")
+        pf = rotated_batches(3, 2, kv_dtype=torch.float8_e4m3fn)
+        flops = prefill_flops(pf[0])
+        pms = run_paged(pf, max(10, args.steps // 2), 3)
+        tflops = flops / (pms * 1e-3) / 1e12
+        extras["config3_prefill_fp8kv"] = {
+            "ms_per_call": round(pms, 4), "gflop": round(flops / 1e9, 3),
+            "tflops": round(tflops, 2), "frac_of_bf16_mfma_peak": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4)}
+        log(f"config 3 fp8 KV: {pms * 1e3:.1f} us, {tflops:.1f} TFLOP/s")
         del pf
         torch.cuda.empty_cache()
     if "4" in wanted:

@@ -1063,33 +1063,50 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_lds_kernel(const Paged
 // Staging maps and the softmax are those of paged_prefill_lds_kernel, except that K
 // rows are swizzled over 16 chunks (key & 15) instead of 8; K/V slots rotate by three and the score accumulators by two, so the loop is unrolled by
 // six with every buffer named at compile time.
-template <typename TQ>
+template <typename TQ, typename TKV>
 __global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedParams p) {
+  constexpr bool kFp8 = std::is_same_v<TKV, fp8_t>;
   constexpr int D = 128;
   constexpr int kWaves = 8;
   constexpr int HW = 2;                   // query heads per work item, one per wave set
   constexpr int KW = kTileKeys / kWaves;  // keys of a tile staged by one wave
-  constexpr int kCopies = KW / 4;         // 1 KB direct loads per wave per tile (K and V each)
-  constexpr int KV = KW / 4;              // V keys per lane in the transpose
+  constexpr int kRawRow = kFp8 ? D : D * 2;  // bytes of one staged pool row
+  constexpr int kRowLanes = kRawRow / 16;    // lanes per staged row (16 bytes each)
+  constexpr int kCopies = KW * kRowLanes / kWave;  // direct loads per wave per tile (K and V each)
+  constexpr int KV = 2;                   // V keys per lane in the transpose
   constexpr int kKSteps = D / 16;
   constexpr int kDBlocks = D / 32;
   constexpr int kRow = D * 2;
   constexpr int kTileBytes = kTileKeys * kRow;
+  constexpr int kRawTileBytes = kTileKeys * kRawRow;
   constexpr int kVRow = kTileKeys * 2;
   constexpr int kStageOps = 2 * kCopies;  // vector-memory ops of one tile's stage per lane
-  static_assert(KV == 2 && kTileKeys == 64 && 32 * 4 == kPrefillQueryTile, "tile sizes");
+  static_assert(KW == 8 && kTileKeys == 64 && 32 * 4 == kPrefillQueryTile, "tile sizes");
 
-  __shared__ __align__(16) char k_lds0[kTileBytes];
-  __shared__ __align__(16) char k_lds1[kTileBytes];
-  __shared__ __align__(16) char k_lds2[kTileBytes];
-  __shared__ __align__(16) char r_lds0[kTileBytes];
-  __shared__ __align__(16) char r_lds1[kTileBytes];
-  __shared__ __align__(16) char r_lds2[kTileBytes];
+  // Staging slots (raw pool rows: K and V of three tiles), the 16-bit K the MFMAs read
+  // (for 16-bit pools the staged K itself; for fp8 pools a converted copy, two tiles)
+  // and V^T (two tiles).
+  __shared__ __align__(16) char k_lds0[kRawTileBytes];
+  __shared__ __align__(16) char k_lds1[kRawTileBytes];
+  __shared__ __align__(16) char k_lds2[kRawTileBytes];
+  __shared__ __align__(16) char r_lds0[kRawTileBytes];
+  __shared__ __align__(16) char r_lds1[kRawTileBytes];
+  __shared__ __align__(16) char r_lds2[kRawTileBytes];
+  __shared__ __align__(16) char kc_lds0[kFp8 ? kTileBytes : 16];  // converted K, even tiles
+  __shared__ __align__(16) char kc_lds1[kFp8 ? kTileBytes : 16];  // converted K, odd tiles
   __shared__ __align__(1024) char v_lds0[kTileBytes];  // V^T of even tiles
   __shared__ __align__(1024) char v_lds1[kTileBytes];  // V^T of odd tiles
   auto k_arr = [&](auto slot) __attribute__((always_inline)) -> char* {
     constexpr int X = decltype(slot)::value;
     if constexpr (X == 0) return k_lds0; else if constexpr (X == 1) return k_lds1; else return k_lds2;
+  };
+  // The K the MFMAs of tile t read: staging slot t % 3, or converted buffer t & 1.
+  auto kmma_arr = [&](auto slot, auto par) __attribute__((always_inline)) -> char* {
+    if constexpr (kFp8) {
+      if constexpr (decltype(par)::value == 0) return kc_lds0; else return kc_lds1;
+    } else {
+      return k_arr(slot);
+    }
   };
   auto r_arr = [&](auto slot) __attribute__((always_inline)) -> char* {
     constexpr int X = decltype(slot)::value;
@@ -1144,14 +1161,23 @@ __global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedPara
   const int head0 = (c / chunks) * group + (c % chunks) * HW + hs;
 
   // ---- per-lane constants of the staging and fragment maps (as paged_prefill_lds_kernel).
+  // Copy j of a wave's keys: lane -> key kRowLanes-lane row (64 / kRowLanes) j + lane /
+  // kRowLanes, 16-byte chunk lane % kRowLanes.
+  constexpr int kKeysPerCopy = kWave / kRowLanes;
   uint32_t k_src_off[kCopies], v_src_off[kCopies], k_src_chunk[kCopies];
 #pragma unroll
   for (int j = 0; j < kCopies; ++j) {
-    // K rows: chunk c of key r at chunk c ^ (r & 15), so the 16 lanes of a fragment
-    // read that one LDS cycle serves (16 keys, one chunk) fall in distinct banks.
-    k_src_chunk[j] = (((lane & 15) ^ ((KW * wave + 4 * j + (lane >> 4)) & 15)) * 16);
-    k_src_off[j] = static_cast<uint32_t>(4 * j + (lane >> 4)) * row_bytes + k_src_chunk[j];
-    v_src_off[j] = static_cast<uint32_t>(4 * j + (lane >> 4)) * row_bytes + (lane & 15) * 16;
+    const int key = kKeysPerCopy * j + lane / kRowLanes;  // wave-local
+    if constexpr (kFp8) {
+      // raw rows as they are; the conversion places the chunks
+      k_src_chunk[j] = (lane % kRowLanes) * 16;
+    } else {
+      // K rows: chunk c of key r at chunk c ^ (r & 15), so the 16 lanes of a fragment
+      // read that one LDS cycle serves (16 keys, one chunk) fall in distinct banks.
+      k_src_chunk[j] = (((lane & 15) ^ ((KW * wave + key) & 15)) * 16);
+    }
+    k_src_off[j] = static_cast<uint32_t>(key) * row_bytes + k_src_chunk[j];
+    v_src_off[j] = static_cast<uint32_t>(key) * row_bytes + (lane % kRowLanes) * 16;
   }
   const int v_chunk = lane & 15;
   const int v_key = KW * wave + KV * (lane >> 4);
@@ -1175,35 +1201,77 @@ __global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedPara
     const int key0 = min(min(t, nt - 1) * kTileKeys + KW * wave, context - 1);
     return sload(table + (key0 >> p.block_shift));
   };
+  // fp8 pools: the page's K and V scales of each staged slot (the wave's keys share a
+  // page), loaded with the page id.
+  float ks[3] = {0.0f, 0.0f, 0.0f}, vs[3] = {0.0f, 0.0f, 0.0f};
   auto stage = [&](int t, int page, auto slot) __attribute__((always_inline)) {
+    constexpr int X = decltype(slot)::value;
     t = min(t, nt - 1);
-    const uint32_t kdst = lds_address(k_arr(slot) + KW * wave * kRow);
-    const uint32_t rdst = lds_address(r_arr(slot) + KW * wave * kRow);
+    const uint32_t kdst = lds_address(k_arr(slot) + KW * wave * kRawRow);
+    const uint32_t rdst = lds_address(r_arr(slot) + KW * wave * kRawRow);
     const int key0 = t * kTileKeys + KW * wave;
     const int last = context - 1;
     const uint64_t head = static_cast<uint64_t>(static_cast<uint32_t>(page)) * page_bytes + head_off;
+    if constexpr (kFp8) {
+      const int64_t si = static_cast<int64_t>(page) * p.hk + kvh;
+      ks[X] = __int_as_float(sload(reinterpret_cast<const int32_t*>(p.k_scales + si)));
+      vs[X] = __int_as_float(sload(reinterpret_cast<const int32_t*>(p.v_scales + si)));
+    }
     if (key0 + KW - 1 <= last) {
       const uint64_t base = head + static_cast<uint32_t>(key0 & p.block_mask) * row_bytes;
 #pragma unroll
       for (int j = 0; j < kCopies; ++j) {
-        copy_to_lds(kpool + base, k_src_off[j], kdst + 4 * j * kRow);
-        copy_to_lds(vpool + base, v_src_off[j], rdst + 4 * j * kRow);
+        copy_to_lds(kpool + base, k_src_off[j], kdst + kKeysPerCopy * j * kRawRow);
+        copy_to_lds(vpool + base, v_src_off[j], rdst + kKeysPerCopy * j * kRawRow);
       }
     } else {
 #pragma unroll
       for (int j = 0; j < kCopies; ++j) {
-        const uint32_t row = static_cast<uint32_t>(min(key0 + 4 * j + (lane >> 4), last) & p.block_mask) * row_bytes;
-        copy_to_lds(kpool + head, row + k_src_chunk[j], kdst + 4 * j * kRow);
-        copy_to_lds(vpool + head, row + (lane & 15) * 16, rdst + 4 * j * kRow);
+        const uint32_t row = static_cast<uint32_t>(min(key0 + kKeysPerCopy * j + lane / kRowLanes, last) &
+                                                   p.block_mask) * row_bytes;
+        copy_to_lds(kpool + head, row + k_src_chunk[j], kdst + kKeysPerCopy * j * kRawRow);
+        copy_to_lds(vpool + head, row + (lane % kRowLanes) * 16, rdst + kKeysPerCopy * j * kRawRow);
       }
     }
   };
+  // fp8 pools: eight codes of a raw row -> eight 16-bit elements times the page scale.
+  auto dequant8 = [&](const u32x2& w, float scale) __attribute__((always_inline)) -> u32x4 {
+    u32x4 out;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w[i]), false);
+      const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w[i]), true);
+      out[2 * i] = Mma<TQ>::pack2(lo[0] * scale, lo[1] * scale);
+      out[2 * i + 1] = Mma<TQ>::pack2(hi[0] * scale, hi[1] * scale);
+    }
+    return out;
+  };
+  // fp8 pools: this wave's staged K rows of slot `slot` (tile-local keys KW * wave ..
+  // +7, each lane 16 codes of one row) -> converted K buffer `par`, in the swizzled
+  // layout the fragment reads use (logical chunk c of key r at chunk c ^ (r & 15)).
+  typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+  auto convert_k = [&](auto slot, auto par) __attribute__((always_inline)) {
+    constexpr int X = decltype(slot)::value;
+    const int key = KW * wave + lane / kRowLanes;
+    const int c = 2 * (lane % kRowLanes);
+    const u32x4 w = *reinterpret_cast<const u32x4*>(k_arr(slot) + key * kRawRow + (lane % kRowLanes) * 16);
+    const uint32_t dst = lds_address(kmma_arr(slot, par) + key * kRow);
+    *reinterpret_cast<lds_u32x4*>(dst + ((c ^ (key & 15)) * 16)) = dequant8(u32x2{w[0], w[1]}, ks[X]);
+    *reinterpret_cast<lds_u32x4*>(dst + (((c + 1) ^ (key & 15)) * 16)) = dequant8(u32x2{w[2], w[3]}, ks[X]);
+  };
   typedef __attribute__((address_space(3))) uint32_t lds_u32;
   auto store_v = [&](auto slot, auto par) __attribute__((always_inline)) {
-    const char* raw = r_arr(slot) + v_key * kRow + v_chunk * 16;
+    constexpr int X = decltype(slot)::value;
     u32x4 vr[KV];
+    if constexpr (kFp8) {
+      const char* raw = r_arr(slot) + v_key * kRawRow + v_chunk * 8;
 #pragma unroll
-    for (int j = 0; j < KV; ++j) vr[j] = *reinterpret_cast<const u32x4*>(raw + j * kRow);
+      for (int j = 0; j < KV; ++j) vr[j] = dequant8(*reinterpret_cast<const u32x2*>(raw + j * kRawRow), vs[X]);
+    } else {
+      const char* raw = r_arr(slot) + v_key * kRow + v_chunk * 16;
+#pragma unroll
+      for (int j = 0; j < KV; ++j) vr[j] = *reinterpret_cast<const u32x4*>(raw + j * kRow);
+    }
     const uint32_t row0 = lds_address(v_arr(par)) + vt_dst + (vt_chunk & 7) * 16;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -1229,9 +1297,9 @@ __global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedPara
   f32x16 sc0[2], sc1[2];  // scores of even / odd tiles
 
   // S(t) = K(t) Q^T from K slot `slot`, fragments read four MFMAs ahead.
-  auto qk = [&](auto slot, f32x16 (&sc)[2]) __attribute__((always_inline)) {
+  auto qk = [&](auto slot, auto kpar, f32x16 (&sc)[2]) __attribute__((always_inline)) {
     constexpr int kLook = 4;
-    const char* kt = k_arr(slot);
+    const char* kt = kmma_arr(slot, kpar);
     auto k_frag = [&](int i) __attribute__((always_inline)) {
       return *reinterpret_cast<const u32x4*>(kt + (i & 1) * 32 * kRow + k_rd[i >> 1]);
     };
@@ -1296,10 +1364,10 @@ __global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedPara
   constexpr int kMfma = 0x008, kDsRead = 0x100, kVec = 0x002 | 0x400;  // VALU and TRANS
   // Phase A of tile t: S(t + 1) = K(t + 1) Q^T from K slot `slot`, each MFMA paired with
   // one K fragment read (four ahead) and one probability of key block 0 of tile t.
-  auto phase_a = [&](auto slot, f32x16 (&nxt)[2], const f32x16 (&cur)[2], float neg_mu,
+  auto phase_a = [&](auto slot, auto kpar, f32x16 (&nxt)[2], const f32x16 (&cur)[2], float neg_mu,
                      float (&pf)[2][16], float (&ps)[4], u32x4 (&pop)[4]) __attribute__((always_inline)) {
     constexpr int kLook = 4;
-    const char* kt = k_arr(slot);
+    const char* kt = kmma_arr(slot, kpar);
     auto k_frag = [&](int i) __attribute__((always_inline)) {
       return *reinterpret_cast<const u32x4*>(kt + (i & 1) * 32 * kRow + k_rd[i >> 1]);
     };
@@ -1379,9 +1447,13 @@ __global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedPara
   stage(2, page_of(2), I2{});
   int pg[3] = {page_of(3), page_of(4), page_of(5)};  // pg[x]: next tile staged into slot x
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kStageOps) : "memory");
+  if constexpr (kFp8) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // tile 0's scales
+    convert_k(I0{}, I0{});
+  }
   store_v(I0{}, I0{});
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  if (w_nt > 0) qk(I0{}, sc0);
+  if (w_nt > 0) qk(I0{}, I0{}, sc0);
 
   // Step for tile t: X = t % 3 (the slots tile t used, restaged with tile t + 3), Y =
   // (t + 1) % 3 (tile t + 1's slots), P = t & 1 (tile t's score and V^T buffers).
@@ -1396,6 +1468,13 @@ __global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedPara
     // Tile t + 1 has landed for this wave (tiles t + 2 may still be in flight); the
     // barrier publishes it and tile t's V^T, and retires tile t - 1.
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kStageOps) : "memory");
+    if constexpr (kFp8) {
+      // This wave's K rows of tile t + 1, converted before the barrier publishes them
+      // (the buffer's last readers, tile t - 1's scores, finished before the previous
+      // barrier). Tile t + 1's scales were loaded three steps ago.
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      convert_k(IY{}, IQ{});
+    }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     store_v(IY{}, IQ{});
     stage(t + 3, pg[X], xs);
@@ -1410,7 +1489,7 @@ __global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedPara
       // Scores of tile t + 1 even past this wave's last tile (the slot then holds a
       // staged copy of a valid tile; the result goes unused): no branch, so the
       // probabilities stay interleaved with these MFMAs.
-      phase_a(IY{}, nxt, cur, neg_mu, pf, ps, pop);
+      phase_a(IY{}, IQ{}, nxt, cur, neg_mu, pf, ps, pop);
       phase_b(par, cur, neg_mu, pf, ps, pop);
       l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
     }
@@ -1584,7 +1663,7 @@ void launch_prefill_lds(const PagedParams& p, int max_query_len, hipStream_t str
     const dim3 grid(cols, p.num_seqs, qtiles);
     if constexpr (HS == 2) {
       if (!p.pf_register_staging) {
-        paged_prefill_pipe_kernel<TQ><<<grid, 512, 0, stream>>>(p);
+        paged_prefill_pipe_kernel<TQ, TQ><<<grid, 512, 0, stream>>>(p);
         return;
       }
     }
@@ -1603,6 +1682,17 @@ hipError_t launch_prefill_d(const PagedParams& p, int max_query_len, hipStream_t
       } else {
         launch_prefill_lds<TQ, 2>(p, max_query_len, stream);
       }
+      return hipGetLastError();
+    }
+  }
+  // fp8 pools at D = 128, GQA pairs, pages of >= 16 keys, the grid schedule: the
+  // pipelined kernel, codes copied straight into LDS and dequantised there.
+  if constexpr (std::is_same_v<TKV, fp8_t> && D == 128) {
+    if (p.block_shift >= 4 && p.scale > 0.0f && !p.pf_register_staging && p.pf_wgs == 0 &&
+        prefill_item_heads(p.hq / p.hk) == 2) {
+      const int cols = p.hk * (p.hq / p.hk / 2);
+      const int qtiles = (max_query_len + kPrefillQueryTile - 1) / kPrefillQueryTile;
+      paged_prefill_pipe_kernel<TQ, fp8_t><<<dim3(cols, p.num_seqs, qtiles), 512, 0, stream>>>(p);
       return hipGetLastError();
     }
   }

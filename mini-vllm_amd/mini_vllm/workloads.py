@@ -152,11 +152,13 @@ CONFIGS = {
 
 
 def config_batch(index: int, device: torch.device | str = "cpu", seed: int = 0,
-                 generator_device: str = "cpu") -> PagedBatch:
+                 generator_device: str = "cpu", kv_dtype: torch.dtype | None = None) -> PagedBatch:
     """The BASELINE.json config ``index`` (1-4), GQA 16q/8kv, D=128, 16-token pages.
 
     Lengths are drawn from their own generator (seed ``seed``) so the shapes do not
     depend on the tensor draws; pools for configs 2-4 hold the needed pages + 10%.
+    ``kv_dtype=torch.float8_e4m3fn`` with config 3 gives its shape over an fp8 pool
+    quantised per (block, kv head) as config 4's is.
     """
     common = dict(num_q_heads=16, num_kv_heads=8, head_dim=128, block_size=16, seed=seed,
                   device=device, generator_device=generator_device)
@@ -172,7 +174,7 @@ def config_batch(index: int, device: torch.device | str = "cpu", seed: int = 0,
         prefixes = _draw_lengths(seed, 8, 0, 1536)
         contexts = [p + 512 for p in prefixes]
         pages = sum(-(-c // 16) for c in contexts)
-        return build_batch(contexts, [512] * 8, dtype=torch.bfloat16,
+        return build_batch(contexts, [512] * 8, dtype=torch.bfloat16, kv_dtype=kv_dtype,
                            pool_blocks=math.ceil(1.1 * pages), **common)
     if index == 4:
         contexts = _draw_lengths(seed, 128, 2048, 8192)

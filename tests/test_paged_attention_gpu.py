@@ -181,6 +181,17 @@ def test_prefill_schedules_in_a_mixed_fp8_batch(extension, device, schedule):
     check(extension, b, dtype=torch.float8_e4m3fn, options=_prefill_schedule(schedule))
 
 
+@pytest.mark.parametrize("block_size", [16, 32, 64])
+def test_fp8_prefill_on_the_pipelined_grid_kernel(extension, device, block_size):
+    """fp8 pools on the grid schedule take the pipelined kernel (codes staged straight
+    into LDS, dequantised there with each page's scale): ragged prefixes, partial last
+    tiles, a decode row, pages of 16 to 64 keys."""
+    b = case([1500, 700, 130, 65, 3000], [512, 300, 130, 1, 200], device, dtype=torch.bfloat16,
+             kv_dtype=torch.float8_e4m3fn, num_q_heads=16, num_kv_heads=8, head_dim=128,
+             block_size=block_size)
+    check(extension, b, dtype=torch.float8_e4m3fn, options={"prefill_schedule": "grid"})
+
+
 @pytest.mark.parametrize("schedule", ["stream", "grid"])
 @pytest.mark.parametrize("scale", [-0.3, 0.0, 2.0])
 def test_prefill_with_unusual_scales(extension, device, scale, schedule):
@@ -328,6 +339,16 @@ def test_config3_chunked_prefill_full_size(extension, device):
     b = config_batch(3, device=device)
     assert prefill_flops(b) > 1e10
     check(extension, b, msg="config 3")
+
+
+@pytest.mark.slow
+def test_config3_chunked_prefill_over_an_fp8_pool_full_size(extension, device):
+    """Config 3's shape (8 x 512-token chunks after prefixes U[0,1536]) over an fp8 pool
+    quantised per (block, kv head), every row against the oracle's dequantise-then-dense
+    path at the fp8 tolerance."""
+    b = config_batch(3, device=device, kv_dtype=torch.float8_e4m3fn)
+    assert b.key_pool.dtype == torch.float8_e4m3fn and prefill_flops(b) > 1e10
+    check(extension, b, msg="config 3, fp8 pool")
 
 
 @pytest.mark.slow
