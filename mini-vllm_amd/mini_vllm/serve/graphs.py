@@ -13,7 +13,11 @@ fixed, so one captured graph serves every decode step of a given shape:
   the block-table width is rounded up to a multiple of 64 pages;
 * before a replay, the iteration's metadata is packed into one pinned host buffer and
   copied into the graph's static input tensors with one host-to-device copy;
-* sampling (argmax) runs after the replay, outside the graph.
+* sampling (argmax) runs after the replay, outside the graph; :meth:`DecodeGraphs.keep`
+  stores the sampled tokens in a device buffer every graph reads, and a sequence that
+  was in the previous replay takes its next input token from there (the graph gathers
+  it by the row the sequence had), so the host need not have read that token yet: the
+  engine schedules and packs the next decode step while the GPU runs this one.
 
 The paged-attention plan in stream mode depends only on the batch size and the bound on
 max_context_len, so the kernels launched inside a graph stay valid for every replay;
@@ -33,20 +37,26 @@ TABLE_QUANTUM = 64  # pages
 
 
 class _Captured:
-    def __init__(self, model, batch_size: int, width: int, dummy_block: int, device) -> None:
+    def __init__(self, model, batch_size: int, width: int, dummy_block: int, device,
+                 prev_tokens: torch.Tensor) -> None:
         p = model.manager.block_size
         self.batch_size, self.width = batch_size, width
         b = batch_size
         i32 = dict(dtype=torch.int32, device=device)
         i64 = dict(dtype=torch.int64, device=device)
-        # Dynamic inputs: [ids | positions] int64 and [context | slots | tables] int32.
-        self.dyn64 = torch.zeros(2 * b, **i64)
+        # Dynamic inputs: [ids | positions | gather rows] int64 and [context | slots |
+        # tables] int32. Row i's input token is prev_tokens[gather[i]] when gather[i] >= 0
+        # (the token sampled for it by the previous replay, still on the device), else
+        # ids[i] from the host.
+        self.dyn64 = torch.zeros(3 * b, **i64)
         self.dyn32 = torch.zeros(2 * b + b * width, **i32)
-        self.host64 = torch.zeros(2 * b, dtype=torch.int64, pin_memory=True)
+        self.host64 = torch.zeros(3 * b, dtype=torch.int64, pin_memory=True)
         self.host32 = torch.zeros(2 * b + b * width, dtype=torch.int32, pin_memory=True)
+        self.prev_tokens = prev_tokens
+        self.input_ids = torch.zeros(b, **i64)
         self.batch = ForwardBatch(
-            input_ids=self.dyn64[:b],
-            positions=self.dyn64[b:],
+            input_ids=self.input_ids,
+            positions=self.dyn64[b:2 * b],
             cu_seqlens_q=torch.arange(b + 1, **i32),
             seq_lens=torch.ones(b, **i32),
             context_lens=self.dyn32[:b],
@@ -69,15 +79,17 @@ class _Captured:
         self.np32 = self.host32.numpy()
         self.row_keys: list = [()] * b
 
-    def fill(self, scheduled) -> None:
+    def fill(self, scheduled, gather: list[int] | None = None) -> None:
         b, w, p = self.batch_size, self.width, self.model.manager.block_size
         manager = self.model.manager
-        ids, pos = self.np64[:b], self.np64[b:]
+        ids, pos, rows = self.np64[:b], self.np64[b:2 * b], self.np64[2 * b:]
         ctx, slots = self.np32[:b], self.np32[b:2 * b]
         tables = self.np32[2 * b:].reshape(b, w)
         for i, (seq, _) in enumerate(scheduled):
             start = seq.num_computed_tokens
-            ids[i] = seq.tokens(start, 1)[0]
+            rows[i] = gather[i] if gather is not None else -1
+            # a gathered row's token may not have reached the host yet
+            ids[i] = seq.tokens(start, 1)[0] if rows[i] < 0 else 0
             pos[i] = start
             ctx[i] = start + 1
             table = manager.table(seq.seq_id)
@@ -88,6 +100,7 @@ class _Captured:
                 tables[i, len(table):] = PADDING_BLOCK
                 self.row_keys[i] = key
         for i in range(len(scheduled), b):
+            rows[i] = -1
             if self.row_keys[i] is not None:
                 ids[i], pos[i], ctx[i], slots[i] = 0, 0, 1, self.dummy_block * p
                 tables[i, 0] = self.dummy_block
@@ -96,6 +109,16 @@ class _Captured:
         self.dyn64.copy_(self.host64, non_blocking=True)
         self.dyn32.copy_(self.host32, non_blocking=True)
 
+    def _gather_inputs(self) -> None:
+        b = self.batch_size
+        host_ids, rows = self.dyn64[:b], self.dyn64[2 * b:]
+        prev = self.prev_tokens.index_select(0, rows.clamp(min=0))
+        self.input_ids.copy_(torch.where(rows >= 0, prev, host_ids))
+
+    def _forward(self) -> torch.Tensor:
+        self._gather_inputs()
+        return self.model(self.batch)
+
     def capture(self) -> None:
         # Warm up on a side stream (allocator pools, BLAS handles, the kernels' per-stream
         # workspaces), then capture on that same stream.
@@ -103,12 +126,12 @@ class _Captured:
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
             for _ in range(2):
-                self.model(self.batch)
+                self._forward()
         torch.cuda.current_stream().wait_stream(side)
         self.graph = torch.cuda.CUDAGraph()
         recorder = _workspace_recorder(self.model)
         with recorder as workspaces, torch.cuda.graph(self.graph, stream=side):
-            self.logits = self.model(self.batch)
+            self.logits = self._forward()
         self.workspaces = list(workspaces)
 
 
@@ -144,24 +167,42 @@ class DecodeGraphs:
         self.dummy_block = manager.table(self._dummy_id)[0]
         self.graphs: dict[tuple[int, int], _Captured] = {}
         self.replays = 0
+        # Tokens sampled by the last replay (row i: sequence prev_rows' key with value i),
+        # read by the next replay's gather.
+        self.prev_tokens = torch.zeros(max(BUCKETS), dtype=torch.int64, device=self.device)
+        self.prev_rows: dict[int, int] = {}
 
     def supports(self, scheduled) -> bool:
         return 0 < len(scheduled) <= self.max_batch and all(n == 1 for _, n in scheduled)
 
     def run(self, scheduled) -> torch.Tensor:
-        """Logits ``len(scheduled) x V`` for a pure-decode iteration."""
+        """Logits ``len(scheduled) x V`` for a pure-decode iteration. A sequence that was
+        in the previous replay, and whose token from it was handed to :meth:`keep`, reads
+        that token on the device."""
         n = len(scheduled)
         bucket = next(b for b in BUCKETS if b >= n)
         widest = max(len(self.model.manager.table(s.seq_id)) for s, _ in scheduled)
         width = -(-widest // TABLE_QUANTUM) * TABLE_QUANTUM
         key = (bucket, width)
+        gather = [self.prev_rows.get(s.seq_id, -1) for s, _ in scheduled]
         entry = self.graphs.get(key)
         if entry is None:
-            entry = _Captured(self.model, bucket, width, self.dummy_block, self.device)
-            entry.fill(scheduled)
+            entry = _Captured(self.model, bucket, width, self.dummy_block, self.device,
+                              self.prev_tokens)
+            entry.fill(scheduled, gather)
             entry.capture()
             self.graphs[key] = entry
-        entry.fill(scheduled)
+        entry.fill(scheduled, gather)
         entry.graph.replay()
         self.replays += 1
         return entry.logits[:n]
+
+    def keep(self, scheduled, tokens: torch.Tensor) -> None:
+        """The tokens just sampled for ``scheduled`` (device, one per row): the next
+        replay gathers its inputs from them."""
+        self.prev_tokens[: len(scheduled)].copy_(tokens)
+        self.prev_rows = {s.seq_id: i for i, (s, _) in enumerate(scheduled)}
+
+    def invalidate(self) -> None:
+        """An iteration ran outside the graphs: no device-held token is current."""
+        self.prev_rows = {}
