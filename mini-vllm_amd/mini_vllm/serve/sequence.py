@@ -9,6 +9,8 @@ from __future__ import annotations
 
 from dataclasses import dataclass, field
 
+from mini_vllm.sampler import GREEDY, SamplingParams
+
 __all__ = ["Sequence"]
 
 
@@ -20,6 +22,7 @@ class Sequence:
     output: list[int] = field(default_factory=list)
     num_computed_tokens: int = 0
     preemptions: int = 0
+    params: SamplingParams = GREEDY  # how its tokens are drawn (reference sequence.py)
 
     @property
     def token_ids(self) -> list[int]:

@@ -157,3 +157,30 @@ def test_two_long_prompts_do_not_evict_each_other_forever(num_blocks):
     assert not sched.has_work, "the scheduler did not finish"
     assert preempted > 0 and all(len(s.output) == 8 for s in seqs)
     manager.check_no_leaks()
+
+
+def test_sampled_requests_are_reproducible_and_greedy_ones_unchanged(model):
+    """Requests with their own sampling parameters beside greedy ones (reference
+    serve/engine.py:252-330): the greedy requests still equal the dense recompute,
+    the sampled ones repeat exactly under the same generator seed and differ under
+    another, and every token is in the vocabulary."""
+    from mini_vllm.sampler import SamplingParams
+
+    config, weights = model
+    ps = prompts(6, 3, 30, config.vocab_size, seed=1)
+    hot = SamplingParams(temperature=1.5, top_k=50, top_p=0.95)
+    params = [None, hot, None, hot, SamplingParams(temperature=0.0), hot]
+
+    def run(seed):
+        engine = make_engine(config, weights)
+        engine.generator = torch.Generator().manual_seed(seed)
+        return engine.generate(ps, MAX_TOKENS, params)
+
+    first, again, other = run(5), run(5), run(6)
+    assert first == again and first != other
+    for i in (0, 2, 4):
+        tok, logits = generate_greedy(config, weights, ps[i], MAX_TOKENS)
+        assert_tokens_match(first[i], tok, logits, tie_tol=1e-4, msg=f"greedy request {i}")
+    assert all(0 <= t < config.vocab_size for g in first for t in g)
+    with pytest.raises(ValueError, match="sampling params"):
+        make_engine(config, weights).generate(ps, 2, [hot])

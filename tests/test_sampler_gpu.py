@@ -57,3 +57,71 @@ def test_strided_rows_and_ops_dispatch(extension, device):
     assert torch.equal(ops.argmax(xd, use_cuda=True), xd.argmax(dim=-1))
     with pytest.raises(RuntimeError, match="contiguous rows"):
         extension.argmax(base.t())
+
+
+# ------------------------------------------------- temperature / top-k / top-p
+
+
+def _oracle_probs(logits, params):
+    from oracle import sampler as osm
+
+    return torch.from_numpy(osm.sampling_probabilities(
+        logits.float().cpu().numpy(), params.temperature, params.top_k, params.top_p)).float()
+
+
+@pytest.mark.parametrize("params", [
+    "greedy", "t1", "t0.7_k50", "t1.2_p0.9", "t0.8_k8_p0.9", "p1e-6"])
+def test_device_sampling_probabilities_match_the_oracle(device, params):
+    """At the Qwen3 vocabulary (151936) with bf16 logits, on the device, against the
+    float64 oracle (ties, which bf16 logits make common, in vocabulary order on both
+    sides)."""
+    from mini_vllm.sampler import SamplingParams, sampling_probabilities
+
+    sp = {"greedy": SamplingParams(temperature=0.0), "t1": SamplingParams(),
+          "t0.7_k50": SamplingParams(temperature=0.7, top_k=50),
+          "t1.2_p0.9": SamplingParams(temperature=1.2, top_p=0.9),
+          "t0.8_k8_p0.9": SamplingParams(temperature=0.8, top_k=8, top_p=0.9),
+          "p1e-6": SamplingParams(top_p=1e-6)}[params]
+    gen = torch.Generator().manual_seed(17)
+    logits = (torch.randn(8, 151936, generator=gen) * 3).to(torch.bfloat16).to(device)
+    got = sampling_probabilities(logits, sp)
+    assert got.is_cuda and got.dtype == torch.float32
+    want = _oracle_probs(logits, sp)
+    assert torch.equal(got.cpu() > 0, want > 0), "kept sets differ"
+    assert torch.allclose(got.cpu(), want, rtol=1e-4, atol=1e-7)
+
+
+def test_device_draws_are_reproducible_under_a_cuda_generator(device):
+    from mini_vllm.sampler import SamplingParams, sample, sampling_probabilities
+
+    logits = torch.randn(32, 151936, device=device, dtype=torch.bfloat16)
+    rows = [SamplingParams(temperature=0.0), SamplingParams(temperature=1.0, top_k=40, top_p=0.9)] * 16
+    kept = sampling_probabilities(logits, rows) > 0
+    draws = []
+    for seed in (3, 3, 4):
+        g = torch.Generator(device=device).manual_seed(seed)
+        draws.append(sample(logits, rows, generator=g))
+    assert torch.equal(draws[0], draws[1]) and not torch.equal(draws[0], draws[2])
+    for d in draws:
+        assert d.is_cuda and bool(kept[torch.arange(32, device=device), d].all())
+        assert torch.equal(d[0::2], logits[0::2].argmax(-1))
+
+
+def test_device_draw_frequencies_follow_the_distribution(device):
+    """20000 draws of one 8-token row at temperature 0.8 with top-k 6: every kept
+    token's frequency within 4 standard errors of its probability, none outside."""
+    import math
+
+    from mini_vllm.sampler import SamplingParams, sample, sampling_probabilities
+
+    draws = 20000
+    row = torch.tensor([[2.0, 1.5, 1.0, 0.5, 0.0, -0.5, -1.0, -2.0]], device=device)
+    sp = SamplingParams(temperature=0.8, top_k=6)
+    p = sampling_probabilities(row, sp)[0].cpu()
+    tokens = sample(row.expand(draws, -1).contiguous(), sp,
+                    generator=torch.Generator(device=device).manual_seed(0))
+    freq = torch.bincount(tokens.cpu(), minlength=8).double() / draws
+    assert float(freq[6:].sum()) == 0.0
+    for t in range(6):
+        se = math.sqrt(float(p[t]) * (1 - float(p[t])) / draws)
+        assert abs(float(freq[t]) - float(p[t])) < 4 * se, f"token {t}"
