@@ -301,6 +301,42 @@ def run_linear(steps: int = 20) -> dict:
     return out
 
 
+def run_prefill_gemm(steps: int = 20, tokens: int = 2048) -> dict:
+    """The four projections of a config-5 prefill iteration (2048 tokens, Qwen3-0.6B
+    shapes, bf16, fp32 accumulate) as the model runs them (``ops.linear``: the vendor
+    BLAS while the hand-written MFMA GEMM is held back as slower), and each of the two
+    paths on every shape. Four weight copies rotated; timed as graph replays of
+    back-to-back calls. FLOPs = 2 M N K."""
+    from mini_vllm.kernels import ops
+    from mini_vllm.kernels.extension import load_extension
+
+    ext = load_extension()
+    bf = torch.bfloat16
+    shapes = {"qkv": (4096, 1024), "o": (1024, 2048), "gate_up": (6144, 1024), "down": (1024, 3072)}
+    out = {}
+    for name, (n, k) in shapes.items():
+        ws = [torch.randn(n, k, device="cuda", dtype=bf) * 0.02 for _ in range(4)]
+        x = torch.randn(tokens, k, device="cuda", dtype=bf)
+        flop = 2 * tokens * n * k
+        ms = graph_time(lambda i: ops.linear(x, ws[i % 4], use_cuda=True), steps)
+        gemm_ms = graph_time(lambda i: ext.gemm(x, ws[i % 4]), steps)
+        blas_ms = graph_time(lambda i: x @ ws[i % 4].t(), steps)
+        tflops = flop / (ms * 1e-3) / 1e12
+        out[name] = {"m": tokens, "n": n, "k": k, "us": round(ms * 1e3, 1),
+                     "tflops": round(tflops, 1),
+                     "frac_of_bf16_mfma_peak": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4),
+                     "path": "blas" if "gemm" in ops.NOT_YET_FASTER else "gemm",
+                     "gemm_us": round(gemm_ms * 1e3, 1),
+                     "gemm_tflops": round(flop / (gemm_ms * 1e-3) / 1e12, 1),
+                     "blas_us": round(blas_ms * 1e3, 1),
+                     "blas_tflops": round(flop / (blas_ms * 1e-3) / 1e12, 1)}
+        log(f"prefill gemm {name} ({tokens}x{n}x{k}): {ms * 1e3:.1f} us, {tflops:.0f} TFLOP/s "
+            f"(hand GEMM {gemm_ms * 1e3:.1f} us, BLAS {blas_ms * 1e3:.1f} us)")
+        del ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def run_elementwise(steps: int = 20) -> dict:
     """RMSNorm (E=1024 and per-head D=128), RoPE (16 heads x 128) and SwiGLU (I=3072)
     at bf16 on ~256 MB operands, three rotated copies each so every call reads HBM.
@@ -489,13 +525,13 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--copies", type=int, default=3, help="rotated pool copies (defeat the MALL)")
     parser.add_argument("--skip-extras", action="store_true", help="headline config 2 only")
-    parser.add_argument("--extras", default="3,3fp8,4,5,ew,kv,dense,linear,copy",
+    parser.add_argument("--extras", default="3,3fp8,4,5,ew,kv,dense,linear,gemm,copy",
                         help="comma list of extras to run: 3 (prefill), 3fp8 (prefill over an "
                              "fp8 pool), 4 (fp8 decode), "
                              "5 (engine), 5small (engine, 64 x 128 tokens), 5fp8 (engine, fp8 "
                              "KV cache), ew (elementwise "
                              "kernels), kv (KV write), dense (dense-cache attention), linear "
-                             "(decode projections and argmax), copy")
+                             "(decode projections and argmax), gemm (prefill projections), copy")
     parser.add_argument("--no-cpu", action="store_true")
     args = parser.parse_args()
 
@@ -577,6 +613,8 @@ def main() -> int:
         extras["dense_attention"] = run_dense()
     if "linear" in wanted:
         extras["decode_projections"] = run_linear()
+    if "gemm" in wanted:
+        extras["prefill_projections"] = run_prefill_gemm()
     if "5" in wanted:
         log("config 5: Qwen3-0.6B-shaped engine, 256 requests x 256 tokens")
         extras["config5_engine"] = run_engine()

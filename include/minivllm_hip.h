@@ -352,6 +352,15 @@ int mvllm_linear_swiglu(void* y, const void* x, const void* w_gate_up, int64_t m
                         int64_t k, int32_t dtype, void* workspace, uint64_t workspace_bytes,
                         void* stream);
 
+/* y [m, n] = x [m, k] w [n, k]^T for prefill-sized x (any m), all row-major and
+ * contiguous, 16-byte aligned, fp16 or bf16 (dtype), fp32 accumulation and one rounding;
+ * n and k multiples of 64. Replaces the BLAS matmul the reference's projections run
+ * through at prefill sizes (model/basics.py linear, called from model/qwen3_paged.py:71-95,
+ * 110 and 141-143): the q/k/v, o, gate/up and down projections of a prefill chunk.
+ * Unserved shapes return MVLLM_ERR_UNSUPPORTED before any launch. */
+int mvllm_gemm(void* y, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
+               int32_t dtype, void* stream);
+
 /* h_out = residual + x w^T (rounded as mvllm_linear_residual) and normed = RMSNorm(h_out)
  * with norm_weight and eps (rounded as mvllm_rmsnorm: bit for bit the two entries in
  * sequence), h_out, normed, residual [m, n], norm_weight [n]: the o and down projections

@@ -18,6 +18,7 @@
 #include "dense.hpp"
 #include "elementwise.hpp"
 #include "kv_write.hpp"
+#include "gemm.hpp"
 #include "linear.hpp"
 #include "sampler.hpp"
 #include "paged_attention.hpp"
@@ -450,7 +451,7 @@ extern "C" {
 
 const char* mvllm_last_error(void) { return g_error; }
 
-int mvllm_abi_version(void) { return 8; }
+int mvllm_abi_version(void) { return 9; }
 
 #ifndef MVLLM_SOURCE_HASH
 #define MVLLM_SOURCE_HASH "unstamped"
@@ -1104,6 +1105,32 @@ int mvllm_linear_residual_rmsnorm(void* h_out, void* normed, const void* x, cons
                         h_out, normed, x, w, residual, norm_weight, m, n, k, eps, dtype, workspace,
                         static_cast<hipStream_t>(stream)),
                     "linear_residual_rmsnorm: launch");
+}
+
+int mvllm_gemm(void* y, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
+               int32_t dtype, void* stream) {
+  g_error[0] = '\0';
+  if (m < 0 || n < 0 || k < 0) return fail(MVLLM_ERR_INVALID, "gemm: negative size");
+  if (m == 0 || n == 0) return MVLLM_OK;
+  if (dtype != mvllm::kF16 && dtype != mvllm::kBF16) {
+    return fail(MVLLM_ERR_UNSUPPORTED, "gemm: dtype code %d is not served; fp16 or bf16", dtype);
+  }
+  if (x == nullptr || w == nullptr || y == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "gemm: a required pointer is NULL");
+  }
+  if (!mvllm::gemm_supported(dtype, m, n, k)) {
+    return fail(MVLLM_ERR_UNSUPPORTED,
+                "gemm: shape M=%lld N=%lld K=%lld is not served; N and K must be multiples of "
+                "64 and every operand under 2 GiB",
+                static_cast<long long>(m), static_cast<long long>(n), static_cast<long long>(k));
+  }
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+       reinterpret_cast<uintptr_t>(y)) % 16 != 0) {
+    return fail(MVLLM_ERR_INVALID, "gemm: x, w and y must be 16-byte aligned");
+  }
+  return hip_status(mvllm::launch_gemm(y, x, w, m, n, k, dtype, device_cus(), -1,
+                                       static_cast<hipStream_t>(stream)),
+                    "gemm: launch");
 }
 
 int mvllm_kv_write(void* key_pool, void* value_pool, float* k_scales, float* v_scales,

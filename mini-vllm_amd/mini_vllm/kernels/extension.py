@@ -60,7 +60,7 @@ HIP_FLAGS = [
 # reference's PyTorch expressions round, so FMA contraction is off there.
 EXTRA_FLAGS = {"elementwise.hip": ["-ffp-contract=off"], "linear.hip": ["-ffp-contract=off"]}
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 DTYPE_CODES: dict[torch.dtype, int] = {
     torch.float32: 0,
@@ -285,6 +285,8 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_linear_swiglu.argtypes = [p, p, p, i64, i64, i64, i32, p, u64, p]
     lib.mvllm_linear_residual_rmsnorm.restype = ctypes.c_int
     lib.mvllm_linear_residual_rmsnorm.argtypes = [p, p, p, p, p, p, i64, i64, i64, f32, i32, p, u64, p]
+    lib.mvllm_gemm.restype = ctypes.c_int
+    lib.mvllm_gemm.argtypes = [p, p, p, i64, i64, i64, i32, p]
 
 
 EXPORTED_SYMBOLS = (
@@ -314,6 +316,7 @@ EXPORTED_SYMBOLS = (
     "mvllm_linear_split",
     "mvllm_linear_residual",
     "mvllm_linear_swiglu",
+    "mvllm_gemm",
 )
 
 
@@ -747,6 +750,32 @@ class HipExtension:
             norm_weight.data_ptr(), x.shape[0], n, x.shape[1], float(eps), DTYPE_CODES[x.dtype],
             *self._linear_ws(x, n), _stream(x.device)))
         return h, normed
+
+    def gemm_supported(self, x: torch.Tensor, w: torch.Tensor) -> bool:
+        """Whether :meth:`gemm` serves ``x @ w.T``: 2-D, contiguous, 16-byte aligned,
+        fp16 / bf16 of one dtype, N and K multiples of 64, each operand under 2 GiB."""
+        if (x.dim() != 2 or w.dim() != 2 or x.dtype != w.dtype
+                or x.dtype not in (torch.float16, torch.bfloat16) or x.shape[1] != w.shape[1]
+                or not x.is_contiguous() or not w.is_contiguous()
+                or (x.data_ptr() | w.data_ptr()) % 16):
+            return False
+        m, k = x.shape
+        n = w.shape[0]
+        return (m >= 1 and n >= 64 and n % 64 == 0 and k >= 64 and k % 64 == 0
+                and 2 * m * k < 2**31 and 2 * n * k < 2**31 and m * n < 2**31)
+
+    def gemm(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        """``x @ w.T`` for prefill-sized ``x`` [M, K] against a row-major weight [N, K]:
+        the MFMA GEMM (fp32 accumulation, one rounding to x's dtype)."""
+        if not self.gemm_supported(x, w):
+            raise RuntimeError(f"gemm: x {tuple(x.shape)} {x.dtype} and w {tuple(w.shape)} "
+                               f"{w.dtype} are not served (2-D contiguous 16-byte aligned fp16 or "
+                               "bf16 of one dtype, N and K multiples of 64)")
+        y = torch.empty((x.shape[0], w.shape[0]), dtype=x.dtype, device=x.device)
+        self._check(self.lib.mvllm_gemm(y.data_ptr(), x.data_ptr(), w.data_ptr(), x.shape[0],
+                                        w.shape[0], x.shape[1], DTYPE_CODES[x.dtype],
+                                        _stream(x.device)))
+        return y
 
     def qk_norm_rope_supported(self, dtype: torch.dtype, head_dim: int) -> bool:
         """Whether the fused kernel serves this dtype / head dim (16-byte chunks per head

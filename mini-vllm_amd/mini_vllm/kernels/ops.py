@@ -82,10 +82,16 @@ CUDA_KERNELS: dict[str, tuple[bool, str]] = {
     "kv_write": (True, "csrc/kv_write.hip"),
     "qk_norm_rope": (True, "csrc/elementwise.hip"),
     "linear": (True, "csrc/linear.hip (at most 64 rows; vendor BLAS above)"),
+    "gemm": (True, "csrc/gemm.hip (prefill-sized projections)"),
 }
 
 # Kernels that exist but are deliberately not dispatched, with the reason.
-NOT_YET_FASTER: dict[str, str] = {}
+NOT_YET_FASTER: dict[str, str] = {
+    "gemm": ("csrc/gemm.hip (prefill projections): measured on random bf16 data at M = 2048 "
+             "slower than the vendor BLAS on every Qwen3-0.6B projection (q/k/v 26.4 us vs "
+             "21.4, o 17.5 vs 15.5, gate/up 45.5 vs 28.5, down 23.3 vs 20.8); prefill "
+             "projections stay on the BLAS"),
+}
 
 MAX_PAGED_HEAD_DIM = 256
 PAGED_HEAD_DIMS = (32, 64, 128, 256)
@@ -330,19 +336,36 @@ def _skinny_ext(x: torch.Tensor, w: PackedWeight, n: int, use_cuda: bool):
     return ext if ext.linear_supported(x, w.packed, n) else None
 
 
+def _gemm(x: torch.Tensor, dense: torch.Tensor, use_cuda: bool) -> torch.Tensor | None:
+    """``x @ dense.T`` on the prefill GEMM (``csrc/gemm.hip``) when it is dispatched
+    (not held back in NOT_YET_FASTER) and serves the shape (device fp16/bf16, N and K
+    multiples of 64, contiguous), else None: the caller takes the vendor BLAS, a size
+    dispatch between two device paths (a CPU tensor with ``use_cuda=True`` is recorded
+    by the skinny op's gate instead)."""
+    if "gemm" in NOT_YET_FASTER or not (use_cuda and x.is_cuda and x.dim() == 2):
+        return None
+    ext = load_extension()
+    return ext.gemm(x, dense) if ext.gemm_supported(x, dense) else None
+
+
 def linear(x: torch.Tensor, w: torch.Tensor | PackedWeight, use_cuda: bool = False) -> torch.Tensor:
     """``x @ w.T`` (no bias), the projections of model/basics.py ``linear``.
 
-    Kernel: ``csrc/linear.hip`` for decode-sized ``x`` (at most 64 rows of f16/bf16, K a
+    Kernels: ``csrc/linear.hip`` for decode-sized ``x`` (at most 64 rows of f16/bf16, K a
     multiple of 64) against a :class:`PackedWeight`: a weight-bandwidth-bound skinny
-    GEMM. Larger ``x`` (prefill chunks) is a real GEMM and goes to the vendor BLAS
-    through torch, as every projection does in the reference; that is a dispatch by
-    size, both paths on the device. A plain tensor weight always takes the BLAS.
+    GEMM; ``csrc/gemm.hip`` for larger ``x`` (prefill chunks: an MFMA GEMM over the
+    row-major weight, N and K multiples of 64). Other shapes take the vendor BLAS
+    through torch, as every projection does in the reference: a dispatch by size, all
+    paths on the device.
     """
     dense = w.dense if isinstance(w, PackedWeight) else w
     ext = _skinny_ext(x, w, dense.shape[0], use_cuda)
     if ext is not None:
         return ext.linear(x, w.packed, dense.shape[0])
+    if not skinny(x, use_cuda):
+        y = _gemm(x, dense, use_cuda)
+        if y is not None:
+            return y
     return x @ dense.t()
 
 
@@ -365,7 +388,8 @@ def linear_split(x: torch.Tensor, w: PackedWeight, sizes: tuple[int, ...],
     ext = _skinny_ext(x, w, w.shape[0], use_cuda)
     if ext is not None and len(sizes) <= 3 and all(s % 32 == 0 for s in sizes[:-1]):
         return ext.linear_split(x, w.packed, tuple(sizes))
-    parts = (x @ w.dense.t()).split(list(sizes), dim=-1)
+    y = None if skinny(x, use_cuda) else _gemm(x, w.dense, use_cuda)
+    parts = (y if y is not None else x @ w.dense.t()).split(list(sizes), dim=-1)
     return parts if views else tuple(t.contiguous() for t in parts)
 
 
@@ -376,7 +400,7 @@ def linear_residual(x: torch.Tensor, w: PackedWeight, residual: torch.Tensor,
     ext = _skinny_ext(x, w, w.shape[0], use_cuda)
     if ext is not None and residual.is_contiguous() and residual.dtype == x.dtype:
         return ext.linear_residual(x, w.packed, residual)
-    return residual + x @ w.dense.t()
+    return residual + linear(x, w.dense, use_cuda=use_cuda)
 
 
 def linear_residual_rmsnorm(x: torch.Tensor, w: PackedWeight, residual: torch.Tensor,
@@ -402,7 +426,7 @@ def linear_swiglu(x: torch.Tensor, w_gate_up: PackedWeight, use_cuda: bool = Fal
     ext = _skinny_ext(x, w_gate_up, n, use_cuda)
     if ext is not None and n % 32 == 0:
         return ext.linear_swiglu(x, w_gate_up.packed, n // 2)
-    y = x @ w_gate_up.dense.t()
+    y = linear(x, w_gate_up.dense, use_cuda=use_cuda)
     if _use_kernel("swiglu", use_cuda, y) and y.dim() == 2 and n % 32 == 0:
         # prefill-sized: SwiGLU straight off the interleaved product, no gate/up copies
         return load_extension().swiglu_interleaved(y)
