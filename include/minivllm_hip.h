@@ -58,9 +58,12 @@ const char* mvllm_build_id(void);
 #define MVLLM_DECODE_STREAM 1 /* persistent workgroups, equal shares of all decode keys */
 #define MVLLM_DECODE_GRID 2   /* one workgroup per (sequence, split) */
 #define MVLLM_DECODE_BY_ROW 3 /* one workgroup per (query row, split), prefill rows too */
+#define MVLLM_DECODE_HEADS 4  /* one workgroup per (sequence, head unit), its waves splitting
+                                 the keys; no partials */
 typedef struct mvllm_paged_plan {
   int32_t decode_mode;       /* MVLLM_DECODE_* */
-  int32_t decode_workgroups; /* stream: workgroups launched; grid modes: split-axis extent */
+  int32_t decode_workgroups; /* stream, heads: workgroups launched; grid modes: split-axis
+                                extent */
   int32_t split_tokens;      /* grid modes: keys per split */
   int32_t prefill_mfma;      /* 1: prefill rows go to the MFMA prefill kernel */
   uint64_t workspace_bytes;  /* split partials and their index; 0 when none are needed */
@@ -75,14 +78,19 @@ typedef struct mvllm_paged_plan {
  * planner's own choice. The library reads no environment: the schedule depends on
  * the sizes, the device's CU count and these options only. */
 typedef struct mvllm_plan_options {
-  int32_t decode_schedule;     /* 0 auto; MVLLM_DECODE_STREAM or MVLLM_DECODE_GRID forces one */
+  int32_t decode_schedule;     /* 0 auto; MVLLM_DECODE_STREAM, MVLLM_DECODE_GRID or
+                                  MVLLM_DECODE_HEADS forces one */
   int32_t decode_wgs_per_cu;   /* stream decode: workgroups per CU (default 1) */
-  int32_t decode_waves_per_cu; /* grid decode: waves per CU the splits aim for (default 16) */
+  int32_t decode_waves_per_cu; /* grid decode: waves per CU the splits aim for (default 16);
+                                  heads decode: waves per workgroup, 4 or 8 (default 8) */
   int32_t decode_split_tokens; /* grid decode: keys per split (default from the wave target) */
   int32_t prefill_schedule;    /* 0 auto; 1 forces the stream schedule, 2 the grid */
   int32_t prefill_wgs_per_cu;  /* stream prefill: workgroups per CU (default 1) */
   int32_t prefill_staging;     /* 0 auto (direct-to-LDS copies where served); 1 forces the
                                   register-staged prefill kernel */
+  int32_t prefill_share_tiles; /* stream prefill: fewest 64-key tiles per workgroup share
+                                  while a quarter of the workgroups stay busy (default 4):
+                                  small work uses fewer workgroups */
   int32_t reserved;            /* must be 0 */
 } mvllm_plan_options;
 

@@ -64,27 +64,41 @@ struct Options {
   int decode_schedule = 0;
   int decode_wgs_per_cu = 1;
   int decode_waves_per_cu = 16;
+  int heads_waves = 8;
   int decode_split_tokens = 0;
   int prefill_schedule = 0;
   int prefill_wgs_per_cu = 1;
+  int prefill_share_tiles = mvllm::kPrefillShareTiles;
   int prefill_staging = 0;
 };
 
 int read_options(const mvllm_plan_options* o, Options& out) {
   out = Options{};
   if (o == nullptr) return MVLLM_OK;
-  if (o->decode_schedule < 0 || o->decode_schedule > MVLLM_DECODE_GRID ||
+  if (o->decode_schedule < 0 || o->decode_schedule > MVLLM_DECODE_HEADS ||
+      o->decode_schedule == MVLLM_DECODE_BY_ROW ||
       o->prefill_schedule < 0 || o->prefill_schedule > 2 || o->prefill_staging < 0 ||
       o->prefill_staging > 1 || o->decode_wgs_per_cu < 0 || o->decode_waves_per_cu < 0 ||
-      o->decode_split_tokens < 0 || o->prefill_wgs_per_cu < 0 || o->reserved != 0) {
+      o->decode_split_tokens < 0 || o->prefill_wgs_per_cu < 0 || o->prefill_share_tiles < 0 ||
+      o->reserved != 0) {
     return fail(MVLLM_ERR_INVALID, "paged_attention: plan options out of range");
   }
   out.decode_schedule = o->decode_schedule;
   if (o->decode_wgs_per_cu > 0) out.decode_wgs_per_cu = o->decode_wgs_per_cu;
   if (o->decode_waves_per_cu > 0) out.decode_waves_per_cu = o->decode_waves_per_cu;
+  if (o->decode_schedule == MVLLM_DECODE_HEADS && o->decode_waves_per_cu > 0) {
+    if (o->decode_waves_per_cu != 4 && o->decode_waves_per_cu != 8) {
+      return fail(MVLLM_ERR_INVALID,
+                  "paged_attention: the heads decode schedule takes 4 or 8 waves per "
+                  "workgroup, got %d",
+                  o->decode_waves_per_cu);
+    }
+    out.heads_waves = o->decode_waves_per_cu;
+  }
   out.decode_split_tokens = o->decode_split_tokens;
   out.prefill_schedule = o->prefill_schedule;
   if (o->prefill_wgs_per_cu > 0) out.prefill_wgs_per_cu = o->prefill_wgs_per_cu;
+  if (o->prefill_share_tiles > 0) out.prefill_share_tiles = o->prefill_share_tiles;
   out.prefill_staging = o->prefill_staging;
   return MVLLM_OK;
 }
@@ -138,6 +152,8 @@ struct Plan {
   mvllm_paged_plan pub;
   int max_splits = 1;
   int register_staging = 0;  // prefill: the register-staged kernel even where direct-to-LDS serves
+  int heads_waves = 0;       // heads decode: waves per workgroup
+  int prefill_share_tiles = mvllm::kPrefillShareTiles;  // stream prefill: fewest tiles a share
   uint64_t off_o = 0;       // byte offsets into the workspace
   uint64_t off_ml = 0;
   uint64_t off_pf = 0;      // stream prefill: [prefix][O partials][(m, l) partials]
@@ -167,6 +183,7 @@ void plan_prefill(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, 
                   int32_t d, const Options& o) {
   if (!plan.pub.prefill_mfma) return;
   plan.register_staging = o.prefill_staging;
+  plan.prefill_share_tiles = o.prefill_share_tiles;
   if (num_seqs > mvllm::kMaxStreamSeqs) return;
   const int forced = o.prefill_schedule;
   if (forced == 2) return;
@@ -212,6 +229,8 @@ void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, i
     plan.pub.decode_mode = MVLLM_DECODE_BY_ROW;
   } else if (all_prefill || num_seqs == 0) {
     plan.pub.decode_mode = MVLLM_DECODE_NONE;
+  } else if (o.decode_schedule == MVLLM_DECODE_HEADS) {
+    plan.pub.decode_mode = MVLLM_DECODE_HEADS;
   } else if (num_seqs <= mvllm::kMaxStreamSeqs && units <= 8 &&
              static_cast<int64_t>(num_seqs) * max_ctx < (int64_t{1} << 31) &&
              o.decode_schedule != MVLLM_DECODE_GRID) {
@@ -234,6 +253,11 @@ void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, i
     plan.off_o = head;
     plan.off_ml = plan.off_o + align256(entries * d * sizeof(float));
     plan.pub.workspace_bytes = plan.off_ml + align256(entries * 2 * sizeof(float));
+    return;
+  }
+  if (plan.pub.decode_mode == MVLLM_DECODE_HEADS) {
+    plan.heads_waves = o.heads_waves;
+    plan.pub.decode_workgroups = static_cast<int32_t>(num_seqs * units);
     return;
   }
   if (plan.pub.decode_mode == MVLLM_DECODE_NONE) return;
@@ -270,7 +294,9 @@ int launch_planned(const Plan& plan, mvllm::PagedParams& p, void* workspace, int
   p.split_tokens = plan.pub.split_tokens > 0 ? plan.pub.split_tokens : mvllm::kMaxSplitTokens;
   p.max_splits = plan.max_splits;
   p.by_row = plan.pub.decode_mode == MVLLM_DECODE_BY_ROW ? 1 : 0;
+  p.heads_waves = plan.pub.decode_mode == MVLLM_DECODE_HEADS ? plan.heads_waves : 0;
   p.pf_register_staging = plan.register_staging;
+  p.pf_share_tiles = plan.prefill_share_tiles;
   if (plan.pub.workspace_bytes > 0) {
     char* ws = static_cast<char*>(workspace);
     if (plan.pub.decode_mode == MVLLM_DECODE_STREAM) p.seq_prefix = reinterpret_cast<int*>(ws);
@@ -451,7 +477,7 @@ extern "C" {
 
 const char* mvllm_last_error(void) { return g_error; }
 
-int mvllm_abi_version(void) { return 9; }
+int mvllm_abi_version(void) { return 10; }
 
 #ifndef MVLLM_SOURCE_HASH
 #define MVLLM_SOURCE_HASH "unstamped"

@@ -20,6 +20,22 @@ constexpr int kMaxStreamSeqs = 4096;
 constexpr int kPrefillQueryTile = 128;
 // Most stream-prefill workgroups (the merge lists an item's pieces in LDS).
 constexpr int kMaxPrefillWgs = 2048;
+// Stream prefill: the shares used of `wgs` workgroups, each of at least `min_tiles`
+// 64-key tiles while that leaves a quarter of the workgroups busy. A share also pays
+// for loading its items' queries and for writing and merging (m, l, O) pieces of 128
+// query rows: a 512-token chunk behind a 1-2K prefix spread over every CU is cut into
+// shares of two or three tiles, most of their time then going to that overhead
+// (measured, 31 decode rows + one chunk, whole call: shares of >= 4 tiles 70-80 us
+// against 76-81 us with one tile; 4K-16K prefixes 2-7% faster).
+constexpr int kPrefillShareTiles = 4;
+__host__ __device__ inline int64_t prefill_stream_shares(int64_t total_units, int64_t wgs,
+                                                         int min_tiles) {
+  const int64_t per = min_tiles > 1 ? min_tiles : 1;
+  int64_t shares = (total_units + per - 1) / per;
+  const int64_t floor = total_units < wgs / 4 ? total_units : wgs / 4;
+  if (shares < floor) shares = floor;
+  return shares < 1 ? 1 : (shares < wgs ? shares : wgs);
+}
 // XCDs (each with its own L2) that workgroups are dispatched to round robin on MI355X.
 constexpr int kXcds = 8;
 constexpr int kPrefillKeyTile = 64;
@@ -91,6 +107,8 @@ struct PagedParams {
   int split_tokens;   // grid decode: nominal keys per split
   int max_splits;     // grid decode: grid extent along the split axis
   int by_row;         // grid decode: 1 = one unit per query row (serves prefill rows too)
+  int heads_waves;    // decode: > 0 selects the heads schedule, this many waves per
+                      // (sequence, head unit) workgroup
   float scale;
   float* part_o;      // split partials, D fp32 each
   float* part_ml;     // split partials' (running max in log2 units, sum)
@@ -100,6 +118,7 @@ struct PagedParams {
   float* pf_o;        // stream prefill partials: [2 * pf_wgs][heads][128][D] fp32, each
                       // piece normalised by its own sum
   float* pf_ml;       // their (max in log2 units, sum) per row: [2 * pf_wgs][heads][128][2]
+  int pf_share_tiles;       // stream prefill: fewest key tiles per share
   int pf_register_staging;  // 1: the register-staged prefill kernel even where the
                             // direct-to-LDS one serves (a plan option, for measurement)
 };

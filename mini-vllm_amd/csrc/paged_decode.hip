@@ -439,6 +439,77 @@ __global__ __launch_bounds__(1024) void paged_decode_stream_merge_kernel(const P
   }
 }
 
+// ------------------------------------------------------------ heads schedule
+
+// One workgroup per (decode sequence, wave unit): its W waves take W contiguous,
+// 16-key-aligned runs of the sequence's keys, stream them for the unit's kv head and
+// query heads, and combine their states through LDS (the reference's rescale,
+// paged_attention.cu:284-301, over the waves in order). The output is written by the
+// same launch: no partials, no second kernel. Sequences that are prefill chunks (or
+// have no context) leave the workgroup idle.
+template <typename TQ, typename TKV, int D, int GC, int W>
+__global__ __launch_bounds__(W * kWave) void paged_decode_heads_kernel(const PagedParams p) {
+  using K = Decode<TKV, D, GC>;
+  __shared__ float s_ml[W][GC][2];
+  __shared__ float s_o[W][GC][D];
+
+  const int seq = blockIdx.y;
+  if (p.seq_lens[seq] != 1) return;  // whole workgroup: no barrier follows for it
+  const int ctx = p.context_lens[seq];
+  if (ctx <= 0) return;  // whole workgroup
+  int kvh = 0, h0 = 0;
+  if (!wave_unit<GC>(p, blockIdx.x, kvh, h0)) return;  // whole workgroup
+
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  const int g = lane / K::R;
+  const int r = lane % K::R;
+  const int row = p.cu_seqlens_q[seq];
+  const int per = ((ctx + W - 1) / W + 15) & ~15;
+  const int sb = min(wave * per, ctx);
+  const int se = min(sb + per, ctx);
+
+  typename K::State st;
+  K::init(st);
+  if (sb < se) {
+    float qf[GC][K::E];
+    K::template load_queries<TQ>(p, row, h0, r, qf);
+    const int32_t* table = p.block_tables + static_cast<int64_t>(seq) * p.max_blocks;
+    K::stream(p, table, nullptr, 0, kvh, sb, se, g, r, qf, p.scale * kLog2e, st);
+  }
+  K::merge_row_groups(st);
+  if (g == 0) {
+#pragma unroll
+    for (int h = 0; h < GC; ++h) {
+#pragma unroll
+      for (int e = 0; e < K::E; ++e) s_o[wave][h][r * K::E + e] = st.acc[h][e];
+      if (r == 0) {
+        s_ml[wave][h][0] = st.m[h];
+        s_ml[wave][h][1] = st.l[h];
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < GC * D; i += W * kWave) {
+    const int h = i / D;
+    const int d = i % D;
+    float m = -INFINITY, l = 0.0f, o = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float mw = s_ml[w][h][0];
+      const float mx = fmaxf(m, mw);
+      const float mu = mx == -INFINITY ? 0.0f : mx;
+      const float a = fast_exp2(m - mu);
+      const float b = fast_exp2(mw - mu);
+      l = l * a + s_ml[w][h][1] * b;
+      o = o * a + s_o[w][h][d] * b;
+      m = mx;
+    }
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    Elem<TQ>::store(p.out, (static_cast<int64_t>(row) * p.hq + h0 + h) * D + d, o * inv);
+  }
+}
+
 // -------------------------------------------------------------- grid schedule
 
 template <typename TQ, typename TKV, int D, int GC>
@@ -557,6 +628,15 @@ hipError_t launch_decode_g(const PagedParams& p, hipStream_t stream) {
   const int units = p.hk * (p.hq / p.hk / GC);
   const int waves = decode_waves(p, GC);
   constexpr int kHeadsPerMergeBlock = 4;
+  if (p.heads_waves > 0) {
+    const dim3 grid(units, p.num_seqs);
+    switch (p.heads_waves) {
+      case 4: paged_decode_heads_kernel<TQ, TKV, D, GC, 4><<<grid, 4 * kWave, 0, stream>>>(p); break;
+      case 8: paged_decode_heads_kernel<TQ, TKV, D, GC, 8><<<grid, 8 * kWave, 0, stream>>>(p); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   if (p.stream_wgs > 0) {
     if (units > 8) return hipErrorInvalidValue;  // planner keeps stream mode to <= 8 units
     paged_decode_stream_kernel<TQ, TKV, D, GC><<<p.stream_wgs, waves * kWave, 0, stream>>>(p);

@@ -147,6 +147,16 @@ __device__ __forceinline__ int xcd_share(int bid, int n) {
   return n % kXcds == 0 ? (bid % kXcds) * (n / kXcds) + bid / kXcds : bid;
 }
 
+// The share of workgroup `bid` of `grid` when only `shares` <= grid are used, or -1:
+// each XCD takes ceil(shares / 8) consecutive shares (xcd_share when shares == grid).
+__device__ __forceinline__ int xcd_share_of(int bid, int grid, int shares) {
+  if (grid % kXcds != 0) return bid < shares ? bid : -1;
+  const int per = (shares + kXcds - 1) / kXcds;
+  const int slot = bid / kXcds;
+  const int share = (bid % kXcds) * per + slot;
+  return slot < per && share < shares ? share : -1;
+}
+
 // Work units of sequence s over all its items (0 for decode rows).
 __device__ __forceinline__ int prefill_seq_units(int context, int len, int cols) {
   if (len <= 1) return 0;
@@ -158,19 +168,15 @@ __device__ __forceinline__ int prefill_seq_units(int context, int len, int cols)
 
 // Position `k` at unit u of the stream described by the prefix `pre` ([n + 1] work
 // units before each sequence, pre[n] > u).
-__device__ __forceinline__ void seek(Cursor& k, const PagedParams& p, const int* pre, int n,
-                                     int cols, int u) {
-  int a = 0, b = n;  // invariant: pre[a] <= u < pre[b]
-  while (b - a > 1) {
-    const int mid = (a + b) >> 1;
-    if (uniform(pre[mid]) <= u) a = mid; else b = mid;
-  }
+// The rest of a seek once the sequence is known: unit u of sequence a, whose units are
+// [base, next).
+__device__ __forceinline__ void seek_in(Cursor& k, const PagedParams& p, int a, int base,
+                                        int next, int cols, int u) {
   k.u = u;
   k.s = a;
   k.context = sload(p.context_lens + a);
   k.len = sload(p.seq_lens + a);
-  const int base = uniform(pre[a]);
-  const int per_col = (uniform(pre[a + 1]) - base) / cols;
+  const int per_col = (next - base) / cols;
   int r = u - base;
   k.c = r / per_col;
   k.kvh = k.c / (cols / p.hk);
@@ -185,10 +191,21 @@ __device__ __forceinline__ void seek(Cursor& k, const PagedParams& p, const int*
   k.t = r;
 }
 
+__device__ __forceinline__ void seek(Cursor& k, const PagedParams& p, const int* pre, int n,
+                                     int cols, int u) {
+  int a = 0, b = n;  // invariant: pre[a] <= u < pre[b]
+  while (b - a > 1) {
+    const int mid = (a + b) >> 1;
+    if (uniform(pre[mid]) <= u) a = mid; else b = mid;
+  }
+  seek_in(k, p, a, uniform(pre[a]), uniform(pre[a + 1]), cols, u);
+}
+
 // This workgroup's work units [u0, u1) and the cursor at u0; false when it has none.
-// Every thread must call it: the stream schedule's prefix scan ends in a barrier.
+// Every thread must call it: the stream schedule's prefix scan ends in a barrier. The
+// stream schedule sets `share` (the workgroup's share, which names its piece slots).
 template <int kThreads, bool kGridOnly = false>
-__device__ __forceinline__ bool prefill_work(const PagedParams& p, int cols, int share,
+__device__ __forceinline__ bool prefill_work(const PagedParams& p, int cols, int& share,
                                              int* s_prefix, Cursor& cur, int& u0, int& u1) {
   const int tid = threadIdx.x;
   const int n = p.num_seqs;
@@ -219,8 +236,12 @@ __device__ __forceinline__ bool prefill_work(const PagedParams& p, int cols, int
     if (blockIdx.x == 0) {
       for (int s = tid; s <= n; s += kThreads) p.pf_prefix[s] = s_prefix[s];
     }
-    u0 = static_cast<int>(share_begin(share, total, gridDim.x));
-    u1 = static_cast<int>(share_begin(share + 1, total, gridDim.x));
+    const int shares =
+        static_cast<int>(prefill_stream_shares(total, gridDim.x, p.pf_share_tiles));
+    share = xcd_share_of(blockIdx.x, gridDim.x, shares);
+    if (share < 0) return false;  // whole workgroup: no barrier follows for it
+    u0 = static_cast<int>(share_begin(share, total, shares));
+    u1 = static_cast<int>(share_begin(share + 1, total, shares));
     if (u0 >= u1) return false;  // whole workgroup: no barrier follows for it
     seek(cur, p, s_prefix, n, cols, u0);
     return true;
@@ -280,7 +301,7 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_kernel(const PagedPara
   const int chunks = group / HW;
   const int cols = p.hk * chunks;
   const bool stream = p.pf_wgs > 0;
-  const int share = xcd_share(blockIdx.x, gridDim.x);
+  int share = xcd_share(blockIdx.x, gridDim.x);
 
   // ---- this workgroup's units [u0, u1) and the cursor at u0.
   Cursor cur;
@@ -706,7 +727,7 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_lds_kernel(const Paged
   // Compiled per schedule: the grid's kernel carries none of the stream's cursor
   // seeking (whose registers otherwise spill into the tile loop).
   constexpr bool stream = kStream;
-  const int share = xcd_share(blockIdx.x, gridDim.x);
+  int share = xcd_share(blockIdx.x, gridDim.x);
 
   Cursor cur;
   int u0, u1;
@@ -1522,66 +1543,97 @@ __global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedPara
   }
 }
 
-// Combine the pieces of every prefill item cut between stream workgroups. Workgroup b
-// looks at the start of share b; if that falls inside an item and is the item's first
-// such boundary, it merges the item. The item's piece slots are listed once in LDS;
-// each of 1024 threads then owns kElems float4 columns of output rows and combines
-// the pieces kPieces at a time, with every load of a batch issued together (the
-// partials come from L2 / MALL, so latency, not bandwidth, sets this kernel's time).
+// Combine the pieces of every prefill item cut between stream workgroups. An item
+// spread over shares first .. last (the shares holding its first and last key) has
+// last - first boundaries inside it (the starts of shares first + 1 .. last); the
+// kMergeSub workgroups of each boundary merge their own slice of the item's
+// HW x rows x D outputs, so an item's merge is spread over as many CUs as it has
+// pieces (the partials come from L2 / MALL: one CU per item left the merge bound by
+// that CU's load bandwidth). The item's piece slots are listed in LDS (an empty share
+// holds none: slot -1); each thread owns kElems float4 columns of its slice and
+// combines the pieces kPieces at a time, with every load of a batch issued together.
+constexpr int kMergeSub = 4;
+constexpr int kMergeThreads = 256;
+
 template <typename TQ, int D, int HW>
-__global__ __launch_bounds__(1024) void paged_prefill_merge_kernel(const PagedParams p) {
-  constexpr int kElems = 4;
-  constexpr int kPieces = 4;
+__global__ __launch_bounds__(kMergeThreads) void paged_prefill_merge_kernel(const PagedParams p) {
+  constexpr int kElems = 2;
+  constexpr int kPieces = 8;
   __shared__ int s_slots[kMaxPrefillWgs];
-  __shared__ int s_pieces;
-  // Boundary b is the start of share b, merged on the XCD that computed share b.
-  const int b = xcd_share(blockIdx.x, gridDim.x);
-  if (b == 0) return;
-  const int64_t wgs = p.pf_wgs;
+  const int64_t grid = p.pf_wgs;
+  const int bid = static_cast<int>(blockIdx.x % grid);
+  const int sub = static_cast<int>(blockIdx.x / grid);
   const int n = p.num_seqs;
-  const int total = sload(p.pf_prefix + n);
-  const int64_t x = share_begin(b, total, wgs);
-  if (x >= total) return;
   const int group = p.hq / p.hk;
   const int chunks = group / HW;
   const int cols = p.hk * chunks;
+  // Find the item at the share's start. With fewer than 64 sequences every lane loads
+  // one prefix entry at once and a ballot finds the sequence: one memory round trip
+  // where a binary search makes one per step (the merge is short, so this chain is a
+  // large part of it).
+  const int lane = threadIdx.x % kWave;
+  int v = 0;
+  int total;
+  if (n < kWave) {
+    v = p.pf_prefix[min(lane, n)];
+    total = __shfl(v, n, kWave);
+  } else {
+    total = sload(p.pf_prefix + n);
+  }
+  // The shares the prefill kernel used; boundary b is the start of share b, merged on
+  // the XCD that computed share b (workgroups bid and bid + grid share an XCD when the
+  // grid is a multiple of 8).
+  const int64_t wgs = prefill_stream_shares(total, grid, p.pf_share_tiles);
+  const int b = xcd_share_of(bid, static_cast<int>(grid), static_cast<int>(wgs));
+  if (b <= 0) return;
+  const int64_t x = share_begin(b, total, wgs);
+  if (x >= total) return;
   Cursor k;
-  seek(k, p, p.pf_prefix, n, cols, static_cast<int>(x));
+  if (n < kWave) {
+    const uint64_t le = __ballot(lane <= n && v <= x);
+    const int a = __popcll(le) - 1;  // pre[a] <= x < pre[a + 1]
+    seek_in(k, p, a, uniform(__shfl(v, a, kWave)), uniform(__shfl(v, a + 1, kWave)), cols,
+            static_cast<int>(x));
+  } else {
+    seek(k, p, p.pf_prefix, n, cols, static_cast<int>(x));
+  }
   if (k.t == 0) return;  // the share starts an item: nothing is cut here
   const int64_t start = x - k.t;
   const int64_t end = start + k.nt;
-  if (share_begin(b - 1, total, wgs) > start) return;  // an earlier boundary merges it
-  if (threadIdx.x == 0) {
-    // Shares overlapping [start, end): the first holds the item as its last piece
-    // (slot 2w + 1) unless its share starts exactly there; later ones as their first
-    // (slot 2w). Empty shares hold nothing.
-    const int64_t first = share_owner(start, total, wgs);
-    int np = 0;
-    for (int64_t g = first; g < wgs; ++g) {
-      const int64_t gs = share_begin(g, total, wgs);
-      if (gs >= end) break;
-      if (gs == share_begin(g + 1, total, wgs)) continue;
-      s_slots[np++] = static_cast<int>(2 * g + (g == first && gs < start ? 1 : 0));
-    }
-    s_pieces = np;
+  // start < x <= end - 1, so first < b <= last.
+  const int64_t first = share_owner(start, total, wgs);
+  const int64_t last = share_owner(end - 1, total, wgs);
+  const int pieces = static_cast<int>(last - first + 1);
+  const int slices = static_cast<int>(last - first) * kMergeSub;
+  const int slice = static_cast<int>(b - first - 1) * kMergeSub + sub;
+  // Piece i is share first + i: the item's last piece in that share (slot 2w + 1) for
+  // the first share unless it starts exactly at the item, its first piece (slot 2w)
+  // for the others.
+  for (int i = threadIdx.x; i < pieces; i += blockDim.x) {
+    const int64_t g = first + i;
+    const int64_t gs = share_begin(g, total, wgs);
+    const bool empty = gs == share_begin(g + 1, total, wgs);
+    s_slots[i] = empty ? -1 : static_cast<int>(2 * g + (i == 0 && gs < start ? 1 : 0));
   }
   __syncthreads();
-  const int pieces = s_pieces;
   const int qb = k.q * kPrefillQueryTile;
   const int rows = min(kPrefillQueryTile, k.len - qb);
   const int head0 = (k.c / chunks) * group + (k.c % chunks) * HW;
   const int row0 = sload(p.cu_seqlens_q + k.s) + qb;
   constexpr int kD4 = D / 4;
   const int n4 = HW * rows * kD4;
+  const int lo = static_cast<int>(static_cast<int64_t>(slice) * n4 / slices);
+  const int hi = static_cast<int>(static_cast<int64_t>(slice + 1) * n4 / slices);
+  const int slot0 = s_slots[0];  // piece 0 holds the item's first key: never empty
   const int nthreads = static_cast<int>(blockDim.x);
-  for (int j0 = threadIdx.x; j0 < n4; j0 += kElems * nthreads) {
+  for (int j0 = lo + threadIdx.x; j0 < hi; j0 += kElems * nthreads) {
     int64_t prow[kElems];
     int dcol[kElems];
     float m[kElems], l[kElems];
     f32x4 acc[kElems];
 #pragma unroll
     for (int e = 0; e < kElems; ++e) {
-      const int j = min(j0 + e * nthreads, n4 - 1);
+      const int j = min(j0 + e * nthreads, hi - 1);
       const int hw = j / (rows * kD4);
       const int rem = j - hw * rows * kD4;
       const int row = rem / kD4;
@@ -1594,10 +1646,12 @@ __global__ __launch_bounds__(1024) void paged_prefill_merge_kernel(const PagedPa
     for (int i0 = 0; i0 < pieces; i0 += kPieces) {
       float2 ml[kPieces][kElems];
       f32x4 oi[kPieces][kElems];
+      int slot[kPieces];
 #pragma unroll
       for (int i = 0; i < kPieces; ++i) {
-        const int64_t base =
-            static_cast<int64_t>(s_slots[min(i0 + i, pieces - 1)]) * HW * kPrefillQueryTile;
+        slot[i] = i0 + i < pieces ? s_slots[i0 + i] : -1;
+        const int64_t base = static_cast<int64_t>(slot[i] >= 0 ? slot[i] : slot0) * HW *
+                             kPrefillQueryTile;
 #pragma unroll
         for (int e = 0; e < kElems; ++e) {
           ml[i][e] = *reinterpret_cast<const float2*>(p.pf_ml + (base + prow[e]) * 2);
@@ -1606,7 +1660,7 @@ __global__ __launch_bounds__(1024) void paged_prefill_merge_kernel(const PagedPa
       }
 #pragma unroll
       for (int i = 0; i < kPieces; ++i) {
-        if (i0 + i >= pieces) break;
+        if (slot[i] < 0) continue;  // past the last piece, or an empty share
 #pragma unroll
         for (int e = 0; e < kElems; ++e) {
           // Piece rows are normalised: weight them by l_i * 2^(m_i - max).
@@ -1622,7 +1676,7 @@ __global__ __launch_bounds__(1024) void paged_prefill_merge_kernel(const PagedPa
     }
 #pragma unroll
     for (int e = 0; e < kElems; ++e) {
-      if (j0 + e * nthreads >= n4) continue;
+      if (j0 + e * nthreads >= hi) continue;
       const int hw = static_cast<int>(prow[e] / kPrefillQueryTile);
       const int row = static_cast<int>(prow[e] - static_cast<int64_t>(hw) * kPrefillQueryTile);
       const float inv = l[e] > 0.0f ? 1.0f / l[e] : 0.0f;
@@ -1643,7 +1697,7 @@ void launch_prefill_cfg(const PagedParams& p, int max_query_len, hipStream_t str
   constexpr int HW = HCW * HS;
   if (p.pf_wgs > 0) {
     paged_prefill_kernel<TQ, TKV, D, HCW, HS><<<p.pf_wgs, 256 * HS, 0, stream>>>(p);
-    paged_prefill_merge_kernel<TQ, D, HW><<<p.pf_wgs, 1024, 0, stream>>>(p);
+    paged_prefill_merge_kernel<TQ, D, HW><<<kMergeSub * p.pf_wgs, kMergeThreads, 0, stream>>>(p);
   } else {
     const int cols = p.hk * (p.hq / p.hk / HW);
     const int qtiles = (max_query_len + kPrefillQueryTile - 1) / kPrefillQueryTile;
@@ -1656,7 +1710,7 @@ template <typename TQ, int HS>
 void launch_prefill_lds(const PagedParams& p, int max_query_len, hipStream_t stream) {
   if (p.pf_wgs > 0) {
     paged_prefill_lds_kernel<TQ, HS, true><<<p.pf_wgs, 256 * HS, 0, stream>>>(p);
-    paged_prefill_merge_kernel<TQ, 128, HS><<<p.pf_wgs, 1024, 0, stream>>>(p);
+    paged_prefill_merge_kernel<TQ, 128, HS><<<kMergeSub * p.pf_wgs, kMergeThreads, 0, stream>>>(p);
   } else {
     const int cols = p.hk * (p.hq / p.hk / HS);
     const int qtiles = (max_query_len + kPrefillQueryTile - 1) / kPrefillQueryTile;

@@ -60,7 +60,7 @@ HIP_FLAGS = [
 # reference's PyTorch expressions round, so FMA contraction is off there.
 EXTRA_FLAGS = {"elementwise.hip": ["-ffp-contract=off"], "linear.hip": ["-ffp-contract=off"]}
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 DTYPE_CODES: dict[torch.dtype, int] = {
     torch.float32: 0,
@@ -183,16 +183,17 @@ class _PlanOptions(ctypes.Structure):
         ("prefill_schedule", ctypes.c_int32),
         ("prefill_wgs_per_cu", ctypes.c_int32),
         ("prefill_staging", ctypes.c_int32),
+        ("prefill_share_tiles", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
     ]
 
 
-SCHEDULES = {"stream": 1, "grid": 2}
+SCHEDULES = {"stream": 1, "grid": 2, "heads": 4}
 
 
 def make_plan_options(options: dict[str, Any] | None) -> "_PlanOptions | None":
     """``mvllm_plan_options`` from a dict of its field names (schedules may be given as
-    "stream" / "grid"); None for the planner's defaults."""
+    "stream" / "grid" / "heads"); None for the planner's defaults."""
     if not options:
         return None
     fields = {name for name, _ in _PlanOptions._fields_} - {"reserved"}
@@ -216,7 +217,7 @@ class _Plan(ctypes.Structure):
     ]
 
 
-DECODE_MODES = {0: "none", 1: "stream", 2: "grid", 3: "by_row"}
+DECODE_MODES = {0: "none", 1: "stream", 2: "grid", 3: "by_row", 4: "heads"}
 
 
 def _bind(lib: ctypes.CDLL) -> None:

@@ -13,7 +13,7 @@ from dataclasses import dataclass
 
 import torch
 
-__all__ = ["ForwardBatch", "PADDING_BLOCK"]
+__all__ = ["BatchStager", "ForwardBatch", "PADDING_BLOCK"]
 
 PADDING_BLOCK = -1
 
@@ -72,4 +72,109 @@ class ForwardBatch:
             max_query_len=max(lens),
             max_context_len=max(contexts),
             seq_ids=tuple(seq_ids),
+        )
+
+
+class BatchStager:
+    """Builds :class:`ForwardBatch` for a GPU without waiting for it.
+
+    ``ForwardBatch.from_scheduled`` makes eight tensors from Python lists, and each
+    blocking host-to-device copy waits for every kernel already queued, so the host could
+    not prepare iteration i + 1 while the GPU runs iteration i. Here the metadata is
+    written into pinned host memory (one int64 and one int32 block) and copied with two
+    asynchronous copies into fresh device tensors that the batch's fields are views of.
+    The pinned blocks are a small ring: a block is rewritten only after the event
+    recorded behind its last copy has passed.
+
+    A decode row whose input token was sampled by the previous iteration but not yet
+    read by the host (``gather``: sequence id -> row of ``prev_tokens``) takes that token
+    on the device.
+    """
+
+    RING = 3
+
+    def __init__(self, device) -> None:
+        self.device = torch.device(device)
+        self._ring: list[list] = [[None, None, None] for _ in range(self.RING)]  # host64, host32, event
+        self._turn = 0
+
+    def _slot(self, n64: int, n32: int):
+        slot = self._ring[self._turn]
+        self._turn = (self._turn + 1) % self.RING
+        if slot[2] is not None:
+            slot[2].synchronize()
+        if slot[0] is None or slot[0].numel() < n64:
+            slot[0] = torch.empty(max(n64, 4096), dtype=torch.int64, pin_memory=True)
+        if slot[1] is None or slot[1].numel() < n32:
+            slot[1] = torch.empty(max(n32, 16384), dtype=torch.int32, pin_memory=True)
+        return slot
+
+    def build(self, scheduled, manager, prev_tokens: torch.Tensor | None = None,
+              gather: dict[int, int] | None = None) -> ForwardBatch:
+        n = len(scheduled)
+        counts = [count for _, count in scheduled]
+        total = sum(counts)
+        tables = [manager.table(seq.seq_id) for seq, _ in scheduled]
+        widest = max(len(t) for t in tables)
+        # int64: ids | positions | gather rows | last rows; int32: cu | lens | context |
+        # slots | tables
+        n64 = 3 * total + n
+        n32 = (n + 1) + 2 * n + total + n * widest
+        slot = self._slot(n64, n32)
+        h64 = slot[0][:n64].numpy()
+        h32 = slot[1][:n32].numpy()
+        ids, pos, rows, last = (h64[:total], h64[total:2 * total], h64[2 * total:3 * total],
+                                h64[3 * total:])
+        cu, lens, ctx = h32[:n + 1], h32[n + 1:2 * n + 1], h32[2 * n + 1:3 * n + 1]
+        slots = h32[3 * n + 1:3 * n + 1 + total]
+        tab = h32[3 * n + 1 + total:].reshape(n, widest)
+        tab.fill(PADDING_BLOCK)
+        rows.fill(-1)
+        cu[0] = 0
+        gathered = False
+        at = 0
+        for i, ((seq, count), table) in enumerate(zip(scheduled, tables)):
+            start = seq.num_computed_tokens
+            if count < 1 or start + count > len(seq):
+                raise ValueError(f"sequence {seq.seq_id}: cannot compute {count} tokens from {start}")
+            row = gather.get(seq.seq_id, -1) if gather else -1
+            if row >= 0 and count == 1:
+                ids[at] = 0
+                rows[at] = row
+                gathered = True
+            else:
+                ids[at:at + count] = seq.tokens(start, count)
+            pos[at:at + count] = range(start, start + count)
+            slots[at:at + count] = manager.slots(seq.seq_id, start, count)
+            at += count
+            cu[i + 1] = at
+            lens[i] = count
+            ctx[i] = start + count
+            last[i] = at - 1
+            tab[i, :len(table)] = table
+        d64 = torch.empty(n64, dtype=torch.int64, device=self.device)
+        d32 = torch.empty(n32, dtype=torch.int32, device=self.device)
+        d64.copy_(slot[0][:n64], non_blocking=True)
+        d32.copy_(slot[1][:n32], non_blocking=True)
+        event = torch.cuda.Event()
+        event.record()
+        slot[2] = event
+        input_ids = d64[:total]
+        if gathered:
+            if prev_tokens is None:
+                raise ValueError("a gathered row needs prev_tokens")
+            g = d64[2 * total:3 * total]
+            input_ids = torch.where(g >= 0, prev_tokens.index_select(0, g.clamp(min=0)), input_ids)
+        return ForwardBatch(
+            input_ids=input_ids,
+            positions=d64[total:2 * total],
+            cu_seqlens_q=d32[:n + 1],
+            seq_lens=d32[n + 1:2 * n + 1],
+            context_lens=d32[2 * n + 1:3 * n + 1],
+            slot_mapping=d32[3 * n + 1:3 * n + 1 + total],
+            block_tables=d32[3 * n + 1 + total:].view(n, widest),
+            last_row_indices=d64[3 * total:],
+            max_query_len=max(counts),
+            max_context_len=int(ctx.max()),
+            seq_ids=tuple(seq.seq_id for seq, _ in scheduled),
         )

@@ -98,6 +98,50 @@ def test_decode_graphs_match_eager(extension, device, dtype, head_dim):
     assert graphs.replays == 4 and len(graphs.graphs) == 1
 
 
+BATCH_FIELDS = ("input_ids", "positions", "cu_seqlens_q", "seq_lens", "context_lens",
+                "slot_mapping", "block_tables", "last_row_indices")
+
+
+def test_staged_batch_matches_from_scheduled(extension, device):
+    """BatchStager (pinned staging, asynchronous copies) builds the batch that
+    ForwardBatch.from_scheduled builds, also when its pinned ring is reused; decode rows
+    named in `gather` take their token from the device buffer instead."""
+    from mini_vllm.serve.batch import BatchStager, ForwardBatch
+
+    config = tiny_config(torch.float32)
+    weights = random_weights(config, seed=4, device=device)
+    engine = make_engine(config, weights, use_cuda=True, device=device,
+                         sched=SchedulerConfig(max_batched_tokens=40, chunk_size=16))
+    for p in prompts(5, 5, 60, config.vocab_size, seed=3):
+        engine.add_request(p, 30)
+    for _ in range(20):  # until one iteration mixes decode rows and chunks
+        out = engine.scheduler.schedule()
+        counts = [n for _, n in out.scheduled]
+        if 1 in counts and max(counts) > 1:
+            break
+        engine.scheduler.commit(out, [0] * len(out.scheduled))
+    else:
+        pytest.fail("no mixed iteration")
+    manager = engine.model.manager
+    want = ForwardBatch.from_scheduled(out.scheduled, manager, device)
+    stager = BatchStager(device)
+    for _ in range(2 * BatchStager.RING):
+        got = stager.build(out.scheduled, manager)
+        for f in BATCH_FIELDS:
+            assert torch.equal(getattr(got, f), getattr(want, f)), f
+        assert (got.max_query_len, got.max_context_len, got.seq_ids) == \
+            (want.max_query_len, want.max_context_len, want.seq_ids)
+    prev = torch.arange(1000, 1064, device=device)
+    decode = [(i, s.seq_id) for i, (s, n) in enumerate(out.scheduled) if n == 1]
+    gather = {sid: 3 + j for j, (_, sid) in enumerate(decode)}
+    got = stager.build(out.scheduled, manager, prev, gather)
+    expect = want.input_ids.clone()
+    for j, (i, _) in enumerate(decode):
+        expect[int(want.cu_seqlens_q[i])] = 1003 + j
+    assert torch.equal(got.input_ids, expect)
+    assert torch.equal(got.positions, want.positions)
+
+
 @pytest.mark.parametrize("sched", [SchedulerConfig(), SchedulerConfig(max_batched_tokens=24, chunk_size=8)],
                          ids=["one-pass", "chunked"])
 def test_engine_with_decode_graphs_matches_dense_recompute(extension, device, sched):

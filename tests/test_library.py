@@ -107,6 +107,22 @@ def test_plan_options_are_explicit_and_checked(lib, monkeypatch):
         extension.make_plan_options({"decode_sched": 1})
 
 
+def test_heads_decode_schedule_plan(lib):
+    """Forced per-(sequence, head unit) decode: one workgroup per sequence and unit, no
+    workspace; 4 or 8 waves per workgroup, anything else refused; by-row is not a
+    schedule one can force."""
+    plan = _plan(lib, 32, 32, 16, 8, 128, 16, 1, 4096, 2, 2, options={"decode_schedule": "heads"})
+    assert plan.decode_mode == 4 and plan.workspace_bytes == 0
+    assert plan.decode_workgroups == 32 * 8  # GQA pairs: one unit per kv head
+    four = _plan(lib, 32, 32, 16, 8, 128, 16, 1, 4096, 2, 2,
+                 options={"decode_schedule": "heads", "decode_waves_per_cu": 4})
+    assert four.decode_mode == 4
+    for bad in ({"decode_schedule": "heads", "decode_waves_per_cu": 6}, {"decode_schedule": 3}):
+        opts = extension.make_plan_options(bad)
+        assert lib.mvllm_paged_attention_plan(32, 32, 16, 8, 128, 16, 1, 4096, 2, 2,
+                                              ctypes.byref(opts), ctypes.byref(extension._Plan())) == 1
+
+
 def test_the_library_carries_the_id_of_its_sources(lib):
     assert lib.mvllm_build_id().decode() == extension.source_hash()
 

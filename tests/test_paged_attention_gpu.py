@@ -69,17 +69,36 @@ def test_decode_over_a_long_context_uses_the_split_path(extension, device):
     check(extension, b)
 
 
-@pytest.mark.parametrize("schedule", ["stream", "grid"])
+DECODE_SCHEDULES = {"stream": None, "grid": {"decode_schedule": "grid"},
+                    "heads": {"decode_schedule": "heads"},
+                    "heads4": {"decode_schedule": "heads", "decode_waves_per_cu": 4}}
+
+
+@pytest.mark.parametrize("schedule", sorted(DECODE_SCHEDULES))
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_both_decode_schedules_agree_with_the_oracle(extension, device, schedule, dtype):
-    """The stream schedule (default) and the split grid (forced) on a ragged batch,
-    including sequences shorter than one workgroup's share and longer than many."""
-    options = {"decode_schedule": "grid"} if schedule == "grid" else None
+def test_every_decode_schedule_agrees_with_the_oracle(extension, device, schedule, dtype):
+    """The stream schedule (default), the split grid and the per-(sequence, head)
+    workgroups (forced) on a ragged batch, including sequences shorter than one
+    workgroup's share (or than its waves) and longer than many."""
+    options = DECODE_SCHEDULES[schedule]
     b = case([8192, 33, 4096, 17, 1, 700, 2], [1] * 7, device, dtype=dtype)
     plan = extension.paged_attention_plan(7, 7, HQ, HK, D, 16, 1, 8192, dtype, dtype,
                                           plan_options=options)
-    assert plan["decode_mode"] == schedule
+    assert plan["decode_mode"] == schedule.rstrip("4")
+    if schedule.startswith("heads"):
+        assert plan["workspace_bytes"] == 0
     check(extension, b, options=options)
+
+
+@pytest.mark.parametrize("kv_dtype", [None, torch.float8_e4m3fn])
+def test_heads_decode_schedule_in_a_mixed_batch(extension, device, kv_dtype):
+    """Prefill chunks beside decode rows: the heads schedule leaves the chunks to the
+    prefill kernel; GQA groups of 2 and 4, fp8 pools with their scales."""
+    for heads, kv_heads in ((16, 8), (16, 4)):
+        b = case([900, 2500, 40, 700, 5], [1, 400, 1, 1, 5], device, dtype=torch.bfloat16,
+                 kv_dtype=kv_dtype, num_q_heads=heads, num_kv_heads=kv_heads, head_dim=128)
+        check(extension, b, dtype=kv_dtype or torch.bfloat16,
+              options={"decode_schedule": "heads"})
 
 
 @pytest.mark.parametrize("wgs_per_cu", ["1", "4"])
@@ -165,13 +184,35 @@ def test_prefill_schedules_on_a_ragged_batch(extension, device, schedule, heads,
     check(extension, b, options=options)
 
 
+@pytest.mark.parametrize("decodes", [27, 66])
+def test_prefill_stream_beside_many_decode_rows(extension, device, decodes):
+    """Chunks cut between stream workgroups in batches of fewer and of more than 64
+    sequences (the merge finds an item's sequence by a one-wave ballot below 64 and by
+    a binary search above)."""
+    gen = torch.Generator().manual_seed(decodes)
+    contexts = torch.randint(1, 2300, (decodes,), generator=gen).tolist()
+    b = case(contexts + [1600, 512, 900], [1] * decodes + [512, 512, 77], device,
+             dtype=torch.bfloat16, num_q_heads=16, num_kv_heads=8, head_dim=128)
+    check(extension, b, options={"prefill_schedule": "stream"})
+
+
 @pytest.mark.parametrize("wgs_per_cu", ["1", "3"])
 def test_prefill_stream_with_more_workgroups_than_tiles(extension, device, wgs_per_cu):
-    """A two-tile prefill over hundreds of workgroups: most shares are empty, and each
-    tile of an item may sit in a different workgroup."""
+    """A two-tile prefill over hundreds of workgroups: most workgroups idle, and with
+    one-tile shares each tile of an item sits in a different workgroup."""
     b = case([70, 3], [70, 3], device, dtype=torch.bfloat16, num_q_heads=4, num_kv_heads=2,
              head_dim=64)
-    check(extension, b, options={"prefill_wgs_per_cu": wgs_per_cu, "prefill_schedule": "stream"})
+    for tiles in ("1", "4"):
+        check(extension, b, options={"prefill_wgs_per_cu": wgs_per_cu, "prefill_schedule": "stream",
+                                     "prefill_share_tiles": tiles})
+
+
+@pytest.mark.parametrize("tiles", ["1", "3", "64"])
+def test_prefill_stream_share_sizes(extension, device, tiles):
+    """Shares of one tile (every item cut into many pieces), of a few, and so large that
+    the quarter-grid floor sets their number: the same attention."""
+    b = case([2000, 700, 1300, 64], [512, 300, 512, 64], device, dtype=torch.bfloat16)
+    check(extension, b, options={"prefill_schedule": "stream", "prefill_share_tiles": tiles})
 
 
 @pytest.mark.parametrize("schedule", ["stream", "grid"])
