@@ -70,7 +70,10 @@ typedef struct mvllm_paged_plan {
   int32_t prefill_workgroups; /* MFMA prefill: > 0 persistent workgroups with balanced
                                  shares of all key tiles (cut items merged after);
                                  0 one workgroup per (sequence, heads, query tile) */
-  int32_t reserved;
+  int32_t prefill_pieces;     /* MFMA prefill on the grid: > 1 items longer than ~1.2x
+                                 the mean work per CU are cut into at most this many key
+                                 ranges, run in the same launch longest first and merged
+                                 by the last to finish; 0 every item whole */
 } mvllm_paged_plan;
 
 /* Explicit overrides of the planner's schedule choices, for measurement and for tests
@@ -89,9 +92,14 @@ typedef struct mvllm_plan_options {
   int32_t prefill_staging;     /* 0 auto (direct-to-LDS copies where served); 1 forces the
                                   register-staged prefill kernel */
   int32_t prefill_share_tiles; /* stream prefill: fewest 64-key tiles per workgroup share
-                                  while a quarter of the workgroups stay busy (default 4):
-                                  small work uses fewer workgroups */
-  int32_t reserved;            /* must be 0 */
+                                  while a quarter of the workgroups stay busy; grid
+                                  prefill: fewest tiles per piece of a cut item
+                                  (default 4): small work uses fewer workgroups */
+  int32_t prefill_pieces;      /* grid prefill: most key-range pieces per item (default
+                                  8); 1 keeps every item whole */
+  int32_t prefill_piece_pct;   /* grid prefill: an item is cut into pieces of at least this
+                                  percentage of the mean key tiles per CU (default 150,
+                                  at least 50) */
 } mvllm_plan_options;
 
 /* Plan a paged_attention call. Depends only on the host-side sizes below and the

@@ -70,6 +70,8 @@ struct Options {
   int prefill_wgs_per_cu = 1;
   int prefill_share_tiles = mvllm::kPrefillShareTiles;
   int prefill_staging = 0;
+  int prefill_pieces = mvllm::kSplitDefaultPieces;
+  int prefill_piece_pct = mvllm::kSplitDefaultPct;
 };
 
 int read_options(const mvllm_plan_options* o, Options& out) {
@@ -80,7 +82,8 @@ int read_options(const mvllm_plan_options* o, Options& out) {
       o->prefill_schedule < 0 || o->prefill_schedule > 2 || o->prefill_staging < 0 ||
       o->prefill_staging > 1 || o->decode_wgs_per_cu < 0 || o->decode_waves_per_cu < 0 ||
       o->decode_split_tokens < 0 || o->prefill_wgs_per_cu < 0 || o->prefill_share_tiles < 0 ||
-      o->reserved != 0) {
+      o->prefill_pieces < 0 || o->prefill_pieces > 64 || o->prefill_piece_pct < 0 ||
+      (o->prefill_piece_pct > 0 && o->prefill_piece_pct < 50) || o->prefill_piece_pct > 10000) {
     return fail(MVLLM_ERR_INVALID, "paged_attention: plan options out of range");
   }
   out.decode_schedule = o->decode_schedule;
@@ -100,6 +103,8 @@ int read_options(const mvllm_plan_options* o, Options& out) {
   if (o->prefill_wgs_per_cu > 0) out.prefill_wgs_per_cu = o->prefill_wgs_per_cu;
   if (o->prefill_share_tiles > 0) out.prefill_share_tiles = o->prefill_share_tiles;
   out.prefill_staging = o->prefill_staging;
+  if (o->prefill_pieces > 0) out.prefill_pieces = o->prefill_pieces;
+  if (o->prefill_piece_pct > 0) out.prefill_piece_pct = o->prefill_piece_pct;
   return MVLLM_OK;
 }
 
@@ -159,6 +164,10 @@ struct Plan {
   uint64_t off_pf = 0;      // stream prefill: [prefix][O partials][(m, l) partials]
   uint64_t off_pf_o = 0;
   uint64_t off_pf_ml = 0;
+  int split_ranks = 0;      // split prefill grid: rank extent, partial slots per column,
+  int split_slots = 0;      // piece length (percent of the mean tiles per CU)
+  int split_pct = 0;
+  uint64_t off_split = 0;   // split prefill grid: the partial slots
 };
 
 uint64_t align256(uint64_t v) { return (v + 255) / 256 * 256; }
@@ -179,18 +188,54 @@ void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, i
 // from host sizes: ceil(num_tokens / 128) query tiles per kv column. The
 // prefill_schedule option 1 / 2 forces stream / grid. The stream's workspace follows
 // the decode part's.
+// The grid's split (pieces of long items, merged in the same launch) where the
+// pipelined kernel runs it: D = 128, GQA pairs, pages of >= 16 keys, 16-bit or fp8
+// pools, and at most kSplitMaxItems items (bounded from host sizes: a sequence of L
+// queries has ceil(L / 128) items, so there are at most min(num_seqs * ceil(max_q /
+// 128), ceil(num_tokens / 128) + num_seqs)) over at most kSplitMaxCols columns.
+void plan_split(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk,
+                int32_t d, int32_t block_size, int32_t max_q, int32_t q_dtype, int32_t kv_dtype,
+                const Options& o) {
+  if (o.prefill_pieces < 2 || o.prefill_staging != 0 || d != 128 ||
+      mvllm::prefill_item_heads(hq / hk) != 2 || block_size < 16) {
+    return;
+  }
+  if (q_dtype != mvllm::kF16 && q_dtype != mvllm::kBF16) return;
+  if (kv_dtype != q_dtype && kv_dtype != mvllm::kFP8E4M3) return;
+  const int64_t q_tiles = (max_q + mvllm::kPrefillQueryTile - 1) / mvllm::kPrefillQueryTile;
+  const int64_t by_seqs = static_cast<int64_t>(num_seqs) * q_tiles;
+  const int64_t by_tokens =
+      (static_cast<int64_t>(num_tokens) + mvllm::kPrefillQueryTile - 1) / mvllm::kPrefillQueryTile +
+      num_seqs;
+  const int64_t items = by_seqs < by_tokens ? by_seqs : by_tokens;
+  const int cols = hq / 2;
+  if (items > mvllm::kSplitMaxItems || cols > mvllm::kSplitMaxCols) return;
+  const int cus = device_cus();
+  plan.pub.prefill_pieces = o.prefill_pieces;
+  plan.split_pct = o.prefill_piece_pct;
+  plan.split_ranks = static_cast<int>(items) + mvllm::split_extra_ranks(cus, cols, plan.split_pct);
+  plan.split_slots = mvllm::split_slots(cus, cols, plan.split_pct);
+  plan.off_split = align256(plan.pub.workspace_bytes);
+  plan.pub.workspace_bytes =
+      plan.off_split + static_cast<uint64_t>(plan.split_slots) * cols * mvllm::kSplitSlotFloats *
+                           sizeof(float);
+}
+
 void plan_prefill(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk,
-                  int32_t d, const Options& o) {
+                  int32_t d, int32_t block_size, int32_t max_q, int32_t q_dtype,
+                  int32_t kv_dtype, const Options& o) {
   if (!plan.pub.prefill_mfma) return;
   plan.register_staging = o.prefill_staging;
   plan.prefill_share_tiles = o.prefill_share_tiles;
-  if (num_seqs > mvllm::kMaxStreamSeqs) return;
   const int forced = o.prefill_schedule;
-  if (forced == 2) return;
   const int64_t items = static_cast<int64_t>((num_tokens + mvllm::kPrefillQueryTile - 1) /
                                              mvllm::kPrefillQueryTile) *
                         (hq / mvllm::prefill_item_heads(hq / hk));
-  if (forced != 1 && 2 * items >= device_cus()) return;
+  if (num_seqs > mvllm::kMaxStreamSeqs || forced == 2 ||
+      (forced != 1 && 2 * items >= device_cus())) {
+    plan_split(plan, num_tokens, num_seqs, hq, hk, d, block_size, max_q, q_dtype, kv_dtype, o);
+    return;
+  }
   int64_t wgs = static_cast<int64_t>(o.prefill_wgs_per_cu) * device_cus();
   if (wgs > mvllm::kMaxPrefillWgs) wgs = mvllm::kMaxPrefillWgs;
   const uint64_t rows = static_cast<uint64_t>(2 * wgs) * mvllm::prefill_item_heads(hq / hk) *
@@ -208,7 +253,7 @@ Plan make_plan(int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t hk, int
   Plan plan{};
   plan_decode(plan, num_tokens, num_seqs, hq, hk, d, block_size, max_q, max_ctx, q_dtype,
               kv_dtype, o);
-  plan_prefill(plan, num_tokens, num_seqs, hq, hk, d, o);
+  plan_prefill(plan, num_tokens, num_seqs, hq, hk, d, block_size, max_q, q_dtype, kv_dtype, o);
   return plan;
 }
 
@@ -285,6 +330,48 @@ void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, i
   }
 }
 
+// Arrival counters of the split prefill grid, in a static device array (each GPU holds
+// its own from the library's load until the process ends; it starts at zero and every
+// launch leaves its counters at zero). A stream takes one region of it on its first
+// split launch and keeps it, so launches that may overlap in time (other streams)
+// never share counters, while one stream's launches run in order. A stream beyond the
+// regions runs its prefill with every item whole. Host code never names the array
+// itself: each device's address comes from hipGetSymbolAddress, kept here.
+constexpr int kCounterRegions = 32;
+constexpr int kCounterInts = mvllm::kSplitMaxItems * mvllm::kSplitMaxCols;
+static __device__ __align__(256) int split_counters[kCounterRegions * kCounterInts];
+
+constexpr int kCounterDevices = 64;
+std::mutex g_counter_mutex;
+int* g_counter_base[kCounterDevices] = {};
+hipStream_t g_counter_owner[kCounterDevices][kCounterRegions] = {};
+bool g_counter_used[kCounterDevices][kCounterRegions] = {};
+
+// The counter region of (current device, stream), or nullptr when there is none to give.
+int* split_counters_for(hipStream_t stream) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kCounterDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_counter_mutex);
+  if (g_counter_base[dev] == nullptr) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(split_counters)) != hipSuccess || ptr == nullptr) {
+      return nullptr;
+    }
+    g_counter_base[dev] = static_cast<int*>(ptr);
+  }
+  int free_region = -1;
+  for (int r = 0; r < kCounterRegions; ++r) {
+    if (g_counter_used[dev][r] && g_counter_owner[dev][r] == stream) {
+      return g_counter_base[dev] + r * kCounterInts;
+    }
+    if (!g_counter_used[dev][r] && free_region < 0) free_region = r;
+  }
+  if (free_region < 0) return nullptr;
+  g_counter_used[dev][free_region] = true;
+  g_counter_owner[dev][free_region] = stream;
+  return g_counter_base[dev] + free_region * kCounterInts;
+}
+
 // Fills the plan's schedule fields and workspace pointers into `p` and launches the
 // decode and prefill kernels the plan names (shared by the paged and dense entries).
 int launch_planned(const Plan& plan, mvllm::PagedParams& p, void* workspace, int32_t q_dtype,
@@ -307,6 +394,17 @@ int launch_planned(const Plan& plan, mvllm::PagedParams& p, void* workspace, int
       p.pf_prefix = reinterpret_cast<int*>(ws + plan.off_pf);
       p.pf_o = reinterpret_cast<float*>(ws + plan.off_pf_o);
       p.pf_ml = reinterpret_cast<float*>(ws + plan.off_pf_ml);
+    }
+    if (plan.pub.prefill_pieces > 1) {
+      p.pf_count = split_counters_for(s);
+      if (p.pf_count != nullptr) {
+        p.pf_pieces = plan.pub.prefill_pieces;
+        p.pf_ranks = plan.split_ranks;
+        p.pf_slots = plan.split_slots;
+        p.pf_cus = device_cus();
+        p.pf_piece_pct = plan.split_pct;
+        p.pf_part = reinterpret_cast<float*>(ws + plan.off_split);
+      }
     }
   }
   if (plan.pub.decode_mode != MVLLM_DECODE_NONE) {
@@ -477,7 +575,7 @@ extern "C" {
 
 const char* mvllm_last_error(void) { return g_error; }
 
-int mvllm_abi_version(void) { return 10; }
+int mvllm_abi_version(void) { return 11; }
 
 #ifndef MVLLM_SOURCE_HASH
 #define MVLLM_SOURCE_HASH "unstamped"
@@ -541,8 +639,14 @@ int paged_attention_entry(const char* name, void* out, const void* q, const void
                 "paged_attention: k_scales and v_scales are required for a float8 pool and "
                 "only for one");
   }
-  const Plan plan = make_plan(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim,
-                              block_size, max_query_len, max_context_len, q_dtype, kv_dtype, o);
+  Plan plan = make_plan(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
+                        max_query_len, max_context_len, q_dtype, kv_dtype, o);
+  if (static_scratch && plan.pub.workspace_bytes > workspace_bytes && plan.pub.prefill_pieces > 1) {
+    // The split grid's partial slots do not fit the static scratch: items stay whole.
+    o.prefill_pieces = 1;
+    plan = make_plan(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
+                     max_query_len, max_context_len, q_dtype, kv_dtype, o);
+  }
   const uint64_t need = plan.pub.workspace_bytes;
   if (static_scratch && need > workspace_bytes) {
     return fail(MVLLM_ERR_UNSUPPORTED,

@@ -40,6 +40,30 @@ __host__ __device__ inline int64_t prefill_stream_shares(int64_t total_units, in
 constexpr int kXcds = 8;
 constexpr int kPrefillKeyTile = 64;
 
+// Split grid (prefill): items longer than a piece length (a percentage of the mean work
+// per CU, kSplitDefaultPct by default) are cut into key
+// ranges ("pieces") run by workgroups of their own in one launch, longest piece first;
+// the last piece of an item to finish merges the others' (m, l, O) partials. Every
+// workgroup derives the same schedule from the sequences' sizes, one wave lane per
+// item, so the items of one call are at most kSplitMaxItems and the columns at most
+// kSplitMaxCols (the counters' extent).
+constexpr int kSplitMaxItems = 64;
+constexpr int kSplitMaxCols = 64;
+constexpr int kSplitDefaultPieces = 8;
+// Floats of one piece's partial: 8 waves x 64 lanes x (64 of O + (m, l)).
+constexpr int kSplitSlotFloats = 8 * 64 * 66;
+constexpr int kSplitDefaultPct = 150;
+// Host bounds of the split grid over `cols` columns on `cus` CUs with pieces of at least
+// pct% of the mean work per CU: the extra pieces of one column number fewer than
+// 100 cus / (pct cols); the partial slots of one column (every piece of a cut item
+// holds one) at most twice that.
+__host__ __device__ inline int split_extra_ranks(int cus, int cols, int pct) {
+  return (100 * cus + pct * cols - 1) / (pct * cols);
+}
+__host__ __device__ inline int split_slots(int cus, int cols, int pct) {
+  return 2 * split_extra_ranks(cus, cols, pct);
+}
+
 // Query heads per prefill work item: two heads of a GQA group share every K/V tile
 // staged in LDS when the group size is even.
 __host__ __device__ inline int prefill_item_heads(int group) { return group % 2 == 0 ? 2 : 1; }
@@ -118,9 +142,20 @@ struct PagedParams {
   float* pf_o;        // stream prefill partials: [2 * pf_wgs][heads][128][D] fp32, each
                       // piece normalised by its own sum
   float* pf_ml;       // their (max in log2 units, sum) per row: [2 * pf_wgs][heads][128][2]
-  int pf_share_tiles;       // stream prefill: fewest key tiles per share
+  int pf_share_tiles;       // stream prefill: fewest key tiles per share; split grid:
+                            // fewest key tiles per piece
   int pf_register_staging;  // 1: the register-staged prefill kernel even where the
                             // direct-to-LDS one serves (a plan option, for measurement)
+  int pf_pieces;      // split grid: > 1 cuts long items into at most this many pieces (a
+                      // 1-D grid of pf_ranks x columns); otherwise the (column,
+                      // sequence, query tile) grid with every item whole
+  int pf_ranks;       // split grid: grid extent in ranks (items + extra pieces bound)
+  int pf_slots;       // split grid: partial slots per column
+  int pf_cus;         // split grid: the device's CUs
+  int pf_piece_pct;   // split grid: piece length, percent of the mean tiles per CU
+  int* pf_count;      // split grid: [kSplitMaxItems][columns] arrival counters, zero
+                      // before the launch and left zero by it
+  float* pf_part;     // split grid: [pf_slots][columns] partials of kSplitSlotFloats
 };
 
 // Splits of one row: as many as its visible context needs at `split_tokens` keys

@@ -264,6 +264,155 @@ __device__ __forceinline__ bool prefill_work(const PagedParams& p, int cols, int
   return true;
 }
 
+// The split grid's piece at position `rank` (workgroup blockIdx.x / columns; the first
+// pf_ranks - (pieces) positions are empty, then the pieces in rank order), computed by one
+// wave from the sequences' sizes (no host read, no other launch; every workgroup
+// derives the same schedule). Items (sequence, query tile) are numbered sequence by
+// sequence, lane i holding item i:
+//  * piece length L = max(fewest tiles, ceil(pct% of the mean tiles per CU)); an item
+//    of nt tiles is cut into P = min(pieces, ceil(nt / L)) key ranges of floor-divided
+//    tiles (P - 1 < nt / L, so the extra pieces number fewer than 100 cus / (pct cols)
+//    and the cut items' pieces fewer than twice that: within the grid's ranks and
+//    slots; an item that would still pass them, counted with every earlier item's
+//    pieces, stays whole);
+//  * ranks go longest piece first (ties by item index), an item's pieces consecutive;
+//  * a cut item's pieces hold partial slots slot0 .. slot0 + P - 1 (prefix over the
+//    cut items in index order).
+// Scans are DPP; the all-pairs rank count reads every item's (longest piece,
+// pieces) from LDS with broadcast loads, so no step is a chain of per-item scalar reads.
+// False for an empty position (the grid is a host-side bound).
+struct SplitPiece {
+  int s, q, item, piece, pieces, slot0, tb, te;
+};
+
+struct SplitLds {
+  int4 rec[kSplitMaxItems];  // item i: (sequence, query tile, tiles, 0)
+  int2 kp[kSplitMaxItems];   // item i: (its longest piece, its pieces)
+  int out[10];               // the schedule's result for the other waves
+};
+
+// Inclusive prefix sum over the wave's 64 lanes: DPP row shifts 1, 2, 4, 8 (within
+// each 16-lane row; a lane whose source lies outside its row adds 0), then lane 15's
+// row total broadcast into rows 1 and 3 and lane 31's into rows 2 and 3.
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return v;
+}
+
+__device__ __forceinline__ bool split_piece_wave(const PagedParams& p, int cols, int rank,
+                                                 SplitLds& lds, SplitPiece& out) {
+  const int lane = threadIdx.x % kWave;
+  const int n = p.num_seqs;
+  // Items in sequence order: lane s of each 64-sequence chunk lists its query tiles.
+  // (One wave's LDS accesses complete in order, so its lanes read what others wrote.)
+  int items = 0;
+  for (int base = 0; base < n; base += kWave) {
+    int len = 0, ctx = 0;
+    if (base + lane < n) {
+      len = p.seq_lens[base + lane];
+      ctx = p.context_lens[base + lane];
+    }
+    const int qts = len > 1 ? (len + kPrefillQueryTile - 1) / kPrefillQueryTile : 0;
+    const int pre = items + wave_inclusive_scan(qts) - qts;
+    for (int q = 0; q < qts && pre + q < kSplitMaxItems; ++q) {
+      lds.rec[pre + q] = make_int4(base + lane, q, prefill_item_tiles(ctx, len, q), 0);
+    }
+    items = __builtin_amdgcn_readlane(pre + qts, kWave - 1);
+  }
+  items = min(items, kSplitMaxItems);  // the host bound rules out more
+  const bool have = lane < items;
+  const int4 r = have ? lds.rec[lane] : make_int4(0, 0, 0, 0);
+  const int nt = r.z;
+  const int total = __builtin_amdgcn_readlane(wave_inclusive_scan(nt), kWave - 1);
+  // pct percent of the mean tiles per CU, rounded up
+  const int64_t scaled = static_cast<int64_t>(p.pf_piece_pct) * total * cols;
+  int piece_len = static_cast<int>((scaled + 100 * p.pf_cus - 1) / (100 * p.pf_cus));
+  piece_len = max(piece_len, max(p.pf_share_tiles, 1));
+  int pcs = have ? max(min(p.pf_pieces, (nt + piece_len - 1) / piece_len), 1) : 0;
+  // Extra pieces (low 16 bits) and cut items' slots (high 16 bits) before this item;
+  // both stay below 64 x 64.
+  const int both = (have ? pcs - 1 : 0) | ((pcs > 1 ? pcs : 0) << 16);
+  const int before = wave_inclusive_scan(both) - both;
+  const int extra_before = before & 0xffff, slots_before = before >> 16;
+  if (pcs > 1 && (items + extra_before + pcs - 1 > p.pf_ranks || slots_before + pcs > p.pf_slots)) {
+    pcs = 1;
+  }
+  const int cut = pcs > 1 ? pcs : 0;
+  const int slot0 = wave_inclusive_scan(cut) - cut;
+  // The grid's first positions are the ranks it has beyond the pieces (empty): they
+  // end here, while every CU is still free, rather than after the last piece.
+  const int ranks = items + __builtin_amdgcn_readlane(wave_inclusive_scan(have ? pcs - 1 : 0), kWave - 1);
+  rank -= p.pf_ranks - ranks;
+  if (rank < 0) return false;
+  const int key = have ? (nt + pcs - 1) / pcs : 0;
+  lds.kp[lane] = make_int2(key, pcs);
+  // Pieces ranked before this item's first: every item's pair read with 16-byte
+  // broadcast loads, all of a half issued before any is used.
+  int start = 0;
+#pragma unroll
+  for (int h = 0; h < kSplitMaxItems; h += kSplitMaxItems / 2) {
+    int4 two[kSplitMaxItems / 4];
+#pragma unroll
+    for (int k = 0; k < kSplitMaxItems / 4; ++k) two[k] = *reinterpret_cast<const int4*>(&lds.kp[h + 2 * k]);
+#pragma unroll
+    for (int k = 0; k < kSplitMaxItems / 4; ++k) {
+      const int j = h + 2 * k;
+      if (two[k].x > key || (two[k].x == key && j < lane)) start += two[k].y;
+      if (two[k].z > key || (two[k].z == key && j + 1 < lane)) start += two[k].w;
+    }
+  }
+  const uint64_t mine = __builtin_amdgcn_ballot_w64(have && start <= rank && rank < start + pcs);
+  if (mine == 0) return false;
+  const int i = __builtin_ctzll(mine);
+  out.s = __builtin_amdgcn_readlane(r.x, i);
+  out.q = __builtin_amdgcn_readlane(r.y, i);
+  out.item = i;
+  out.pieces = __builtin_amdgcn_readlane(pcs, i);
+  out.piece = rank - __builtin_amdgcn_readlane(start, i);
+  out.slot0 = __builtin_amdgcn_readlane(slot0, i);
+  const int nti = __builtin_amdgcn_readlane(nt, i);
+  out.tb = out.piece * nti / out.pieces;
+  out.te = (out.piece + 1) * nti / out.pieces;
+  return true;
+}
+
+// Every wave's copy of the schedule: wave 0 computes it, the workgroup's barrier
+// publishes it. False (for the whole workgroup) past the last piece.
+__device__ __forceinline__ bool split_piece(const PagedParams& p, int cols, int rank,
+                                            SplitLds& lds, SplitPiece& out) {
+  if (threadIdx.x < kWave) {
+    SplitPiece mine{};
+    const bool got = split_piece_wave(p, cols, rank, lds, mine);
+    if (threadIdx.x == 0) {
+      lds.out[0] = got ? 1 : 0;
+      lds.out[1] = mine.s;
+      lds.out[2] = mine.q;
+      lds.out[3] = mine.item;
+      lds.out[4] = mine.piece;
+      lds.out[5] = mine.pieces;
+      lds.out[6] = mine.slot0;
+      lds.out[7] = mine.tb;
+      lds.out[8] = mine.te;
+    }
+  }
+  __syncthreads();
+  if (__builtin_amdgcn_readfirstlane(lds.out[0]) == 0) return false;
+  out.s = __builtin_amdgcn_readfirstlane(lds.out[1]);
+  out.q = __builtin_amdgcn_readfirstlane(lds.out[2]);
+  out.item = __builtin_amdgcn_readfirstlane(lds.out[3]);
+  out.piece = __builtin_amdgcn_readfirstlane(lds.out[4]);
+  out.pieces = __builtin_amdgcn_readfirstlane(lds.out[5]);
+  out.slot0 = __builtin_amdgcn_readfirstlane(lds.out[6]);
+  out.tb = __builtin_amdgcn_readfirstlane(lds.out[7]);
+  out.te = __builtin_amdgcn_readfirstlane(lds.out[8]);
+  return true;
+}
+
 }  // namespace
 
 template <typename TQ, typename TKV, int D, int HCW, int HS>
@@ -1084,7 +1233,7 @@ __global__ __launch_bounds__(256 * HS) void paged_prefill_lds_kernel(const Paged
 // Staging maps and the softmax are those of paged_prefill_lds_kernel, except that K
 // rows are swizzled over 16 chunks (key & 15) instead of 8; K/V slots rotate by three and the score accumulators by two, so the loop is unrolled by
 // six with every buffer named at compile time.
-template <typename TQ, typename TKV>
+template <typename TQ, typename TKV, bool kSplit>
 __global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedParams p) {
   constexpr bool kFp8 = std::is_same_v<TKV, fp8_t>;
   constexpr int D = 128;
@@ -1145,20 +1294,39 @@ __global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedPara
   const int hs = wave / 4;  // head of the pair
   const int wq = wave % 4;  // 32-position query block
 
-  // ---- the work item: (sequence blockIdx.y, column blockIdx.x, query tile), query
-  // tiles dispatched longest first.
+  // ---- the work item: (sequence, column, query tile) and the key tiles [tb, te) of
+  // it this workgroup walks. Item grid: sequence blockIdx.y, column blockIdx.x, query
+  // tiles dispatched longest first, every item whole. Split grid: the piece of rank
+  // blockIdx.x / columns (split_piece), column blockIdx.x % columns, so one XCD keeps
+  // the same columns (and their K/V) as in the item grid.
   const int group = p.hq / p.hk;
   const int chunks = group / HW;
-  const int s = blockIdx.y;
+  int s, qt, c, tb, te;
+  SplitPiece piece{};
+  if constexpr (kSplit) {
+    const int cols = p.hk * chunks;
+    c = static_cast<int>(blockIdx.x) % cols;
+    __shared__ SplitLds split_lds;
+    if (!split_piece(p, cols, static_cast<int>(blockIdx.x) / cols, split_lds, piece)) return;
+    s = uniform(piece.s);
+    qt = uniform(piece.q);
+    tb = uniform(piece.tb);
+    te = uniform(piece.te);
+  } else {
+    s = blockIdx.y;
+    qt = static_cast<int>(gridDim.z) - 1 - static_cast<int>(blockIdx.z);
+    c = blockIdx.x;
+  }
   const int len = sload(p.seq_lens + s);
   const int context = sload(p.context_lens + s);
-  if (len <= 1) return;  // a decode row: the decode kernel has it
-  const int qtiles = (len + kPrefillQueryTile - 1) / kPrefillQueryTile;
-  const int qt = static_cast<int>(gridDim.z) - 1 - static_cast<int>(blockIdx.z);
-  if (qt >= qtiles) return;
-  const int c = blockIdx.x;
+  if constexpr (!kSplit) {
+    if (len <= 1) return;  // a decode row: the decode kernel has it
+    const int qtiles = (len + kPrefillQueryTile - 1) / kPrefillQueryTile;
+    if (qt >= qtiles) return;
+    tb = 0;
+    te = prefill_item_tiles(context, len, qt);
+  }
   const int kvh = c / chunks;
-  const int nt = prefill_item_tiles(context, len, qt);
 
   const float score_c = p.scale * kLog2e;  // > 0 (the dispatcher's condition)
   const char* kpool = static_cast<const char*>(p.k_pool);
@@ -1219,7 +1387,7 @@ __global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedPara
 
   // Page id of this wave's keys of tile t (past the last tile: the last tile again).
   auto page_of = [&](int t) __attribute__((always_inline)) -> int {
-    const int key0 = min(min(t, nt - 1) * kTileKeys + KW * wave, context - 1);
+    const int key0 = min(min(t, te - 1) * kTileKeys + KW * wave, context - 1);
     return sload(table + (key0 >> p.block_shift));
   };
   // fp8 pools: the page's K and V scales of each staged slot (the wave's keys share a
@@ -1227,7 +1395,7 @@ __global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedPara
   float ks[3] = {0.0f, 0.0f, 0.0f}, vs[3] = {0.0f, 0.0f, 0.0f};
   auto stage = [&](int t, int page, auto slot) __attribute__((always_inline)) {
     constexpr int X = decltype(slot)::value;
-    t = min(t, nt - 1);
+    t = min(t, te - 1);
     const uint32_t kdst = lds_address(k_arr(slot) + KW * wave * kRawRow);
     const uint32_t rdst = lds_address(r_arr(slot) + KW * wave * kRawRow);
     const int key0 = t * kTileKeys + KW * wave;
@@ -1461,12 +1629,12 @@ __global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedPara
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
 
-  // ---- prologue: tiles 0-2 staged, page ids of tiles 3-5 fetched; tile 0's V^T built
-  // and its scores computed.
-  stage(0, page_of(0), I0{});
-  stage(1, page_of(1), I1{});
-  stage(2, page_of(2), I2{});
-  int pg[3] = {page_of(3), page_of(4), page_of(5)};  // pg[x]: next tile staged into slot x
+  // ---- prologue: tiles tb .. tb + 2 staged, page ids of the next three fetched; tile
+  // tb's V^T built and its scores computed. Slots and buffers go by t - tb.
+  stage(tb, page_of(tb), I0{});
+  stage(tb + 1, page_of(tb + 1), I1{});
+  stage(tb + 2, page_of(tb + 2), I2{});
+  int pg[3] = {page_of(tb + 3), page_of(tb + 4), page_of(tb + 5)};  // pg[x]: next tile staged into slot x
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kStageOps) : "memory");
   if constexpr (kFp8) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // tile 0's scales
@@ -1474,10 +1642,11 @@ __global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedPara
   }
   store_v(I0{}, I0{});
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  if (w_nt > 0) qk(I0{}, I0{}, sc0);
+  if (tb < w_nt) qk(I0{}, I0{}, sc0);
 
-  // Step for tile t: X = t % 3 (the slots tile t used, restaged with tile t + 3), Y =
-  // (t + 1) % 3 (tile t + 1's slots), P = t & 1 (tile t's score and V^T buffers).
+  // Step for tile t: X = (t - tb) % 3 (the slots tile t used, restaged with tile t + 3),
+  // Y = (t - tb + 1) % 3 (tile t + 1's slots), P = (t - tb) & 1 (tile t's score and V^T
+  // buffers).
   auto step = [&](int t, auto xs, auto par) __attribute__((always_inline)) {
     constexpr int X = decltype(xs)::value;
     constexpr int Y = (X + 1) % 3;
@@ -1515,16 +1684,94 @@ __global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedPara
       l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
     }
   };
-  for (int t = 0; t < nt; t += 6) {
+  for (int t = tb; t < te; t += 6) {
     step(t, I0{}, I0{});
-    if (t + 1 < nt) step(t + 1, I1{}, I1{});
-    if (t + 2 < nt) step(t + 2, I2{}, I0{});
-    if (t + 3 < nt) step(t + 3, I0{}, I1{});
-    if (t + 4 < nt) step(t + 4, I1{}, I0{});
-    if (t + 5 < nt) step(t + 5, I2{}, I1{});
+    if (t + 1 < te) step(t + 1, I1{}, I1{});
+    if (t + 2 < te) step(t + 2, I2{}, I0{});
+    if (t + 3 < te) step(t + 3, I0{}, I1{});
+    if (t + 4 < te) step(t + 4, I1{}, I0{});
+    if (t + 5 < te) step(t + 5, I2{}, I1{});
   }
   // No copy may still be writing LDS when the workgroup ends.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if constexpr (kSplit) {
+    // A cut item: every piece stores its (m, l, O) partial (each lane its own, in the
+    // lane order every piece shares), then counts itself in; the last to arrive
+    // resets the counter for the next launch and merges the other pieces' partials
+    // into its own accumulators before the usual normalise and store.
+    //
+    // The partials are written and read with relaxed atomic stores and loads at agent
+    // (device) scope, which the hardware keeps coherent per location across the XCDs'
+    // L2s (scope bits on each access) rather than with a fence: an agent-scope fence
+    // writes back and invalidates the whole L2 of the XCD, dropping the K/V lines
+    // every other workgroup there is reading (measured: cut pieces ran at 5.6 us per
+    // tile against 3.5). Order: a piece's stores complete (vmcnt(0), every wave, then
+    // the barrier) before its counter increment is issued; the last piece issues its
+    // loads only after the increment has returned, through the barrier that
+    // publishes the result.
+    if (piece.pieces > 1) {
+      __shared__ int split_last;
+      const int cols = p.hk * chunks;
+      auto slot_of = [&](int j) __attribute__((always_inline)) -> float* {
+        return p.pf_part + (static_cast<int64_t>(piece.slot0 + j) * cols + c) * kSplitSlotFloats;
+      };
+      auto o_at = [&](float* slot, int k) __attribute__((always_inline)) -> float* {
+        return slot + ((wave * 16 + k) * kWave + lane) * 4;
+      };
+      auto ml_at = [&](float* slot) __attribute__((always_inline)) -> float* {
+        return slot + kWaves * kWave * 64 + (wave * kWave + lane) * 2;
+      };
+      auto put = [&](float* at, float v) __attribute__((always_inline)) {
+        __hip_atomic_store(at, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      };
+      auto get = [&](float* at) __attribute__((always_inline)) -> float {
+        return __hip_atomic_load(at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      };
+      {
+        float* mine = slot_of(piece.piece);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const f32x16& a = o[k >> 2];
+          const int r = 4 * (k & 3);
+          float* at = o_at(mine, k);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) put(at + e, a[r + e]);
+        }
+        put(ml_at(mine), m_run);
+        put(ml_at(mine) + 1, l_run);
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (tid == 0) {
+        int* count = p.pf_count + piece.item * cols + c;
+        const int before = __hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = before == piece.pieces - 1 ? 1 : 0;
+        if (last) __hip_atomic_store(count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        split_last = last;
+      }
+      __syncthreads();
+      if (split_last == 0) return;
+      for (int j = 0; j < piece.pieces; ++j) {
+        if (j == piece.piece) continue;
+        float* other = slot_of(j);
+        const float m_o = get(ml_at(other));
+        const float l_o = get(ml_at(other) + 1);
+        const float m_new = fmaxf(m_run, m_o);
+        const float fa = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+        const float fb = m_o == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_o - m_new);
+        l_run = l_run * fa + l_o * fb;
+        m_run = m_new;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          f32x16& a = o[k >> 2];
+          const int r = 4 * (k & 3);
+          float* at = o_at(other, k);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a[r + e] = a[r + e] * fa + get(at + e) * fb;
+        }
+      }
+    }
+  }
   if (!w_active || !my_valid) return;
   const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
@@ -1706,6 +1953,19 @@ void launch_prefill_cfg(const PagedParams& p, int max_query_len, hipStream_t str
   }
 }
 
+// The pipelined kernel on the item grid, or on the split grid when the plan cuts items
+// (pf_pieces > 1, with the counters and partial slots it names).
+template <typename TQ, typename TKV>
+void launch_prefill_pipe(const PagedParams& p, int max_query_len, hipStream_t stream) {
+  const int cols = p.hk * (p.hq / p.hk / 2);
+  if (p.pf_pieces > 1 && p.pf_count != nullptr && p.pf_part != nullptr) {
+    paged_prefill_pipe_kernel<TQ, TKV, true><<<cols * p.pf_ranks, 512, 0, stream>>>(p);
+    return;
+  }
+  const int qtiles = (max_query_len + kPrefillQueryTile - 1) / kPrefillQueryTile;
+  paged_prefill_pipe_kernel<TQ, TKV, false><<<dim3(cols, p.num_seqs, qtiles), 512, 0, stream>>>(p);
+}
+
 template <typename TQ, int HS>
 void launch_prefill_lds(const PagedParams& p, int max_query_len, hipStream_t stream) {
   if (p.pf_wgs > 0) {
@@ -1717,7 +1977,7 @@ void launch_prefill_lds(const PagedParams& p, int max_query_len, hipStream_t str
     const dim3 grid(cols, p.num_seqs, qtiles);
     if constexpr (HS == 2) {
       if (!p.pf_register_staging) {
-        paged_prefill_pipe_kernel<TQ, TQ><<<grid, 512, 0, stream>>>(p);
+        launch_prefill_pipe<TQ, TQ>(p, max_query_len, stream);
         return;
       }
     }
@@ -1744,9 +2004,7 @@ hipError_t launch_prefill_d(const PagedParams& p, int max_query_len, hipStream_t
   if constexpr (std::is_same_v<TKV, fp8_t> && D == 128) {
     if (p.block_shift >= 4 && p.scale > 0.0f && !p.pf_register_staging && p.pf_wgs == 0 &&
         prefill_item_heads(p.hq / p.hk) == 2) {
-      const int cols = p.hk * (p.hq / p.hk / 2);
-      const int qtiles = (max_query_len + kPrefillQueryTile - 1) / kPrefillQueryTile;
-      paged_prefill_pipe_kernel<TQ, fp8_t><<<dim3(cols, p.num_seqs, qtiles), 512, 0, stream>>>(p);
+      launch_prefill_pipe<TQ, fp8_t>(p, max_query_len, stream);
       return hipGetLastError();
     }
   }

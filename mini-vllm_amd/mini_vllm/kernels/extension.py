@@ -60,7 +60,7 @@ HIP_FLAGS = [
 # reference's PyTorch expressions round, so FMA contraction is off there.
 EXTRA_FLAGS = {"elementwise.hip": ["-ffp-contract=off"], "linear.hip": ["-ffp-contract=off"]}
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 DTYPE_CODES: dict[torch.dtype, int] = {
     torch.float32: 0,
@@ -184,7 +184,8 @@ class _PlanOptions(ctypes.Structure):
         ("prefill_wgs_per_cu", ctypes.c_int32),
         ("prefill_staging", ctypes.c_int32),
         ("prefill_share_tiles", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("prefill_pieces", ctypes.c_int32),
+        ("prefill_piece_pct", ctypes.c_int32),
     ]
 
 
@@ -196,7 +197,7 @@ def make_plan_options(options: dict[str, Any] | None) -> "_PlanOptions | None":
     "stream" / "grid" / "heads"); None for the planner's defaults."""
     if not options:
         return None
-    fields = {name for name, _ in _PlanOptions._fields_} - {"reserved"}
+    fields = {name for name, _ in _PlanOptions._fields_}
     unknown = set(options) - fields
     if unknown:
         raise ValueError(f"unknown plan options {sorted(unknown)}; known: {sorted(fields)}")
@@ -213,7 +214,7 @@ class _Plan(ctypes.Structure):
         ("prefill_mfma", ctypes.c_int32),
         ("workspace_bytes", ctypes.c_uint64),
         ("prefill_workgroups", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("prefill_pieces", ctypes.c_int32),
     ]
 
 

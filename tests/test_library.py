@@ -78,15 +78,36 @@ def _plan(lib, *args, options=None):
     return plan
 
 
-def test_prefill_grid_schedule_needs_no_workspace(lib):
-    # enough 128-query items to fill the CUs: the grid schedule
+SLOT_BYTES = 8 * 64 * 66 * 4  # one piece's (m, l, O) partial: 8 waves x 64 lanes
+
+
+def test_prefill_grid_schedule_workspace(lib):
+    """Enough 128-query items to fill the CUs: the grid schedule. Where the pipelined
+    kernel runs it (D 128, GQA pairs, 16-bit or fp8 pools, <= 64 items) it may cut long
+    items into pieces, whose partial slots are the only workspace it needs; with
+    prefill_pieces = 1 (or where the pipelined kernel does not run) it needs none."""
     plan = _plan(lib, 4096, 8, 16, 8, 128, 16, 512, 2048, 2, 2)
-    assert plan.prefill_mfma == 1 and plan.prefill_workgroups == 0 and plan.workspace_bytes == 0
-    plan = _plan(lib, 512, 1, 16, 8, 128, 16, 512, 8192, 2, 2, options={"prefill_schedule": "grid"})
+    assert plan.prefill_mfma == 1 and plan.prefill_workgroups == 0
+    assert plan.prefill_pieces == 8
+    # at most 2 * ceil(100 cus / (150 cols)) slots per column, 8 columns (256 CUs without
+    # a GPU)
+    assert 0 < plan.workspace_bytes <= 2 * 22 * 8 * SLOT_BYTES + 256
+    whole = _plan(lib, 4096, 8, 16, 8, 128, 16, 512, 2048, 2, 2, options={"prefill_pieces": 1})
+    assert whole.prefill_pieces == 0 and whole.workspace_bytes == 0
+    fp8 = _plan(lib, 4096, 8, 16, 8, 128, 16, 512, 2048, 2, 3)
+    assert fp8.prefill_pieces == 8
+    for args in [(4096, 8, 16, 8, 64, 16, 512, 2048, 2, 2),    # D 64: the item kernel
+                 (4096, 8, 12, 4, 128, 16, 512, 2048, 2, 2),   # groups of 3: one head a wave
+                 (4096, 8, 16, 8, 128, 8, 512, 2048, 2, 2),    # pages of 8 keys
+                 (8192, 128, 16, 8, 128, 16, 64, 2048, 2, 2)]:  # 128 items > 64
+        other = _plan(lib, *args)
+        assert other.prefill_pieces == 0 and other.workspace_bytes == 0, args
+    plan = _plan(lib, 512, 1, 16, 8, 128, 16, 512, 8192, 2, 2,
+                 options={"prefill_schedule": "grid", "prefill_pieces": 1})
     assert plan.prefill_workgroups == 0 and plan.workspace_bytes == 0
     plan = _plan(lib, 4096, 8, 16, 8, 128, 16, 512, 2048, 2, 2,
                  options={"prefill_schedule": "stream"})
-    assert plan.prefill_workgroups > 0
+    assert plan.prefill_workgroups > 0 and plan.prefill_pieces == 0
 
 
 def test_plan_options_are_explicit_and_checked(lib, monkeypatch):

@@ -233,6 +233,68 @@ def test_fp8_prefill_on_the_pipelined_grid_kernel(extension, device, block_size)
     check(extension, b, dtype=torch.float8_e4m3fn, options={"prefill_schedule": "grid"})
 
 
+def _split(pieces, share_tiles=1):
+    return {"prefill_schedule": "grid", "prefill_pieces": pieces,
+            "prefill_share_tiles": share_tiles}
+
+
+@pytest.mark.parametrize("pieces", [2, 3, 16])
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
+def test_split_grid_cuts_long_items(extension, device, pieces, kv_dtype):
+    """The grid cuts items longer than ~1.2x the mean work per CU into key ranges run by
+    workgroups of their own in the same launch, the last piece to finish merging the
+    others: a 6000-key prefix beside short chunks (its items cut into up to 5 pieces),
+    ragged chunk ends, a decode row, an fp8 pool."""
+    b = case([6000, 700, 130, 65, 3000], [512, 300, 130, 1, 200], device, dtype=torch.bfloat16,
+             kv_dtype=kv_dtype, num_q_heads=16, num_kv_heads=8, head_dim=128)
+    plan = extension.paged_attention_plan(b.q.shape[0], 5, 16, 8, 128, 16, 512, 6000,
+                                          torch.bfloat16, kv_dtype, plan_options=_split(pieces))
+    assert plan["prefill_pieces"] == pieces and plan["workspace_bytes"] > 0
+    check(extension, b, dtype=kv_dtype, options=_split(pieces))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_split_grid_one_long_prompt(extension, device, dtype):
+    """One sequence alone: every item long against the mean, so each is cut (up to 7
+    pieces of ~13 tiles); the pieces' merge order differs from call to call, the result
+    within tolerance every time, and the arrival counters are left at zero for the next
+    call (three calls in a row, each checked)."""
+    b = case([6100], [512], device, dtype=dtype, num_q_heads=16, num_kv_heads=8, head_dim=128)
+    want = oracle(b)
+    for _ in range(3):
+        got = kernel(extension, b, _split(16))
+        assert_max_abs(got, want, ATTN_ATOL[dtype], "split, one long prompt")
+
+
+def test_split_grid_matches_the_whole_item_grid(extension, device):
+    """Config 3's shape on the split grid (the default) and with every item whole: both
+    within tolerance of the oracle and of each other."""
+    b = config_batch(3, device=device)
+    whole = kernel(extension, b, {"prefill_schedule": "grid", "prefill_pieces": 1})
+    split = kernel(extension, b, {"prefill_schedule": "grid"})
+    assert_max_abs(split.float(), whole.float(), 2 * ATTN_ATOL[torch.bfloat16], "split vs whole")
+
+
+def test_split_grid_piece_lengths_and_bounds(extension, device):
+    """Pieces at the floor of one tile and of many tiles, beside decode rows and a batch
+    of 64 items (the most the split schedule takes), and of 65 (items stay whole)."""
+    b = case([2000, 900, 64, 3000, 17], [512, 1, 64, 512, 1], device, dtype=torch.bfloat16,
+             num_q_heads=16, num_kv_heads=8, head_dim=128)
+    for tiles in (1, 8, 64):
+        check(extension, b, options=_split(4, tiles))
+    for seqs in (64, 65):
+        gen = torch.Generator().manual_seed(seqs)
+        ctx = torch.randint(40, 1500, (seqs,), generator=gen).tolist()
+        lens = [min(c, 100) for c in ctx]
+        bb = case(ctx, lens, device, dtype=torch.bfloat16, num_q_heads=16, num_kv_heads=8,
+                  head_dim=128)
+        plan = extension.paged_attention_plan(bb.q.shape[0], seqs, 16, 8, 128, 16, max(lens),
+                                              max(ctx), torch.bfloat16, torch.bfloat16,
+                                              plan_options=_split(4))
+        assert (plan["prefill_pieces"] > 1) == (seqs <= 64)
+        check(extension, bb, options=_split(4))
+
+
 @pytest.mark.parametrize("schedule", ["stream", "grid"])
 @pytest.mark.parametrize("scale", [-0.3, 0.0, 2.0])
 def test_prefill_with_unusual_scales(extension, device, scale, schedule):

@@ -56,12 +56,23 @@ def test_noalloc_equals_the_workspace_entry_on_two_calls(extension, device, kv_d
 
 
 def test_noalloc_mixed_batch_with_the_grid_prefill(extension, device):
-    """Decodes beside prefill chunks: the prefill on the grid schedule (no scratch), the
-    decode partials in the static array; then a smaller decode-only call."""
+    """Decodes beside prefill chunks: the prefill on the grid schedule with every item
+    whole (no scratch), the decode partials in the static array; then a smaller
+    decode-only call. With the planner's defaults the workspace entry may cut long items
+    into pieces whose partials do not fit the static scratch: the allocation-free entry
+    then keeps its items whole, the same result as the workspace entry asked for whole
+    items, and within the bf16 tolerance of the cut run."""
     b = build_batch([1500, 700, 64, 300], [1, 300, 64, 1], dtype=torch.bfloat16,
                     num_q_heads=16, num_kv_heads=8, head_dim=128, seed=23, device=device)
-    got, want = _both(extension, b, {"prefill_schedule": "grid"})
+    whole = {"prefill_schedule": "grid", "prefill_pieces": 1}
+    got, want = _both(extension, b, whole)
     assert torch.equal(got, want)
+    cut = extension.paged_attention(*b.args(), plan_options={"prefill_schedule": "grid"})
+    default = torch.full_like(cut, float("nan"))
+    assert _noalloc(extension, b, default, {"prefill_schedule": "grid"}) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(default, want)
+    assert (cut.float() - want.float()).abs().max().item() <= 2e-2
     small = build_batch([40, 5], [1, 1], dtype=torch.bfloat16, num_q_heads=16, num_kv_heads=8,
                         head_dim=128, seed=24, device=device)
     got, want = _both(extension, small)
