@@ -153,6 +153,30 @@ def run_engine(requests: int = 256, max_tokens: int = 256, max_sequences: int = 
     }
 
 
+def run_prefill_occupancy(steps: int = 20, tiles: int = 16) -> dict:
+    """Items of `tiles` 64-key tiles (128 queries after a prefix, bf16, GQA 16/8, D 128) on
+    the item grid, as many as half the CUs and as all of them: the per-tile cost of one
+    CU when every CU is busy against when half are (a counter pass under rocprofv3 tells
+    the two launches apart by their grid size)."""
+    from mini_vllm.kernels import ops  # noqa: F401  (strict-mode import side effects)
+    from mini_vllm.kernels.extension import load_extension
+    from mini_vllm.workloads import build_batch
+
+    ext = load_extension()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    out = {}
+    for items in (cus // 2, cus):
+        seqs = items // 8
+        b = build_batch([64 * tiles] * seqs, [128] * seqs, dtype=torch.bfloat16,
+                        num_q_heads=16, num_kv_heads=8, head_dim=128, seed=0, device="cuda",
+                        generator_device="cuda")
+        opts = {"prefill_schedule": "grid", "prefill_pieces": 1}
+        ms = time_steps(lambda i: ext.paged_attention(*b.args(), plan_options=opts), steps, 3)
+        out[f"items{items}"] = {"us": round(ms * 1e3, 1), "us_per_tile": round(ms * 1e3 / tiles, 2)}
+        del b
+    return out
+
+
 def run_kv_write(steps: int = 20) -> dict:
     """The paged KV write (one layer, 8 kv heads x 128, 16-token pages): 2048 tokens (one
     engine iteration's budget) and 65536 tokens (bandwidth), into shuffled slots of a
@@ -531,7 +555,8 @@ def main() -> int:
                              "5 (engine), 5small (engine, 64 x 128 tokens), 5fp8 (engine, fp8 "
                              "KV cache), ew (elementwise "
                              "kernels), kv (KV write), dense (dense-cache attention), linear "
-                             "(decode projections and argmax), gemm (prefill projections), copy")
+                             "(decode projections and argmax), gemm (prefill projections), copy, "
+                             "pfocc (prefill items of 16 tiles on half and on all of the CUs)")
     parser.add_argument("--no-cpu", action="store_true")
     args = parser.parse_args()
 
@@ -619,6 +644,9 @@ def main() -> int:
         log("config 5: Qwen3-0.6B-shaped engine, 256 requests x 256 tokens")
         extras["config5_engine"] = run_engine()
         log(f"config 5 (decode graphs on): {extras['config5_engine']}")
+    if "pfocc" in wanted:
+        extras["prefill_occupancy"] = run_prefill_occupancy()
+        log(f"prefill occupancy: {extras['prefill_occupancy']}")
     if "5small" in wanted:
         # A shorter engine run (64 requests x 128 tokens), sized for a kernel trace.
         extras["config5_engine_small"] = run_engine(requests=64, max_tokens=128)

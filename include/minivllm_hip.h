@@ -100,6 +100,10 @@ typedef struct mvllm_plan_options {
   int32_t prefill_piece_pct;   /* grid prefill: an item is cut into pieces of at least this
                                   percentage of the mean key tiles per CU (default 150,
                                   at least 50) */
+  int32_t decode_merge;        /* stream decode: 0 auto (a merge kernel after the decode
+                                  launch combines cut sequences); 1 forces the merge
+                                  into the decode launch, by each cut sequence's last
+                                  piece (same bits, measured slower) */
 } mvllm_plan_options;
 
 /* Plan a paged_attention call. Depends only on the host-side sizes below and the

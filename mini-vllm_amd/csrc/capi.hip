@@ -72,6 +72,7 @@ struct Options {
   int prefill_staging = 0;
   int prefill_pieces = mvllm::kSplitDefaultPieces;
   int prefill_piece_pct = mvllm::kSplitDefaultPct;
+  int decode_merge = 0;
 };
 
 int read_options(const mvllm_plan_options* o, Options& out) {
@@ -83,7 +84,8 @@ int read_options(const mvllm_plan_options* o, Options& out) {
       o->prefill_staging > 1 || o->decode_wgs_per_cu < 0 || o->decode_waves_per_cu < 0 ||
       o->decode_split_tokens < 0 || o->prefill_wgs_per_cu < 0 || o->prefill_share_tiles < 0 ||
       o->prefill_pieces < 0 || o->prefill_pieces > 64 || o->prefill_piece_pct < 0 ||
-      (o->prefill_piece_pct > 0 && o->prefill_piece_pct < 50) || o->prefill_piece_pct > 10000) {
+      (o->prefill_piece_pct > 0 && o->prefill_piece_pct < 50) || o->prefill_piece_pct > 10000 ||
+      o->decode_merge < 0 || o->decode_merge > 1) {
     return fail(MVLLM_ERR_INVALID, "paged_attention: plan options out of range");
   }
   out.decode_schedule = o->decode_schedule;
@@ -105,6 +107,7 @@ int read_options(const mvllm_plan_options* o, Options& out) {
   out.prefill_staging = o->prefill_staging;
   if (o->prefill_pieces > 0) out.prefill_pieces = o->prefill_pieces;
   if (o->prefill_piece_pct > 0) out.prefill_piece_pct = o->prefill_piece_pct;
+  out.decode_merge = o->decode_merge;
   return MVLLM_OK;
 }
 
@@ -167,6 +170,7 @@ struct Plan {
   int split_ranks = 0;      // split prefill grid: rank extent, partial slots per column,
   int split_slots = 0;      // piece length (percent of the mean tiles per CU)
   int split_pct = 0;
+  int decode_merge_in_launch = 0;  // stream decode: 1 merges cut sequences in the launch
   uint64_t off_split = 0;   // split prefill grid: the partial slots
 };
 
@@ -285,6 +289,7 @@ void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, i
   }
 
   if (plan.pub.decode_mode == MVLLM_DECODE_STREAM) {
+    plan.decode_merge_in_launch = o.decode_merge;
     // A few workgroups per CU, each streaming an equal share of all decode keys; no
     // more workgroups than there are ~64-key shares in the largest possible batch.
     int64_t wgs = static_cast<int64_t>(o.decode_wgs_per_cu) * device_cus();
@@ -330,7 +335,9 @@ void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, i
   }
 }
 
-// Arrival counters of the split prefill grid, in a static device array (each GPU holds
+// Arrival counters of the split prefill grid and of the stream decode's in-launch merge
+// (one launch at a time uses them: a call's decode launch leaves them at zero before
+// its prefill launch starts), in a static device array (each GPU holds
 // its own from the library's load until the process ends; it starts at zero and every
 // launch leaves its counters at zero). A stream takes one region of it on its first
 // split launch and keeps it, so launches that may overlap in time (other streams)
@@ -339,6 +346,7 @@ void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, i
 // itself: each device's address comes from hipGetSymbolAddress, kept here.
 constexpr int kCounterRegions = 32;
 constexpr int kCounterInts = mvllm::kSplitMaxItems * mvllm::kSplitMaxCols;
+static_assert(kCounterInts >= mvllm::kMaxStreamSeqs, "one decode counter per sequence");
 static __device__ __align__(256) int split_counters[kCounterRegions * kCounterInts];
 
 constexpr int kCounterDevices = 64;
@@ -386,7 +394,11 @@ int launch_planned(const Plan& plan, mvllm::PagedParams& p, void* workspace, int
   p.pf_share_tiles = plan.prefill_share_tiles;
   if (plan.pub.workspace_bytes > 0) {
     char* ws = static_cast<char*>(workspace);
-    if (plan.pub.decode_mode == MVLLM_DECODE_STREAM) p.seq_prefix = reinterpret_cast<int*>(ws);
+    if (plan.pub.decode_mode == MVLLM_DECODE_STREAM) {
+      p.seq_prefix = reinterpret_cast<int*>(ws);
+      // Forced (measurement): cut sequences merged in the decode launch, given counters.
+      if (plan.decode_merge_in_launch == 1) p.dec_count = split_counters_for(s);
+    }
     p.part_o = reinterpret_cast<float*>(ws + plan.off_o);
     p.part_ml = reinterpret_cast<float*>(ws + plan.off_ml);
     if (plan.pub.prefill_workgroups > 0) {

@@ -156,6 +156,8 @@ struct PagedParams {
   int* pf_count;      // split grid: [kSplitMaxItems][columns] arrival counters, zero
                       // before the launch and left zero by it
   float* pf_part;     // split grid: [pf_slots][columns] partials of kSplitSlotFloats
+  int* dec_count;     // stream decode: non-null merges cut sequences in the decode launch,
+                      // [num_seqs] arrival counters, zero before the launch and left zero
 };
 
 // Splits of one row: as many as its visible context needs at `split_tokens` keys

@@ -280,6 +280,79 @@ struct Decode {
       }
     }
   }
+
+  // write_partial (heads at consecutive indices) with relaxed agent-scope atomic
+  // stores, for a merge in the same launch by another workgroup.
+  __device__ static void write_partial_coherent(const PagedParams& p, int64_t pidx0, int r,
+                                                const State& st) {
+#pragma unroll
+    for (int h = 0; h < GC; ++h) {
+      const int64_t pidx = pidx0 + h;
+      float* po = p.part_o + pidx * D + r * E;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        __hip_atomic_store(po + e, st.acc[h][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (r == 0) {
+        __hip_atomic_store(p.part_ml + pidx * 2, st.m[h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.part_ml + pidx * 2 + 1, st.l[h], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+
+  // Replace `st` (piece `self` of the sequence) with the merge of all its pieces, folded
+  // in piece order from an empty state exactly as the merge kernel folds them (piece i
+  // in slot (first + i + seq), this piece's own from registers), so the result is the
+  // same whichever piece finishes last; the loads of kBatch pieces are issued together.
+  __device__ static void merge_pieces(const PagedParams& p, int64_t first, int pieces, int self,
+                                      int seq, int h0, int r, State& st) {
+    constexpr int kBatch = 4;
+    auto get = [](const float* at) __attribute__((always_inline)) -> float {
+      return __hip_atomic_load(at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+#pragma unroll
+    for (int h = 0; h < GC; ++h) {
+      float m = -INFINITY, l = 0.0f, o[E];
+#pragma unroll
+      for (int e = 0; e < E; ++e) o[e] = 0.0f;
+      for (int i0 = 0; i0 < pieces; i0 += kBatch) {
+        float mi[kBatch], li[kBatch], oi[kBatch][E];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          const int i = min(i0 + u, pieces - 1);
+          const int64_t pidx = (first + i + seq) * p.hq + h0 + h;
+          if (i == self) {
+            mi[u] = st.m[h];
+            li[u] = st.l[h];
+#pragma unroll
+            for (int e = 0; e < E; ++e) oi[u][e] = st.acc[h][e];
+          } else {
+            mi[u] = get(p.part_ml + pidx * 2);
+            li[u] = get(p.part_ml + pidx * 2 + 1);
+#pragma unroll
+            for (int e = 0; e < E; ++e) oi[u][e] = get(p.part_o + pidx * D + r * E + e);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          if (i0 + u >= pieces) continue;
+          const float mn = fmaxf(m, mi[u]);
+          const float mu = mn == -INFINITY ? 0.0f : mn;
+          const float a = fast_exp2(m - mu);
+          const float b = fast_exp2(mi[u] - mu);
+          l = l * a + li[u] * b;
+#pragma unroll
+          for (int e = 0; e < E; ++e) o[e] = o[e] * a + oi[u][e] * b;
+          m = mn;
+        }
+      }
+      st.m[h] = m;
+      st.l[h] = l;
+#pragma unroll
+      for (int e = 0; e < E; ++e) st.acc[h][e] = o[e];
+    }
+  }
 };
 
 // The (kv head, head chunk) unit of a wave; false when the wave has none.
@@ -296,10 +369,22 @@ __device__ __forceinline__ bool wave_unit(const PagedParams& p, int unit, int& k
 
 // ------------------------------------------------------------ stream schedule
 
-template <typename TQ, typename TKV, int D, int GC>
+// kFuse (a plan option, for measurement): a sequence cut between workgroups is merged
+// by the last of its pieces to finish, in this launch (no merge kernel). Measured
+// slower than the merge kernel: config 2 116-121 us against 109-111, and the config-5
+// engine 10.5K against 12.6K output tok/s (sequences of ~1200 keys cut into ~8 pieces:
+// each last piece's uncached partial reads and the workgroup barriers at cut
+// segments sit at the end of the launch). Every piece stores its (m, l, O) partial
+// with relaxed agent-scope atomic stores (kept coherent per location across the XCDs'
+// L2s; an agent-scope fence would write back and invalidate the whole L2 of the XCD),
+// waits for them to complete and counts itself in on the sequence's arrival counter;
+// the one that finds all others in resets the counter and combines their partials,
+// read with agent-scope atomic loads, with its own state.
+template <typename TQ, typename TKV, int D, int GC, bool kFuse>
 __global__ __launch_bounds__(512) void paged_decode_stream_kernel(const PagedParams p) {
   using K = Decode<TKV, D, GC>;
   __shared__ int s_prefix[kMaxStreamSeqs + 1];  // decode keys before sequence s
+  __shared__ int s_last;                        // kFuse: this workgroup merges the sequence
 
   const int n = p.num_seqs;
   const int tid = threadIdx.x;
@@ -359,19 +444,42 @@ __global__ __launch_bounds__(512) void paged_decode_stream_kernel(const PagedPar
     const int sb = static_cast<int>(pos - base);
     const int se = static_cast<int>(min(hi, static_cast<int64_t>(s_prefix[seq + 1])) - base);
     const int row = p.cu_seqlens_q[seq];
+    const bool whole = sb == 0 && se == ctx;
+    typename K::State st;
     if (active) {
       float qf[GC][K::E];
       K::template load_queries<TQ>(p, row, h0, r, qf);
-      typename K::State st;
       K::init(st);
       const int32_t* table = p.block_tables + static_cast<int64_t>(seq) * p.max_blocks;
       K::stream(p, table, nullptr, 0, kvh, sb, se, g, r, qf, score_scale, st);
       K::merge_row_groups(st);
       if (g == 0) {
-        if (sb == 0 && se == ctx) {
+        if (whole) {
           K::template write_output<TQ>(p, row, h0, r, st);
+        } else if constexpr (kFuse) {
+          K::write_partial_coherent(p, (static_cast<int64_t>(blockIdx.x) + seq) * p.hq + h0, r, st);
         } else {
           K::write_partial(p, (static_cast<int64_t>(blockIdx.x) + seq) * p.hq + h0, 1, r, st);
+        }
+      }
+    }
+    if constexpr (kFuse) {
+      if (!whole) {  // uniform over the workgroup
+        const int64_t first = share_owner(base, total, wgs);
+        const int pieces = static_cast<int>(share_owner(base + ctx - 1, total, wgs) - first + 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0) {
+          int* count = p.dec_count + seq;
+          const int before = __hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const int last = before == pieces - 1 ? 1 : 0;
+          if (last) __hip_atomic_store(count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          s_last = last;
+        }
+        __syncthreads();
+        if (s_last != 0 && active && g == 0) {
+          K::merge_pieces(p, first, pieces, static_cast<int>(blockIdx.x - first), seq, h0, r, st);
+          K::template write_output<TQ>(p, row, h0, r, st);
         }
       }
     }
@@ -639,7 +747,11 @@ hipError_t launch_decode_g(const PagedParams& p, hipStream_t stream) {
   }
   if (p.stream_wgs > 0) {
     if (units > 8) return hipErrorInvalidValue;  // planner keeps stream mode to <= 8 units
-    paged_decode_stream_kernel<TQ, TKV, D, GC><<<p.stream_wgs, waves * kWave, 0, stream>>>(p);
+    if (p.dec_count != nullptr) {
+      paged_decode_stream_kernel<TQ, TKV, D, GC, true><<<p.stream_wgs, waves * kWave, 0, stream>>>(p);
+      return hipGetLastError();
+    }
+    paged_decode_stream_kernel<TQ, TKV, D, GC, false><<<p.stream_wgs, waves * kWave, 0, stream>>>(p);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     const int n4 = p.hq * D / 4;

@@ -1751,25 +1751,36 @@ __global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedPara
       }
       __syncthreads();
       if (split_last == 0) return;
+      // All pieces folded in piece order from an empty state (this piece's own from
+      // registers), so the result is the same whichever piece finishes last.
+      float m_acc = -INFINITY, l_acc = 0.0f;
+      f32x16 o_acc[kDBlocks];
+#pragma unroll
+      for (int db = 0; db < kDBlocks; ++db) o_acc[db] = f32x16{};
       for (int j = 0; j < piece.pieces; ++j) {
-        if (j == piece.piece) continue;
         float* other = slot_of(j);
-        const float m_o = get(ml_at(other));
-        const float l_o = get(ml_at(other) + 1);
-        const float m_new = fmaxf(m_run, m_o);
-        const float fa = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+        const bool own = j == piece.piece;
+        const float m_o = own ? m_run : get(ml_at(other));
+        const float l_o = own ? l_run : get(ml_at(other) + 1);
+        const float m_new = fmaxf(m_acc, m_o);
+        const float fa = m_acc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_acc - m_new);
         const float fb = m_o == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_o - m_new);
-        l_run = l_run * fa + l_o * fb;
-        m_run = m_new;
+        l_acc = l_acc * fa + l_o * fb;
+        m_acc = m_new;
 #pragma unroll
         for (int k = 0; k < 16; ++k) {
-          f32x16& a = o[k >> 2];
+          f32x16& a = o_acc[k >> 2];
+          const f32x16& mine = o[k >> 2];
           const int r = 4 * (k & 3);
           float* at = o_at(other, k);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) a[r + e] = a[r + e] * fa + get(at + e) * fb;
+          for (int e = 0; e < 4; ++e) a[r + e] = a[r + e] * fa + (own ? mine[r + e] : get(at + e)) * fb;
         }
       }
+      m_run = m_acc;
+      l_run = l_acc;
+#pragma unroll
+      for (int db = 0; db < kDBlocks; ++db) o[db] = o_acc[db];
     }
   }
   if (!w_active || !my_valid) return;

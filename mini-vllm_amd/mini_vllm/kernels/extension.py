@@ -186,6 +186,7 @@ class _PlanOptions(ctypes.Structure):
         ("prefill_share_tiles", ctypes.c_int32),
         ("prefill_pieces", ctypes.c_int32),
         ("prefill_piece_pct", ctypes.c_int32),
+        ("decode_merge", ctypes.c_int32),
     ]
 
 

@@ -115,6 +115,28 @@ def test_a_ragged_decode_batch_with_empty_splits(extension, device):
     check(extension, b)
 
 
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("wgs_per_cu", ["1", "3"])
+def test_stream_decode_merge_in_launch_and_by_kernel(extension, device, kv_dtype, wgs_per_cu):
+    """Sequences cut between stream workgroups are merged by the merge kernel after the
+    decode launch (the default) or, forced, by their last piece inside it: both match
+    the oracle and give the same bits, on calls in a row (the arrival counters are left
+    at zero for the next), with sequences of one piece, of two and of dozens, and
+    prefill rows beside them."""
+    b = case([12000, 700, 33, 4096, 1, 2500, 300], [1, 1, 1, 1, 1, 1, 64], device,
+             dtype=torch.bfloat16, kv_dtype=kv_dtype, num_q_heads=16, num_kv_heads=8,
+             head_dim=128)
+    want = oracle(b)
+    runs = []
+    for merge in (1, 0, 1, 1):
+        got = kernel(extension, b, {"decode_merge": merge, "decode_wgs_per_cu": wgs_per_cu})
+        assert_max_abs(got, want, ATTN_ATOL[kv_dtype], f"decode_merge {merge}")
+        runs.append(got)
+    # Whichever piece merges folds every piece in piece order, as the merge kernel does.
+    for got in runs[1:]:
+        assert torch.equal(got, runs[0])
+
+
 @pytest.mark.parametrize("split_tokens", ["64", "1024"])
 def test_forced_split_sizes_agree(extension, device, split_tokens):
     check(extension, case([3000, 129, 64, 1], [1, 1, 1, 1], device, dtype=torch.bfloat16),
@@ -256,14 +278,17 @@ def test_split_grid_cuts_long_items(extension, device, pieces, kv_dtype):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_split_grid_one_long_prompt(extension, device, dtype):
     """One sequence alone: every item long against the mean, so each is cut (up to 7
-    pieces of ~13 tiles); the pieces' merge order differs from call to call, the result
-    within tolerance every time, and the arrival counters are left at zero for the next
-    call (three calls in a row, each checked)."""
+    pieces of ~13 tiles); whichever piece finishes last folds them in piece order, so
+    three calls in a row give the same bits (and each finds the arrival counters left
+    at zero by the one before)."""
     b = case([6100], [512], device, dtype=dtype, num_q_heads=16, num_kv_heads=8, head_dim=128)
     want = oracle(b)
+    first = None
     for _ in range(3):
         got = kernel(extension, b, _split(16))
         assert_max_abs(got, want, ATTN_ATOL[dtype], "split, one long prompt")
+        first = got if first is None else first
+        assert torch.equal(got, first)
 
 
 def test_split_grid_matches_the_whole_item_grid(extension, device):
