@@ -393,6 +393,44 @@ int mvllm_linear_residual_rmsnorm(void* h_out, void* normed, const void* x, cons
                                   int64_t n, int64_t k, float eps, int32_t dtype, void* workspace,
                                   uint64_t workspace_bytes, void* stream);
 
+/* A decode-only step's attention and o projection with its residual and RMSNorm, in
+ * three launches where mvllm_paged_attention + mvllm_linear_residual_rmsnorm take four:
+ * the paged decode leaves every sequence's pieces as partials, and the projection's
+ * first launch merges each head's pieces (in piece order, rounded as
+ * mvllm_paged_attention stores its output) straight into that head's k-steps of the
+ * packed W_o; the second adds the heads' partial sums, the residual and the RMSNorm as
+ * mvllm_linear_residual_rmsnorm does. Replaces, for decode steps,
+ * `ops.paged_attention` (paged_attention.cu:598-711) followed by `h + wo(attn)` and the
+ * next `ops.rmsnorm` (model/qwen3_paged.py:85-99,134-138); the attention output itself
+ * is not materialised. The paged arguments are mvllm_paged_attention's for num_seqs
+ * decode rows (num_tokens = num_seqs, max_query_len = 1); w_o_packed is
+ * mvllm_linear_pack of W_o [n, num_q_heads * head_dim]; h_out, normed and residual
+ * [num_seqs, n] of q_dtype, norm_weight [n]. Served: head_dim 128, q_dtype bf16 or f16,
+ * num_seqs <= 64, n a multiple of 256 in [512, 4096], the stream decode schedule (at
+ * most 4096 sequences, GQA groups of <= 8 kv-head units); anything else returns
+ * MVLLM_ERR_UNSUPPORTED before any launch. The workspace (256-byte aligned, no
+ * initialisation) is mvllm_paged_attention_o_proj_workspace_bytes. The result is within
+ * the projection's rounding of the two-entry sequence (K is summed per head rather than
+ * per 256 elements), not bit for bit. */
+int mvllm_paged_attention_o_proj(void* h_out, void* normed, const void* q, const void* key_pool,
+                                 const void* value_pool, const float* k_scales,
+                                 const float* v_scales, const int32_t* block_tables,
+                                 const int32_t* cu_seqlens_q, const int32_t* context_lens,
+                                 const int32_t* seq_lens, int32_t num_seqs, int32_t num_q_heads,
+                                 int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                 int64_t num_blocks, int32_t max_blocks_per_seq,
+                                 int32_t max_context_len, float scale, int32_t q_dtype,
+                                 int32_t kv_dtype, const void* w_o_packed, int64_t n,
+                                 const void* residual, const void* norm_weight, float eps,
+                                 void* workspace, uint64_t workspace_bytes, void* stream);
+
+/* The workspace mvllm_paged_attention_o_proj needs for these sizes, or 0 with
+ * mvllm_last_error set when the shape is not served. Host-only. */
+uint64_t mvllm_paged_attention_o_proj_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
+                                                      int32_t num_kv_heads, int32_t head_dim,
+                                                      int32_t block_size, int32_t max_context_len,
+                                                      int32_t q_dtype, int32_t kv_dtype, int64_t n);
+
 /* Greedy sampling: out[r] (int64) = index of the maximum of logits row r, for `rows`
  * rows of `vocab` logits each, `row_stride` elements apart, dtype f32/f16/bf16. The
  * order is torch.argmax's: NaN above every number, -0 equal to +0, and among equal

@@ -617,9 +617,49 @@ int mvllm_paged_attention_plan(int32_t num_tokens, int32_t num_seqs, int32_t num
 
 namespace {
 
+// The o projection mvllm_paged_attention_o_proj runs after a decode-only paged call.
+struct OProj {
+  void* h_out;
+  void* normed;
+  const void* w;
+  int64_t n;
+  const void* residual;
+  const void* norm_weight;
+  float eps;
+};
+
+// Checks that the fused decode + o projection serves this plan and shape; the byte
+// offset of its per-head partial sums in the workspace and the workspace it needs.
+int o_proj_layout(const Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t d,
+                  int32_t max_q, int32_t q_dtype, int64_t n, uint64_t& off, uint64_t& need) {
+  if (max_q != 1 || num_tokens != num_seqs) {
+    return fail(MVLLM_ERR_UNSUPPORTED,
+                "paged_attention_o_proj: every sequence must be one decode row (num_tokens == "
+                "num_seqs, max_query_len == 1)");
+  }
+  if (plan.pub.decode_mode != MVLLM_DECODE_STREAM) {
+    return fail(MVLLM_ERR_UNSUPPORTED,
+                "paged_attention_o_proj: the batch does not run on the stream decode schedule "
+                "(at most %d sequences, GQA groups of at most 8 kv-head units)",
+                mvllm::kMaxStreamSeqs);
+  }
+  if (!mvllm::paged_o_proj_supported(q_dtype, num_seqs, n, hq, d)) {
+    return fail(MVLLM_ERR_UNSUPPORTED,
+                "paged_attention_o_proj: not served for dtype code %d, %d sequences, n=%lld, "
+                "head dim %d (16-bit, <= 64 sequences, n a multiple of 256 in [512, 4096], "
+                "head dim 128)",
+                q_dtype, num_seqs, static_cast<long long>(n), d);
+  }
+  off = align256(plan.pub.workspace_bytes);
+  need = off + mvllm::paged_o_proj_partial_bytes(num_seqs, n, hq);
+  return MVLLM_OK;
+}
+
 // The paged entry behind mvllm_paged_attention and mvllm_paged_attention_noalloc: the
 // scratch pointer is the caller's workspace for the first and this library's static
-// device array for the second (`name` prefixes the errors).
+// device array for the second (`name` prefixes the errors). With `oproj` (from
+// mvllm_paged_attention_o_proj) the decode leaves its pieces as partials, `out` is not
+// written, and the o projection with its residual and RMSNorm runs from those partials.
 int paged_attention_entry(const char* name, void* out, const void* q, const void* key_pool,
                           const void* value_pool, const float* k_scales, const float* v_scales,
                           const int32_t* block_tables, const int32_t* cu_seqlens_q,
@@ -629,7 +669,8 @@ int paged_attention_entry(const char* name, void* out, const void* q, const void
                           int64_t num_blocks, int32_t max_blocks_per_seq, int32_t max_query_len,
                           int32_t max_context_len, float scale, int32_t q_dtype,
                           int32_t kv_dtype, const mvllm_plan_options* options, void* workspace,
-                          uint64_t workspace_bytes, void* stream, bool static_scratch) {
+                          uint64_t workspace_bytes, void* stream, bool static_scratch,
+                          const OProj* oproj = nullptr) {
   int rc = check_paged_shape(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim,
                              block_size, max_query_len, max_context_len, q_dtype, kv_dtype);
   if (rc != MVLLM_OK) return rc;
@@ -637,10 +678,23 @@ int paged_attention_entry(const char* name, void* out, const void* q, const void
   rc = read_options(options, o);
   if (rc != MVLLM_OK) return rc;
   if (num_tokens == 0 || num_seqs == 0) return MVLLM_OK;
-  if (out == nullptr || q == nullptr || key_pool == nullptr || value_pool == nullptr ||
-      block_tables == nullptr || cu_seqlens_q == nullptr || context_lens == nullptr ||
-      seq_lens == nullptr) {
-    return fail(MVLLM_ERR_INVALID, "paged_attention: a required pointer is NULL");
+  if ((out == nullptr && oproj == nullptr) || q == nullptr || key_pool == nullptr ||
+      value_pool == nullptr || block_tables == nullptr || cu_seqlens_q == nullptr ||
+      context_lens == nullptr || seq_lens == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "%s: a required pointer is NULL", name);
+  }
+  if (oproj != nullptr) {
+    if (oproj->h_out == nullptr || oproj->normed == nullptr || oproj->w == nullptr ||
+        oproj->residual == nullptr || oproj->norm_weight == nullptr) {
+      return fail(MVLLM_ERR_INVALID, "%s: a required pointer is NULL", name);
+    }
+    if ((reinterpret_cast<uintptr_t>(oproj->h_out) | reinterpret_cast<uintptr_t>(oproj->normed) |
+         reinterpret_cast<uintptr_t>(oproj->residual) |
+         reinterpret_cast<uintptr_t>(oproj->norm_weight) | reinterpret_cast<uintptr_t>(oproj->w)) %
+            16 != 0) {
+      return fail(MVLLM_ERR_INVALID, "%s: every buffer must be 16-byte aligned", name);
+    }
+    o.decode_merge = 0;  // the projection merges
   }
   if (num_blocks <= 0 || max_blocks_per_seq <= 0) {
     return fail(MVLLM_ERR_INVALID, "paged_attention: empty pool or block table");
@@ -659,7 +713,13 @@ int paged_attention_entry(const char* name, void* out, const void* q, const void
     plan = make_plan(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
                      max_query_len, max_context_len, q_dtype, kv_dtype, o);
   }
-  const uint64_t need = plan.pub.workspace_bytes;
+  uint64_t need = plan.pub.workspace_bytes;
+  uint64_t o_off = 0;
+  if (oproj != nullptr) {
+    rc = o_proj_layout(plan, num_tokens, num_seqs, num_q_heads, head_dim, max_query_len, q_dtype,
+                       oproj->n, o_off, need);
+    if (rc != MVLLM_OK) return rc;
+  }
   if (static_scratch && need > workspace_bytes) {
     return fail(MVLLM_ERR_UNSUPPORTED,
                 "%s: this call needs %llu bytes of scratch, more than the library's static "
@@ -705,8 +765,20 @@ int paged_attention_entry(const char* name, void* out, const void* q, const void
   p.kv_head_bytes = static_cast<int64_t>(head_dim) * kv_elem;
   p.kv_row_bytes = p.kv_head_bytes * num_kv_heads;
   p.scale = scale;
-  return launch_planned(plan, p, workspace, q_dtype, kv_dtype, head_dim, max_query_len,
-                        static_cast<hipStream_t>(stream), name);
+  p.dec_defer = oproj != nullptr ? 1 : 0;
+  rc = launch_planned(plan, p, workspace, q_dtype, kv_dtype, head_dim, max_query_len,
+                      static_cast<hipStream_t>(stream), name);
+  if (rc != MVLLM_OK || oproj == nullptr) return rc;
+  char* ws = static_cast<char*>(workspace);
+  return hip_status(
+      mvllm::launch_paged_o_proj(oproj->h_out, oproj->normed,
+                                 reinterpret_cast<const float*>(ws + plan.off_o),
+                                 reinterpret_cast<const float*>(ws + plan.off_ml),
+                                 reinterpret_cast<const int*>(ws), plan.pub.decode_workgroups,
+                                 num_q_heads, oproj->w, oproj->residual, oproj->norm_weight,
+                                 num_seqs, oproj->n, oproj->eps, q_dtype, ws + o_off,
+                                 static_cast<hipStream_t>(stream)),
+      name);
 }
 
 // The allocation-free entry's scratch: one array per device, held from the library's
@@ -789,6 +861,49 @@ int mvllm_paged_attention_noalloc(void* out, const void* q, const void* key_pool
                                head_dim, block_size, num_blocks, max_blocks_per_seq,
                                max_query_len, max_context_len, scale, q_dtype, kv_dtype,
                                options, ws, kNoallocScratchBytes, stream, true);
+}
+
+int mvllm_paged_attention_o_proj(void* h_out, void* normed, const void* q, const void* key_pool,
+                                 const void* value_pool, const float* k_scales,
+                                 const float* v_scales, const int32_t* block_tables,
+                                 const int32_t* cu_seqlens_q, const int32_t* context_lens,
+                                 const int32_t* seq_lens, int32_t num_seqs, int32_t num_q_heads,
+                                 int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                 int64_t num_blocks, int32_t max_blocks_per_seq,
+                                 int32_t max_context_len, float scale, int32_t q_dtype,
+                                 int32_t kv_dtype, const void* w_o_packed, int64_t n,
+                                 const void* residual, const void* norm_weight, float eps,
+                                 void* workspace, uint64_t workspace_bytes, void* stream) {
+  g_error[0] = '\0';
+  if (n <= 0) return fail(MVLLM_ERR_INVALID, "paged_attention_o_proj: n must be positive");
+  const OProj oproj{h_out, normed, w_o_packed, n, residual, norm_weight, eps};
+  return paged_attention_entry("paged_attention_o_proj", nullptr, q, key_pool, value_pool,
+                               k_scales, v_scales, block_tables, cu_seqlens_q, context_lens,
+                               seq_lens, num_seqs, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                               block_size, num_blocks, max_blocks_per_seq, 1, max_context_len,
+                               scale, q_dtype, kv_dtype, nullptr, workspace, workspace_bytes,
+                               stream, false, &oproj);
+}
+
+uint64_t mvllm_paged_attention_o_proj_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
+                                                      int32_t num_kv_heads, int32_t head_dim,
+                                                      int32_t block_size, int32_t max_context_len,
+                                                      int32_t q_dtype, int32_t kv_dtype, int64_t n) {
+  g_error[0] = '\0';
+  if (check_paged_shape(num_seqs, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, 1,
+                        max_context_len, q_dtype, kv_dtype) != MVLLM_OK) {
+    return 0;
+  }
+  Options o;
+  o.decode_merge = 0;
+  const Plan plan = make_plan(num_seqs, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                              block_size, 1, max_context_len, q_dtype, kv_dtype, o);
+  uint64_t off = 0, need = 0;
+  if (o_proj_layout(plan, num_seqs, num_seqs, num_q_heads, head_dim, 1, q_dtype, n, off, need) !=
+      MVLLM_OK) {
+    return 0;
+  }
+  return need;
 }
 
 int mvllm_dense_attention_plan(const mvllm_dense_args* args, uint64_t* workspace_bytes) {

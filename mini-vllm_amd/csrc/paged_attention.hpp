@@ -158,6 +158,9 @@ struct PagedParams {
   float* pf_part;     // split grid: [pf_slots][columns] partials of kSplitSlotFloats
   int* dec_count;     // stream decode: non-null merges cut sequences in the decode launch,
                       // [num_seqs] arrival counters, zero before the launch and left zero
+  int dec_defer;      // stream decode: 1 leaves every sequence's pieces as partials (whole
+                      // sequences too, one piece) for the caller's merge; no output, no
+                      // merge kernel
 };
 
 // Splits of one row: as many as its visible context needs at `split_tokens` keys

@@ -454,7 +454,7 @@ __global__ __launch_bounds__(512) void paged_decode_stream_kernel(const PagedPar
       K::stream(p, table, nullptr, 0, kvh, sb, se, g, r, qf, score_scale, st);
       K::merge_row_groups(st);
       if (g == 0) {
-        if (whole) {
+        if (whole && p.dec_defer == 0) {
           K::template write_output<TQ>(p, row, h0, r, st);
         } else if constexpr (kFuse) {
           K::write_partial_coherent(p, (static_cast<int64_t>(blockIdx.x) + seq) * p.hq + h0, r, st);
@@ -753,7 +753,7 @@ hipError_t launch_decode_g(const PagedParams& p, hipStream_t stream) {
     }
     paged_decode_stream_kernel<TQ, TKV, D, GC, false><<<p.stream_wgs, waves * kWave, 0, stream>>>(p);
     hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
+    if (err != hipSuccess || p.dec_defer != 0) return err;
     const int n4 = p.hq * D / 4;
     const int threads = n4 >= 1024 ? 1024 : (n4 + kWave - 1) / kWave * kWave;
     paged_decode_stream_merge_kernel<TQ, D><<<p.num_seqs, threads, 0, stream>>>(p, p.stream_wgs);

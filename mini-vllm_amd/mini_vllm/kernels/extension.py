@@ -290,6 +290,11 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_linear_residual_rmsnorm.argtypes = [p, p, p, p, p, p, i64, i64, i64, f32, i32, p, u64, p]
     lib.mvllm_gemm.restype = ctypes.c_int
     lib.mvllm_gemm.argtypes = [p, p, p, i64, i64, i64, i32, p]
+    lib.mvllm_paged_attention_o_proj.restype = ctypes.c_int
+    lib.mvllm_paged_attention_o_proj.argtypes = (
+        [p] * 11 + [i32] * 5 + [i64, i32, i32, f32, i32, i32, p, i64, p, p, f32, p, u64, p])
+    lib.mvllm_paged_attention_o_proj_workspace_bytes.restype = u64
+    lib.mvllm_paged_attention_o_proj_workspace_bytes.argtypes = [i32] * 8 + [i64]
 
 
 EXPORTED_SYMBOLS = (
@@ -320,6 +325,8 @@ EXPORTED_SYMBOLS = (
     "mvllm_linear_residual",
     "mvllm_linear_swiglu",
     "mvllm_gemm",
+    "mvllm_paged_attention_o_proj",
+    "mvllm_paged_attention_o_proj_workspace_bytes",
 )
 
 
@@ -1077,30 +1084,10 @@ class HipExtension:
         out["decode_mode"] = DECODE_MODES.get(out["decode_mode"], out["decode_mode"])
         return out
 
-    def paged_attention(
-        self,
-        q: torch.Tensor,
-        key_pool: torch.Tensor,
-        value_pool: torch.Tensor,
-        block_tables: torch.Tensor,
-        cu_seqlens_q: torch.Tensor,
-        context_lens: torch.Tensor,
-        seq_lens: torch.Tensor,
-        max_query_len: int,
-        max_context_len: int,
-        scale: float,
-        k_scale: torch.Tensor | None = None,
-        v_scale: torch.Tensor | None = None,
-        out: torch.Tensor | None = None,
-        plan_options: dict[str, Any] | None = None,
-    ) -> torch.Tensor:
-        """Ragged decode + prefill over a paged cache (reference csrc/paged_attention.cu:598-711).
-
-        Same positional arguments and refusals as the reference. Additions, all optional:
-        ``k_scale``/``v_scale`` (``num_blocks x H_k`` fp32) for a float8_e4m3fn pool,
-        ``out`` to write into a caller-owned ``T x H_q x D`` tensor, and ``plan_options``
-        (``mvllm_plan_options`` fields by name) to force a schedule.
-        """
+    def _paged_checks(self, q, key_pool, value_pool, block_tables, cu_seqlens_q, context_lens,
+                      seq_lens, max_query_len, max_context_len, k_scale, v_scale):
+        """The reference's refusals for a paged call (``paged_attention.cu:608-676``) and this
+        library's: raises RuntimeError; returns the contiguous metadata."""
         if not (q.is_cuda and key_pool.is_cuda and value_pool.is_cuda):
             raise RuntimeError("paged_attention: q and the pools must be CUDA tensors")
         if q.dim() != 3:
@@ -1195,6 +1182,38 @@ class HipExtension:
         cu_seqlens_q = cu_seqlens_q.contiguous()
         context_lens = context_lens.contiguous()
         seq_lens = seq_lens.contiguous()
+        return cu_seqlens_q, context_lens, seq_lens
+
+    def paged_attention(
+        self,
+        q: torch.Tensor,
+        key_pool: torch.Tensor,
+        value_pool: torch.Tensor,
+        block_tables: torch.Tensor,
+        cu_seqlens_q: torch.Tensor,
+        context_lens: torch.Tensor,
+        seq_lens: torch.Tensor,
+        max_query_len: int,
+        max_context_len: int,
+        scale: float,
+        k_scale: torch.Tensor | None = None,
+        v_scale: torch.Tensor | None = None,
+        out: torch.Tensor | None = None,
+        plan_options: dict[str, Any] | None = None,
+    ) -> torch.Tensor:
+        """Ragged decode + prefill over a paged cache (reference csrc/paged_attention.cu:598-711).
+
+        Same positional arguments and refusals as the reference. Additions, all optional:
+        ``k_scale``/``v_scale`` (``num_blocks x H_k`` fp32) for a float8_e4m3fn pool,
+        ``out`` to write into a caller-owned ``T x H_q x D`` tensor, and ``plan_options``
+        (``mvllm_plan_options`` fields by name) to force a schedule.
+        """
+        cu_seqlens_q, context_lens, seq_lens = self._paged_checks(
+            q, key_pool, value_pool, block_tables, cu_seqlens_q, context_lens, seq_lens,
+            max_query_len, max_context_len, k_scale, v_scale)
+        fp8 = key_pool.dtype == torch.float8_e4m3fn
+        num_blocks, block_size, num_kv_heads, head_dim = key_pool.shape
+        num_sequences = seq_lens.shape[0]
 
         if out is None:
             out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
@@ -1260,6 +1279,74 @@ class HipExtension:
             )
         )
         return out
+
+    def paged_attention_o_proj_supported(self, q: torch.Tensor, w_o_packed: torch.Tensor,
+                                         residual: torch.Tensor) -> bool:
+        """Whether :meth:`paged_attention_o_proj` serves this decode step: one row per
+        sequence (q T x H_q x 128, 16-bit), at most 64 rows, W_o packed for H_q x 128
+        columns, the hidden size a multiple of 256 in [512, 4096]."""
+        if q.dim() != 3 or residual.dim() != 2 or q.dtype not in (torch.float16, torch.bfloat16):
+            return False
+        t, hq, d = q.shape
+        n = residual.shape[1]
+        return (d == 128 and 1 <= t <= 64 and n % 256 == 0 and 512 <= n <= 4096
+                and w_o_packed.dtype == q.dtype and w_o_packed.is_contiguous()
+                and w_o_packed.numel() == -(-n // 32) * 32 * hq * d)
+
+    def paged_attention_o_proj(self, q: torch.Tensor, key_pool: torch.Tensor,
+                               value_pool: torch.Tensor, block_tables: torch.Tensor,
+                               cu_seqlens_q: torch.Tensor, context_lens: torch.Tensor,
+                               seq_lens: torch.Tensor, max_context_len: int, scale: float,
+                               w_o_packed: torch.Tensor, residual: torch.Tensor,
+                               norm_weight: torch.Tensor, eps: float,
+                               k_scale: torch.Tensor | None = None,
+                               v_scale: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """A decode step's attention and o projection with its residual and RMSNorm
+        (``mvllm_paged_attention_o_proj``): (h, normed) with h = residual + attn @ W_o.T
+        and normed = rmsnorm(h, norm_weight, eps), attn being ``paged_attention`` of the
+        same arguments (every sequence one decode row); the attention output is merged
+        straight into the projection, never stored."""
+        cu_seqlens_q, context_lens, seq_lens = self._paged_checks(
+            q, key_pool, value_pool, block_tables, cu_seqlens_q, context_lens, seq_lens, 1,
+            max_context_len, k_scale, v_scale)
+        num_blocks, block_size, num_kv_heads, head_dim = key_pool.shape
+        t, hq, _ = q.shape
+        num_sequences = seq_lens.shape[0]
+        if t != num_sequences:
+            raise RuntimeError("paged_attention_o_proj: every sequence must be one decode row "
+                               f"(got {t} rows for {num_sequences} sequences)")
+        if not self.paged_attention_o_proj_supported(q, w_o_packed, residual):
+            raise RuntimeError(
+                f"paged_attention_o_proj: q {tuple(q.shape)} {q.dtype} with residual "
+                f"{tuple(residual.shape)} and a packed W_o of {w_o_packed.numel()} elements is not "
+                "served (16-bit, head dim 128, <= 64 rows, hidden size a multiple of 256 in "
+                "[512, 4096])")
+        n = residual.shape[1]
+        if (residual.shape != (t, n) or residual.dtype != q.dtype or not residual.is_contiguous()
+                or norm_weight.shape != (n,) or norm_weight.dtype != q.dtype
+                or not norm_weight.is_contiguous()):
+            raise RuntimeError("paged_attention_o_proj: residual must be a contiguous T x N "
+                               "tensor and norm_weight a contiguous N vector, both of q's dtype")
+        q_code = DTYPE_CODES[q.dtype]
+        kv_code = DTYPE_CODES[key_pool.dtype]
+        need = int(self.lib.mvllm_paged_attention_o_proj_workspace_bytes(
+            num_sequences, hq, num_kv_heads, head_dim, block_size, int(max_context_len), q_code,
+            kv_code, n))
+        if need == 0:
+            raise RuntimeError(self.lib.mvllm_last_error().decode(errors="replace")
+                               or "paged_attention_o_proj: not served")
+        workspace = self.workspace(q.device, need)
+        h = torch.empty_like(residual)
+        normed = torch.empty_like(residual)
+        self._check(self.lib.mvllm_paged_attention_o_proj(
+            h.data_ptr(), normed.data_ptr(), q.data_ptr(), key_pool.data_ptr(),
+            value_pool.data_ptr(), _ptr(k_scale), _ptr(v_scale), block_tables.data_ptr(),
+            cu_seqlens_q.data_ptr(), context_lens.data_ptr(), seq_lens.data_ptr(), num_sequences,
+            hq, num_kv_heads, head_dim, block_size, num_blocks, block_tables.shape[1],
+            int(max_context_len), float(scale), q_code, kv_code, w_o_packed.data_ptr(), n,
+            residual.data_ptr(), norm_weight.data_ptr(), float(eps), workspace.data_ptr(),
+            workspace.numel(), _stream(q.device)))
+        return h, normed
 
 
 def load_extension(verbose: bool = False) -> HipExtension:

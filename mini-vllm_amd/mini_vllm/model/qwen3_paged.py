@@ -140,9 +140,38 @@ class Qwen3Paged:
         self.lm_head = (ops.pack_weight(weights["embedding"], use_cuda=True) if use_cuda
                         else weights["embedding"])
 
+    def _attention_block(self, layer: int, w: dict, p: dict, x: torch.Tensor, h: torch.Tensor,
+                         batch, fused: bool) -> tuple[torch.Tensor, torch.Tensor]:
+        """(h + wo(attention(x)), mlp_norm of that) for normed input x: on a decode-only
+        step with the kernels on, the decode's pieces merged straight into the o
+        projection (``ops.paged_attention_o_proj``); otherwise the attention output,
+        then the projection with its residual and norm."""
+        c = self.config
+        if fused and batch.max_query_len == 1:
+            q = self._queries(layer, w, p, x, batch, fused)
+            kv = self.manager.kv
+            k_scale, v_scale = kv.layer_scales(layer)
+            both = ops.paged_attention_o_proj(
+                q, kv.layer_keys(layer), kv.layer_values(layer), batch.block_tables,
+                batch.cu_seqlens_q, batch.context_lens, batch.seq_lens, batch.max_context_len,
+                1.0 / math.sqrt(c.head_dim), p.get("o"), h, w["mlp_norm"], c.rms_norm_eps,
+                use_cuda=self.use_cuda, k_scale=k_scale, v_scale=v_scale)
+            if both is not None:
+                return both
+            out = self._paged(layer, q, batch)
+        else:
+            out = self._attention(layer, w, p, x, batch, fused)
+        return self._residual_norm(out, p.get("o"), w["wo"], h, w["mlp_norm"], fused)
+
     def _attention(self, layer: int, w: dict, p: dict, x: torch.Tensor, batch,
                    fused: bool) -> torch.Tensor:
         """The attention output (``T x H_q D``) of normed input x, before ``wo``."""
+        return self._paged(layer, self._queries(layer, w, p, x, batch, fused), batch)
+
+    def _queries(self, layer: int, w: dict, p: dict, x: torch.Tensor, batch,
+                 fused: bool) -> torch.Tensor:
+        """q (``T x H_q x D``, contiguous) of normed input x after QK-norm and RoPE, with
+        this step's K and V written to the layer's pages."""
         c = self.config
         t = x.shape[0]
         u = self.use_cuda
@@ -164,13 +193,19 @@ class Qwen3Paged:
             q, k = ops.qk_norm_rope(q.contiguous(), k.contiguous(), w["q_norm"], w["k_norm"],
                                     batch.positions, self.cos, self.sin, c.rms_norm_eps, use_cuda=u)
             kv.write(layer, batch.slot_mapping, k, v.contiguous(), use_cuda=u)
+        return q.contiguous()
+
+    def _paged(self, layer: int, q: torch.Tensor, batch) -> torch.Tensor:
+        """The paged attention of q over the layer's pages (``T x H_q D``)."""
+        c = self.config
+        kv = self.manager.kv
         k_scale, v_scale = kv.layer_scales(layer)
         out = ops.paged_attention(
-            q.contiguous(), kv.layer_keys(layer), kv.layer_values(layer), batch.block_tables,
+            q, kv.layer_keys(layer), kv.layer_values(layer), batch.block_tables,
             batch.cu_seqlens_q, batch.context_lens, batch.seq_lens, batch.max_query_len,
-            batch.max_context_len, 1.0 / math.sqrt(c.head_dim), use_cuda=u,
+            batch.max_context_len, 1.0 / math.sqrt(c.head_dim), use_cuda=self.use_cuda,
             k_scale=k_scale, v_scale=v_scale)
-        return out.view(t, c.q_size)
+        return out.view(q.shape[0], c.q_size)
 
     def _residual_norm(self, x: torch.Tensor, pw, dense_w: torch.Tensor, h: torch.Tensor,
                        norm_w: torch.Tensor, fused: bool) -> tuple[torch.Tensor, torch.Tensor]:
@@ -205,8 +240,7 @@ class Qwen3Paged:
         for layer, (w, p) in enumerate(zip(self.layers, self.packed)):
             # normed = attn_norm(h) of this layer, computed by the previous layer's
             # down projection (or above, for the first layer).
-            out = self._attention(layer, w, p, normed, batch, fused)
-            h, normed = self._residual_norm(out, p.get("o"), w["wo"], h, w["mlp_norm"], fused)
+            h, normed = self._attention_block(layer, w, p, normed, h, batch, fused)
             if fused and "gate_up" in p:
                 gated = ops.linear_swiglu(normed, p["gate_up"], use_cuda=u)
             else:
