@@ -157,6 +157,46 @@ def test_engine_with_decode_graphs_matches_dense_recompute(extension, device, sc
         assert_tokens_match(g, tok, logits, tie_tol=1e-4, msg=f"prompt {i}")
 
 
+def test_step_returns_finished_outputs_complete(extension, device):
+    """With decode graphs a greedy iteration's tokens are filled in one iteration late;
+    ``step()`` still returns finished sequences with every token in place (it waits for
+    them), ``step(resolve_finished=False)`` + ``flush()`` and ``generate`` (which finishes
+    sequences without waiting) give the same tokens."""
+    config = tiny_config(torch.float32)
+    weights = random_weights(config, seed=5, device=device)
+    ps = prompts(6, 3, 60, config.vocab_size, seed=2)
+    sched = SchedulerConfig(max_batched_tokens=24, chunk_size=8, max_sequences=3)
+    lengths = [3, 9, 5, 12, 7, 4]  # sequences finish in different iterations
+
+    def fresh():
+        return make_engine(config, weights, use_cuda=True, device=device, sched=sched,
+                           use_graphs=True)
+
+    engine = fresh()
+    seqs = [engine.add_request(p, n) for p, n in zip(ps, lengths)]
+    finished = 0
+    while engine.scheduler.has_work:
+        for seq in engine.step():
+            finished += 1
+            assert len(seq.output) == seq.max_tokens and min(seq.output) >= 0, seq.output
+    assert finished == len(ps) and engine.graphs.replays > 0
+    eager = [list(s.output) for s in seqs]
+
+    lazy = fresh()
+    seqs = [lazy.add_request(p, n) for p, n in zip(ps, lengths)]
+    while lazy.scheduler.has_work:
+        lazy.step(resolve_finished=False)
+    lazy.flush()
+    assert [list(s.output) for s in seqs] == eager
+
+    # generate (one length for all) against a step-driven run of the same schedule
+    engine = fresh()
+    seqs = [engine.add_request(p, 6) for p in ps]
+    while engine.scheduler.has_work:
+        engine.step()
+    assert fresh().generate(ps, 6) == [list(s.output) for s in seqs]
+
+
 @pytest.fixture(scope="module")
 def qwen3_06b(device):
     """BASELINE config 5's model: Qwen3-0.6B's shape (28 layers, 16q/8kv, D=128, vocab
