@@ -381,6 +381,26 @@ int mvllm_linear_swiglu(void* y, const void* x, const void* w_gate_up, int64_t m
 int mvllm_gemm(void* y, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
                int32_t dtype, void* stream);
 
+/* y [m, n] = x [m, k] w [n, k]^T through hipBLASLt, all row-major and contiguous,
+ * 16-byte aligned, fp16 or bf16 (dtype), fp32 accumulation: the vendor BLAS product the
+ * reference's projections run at prefill sizes (mini_vllm/basics.py:18 linear, x @ w.T
+ * through torch, called from model/qwen3_paged.py:71-95, 110 and 141-143), with its
+ * per-call set-up kept: the matmul and layout descriptors are made on the first call of
+ * each (device, dtype, m, n, k), the heuristic's algorithm on the first call of each
+ * (device, dtype, n, k, 128-row bucket of m) - chosen for the bucket's largest, odd, m;
+ * m a multiple of 128 and a shape hipBLASLt refuses it for get their own - and both
+ * reused (at most 4096 shapes
+ * kept; past that all are dropped and made again as called), and a 32 MiB
+ * workspace is allocated on the first call of each (device, stream) that needs one
+ * (hipMalloc, held until the process ends: a first call is not graph-capturable).
+ * Calls from several host threads are serialised. A shape hipBLASLt has no algorithm
+ * for returns MVLLM_ERR_UNSUPPORTED before any launch. */
+int mvllm_blas_linear(void* y, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
+                      int32_t dtype, void* stream);
+
+/* Shapes mvllm_blas_linear currently keeps (for tests). */
+int mvllm_blas_plans_cached(void);
+
 /* h_out = residual + x w^T (rounded as mvllm_linear_residual) and normed = RMSNorm(h_out)
  * with norm_weight and eps (rounded as mvllm_rmsnorm: bit for bit the two entries in
  * sequence), h_out, normed, residual [m, n], norm_weight [n]: the o and down projections

@@ -14,6 +14,7 @@
 #include <mutex>
 
 #include "../../include/minivllm_hip.h"
+#include "blas.hpp"
 #include "common.hpp"
 #include "dense.hpp"
 #include "elementwise.hpp"
@@ -587,7 +588,7 @@ extern "C" {
 
 const char* mvllm_last_error(void) { return g_error; }
 
-int mvllm_abi_version(void) { return 11; }
+int mvllm_abi_version(void) { return 12; }
 
 #ifndef MVLLM_SOURCE_HASH
 #define MVLLM_SOURCE_HASH "unstamped"
@@ -1389,6 +1390,43 @@ int mvllm_gemm(void* y, const void* x, const void* w, int64_t m, int64_t n, int6
                                        static_cast<hipStream_t>(stream)),
                     "gemm: launch");
 }
+
+int mvllm_blas_linear(void* y, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
+                      int32_t dtype, void* stream) {
+  g_error[0] = '\0';
+  if (m < 0 || n < 0 || k < 0) return fail(MVLLM_ERR_INVALID, "blas_linear: negative size");
+  if (m == 0 || n == 0) return MVLLM_OK;
+  if (k == 0) return fail(MVLLM_ERR_UNSUPPORTED, "blas_linear: k = 0 is not served");
+  if (dtype != mvllm::kF16 && dtype != mvllm::kBF16) {
+    return fail(MVLLM_ERR_UNSUPPORTED, "blas_linear: dtype code %d is not served; fp16 or bf16",
+                dtype);
+  }
+  if (x == nullptr || w == nullptr || y == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "blas_linear: a required pointer is NULL");
+  }
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+       reinterpret_cast<uintptr_t>(y)) % 16 != 0) {
+    return fail(MVLLM_ERR_INVALID, "blas_linear: x, w and y must be 16-byte aligned");
+  }
+  const mvllm::BlasStatus st = mvllm::blas_linear(y, x, w, m, n, k, dtype,
+                                                  static_cast<hipStream_t>(stream));
+  switch (st.kind) {
+    case 0:
+      return MVLLM_OK;
+    case 1:
+      return fail(MVLLM_ERR_HIP, "blas_linear: %s: HIP error %d (%s)", st.what, st.code,
+                  hipGetErrorString(static_cast<hipError_t>(st.code)));
+    case 3:
+      return fail(MVLLM_ERR_UNSUPPORTED, "blas_linear: M=%lld N=%lld K=%lld: %s",
+                  static_cast<long long>(m), static_cast<long long>(n),
+                  static_cast<long long>(k), st.what);
+    default:
+      return fail(MVLLM_ERR_HIP, "blas_linear: hipBLASLt %s failed with status %d", st.what,
+                  st.code);
+  }
+}
+
+int mvllm_blas_plans_cached(void) { return mvllm::blas_plans_cached(); }
 
 int mvllm_kv_write(void* key_pool, void* value_pool, float* k_scales, float* v_scales,
                    const void* key, const void* value, const int32_t* slot_mapping,

@@ -60,7 +60,11 @@ HIP_FLAGS = [
 # reference's PyTorch expressions round, so FMA contraction is off there.
 EXTRA_FLAGS = {"elementwise.hip": ["-ffp-contract=off"], "linear.hip": ["-ffp-contract=off"]}
 
-ABI_VERSION = 11
+# hipBLASLt (csrc/blas.hip). Its soname is the one torch's bundled copy carries, so in a
+# process that has imported torch the library binds to that copy.
+LINK_LIBS = ["-L/opt/rocm/lib", "-lhipblaslt"]
+
+ABI_VERSION = 12
 
 DTYPE_CODES: dict[torch.dtype, int] = {
     torch.float32: 0,
@@ -96,7 +100,7 @@ def source_hash() -> str | None:
     if not any(f.suffix == ".hip" for f in files):
         return None
     h = hashlib.sha256()
-    h.update(repr((HIP_FLAGS, sorted(EXTRA_FLAGS.items()))).encode())
+    h.update(repr((HIP_FLAGS, sorted(EXTRA_FLAGS.items()), LINK_LIBS)).encode())
     for f in files:
         h.update(f.name.encode() + b"\0" + f.read_bytes() + b"\0")
     return h.hexdigest()[:16]
@@ -134,7 +138,8 @@ def build_library(verbose: bool = False, jobs: int | None = None) -> Path:
         objects = list(pool.map(compile_one, sources()))
 
     tmp = LIB_PATH.with_suffix(f".so.tmp{os.getpid()}")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), *LINK_LIBS,
+           "-o", str(tmp)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         raise ToolchainError(f"link failed:\n{result.stderr}{result.stdout}")
@@ -290,6 +295,10 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_linear_residual_rmsnorm.argtypes = [p, p, p, p, p, p, i64, i64, i64, f32, i32, p, u64, p]
     lib.mvllm_gemm.restype = ctypes.c_int
     lib.mvllm_gemm.argtypes = [p, p, p, i64, i64, i64, i32, p]
+    lib.mvllm_blas_linear.restype = ctypes.c_int
+    lib.mvllm_blas_linear.argtypes = [p, p, p, i64, i64, i64, i32, p]
+    lib.mvllm_blas_plans_cached.restype = ctypes.c_int
+    lib.mvllm_blas_plans_cached.argtypes = []
     lib.mvllm_paged_attention_o_proj.restype = ctypes.c_int
     lib.mvllm_paged_attention_o_proj.argtypes = (
         [p] * 11 + [i32] * 5 + [i64, i32, i32, f32, i32, i32, p, i64, p, p, f32, p, u64, p])
@@ -325,6 +334,8 @@ EXPORTED_SYMBOLS = (
     "mvllm_linear_residual",
     "mvllm_linear_swiglu",
     "mvllm_gemm",
+    "mvllm_blas_linear",
+    "mvllm_blas_plans_cached",
     "mvllm_paged_attention_o_proj",
     "mvllm_paged_attention_o_proj_workspace_bytes",
 )
@@ -773,6 +784,37 @@ class HipExtension:
         n = w.shape[0]
         return (m >= 1 and n >= 64 and n % 64 == 0 and k >= 64 and k % 64 == 0
                 and 2 * m * k < 2**31 and 2 * n * k < 2**31 and m * n < 2**31)
+
+    @staticmethod
+    def blas_linear_supported(x: torch.Tensor, w: torch.Tensor) -> bool:
+        """Whether :meth:`blas_linear` serves ``x @ w.T``: device tensors, 2-D, contiguous,
+        16-byte aligned, fp16 / bf16 of one dtype, K >= 1."""
+        return (x.dim() == 2 and w.dim() == 2 and x.dtype == w.dtype
+                and x.dtype in (torch.float16, torch.bfloat16) and x.shape[1] == w.shape[1]
+                and x.shape[1] >= 1 and x.is_cuda and w.device == x.device
+                and x.is_contiguous() and w.is_contiguous()
+                and (x.data_ptr() | w.data_ptr()) % 16 == 0)
+
+    def blas_linear(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor | None:
+        """``x @ w.T`` through the library's hipBLASLt entry (descriptors and algorithm
+        kept per shape), or None when hipBLASLt has no algorithm for the shape (the
+        caller takes torch's product). Unserved operands raise."""
+        if not self.blas_linear_supported(x, w):
+            raise RuntimeError(f"blas_linear: x {tuple(x.shape)} {x.dtype} and w {tuple(w.shape)} "
+                               f"{w.dtype} are not served (2-D contiguous 16-byte aligned device "
+                               "fp16 or bf16 of one dtype, matching K)")
+        y = torch.empty((x.shape[0], w.shape[0]), dtype=x.dtype, device=x.device)
+        rc = self.lib.mvllm_blas_linear(y.data_ptr(), x.data_ptr(), w.data_ptr(), x.shape[0],
+                                        w.shape[0], x.shape[1], DTYPE_CODES[x.dtype],
+                                        _stream(x.device))
+        if rc == 2:  # MVLLM_ERR_UNSUPPORTED: no algorithm for this shape
+            return None
+        self._check(rc)
+        return y
+
+    def blas_plans_cached(self) -> int:
+        """Shapes the hipBLASLt entry currently keeps."""
+        return int(self.lib.mvllm_blas_plans_cached())
 
     def gemm(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
         """``x @ w.T`` for prefill-sized ``x`` [M, K] against a row-major weight [N, K]:

@@ -84,6 +84,8 @@ CUDA_KERNELS: dict[str, tuple[bool, str]] = {
     "qk_norm_rope": (True, "csrc/elementwise.hip"),
     "linear": (True, "csrc/linear.hip (at most 64 rows; vendor BLAS above)"),
     "gemm": (True, "csrc/gemm.hip (prefill-sized projections)"),
+    "blas_linear": (True, "csrc/blas.hip (prefill-sized projections on hipBLASLt, set-up kept "
+                          "per shape)"),
     "paged_attention_o_proj": (True, "csrc/paged_decode.hip (pieces left as partials) + "
                                      "csrc/linear.hip (merged into the o projection)"),
 }
@@ -358,24 +360,44 @@ def _gemm(x: torch.Tensor, dense: torch.Tensor, use_cuda: bool) -> torch.Tensor 
     return ext.gemm(x, dense) if ext.gemm_supported(x, dense) else None
 
 
+def _blas(x: torch.Tensor, dense: torch.Tensor, use_cuda: bool) -> torch.Tensor | None:
+    """``x @ dense.T`` through the library's hipBLASLt entry (``csrc/blas.hip``: the
+    vendor product with its descriptors and algorithm kept per shape, where torch makes
+    them on every call: ~18.5 us of host time a call, more than the GPU time of a
+    prefill chunk's projection) when it is dispatched and serves the operands (device
+    fp16/bf16, 2-D contiguous), else None: the caller takes torch's product."""
+    if "blas_linear" in NOT_YET_FASTER or not (use_cuda and x.is_cuda and x.dim() == 2):
+        return None
+    ext = load_extension()
+    return ext.blas_linear(x, dense) if ext.blas_linear_supported(x, dense) else None
+
+
+def _prefill_product(x: torch.Tensor, dense: torch.Tensor, use_cuda: bool) -> torch.Tensor:
+    """``x @ dense.T`` for a prefill-sized ``x``: the MFMA GEMM when dispatched, else the
+    vendor BLAS (the library's entry, else torch's)."""
+    y = _gemm(x, dense, use_cuda)
+    if y is None:
+        y = _blas(x, dense, use_cuda)
+    return y if y is not None else x @ dense.t()
+
+
 def linear(x: torch.Tensor, w: torch.Tensor | PackedWeight, use_cuda: bool = False) -> torch.Tensor:
     """``x @ w.T`` (no bias), the projections of model/basics.py ``linear``.
 
     Kernels: ``csrc/linear.hip`` for decode-sized ``x`` (at most 64 rows of f16/bf16, K a
     multiple of 64) against a :class:`PackedWeight`: a weight-bandwidth-bound skinny
     GEMM; ``csrc/gemm.hip`` for larger ``x`` (prefill chunks: an MFMA GEMM over the
-    row-major weight, N and K multiples of 64). Other shapes take the vendor BLAS
-    through torch, as every projection does in the reference: a dispatch by size, all
-    paths on the device.
+    row-major weight, N and K multiples of 64; held back while slower). Other shapes
+    take the vendor BLAS, as every projection does in the reference: for device
+    fp16/bf16 through ``csrc/blas.hip`` (hipBLASLt with the per-shape set-up kept),
+    else through torch - a dispatch by size, all paths on the device.
     """
     dense = w.dense if isinstance(w, PackedWeight) else w
     ext = _skinny_ext(x, w, dense.shape[0], use_cuda)
     if ext is not None:
         return ext.linear(x, w.packed, dense.shape[0])
     if not skinny(x, use_cuda):
-        y = _gemm(x, dense, use_cuda)
-        if y is not None:
-            return y
+        return _prefill_product(x, dense, use_cuda)
     return x @ dense.t()
 
 
@@ -398,8 +420,8 @@ def linear_split(x: torch.Tensor, w: PackedWeight, sizes: tuple[int, ...],
     ext = _skinny_ext(x, w, w.shape[0], use_cuda)
     if ext is not None and len(sizes) <= 3 and all(s % 32 == 0 for s in sizes[:-1]):
         return ext.linear_split(x, w.packed, tuple(sizes))
-    y = None if skinny(x, use_cuda) else _gemm(x, w.dense, use_cuda)
-    parts = (y if y is not None else x @ w.dense.t()).split(list(sizes), dim=-1)
+    y = x @ w.dense.t() if skinny(x, use_cuda) else _prefill_product(x, w.dense, use_cuda)
+    parts = y.split(list(sizes), dim=-1)
     return parts if views else tuple(t.contiguous() for t in parts)
 
 

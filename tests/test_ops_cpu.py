@@ -114,7 +114,7 @@ def test_dispatch_report_names_every_op():
     assert set(ops.cuda_kernel_names()) == {"rmsnorm", "rope", "swiglu", "paged_attention", "kv_write",
                                             "qk_norm_rope", "linear", "decode_attention",
                                             "flash_prefill", "argmax", "gemm",
-                                            "paged_attention_o_proj"}
+                                            "paged_attention_o_proj", "blas_linear"}
     assert "gemm" in ops.NOT_YET_FASTER and "gemm.hip (prefill-sized projections) is slower" in on
 
 
