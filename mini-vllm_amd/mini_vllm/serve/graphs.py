@@ -14,10 +14,11 @@ fixed, so one captured graph serves every decode step of a given shape:
 * before a replay, the iteration's metadata is packed into one pinned host buffer and
   copied into the graph's static input tensors with one host-to-device copy;
 * sampling (argmax) runs after the replay, outside the graph; :meth:`DecodeGraphs.keep`
-  stores the sampled tokens in a device buffer every graph reads, and a sequence that
-  was in the previous replay takes its next input token from there (the graph gathers
-  it by the row the sequence had), so the host need not have read that token yet: the
-  engine schedules and packs the next decode step while the GPU runs this one.
+  stores the sampled tokens in a device buffer every graph reads, and a sequence whose
+  token from the previous iteration was committed takes its next input token from there
+  (the graph gathers it by the row the sequence had), so the host need not have read
+  that token yet: the engine schedules and packs the next decode step while the GPU
+  runs this one.
 
 The paged-attention plan in stream mode depends only on the batch size and the bound on
 max_context_len, so the kernels launched inside a graph stay valid for every replay;
@@ -197,11 +198,15 @@ class DecodeGraphs:
         self.replays += 1
         return entry.logits[:n]
 
-    def keep(self, scheduled, tokens: torch.Tensor) -> None:
-        """The tokens just sampled for ``scheduled`` (device, one per row): the next
-        replay gathers its inputs from them."""
+    def keep(self, scheduled, tokens: torch.Tensor, committed) -> None:
+        """The tokens just sampled for ``scheduled`` (device, one per row) and the rows
+        ``committed`` whose token became its sequence's new last token: the next replay
+        gathers its inputs from those rows only. A row whose token was discarded (a
+        prompt chunk that did not reach the prompt's end, or a recompute chunk short of
+        the sequence's end) is not kept: that sequence's next input is a token the host
+        already has."""
         self.prev_tokens[: len(scheduled)].copy_(tokens)
-        self.prev_rows = {s.seq_id: i for i, (s, _) in enumerate(scheduled)}
+        self.prev_rows = {scheduled[i][0].seq_id: i for i in committed}
 
     def invalidate(self) -> None:
         """An iteration ran outside the graphs: no device-held token is current."""

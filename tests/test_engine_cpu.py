@@ -184,3 +184,56 @@ def test_sampled_requests_are_reproducible_and_greedy_ones_unchanged(model):
     assert all(0 <= t < config.vocab_size for g in first for t in g)
     with pytest.raises(ValueError, match="sampling params"):
         make_engine(config, weights).generate(ps, 2, [hot])
+
+
+class _EagerGraphs:
+    """Stands in for DecodeGraphs.run on the CPU: the same input rule (a sequence in
+    ``prev_rows`` takes ``prev_tokens[row]`` as its input token, every other row the
+    host's token) without capturing a graph, so the engine's bookkeeping of which
+    sampled tokens the next iteration may gather is checked here. Records every
+    (sequence, position, token fed)."""
+
+    def __init__(self, graphs):
+        self.graphs = graphs
+        self.fed = []
+
+    def __call__(self, scheduled):
+        from dataclasses import replace
+
+        from mini_vllm.serve.batch import ForwardBatch
+
+        g = self.graphs
+        batch = ForwardBatch.from_scheduled(scheduled, g.model.manager, "cpu")
+        ids = batch.input_ids.clone()
+        for i, (seq, _) in enumerate(scheduled):
+            row = g.prev_rows.get(seq.seq_id, -1)
+            if row >= 0:
+                ids[i] = g.prev_tokens[row]
+            self.fed.append((seq, seq.num_computed_tokens, int(ids[i])))
+        g.replays += 1
+        return g.model(replace(batch, input_ids=ids))
+
+
+@pytest.mark.parametrize("lengths,sched", [
+    ((9, 17), SchedulerConfig(max_batched_tokens=24, chunk_size=8)),   # last chunk 1 token
+    # two rows decode, so a 3-token budget leaves the third prompt 1-token chunks
+    ((2, 2, 12), SchedulerConfig(max_batched_tokens=3, chunk_size=8)),
+], ids=["chunk-plus-one", "one-token-chunks"])
+def test_decode_rows_gather_only_committed_tokens(model, lengths, sched):
+    """Iterations whose rows are all one token go to the decode graphs even when a row
+    is a prompt chunk that does not finish its prompt; that row's sampled token is
+    discarded, so the next iteration must not feed it back as the sequence's input.
+    Every token fed to a replay is the sequence's token at that position, and the
+    tokens match the float64 recompute (the graph replay is emulated eagerly)."""
+    config, weights = model
+    g = torch.Generator().manual_seed(21)
+    ps = [torch.randint(0, config.vocab_size, (n,), generator=g).tolist() for n in lengths]
+    engine = make_engine(config, weights, sched=sched, use_graphs=True)
+    replay = engine.graphs.run = _EagerGraphs(engine.graphs)
+    got = engine.generate(ps, MAX_TOKENS)
+    assert engine.graphs.replays > 0
+    for seq, pos, token in replay.fed:
+        assert seq.tokens(pos, 1)[0] == token, (seq.seq_id, pos)
+    for i, (p, g) in enumerate(zip(ps, got)):
+        tok, logits = generate_greedy(config, weights, p, MAX_TOKENS)
+        assert_tokens_match(g, tok, logits, tie_tol=1e-4, msg=f"prompt {i}")

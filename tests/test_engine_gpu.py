@@ -335,3 +335,37 @@ def test_fp8_kv_cache_engine_kernels_match_the_torch_path(extension, device, sch
     kern, ref = runs
     assert all(k[0] == r[0] for k, r in zip(kern, ref))
     assert sum(k == r for k, r in zip(kern, ref)) >= len(ps) - 1
+
+
+@pytest.mark.parametrize("lengths,sched,num_blocks", [
+    ((9, 17), SchedulerConfig(max_batched_tokens=24, chunk_size=8), 64),   # last chunk 1 token
+    ((2, 2, 12), SchedulerConfig(max_batched_tokens=3, chunk_size=8), 64),  # 1-token chunks
+    # a pool of 6 pages of 4 tokens: sequences are preempted and recomputed, in
+    # 1-token chunks beside decode rows
+    ((3, 5, 14), SchedulerConfig(max_batched_tokens=3, chunk_size=8), 7),
+], ids=["chunk-plus-one", "one-token-chunks", "recompute"])
+def test_decode_graphs_feed_only_committed_tokens(extension, device, lengths, sched, num_blocks):
+    """An iteration whose rows are all one token replays a decode graph even when a row
+    is a prompt (or recompute) chunk short of its sequence's end, whose sampled token is
+    discarded: the next replay must feed that sequence its own next token, not the
+    discarded one. Weights of std 0.3 make the continuation depend on every input token
+    (at std 0.02 a wrong input token rarely changes the argmax); tokens against the
+    float64 recompute and the engine without graphs."""
+    config = tiny_config(torch.float32)
+    weights = random_weights(config, seed=3, std=0.3, device=device)
+    g = torch.Generator().manual_seed(21)
+    ps = [torch.randint(0, config.vocab_size, (n,), generator=g).tolist() for n in lengths]
+    want = _reference(config, weights, ps)
+    runs = {}
+    for graphs in (True, False):
+        engine = make_engine(config, weights, num_blocks=num_blocks + graphs,
+                             block_size=4 if num_blocks < 64 else 16, use_cuda=True,
+                             device=device, sched=sched, use_graphs=graphs)
+        runs[graphs] = engine.generate(ps, MAX_TOKENS)
+        if graphs:
+            assert engine.graphs.replays > 0
+        if num_blocks < 64:
+            assert engine.stats.preemptions > 0, "the pool was meant to force preemption"
+        engine.model.manager.check_no_leaks()
+        for i, (got, (tok, logits)) in enumerate(zip(runs[graphs], want)):
+            assert_tokens_match(got, tok, logits, tie_tol=1e-4, msg=f"graphs={graphs} prompt {i}")
