@@ -174,16 +174,15 @@ def test_decode_staircase_across_pieces(extension, device, path, kv_dtype):
     assert_max_abs(got, oracle(b), tol(torch.bfloat16, kv_dtype), f"{path} staircase")
 
 
-@pytest.mark.parametrize("kv_dtype", KV_POOLS, ids=KV_IDS)
+@pytest.mark.parametrize("dtype,kv_dtype", [(torch.float32, None), (torch.bfloat16, None),
+                                            (torch.bfloat16, torch.float8_e4m3fn)],
+                         ids=["fp32", "bf16", "bf16-fp8"])
 @pytest.mark.parametrize("path", sorted(DECODE_PATHS))
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_decode_logits_that_would_overflow(extension, device, path, dtype, kv_dtype):
     """``test_handles_logits_that_would_overflow``: q = k = 30, so every score is
     30 * 30 * 128 / sqrt(128) ~ 10182, far past exp's range; subtracting the running max
     makes every weight 1 and the output the mean of the values. One short sequence and
     one cut into many pieces."""
-    if dtype == torch.float32 and kv_dtype is not None:
-        pytest.skip("fp8 pools serve 16-bit queries")
     b = directed([100, 5000], [1, 1], dtype=dtype, kv_dtype=kv_dtype, base=30.0, q_fill=30.0)
     got = run(extension, b, DECODE_PATHS[path])
     assert torch.isfinite(got).all(), "the running max is not being subtracted"
