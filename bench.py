@@ -134,7 +134,12 @@ def run_engine(requests: int = 256, max_tokens: int = 256, max_sequences: int = 
         return LLMEngine(Qwen3Paged(config, weights, manager, use_cuda=True), sched, device="cuda",
                          use_graphs=use_graphs)
 
-    engine().generate(prompts[:4], 4)  # warm up kernels and BLAS handles
+    warm = engine()
+    warm.generate(prompts[:4], 4)  # warm up kernels and BLAS handles
+    # the hipBLASLt entry chooses its algorithm per row-count class at first use: do it
+    # for every class the 2048-token budget can produce before the timed run
+    tuned = warm.model.prepare_prefill_products(CONFIG5_BUDGET)
+    del warm
     torch.cuda.synchronize()
     eng = engine()
     eng.generate(prompts, max_tokens)
@@ -150,6 +155,7 @@ def run_engine(requests: int = 256, max_tokens: int = 256, max_sequences: int = 
         "decode_only_iterations": st.decode_only_iterations,
         "decode_graphs": use_graphs,
         "kv_dtype": str(kv_dtype or config.dtype).replace("torch.", ""),
+        "prefill_products_prepared": tuned,
     }
 
 
@@ -327,10 +333,14 @@ def run_linear(steps: int = 20) -> dict:
 
 def run_prefill_gemm(steps: int = 20, tokens: int = 2048) -> dict:
     """The four projections of a config-5 prefill iteration (2048 tokens, Qwen3-0.6B
-    shapes, bf16, fp32 accumulate) as the model runs them (``ops.linear``: the vendor
-    BLAS while the hand-written MFMA GEMM is held back as slower), and each of the two
-    paths on every shape. Four weight copies rotated; timed as graph replays of
-    back-to-back calls. FLOPs = 2 M N K."""
+    shapes, bf16, fp32 accumulate) as the model runs them (``ops.linear``: the library's
+    hipBLASLt entry, whose first call of a shape times the heuristic's 16 candidates and
+    keeps the fastest; then again after ``blas_tune`` has swept every algorithm for the
+    shape, as the engine's start-up does), against torch's product (the same library,
+    the heuristic's first algorithm, set-up made per call). Four weight copies rotated;
+    timed as graph replays of back-to-back calls. FLOPs = 2 M N K. ``choice`` is the
+    library's record of how it chose (candidates, the kept one's index - past 15 one of
+    the sweep's - and the heuristic first's and the kept one's time)."""
     from mini_vllm.kernels import ops
     from mini_vllm.kernels.extension import load_extension
 
@@ -342,20 +352,28 @@ def run_prefill_gemm(steps: int = 20, tokens: int = 2048) -> dict:
         ws = [torch.randn(n, k, device="cuda", dtype=bf) * 0.02 for _ in range(4)]
         x = torch.randn(tokens, k, device="cuda", dtype=bf)
         flop = 2 * tokens * n * k
-        ms = graph_time(lambda i: ops.linear(x, ws[i % 4], use_cuda=True), steps)
-        gemm_ms = graph_time(lambda i: ext.gemm(x, ws[i % 4]), steps)
+        def rounded(choice):
+            return {key: round(v, 2) if isinstance(v, float) else v for key, v in choice.items()}
+
         blas_ms = graph_time(lambda i: x @ ws[i % 4].t(), steps)
+        # the heuristic's first 16 algorithms, timed at the first call
+        h_ms = graph_time(lambda i: ops.linear(x, ws[i % 4], use_cuda=True), steps)
+        h_choice = ext.blas_choice(tokens, n, k, bf)
+        # with every algorithm swept once (as prepare_prefill_products does at start-up)
+        swept = ext.blas_tune(x, ws[0])
+        ms = graph_time(lambda i: ops.linear(x, ws[i % 4], use_cuda=True), steps)
+        choice = ext.blas_choice(tokens, n, k, bf)
         tflops = flop / (ms * 1e-3) / 1e12
         out[name] = {"m": tokens, "n": n, "k": k, "us": round(ms * 1e3, 1),
                      "tflops": round(tflops, 1),
                      "frac_of_bf16_mfma_peak": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4),
-                     "path": "blas" if "gemm" in ops.NOT_YET_FASTER else "gemm",
-                     "gemm_us": round(gemm_ms * 1e3, 1),
-                     "gemm_tflops": round(flop / (gemm_ms * 1e-3) / 1e12, 1),
-                     "blas_us": round(blas_ms * 1e3, 1),
-                     "blas_tflops": round(flop / (blas_ms * 1e-3) / 1e12, 1)}
-        log(f"prefill gemm {name} ({tokens}x{n}x{k}): {ms * 1e3:.1f} us, {tflops:.0f} TFLOP/s "
-            f"(hand GEMM {gemm_ms * 1e3:.1f} us, BLAS {blas_ms * 1e3:.1f} us)")
+                     "algorithms_swept": swept, "choice": rounded(choice),
+                     "heuristic_us": round(h_ms * 1e3, 1), "heuristic_choice": rounded(h_choice),
+                     "torch_us": round(blas_ms * 1e3, 1),
+                     "torch_tflops": round(flop / (blas_ms * 1e-3) / 1e12, 1)}
+        log(f"prefill projection {name} ({tokens}x{n}x{k}): {ms * 1e3:.1f} us, {tflops:.0f} "
+            f"TFLOP/s after sweeping {swept} algorithms (heuristic's 16: {h_ms * 1e3:.1f} us; "
+            f"torch {blas_ms * 1e3:.1f} us); choice {choice}")
         del ws
         torch.cuda.empty_cache()
     return out
@@ -555,7 +573,7 @@ def main() -> int:
                              "5 (engine), 5small (engine, 64 x 128 tokens), 5fp8 (engine, fp8 "
                              "KV cache), ew (elementwise "
                              "kernels), kv (KV write), dense (dense-cache attention), linear "
-                             "(decode projections and argmax), gemm (prefill projections), copy, "
+                             "(decode projections and argmax), gemm (prefill projections on hipBLASLt), copy, "
                              "pfocc (prefill items of 16 tiles on half and on all of the CUs)")
     parser.add_argument("--no-cpu", action="store_true")
     args = parser.parse_args()

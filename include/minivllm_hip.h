@@ -58,12 +58,9 @@ const char* mvllm_build_id(void);
 #define MVLLM_DECODE_STREAM 1 /* persistent workgroups, equal shares of all decode keys */
 #define MVLLM_DECODE_GRID 2   /* one workgroup per (sequence, split) */
 #define MVLLM_DECODE_BY_ROW 3 /* one workgroup per (query row, split), prefill rows too */
-#define MVLLM_DECODE_HEADS 4  /* one workgroup per (sequence, head unit), its waves splitting
-                                 the keys; no partials */
 typedef struct mvllm_paged_plan {
   int32_t decode_mode;       /* MVLLM_DECODE_* */
-  int32_t decode_workgroups; /* stream, heads: workgroups launched; grid modes: split-axis
-                                extent */
+  int32_t decode_workgroups; /* stream: workgroups launched; grid modes: split-axis extent */
   int32_t split_tokens;      /* grid modes: keys per split */
   int32_t prefill_mfma;      /* 1: prefill rows go to the MFMA prefill kernel */
   uint64_t workspace_bytes;  /* split partials and their index; 0 when none are needed */
@@ -81,11 +78,10 @@ typedef struct mvllm_paged_plan {
  * planner's own choice. The library reads no environment: the schedule depends on
  * the sizes, the device's CU count and these options only. */
 typedef struct mvllm_plan_options {
-  int32_t decode_schedule;     /* 0 auto; MVLLM_DECODE_STREAM, MVLLM_DECODE_GRID or
-                                  MVLLM_DECODE_HEADS forces one */
+  int32_t decode_schedule;     /* 0 auto; MVLLM_DECODE_STREAM or MVLLM_DECODE_GRID forces
+                                  one */
   int32_t decode_wgs_per_cu;   /* stream decode: workgroups per CU (default 1) */
-  int32_t decode_waves_per_cu; /* grid decode: waves per CU the splits aim for (default 16);
-                                  heads decode: waves per workgroup, 4 or 8 (default 8) */
+  int32_t decode_waves_per_cu; /* grid decode: waves per CU the splits aim for (default 16) */
   int32_t decode_split_tokens; /* grid decode: keys per split (default from the wave target) */
   int32_t prefill_schedule;    /* 0 auto; 1 forces the stream schedule, 2 the grid */
   int32_t prefill_wgs_per_cu;  /* stream prefill: workgroups per CU (default 1) */
@@ -100,10 +96,6 @@ typedef struct mvllm_plan_options {
   int32_t prefill_piece_pct;   /* grid prefill: an item is cut into pieces of at least this
                                   percentage of the mean key tiles per CU (default 150,
                                   at least 50) */
-  int32_t decode_merge;        /* stream decode: 0 auto (a merge kernel after the decode
-                                  launch combines cut sequences); 1 forces the merge
-                                  into the decode launch, by each cut sequence's last
-                                  piece (same bits, measured slower) */
 } mvllm_plan_options;
 
 /* Plan a paged_attention call. Depends only on the host-side sizes below and the
@@ -372,34 +364,57 @@ int mvllm_linear_swiglu(void* y, const void* x, const void* w_gate_up, int64_t m
                         int64_t k, int32_t dtype, void* workspace, uint64_t workspace_bytes,
                         void* stream);
 
-/* y [m, n] = x [m, k] w [n, k]^T for prefill-sized x (any m), all row-major and
- * contiguous, 16-byte aligned, fp16 or bf16 (dtype), fp32 accumulation and one rounding;
- * n and k multiples of 64. Replaces the BLAS matmul the reference's projections run
- * through at prefill sizes (model/basics.py linear, called from model/qwen3_paged.py:71-95,
- * 110 and 141-143): the q/k/v, o, gate/up and down projections of a prefill chunk.
- * Unserved shapes return MVLLM_ERR_UNSUPPORTED before any launch. */
-int mvllm_gemm(void* y, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
-               int32_t dtype, void* stream);
-
 /* y [m, n] = x [m, k] w [n, k]^T through hipBLASLt, all row-major and contiguous,
  * 16-byte aligned, fp16 or bf16 (dtype), fp32 accumulation: the vendor BLAS product the
  * reference's projections run at prefill sizes (mini_vllm/basics.py:18 linear, x @ w.T
  * through torch, called from model/qwen3_paged.py:71-95, 110 and 141-143), with its
  * per-call set-up kept: the matmul and layout descriptors are made on the first call of
- * each (device, dtype, m, n, k), the heuristic's algorithm on the first call of each
- * (device, dtype, n, k, 128-row bucket of m) - chosen for the bucket's largest, odd, m;
- * m a multiple of 128 and a shape hipBLASLt refuses it for get their own - and both
- * reused (at most 4096 shapes
- * kept; past that all are dropped and made again as called), and a 32 MiB
- * workspace is allocated on the first call of each (device, stream) that needs one
- * (hipMalloc, held until the process ends: a first call is not graph-capturable).
- * Calls from several host threads are serialised. A shape hipBLASLt has no algorithm
- * for returns MVLLM_ERR_UNSUPPORTED before any launch. */
+ * each (device, dtype, m, n, k), the algorithm on the first call of each (device, dtype,
+ * n, k, 128-row bucket of m) - the fastest of the heuristic's first 16 candidates for
+ * the bucket's largest, odd, m, each timed on that call's own operands (one host wait;
+ * a call whose stream is being captured takes the heuristic's first untimed); m a
+ * multiple of 128 gets its exact shape's candidates, and a shape hipBLASLt refuses the
+ * bucket's algorithm for gets the heuristic's first for its own m - and both reused (at
+ * most 4096 shapes kept; past that all are dropped and made again as called).
+ * `workspace` is the caller's: at least mvllm_blas_workspace_bytes() bytes, 256-byte
+ * aligned; calls on one stream may share one (they are ordered). The library allocates
+ * no device memory. Calls from several host threads are serialised. A shape hipBLASLt
+ * has no algorithm for returns MVLLM_ERR_UNSUPPORTED before any launch. */
 int mvllm_blas_linear(void* y, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
-                      int32_t dtype, void* stream);
+                      int32_t dtype, void* workspace, uint64_t workspace_bytes, void* stream);
+
+/* Bytes of the workspace mvllm_blas_linear takes. */
+uint64_t mvllm_blas_workspace_bytes(void);
+
+/* An explicit sweep for mvllm_blas_linear (no counterpart in the reference, which takes
+ * torch's heuristic algorithm): times every algorithm hipBLASLt holds that serves
+ * y = x w^T at this (m, n, k) on the caller's operands and stream (one warm-up and 3 runs
+ * each, one host wait per algorithm: ~0.5 s for a Qwen3-0.6B projection) and keeps the 12
+ * fastest as extra candidates that every later algorithm choice of (n, k) also times,
+ * each checked against that bucket's m first; choices already made for (n, k) are made
+ * again. Leaves y = x w^T. Operands and workspace as mvllm_blas_linear; refused with
+ * MVLLM_ERR_UNSUPPORTED while `stream` is being captured (it waits on the host).
+ * `timed` (may be NULL) receives the algorithms timed. Serving engines call it once per
+ * projection shape at start-up. */
+int mvllm_blas_tune(void* y, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
+                    int32_t dtype, void* workspace, uint64_t workspace_bytes, void* stream,
+                    int32_t* timed);
 
 /* Shapes mvllm_blas_linear currently keeps (for tests). */
 int mvllm_blas_plans_cached(void);
+
+/* How mvllm_blas_linear chose the algorithm it keeps for a shape. */
+typedef struct mvllm_blas_choice {
+  int32_t candidates; /* the heuristic's candidates considered */
+  int32_t timed;      /* how many were timed (0: the first taken untimed) */
+  int32_t chosen;     /* the kept one's index in the heuristic's order */
+  float first_us;     /* the heuristic's first, per product (-1 untimed) */
+  float chosen_us;    /* the kept one, per product (-1 untimed) */
+} mvllm_blas_choice;
+
+/* The choice record for (current device, dtype, m, n, k); MVLLM_ERR_INVALID if that
+ * shape has not been called (or was dropped). For reports and tests. */
+int mvllm_blas_tuning(int64_t m, int64_t n, int64_t k, int32_t dtype, mvllm_blas_choice* out);
 
 /* h_out = residual + x w^T (rounded as mvllm_linear_residual) and normed = RMSNorm(h_out)
  * with norm_weight and eps (rounded as mvllm_rmsnorm: bit for bit the two entries in
@@ -412,44 +427,6 @@ int mvllm_linear_residual_rmsnorm(void* h_out, void* normed, const void* x, cons
                                   const void* residual, const void* norm_weight, int64_t m,
                                   int64_t n, int64_t k, float eps, int32_t dtype, void* workspace,
                                   uint64_t workspace_bytes, void* stream);
-
-/* A decode-only step's attention and o projection with its residual and RMSNorm, in
- * three launches where mvllm_paged_attention + mvllm_linear_residual_rmsnorm take four:
- * the paged decode leaves every sequence's pieces as partials, and the projection's
- * first launch merges each head's pieces (in piece order, rounded as
- * mvllm_paged_attention stores its output) straight into that head's k-steps of the
- * packed W_o; the second adds the heads' partial sums, the residual and the RMSNorm as
- * mvllm_linear_residual_rmsnorm does. Replaces, for decode steps,
- * `ops.paged_attention` (paged_attention.cu:598-711) followed by `h + wo(attn)` and the
- * next `ops.rmsnorm` (model/qwen3_paged.py:85-99,134-138); the attention output itself
- * is not materialised. The paged arguments are mvllm_paged_attention's for num_seqs
- * decode rows (num_tokens = num_seqs, max_query_len = 1); w_o_packed is
- * mvllm_linear_pack of W_o [n, num_q_heads * head_dim]; h_out, normed and residual
- * [num_seqs, n] of q_dtype, norm_weight [n]. Served: head_dim 128, q_dtype bf16 or f16,
- * num_seqs <= 64, n a multiple of 256 in [512, 4096], the stream decode schedule (at
- * most 4096 sequences, GQA groups of <= 8 kv-head units); anything else returns
- * MVLLM_ERR_UNSUPPORTED before any launch. The workspace (256-byte aligned, no
- * initialisation) is mvllm_paged_attention_o_proj_workspace_bytes. The result is within
- * the projection's rounding of the two-entry sequence (K is summed per head rather than
- * per 256 elements), not bit for bit. */
-int mvllm_paged_attention_o_proj(void* h_out, void* normed, const void* q, const void* key_pool,
-                                 const void* value_pool, const float* k_scales,
-                                 const float* v_scales, const int32_t* block_tables,
-                                 const int32_t* cu_seqlens_q, const int32_t* context_lens,
-                                 const int32_t* seq_lens, int32_t num_seqs, int32_t num_q_heads,
-                                 int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                                 int64_t num_blocks, int32_t max_blocks_per_seq,
-                                 int32_t max_context_len, float scale, int32_t q_dtype,
-                                 int32_t kv_dtype, const void* w_o_packed, int64_t n,
-                                 const void* residual, const void* norm_weight, float eps,
-                                 void* workspace, uint64_t workspace_bytes, void* stream);
-
-/* The workspace mvllm_paged_attention_o_proj needs for these sizes, or 0 with
- * mvllm_last_error set when the shape is not served. Host-only. */
-uint64_t mvllm_paged_attention_o_proj_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
-                                                      int32_t num_kv_heads, int32_t head_dim,
-                                                      int32_t block_size, int32_t max_context_len,
-                                                      int32_t q_dtype, int32_t kv_dtype, int64_t n);
 
 /* Greedy sampling: out[r] (int64) = index of the maximum of logits row r, for `rows`
  * rows of `vocab` logits each, `row_stride` elements apart, dtype f32/f16/bf16. The

@@ -19,7 +19,6 @@
 #include "dense.hpp"
 #include "elementwise.hpp"
 #include "kv_write.hpp"
-#include "gemm.hpp"
 #include "linear.hpp"
 #include "sampler.hpp"
 #include "paged_attention.hpp"
@@ -65,7 +64,6 @@ struct Options {
   int decode_schedule = 0;
   int decode_wgs_per_cu = 1;
   int decode_waves_per_cu = 16;
-  int heads_waves = 8;
   int decode_split_tokens = 0;
   int prefill_schedule = 0;
   int prefill_wgs_per_cu = 1;
@@ -73,34 +71,22 @@ struct Options {
   int prefill_staging = 0;
   int prefill_pieces = mvllm::kSplitDefaultPieces;
   int prefill_piece_pct = mvllm::kSplitDefaultPct;
-  int decode_merge = 0;
 };
 
 int read_options(const mvllm_plan_options* o, Options& out) {
   out = Options{};
   if (o == nullptr) return MVLLM_OK;
-  if (o->decode_schedule < 0 || o->decode_schedule > MVLLM_DECODE_HEADS ||
-      o->decode_schedule == MVLLM_DECODE_BY_ROW ||
+  if (o->decode_schedule < 0 || o->decode_schedule > MVLLM_DECODE_GRID ||
       o->prefill_schedule < 0 || o->prefill_schedule > 2 || o->prefill_staging < 0 ||
       o->prefill_staging > 1 || o->decode_wgs_per_cu < 0 || o->decode_waves_per_cu < 0 ||
       o->decode_split_tokens < 0 || o->prefill_wgs_per_cu < 0 || o->prefill_share_tiles < 0 ||
       o->prefill_pieces < 0 || o->prefill_pieces > 64 || o->prefill_piece_pct < 0 ||
-      (o->prefill_piece_pct > 0 && o->prefill_piece_pct < 50) || o->prefill_piece_pct > 10000 ||
-      o->decode_merge < 0 || o->decode_merge > 1) {
+      (o->prefill_piece_pct > 0 && o->prefill_piece_pct < 50) || o->prefill_piece_pct > 10000) {
     return fail(MVLLM_ERR_INVALID, "paged_attention: plan options out of range");
   }
   out.decode_schedule = o->decode_schedule;
   if (o->decode_wgs_per_cu > 0) out.decode_wgs_per_cu = o->decode_wgs_per_cu;
   if (o->decode_waves_per_cu > 0) out.decode_waves_per_cu = o->decode_waves_per_cu;
-  if (o->decode_schedule == MVLLM_DECODE_HEADS && o->decode_waves_per_cu > 0) {
-    if (o->decode_waves_per_cu != 4 && o->decode_waves_per_cu != 8) {
-      return fail(MVLLM_ERR_INVALID,
-                  "paged_attention: the heads decode schedule takes 4 or 8 waves per "
-                  "workgroup, got %d",
-                  o->decode_waves_per_cu);
-    }
-    out.heads_waves = o->decode_waves_per_cu;
-  }
   out.decode_split_tokens = o->decode_split_tokens;
   out.prefill_schedule = o->prefill_schedule;
   if (o->prefill_wgs_per_cu > 0) out.prefill_wgs_per_cu = o->prefill_wgs_per_cu;
@@ -108,7 +94,6 @@ int read_options(const mvllm_plan_options* o, Options& out) {
   out.prefill_staging = o->prefill_staging;
   if (o->prefill_pieces > 0) out.prefill_pieces = o->prefill_pieces;
   if (o->prefill_piece_pct > 0) out.prefill_piece_pct = o->prefill_piece_pct;
-  out.decode_merge = o->decode_merge;
   return MVLLM_OK;
 }
 
@@ -161,7 +146,6 @@ struct Plan {
   mvllm_paged_plan pub;
   int max_splits = 1;
   int register_staging = 0;  // prefill: the register-staged kernel even where direct-to-LDS serves
-  int heads_waves = 0;       // heads decode: waves per workgroup
   int prefill_share_tiles = mvllm::kPrefillShareTiles;  // stream prefill: fewest tiles a share
   uint64_t off_o = 0;       // byte offsets into the workspace
   uint64_t off_ml = 0;
@@ -171,7 +155,6 @@ struct Plan {
   int split_ranks = 0;      // split prefill grid: rank extent, partial slots per column,
   int split_slots = 0;      // piece length (percent of the mean tiles per CU)
   int split_pct = 0;
-  int decode_merge_in_launch = 0;  // stream decode: 1 merges cut sequences in the launch
   uint64_t off_split = 0;   // split prefill grid: the partial slots
 };
 
@@ -279,8 +262,6 @@ void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, i
     plan.pub.decode_mode = MVLLM_DECODE_BY_ROW;
   } else if (all_prefill || num_seqs == 0) {
     plan.pub.decode_mode = MVLLM_DECODE_NONE;
-  } else if (o.decode_schedule == MVLLM_DECODE_HEADS) {
-    plan.pub.decode_mode = MVLLM_DECODE_HEADS;
   } else if (num_seqs <= mvllm::kMaxStreamSeqs && units <= 8 &&
              static_cast<int64_t>(num_seqs) * max_ctx < (int64_t{1} << 31) &&
              o.decode_schedule != MVLLM_DECODE_GRID) {
@@ -290,7 +271,6 @@ void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, i
   }
 
   if (plan.pub.decode_mode == MVLLM_DECODE_STREAM) {
-    plan.decode_merge_in_launch = o.decode_merge;
     // A few workgroups per CU, each streaming an equal share of all decode keys; no
     // more workgroups than there are ~64-key shares in the largest possible batch.
     int64_t wgs = static_cast<int64_t>(o.decode_wgs_per_cu) * device_cus();
@@ -304,11 +284,6 @@ void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, i
     plan.off_o = head;
     plan.off_ml = plan.off_o + align256(entries * d * sizeof(float));
     plan.pub.workspace_bytes = plan.off_ml + align256(entries * 2 * sizeof(float));
-    return;
-  }
-  if (plan.pub.decode_mode == MVLLM_DECODE_HEADS) {
-    plan.heads_waves = o.heads_waves;
-    plan.pub.decode_workgroups = static_cast<int32_t>(num_seqs * units);
     return;
   }
   if (plan.pub.decode_mode == MVLLM_DECODE_NONE) return;
@@ -336,9 +311,7 @@ void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, i
   }
 }
 
-// Arrival counters of the split prefill grid and of the stream decode's in-launch merge
-// (one launch at a time uses them: a call's decode launch leaves them at zero before
-// its prefill launch starts), in a static device array (each GPU holds
+// Arrival counters of the split prefill grid, in a static device array (each GPU holds
 // its own from the library's load until the process ends; it starts at zero and every
 // launch leaves its counters at zero). A stream takes one region of it on its first
 // split launch and keeps it, so launches that may overlap in time (other streams)
@@ -347,7 +320,6 @@ void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, i
 // itself: each device's address comes from hipGetSymbolAddress, kept here.
 constexpr int kCounterRegions = 32;
 constexpr int kCounterInts = mvllm::kSplitMaxItems * mvllm::kSplitMaxCols;
-static_assert(kCounterInts >= mvllm::kMaxStreamSeqs, "one decode counter per sequence");
 static __device__ __align__(256) int split_counters[kCounterRegions * kCounterInts];
 
 constexpr int kCounterDevices = 64;
@@ -390,16 +362,11 @@ int launch_planned(const Plan& plan, mvllm::PagedParams& p, void* workspace, int
   p.split_tokens = plan.pub.split_tokens > 0 ? plan.pub.split_tokens : mvllm::kMaxSplitTokens;
   p.max_splits = plan.max_splits;
   p.by_row = plan.pub.decode_mode == MVLLM_DECODE_BY_ROW ? 1 : 0;
-  p.heads_waves = plan.pub.decode_mode == MVLLM_DECODE_HEADS ? plan.heads_waves : 0;
   p.pf_register_staging = plan.register_staging;
   p.pf_share_tiles = plan.prefill_share_tiles;
   if (plan.pub.workspace_bytes > 0) {
     char* ws = static_cast<char*>(workspace);
-    if (plan.pub.decode_mode == MVLLM_DECODE_STREAM) {
-      p.seq_prefix = reinterpret_cast<int*>(ws);
-      // Forced (measurement): cut sequences merged in the decode launch, given counters.
-      if (plan.decode_merge_in_launch == 1) p.dec_count = split_counters_for(s);
-    }
+    if (plan.pub.decode_mode == MVLLM_DECODE_STREAM) p.seq_prefix = reinterpret_cast<int*>(ws);
     p.part_o = reinterpret_cast<float*>(ws + plan.off_o);
     p.part_ml = reinterpret_cast<float*>(ws + plan.off_ml);
     if (plan.pub.prefill_workgroups > 0) {
@@ -588,7 +555,7 @@ extern "C" {
 
 const char* mvllm_last_error(void) { return g_error; }
 
-int mvllm_abi_version(void) { return 12; }
+int mvllm_abi_version(void) { return 13; }
 
 #ifndef MVLLM_SOURCE_HASH
 #define MVLLM_SOURCE_HASH "unstamped"
@@ -618,49 +585,9 @@ int mvllm_paged_attention_plan(int32_t num_tokens, int32_t num_seqs, int32_t num
 
 namespace {
 
-// The o projection mvllm_paged_attention_o_proj runs after a decode-only paged call.
-struct OProj {
-  void* h_out;
-  void* normed;
-  const void* w;
-  int64_t n;
-  const void* residual;
-  const void* norm_weight;
-  float eps;
-};
-
-// Checks that the fused decode + o projection serves this plan and shape; the byte
-// offset of its per-head partial sums in the workspace and the workspace it needs.
-int o_proj_layout(const Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, int32_t d,
-                  int32_t max_q, int32_t q_dtype, int64_t n, uint64_t& off, uint64_t& need) {
-  if (max_q != 1 || num_tokens != num_seqs) {
-    return fail(MVLLM_ERR_UNSUPPORTED,
-                "paged_attention_o_proj: every sequence must be one decode row (num_tokens == "
-                "num_seqs, max_query_len == 1)");
-  }
-  if (plan.pub.decode_mode != MVLLM_DECODE_STREAM) {
-    return fail(MVLLM_ERR_UNSUPPORTED,
-                "paged_attention_o_proj: the batch does not run on the stream decode schedule "
-                "(at most %d sequences, GQA groups of at most 8 kv-head units)",
-                mvllm::kMaxStreamSeqs);
-  }
-  if (!mvllm::paged_o_proj_supported(q_dtype, num_seqs, n, hq, d)) {
-    return fail(MVLLM_ERR_UNSUPPORTED,
-                "paged_attention_o_proj: not served for dtype code %d, %d sequences, n=%lld, "
-                "head dim %d (16-bit, <= 64 sequences, n a multiple of 256 in [512, 4096], "
-                "head dim 128)",
-                q_dtype, num_seqs, static_cast<long long>(n), d);
-  }
-  off = align256(plan.pub.workspace_bytes);
-  need = off + mvllm::paged_o_proj_partial_bytes(num_seqs, n, hq);
-  return MVLLM_OK;
-}
-
 // The paged entry behind mvllm_paged_attention and mvllm_paged_attention_noalloc: the
 // scratch pointer is the caller's workspace for the first and this library's static
-// device array for the second (`name` prefixes the errors). With `oproj` (from
-// mvllm_paged_attention_o_proj) the decode leaves its pieces as partials, `out` is not
-// written, and the o projection with its residual and RMSNorm runs from those partials.
+// device array for the second (`name` prefixes the errors).
 int paged_attention_entry(const char* name, void* out, const void* q, const void* key_pool,
                           const void* value_pool, const float* k_scales, const float* v_scales,
                           const int32_t* block_tables, const int32_t* cu_seqlens_q,
@@ -670,8 +597,7 @@ int paged_attention_entry(const char* name, void* out, const void* q, const void
                           int64_t num_blocks, int32_t max_blocks_per_seq, int32_t max_query_len,
                           int32_t max_context_len, float scale, int32_t q_dtype,
                           int32_t kv_dtype, const mvllm_plan_options* options, void* workspace,
-                          uint64_t workspace_bytes, void* stream, bool static_scratch,
-                          const OProj* oproj = nullptr) {
+                          uint64_t workspace_bytes, void* stream, bool static_scratch) {
   int rc = check_paged_shape(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim,
                              block_size, max_query_len, max_context_len, q_dtype, kv_dtype);
   if (rc != MVLLM_OK) return rc;
@@ -679,23 +605,10 @@ int paged_attention_entry(const char* name, void* out, const void* q, const void
   rc = read_options(options, o);
   if (rc != MVLLM_OK) return rc;
   if (num_tokens == 0 || num_seqs == 0) return MVLLM_OK;
-  if ((out == nullptr && oproj == nullptr) || q == nullptr || key_pool == nullptr ||
+  if (out == nullptr || q == nullptr || key_pool == nullptr ||
       value_pool == nullptr || block_tables == nullptr || cu_seqlens_q == nullptr ||
       context_lens == nullptr || seq_lens == nullptr) {
     return fail(MVLLM_ERR_INVALID, "%s: a required pointer is NULL", name);
-  }
-  if (oproj != nullptr) {
-    if (oproj->h_out == nullptr || oproj->normed == nullptr || oproj->w == nullptr ||
-        oproj->residual == nullptr || oproj->norm_weight == nullptr) {
-      return fail(MVLLM_ERR_INVALID, "%s: a required pointer is NULL", name);
-    }
-    if ((reinterpret_cast<uintptr_t>(oproj->h_out) | reinterpret_cast<uintptr_t>(oproj->normed) |
-         reinterpret_cast<uintptr_t>(oproj->residual) |
-         reinterpret_cast<uintptr_t>(oproj->norm_weight) | reinterpret_cast<uintptr_t>(oproj->w)) %
-            16 != 0) {
-      return fail(MVLLM_ERR_INVALID, "%s: every buffer must be 16-byte aligned", name);
-    }
-    o.decode_merge = 0;  // the projection merges
   }
   if (num_blocks <= 0 || max_blocks_per_seq <= 0) {
     return fail(MVLLM_ERR_INVALID, "paged_attention: empty pool or block table");
@@ -714,13 +627,7 @@ int paged_attention_entry(const char* name, void* out, const void* q, const void
     plan = make_plan(num_tokens, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
                      max_query_len, max_context_len, q_dtype, kv_dtype, o);
   }
-  uint64_t need = plan.pub.workspace_bytes;
-  uint64_t o_off = 0;
-  if (oproj != nullptr) {
-    rc = o_proj_layout(plan, num_tokens, num_seqs, num_q_heads, head_dim, max_query_len, q_dtype,
-                       oproj->n, o_off, need);
-    if (rc != MVLLM_OK) return rc;
-  }
+  const uint64_t need = plan.pub.workspace_bytes;
   if (static_scratch && need > workspace_bytes) {
     return fail(MVLLM_ERR_UNSUPPORTED,
                 "%s: this call needs %llu bytes of scratch, more than the library's static "
@@ -766,20 +673,8 @@ int paged_attention_entry(const char* name, void* out, const void* q, const void
   p.kv_head_bytes = static_cast<int64_t>(head_dim) * kv_elem;
   p.kv_row_bytes = p.kv_head_bytes * num_kv_heads;
   p.scale = scale;
-  p.dec_defer = oproj != nullptr ? 1 : 0;
-  rc = launch_planned(plan, p, workspace, q_dtype, kv_dtype, head_dim, max_query_len,
-                      static_cast<hipStream_t>(stream), name);
-  if (rc != MVLLM_OK || oproj == nullptr) return rc;
-  char* ws = static_cast<char*>(workspace);
-  return hip_status(
-      mvllm::launch_paged_o_proj(oproj->h_out, oproj->normed,
-                                 reinterpret_cast<const float*>(ws + plan.off_o),
-                                 reinterpret_cast<const float*>(ws + plan.off_ml),
-                                 reinterpret_cast<const int*>(ws), plan.pub.decode_workgroups,
-                                 num_q_heads, oproj->w, oproj->residual, oproj->norm_weight,
-                                 num_seqs, oproj->n, oproj->eps, q_dtype, ws + o_off,
-                                 static_cast<hipStream_t>(stream)),
-      name);
+  return launch_planned(plan, p, workspace, q_dtype, kv_dtype, head_dim, max_query_len,
+                        static_cast<hipStream_t>(stream), name);
 }
 
 // The allocation-free entry's scratch: one array per device, held from the library's
@@ -862,49 +757,6 @@ int mvllm_paged_attention_noalloc(void* out, const void* q, const void* key_pool
                                head_dim, block_size, num_blocks, max_blocks_per_seq,
                                max_query_len, max_context_len, scale, q_dtype, kv_dtype,
                                options, ws, kNoallocScratchBytes, stream, true);
-}
-
-int mvllm_paged_attention_o_proj(void* h_out, void* normed, const void* q, const void* key_pool,
-                                 const void* value_pool, const float* k_scales,
-                                 const float* v_scales, const int32_t* block_tables,
-                                 const int32_t* cu_seqlens_q, const int32_t* context_lens,
-                                 const int32_t* seq_lens, int32_t num_seqs, int32_t num_q_heads,
-                                 int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                                 int64_t num_blocks, int32_t max_blocks_per_seq,
-                                 int32_t max_context_len, float scale, int32_t q_dtype,
-                                 int32_t kv_dtype, const void* w_o_packed, int64_t n,
-                                 const void* residual, const void* norm_weight, float eps,
-                                 void* workspace, uint64_t workspace_bytes, void* stream) {
-  g_error[0] = '\0';
-  if (n <= 0) return fail(MVLLM_ERR_INVALID, "paged_attention_o_proj: n must be positive");
-  const OProj oproj{h_out, normed, w_o_packed, n, residual, norm_weight, eps};
-  return paged_attention_entry("paged_attention_o_proj", nullptr, q, key_pool, value_pool,
-                               k_scales, v_scales, block_tables, cu_seqlens_q, context_lens,
-                               seq_lens, num_seqs, num_seqs, num_q_heads, num_kv_heads, head_dim,
-                               block_size, num_blocks, max_blocks_per_seq, 1, max_context_len,
-                               scale, q_dtype, kv_dtype, nullptr, workspace, workspace_bytes,
-                               stream, false, &oproj);
-}
-
-uint64_t mvllm_paged_attention_o_proj_workspace_bytes(int32_t num_seqs, int32_t num_q_heads,
-                                                      int32_t num_kv_heads, int32_t head_dim,
-                                                      int32_t block_size, int32_t max_context_len,
-                                                      int32_t q_dtype, int32_t kv_dtype, int64_t n) {
-  g_error[0] = '\0';
-  if (check_paged_shape(num_seqs, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, 1,
-                        max_context_len, q_dtype, kv_dtype) != MVLLM_OK) {
-    return 0;
-  }
-  Options o;
-  o.decode_merge = 0;
-  const Plan plan = make_plan(num_seqs, num_seqs, num_q_heads, num_kv_heads, head_dim,
-                              block_size, 1, max_context_len, q_dtype, kv_dtype, o);
-  uint64_t off = 0, need = 0;
-  if (o_proj_layout(plan, num_seqs, num_seqs, num_q_heads, head_dim, 1, q_dtype, n, off, need) !=
-      MVLLM_OK) {
-    return 0;
-  }
-  return need;
 }
 
 int mvllm_dense_attention_plan(const mvllm_dense_args* args, uint64_t* workspace_bytes) {
@@ -1365,34 +1217,10 @@ int mvllm_linear_residual_rmsnorm(void* h_out, void* normed, const void* x, cons
                     "linear_residual_rmsnorm: launch");
 }
 
-int mvllm_gemm(void* y, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
-               int32_t dtype, void* stream) {
-  g_error[0] = '\0';
-  if (m < 0 || n < 0 || k < 0) return fail(MVLLM_ERR_INVALID, "gemm: negative size");
-  if (m == 0 || n == 0) return MVLLM_OK;
-  if (dtype != mvllm::kF16 && dtype != mvllm::kBF16) {
-    return fail(MVLLM_ERR_UNSUPPORTED, "gemm: dtype code %d is not served; fp16 or bf16", dtype);
-  }
-  if (x == nullptr || w == nullptr || y == nullptr) {
-    return fail(MVLLM_ERR_INVALID, "gemm: a required pointer is NULL");
-  }
-  if (!mvllm::gemm_supported(dtype, m, n, k)) {
-    return fail(MVLLM_ERR_UNSUPPORTED,
-                "gemm: shape M=%lld N=%lld K=%lld is not served; N and K must be multiples of "
-                "64 and every operand under 2 GiB",
-                static_cast<long long>(m), static_cast<long long>(n), static_cast<long long>(k));
-  }
-  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
-       reinterpret_cast<uintptr_t>(y)) % 16 != 0) {
-    return fail(MVLLM_ERR_INVALID, "gemm: x, w and y must be 16-byte aligned");
-  }
-  return hip_status(mvllm::launch_gemm(y, x, w, m, n, k, dtype, device_cus(), -1,
-                                       static_cast<hipStream_t>(stream)),
-                    "gemm: launch");
-}
+uint64_t mvllm_blas_workspace_bytes(void) { return mvllm::kBlasWorkspaceBytes; }
 
 int mvllm_blas_linear(void* y, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
-                      int32_t dtype, void* stream) {
+                      int32_t dtype, void* workspace, uint64_t workspace_bytes, void* stream) {
   g_error[0] = '\0';
   if (m < 0 || n < 0 || k < 0) return fail(MVLLM_ERR_INVALID, "blas_linear: negative size");
   if (m == 0 || n == 0) return MVLLM_OK;
@@ -1408,7 +1236,15 @@ int mvllm_blas_linear(void* y, const void* x, const void* w, int64_t m, int64_t 
        reinterpret_cast<uintptr_t>(y)) % 16 != 0) {
     return fail(MVLLM_ERR_INVALID, "blas_linear: x, w and y must be 16-byte aligned");
   }
-  const mvllm::BlasStatus st = mvllm::blas_linear(y, x, w, m, n, k, dtype,
+  if (workspace == nullptr || workspace_bytes < mvllm::kBlasWorkspaceBytes ||
+      reinterpret_cast<uintptr_t>(workspace) % 256 != 0) {
+    return fail(MVLLM_ERR_INVALID,
+                "blas_linear: the workspace must be 256-byte aligned and hold %llu bytes "
+                "(mvllm_blas_workspace_bytes), got %llu",
+                static_cast<unsigned long long>(mvllm::kBlasWorkspaceBytes),
+                static_cast<unsigned long long>(workspace_bytes));
+  }
+  const mvllm::BlasStatus st = mvllm::blas_linear(y, x, w, m, n, k, dtype, workspace,
                                                   static_cast<hipStream_t>(stream));
   switch (st.kind) {
     case 0:
@@ -1427,6 +1263,69 @@ int mvllm_blas_linear(void* y, const void* x, const void* w, int64_t m, int64_t 
 }
 
 int mvllm_blas_plans_cached(void) { return mvllm::blas_plans_cached(); }
+
+int mvllm_blas_tune(void* y, const void* x, const void* w, int64_t m, int64_t n, int64_t k,
+                    int32_t dtype, void* workspace, uint64_t workspace_bytes, void* stream,
+                    int32_t* timed) {
+  g_error[0] = '\0';
+  if (timed != nullptr) *timed = 0;
+  if (m <= 0 || n <= 0 || k <= 0) return fail(MVLLM_ERR_INVALID, "blas_tune: sizes must be positive");
+  if (dtype != mvllm::kF16 && dtype != mvllm::kBF16) {
+    return fail(MVLLM_ERR_UNSUPPORTED, "blas_tune: dtype code %d is not served; fp16 or bf16",
+                dtype);
+  }
+  if (x == nullptr || w == nullptr || y == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "blas_tune: a required pointer is NULL");
+  }
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+       reinterpret_cast<uintptr_t>(y)) % 16 != 0) {
+    return fail(MVLLM_ERR_INVALID, "blas_tune: x, w and y must be 16-byte aligned");
+  }
+  if (workspace == nullptr || workspace_bytes < mvllm::kBlasWorkspaceBytes ||
+      reinterpret_cast<uintptr_t>(workspace) % 256 != 0) {
+    return fail(MVLLM_ERR_INVALID,
+                "blas_tune: the workspace must be 256-byte aligned and hold %llu bytes "
+                "(mvllm_blas_workspace_bytes), got %llu",
+                static_cast<unsigned long long>(mvllm::kBlasWorkspaceBytes),
+                static_cast<unsigned long long>(workspace_bytes));
+  }
+  int count = 0;
+  const mvllm::BlasStatus st = mvllm::blas_tune(y, x, w, m, n, k, dtype, workspace,
+                                                static_cast<hipStream_t>(stream), count);
+  if (timed != nullptr) *timed = count;
+  switch (st.kind) {
+    case 0:
+      return MVLLM_OK;
+    case 1:
+      return fail(MVLLM_ERR_HIP, "blas_tune: %s: HIP error %d (%s)", st.what, st.code,
+                  hipGetErrorString(static_cast<hipError_t>(st.code)));
+    case 3:
+    case 4:
+      return fail(MVLLM_ERR_UNSUPPORTED, "blas_tune: M=%lld N=%lld K=%lld: %s",
+                  static_cast<long long>(m), static_cast<long long>(n),
+                  static_cast<long long>(k), st.what);
+    default:
+      return fail(MVLLM_ERR_HIP, "blas_tune: hipBLASLt %s failed with status %d", st.what,
+                  st.code);
+  }
+}
+
+int mvllm_blas_tuning(int64_t m, int64_t n, int64_t k, int32_t dtype, mvllm_blas_choice* out) {
+  g_error[0] = '\0';
+  if (out == nullptr) return fail(MVLLM_ERR_INVALID, "blas_tuning: out is NULL");
+  mvllm::BlasTuning t;
+  if (!mvllm::blas_tuning(m, n, k, dtype, t)) {
+    return fail(MVLLM_ERR_INVALID, "blas_tuning: M=%lld N=%lld K=%lld dtype %d was not called",
+                static_cast<long long>(m), static_cast<long long>(n), static_cast<long long>(k),
+                dtype);
+  }
+  out->candidates = t.candidates;
+  out->timed = t.timed;
+  out->chosen = t.chosen;
+  out->first_us = t.first_us;
+  out->chosen_us = t.chosen_us;
+  return MVLLM_OK;
+}
 
 int mvllm_kv_write(void* key_pool, void* value_pool, float* k_scales, float* v_scales,
                    const void* key, const void* value, const int32_t* slot_mapping,

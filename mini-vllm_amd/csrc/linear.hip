@@ -423,153 +423,6 @@ __global__ __launch_bounds__(kWave) void skinny_reduce_norm_kernel(
   }
 }
 
-// A decode step's o projection straight from the paged decode's partials (the decode
-// launch left every sequence's pieces in its workspace, `dec_defer`), in place of the
-// decode's merge kernel and the projection's partial-sum launch. One workgroup per
-// (query head, 8 tiles of 32 output columns): it folds the head's pieces of every row
-// (sequence r is row r of a decode-only batch) in piece order from an empty state and
-// rounds them to the activation dtype - what the merge kernel stores as the attention
-// output - into LDS, then multiplies them into the head's 8 k-steps of the packed W_o,
-// the weight loads issued before the merge. Its partial sums go to partials[tile][head]
-// [row][col]: K cut at head boundaries (the reduce-norm kernel adds the heads' partials in
-// head order), where the two-launch projection cuts K every 256 elements.
-constexpr int kOHeadDim = 128;
-constexpr int kOTilesPerWave = 2;
-constexpr int kOTilesPerGroup = kGroup * kOTilesPerWave;
-
-struct DecodePieces {
-  const float* part_o;    // [slot * H_q + head][128]
-  const float* part_ml;   // [slot * H_q + head][2]: running max (log2 units), sum
-  const int* seq_prefix;  // [m + 1] decode keys before each sequence
-  int stream_wgs;         // the decode launch's workgroups
-  int hq;
-};
-
-template <typename T, int MB>
-__global__ __launch_bounds__(kGroup * kWave) void merge_o_partial_kernel(
-    float* __restrict__ partials, const DecodePieces pin, const void* __restrict__ w, int m, int k) {
-  constexpr int kRows = MB * 32;
-  constexpr int kHeadSteps = kOHeadDim / 16;
-  constexpr int kRowChunks = kOHeadDim / 8;  // 16-byte chunks of one x row
-  __shared__ __attribute__((aligned(16))) char xs[kRows * kOHeadDim * 2];
-  const int hd = blockIdx.y;
-  const int lane = threadIdx.x % kWave;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int l32 = lane & 31;
-  const int hsel = lane >> 5;
-  const int steps = k / 16;
-
-  // This wave's tiles of W_o, the head's k-steps (1 KB each, the lane's 16 B), loaded
-  // right after the first batch of partials so that batch's fold does not wait for them.
-  u32x4 a[kOTilesPerWave][kHeadSteps];
-  bool weights_loaded = false;
-  auto load_weights = [&]() __attribute__((always_inline)) {
-#pragma unroll
-    for (int t = 0; t < kOTilesPerWave; ++t) {
-      const int tile = blockIdx.x * kOTilesPerGroup + kOTilesPerWave * wave + t;
-      const char* wp = static_cast<const char*>(w) +
-                       (static_cast<int64_t>(tile) * steps + hd * kHeadSteps) * 1024 + lane * 16;
-#pragma unroll
-      for (int u = 0; u < kHeadSteps; ++u) a[t][u] = load16(wp + u * 1024);
-    }
-    weights_loaded = true;
-  };
-
-  // The head's attention output of every row: thread -> (row, 16 elements); chunk c of
-  // row r at chunk c ^ (r & 15) (the fragment reads below: 32 rows at one chunk).
-  const int64_t total = pin.seq_prefix[m];
-  const int64_t wgs = decode_stream_shares(total, pin.stream_wgs);
-  for (int i = threadIdx.x; i < kRows * (kOHeadDim / 16); i += kGroup * kWave) {
-    const int row = i / (kOHeadDim / 16);
-    const int d0 = (i % (kOHeadDim / 16)) * 16;
-    float mx = -INFINITY, l = 0.0f;
-    f32x4 o[4] = {};
-    if (row < m) {
-      const int64_t begin = pin.seq_prefix[row];
-      const int64_t end = pin.seq_prefix[row + 1];
-      if (end > begin) {
-        const int64_t first = share_owner(begin, total, wgs);
-        const int pieces = static_cast<int>(share_owner(end - 1, total, wgs) - first + 1);
-        // The loads of kBatch pieces go out together, then they are folded in order.
-        constexpr int kBatch = 8;
-        for (int i0 = 0; i0 < pieces; i0 += kBatch) {
-          float mi[kBatch], li[kBatch];
-          f32x4 oi[kBatch][4];
-#pragma unroll
-          for (int u = 0; u < kBatch; ++u) {
-            const int64_t pidx = (first + min(i0 + u, pieces - 1) + row) * pin.hq + hd;
-            mi[u] = pin.part_ml[pidx * 2];
-            li[u] = pin.part_ml[pidx * 2 + 1];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              oi[u][q] = *reinterpret_cast<const f32x4*>(pin.part_o + pidx * kOHeadDim + d0 + 4 * q);
-            }
-          }
-          if (!weights_loaded) load_weights();
-#pragma unroll
-          for (int u = 0; u < kBatch; ++u) {
-            if (i0 + u >= pieces) continue;
-            const float mn = fmaxf(mx, mi[u]);
-            const float mu = mn == -INFINITY ? 0.0f : mn;
-            const float fa = __builtin_amdgcn_exp2f(mx - mu);
-            const float fb = __builtin_amdgcn_exp2f(mi[u] - mu);
-            l = l * fa + li[u] * fb;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) o[q] = o[q] * fa + oi[u][q] * fb;
-            mx = mn;
-          }
-        }
-      }
-    }
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      u32x4 v;
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const int j = 8 * half + e;
-        v[e / 2] = static_cast<uint32_t>(LinMma<T>::bits(o[j / 4][j % 4] * inv)) |
-                   (static_cast<uint32_t>(LinMma<T>::bits(o[(j + 1) / 4][(j + 1) % 4] * inv)) << 16);
-      }
-      const int chunk = (d0 / 8 + half) ^ (row & 15);
-      *reinterpret_cast<u32x4*>(xs + (row * kRowChunks + chunk) * 16) = v;
-    }
-  }
-  if (!weights_loaded) load_weights();
-  __syncthreads();
-
-  f32x16 acc[kOTilesPerWave][MB];
-#pragma unroll
-  for (int t = 0; t < kOTilesPerWave; ++t) {
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) acc[t][mb] = f32x16{};
-  }
-#pragma unroll
-  for (int u = 0; u < kHeadSteps; ++u) {
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const int row = mb * 32 + l32;
-      const u32x4 b = *reinterpret_cast<const u32x4*>(xs + (row * kRowChunks + ((2 * u + hsel) ^ (row & 15))) * 16);
-#pragma unroll
-      for (int t = 0; t < kOTilesPerWave; ++t) acc[t][mb] = LinMma<T>::run(a[t][u], b, acc[t][mb]);
-    }
-  }
-#pragma unroll
-  for (int t = 0; t < kOTilesPerWave; ++t) {
-    const int tile = blockIdx.x * kOTilesPerGroup + kOTilesPerWave * wave + t;
-    float* dst = partials + (static_cast<int64_t>(tile) * pin.hq + hd) * (kRows * kColTile);
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      float* row = dst + (mb * 32 + l32) * kColTile + 4 * hsel;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        *reinterpret_cast<f32x4*>(row + 8 * q) =
-            f32x4{acc[t][mb][4 * q], acc[t][mb][4 * q + 1], acc[t][mb][4 * q + 2], acc[t][mb][4 * q + 3]};
-      }
-    }
-  }
-}
-
 int row_blocks(int64_t m) { return m <= 32 ? 1 : 2; }
 
 template <typename T, int MB, int EPI>
@@ -647,30 +500,6 @@ hipError_t launch_reduce_norm(void* h_out, void* normed, const float* partials, 
   return hipGetLastError();
 }
 
-template <typename T>
-hipError_t launch_paged_o_t(void* h_out, void* normed, const DecodePieces& pin, const void* w,
-                            const void* residual, const void* norm_weight, int m, int n, float eps,
-                            float* partials, hipStream_t stream) {
-  const int k = pin.hq * kOHeadDim;
-  const dim3 grid(static_cast<unsigned>(n / (kOTilesPerGroup * kColTile)), static_cast<unsigned>(pin.hq));
-  const int mb = row_blocks(m);
-  if (mb == 1) {
-    merge_o_partial_kernel<T, 1><<<grid, kGroup * kWave, 0, stream>>>(partials, pin, w, m, k);
-  } else {
-    merge_o_partial_kernel<T, 2><<<grid, kGroup * kWave, 0, stream>>>(partials, pin, w, m, k);
-  }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  const int per_lane = n / 8 / kWave;
-  if (per_lane <= 2) {
-    return launch_reduce_norm<T, 2>(h_out, normed, partials, residual, norm_weight, m, n, pin.hq, eps, mb, stream);
-  }
-  if (per_lane <= 4) {
-    return launch_reduce_norm<T, 4>(h_out, normed, partials, residual, norm_weight, m, n, pin.hq, eps, mb, stream);
-  }
-  return launch_reduce_norm<T, 8>(h_out, normed, partials, residual, norm_weight, m, n, pin.hq, eps, mb, stream);
-}
-
 // Packs W [n, k] (row-major) into the fragment order: one thread per 16 bytes.
 __global__ void pack_kernel(uint4* __restrict__ dst, const uint4* __restrict__ src, int64_t n,
                             int64_t k) {
@@ -746,32 +575,6 @@ hipError_t launch_skinny_linear_swiglu(void* y, const void* x, const void* w_gat
                                        hipStream_t stream) {
   return launch_e<kLinearSwiglu>(Out{y, nullptr, nullptr, nullptr, 0, 0}, x, w_gate_up, m, 2 * n_out,
                                  k, dtype, workspace, stream);
-}
-
-bool paged_o_proj_supported(int dtype, int64_t m, int64_t n, int hq, int head_dim) {
-  return (dtype == kBF16 || dtype == kF16) && head_dim == kOHeadDim && m >= 1 &&
-         m <= kSkinnyMaxRows && hq >= 1 && n % (kOTilesPerGroup * kColTile) == 0 && n >= 512 &&
-         n <= 4096;
-}
-
-uint64_t paged_o_proj_partial_bytes(int64_t m, int64_t n, int hq) {
-  return static_cast<uint64_t>(n / kColTile) * hq * row_blocks(m) * 32 * kColTile * sizeof(float);
-}
-
-hipError_t launch_paged_o_proj(void* h_out, void* normed, const float* part_o, const float* part_ml,
-                               const int* seq_prefix, int stream_wgs, int hq, const void* w,
-                               const void* residual, const void* norm_weight, int64_t m, int64_t n,
-                               float eps, int dtype, void* partials, hipStream_t stream) {
-  const DecodePieces pin{part_o, part_ml, seq_prefix, stream_wgs, hq};
-  const int mi = static_cast<int>(m), ni = static_cast<int>(n);
-  float* pp = static_cast<float*>(partials);
-  if (dtype == kBF16) {
-    return launch_paged_o_t<bf16_t>(h_out, normed, pin, w, residual, norm_weight, mi, ni, eps, pp, stream);
-  }
-  if (dtype == kF16) {
-    return launch_paged_o_t<f16_t>(h_out, normed, pin, w, residual, norm_weight, mi, ni, eps, pp, stream);
-  }
-  return hipErrorInvalidValue;
 }
 
 hipError_t launch_skinny_linear_residual_rmsnorm(void* h_out, void* normed, const void* x,

@@ -55,17 +55,4 @@ hipError_t launch_skinny_linear_residual_rmsnorm(void* h_out, void* normed, cons
                                                  int64_t k, float eps, int dtype, void* workspace,
                                                  hipStream_t stream);
 
-// The o projection of a decode-only step with its residual and RMSNorm, from the paged
-// decode's deferred partials (part_o / part_ml / seq_prefix of its stream schedule over
-// `stream_wgs` workgroups): h = T(residual + T(attn w^T)), normed = RMSNorm(h) * weight,
-// attn = the merged attention output (H_q heads of 128) of row r = sequence r. Served
-// for 16-bit activations, m <= 64 rows, n a multiple of 256 in [512, 4096].
-bool paged_o_proj_supported(int dtype, int64_t m, int64_t n, int hq, int head_dim);
-// Bytes of the fp32 per-head partial sums it needs (caller-owned, no initialisation).
-uint64_t paged_o_proj_partial_bytes(int64_t m, int64_t n, int hq);
-hipError_t launch_paged_o_proj(void* h_out, void* normed, const float* part_o, const float* part_ml,
-                               const int* seq_prefix, int stream_wgs, int hq, const void* w,
-                               const void* residual, const void* norm_weight, int64_t m, int64_t n,
-                               float eps, int dtype, void* partials, hipStream_t stream);
-
 }  // namespace mvllm

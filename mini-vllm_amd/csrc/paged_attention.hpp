@@ -131,8 +131,6 @@ struct PagedParams {
   int split_tokens;   // grid decode: nominal keys per split
   int max_splits;     // grid decode: grid extent along the split axis
   int by_row;         // grid decode: 1 = one unit per query row (serves prefill rows too)
-  int heads_waves;    // decode: > 0 selects the heads schedule, this many waves per
-                      // (sequence, head unit) workgroup
   float scale;
   float* part_o;      // split partials, D fp32 each
   float* part_ml;     // split partials' (running max in log2 units, sum)
@@ -156,11 +154,6 @@ struct PagedParams {
   int* pf_count;      // split grid: [kSplitMaxItems][columns] arrival counters, zero
                       // before the launch and left zero by it
   float* pf_part;     // split grid: [pf_slots][columns] partials of kSplitSlotFloats
-  int* dec_count;     // stream decode: non-null merges cut sequences in the decode launch,
-                      // [num_seqs] arrival counters, zero before the launch and left zero
-  int dec_defer;      // stream decode: 1 leaves every sequence's pieces as partials (whole
-                      // sequences too, one piece) for the caller's merge; no output, no
-                      // merge kernel
 };
 
 // Splits of one row: as many as its visible context needs at `split_tokens` keys

@@ -280,79 +280,6 @@ struct Decode {
       }
     }
   }
-
-  // write_partial (heads at consecutive indices) with relaxed agent-scope atomic
-  // stores, for a merge in the same launch by another workgroup.
-  __device__ static void write_partial_coherent(const PagedParams& p, int64_t pidx0, int r,
-                                                const State& st) {
-#pragma unroll
-    for (int h = 0; h < GC; ++h) {
-      const int64_t pidx = pidx0 + h;
-      float* po = p.part_o + pidx * D + r * E;
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        __hip_atomic_store(po + e, st.acc[h][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      if (r == 0) {
-        __hip_atomic_store(p.part_ml + pidx * 2, st.m[h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(p.part_ml + pidx * 2 + 1, st.l[h], __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-  }
-
-  // Replace `st` (piece `self` of the sequence) with the merge of all its pieces, folded
-  // in piece order from an empty state exactly as the merge kernel folds them (piece i
-  // in slot (first + i + seq), this piece's own from registers), so the result is the
-  // same whichever piece finishes last; the loads of kBatch pieces are issued together.
-  __device__ static void merge_pieces(const PagedParams& p, int64_t first, int pieces, int self,
-                                      int seq, int h0, int r, State& st) {
-    constexpr int kBatch = 4;
-    auto get = [](const float* at) __attribute__((always_inline)) -> float {
-      return __hip_atomic_load(at, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    };
-#pragma unroll
-    for (int h = 0; h < GC; ++h) {
-      float m = -INFINITY, l = 0.0f, o[E];
-#pragma unroll
-      for (int e = 0; e < E; ++e) o[e] = 0.0f;
-      for (int i0 = 0; i0 < pieces; i0 += kBatch) {
-        float mi[kBatch], li[kBatch], oi[kBatch][E];
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-          const int i = min(i0 + u, pieces - 1);
-          const int64_t pidx = (first + i + seq) * p.hq + h0 + h;
-          if (i == self) {
-            mi[u] = st.m[h];
-            li[u] = st.l[h];
-#pragma unroll
-            for (int e = 0; e < E; ++e) oi[u][e] = st.acc[h][e];
-          } else {
-            mi[u] = get(p.part_ml + pidx * 2);
-            li[u] = get(p.part_ml + pidx * 2 + 1);
-#pragma unroll
-            for (int e = 0; e < E; ++e) oi[u][e] = get(p.part_o + pidx * D + r * E + e);
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-          if (i0 + u >= pieces) continue;
-          const float mn = fmaxf(m, mi[u]);
-          const float mu = mn == -INFINITY ? 0.0f : mn;
-          const float a = fast_exp2(m - mu);
-          const float b = fast_exp2(mi[u] - mu);
-          l = l * a + li[u] * b;
-#pragma unroll
-          for (int e = 0; e < E; ++e) o[e] = o[e] * a + oi[u][e] * b;
-          m = mn;
-        }
-      }
-      st.m[h] = m;
-      st.l[h] = l;
-#pragma unroll
-      for (int e = 0; e < E; ++e) st.acc[h][e] = o[e];
-    }
-  }
 };
 
 // The (kv head, head chunk) unit of a wave; false when the wave has none.
@@ -369,22 +296,10 @@ __device__ __forceinline__ bool wave_unit(const PagedParams& p, int unit, int& k
 
 // ------------------------------------------------------------ stream schedule
 
-// kFuse (a plan option, for measurement): a sequence cut between workgroups is merged
-// by the last of its pieces to finish, in this launch (no merge kernel). Measured
-// slower than the merge kernel: config 2 116-121 us against 109-111, and the config-5
-// engine 10.5K against 12.6K output tok/s (sequences of ~1200 keys cut into ~8 pieces:
-// each last piece's uncached partial reads and the workgroup barriers at cut
-// segments sit at the end of the launch). Every piece stores its (m, l, O) partial
-// with relaxed agent-scope atomic stores (kept coherent per location across the XCDs'
-// L2s; an agent-scope fence would write back and invalidate the whole L2 of the XCD),
-// waits for them to complete and counts itself in on the sequence's arrival counter;
-// the one that finds all others in resets the counter and combines their partials,
-// read with agent-scope atomic loads, with its own state.
-template <typename TQ, typename TKV, int D, int GC, bool kFuse>
+template <typename TQ, typename TKV, int D, int GC>
 __global__ __launch_bounds__(512) void paged_decode_stream_kernel(const PagedParams p) {
   using K = Decode<TKV, D, GC>;
   __shared__ int s_prefix[kMaxStreamSeqs + 1];  // decode keys before sequence s
-  __shared__ int s_last;                        // kFuse: this workgroup merges the sequence
 
   const int n = p.num_seqs;
   const int tid = threadIdx.x;
@@ -454,32 +369,10 @@ __global__ __launch_bounds__(512) void paged_decode_stream_kernel(const PagedPar
       K::stream(p, table, nullptr, 0, kvh, sb, se, g, r, qf, score_scale, st);
       K::merge_row_groups(st);
       if (g == 0) {
-        if (whole && p.dec_defer == 0) {
+        if (whole) {
           K::template write_output<TQ>(p, row, h0, r, st);
-        } else if constexpr (kFuse) {
-          K::write_partial_coherent(p, (static_cast<int64_t>(blockIdx.x) + seq) * p.hq + h0, r, st);
         } else {
           K::write_partial(p, (static_cast<int64_t>(blockIdx.x) + seq) * p.hq + h0, 1, r, st);
-        }
-      }
-    }
-    if constexpr (kFuse) {
-      if (!whole) {  // uniform over the workgroup
-        const int64_t first = share_owner(base, total, wgs);
-        const int pieces = static_cast<int>(share_owner(base + ctx - 1, total, wgs) - first + 1);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (tid == 0) {
-          int* count = p.dec_count + seq;
-          const int before = __hip_atomic_fetch_add(count, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          const int last = before == pieces - 1 ? 1 : 0;
-          if (last) __hip_atomic_store(count, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          s_last = last;
-        }
-        __syncthreads();
-        if (s_last != 0 && active && g == 0) {
-          K::merge_pieces(p, first, pieces, static_cast<int>(blockIdx.x - first), seq, h0, r, st);
-          K::template write_output<TQ>(p, row, h0, r, st);
         }
       }
     }
@@ -544,77 +437,6 @@ __global__ __launch_bounds__(1024) void paged_decode_stream_merge_kernel(const P
     const int64_t obase = (static_cast<int64_t>(row) * p.hq + head) * D + d;
 #pragma unroll
     for (int k = 0; k < 4; ++k) Elem<TQ>::store(p.out, obase + k, o[k] * inv);
-  }
-}
-
-// ------------------------------------------------------------ heads schedule
-
-// One workgroup per (decode sequence, wave unit): its W waves take W contiguous,
-// 16-key-aligned runs of the sequence's keys, stream them for the unit's kv head and
-// query heads, and combine their states through LDS (the reference's rescale,
-// paged_attention.cu:284-301, over the waves in order). The output is written by the
-// same launch: no partials, no second kernel. Sequences that are prefill chunks (or
-// have no context) leave the workgroup idle.
-template <typename TQ, typename TKV, int D, int GC, int W>
-__global__ __launch_bounds__(W * kWave) void paged_decode_heads_kernel(const PagedParams p) {
-  using K = Decode<TKV, D, GC>;
-  __shared__ float s_ml[W][GC][2];
-  __shared__ float s_o[W][GC][D];
-
-  const int seq = blockIdx.y;
-  if (p.seq_lens[seq] != 1) return;  // whole workgroup: no barrier follows for it
-  const int ctx = p.context_lens[seq];
-  if (ctx <= 0) return;  // whole workgroup
-  int kvh = 0, h0 = 0;
-  if (!wave_unit<GC>(p, blockIdx.x, kvh, h0)) return;  // whole workgroup
-
-  const int wave = threadIdx.x / kWave;
-  const int lane = threadIdx.x % kWave;
-  const int g = lane / K::R;
-  const int r = lane % K::R;
-  const int row = p.cu_seqlens_q[seq];
-  const int per = ((ctx + W - 1) / W + 15) & ~15;
-  const int sb = min(wave * per, ctx);
-  const int se = min(sb + per, ctx);
-
-  typename K::State st;
-  K::init(st);
-  if (sb < se) {
-    float qf[GC][K::E];
-    K::template load_queries<TQ>(p, row, h0, r, qf);
-    const int32_t* table = p.block_tables + static_cast<int64_t>(seq) * p.max_blocks;
-    K::stream(p, table, nullptr, 0, kvh, sb, se, g, r, qf, p.scale * kLog2e, st);
-  }
-  K::merge_row_groups(st);
-  if (g == 0) {
-#pragma unroll
-    for (int h = 0; h < GC; ++h) {
-#pragma unroll
-      for (int e = 0; e < K::E; ++e) s_o[wave][h][r * K::E + e] = st.acc[h][e];
-      if (r == 0) {
-        s_ml[wave][h][0] = st.m[h];
-        s_ml[wave][h][1] = st.l[h];
-      }
-    }
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < GC * D; i += W * kWave) {
-    const int h = i / D;
-    const int d = i % D;
-    float m = -INFINITY, l = 0.0f, o = 0.0f;
-#pragma unroll
-    for (int w = 0; w < W; ++w) {
-      const float mw = s_ml[w][h][0];
-      const float mx = fmaxf(m, mw);
-      const float mu = mx == -INFINITY ? 0.0f : mx;
-      const float a = fast_exp2(m - mu);
-      const float b = fast_exp2(mw - mu);
-      l = l * a + s_ml[w][h][1] * b;
-      o = o * a + s_o[w][h][d] * b;
-      m = mx;
-    }
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    Elem<TQ>::store(p.out, (static_cast<int64_t>(row) * p.hq + h0 + h) * D + d, o * inv);
   }
 }
 
@@ -736,24 +558,11 @@ hipError_t launch_decode_g(const PagedParams& p, hipStream_t stream) {
   const int units = p.hk * (p.hq / p.hk / GC);
   const int waves = decode_waves(p, GC);
   constexpr int kHeadsPerMergeBlock = 4;
-  if (p.heads_waves > 0) {
-    const dim3 grid(units, p.num_seqs);
-    switch (p.heads_waves) {
-      case 4: paged_decode_heads_kernel<TQ, TKV, D, GC, 4><<<grid, 4 * kWave, 0, stream>>>(p); break;
-      case 8: paged_decode_heads_kernel<TQ, TKV, D, GC, 8><<<grid, 8 * kWave, 0, stream>>>(p); break;
-      default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
-  }
   if (p.stream_wgs > 0) {
     if (units > 8) return hipErrorInvalidValue;  // planner keeps stream mode to <= 8 units
-    if (p.dec_count != nullptr) {
-      paged_decode_stream_kernel<TQ, TKV, D, GC, true><<<p.stream_wgs, waves * kWave, 0, stream>>>(p);
-      return hipGetLastError();
-    }
-    paged_decode_stream_kernel<TQ, TKV, D, GC, false><<<p.stream_wgs, waves * kWave, 0, stream>>>(p);
+    paged_decode_stream_kernel<TQ, TKV, D, GC><<<p.stream_wgs, waves * kWave, 0, stream>>>(p);
     hipError_t err = hipGetLastError();
-    if (err != hipSuccess || p.dec_defer != 0) return err;
+    if (err != hipSuccess) return err;
     const int n4 = p.hq * D / 4;
     const int threads = n4 >= 1024 ? 1024 : (n4 + kWave - 1) / kWave * kWave;
     paged_decode_stream_merge_kernel<TQ, D><<<p.num_seqs, threads, 0, stream>>>(p, p.stream_wgs);

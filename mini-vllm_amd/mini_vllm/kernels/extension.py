@@ -64,7 +64,7 @@ EXTRA_FLAGS = {"elementwise.hip": ["-ffp-contract=off"], "linear.hip": ["-ffp-co
 # process that has imported torch the library binds to that copy.
 LINK_LIBS = ["-L/opt/rocm/lib", "-lhipblaslt"]
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 DTYPE_CODES: dict[torch.dtype, int] = {
     torch.float32: 0,
@@ -191,16 +191,15 @@ class _PlanOptions(ctypes.Structure):
         ("prefill_share_tiles", ctypes.c_int32),
         ("prefill_pieces", ctypes.c_int32),
         ("prefill_piece_pct", ctypes.c_int32),
-        ("decode_merge", ctypes.c_int32),
     ]
 
 
-SCHEDULES = {"stream": 1, "grid": 2, "heads": 4}
+SCHEDULES = {"stream": 1, "grid": 2}
 
 
 def make_plan_options(options: dict[str, Any] | None) -> "_PlanOptions | None":
     """``mvllm_plan_options`` from a dict of its field names (schedules may be given as
-    "stream" / "grid" / "heads"); None for the planner's defaults."""
+    "stream" / "grid"); None for the planner's defaults."""
     if not options:
         return None
     fields = {name for name, _ in _PlanOptions._fields_}
@@ -224,7 +223,19 @@ class _Plan(ctypes.Structure):
     ]
 
 
-DECODE_MODES = {0: "none", 1: "stream", 2: "grid", 3: "by_row", 4: "heads"}
+class _BlasChoice(ctypes.Structure):
+    """``mvllm_blas_choice`` of include/minivllm_hip.h."""
+
+    _fields_ = [
+        ("candidates", ctypes.c_int32),
+        ("timed", ctypes.c_int32),
+        ("chosen", ctypes.c_int32),
+        ("first_us", ctypes.c_float),
+        ("chosen_us", ctypes.c_float),
+    ]
+
+
+DECODE_MODES = {0: "none", 1: "stream", 2: "grid", 3: "by_row"}
 
 
 def _bind(lib: ctypes.CDLL) -> None:
@@ -293,17 +304,17 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_linear_swiglu.argtypes = [p, p, p, i64, i64, i64, i32, p, u64, p]
     lib.mvllm_linear_residual_rmsnorm.restype = ctypes.c_int
     lib.mvllm_linear_residual_rmsnorm.argtypes = [p, p, p, p, p, p, i64, i64, i64, f32, i32, p, u64, p]
-    lib.mvllm_gemm.restype = ctypes.c_int
-    lib.mvllm_gemm.argtypes = [p, p, p, i64, i64, i64, i32, p]
     lib.mvllm_blas_linear.restype = ctypes.c_int
-    lib.mvllm_blas_linear.argtypes = [p, p, p, i64, i64, i64, i32, p]
+    lib.mvllm_blas_linear.argtypes = [p, p, p, i64, i64, i64, i32, p, u64, p]
+    lib.mvllm_blas_workspace_bytes.restype = u64
+    lib.mvllm_blas_workspace_bytes.argtypes = []
     lib.mvllm_blas_plans_cached.restype = ctypes.c_int
     lib.mvllm_blas_plans_cached.argtypes = []
-    lib.mvllm_paged_attention_o_proj.restype = ctypes.c_int
-    lib.mvllm_paged_attention_o_proj.argtypes = (
-        [p] * 11 + [i32] * 5 + [i64, i32, i32, f32, i32, i32, p, i64, p, p, f32, p, u64, p])
-    lib.mvllm_paged_attention_o_proj_workspace_bytes.restype = u64
-    lib.mvllm_paged_attention_o_proj_workspace_bytes.argtypes = [i32] * 8 + [i64]
+    lib.mvllm_blas_tune.restype = ctypes.c_int
+    lib.mvllm_blas_tune.argtypes = [p, p, p, i64, i64, i64, i32, p, u64, p, ctypes.POINTER(i32)]
+    lib.mvllm_blas_tuning.restype = ctypes.c_int
+    lib.mvllm_blas_tuning.argtypes = [i64, i64, i64, i32, ctypes.POINTER(_BlasChoice)]
+
 
 
 EXPORTED_SYMBOLS = (
@@ -333,11 +344,11 @@ EXPORTED_SYMBOLS = (
     "mvllm_linear_split",
     "mvllm_linear_residual",
     "mvllm_linear_swiglu",
-    "mvllm_gemm",
     "mvllm_blas_linear",
+    "mvllm_blas_workspace_bytes",
     "mvllm_blas_plans_cached",
-    "mvllm_paged_attention_o_proj",
-    "mvllm_paged_attention_o_proj_workspace_bytes",
+    "mvllm_blas_tuning",
+    "mvllm_blas_tune",
 )
 
 
@@ -772,19 +783,6 @@ class HipExtension:
             *self._linear_ws(x, n), _stream(x.device)))
         return h, normed
 
-    def gemm_supported(self, x: torch.Tensor, w: torch.Tensor) -> bool:
-        """Whether :meth:`gemm` serves ``x @ w.T``: 2-D, contiguous, 16-byte aligned,
-        fp16 / bf16 of one dtype, N and K multiples of 64, each operand under 2 GiB."""
-        if (x.dim() != 2 or w.dim() != 2 or x.dtype != w.dtype
-                or x.dtype not in (torch.float16, torch.bfloat16) or x.shape[1] != w.shape[1]
-                or not x.is_contiguous() or not w.is_contiguous()
-                or (x.data_ptr() | w.data_ptr()) % 16):
-            return False
-        m, k = x.shape
-        n = w.shape[0]
-        return (m >= 1 and n >= 64 and n % 64 == 0 and k >= 64 and k % 64 == 0
-                and 2 * m * k < 2**31 and 2 * n * k < 2**31 and m * n < 2**31)
-
     @staticmethod
     def blas_linear_supported(x: torch.Tensor, w: torch.Tensor) -> bool:
         """Whether :meth:`blas_linear` serves ``x @ w.T``: device tensors, 2-D, contiguous,
@@ -804,9 +802,10 @@ class HipExtension:
                                f"{w.dtype} are not served (2-D contiguous 16-byte aligned device "
                                "fp16 or bf16 of one dtype, matching K)")
         y = torch.empty((x.shape[0], w.shape[0]), dtype=x.dtype, device=x.device)
+        ws = self.workspace(x.device, int(self.lib.mvllm_blas_workspace_bytes()))
         rc = self.lib.mvllm_blas_linear(y.data_ptr(), x.data_ptr(), w.data_ptr(), x.shape[0],
                                         w.shape[0], x.shape[1], DTYPE_CODES[x.dtype],
-                                        _stream(x.device))
+                                        ws.data_ptr(), ws.numel(), _stream(x.device))
         if rc == 2:  # MVLLM_ERR_UNSUPPORTED: no algorithm for this shape
             return None
         self._check(rc)
@@ -816,18 +815,31 @@ class HipExtension:
         """Shapes the hipBLASLt entry currently keeps."""
         return int(self.lib.mvllm_blas_plans_cached())
 
-    def gemm(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-        """``x @ w.T`` for prefill-sized ``x`` [M, K] against a row-major weight [N, K]:
-        the MFMA GEMM (fp32 accumulation, one rounding to x's dtype)."""
-        if not self.gemm_supported(x, w):
-            raise RuntimeError(f"gemm: x {tuple(x.shape)} {x.dtype} and w {tuple(w.shape)} "
-                               f"{w.dtype} are not served (2-D contiguous 16-byte aligned fp16 or "
-                               "bf16 of one dtype, N and K multiples of 64)")
+    def blas_tune(self, x: torch.Tensor, w: torch.Tensor) -> int:
+        """Time every hipBLASLt algorithm for ``x @ w.T`` at x's row count and keep the
+        fastest as extra candidates for every later choice of w's shape
+        (``mvllm_blas_tune``; ~0.5 s, waits on the host, not under graph capture).
+        Returns the algorithms timed."""
+        if not self.blas_linear_supported(x, w):
+            raise RuntimeError(f"blas_tune: x {tuple(x.shape)} {x.dtype} and w {tuple(w.shape)} "
+                               f"{w.dtype} are not served")
         y = torch.empty((x.shape[0], w.shape[0]), dtype=x.dtype, device=x.device)
-        self._check(self.lib.mvllm_gemm(y.data_ptr(), x.data_ptr(), w.data_ptr(), x.shape[0],
-                                        w.shape[0], x.shape[1], DTYPE_CODES[x.dtype],
-                                        _stream(x.device)))
-        return y
+        ws = self.workspace(x.device, int(self.lib.mvllm_blas_workspace_bytes()))
+        timed = ctypes.c_int32(0)
+        self._check(self.lib.mvllm_blas_tune(y.data_ptr(), x.data_ptr(), w.data_ptr(), x.shape[0],
+                                             w.shape[0], x.shape[1], DTYPE_CODES[x.dtype],
+                                             ws.data_ptr(), ws.numel(), _stream(x.device),
+                                             ctypes.byref(timed)))
+        return int(timed.value)
+
+    def blas_choice(self, m: int, n: int, k: int, dtype: torch.dtype) -> dict[str, Any]:
+        """How the hipBLASLt entry chose the algorithm it keeps for (m, n, k, dtype) on the
+        current device: the heuristic's candidates, how many were timed, the kept one's
+        index in the heuristic's order, and the first's and the kept one's us per product
+        (-1 untimed)."""
+        out = _BlasChoice()
+        self._check(self.lib.mvllm_blas_tuning(m, n, k, DTYPE_CODES[dtype], ctypes.byref(out)))
+        return {f: getattr(out, f) for f, _ in _BlasChoice._fields_}
 
     def qk_norm_rope_supported(self, dtype: torch.dtype, head_dim: int) -> bool:
         """Whether the fused kernel serves this dtype / head dim (16-byte chunks per head
@@ -1321,74 +1333,6 @@ class HipExtension:
             )
         )
         return out
-
-    def paged_attention_o_proj_supported(self, q: torch.Tensor, w_o_packed: torch.Tensor,
-                                         residual: torch.Tensor) -> bool:
-        """Whether :meth:`paged_attention_o_proj` serves this decode step: one row per
-        sequence (q T x H_q x 128, 16-bit), at most 64 rows, W_o packed for H_q x 128
-        columns, the hidden size a multiple of 256 in [512, 4096]."""
-        if q.dim() != 3 or residual.dim() != 2 or q.dtype not in (torch.float16, torch.bfloat16):
-            return False
-        t, hq, d = q.shape
-        n = residual.shape[1]
-        return (d == 128 and 1 <= t <= 64 and n % 256 == 0 and 512 <= n <= 4096
-                and w_o_packed.dtype == q.dtype and w_o_packed.is_contiguous()
-                and w_o_packed.numel() == -(-n // 32) * 32 * hq * d)
-
-    def paged_attention_o_proj(self, q: torch.Tensor, key_pool: torch.Tensor,
-                               value_pool: torch.Tensor, block_tables: torch.Tensor,
-                               cu_seqlens_q: torch.Tensor, context_lens: torch.Tensor,
-                               seq_lens: torch.Tensor, max_context_len: int, scale: float,
-                               w_o_packed: torch.Tensor, residual: torch.Tensor,
-                               norm_weight: torch.Tensor, eps: float,
-                               k_scale: torch.Tensor | None = None,
-                               v_scale: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
-        """A decode step's attention and o projection with its residual and RMSNorm
-        (``mvllm_paged_attention_o_proj``): (h, normed) with h = residual + attn @ W_o.T
-        and normed = rmsnorm(h, norm_weight, eps), attn being ``paged_attention`` of the
-        same arguments (every sequence one decode row); the attention output is merged
-        straight into the projection, never stored."""
-        cu_seqlens_q, context_lens, seq_lens = self._paged_checks(
-            q, key_pool, value_pool, block_tables, cu_seqlens_q, context_lens, seq_lens, 1,
-            max_context_len, k_scale, v_scale)
-        num_blocks, block_size, num_kv_heads, head_dim = key_pool.shape
-        t, hq, _ = q.shape
-        num_sequences = seq_lens.shape[0]
-        if t != num_sequences:
-            raise RuntimeError("paged_attention_o_proj: every sequence must be one decode row "
-                               f"(got {t} rows for {num_sequences} sequences)")
-        if not self.paged_attention_o_proj_supported(q, w_o_packed, residual):
-            raise RuntimeError(
-                f"paged_attention_o_proj: q {tuple(q.shape)} {q.dtype} with residual "
-                f"{tuple(residual.shape)} and a packed W_o of {w_o_packed.numel()} elements is not "
-                "served (16-bit, head dim 128, <= 64 rows, hidden size a multiple of 256 in "
-                "[512, 4096])")
-        n = residual.shape[1]
-        if (residual.shape != (t, n) or residual.dtype != q.dtype or not residual.is_contiguous()
-                or norm_weight.shape != (n,) or norm_weight.dtype != q.dtype
-                or not norm_weight.is_contiguous()):
-            raise RuntimeError("paged_attention_o_proj: residual must be a contiguous T x N "
-                               "tensor and norm_weight a contiguous N vector, both of q's dtype")
-        q_code = DTYPE_CODES[q.dtype]
-        kv_code = DTYPE_CODES[key_pool.dtype]
-        need = int(self.lib.mvllm_paged_attention_o_proj_workspace_bytes(
-            num_sequences, hq, num_kv_heads, head_dim, block_size, int(max_context_len), q_code,
-            kv_code, n))
-        if need == 0:
-            raise RuntimeError(self.lib.mvllm_last_error().decode(errors="replace")
-                               or "paged_attention_o_proj: not served")
-        workspace = self.workspace(q.device, need)
-        h = torch.empty_like(residual)
-        normed = torch.empty_like(residual)
-        self._check(self.lib.mvllm_paged_attention_o_proj(
-            h.data_ptr(), normed.data_ptr(), q.data_ptr(), key_pool.data_ptr(),
-            value_pool.data_ptr(), _ptr(k_scale), _ptr(v_scale), block_tables.data_ptr(),
-            cu_seqlens_q.data_ptr(), context_lens.data_ptr(), seq_lens.data_ptr(), num_sequences,
-            hq, num_kv_heads, head_dim, block_size, num_blocks, block_tables.shape[1],
-            int(max_context_len), float(scale), q_code, kv_code, w_o_packed.data_ptr(), n,
-            residual.data_ptr(), norm_weight.data_ptr(), float(eps), workspace.data_ptr(),
-            workspace.numel(), _stream(q.device)))
-        return h, normed
 
 
 def load_extension(verbose: bool = False) -> HipExtension:

@@ -60,7 +60,6 @@ __all__ = [
     "linear_swiglu",
     "pack_weight",
     "paged_attention",
-    "paged_attention_o_proj",
     "qk_norm_rope",
     "qk_norm_rope_kv_write",
     "rmsnorm",
@@ -83,27 +82,12 @@ CUDA_KERNELS: dict[str, tuple[bool, str]] = {
     "kv_write": (True, "csrc/kv_write.hip"),
     "qk_norm_rope": (True, "csrc/elementwise.hip"),
     "linear": (True, "csrc/linear.hip (at most 64 rows; vendor BLAS above)"),
-    "gemm": (True, "csrc/gemm.hip (prefill-sized projections)"),
     "blas_linear": (True, "csrc/blas.hip (prefill-sized projections on hipBLASLt, set-up kept "
                           "per shape)"),
-    "paged_attention_o_proj": (True, "csrc/paged_decode.hip (pieces left as partials) + "
-                                     "csrc/linear.hip (merged into the o projection)"),
 }
 
 # Kernels that exist but are deliberately not dispatched, with the reason.
-NOT_YET_FASTER: dict[str, str] = {
-    "gemm": ("csrc/gemm.hip (prefill projections): measured on random bf16 data at M = 2048 "
-             "slower than the vendor BLAS on every Qwen3-0.6B projection (q/k/v 26.4 us vs "
-             "21.4, o 17.5 vs 15.5, gate/up 45.5 vs 28.5, down 23.3 vs 20.8); prefill "
-             "projections stay on the BLAS"),
-    "paged_attention_o_proj": (
-        "csrc/linear.hip merge_o_partial_kernel (decode pieces merged straight into the o "
-        "projection): at the config-5 decode shape (32 sequences, 300-2300 keys, graph "
-        "replays) 47.1 us per layer against 45.0-46.0 for paged_attention + "
-        "linear_residual_rmsnorm; its launch takes 10-12 us, as long as the merge and "
-        "partial-sum launches it replaces together (rocprof: 12.3 us before batching the "
-        "piece loads, merge 5.2 + partial 4.8)"),
-}
+NOT_YET_FASTER: dict[str, str] = {}
 
 MAX_PAGED_HEAD_DIM = 256
 PAGED_HEAD_DIMS = (32, 64, 128, 256)
@@ -348,18 +332,6 @@ def _skinny_ext(x: torch.Tensor, w: PackedWeight, n: int, use_cuda: bool):
     return ext if ext.linear_supported(x, w.packed, n) else None
 
 
-def _gemm(x: torch.Tensor, dense: torch.Tensor, use_cuda: bool) -> torch.Tensor | None:
-    """``x @ dense.T`` on the prefill GEMM (``csrc/gemm.hip``) when it is dispatched
-    (not held back in NOT_YET_FASTER) and serves the shape (device fp16/bf16, N and K
-    multiples of 64, contiguous), else None: the caller takes the vendor BLAS, a size
-    dispatch between two device paths (a CPU tensor with ``use_cuda=True`` is recorded
-    by the skinny op's gate instead)."""
-    if "gemm" in NOT_YET_FASTER or not (use_cuda and x.is_cuda and x.dim() == 2):
-        return None
-    ext = load_extension()
-    return ext.gemm(x, dense) if ext.gemm_supported(x, dense) else None
-
-
 def _blas(x: torch.Tensor, dense: torch.Tensor, use_cuda: bool) -> torch.Tensor | None:
     """``x @ dense.T`` through the library's hipBLASLt entry (``csrc/blas.hip``: the
     vendor product with its descriptors and algorithm kept per shape, where torch makes
@@ -373,11 +345,9 @@ def _blas(x: torch.Tensor, dense: torch.Tensor, use_cuda: bool) -> torch.Tensor 
 
 
 def _prefill_product(x: torch.Tensor, dense: torch.Tensor, use_cuda: bool) -> torch.Tensor:
-    """``x @ dense.T`` for a prefill-sized ``x``: the MFMA GEMM when dispatched, else the
-    vendor BLAS (the library's entry, else torch's)."""
-    y = _gemm(x, dense, use_cuda)
-    if y is None:
-        y = _blas(x, dense, use_cuda)
+    """``x @ dense.T`` for a prefill-sized ``x``: the vendor BLAS (the library's entry,
+    else torch's)."""
+    y = _blas(x, dense, use_cuda)
     return y if y is not None else x @ dense.t()
 
 
@@ -386,10 +356,9 @@ def linear(x: torch.Tensor, w: torch.Tensor | PackedWeight, use_cuda: bool = Fal
 
     Kernels: ``csrc/linear.hip`` for decode-sized ``x`` (at most 64 rows of f16/bf16, K a
     multiple of 64) against a :class:`PackedWeight`: a weight-bandwidth-bound skinny
-    GEMM; ``csrc/gemm.hip`` for larger ``x`` (prefill chunks: an MFMA GEMM over the
-    row-major weight, N and K multiples of 64; held back while slower). Other shapes
-    take the vendor BLAS, as every projection does in the reference: for device
-    fp16/bf16 through ``csrc/blas.hip`` (hipBLASLt with the per-shape set-up kept),
+    GEMM. Larger ``x`` (prefill chunks) and other shapes take the vendor BLAS, as every
+    projection does in the reference: for device fp16/bf16 through ``csrc/blas.hip``
+    (hipBLASLt with the per-shape set-up kept and the fastest candidate algorithm),
     else through torch - a dispatch by size, all paths on the device.
     """
     dense = w.dense if isinstance(w, PackedWeight) else w
@@ -449,35 +418,6 @@ def linear_residual_rmsnorm(x: torch.Tensor, w: PackedWeight, residual: torch.Te
             or norm_weight.dtype != x.dtype or not norm_weight.is_contiguous()):
         return None
     return ext.linear_residual_rmsnorm(x, w.packed, residual, norm_weight, eps)
-
-
-def paged_attention_o_proj(q: torch.Tensor, key_pool: torch.Tensor, value_pool: torch.Tensor,
-                           block_tables: torch.Tensor, cu_seqlens_q: torch.Tensor,
-                           context_lens: torch.Tensor, seq_lens: torch.Tensor,
-                           max_context_len: int, scale: float, w_o: PackedWeight,
-                           residual: torch.Tensor, norm_weight: torch.Tensor, eps: float = 1e-6,
-                           use_cuda: bool = False, *, k_scale: torch.Tensor | None = None,
-                           v_scale: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor] | None:
-    """(h, rmsnorm(h)) for h = residual + paged_attention(...) @ w_o.T over a decode-only
-    batch (every sequence one query row): the decode's pieces merged straight into the
-    o projection (``csrc/paged_decode.hip`` + ``csrc/linear.hip``), three launches where
-    ``paged_attention`` and ``linear_residual_rmsnorm`` take four. Within the
-    projection's rounding of those two ops (K summed per head). None where it does not
-    serve the call (not a decode-only batch, more than 64 rows, head dim other than 128,
-    ...): the caller runs the two ops. Not dispatched on the PyTorch path either."""
-    if (not _use_kernel("paged_attention_o_proj", use_cuda, q) or not isinstance(w_o, PackedWeight)
-            or w_o.packed is None or q.dim() != 3 or q.shape[0] != seq_lens.shape[0]):
-        return None
-    ext = load_extension()
-    if (not ext.paged_attention_o_proj_supported(q, w_o.packed, residual)
-            or _kernel_can_page(q, key_pool, value_pool, block_tables,
-                                (cu_seqlens_q, context_lens, seq_lens)) is not None
-            or not residual.is_contiguous() or residual.dtype != q.dtype
-            or norm_weight.dtype != q.dtype or not norm_weight.is_contiguous()):
-        return None
-    return ext.paged_attention_o_proj(q, key_pool, value_pool, block_tables, cu_seqlens_q,
-                                      context_lens, seq_lens, int(max_context_len), scale,
-                                      w_o.packed, residual, norm_weight, eps, k_scale, v_scale)
 
 
 def linear_swiglu(x: torch.Tensor, w_gate_up: PackedWeight, use_cuda: bool = False) -> torch.Tensor:

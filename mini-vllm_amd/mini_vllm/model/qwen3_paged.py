@@ -140,27 +140,47 @@ class Qwen3Paged:
         self.lm_head = (ops.pack_weight(weights["embedding"], use_cuda=True) if use_cuda
                         else weights["embedding"])
 
+    @torch.no_grad()
+    def prepare_prefill_products(self, max_tokens: int, sweep: bool = True) -> int:
+        """Choose the library's hipBLASLt algorithms for the prefill-sized projections
+        now rather than during serving: with ``sweep``, every algorithm is timed once per
+        projection shape at ``max_tokens`` rows (its fastest join every later choice);
+        then each shape runs once for every row count class up to ``max_tokens``, so an
+        algorithm is chosen (and timed) for each 128-row bucket and each whole multiple
+        of 128. The layers share their shapes, so layer 0's weights stand for all.
+        Returns the products run (0 on the PyTorch path, which keeps nothing)."""
+        if not self.use_cuda or not self.packed:
+            return 0
+        w, p = self.layers[0], self.packed[0]
+        weights = [p["qkv"], p["o"], p.get("gate_up", w["gate"]), p["down"]]
+        device, dtype = self.weights["embedding"].device, self.config.dtype
+        runs = 0
+        if sweep and max_tokens > 64 and dtype in (torch.float16, torch.bfloat16):
+            from mini_vllm.kernels.extension import load_extension
+
+            ext = load_extension()
+            for pw in weights:
+                dense = pw.dense if isinstance(pw, ops.PackedWeight) else pw
+                # random rows: constant operands time some kernels faster than real data
+                x = torch.randn(max_tokens, dense.shape[1], device=device).to(dtype)
+                if ext.blas_linear_supported(x, dense):
+                    ext.blas_tune(x, dense)
+                    runs += 1
+        for j in range(max_tokens // 128 + 1):
+            for m in (128 * j + 65, 128 * (j + 1)):
+                if m > max_tokens or m <= 64:
+                    continue
+                for pw in weights:
+                    k = pw.shape[1]
+                    ops.linear(torch.randn(m, k, device=device).to(dtype), pw, use_cuda=True)
+                    runs += 1
+        return runs
+
     def _attention_block(self, layer: int, w: dict, p: dict, x: torch.Tensor, h: torch.Tensor,
                          batch, fused: bool) -> tuple[torch.Tensor, torch.Tensor]:
-        """(h + wo(attention(x)), mlp_norm of that) for normed input x: on a decode-only
-        step with the kernels on, the decode's pieces merged straight into the o
-        projection (``ops.paged_attention_o_proj``); otherwise the attention output,
-        then the projection with its residual and norm."""
-        c = self.config
-        if fused and batch.max_query_len == 1:
-            q = self._queries(layer, w, p, x, batch, fused)
-            kv = self.manager.kv
-            k_scale, v_scale = kv.layer_scales(layer)
-            both = ops.paged_attention_o_proj(
-                q, kv.layer_keys(layer), kv.layer_values(layer), batch.block_tables,
-                batch.cu_seqlens_q, batch.context_lens, batch.seq_lens, batch.max_context_len,
-                1.0 / math.sqrt(c.head_dim), p.get("o"), h, w["mlp_norm"], c.rms_norm_eps,
-                use_cuda=self.use_cuda, k_scale=k_scale, v_scale=v_scale)
-            if both is not None:
-                return both
-            out = self._paged(layer, q, batch)
-        else:
-            out = self._attention(layer, w, p, x, batch, fused)
+        """(h + wo(attention(x)), mlp_norm of that) for normed input x: the attention
+        output, then the projection with its residual and norm."""
+        out = self._attention(layer, w, p, x, batch, fused)
         return self._residual_norm(out, p.get("o"), w["wo"], h, w["mlp_norm"], fused)
 
     def _attention(self, layer: int, w: dict, p: dict, x: torch.Tensor, batch,

@@ -46,21 +46,66 @@ def test_matches_float64_and_torch(extension, device, dtype, m):
         assert ((y.double() - theirs.double()).abs() <= 2 * bound).all(), (m, n, k)
 
 
-@pytest.mark.parametrize("n,k", [(4096, 1024), (1024, 3072)])
-def test_every_row_count_of_the_buckets(extension, device, n, k):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n,k", SHAPES)
+def test_every_row_count_of_the_buckets(extension, device, n, k, dtype):
     """m values share one algorithm per 128-row bucket (chosen at the bucket's largest,
-    odd, m): every m - bucket edges, odd and even, from 65 to 2048 - stays within the
-    bound, the algorithm not assuming anything of m."""
+    odd, m, timed at the bucket's first call): every m - bucket edges, odd and even,
+    from 65 to 2048 - stays within the bound, the algorithm not assuming anything of m;
+    for every shape of the model and both 16-bit dtypes."""
     gen = torch.Generator().manual_seed(n + k)
-    x = torch.randn(2048, k, generator=gen).to(torch.bfloat16).to(device)
-    w = (torch.randn(n, k, generator=gen) * 0.02).to(torch.bfloat16).to(device)
+    x = torch.randn(2048, k, generator=gen).to(dtype).to(device)
+    w = (torch.randn(n, k, generator=gen) * 0.02).to(dtype).to(device)
     ms = sorted(set(list(range(65, 2049, 61)) + [127, 128, 129, 255, 256, 257, 1023, 1024,
                                                  1025, 1535, 1536, 2047, 2048]))
     for m in ms:
         y = extension.blas_linear(x[:m], w)
-        ref, bound = _bound(x[:m], w, torch.bfloat16)
+        ref, bound = _bound(x[:m], w, dtype)
         err = (y.double() - ref).abs()
         assert (err <= bound).all(), f"m={m}: off by {(err / bound).max().item():.2f} bounds"
+
+
+def test_the_kept_algorithm_is_the_fastest_candidate(extension, device):
+    """A bucket's first call times the heuristic's candidates and keeps the fastest
+    (never slower than the heuristic's first, which is one of them); every m of the
+    bucket then reuses it, and its products stay within the bound."""
+    gen = torch.Generator().manual_seed(11)
+    x = torch.randn(1500, 1024, generator=gen).to(torch.bfloat16).to(device)
+    w = (torch.randn(6144, 1024, generator=gen) * 0.02).to(torch.bfloat16).to(device)
+    extension.blas_linear(x[:1407], w)  # bucket 10 (m 1280-1407)
+    first = extension.blas_choice(1407, 6144, 1024, torch.bfloat16)
+    assert first["candidates"] >= 1 and first["timed"] >= 1
+    assert 0 <= first["chosen"] < first["candidates"]
+    assert first["chosen_us"] <= first["first_us"]
+    for m in (1281, 1300, 1406):
+        y = extension.blas_linear(x[:m], w)
+        assert extension.blas_choice(m, 6144, 1024, torch.bfloat16) == first
+        ref, bound = _bound(x[:m], w, torch.bfloat16)
+        assert ((y.double() - ref).abs() <= bound).all(), m
+
+
+def test_a_first_call_under_graph_capture(extension, device):
+    """A shape first called while its stream is being captured cannot be timed (no host
+    wait inside a capture): it keeps the heuristic's first, untimed, and the replayed
+    graph gives the eager product's bits, replay after replay."""
+    gen = torch.Generator().manual_seed(12)
+    m, n, k = 1024 + 77, 768, 1536  # an (n, k) no other test calls: its bucket is new
+    x = torch.randn(m, k, generator=gen).to(torch.bfloat16).to(device)
+    w = (torch.randn(n, k, generator=gen) * 0.02).to(torch.bfloat16).to(device)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        y = extension.blas_linear(x, w)
+    choice = extension.blas_choice(m, n, k, torch.bfloat16)
+    assert choice["timed"] == 0 and choice["chosen"] == 0 and choice["first_us"] == -1
+    eager = extension.blas_linear(x, w)
+    for _ in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager)
 
 
 def test_kept_shapes_and_a_second_stream(extension, device):
@@ -106,3 +151,39 @@ def test_ops_route_prefill_products_through_it(extension, device):
         extension.blas_linear(xf, wf)
     with pytest.raises(RuntimeError, match="not served"):
         extension.blas_linear(x[:, :512], w[:, :512])  # strided, not contiguous
+
+
+def test_a_sweep_adds_faster_candidates(extension, device):
+    """``blas_tune`` times every algorithm at one row count and leaves y = x w^T; the
+    choices made after it include its fastest (a kept index past the heuristic's 16 is
+    one of them) and are never slower than the heuristic's first; products stay within
+    the bound at the swept m and at other buckets (whose m the kept algorithms are
+    checked against before they are timed)."""
+    gen = torch.Generator().manual_seed(13)
+    n, k = 1536, 512  # a shape no other test calls
+    x = torch.randn(1024, k, generator=gen).to(torch.bfloat16).to(device)
+    w = (torch.randn(n, k, generator=gen) * 0.02).to(torch.bfloat16).to(device)
+    before = extension.blas_linear(x[:700], w)
+    timed = extension.blas_tune(x, w)
+    assert timed > 16
+    for m in (700, 1024, 333):
+        y = extension.blas_linear(x[:m], w)
+        ref, bound = _bound(x[:m], w, torch.bfloat16)
+        assert ((y.double() - ref).abs() <= bound).all(), m
+        choice = extension.blas_choice(m, n, k, torch.bfloat16)
+        assert choice["timed"] >= 1 and choice["chosen_us"] <= choice["first_us"]
+        if m == 1024:  # the swept shape itself: all 12 kept algorithms serve it
+            assert choice["candidates"] >= 13, choice
+    assert ((extension.blas_linear(x[:700], w).double() - before.double()).abs()
+            <= 2 * _bound(x[:700], w, torch.bfloat16)[1]).all()
+
+
+def test_a_sweep_is_refused_under_capture(extension, device):
+    x = torch.randn(256, 512, device=device).to(torch.bfloat16)
+    w = torch.randn(512, 512, device=device).to(torch.bfloat16)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="capturing"):
+        with torch.cuda.graph(graph, stream=side):
+            extension.blas_tune(x, w)

@@ -64,6 +64,16 @@ def test_paged_attention_refusals(lib, over, code, message):
     assert message in lib.mvllm_last_error().decode()
 
 
+def test_blas_linear_takes_the_callers_workspace(lib):
+    """The hipBLASLt entry allocates nothing: a missing, short or misaligned workspace is
+    refused before any HIP call."""
+    need = lib.mvllm_blas_workspace_bytes()
+    assert need >= 1 << 20
+    for ws, nbytes in ((None, need), (4096, need - 1), (4096 + 16, need)):
+        assert lib.mvllm_blas_linear(256, 512, 768, 64, 128, 128, 2, ws, nbytes, None) == 1
+        assert "workspace" in lib.mvllm_last_error().decode()
+
+
 def test_split_workspace_is_required_when_planned(lib):
     """Decode needs its partials workspace; a missing one is refused, not faulted."""
     assert _paged(lib, num_tokens=1, num_seqs=1, max_ctx=8192) == 4
@@ -128,20 +138,14 @@ def test_plan_options_are_explicit_and_checked(lib, monkeypatch):
         extension.make_plan_options({"decode_sched": 1})
 
 
-def test_heads_decode_schedule_plan(lib):
-    """Forced per-(sequence, head unit) decode: one workgroup per sequence and unit, no
-    workspace; 4 or 8 waves per workgroup, anything else refused; by-row is not a
-    schedule one can force."""
-    plan = _plan(lib, 32, 32, 16, 8, 128, 16, 1, 4096, 2, 2, options={"decode_schedule": "heads"})
-    assert plan.decode_mode == 4 and plan.workspace_bytes == 0
-    assert plan.decode_workgroups == 32 * 8  # GQA pairs: one unit per kv head
-    four = _plan(lib, 32, 32, 16, 8, 128, 16, 1, 4096, 2, 2,
-                 options={"decode_schedule": "heads", "decode_waves_per_cu": 4})
-    assert four.decode_mode == 4
-    for bad in ({"decode_schedule": "heads", "decode_waves_per_cu": 6}, {"decode_schedule": 3}):
+def test_only_the_stream_and_grid_decode_schedules_can_be_forced(lib):
+    """By-row is the planner's own choice for prefill rows without an MFMA kernel, not a
+    schedule one can force; codes past the grid are refused."""
+    for bad in ({"decode_schedule": 3}, {"decode_schedule": 4}):
         opts = extension.make_plan_options(bad)
         assert lib.mvllm_paged_attention_plan(32, 32, 16, 8, 128, 16, 1, 4096, 2, 2,
                                               ctypes.byref(opts), ctypes.byref(extension._Plan())) == 1
+        assert "plan options" in lib.mvllm_last_error().decode()
 
 
 def test_the_library_carries_the_id_of_its_sources(lib):

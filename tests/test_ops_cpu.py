@@ -113,9 +113,8 @@ def test_dispatch_report_names_every_op():
     assert "use_cuda is off" in off
     assert set(ops.cuda_kernel_names()) == {"rmsnorm", "rope", "swiglu", "paged_attention", "kv_write",
                                             "qk_norm_rope", "linear", "decode_attention",
-                                            "flash_prefill", "argmax", "gemm",
-                                            "paged_attention_o_proj", "blas_linear"}
-    assert "gemm" in ops.NOT_YET_FASTER and "gemm.hip (prefill-sized projections) is slower" in on
+                                            "flash_prefill", "argmax", "blas_linear"}
+    assert not ops.NOT_YET_FASTER  # every kernel in the library is dispatched
 
 
 def test_dense_attention_torch_path_decode_and_causal():

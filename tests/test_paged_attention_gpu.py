@@ -69,36 +69,32 @@ def test_decode_over_a_long_context_uses_the_split_path(extension, device):
     check(extension, b)
 
 
-DECODE_SCHEDULES = {"stream": None, "grid": {"decode_schedule": "grid"},
-                    "heads": {"decode_schedule": "heads"},
-                    "heads4": {"decode_schedule": "heads", "decode_waves_per_cu": 4}}
+DECODE_SCHEDULES = {"stream": None, "grid": {"decode_schedule": "grid"}}
 
 
 @pytest.mark.parametrize("schedule", sorted(DECODE_SCHEDULES))
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_every_decode_schedule_agrees_with_the_oracle(extension, device, schedule, dtype):
-    """The stream schedule (default), the split grid and the per-(sequence, head)
-    workgroups (forced) on a ragged batch, including sequences shorter than one
-    workgroup's share (or than its waves) and longer than many."""
+    """The stream schedule (default) and the split grid (forced) on a ragged batch,
+    including sequences shorter than one workgroup's share (or than its waves) and
+    longer than many."""
     options = DECODE_SCHEDULES[schedule]
     b = case([8192, 33, 4096, 17, 1, 700, 2], [1] * 7, device, dtype=dtype)
     plan = extension.paged_attention_plan(7, 7, HQ, HK, D, 16, 1, 8192, dtype, dtype,
                                           plan_options=options)
-    assert plan["decode_mode"] == schedule.rstrip("4")
-    if schedule.startswith("heads"):
-        assert plan["workspace_bytes"] == 0
+    assert plan["decode_mode"] == schedule
     check(extension, b, options=options)
 
 
+@pytest.mark.parametrize("schedule", sorted(DECODE_SCHEDULES))
 @pytest.mark.parametrize("kv_dtype", [None, torch.float8_e4m3fn])
-def test_heads_decode_schedule_in_a_mixed_batch(extension, device, kv_dtype):
-    """Prefill chunks beside decode rows: the heads schedule leaves the chunks to the
+def test_decode_schedules_in_a_mixed_batch(extension, device, kv_dtype, schedule):
+    """Prefill chunks beside decode rows: each decode schedule leaves the chunks to the
     prefill kernel; GQA groups of 2 and 4, fp8 pools with their scales."""
     for heads, kv_heads in ((16, 8), (16, 4)):
         b = case([900, 2500, 40, 700, 5], [1, 400, 1, 1, 5], device, dtype=torch.bfloat16,
                  kv_dtype=kv_dtype, num_q_heads=heads, num_kv_heads=kv_heads, head_dim=128)
-        check(extension, b, dtype=kv_dtype or torch.bfloat16,
-              options={"decode_schedule": "heads"})
+        check(extension, b, dtype=kv_dtype or torch.bfloat16, options=DECODE_SCHEDULES[schedule])
 
 
 @pytest.mark.parametrize("wgs_per_cu", ["1", "4"])
@@ -117,22 +113,19 @@ def test_a_ragged_decode_batch_with_empty_splits(extension, device):
 
 @pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float8_e4m3fn])
 @pytest.mark.parametrize("wgs_per_cu", ["1", "3"])
-def test_stream_decode_merge_in_launch_and_by_kernel(extension, device, kv_dtype, wgs_per_cu):
+def test_stream_decode_merge_of_cut_sequences(extension, device, kv_dtype, wgs_per_cu):
     """Sequences cut between stream workgroups are merged by the merge kernel after the
-    decode launch (the default) or, forced, by their last piece inside it: both match
-    the oracle and give the same bits, on calls in a row (the arrival counters are left
-    at zero for the next), with sequences of one piece, of two and of dozens, and
-    prefill rows beside them."""
+    decode launch: sequences of one piece, of two and of dozens, with prefill rows beside
+    them, on calls in a row that give the same bits."""
     b = case([12000, 700, 33, 4096, 1, 2500, 300], [1, 1, 1, 1, 1, 1, 64], device,
              dtype=torch.bfloat16, kv_dtype=kv_dtype, num_q_heads=16, num_kv_heads=8,
              head_dim=128)
     want = oracle(b)
     runs = []
-    for merge in (1, 0, 1, 1):
-        got = kernel(extension, b, {"decode_merge": merge, "decode_wgs_per_cu": wgs_per_cu})
-        assert_max_abs(got, want, ATTN_ATOL[kv_dtype], f"decode_merge {merge}")
+    for _ in range(3):
+        got = kernel(extension, b, {"decode_wgs_per_cu": wgs_per_cu})
+        assert_max_abs(got, want, ATTN_ATOL[kv_dtype], "stream decode + merge")
         runs.append(got)
-    # Whichever piece merges folds every piece in piece order, as the merge kernel does.
     for got in runs[1:]:
         assert torch.equal(got, runs[0])
 
