@@ -98,6 +98,15 @@ typedef struct mvllm_plan_options {
                                   at least 50) */
 } mvllm_plan_options;
 
+/* The split prefill grid's arrival counters: regions taken on the current device (one
+ * per stream that ran a split launch, at most 32), and the split launches (all devices)
+ * that ran every item whole instead because no region was left or because their
+ * stream was being captured into a graph (a captured launch must not name a stream's
+ * counters: a replay on another stream could overlap it). No counterpart in the
+ * reference. Any pointer may be NULL. */
+void mvllm_split_stats(int32_t* regions_used, int64_t* whole_no_region,
+                       int64_t* whole_capturing);
+
 /* Plan a paged_attention call. Depends only on the host-side sizes below and the
  * options (never on device data), so it is free to call every iteration. Replaces the
  * grid/split selection of the reference's launch_paged_attention / splits_for

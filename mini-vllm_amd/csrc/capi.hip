@@ -316,8 +316,12 @@ void plan_decode(Plan& plan, int32_t num_tokens, int32_t num_seqs, int32_t hq, i
 // launch leaves its counters at zero). A stream takes one region of it on its first
 // split launch and keeps it, so launches that may overlap in time (other streams)
 // never share counters, while one stream's launches run in order. A stream beyond the
-// regions runs its prefill with every item whole. Host code never names the array
-// itself: each device's address comes from hipGetSymbolAddress, kept here.
+// regions runs its prefill with every item whole, and so does a launch made while its
+// stream is being captured into a graph: the graph would carry the capture stream's
+// region in its kernel arguments, and a replay on another stream could then overlap a
+// launch still running on the capture stream over the same counters. Both cases are
+// counted (mvllm_split_stats). Host code never names the array itself: each device's
+// address comes from hipGetSymbolAddress, kept here.
 constexpr int kCounterRegions = 32;
 constexpr int kCounterInts = mvllm::kSplitMaxItems * mvllm::kSplitMaxCols;
 static __device__ __align__(256) int split_counters[kCounterRegions * kCounterInts];
@@ -327,6 +331,8 @@ std::mutex g_counter_mutex;
 int* g_counter_base[kCounterDevices] = {};
 hipStream_t g_counter_owner[kCounterDevices][kCounterRegions] = {};
 bool g_counter_used[kCounterDevices][kCounterRegions] = {};
+std::atomic<int64_t> g_split_whole_no_region{0};   // split launches run whole: no region left
+std::atomic<int64_t> g_split_whole_capturing{0};   // split launches run whole: stream capturing
 
 // The counter region of (current device, stream), or nullptr when there is none to give.
 int* split_counters_for(hipStream_t stream) {
@@ -347,7 +353,10 @@ int* split_counters_for(hipStream_t stream) {
     }
     if (!g_counter_used[dev][r] && free_region < 0) free_region = r;
   }
-  if (free_region < 0) return nullptr;
+  if (free_region < 0) {
+    g_split_whole_no_region.fetch_add(1, std::memory_order_relaxed);
+    return nullptr;
+  }
   g_counter_used[dev][free_region] = true;
   g_counter_owner[dev][free_region] = stream;
   return g_counter_base[dev] + free_region * kCounterInts;
@@ -376,7 +385,14 @@ int launch_planned(const Plan& plan, mvllm::PagedParams& p, void* workspace, int
       p.pf_ml = reinterpret_cast<float*>(ws + plan.off_pf_ml);
     }
     if (plan.pub.prefill_pieces > 1) {
-      p.pf_count = split_counters_for(s);
+      hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(s, &capture) != hipSuccess ||
+          capture != hipStreamCaptureStatusNone) {
+        g_split_whole_capturing.fetch_add(1, std::memory_order_relaxed);
+        p.pf_count = nullptr;  // items whole: a graph must not name a stream's counters
+      } else {
+        p.pf_count = split_counters_for(s);
+      }
       if (p.pf_count != nullptr) {
         p.pf_pieces = plan.pub.prefill_pieces;
         p.pf_ranks = plan.split_ranks;
@@ -561,6 +577,19 @@ int mvllm_abi_version(void) { return 13; }
 #define MVLLM_SOURCE_HASH "unstamped"
 #endif
 const char* mvllm_build_id(void) { return MVLLM_SOURCE_HASH; }
+
+void mvllm_split_stats(int32_t* regions_used, int64_t* whole_no_region,
+                       int64_t* whole_capturing) {
+  int dev = 0;
+  int used = 0;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kCounterDevices) {
+    std::lock_guard<std::mutex> lock(g_counter_mutex);
+    for (int r = 0; r < kCounterRegions; ++r) used += g_counter_used[dev][r] ? 1 : 0;
+  }
+  if (regions_used != nullptr) *regions_used = used;
+  if (whole_no_region != nullptr) *whole_no_region = g_split_whole_no_region.load();
+  if (whole_capturing != nullptr) *whole_capturing = g_split_whole_capturing.load();
+}
 
 int mvllm_paged_attention_plan(int32_t num_tokens, int32_t num_seqs, int32_t num_q_heads,
                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size,

@@ -310,6 +310,8 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_blas_workspace_bytes.argtypes = []
     lib.mvllm_blas_plans_cached.restype = ctypes.c_int
     lib.mvllm_blas_plans_cached.argtypes = []
+    lib.mvllm_split_stats.restype = None
+    lib.mvllm_split_stats.argtypes = [ctypes.POINTER(i32), ctypes.POINTER(i64), ctypes.POINTER(i64)]
     lib.mvllm_blas_tune.restype = ctypes.c_int
     lib.mvllm_blas_tune.argtypes = [p, p, p, i64, i64, i64, i32, p, u64, p, ctypes.POINTER(i32)]
     lib.mvllm_blas_tuning.restype = ctypes.c_int
@@ -349,6 +351,7 @@ EXPORTED_SYMBOLS = (
     "mvllm_blas_plans_cached",
     "mvllm_blas_tuning",
     "mvllm_blas_tune",
+    "mvllm_split_stats",
 )
 
 
@@ -814,6 +817,15 @@ class HipExtension:
     def blas_plans_cached(self) -> int:
         """Shapes the hipBLASLt entry currently keeps."""
         return int(self.lib.mvllm_blas_plans_cached())
+
+    def split_stats(self) -> dict[str, int]:
+        """The split prefill grid's counter regions in use on the current device, and the
+        split launches that ran every item whole (no region left; stream capturing)."""
+        used, no_region, capturing = ctypes.c_int32(0), ctypes.c_int64(0), ctypes.c_int64(0)
+        self.lib.mvllm_split_stats(ctypes.byref(used), ctypes.byref(no_region),
+                                   ctypes.byref(capturing))
+        return {"regions_used": used.value, "whole_no_region": no_region.value,
+                "whole_capturing": capturing.value}
 
     def blas_tune(self, x: torch.Tensor, w: torch.Tensor) -> int:
         """Time every hipBLASLt algorithm for ``x @ w.T`` at x's row count and keep the

@@ -6,15 +6,23 @@ reference's recompute model, model/qwen3.py, restated): no pages, no chunks, no
 kernels, so a paged engine that agrees with it token for token got its batching,
 slots, positions and masks right. Returns the tokens and each step's logits so a test
 can tell a genuine near-tie from a bug.
+
+``DenseQwen3(..., kv_fp8=True)`` is the same model with its K/V cache held the way an
+fp8-e4m3 paged pool holds it (the reference has no fp8 cache): every K/V row written
+through ``oracle.kv_write.kv_write_fp8`` (per-(page, kv head) power-of-two scales,
+rows re-encoded when a scale grows) onto 16-row pages at slot = position, the prompt
+in one write and each generated token in its own, and attention reading the
+dequantised values. Everything else stays float64.
 """
 
 from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 
-__all__ = ["DenseQwen3", "generate_greedy", "generate_greedy_cached"]
+__all__ = ["DenseQwen3", "Fp8Pages", "generate_greedy", "generate_greedy_cached"]
 
 
 def _rms(x, w, eps):
@@ -78,10 +86,57 @@ def _layer_weights(config, weights, dtype):
              if k.startswith(f"layers.{layer}.")} for layer in range(config.num_hidden_layers)]
 
 
-def _forward_cached(config, layers, emb, final_norm, ids, start, cache, dtype):
+class Fp8Pages:
+    """One sequence's K/V as fp8-e4m3 pages, per layer: positions on ``block_size``-row
+    pages with slot = position, written through ``oracle.kv_write.kv_write_fp8`` (the
+    values taken as float32, as the kernels receive them), read back dequantised
+    (code x its page's scale) in float64."""
+
+    def __init__(self, layers: int, kv_heads: int, head_dim: int, block_size: int = 16):
+        self.bs, self.hk, self.d = block_size, kv_heads, head_dim
+        shape = (0, block_size, kv_heads, head_dim)
+        self.codes = [[np.zeros(shape, np.uint8), np.zeros(shape, np.uint8)] for _ in range(layers)]
+        self.scales = [[np.zeros((0, kv_heads), np.float32), np.zeros((0, kv_heads), np.float32)]
+                       for _ in range(layers)]
+        self.values = [[torch.zeros(0, kv_heads, head_dim, dtype=torch.float64) for _ in range(2)]
+                       for _ in range(layers)]
+
+    def write(self, layer: int, start: int, k: torch.Tensor, v: torch.Tensor):
+        """Write rows ``start ..`` of K and V (``t x H_k x D``); returns (keys, values)
+        of every position so far, dequantised."""
+        from oracle.elementwise import fp8_e4m3_decode
+        from oracle.kv_write import kv_write_fp8
+
+        t = k.shape[0]
+        end = start + t
+        blocks = -(-end // self.bs)
+        slots = np.arange(start, end, dtype=np.int64)
+        first = start // self.bs
+        out = []
+        for i, x in enumerate((k, v)):
+            codes, scales = self.codes[layer][i], self.scales[layer][i]
+            if codes.shape[0] < blocks:
+                grow = blocks - codes.shape[0]
+                codes = np.concatenate([codes, np.zeros((grow,) + codes.shape[1:], np.uint8)])
+                scales = np.concatenate([scales, np.zeros((grow, self.hk), np.float32)])
+            codes, scales = kv_write_fp8(codes, scales, slots,
+                                         x.detach().to(torch.float32).cpu().numpy())
+            self.codes[layer][i], self.scales[layer][i] = codes, scales
+            # refresh the dequantised rows of the pages this write touched
+            deq = fp8_e4m3_decode(codes[first:blocks]).astype(np.float64) * \
+                scales[first:blocks][:, None, :, None].astype(np.float64)
+            rows = torch.from_numpy(deq.reshape(-1, self.hk, self.d))
+            kept = self.values[layer][i][:first * self.bs]
+            self.values[layer][i] = torch.cat([kept, rows])[:end]
+            out.append(self.values[layer][i])
+        return out[0], out[1]
+
+
+def _forward_cached(config, layers, emb, final_norm, ids, start, cache, dtype, pages=None):
     """Rows ``start .. start + len(ids) - 1`` of the same dense forward, their K/V
-    appended to ``cache`` (one [keys, values] pair per layer), attending causally over
-    every cached position; returns the last row's logits."""
+    appended to ``cache`` (one [keys, values] pair per layer) - or written to ``pages``
+    (an :class:`Fp8Pages`) - attending causally over every cached position; returns
+    the last row's logits."""
     c = config
     t = len(ids)
     h = emb[torch.tensor(ids)]
@@ -96,12 +151,17 @@ def _forward_cached(config, layers, emb, final_norm, ids, start, cache, dtype):
         v = (x @ lw["wv"].t()).view(t, c.num_key_value_heads, c.head_dim)
         q = _rope(_rms(q, lw["q_norm"], c.rms_norm_eps), pos, c.rope_theta, dtype)
         k = _rope(_rms(k, lw["k_norm"], c.rms_norm_eps), pos, c.rope_theta, dtype)
-        if len(cache) <= layer:
-            cache.append([k, v])
+        if pages is not None:
+            keys, vals = pages.write(layer, start, k, v)
+            keys, vals = keys.to(dtype), vals.to(dtype)
         else:
-            cache[layer] = [torch.cat([cache[layer][0], k]), torch.cat([cache[layer][1], v])]
-        keys = cache[layer][0].repeat_interleave(g, dim=1)
-        vals = cache[layer][1].repeat_interleave(g, dim=1)
+            if len(cache) <= layer:
+                cache.append([k, v])
+            else:
+                cache[layer] = [torch.cat([cache[layer][0], k]), torch.cat([cache[layer][1], v])]
+            keys, vals = cache[layer]
+        keys = keys.repeat_interleave(g, dim=1)
+        vals = vals.repeat_interleave(g, dim=1)
         scores = torch.einsum("qhd,khd->hqk", q, keys) / math.sqrt(c.head_dim) + mask
         att = torch.einsum("hqk,khd->qhd", torch.softmax(scores, -1), vals)
         h = h + att.reshape(t, -1) @ lw["wo"].t()
@@ -116,9 +176,9 @@ class DenseQwen3:
     """The dense model with its weights converted to ``dtype`` once, for several
     :meth:`generate` calls (the 0.6B shape's float64 weights take ~5 GB)."""
 
-    def __init__(self, config, weights, dtype=torch.float64):
+    def __init__(self, config, weights, dtype=torch.float64, kv_fp8: bool = False):
         w = {k: v.detach().cpu() for k, v in weights.items()}
-        self.config, self.dtype = config, dtype
+        self.config, self.dtype, self.kv_fp8 = config, dtype, kv_fp8
         self.layers = _layer_weights(config, w, dtype)
         self.emb, self.final_norm = w["embedding"].to(dtype), w["final_norm"].to(dtype)
 
@@ -127,10 +187,13 @@ class DenseQwen3:
         one pass, then one token per step against the cache. The same dense causal math
         as :func:`generate_greedy` (no pages, no chunks, no kernels). Returns (tokens,
         per-step logits)."""
-        args = (self.config, self.layers, self.emb, self.final_norm)
+        c = self.config
+        args = (c, self.layers, self.emb, self.final_norm)
         cache: list = []
+        pages = (Fp8Pages(c.num_hidden_layers, c.num_key_value_heads, c.head_dim)
+                 if self.kv_fp8 else None)
         tokens, logits = [], []
-        out = _forward_cached(*args, list(prompt), 0, cache, self.dtype)
+        out = _forward_cached(*args, list(prompt), 0, cache, self.dtype, pages)
         pos = len(prompt)
         for _ in range(max_tokens):
             tok = int(out.argmax())
@@ -138,9 +201,30 @@ class DenseQwen3:
             logits.append(out)
             if len(tokens) == max_tokens:
                 break
-            out = _forward_cached(*args, [tok], pos, cache, self.dtype)
+            out = _forward_cached(*args, [tok], pos, cache, self.dtype, pages)
             pos += 1
         return tokens, logits
+
+    def forced(self, prompt, tokens):
+        """Teacher forcing: the logits before each of ``tokens`` when the sequence
+        continues with exactly them (row i predicts tokens[i] from prompt + tokens[:i]),
+        so another model's whole continuation can be judged step by step, not only up to
+        its first divergence."""
+        return _forced(self, prompt, tokens)
+
+
+def _forced(model: "DenseQwen3", prompt, tokens):
+    c = model.config
+    args = (c, model.layers, model.emb, model.final_norm)
+    pages = (Fp8Pages(c.num_hidden_layers, c.num_key_value_heads, c.head_dim)
+             if model.kv_fp8 else None)
+    cache: list = []
+    logits = [_forward_cached(*args, list(prompt), 0, cache, model.dtype, pages)]
+    pos = len(prompt)
+    for tok in list(tokens)[:-1]:
+        logits.append(_forward_cached(*args, [int(tok)], pos, cache, model.dtype, pages))
+        pos += 1
+    return logits
 
 
 def generate_greedy_cached(config, weights, prompt, max_tokens, dtype=torch.float64):

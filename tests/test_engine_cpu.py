@@ -237,3 +237,29 @@ def test_decode_rows_gather_only_committed_tokens(model, lengths, sched):
     for i, (p, g) in enumerate(zip(ps, got)):
         tok, logits = generate_greedy(config, weights, p, MAX_TOKENS)
         assert_tokens_match(g, tok, logits, tie_tol=1e-4, msg=f"prompt {i}")
+
+
+@pytest.mark.parametrize("sched", [SchedulerConfig(), SchedulerConfig(max_batched_tokens=24, chunk_size=8)],
+                         ids=["one-pass", "chunked"])
+def test_fp8_kv_engine_matches_the_fp8_dense_recompute(sched):
+    """An fp8-e4m3 KV pool on the PyTorch path against the float64 dense recompute whose
+    K/V go through oracle/kv_write.py's quantising write (oracle/qwen3_dense.py with
+    kv_fp8): the same greedy tokens up to genuine near-ties. Weights of std 0.3 make
+    the tokens depend on the quantisation: the recompute without it diverges on some
+    prompts, so agreeing with the fp8 one is a real check. The engine's chunks of 8
+    leave pages half written between chunks (their scale grows on the next write), the
+    recompute writes each prompt whole: the same values except where a grown scale
+    re-rounds, which the tie tolerance covers."""
+    from oracle.qwen3_dense import DenseQwen3
+
+    config = tiny_config()
+    weights = random_weights(config, seed=3, std=0.3)
+    ps = prompts(6, 3, 40, config.vocab_size, seed=4)
+    engine = make_engine(config, weights, sched=sched, kv_dtype=torch.float8_e4m3fn)
+    got = engine.generate(ps, MAX_TOKENS)
+    fp8 = [DenseQwen3(config, weights, kv_fp8=True).generate(p, MAX_TOKENS) for p in ps]
+    for i, (g, (tok, logits)) in enumerate(zip(got, fp8)):
+        assert_tokens_match(g, tok, logits, tie_tol=1e-3, msg=f"prompt {i}")
+    plain = DenseQwen3(config, weights)
+    assert any(plain.generate(p, MAX_TOKENS)[0] != t for p, (t, _) in zip(ps, fp8))
+    engine.model.manager.check_no_leaks()

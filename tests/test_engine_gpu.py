@@ -8,6 +8,8 @@ same device. A Qwen3-0.6B-shaped model (random init) runs end to end.
 
 from __future__ import annotations
 
+import math
+
 import pytest
 import torch
 
@@ -40,12 +42,38 @@ def test_fp32_kernels_match_dense_recompute(extension, device, head_dim, sched):
     engine.model.manager.check_no_leaks()
 
 
-def _first_divergence_is_a_tie(got, want_tokens, want_logits):
+def _first_divergence_is_a_tie(got, want_tokens, want_logits, ulps=0):
+    """Where ``got`` first leaves the recompute's tokens, its token must be the
+    recompute's top 2 there (the reference's rule, tests/test_engine.py:470-524) or, with
+    ``ulps``, within that many bf16 steps of the best logit (random-init weights put many
+    tokens within bf16 noise of each other: a third-ranked token a bf16 step behind is
+    still a rounding tie). Returns (ok, step or None)."""
     for i, (a, b) in enumerate(zip(got, want_tokens)):
         if a != b:
             top2 = torch.topk(want_logits[i], 2).indices.tolist()
-            return a in top2, i
+            best = float(want_logits[i].max())
+            step = 2.0 ** (math.floor(math.log2(abs(best))) - 7) if best != 0 else 0.0
+            gap = best - float(want_logits[i][a])
+            return a in top2 or gap <= ulps * step, i
     return True, None
+
+
+def _forced_ties(got, want_logits, ulps):
+    """Teacher-forced check of a whole continuation: ``want_logits[i]`` are the
+    recompute's logits before step i given the engine's own tokens so far. Every
+    engine token must be the recompute's top 2 there or within ``ulps`` bf16 steps of
+    its best logit. Returns (worst step, its gap in bf16 steps, its rank)."""
+    worst = (None, 0.0, 0)
+    for i, (a, logits) in enumerate(zip(got, want_logits)):
+        best = float(logits.max())
+        step = 2.0 ** (math.floor(math.log2(abs(best))) - 7) if best != 0 else 1.0
+        gap = (best - float(logits[a])) / step
+        rank = int((logits > logits[a]).sum())
+        if gap > worst[1]:
+            worst = (i, gap, rank)
+        assert rank < 2 or gap <= ulps, \
+            f"step {i}: token {a} ranks {rank + 1}, {gap:.2f} bf16 steps below the best"
+    return worst
 
 
 @pytest.mark.parametrize("head_dim", [64, 128])
@@ -240,29 +268,64 @@ def test_config5_exact_workload(extension, device, qwen3_06b):
 
 
 @pytest.mark.slow
-@pytest.mark.timeout(600)
+@pytest.mark.timeout(900)
 def test_qwen3_0_6b_bf16_greedy_tokens_match_the_float64_recompute(extension, device, qwen3_06b):
-    """Config-5 prompts trimmed to 256 tokens through the config-5 engine (bf16, decode
-    graphs, chunked budget), 8 greedy tokens each, against the dense float64 recompute
-    of the same weights (oracle/qwen3_dense.py, KV-cached). The reference's bf16 rule
-    (tests/test_engine.py:471-524): where a prompt first diverges, the engine's token
-    must be the recompute's top-2 at that step, and at least half the prompts agree
-    exactly."""
+    """16 config-5 prompts trimmed to 256 tokens through the config-5 engine (bf16,
+    decode graphs, chunked budget), 32 greedy tokens each, against the dense float64
+    recompute of the same weights (oracle/qwen3_dense.py, KV-cached). The reference's
+    bf16 rule (tests/test_engine.py:471-524): where a prompt first diverges, the engine's
+    token must be a rounding tie of the recompute's (its top 2, or within 2 bf16 steps of
+    its best logit), and at least half the prompts agree exactly. Then every one of the
+    512 tokens, teacher-forced (the recompute fed the engine's own continuation), must
+    be such a tie: the check does not stop at the first divergence."""
     from mini_vllm.workloads import config5_prompts
     from oracle.qwen3_dense import DenseQwen3
 
     config, weights = qwen3_06b
-    ps = [p[:256] for p in config5_prompts(6, config.vocab_size)]
+    ps = [p[:256] for p in config5_prompts(16, config.vocab_size)]
     engine = _config5_engine(config, weights, device)
-    got = engine.generate(ps, MAX_TOKENS)
+    got = engine.generate(ps, 32)
     dense = DenseQwen3(config, weights)
     agree = 0
     for i, (g, p) in enumerate(zip(got, ps)):
-        tok, logits = dense.generate(p, MAX_TOKENS)
-        ok, step = _first_divergence_is_a_tie(g, tok, logits)
-        assert ok, f"prompt {i} diverges at step {step} outside the recompute's top 2"
+        tok, logits = dense.generate(p, 32)
+        ok, step = _first_divergence_is_a_tie(g, tok, logits, ulps=2)
+        worst = _forced_ties(g, logits if step is None else dense.forced(p, g), ulps=4)
+        print(f"prompt {i}: first divergence at {step}; worst forced step {worst}", flush=True)
+        assert ok, f"prompt {i} diverges at step {step} outside a rounding tie"
         agree += step is None
     assert agree >= len(ps) // 2, f"only {agree} of {len(ps)} prompts agree exactly"
+
+
+@pytest.mark.slow
+@pytest.mark.timeout(900)
+def test_qwen3_0_6b_fp8_kv_tokens_match_the_fp8_recompute(extension, device, qwen3_06b):
+    """The config-5 engine over an fp8-e4m3 KV cache (quantising write and fp8 attention
+    kernels) against the dense float64 recompute whose K/V pass through
+    oracle/kv_write.py's quantisation (DenseQwen3 with kv_fp8): 16 config-5 prompts
+    trimmed to 256 tokens, 32 greedy tokens each, every token teacher-forced and
+    required to be a rounding tie of the recompute's, and at least half the prompts
+    the recompute's argmax at every step. Free-running agreement is a poor measure
+    here: the engine's K/V are bf16 before they are quantised, so bf16 noise moves some
+    of them across an e4m3 rounding boundary (a step of 1/16 relative), each such code
+    a whole e4m3 step from the recompute's, and one early tie changes every later
+    token."""
+    from mini_vllm.workloads import config5_prompts
+    from oracle.qwen3_dense import DenseQwen3
+
+    config, weights = qwen3_06b
+    ps = [p[:256] for p in config5_prompts(16, config.vocab_size)]
+    engine = _config5_engine(config, weights, device, kv_dtype=torch.float8_e4m3fn)
+    got = engine.generate(ps, 32)
+    dense = DenseQwen3(config, weights, kv_fp8=True)
+    exact = 0
+    for i, (g, p) in enumerate(zip(got, ps)):
+        worst = _forced_ties(g, dense.forced(p, g), ulps=4)
+        print(f"prompt {i}: worst forced step {worst}", flush=True)
+        exact += worst[0] is None  # the recompute's argmax at every step
+    # measured: 9 of 16 prompts take the recompute's argmax at all 32 steps, the other 7
+    # its second-ranked token where they do not
+    assert exact >= len(ps) // 2, f"only {exact} of {len(ps)} prompts follow the argmax"
 
 
 @pytest.mark.slow
@@ -369,3 +432,30 @@ def test_decode_graphs_feed_only_committed_tokens(extension, device, lengths, sc
         engine.model.manager.check_no_leaks()
         for i, (got, (tok, logits)) in enumerate(zip(runs[graphs], want)):
             assert_tokens_match(got, tok, logits, tie_tol=1e-4, msg=f"graphs={graphs} prompt {i}")
+
+
+@pytest.mark.parametrize("sched", [SchedulerConfig(), SchedulerConfig(max_batched_tokens=24, chunk_size=8)],
+                         ids=["one-pass", "chunked"])
+def test_fp8_kv_cache_engine_matches_the_fp8_dense_recompute(extension, device, sched):
+    """The fp8-KV engine on the kernels (fp32 activations, decode graphs) against the
+    float64 dense recompute whose K/V go through oracle/kv_write.py's quantising write
+    (DenseQwen3 with kv_fp8), not against the product's own PyTorch path: equal up to
+    near-ties of 1e-3. Weights of std 0.3 make the tokens depend on the quantisation
+    (the recompute without it diverges). With bf16 activations the comparison is the
+    0.6B test's teacher-forced tie rule: bf16 noise moves K/V across e4m3 rounding
+    boundaries, which a std-0.3 model turns into different tokens."""
+    from oracle.qwen3_dense import DenseQwen3
+
+    config = tiny_config(torch.float32)
+    weights = random_weights(config, seed=3, std=0.3, device=device)
+    ps = prompts(6, 3, 60, config.vocab_size, seed=4)
+    engine = make_engine(config, weights, use_cuda=True, device=device, sched=sched,
+                         kv_dtype=torch.float8_e4m3fn, use_graphs=True)
+    got = engine.generate(ps, MAX_TOKENS)
+    engine.model.manager.check_no_leaks()
+    dense = DenseQwen3(config, weights, kv_fp8=True)
+    fp8 = [dense.generate(p, MAX_TOKENS) for p in ps]
+    for i, (g, (tok, logits)) in enumerate(zip(got, fp8)):
+        assert_tokens_match(g, tok, logits, tie_tol=1e-3, msg=f"prompt {i}")
+    plain = DenseQwen3(config, weights)
+    assert any(plain.generate(p, MAX_TOKENS)[0] != t for p, (t, _) in zip(ps, fp8))

@@ -362,3 +362,59 @@ def test_dense_model_oracle_matches_transformers_qwen3():
             assert tokens == want_tokens, f"prompt {i}"
             got = np.stack([l.numpy() for l in logits])
             assert np.abs(got - want_logits).max() < 1e-6, f"prompt {i}"
+
+
+def test_fp8_pages_of_the_dense_oracle():
+    """oracle/qwen3_dense.py's Fp8Pages: one write of a fresh sequence equals a direct
+    per-(page, kv head) quantisation at scale pow2ceil(amax / 448) (the closed form of the
+    write policy for one run); written token by token, every page ends at the scale of
+    its whole contents and every value within half an e4m3 step of its source (re-encoding
+    under a grown power-of-two scale being exact above the subnormals)."""
+    from oracle.kv_write import pow2_ceil
+    from oracle.qwen3_dense import Fp8Pages
+
+    gen = torch.Generator().manual_seed(5)
+    k = torch.randn(40, 2, 8, generator=gen, dtype=torch.float64) * 3
+    v = torch.randn(40, 2, 8, generator=gen, dtype=torch.float64)
+    pages = Fp8Pages(1, 2, 8)
+    keys, vals = pages.write(0, 0, k, v)
+    for x, got in ((k, keys), (v, vals)):
+        padded = torch.zeros(48, 2, 8, dtype=torch.float64)
+        padded[:40] = x
+        blocks = padded.view(3, 16, 2, 8).float()
+        amax = blocks.abs().amax(dim=(1, 3)).numpy()
+        scale = torch.from_numpy(pow2_ceil(amax / np.float32(448.0)))
+        codes = (blocks / scale[:, None, :, None]).to(torch.float8_e4m3fn)
+        want = (codes.float() * scale[:, None, :, None]).view(48, 2, 8)[:40].double()
+        assert torch.equal(got, want)
+    step = Fp8Pages(1, 2, 8)
+    for t in range(40):
+        keys, vals = step.write(0, t, k[t:t + 1], v[t:t + 1])
+    assert keys.shape == (40, 2, 8)
+    for x, got, i in ((k, keys, 0), (v, vals, 1)):
+        scales = step.scales[0][i]
+        for b in range(3):
+            rows = x[16 * b:16 * b + 16].float()
+            want_s = pow2_ceil((rows.abs().amax(dim=(0, 2)) / 448.0).numpy())
+            assert np.array_equal(scales[b], want_s), b
+            s = torch.from_numpy(want_s).double()[None, :, None]
+            mag = (rows.double() / s).abs()
+            half_step = torch.where(mag < 2.0**-6, 2.0**-10, 2.0 ** (torch.floor(torch.log2(mag)) - 4))
+            assert ((got[16 * b:16 * b + 16] - rows.double()).abs() <= half_step * s + 1e-12).all(), b
+
+
+@pytest.mark.parametrize("kv_fp8", [False, True])
+def test_teacher_forcing_the_greedy_tokens_gives_the_same_logits(kv_fp8):
+    """DenseQwen3.forced fed the model's own greedy continuation returns exactly the
+    logits its generate() saw (same cache path, one token a step), with and without
+    the fp8 pages."""
+    from engine_helpers import tiny_config
+    from mini_vllm.model import random_weights
+    from oracle.qwen3_dense import DenseQwen3
+
+    config = tiny_config()
+    dense = DenseQwen3(config, random_weights(config, seed=1, std=0.3), kv_fp8=kv_fp8)
+    prompt = [5, 9, 100, 7, 300]
+    tokens, logits = dense.generate(prompt, 6)
+    forced = dense.forced(prompt, tokens)
+    assert len(forced) == 6 and all(torch.equal(a, b) for a, b in zip(logits, forced))

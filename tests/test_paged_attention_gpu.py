@@ -587,3 +587,35 @@ def test_the_torch_path_runs_on_device_without_cuda_requested(extension, device)
     b = case([256, 30], [1, 30], device)
     got = ops.paged_attention(*b.args(), use_cuda=False)
     assert_max_abs(got, oracle(b), 1e-5)
+
+
+def test_a_captured_split_prefill_runs_items_whole(extension, device):
+    """A split-grid prefill captured into a graph must not name its stream's arrival
+    counters (a replay on another stream could overlap a launch on the capture stream):
+    captured, it runs every item whole - counted by split_stats - and each replay, also
+    on another stream, matches the oracle and the eager whole-item call's bits."""
+    b = case([6000, 700], [512, 300], device, dtype=torch.bfloat16, num_q_heads=16,
+             num_kv_heads=8, head_dim=128)
+    opts = _split(8)
+    whole = kernel(extension, b, {"prefill_schedule": "grid", "prefill_pieces": 1})
+    kernel(extension, b, opts)  # eager warm-up: the workspace exists before capture
+    before = extension.split_stats()["whole_capturing"]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        out = extension.paged_attention(*b.args(), plan_options=opts)
+    assert extension.split_stats()["whole_capturing"] > before
+    want = oracle(b)
+    other = torch.cuda.Stream()
+    for i in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        if i == 2:
+            with torch.cuda.stream(other):
+                graph.replay()
+        else:
+            graph.replay()
+        torch.cuda.synchronize()
+        assert_max_abs(out, want, ATTN_ATOL[torch.bfloat16], f"replay {i}")
+        assert torch.equal(out, whole)
