@@ -425,6 +425,168 @@ def run_elementwise(steps: int = 20) -> dict:
     return out
 
 
+class ClockSampler:
+    """Polls ``amd-smi metric --clock`` in a background thread and keeps the highest
+    graphics clock (the busiest XCD) and memory clock seen, as the reference's
+    ClockSampler does with nvidia-smi (mini_vllm/bench.py:113-235): one reading taken
+    after the work has finished shows idle clocks, the peak over the run shows whether
+    the card was allowed to run fast while it was measured. A run whose peak is below
+    half the maximum graphics or memory clock is flagged as throttled (the reference's
+    threshold, :135-143)."""
+
+    def __init__(self, interval: float = 1.0) -> None:
+        import shutil
+        import threading
+
+        self.interval = interval
+        self.available = shutil.which("amd-smi") is not None
+        self.samples = 0
+        self.peak_gfx = self.max_gfx = self.peak_mem = self.max_mem = 0
+        self.first = self.last = None
+        self._stop = threading.Event()
+        self._thread = threading.Thread(target=self._poll, daemon=True) if self.available else None
+
+    @staticmethod
+    def read() -> dict | None:
+        import subprocess
+
+        try:
+            out = subprocess.run(["amd-smi", "metric", "-g", "0", "--clock", "--json"],
+                                 capture_output=True, text=True, timeout=10, check=True).stdout
+            data = json.loads(out)
+            clocks = (data["gpu_data"] if isinstance(data, dict) else data)[0]["clock"]
+        except (subprocess.SubprocessError, OSError, ValueError, KeyError, IndexError, TypeError):
+            return None
+
+        def mhz(entry, key):
+            v = entry.get(key) if isinstance(entry, dict) else None
+            return int(v["value"]) if isinstance(v, dict) and "value" in v else 0
+
+        gfx = [c for k, c in clocks.items() if k.startswith("gfx")]
+        mem = [c for k, c in clocks.items() if k.startswith("mem")]
+        return {"gfx_mhz": max((mhz(c, "clk") for c in gfx), default=0),
+                "gfx_max_mhz": max((mhz(c, "max_clk") for c in gfx), default=0),
+                "mem_mhz": max((mhz(c, "clk") for c in mem), default=0),
+                "mem_max_mhz": max((mhz(c, "max_clk") for c in mem), default=0)}
+
+    def _poll(self) -> None:
+        while not self._stop.is_set():
+            r = self.read()
+            if r is not None:
+                self.samples += 1
+                self.first = self.first or r
+                self.last = r
+                self.peak_gfx = max(self.peak_gfx, r["gfx_mhz"])
+                self.peak_mem = max(self.peak_mem, r["mem_mhz"])
+                self.max_gfx = max(self.max_gfx, r["gfx_max_mhz"])
+                self.max_mem = max(self.max_mem, r["mem_max_mhz"])
+            self._stop.wait(self.interval)
+
+    def __enter__(self) -> "ClockSampler":
+        if self._thread is not None:
+            self._thread.start()
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self._stop.set()
+        if self._thread is not None:
+            self._thread.join(timeout=15)
+
+    def report(self) -> dict:
+        if not self.available or self.samples == 0:
+            return {"available": False, "reason": "amd-smi missing or unreadable"}
+        throttled = (self.max_gfx and self.peak_gfx < 0.5 * self.max_gfx) or \
+            (self.max_mem and self.peak_mem < 0.5 * self.max_mem)
+        return {"available": True, "samples": self.samples, "interval_s": self.interval,
+                "peak_gfx_mhz": self.peak_gfx, "max_gfx_mhz": self.max_gfx,
+                "peak_mem_mhz": self.peak_mem, "max_mem_mhz": self.max_mem,
+                "first_sample": self.first, "last_sample": self.last,
+                "throttled": bool(throttled)}
+
+
+def read_ceiling(steps: int = 20, total_bytes: int = 2 << 30, page_bytes: int = 32768) -> dict:
+    """Read-only HBM ceilings from the library's probe (``mvllm_read_probe``): a 2 GiB
+    buffer (8x the Infinity Cache) read as 32 KB pages - one paged pool's page of 16
+    rows x 8 kv heads x 128 bf16 - in address order and in a shuffled order (as the
+    decode reads its pages), each at several resident workgroup counts, best of them.
+    The paged decode's own rate is bounded by the shuffled figure; a device copy (the
+    reference's ceiling) moves reads and writes at once and lands below the decode."""
+    from mini_vllm.kernels.extension import load_extension
+
+    ext = load_extension()
+    base = torch.empty(total_bytes, dtype=torch.uint8, device="cuda")
+    base.view(torch.int32).random_()
+    pages = total_bytes // page_bytes
+    gen = torch.Generator().manual_seed(0)
+    shuffled = torch.randperm(pages, generator=gen).to(torch.int32).cuda()
+    out = {"buffer_bytes": total_bytes, "page_bytes": page_bytes}
+    for name, ids in (("sequential", None), ("shuffled_pages", shuffled)):
+        best = (0.0, 0)
+        for wgs in (256, 512, 1024, 2048):
+            sink = torch.empty(wgs * 256, dtype=torch.int32, device="cuda")
+            ms = time_steps(lambda i: ext.read_probe(base, page_bytes, ids, wgs, sink), steps, 3)
+            gbs = total_bytes / (ms * 1e-3) / 1e9
+            best = max(best, (gbs, wgs))
+        out[f"{name}_gbs"] = round(best[0], 1)
+        out[f"{name}_workgroups"] = best[1]
+        log(f"read ceiling {name}: {best[0]:.0f} GB/s ({best[1]} workgroups)")
+    del base, shuffled
+    torch.cuda.empty_cache()
+    return out
+
+
+def run_kernel_cases(steps: int = 20) -> dict:
+    """The reference's own kernel-benchmark shapes (mini_vllm/bench.py:617-691, bf16,
+    16q/8kv heads, D 128, 16-token pages, shuffled tables): paged decode at (B, S) in
+    {(1, 8192), (16, 1024), (64, 1024)} - bytes = 2 B S H_k D x 2, the reference's rule
+    (:643) - and a prefill chunk at (L, S) in {(512, 2048), (2048, 2048)} - FLOPs over
+    visible pairs, and the reference's bytes moved (q + K + V). Decode pools are rotated
+    over enough copies that a step's pages are not in the 256 MB Infinity Cache. Each
+    against the PyTorch path (the reference's gather-then-dense oracle) on the same GPU,
+    the speedup column of the reference's table."""
+    from mini_vllm.kernels import ops
+    from mini_vllm.workloads import build_batch, prefill_flops
+
+    out = {}
+    for b, S in ((1, 8192), (16, 1024), (64, 1024)):
+        kv = 2 * b * S * 8 * 128 * 2
+        copies = max(2, -(-600_000_000 // kv))
+        batches = [build_batch([S] * b, [1] * b, dtype=torch.bfloat16, seed=c, spare_blocks=0,
+                               device="cuda", generator_device="cuda") for c in range(copies)]
+        ms = run_paged(batches, steps, 3)
+        torch_ms = time_steps(lambda i: ops.paged_attention(*batches[i % copies].args(),
+                                                            use_cuda=False), 3, 1)
+        gbs = kv / (ms * 1e-3) / 1e9
+        out[f"decode_B{b}_S{S}"] = {"us": round(ms * 1e3, 1), "kv_bytes": kv,
+                                    "gbs": round(gbs, 1),
+                                    "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                                    "rotated_copies": copies, "torch_path_us": round(torch_ms * 1e3, 1),
+                                    "speedup_vs_torch_path": round(torch_ms / ms, 1)}
+        log(f"kernel case decode B={b} S={S}: {ms * 1e3:.1f} us, {gbs:.0f} GB/s; "
+            f"torch path {torch_ms * 1e3:.0f} us ({torch_ms / ms:.0f}x)")
+        del batches
+    for L, S in ((512, 2048), (2048, 2048)):
+        batches = [build_batch([S], [L], dtype=torch.bfloat16, seed=c, spare_blocks=0,
+                               device="cuda", generator_device="cuda") for c in range(2)]
+        ms = run_paged(batches, steps, 3)
+        torch_ms = time_steps(lambda i: ops.paged_attention(*batches[i % 2].args(), use_cuda=False),
+                              3, 1)
+        flops = prefill_flops(batches[0])
+        moved = (batches[0].q.numel() + 2 * S * 8 * 128) * 2
+        tflops = flops / (ms * 1e-3) / 1e12
+        out[f"prefill_L{L}_S{S}"] = {"us": round(ms * 1e3, 1), "gflop": round(flops / 1e9, 3),
+                                     "tflops": round(tflops, 1),
+                                     "frac_of_bf16_mfma_peak": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4),
+                                     "bytes_moved": moved,
+                                     "torch_path_us": round(torch_ms * 1e3, 1),
+                                     "speedup_vs_torch_path": round(torch_ms / ms, 1)}
+        log(f"kernel case prefill L={L} S={S}: {ms * 1e3:.1f} us, {tflops:.0f} TFLOP/s; "
+            f"torch path {torch_ms * 1e3:.0f} us ({torch_ms / ms:.0f}x)")
+        del batches
+    torch.cuda.empty_cache()
+    return out
+
+
 def copy_ceiling(nbytes: int, steps: int = 20) -> float:
     """GB/s of a device-to-device copy_ (read + write counted), the practical ceiling
     (method of the reference's mini_vllm/bench.py:448-466)."""
@@ -567,13 +729,15 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--copies", type=int, default=3, help="rotated pool copies (defeat the MALL)")
     parser.add_argument("--skip-extras", action="store_true", help="headline config 2 only")
-    parser.add_argument("--extras", default="3,3fp8,4,5,ew,kv,dense,linear,gemm,copy",
+    parser.add_argument("--extras", default="3,3fp8,4,5,ew,kv,dense,linear,gemm,ceiling,cases",
                         help="comma list of extras to run: 3 (prefill), 3fp8 (prefill over an "
                              "fp8 pool), 4 (fp8 decode), "
                              "5 (engine), 5small (engine, 64 x 128 tokens), 5fp8 (engine, fp8 "
                              "KV cache), ew (elementwise "
                              "kernels), kv (KV write), dense (dense-cache attention), linear "
-                             "(decode projections and argmax), gemm (prefill projections on hipBLASLt), copy, "
+                             "(decode projections and argmax), gemm (prefill projections on hipBLASLt), "
+                             "ceiling (read-only HBM probe: sequential and shuffled 32 KB pages), "
+                             "cases (the reference's kernel-bench shapes), copy (device copy_), "
                              "pfocc (prefill items of 16 tiles on half and on all of the CUs)")
     parser.add_argument("--no-cpu", action="store_true")
     args = parser.parse_args()
@@ -597,6 +761,7 @@ def main() -> int:
     ext = load_extension()
     log(f"library {ext.path}; device {torch.cuda.get_device_name(0)}")
 
+    sampler = ClockSampler().__enter__()
     log("config 2: building inputs")
     batches = rotated_batches(2, args.copies)
     b = batches[0]
@@ -676,6 +841,19 @@ def main() -> int:
     if "copy" in wanted:
         extras["copy_ceiling_gbs"] = round(copy_ceiling(1 << 30), 1)
         log(f"copy_ ceiling {extras['copy_ceiling_gbs']} GB/s (1 GiB device-to-device copies)")
+    if "ceiling" in wanted:
+        ceil = read_ceiling()
+        ceil["config2_frac_of_shuffled"] = round(gbs / ceil["shuffled_pages_gbs"], 4)
+        ceil["config2_frac_of_sequential"] = round(gbs / ceil["sequential_gbs"], 4)
+        extras["read_ceiling"] = ceil
+    if "cases" in wanted:
+        extras["kernel_cases"] = run_kernel_cases()
+    sampler.__exit__(None, None, None)
+    clocks = sampler.report()
+    log(f"gpu clocks over the GPU legs: {clocks}")
+    if clocks.get("throttled"):
+        log("WARNING: the GPU ran below half its clocks during this run; its numbers measure "
+            "the power state, not the code")
 
     cpu = None
     if not args.no_cpu:
@@ -713,6 +891,7 @@ def main() -> int:
             "traffic": measured_traffic(),
         },
         "cpu_baseline": cpu,
+        "gpu_clocks": clocks,
         "extras": extras,
     }
     print(json.dumps(result), flush=True)

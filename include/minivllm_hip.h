@@ -452,6 +452,17 @@ int mvllm_argmax(int64_t* out, const void* logits, int64_t rows, int64_t vocab,
  * Rows may hold up to 64 segments (1048576 logits). */
 uint64_t mvllm_argmax_workspace_bytes(int64_t rows, int64_t vocab);
 
+/* Read-only HBM probe for the benchmark's bandwidth ceiling (no counterpart in the
+ * reference, whose ceiling is a device copy, mini_vllm/bench.py:448-466): reads
+ * `num_pages` pages of `page_bytes` (4-64 KB, a multiple of 4 KB) from `base`, page i at
+ * page_ids[i] (device int32, every id in [0, base_bytes / page_bytes)) or at i when
+ * page_ids is NULL, with `workgroups` workgroups of 256 lanes, each lane's 16-byte
+ * nontemporal loads of a page all in flight before use; stores one folded word per
+ * lane into `sink` (sink_words >= 256 x workgroups). */
+int mvllm_read_probe(const void* base, int64_t base_bytes, const int32_t* page_ids,
+                     int64_t num_pages, int64_t page_bytes, int32_t workgroups, uint32_t* sink,
+                     int64_t sink_words, void* stream);
+
 /* y = a * x + b over n floats: the toolchain smoke test, replacing `mini_vllm_C.hello`
  * (csrc/bindings.cpp:8,37-42 -> csrc/hello.cu:11-21; mini_vllm/kernels/extension.py:349-353). */
 int mvllm_axpby(float* y, const float* x, float a, float b, int64_t n, void* stream);

@@ -21,14 +21,15 @@
 // the bucket's against 6.2 with the exact shape's).
 // Choosing among the candidates: the heuristic's first is not always the fastest on
 // this part, so the first call of a bucket (or exact shape) times every candidate on
-// the call's own operands (one warm-up and kBlasTimedRuns runs each, HIP events on the
-// caller's stream, one host wait) and keeps the fastest; a call made while its stream
+// the call's own operands (one warm-up and kBlasTimedRuns runs each, every run between
+// its own two HIP events on the caller's stream, the least kept, one host wait) and
+// keeps the fastest; a call made while its stream
 // is being captured into a graph cannot wait, so it keeps the heuristic's first
 // without timing. The record of that choice (candidates, the first's and the kept
 // one's time) is kept for reports.
 // The heuristic's first 16 are not the library's best on this part either: timing every
-// algorithm hipBLASLt holds for a shape (~2000 of its ~20000 serve one) found ones
-// 10-25% faster at the Qwen3-0.6B projection shapes. That sweep takes ~0.5 s per shape,
+// algorithm hipBLASLt holds for a shape (~230 of its ~20000 run at a Qwen3-0.6B
+// projection shape) found faster ones. That sweep takes ~0.5 s per shape,
 // too long for a first call, so it is an explicit step (blas_tune, at one row count per
 // (n, k)): its fastest kBlasPreferred algorithms join the heuristic's candidates of every
 // later bucket choice of that (n, k), each checked against the bucket's m first.
@@ -172,35 +173,63 @@ hipblasStatus_t matmul(hipblasLtHandle_t handle, const BlasPlan& plan, const Alg
                          call.stream);
 }
 
-// The fastest of `cands` on the call's own operands: each gets one warm-up and
-// kBlasTimedRuns timed runs between two events on the caller's stream (one host wait
-// per candidate). A candidate hipBLASLt refuses for this m is skipped. Leaves the
-// kept algorithm's record in `best.tuning`. Caller holds the mutex; the stream is not
+// Events bracketing each timed run of a candidate.
+struct RunEvents {
+  hipEvent_t start[kBlasTimedRuns] = {};
+  hipEvent_t stop[kBlasTimedRuns] = {};
+  bool ok = true;
+  RunEvents() {
+    for (int r = 0; r < kBlasTimedRuns; ++r) {
+      ok = ok && hipEventCreate(&start[r]) == hipSuccess && hipEventCreate(&stop[r]) == hipSuccess;
+    }
+  }
+  ~RunEvents() {
+    for (int r = 0; r < kBlasTimedRuns; ++r) {
+      if (start[r]) (void)hipEventDestroy(start[r]);
+      if (stop[r]) (void)hipEventDestroy(stop[r]);
+    }
+  }
+};
+
+// One warm-up and `runs` (<= kBlasTimedRuns) runs of `algo`, each bracketed by its own
+// pair of events, one host wait: the least of the runs' GPU times in ms, or -1 if
+// hipBLASLt refuses the algorithm for these operands. Timing each run on its own keeps
+// the host out of the figure: back-to-back products of ~20 us are issued about as fast
+// as they run, so a pair of events around several of them measures the issue rate, the
+// same for every candidate.
+float time_runs(hipblasLtHandle_t handle, const BlasPlan& plan, const Algo& algo,
+                const Call& call, RunEvents& ev, int runs) {
+  if (matmul(handle, plan, algo, call) != HIPBLAS_STATUS_SUCCESS) return -1.0f;
+  for (int r = 0; r < runs; ++r) {
+    if (hipEventRecord(ev.start[r], call.stream) != hipSuccess ||
+        matmul(handle, plan, algo, call) != HIPBLAS_STATUS_SUCCESS ||
+        hipEventRecord(ev.stop[r], call.stream) != hipSuccess) {
+      return -1.0f;
+    }
+  }
+  if (hipEventSynchronize(ev.stop[runs - 1]) != hipSuccess) return -1.0f;
+  float least = -1.0f;
+  for (int r = 0; r < runs; ++r) {
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, ev.start[r], ev.stop[r]) != hipSuccess) return -1.0f;
+    if (least < 0.0f || ms < least) least = ms;
+  }
+  return least;
+}
+
+// The fastest of `cands` on the call's own operands (time_runs, kBlasTimedRuns runs
+// each). A candidate hipBLASLt refuses for this m is skipped. Leaves the kept
+// algorithm's record in `best.tuning`. Caller holds the mutex; the stream is not
 // capturing.
 BlasStatus fastest(hipblasLtHandle_t handle, const BlasPlan& plan, std::vector<Algo>& cands,
                    const Call& call, Algo& best) {
-  hipEvent_t start = nullptr, stop = nullptr;
-  hipError_t e = hipEventCreate(&start);
-  if (e == hipSuccess) e = hipEventCreate(&stop);
-  if (e != hipSuccess) {
-    if (start) (void)hipEventDestroy(start);
-    return BlasStatus{1, static_cast<int>(e), "tuning events"};
-  }
+  RunEvents ev;
+  if (!ev.ok) return BlasStatus{1, static_cast<int>(hipErrorOutOfMemory), "tuning events"};
   float best_ms = -1.0f, first_ms = -1.0f;
   int best_i = -1, timed = 0;
   for (size_t i = 0; i < cands.size(); ++i) {
-    if (matmul(handle, plan, cands[i], call) != HIPBLAS_STATUS_SUCCESS) continue;
-    e = hipEventRecord(start, call.stream);
-    bool ok = e == hipSuccess;
-    for (int r = 0; ok && r < kBlasTimedRuns; ++r) {
-      ok = matmul(handle, plan, cands[i], call) == HIPBLAS_STATUS_SUCCESS;
-    }
-    if (ok) ok = hipEventRecord(stop, call.stream) == hipSuccess;
-    if (ok) ok = hipEventSynchronize(stop) == hipSuccess;
-    float ms = 0.0f;
-    if (ok) ok = hipEventElapsedTime(&ms, start, stop) == hipSuccess;
-    if (!ok) continue;
-    ms /= kBlasTimedRuns;
+    const float ms = time_runs(handle, plan, cands[i], call, ev, kBlasTimedRuns);
+    if (ms < 0.0f) continue;
     ++timed;
     if (i == 0) first_ms = ms;
     if (best_i < 0 || ms < best_ms) {
@@ -208,8 +237,6 @@ BlasStatus fastest(hipblasLtHandle_t handle, const BlasPlan& plan, std::vector<A
       best_i = static_cast<int>(i);
     }
   }
-  (void)hipEventDestroy(start);
-  (void)hipEventDestroy(stop);
   if (best_i < 0) return BlasStatus{3, 0, "no candidate algorithm ran"};
   best = cands[best_i];
   best.tuning = BlasTuning{static_cast<int>(cands.size()), timed, best_i, first_ms * 1e3f,
@@ -393,13 +420,10 @@ BlasStatus blas_tune(void* y, const void* x, const void* w, int64_t m, int64_t n
     destroy(plan);
     return lt_error(s, "algorithm list");
   }
-  hipEvent_t start = nullptr, stop = nullptr;
-  e = hipEventCreate(&start);
-  if (e == hipSuccess) e = hipEventCreate(&stop);
-  if (e != hipSuccess) {
-    if (start) (void)hipEventDestroy(start);
+  RunEvents ev;
+  if (!ev.ok) {
     destroy(plan);
-    return BlasStatus{1, static_cast<int>(e), "tuning events"};
+    return BlasStatus{1, static_cast<int>(hipErrorOutOfMemory), "tuning events"};
   }
   const Call call{y, x, w, workspace, stream};
   const float alpha = 1.0f, beta = 0.0f;
@@ -414,17 +438,9 @@ BlasStatus blas_tune(void* y, const void* x, const void* w, int64_t m, int64_t n
         need > kBlasWorkspaceBytes) {
       continue;
     }
-    if (matmul(handle, plan, cand, call) != HIPBLAS_STATUS_SUCCESS) continue;
-    bool ok = hipEventRecord(start, stream) == hipSuccess;
-    for (int r = 0; ok && r < kBlasSweepRuns; ++r) ok = matmul(handle, plan, cand, call) == HIPBLAS_STATUS_SUCCESS;
-    if (ok) ok = hipEventRecord(stop, stream) == hipSuccess;
-    if (ok) ok = hipEventSynchronize(stop) == hipSuccess;
-    float ms = 0.0f;
-    if (ok) ok = hipEventElapsedTime(&ms, start, stop) == hipSuccess;
-    if (ok) times.emplace_back(ms, i);
+    const float ms = time_runs(handle, plan, cand, call, ev, kBlasSweepRuns);
+    if (ms >= 0.0f) times.emplace_back(ms, i);
   }
-  (void)hipEventDestroy(start);
-  (void)hipEventDestroy(stop);
   if (times.empty()) {
     destroy(plan);
     return BlasStatus{3, 0, "no algorithm serves this shape"};

@@ -20,7 +20,7 @@ constexpr uint64_t kBlasWorkspaceBytes = 32ull << 20;
 // Heuristic candidates timed on the first call of a bucket (or exact shape), and the
 // timed runs of each.
 constexpr int kBlasCandidates = 16;
-constexpr int kBlasTimedRuns = 4;
+constexpr int kBlasTimedRuns = 5;
 // blas_tune: timed runs of each algorithm in its sweep, and how many of the fastest it
 // keeps as extra candidates.
 constexpr int kBlasSweepRuns = 3;
@@ -47,8 +47,8 @@ BlasStatus blas_linear(void* y, const void* x, const void* w, int64_t m, int64_t
                        int dtype, void* workspace, hipStream_t stream);
 
 // Times every algorithm hipBLASLt holds that serves y = x w^T at (m, n, k) (one warm-up
-// and kBlasSweepRuns runs each, on the caller's operands and stream, one host wait per
-// algorithm) and keeps the kBlasPreferred fastest as extra candidates for every later
+// and kBlasSweepRuns runs each, the least of the runs' own times, on the caller's
+// operands and stream, one host wait per algorithm) and keeps the kBlasPreferred fastest as extra candidates for every later
 // choice of (n, k); choices already made for (n, k) are dropped and made again. Leaves y
 // = x w^T. Refused while `stream` is capturing. `timed` = the algorithms timed.
 BlasStatus blas_tune(void* y, const void* x, const void* w, int64_t m, int64_t n, int64_t k,

@@ -22,6 +22,7 @@
 #include "linear.hpp"
 #include "sampler.hpp"
 #include "paged_attention.hpp"
+#include "probe.hpp"
 
 namespace {
 
@@ -1400,6 +1401,35 @@ int mvllm_kv_write(void* key_pool, void* value_pool, float* k_scales, float* v_s
                                            shift, num_blocks, src_dtype, pool_dtype,
                                            static_cast<hipStream_t>(stream)),
                     "kv_write: launch");
+}
+
+int mvllm_read_probe(const void* base, int64_t base_bytes, const int32_t* page_ids,
+                     int64_t num_pages, int64_t page_bytes, int32_t workgroups, uint32_t* sink,
+                     int64_t sink_words, void* stream) {
+  g_error[0] = '\0';
+  if (base == nullptr || sink == nullptr) return fail(MVLLM_ERR_INVALID, "read_probe: NULL buffer");
+  if (!mvllm::read_probe_supported(page_bytes)) {
+    return fail(MVLLM_ERR_UNSUPPORTED,
+                "read_probe: page_bytes %lld is not served (4, 8, 16, 32 or 64 KB)",
+                static_cast<long long>(page_bytes));
+  }
+  if (num_pages < 0 || base_bytes < 0 || workgroups <= 0 || workgroups > 65536) {
+    return fail(MVLLM_ERR_INVALID, "read_probe: bad page count or workgroups");
+  }
+  if (base_bytes / page_bytes < (page_ids == nullptr ? num_pages : 1)) {
+    return fail(MVLLM_ERR_INVALID, "read_probe: the base buffer holds fewer pages than read");
+  }
+  if (sink_words < mvllm::read_probe_sink_words(workgroups)) {
+    return fail(MVLLM_ERR_INVALID, "read_probe: the sink must hold %d words",
+                mvllm::read_probe_sink_words(workgroups));
+  }
+  if (reinterpret_cast<uintptr_t>(base) % 16 != 0) {
+    return fail(MVLLM_ERR_INVALID, "read_probe: base must be 16-byte aligned");
+  }
+  if (num_pages == 0) return MVLLM_OK;
+  return hip_status(mvllm::launch_read_probe(base, page_ids, num_pages, page_bytes, workgroups,
+                                             sink, static_cast<hipStream_t>(stream)),
+                    "read_probe: launch");
 }
 
 int mvllm_axpby(float* y, const float* x, float a, float b, int64_t n, void* stream) {

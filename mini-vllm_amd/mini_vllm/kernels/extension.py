@@ -310,6 +310,8 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_blas_workspace_bytes.argtypes = []
     lib.mvllm_blas_plans_cached.restype = ctypes.c_int
     lib.mvllm_blas_plans_cached.argtypes = []
+    lib.mvllm_read_probe.restype = ctypes.c_int
+    lib.mvllm_read_probe.argtypes = [p, i64, p, i64, i64, i32, p, i64, p]
     lib.mvllm_split_stats.restype = None
     lib.mvllm_split_stats.argtypes = [ctypes.POINTER(i32), ctypes.POINTER(i64), ctypes.POINTER(i64)]
     lib.mvllm_blas_tune.restype = ctypes.c_int
@@ -352,6 +354,7 @@ EXPORTED_SYMBOLS = (
     "mvllm_blas_tuning",
     "mvllm_blas_tune",
     "mvllm_split_stats",
+    "mvllm_read_probe",
 )
 
 
@@ -817,6 +820,20 @@ class HipExtension:
     def blas_plans_cached(self) -> int:
         """Shapes the hipBLASLt entry currently keeps."""
         return int(self.lib.mvllm_blas_plans_cached())
+
+    def read_probe(self, base: torch.Tensor, page_bytes: int, page_ids: torch.Tensor | None,
+                   workgroups: int, sink: torch.Tensor) -> None:
+        """Read pages of ``base`` (a device buffer) with the library's read-only probe:
+        ``page_ids`` (device int32, each < base bytes / page_bytes) or every page in
+        address order; ``sink`` (device uint8/int32) receives one word per lane. For
+        the benchmark's bandwidth ceiling; enqueued on the current stream."""
+        nbytes = base.numel() * base.element_size()
+        num_pages = page_ids.numel() if page_ids is not None else nbytes // page_bytes
+        if page_ids is not None and (page_ids.dtype != torch.int32 or not page_ids.is_contiguous()):
+            raise RuntimeError("read_probe: page_ids must be contiguous int32")
+        self._check(self.lib.mvllm_read_probe(
+            base.data_ptr(), nbytes, _ptr(page_ids), num_pages, page_bytes, workgroups,
+            sink.data_ptr(), sink.numel() * sink.element_size() // 4, _stream(base.device)))
 
     def split_stats(self) -> dict[str, int]:
         """The split prefill grid's counter regions in use on the current device, and the

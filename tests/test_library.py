@@ -212,3 +212,14 @@ def test_load_extension_refuses_without_a_gpu():
         pytest.skip("a GPU is visible")
     with pytest.raises(extension.ToolchainError, match="no GPU"):
         extension.load_extension()
+
+
+def test_read_probe_refusals(lib):
+    """The bandwidth probe checks its sizes before any launch."""
+    assert lib.mvllm_read_probe(None, 1 << 20, None, 4, 32768, 8, 256, 2048, None) == 1
+    assert lib.mvllm_read_probe(256, 1 << 20, None, 4, 3000, 8, 256, 2048, None) == 2
+    assert "page_bytes" in lib.mvllm_last_error().decode()
+    assert lib.mvllm_read_probe(256, 1 << 16, None, 4, 32768, 8, 256, 2048, None) == 1
+    assert "fewer pages" in lib.mvllm_last_error().decode()
+    assert lib.mvllm_read_probe(256, 1 << 20, None, 4, 32768, 8, 256, 100, None) == 1
+    assert "sink" in lib.mvllm_last_error().decode()
