@@ -78,9 +78,12 @@ __host__ __device__ inline int prefill_item_tiles(int context, int len, int q) {
 // Stream decode: the workgroups that take a share. Shares of at least
 // kMinDecodeShareKeys keys: with few decode keys (a prefill step carrying a handful of
 // decode rows) equal shares over every CU would cut each sequence into dozens of
-// pieces, whose merge then costs more than the keys. Shared by the decode kernel and
-// its merge.
-constexpr int64_t kMinDecodeShareKeys = 128;
+// pieces, whose merge then costs more than the keys. (64 since the merge folds a
+// sequence's pieces in several workgroups and thread groups at once; measured
+// graph-replayed: one 8192-key sequence 23.8 -> 21.0 us, 16 x 1024 keys 25.4 -> 20.6 us
+// against 128, 32 no better; full batches, whose shares are larger, unchanged.) Shared
+// by the decode kernel and its merge.
+constexpr int64_t kMinDecodeShareKeys = 64;
 __host__ __device__ inline int64_t decode_stream_shares(int64_t total_keys, int64_t wgs) {
   const int64_t cap = (total_keys + kMinDecodeShareKeys - 1) / kMinDecodeShareKeys;
   return cap < 1 ? 1 : (cap < wgs ? cap : wgs);

@@ -381,49 +381,66 @@ __global__ __launch_bounds__(512) void paged_decode_stream_kernel(const PagedPar
   }
 }
 
-// Combine the pieces of every decode sequence cut between stream workgroups: one
-// workgroup per sequence, one float4 column of its H_q x D output per thread, the
-// pieces merged online (running max, rescaled sums) so their loads are in flight
-// together. Piece i of sequence s lives in slot (first + i + s), first/last being the
-// workgroups owning the sequence's first and last key.
+// Combine the pieces of every decode sequence cut between stream workgroups. Piece i
+// of sequence s lives in slot (first + i + s), first/last being the workgroups owning
+// the sequence's first and last key. Grid (sequence, block of kMergeCols float4
+// columns of its H_q x D output); in a workgroup, kMergeGroups groups of threads take
+// the pieces round robin (group g: pieces g, g + G, ...), each thread folding its
+// pieces for one float4 column online (running max, rescaled sums) with kMergeBatch
+// pieces' loads in flight at once; the groups' states then meet in LDS and are folded
+// in group order. A long sequence cut into dozens of pieces so costs a few round trips
+// instead of one per eight pieces, and a batch's sequences spread over H_q D / 4 /
+// kMergeCols workgroups each instead of one. The fold order depends on the piece count
+// alone, so a call's result does not depend on timing.
+constexpr int kMergeCols = 128;
+constexpr int kMergeGroups = 4;
+constexpr int kMergeBatch = 8;
+
 template <typename TQ, int D>
-__global__ __launch_bounds__(1024) void paged_decode_stream_merge_kernel(const PagedParams p,
-                                                                         int wgs_i) {
-  constexpr int kBatch = 8;  // pieces whose loads are issued together
+__global__ __launch_bounds__(kMergeCols * kMergeGroups) void paged_decode_stream_merge_kernel(
+    const PagedParams p, int wgs_i) {
+  __shared__ float s_m[kMergeGroups][kMergeCols];
+  __shared__ float s_l[kMergeGroups][kMergeCols];
+  __shared__ f32x4 s_o[kMergeGroups][kMergeCols];
   const int seq = blockIdx.x;
   const int64_t total = p.seq_prefix[p.num_seqs];
   const int64_t wgs = decode_stream_shares(total, wgs_i);
   const int64_t begin = p.seq_prefix[seq];
   const int64_t end = p.seq_prefix[seq + 1];
-  if (end == begin || total == 0) return;
+  if (end == begin || total == 0) return;  // whole workgroup: no barrier follows for it
   const int64_t first = share_owner(begin, total, wgs);
   const int64_t last = share_owner(end - 1, total, wgs);
   if (first == last) return;  // one piece: the decode kernel stored the output
   const bool all_live = total >= wgs;
   const int pieces = static_cast<int>(last - first + 1);
   const int n4 = p.hq * D / 4;
-  const int row = p.cu_seqlens_q[seq];
-  for (int j = threadIdx.x; j < n4; j += blockDim.x) {
-    const int head = (4 * j) / D;
-    const int d = 4 * j - head * D;
-    float m = -INFINITY, l = 0.0f;
-    f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int i0 = 0; i0 < pieces; i0 += kBatch) {
-      float mi[kBatch], li[kBatch];
-      f32x4 oi[kBatch];
+  const int local = threadIdx.x % kMergeCols;
+  const int grp = threadIdx.x / kMergeCols;
+  const int j = blockIdx.y * kMergeCols + local;
+  const bool live = j < n4;
+  const int head = live ? (4 * j) / D : 0;
+  const int d = live ? 4 * j - head * D : 0;
+
+  float m = -INFINITY, l = 0.0f;
+  f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (live) {
+    for (int i0 = grp; i0 < pieces; i0 += kMergeGroups * kMergeBatch) {
+      float mi[kMergeBatch], li[kMergeBatch];
+      f32x4 oi[kMergeBatch];
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        const int i = min(i0 + u, pieces - 1);
+      for (int u = 0; u < kMergeBatch; ++u) {
+        const int i = min(i0 + u * kMergeGroups, pieces - 1);
         const int64_t pidx = (first + i + seq) * p.hq + head;
         mi[u] = p.part_ml[pidx * 2];
         li[u] = p.part_ml[pidx * 2 + 1];
         oi[u] = *reinterpret_cast<const f32x4*>(p.part_o + pidx * D + d);
       }
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
+      for (int u = 0; u < kMergeBatch; ++u) {
+        const int i = i0 + u * kMergeGroups;
         // Beyond the last piece, or a workgroup whose share was empty (fewer keys
         // than workgroups): it wrote nothing and contributes nothing.
-        if (i0 + u >= pieces || !(all_live || share_nonempty(first + i0 + u, total, wgs))) continue;
+        if (i >= pieces || !(all_live || share_nonempty(first + i, total, wgs))) continue;
         const float mn = fmaxf(m, mi[u]);
         const float mu = mn == -INFINITY ? 0.0f : mn;
         const float a = fast_exp2(m - mu);
@@ -433,11 +450,31 @@ __global__ __launch_bounds__(1024) void paged_decode_stream_merge_kernel(const P
         m = mn;
       }
     }
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    const int64_t obase = (static_cast<int64_t>(row) * p.hq + head) * D + d;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) Elem<TQ>::store(p.out, obase + k, o[k] * inv);
   }
+  s_m[grp][local] = m;
+  s_l[grp][local] = l;
+  s_o[grp][local] = o;
+  __syncthreads();
+  if (grp != 0 || !live) return;
+  m = -INFINITY;
+  l = 0.0f;
+  o = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int g = 0; g < kMergeGroups; ++g) {
+    const float mg = s_m[g][local];
+    const float mn = fmaxf(m, mg);
+    const float mu = mn == -INFINITY ? 0.0f : mn;
+    const float a = fast_exp2(m - mu);
+    const float b = fast_exp2(mg - mu);
+    l = l * a + s_l[g][local] * b;
+    o = o * a + s_o[g][local] * b;
+    m = mn;
+  }
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  const int row = p.cu_seqlens_q[seq];
+  const int64_t obase = (static_cast<int64_t>(row) * p.hq + head) * D + d;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) Elem<TQ>::store(p.out, obase + k, o[k] * inv);
 }
 
 // -------------------------------------------------------------- grid schedule
@@ -564,8 +601,9 @@ hipError_t launch_decode_g(const PagedParams& p, hipStream_t stream) {
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     const int n4 = p.hq * D / 4;
-    const int threads = n4 >= 1024 ? 1024 : (n4 + kWave - 1) / kWave * kWave;
-    paged_decode_stream_merge_kernel<TQ, D><<<p.num_seqs, threads, 0, stream>>>(p, p.stream_wgs);
+    const dim3 mgrid(p.num_seqs, (n4 + kMergeCols - 1) / kMergeCols);
+    paged_decode_stream_merge_kernel<TQ, D>
+        <<<mgrid, kMergeCols * kMergeGroups, 0, stream>>>(p, p.stream_wgs);
     return hipGetLastError();
   }
   const dim3 grid(p.max_splits, p.by_row ? p.num_tokens : p.num_seqs, (units + waves - 1) / waves);
