@@ -1477,7 +1477,7 @@ __global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedPara
     const int64_t qrow = static_cast<int64_t>(row_base + local) * p.hq + head0;
     const char* qp = static_cast<const char*>(p.q) + (qrow * D + 8 * hsel) * 2;
 #pragma unroll
-    for (int ks = 0; ks < kKSteps; ++ks) qop[ks] = load16(qp + ks * 32);
+    for (int ks = 0; ks < kKSteps; ++ks) qop[ks] = load16_untracked(qp + ks * 32);
   }
   f32x16 o[kDBlocks];
 #pragma unroll
@@ -1635,7 +1635,15 @@ __global__ __launch_bounds__(512) void paged_prefill_pipe_kernel(const PagedPara
   stage(tb + 1, page_of(tb + 1), I1{});
   stage(tb + 2, page_of(tb + 2), I2{});
   int pg[3] = {page_of(tb + 3), page_of(tb + 4), page_of(tb + 5)};  // pg[x]: next tile staged into slot x
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kStageOps) : "memory");
+  // The queries (the oldest loads) and tile tb have landed. The wait names the query
+  // registers: their loads are untracked, and a wait the compiler placed itself would
+  // sit in the tile loop (the first scores are conditional), draining every step's
+  // fresh copies.
+  asm volatile("s_waitcnt vmcnt(%8)"
+               : "+v"(qop[0]), "+v"(qop[1]), "+v"(qop[2]), "+v"(qop[3]), "+v"(qop[4]),
+                 "+v"(qop[5]), "+v"(qop[6]), "+v"(qop[7])
+               : "n"(2 * kStageOps)
+               : "memory");
   if constexpr (kFp8) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // tile 0's scales
     convert_k(I0{}, I0{});
