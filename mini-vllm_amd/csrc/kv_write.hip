@@ -25,8 +25,11 @@
 // (oracle/kv_write.py) reproduces the bytes exactly; since scales are powers of two the
 // kernel divides by multiplying with the exact reciprocal, which gives the same results.
 
+#include <algorithm>
+
 #include "common.hpp"
 #include "kv_write.hpp"
+#include "paged_attention.hpp"
 
 namespace mvllm {
 
@@ -240,9 +243,15 @@ __global__ __launch_bounds__(256) void kv_write_fp8_kernel(uint8_t* __restrict__
                                                            int num_tokens, int hk, int block_shift,
                                                            int64_t num_blocks, int tokens_per_wg) {
   // Token t starts a run when its slot is in the pool and does not continue the slot of
-  // token t - 1 on the same page.
+  // token t - 1 on the same page. Workgroups go to the XCDs round robin; with the grid a
+  // multiple of 8, XCD x takes the x-th eighth of the token windows (window = (bid % 8)
+  // * grid / 8 + bid / 8), so the slot lines one L2 serves are its own (measured, 2048
+  // tokens of 16-token pages: 14.6 -> 9.7 us).
   const int lane = threadIdx.x % kWave;
-  const int t = static_cast<int>(blockIdx.x) * tokens_per_wg + lane;
+  const int nwin = static_cast<int>(gridDim.x);
+  const int bid = static_cast<int>(blockIdx.x);
+  const int win = nwin % kXcds == 0 ? (bid % kXcds) * (nwin / kXcds) + bid / kXcds : bid;
+  const int t = win * tokens_per_wg + lane;
   bool start = false;
   if (lane < tokens_per_wg && t < num_tokens) {
     const int slot = slots[t];
@@ -256,7 +265,7 @@ __global__ __launch_bounds__(256) void kv_write_fp8_kernel(uint8_t* __restrict__
   }
   uint64_t starts = __builtin_amdgcn_ballot_w64(start);
   while (starts != 0) {
-    const int t0 = static_cast<int>(blockIdx.x) * tokens_per_wg + __builtin_ctzll(starts);
+    const int t0 = win * tokens_per_wg + __builtin_ctzll(starts);
     starts &= starts - 1;
     kv_write_fp8_run<TS, D>(k_pool, v_pool, k_scales, v_scales, key, value, slots, num_tokens,
                             hk, block_shift, t0);
@@ -269,8 +278,14 @@ hipError_t launch_fp8_t(void* k_pool, void* v_pool, float* k_scales, float* v_sc
                         int hk, int head_dim, int block_shift, int64_t num_blocks,
                         hipStream_t stream) {
   if (num_tokens <= 0) return hipSuccess;
-  // tokens per workgroup: about 1024 workgroups, 1 to 64 tokens each
-  const int tpw = num_tokens >= 64 * 1024 ? 64 : (num_tokens >= 2048 ? num_tokens / 1024 : 1);
+  // Tokens per workgroup: one below 2048 tokens (a decode step's rows are runs of one,
+  // each workgroup writes one); from 2048 (prefill chunks: runs of a page each) about
+  // 256 workgroups of up to 16 tokens, so that few workgroups are launched only to find
+  // no run start. Launched workgroups cost time even when idle (measured, 2048 tokens
+  // of 16-token pages: 1024 workgroups 9.7 us, 256 of 8 tokens 6.1 us; 8192 tokens 12.2
+  // -> 10.5 us; 65536 tokens 86.8 -> 82.7 us); runs of one then cost a workgroup up to
+  // 16 in turn (2048 decode rows: 16.6 -> 29.3 us).
+  const int tpw = num_tokens >= 2048 ? std::min(16, num_tokens / 256) : 1;
   const unsigned grid = static_cast<unsigned>((num_tokens + tpw - 1) / tpw);
   // threads per workgroup: the 2 * hk * D / 8 tasks, in whole waves, at most 256
   auto threads = [hk](int dim) {

@@ -115,10 +115,12 @@ def _large_fp8_call(rng, nb, bs, t):
     return np.array(hist, np.int32), np.array(slots, np.int32)
 
 
-@pytest.mark.parametrize("t", [3000, 70000])
+@pytest.mark.parametrize("t", [2048, 3000, 4096, 70000])
 def test_fp8_write_large_calls_match_the_oracle_bytes(extension, device, t):
-    """Calls large enough that a workgroup takes several tokens (2 at 3000, 64 at 70000):
-    runs start anywhere in a workgroup's tokens and cross into the next one's, pages are
+    """Calls large enough that a workgroup takes several tokens (8 at 2048, 11 at 3000,
+    16 at 4096 and 70000; at 2048 and 4096 the grid is a multiple of 8 and the windows go
+    to the XCDs in eighths): runs start anywhere in a workgroup's tokens and cross into
+    the next one's, pages are
     continued mid-way under a grown or kept scale, decode-like single tokens sit among
     long chunks; bytes and scales equal the oracle's. The same call with padding slots
     replaced by slots past the pool leaves the same pool."""
