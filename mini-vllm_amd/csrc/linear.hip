@@ -22,8 +22,8 @@
 //    each), one per wave; a wave issues every load of its range before its first MFMA,
 //    so a projection's weights are requested up front. K <= 1024 (T = 4): one workgroup
 //    of 4 waves per tile of 32 output columns, the waves' 32 x 32 partial sums meeting in
-//    LDS, the epilogue in the same launch. K > 1024: T / 4 workgroups per tile (the
-//    N = 1024 projections of a decode step would otherwise run on 32 CUs), each wave
+//    LDS, the epilogue in the same launch. K > 1024: T one-wave workgroups per tile (the
+//    N = 1024 projections of a decode step would otherwise run on 32 CUs), each
 //    writing its fp32 partial tile to a workspace, and a second launch adds the T
 //    partials and runs the epilogue - a kernel boundary, because a reduction inside one
 //    launch needs device-scope release/acquire fences, which write back and invalidate
@@ -57,6 +57,7 @@
 //    the unfused pair); one wave (workgroup) per row.
 
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 #include "linear.hpp"
@@ -247,22 +248,25 @@ __global__ __launch_bounds__(kGroup * kWave) void skinny_linear_kernel(
   epilogue<T, MB, EPI>(out, blockIdx.x, m, n, total);
 }
 
-// K > 1024: wave g = 4 blockIdx.y + wave of the T writes its fp32 partial tile to
-// partials[tile][g][x row][col] (MB * 32 x rows).
+// K > 1024: wave g = blockIdx.y of the T writes its fp32 partial tile to
+// partials[tile][g][x row][col] (MB * 32 x rows). The waves share nothing, so each is a
+// workgroup of its own: the weights are then requested from as many CUs as there are
+// waves (256 and 384 for the o and down projections of a decode step), and a CU pulls
+// only so many bytes per microsecond (one-wave workgroups against four: 7.7 -> 7.0 us
+// for the o projection with its reduction, 8.6 -> 8.2 for down).
 template <typename T, int MB>
-__global__ __launch_bounds__(kGroup * kWave) void skinny_partial_kernel(
+__global__ __launch_bounds__(kWave) void skinny_partial_kernel(
     float* __restrict__ partials, const void* __restrict__ x, const void* __restrict__ w, int m,
     int k, int total_waves) {
   constexpr int kSlice = MB * 32 * kRowBytes;
-  __shared__ __attribute__((aligned(1024))) char lds[kGroup * kSlice];
+  __shared__ __attribute__((aligned(1024))) char lds[kSlice];
   const int lane = threadIdx.x % kWave;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int l32 = lane & 31;
   const int hsel = lane >> 5;
-  const int g = blockIdx.y * kGroup + wave;
+  const int g = blockIdx.y;
   f32x16 acc[MB];
-  wave_tile<T, MB>(acc, static_cast<const char*>(x), static_cast<const char*>(w),
-                   lds + wave * kSlice, m, k, blockIdx.x, g, total_waves);
+  wave_tile<T, MB>(acc, static_cast<const char*>(x), static_cast<const char*>(w), lds, m, k,
+                   blockIdx.x, g, total_waves);
   float* dst = partials + (static_cast<int64_t>(blockIdx.x) * total_waves + g) * (MB * 32 * kColTile);
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
@@ -320,14 +324,15 @@ __global__ __launch_bounds__(kGroup * kWave) void skinny_reduce_kernel(
 // K > 1024, residual + RMSNorm: one wave (workgroup) per x row, lane r holding 8-column
 // chunks r, r + 64, ... (the lane map of rmsnorm_vec_kernel<T, 64, kCh>): h = T(r +
 // T(sum)), then out = T(T(h * inv) * weight) with inv from the lane-ordered fma sum of
-// squares reduced by group_sum<64>, as that kernel computes it. All of a lane's partial
-// loads for kB waves at a time go out together (kCh x 2 x kB float4s).
-template <typename T, int MB, int kCh>
+// squares reduced by group_sum<64>, as that kernel computes it. The residual and weight
+// chunks, which do not depend on the partials, are requested first; then all of a
+// lane's partial loads for kB waves at a time go out together (kCh x 2 x kB float4s; kB
+// divides T), so the kernel waits on one memory round trip instead of three.
+template <typename T, int MB, int kCh, int kB>
 __global__ __launch_bounds__(kWave) void skinny_reduce_norm_kernel(
     void* __restrict__ h_out, void* __restrict__ normed, const float* __restrict__ partials,
     const void* __restrict__ residual, const void* __restrict__ norm_weight, int m, int n,
     int total_waves, float eps) {
-  constexpr int kB = 32 / kCh;
   constexpr int64_t kTile = MB * 32 * kColTile;
   const int row = blockIdx.x;
   const int r = threadIdx.x;
@@ -336,11 +341,16 @@ __global__ __launch_bounds__(kWave) void skinny_reduce_norm_kernel(
   const char* res = static_cast<const char*>(residual) + static_cast<int64_t>(row) * n * 2;
   char* hrow = static_cast<char*>(h_out) + static_cast<int64_t>(row) * n * 2;
 
+  const char* wr = static_cast<const char*>(norm_weight);
   const float* src[kCh];
+  u32x4 res_v[kCh], w_v[kCh];
 #pragma unroll
   for (int c = 0; c < kCh; ++c) {
-    const int col = min(r + c * kWave, chunks - 1) * 8;
+    const int chunk = min(r + c * kWave, chunks - 1);
+    const int col = chunk * 8;
     src[c] = partials + (col / kColTile) * tile_stride + row * kColTile + col % kColTile;
+    res_v[c] = load16(res + col * 2);
+    w_v[c] = load16(wr + chunk * 16);
   }
   f32x4 sum[kCh][2];
 #pragma unroll
@@ -349,23 +359,24 @@ __global__ __launch_bounds__(kWave) void skinny_reduce_norm_kernel(
     f32x4 v[kCh][2][kB];
 #pragma unroll
     for (int i = 0; i < kB; ++i) {
-      const int64_t off = static_cast<int64_t>(min(g0 + i, total_waves - 1)) * kTile;
+      const int64_t off = static_cast<int64_t>(g0 + i) * kTile;
 #pragma unroll
       for (int c = 0; c < kCh; ++c) {
         v[c][0][i] = *reinterpret_cast<const f32x4*>(src[c] + off);
         v[c][1][i] = *reinterpret_cast<const f32x4*>(src[c] + off + 4);
       }
     }
+    // Every load of the round is issued before the first addition (left to itself the
+    // scheduler interleaves them, one round trip per wave's partial).
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < kB; ++i) {
-      if (g0 + i < total_waves) {
 #pragma unroll
-        for (int c = 0; c < kCh; ++c) {
+      for (int c = 0; c < kCh; ++c) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            sum[c][0][e] = sum[c][0][e] + v[c][0][i][e];
-            sum[c][1][e] = sum[c][1][e] + v[c][1][i][e];
-          }
+        for (int e = 0; e < 4; ++e) {
+          sum[c][0][e] = sum[c][0][e] + v[c][0][i][e];
+          sum[c][1][e] = sum[c][1][e] + v[c][1][i][e];
         }
       }
     }
@@ -379,7 +390,7 @@ __global__ __launch_bounds__(kWave) void skinny_reduce_norm_kernel(
     if (chunk < chunks) {
       const int col = chunk * 8;
       float rf[8];
-      Chunk<T>::unpack(load16(res + col * 2), rf);
+      Chunk<T>::unpack(res_v[c], rf);
       float f[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) f[e] = Elem<T>::round(rf[e] + Elem<T>::round(sum[c][e / 4][e % 4]));
@@ -398,14 +409,13 @@ __global__ __launch_bounds__(kWave) void skinny_reduce_norm_kernel(
   sumsq = group_sum<kWave>(sumsq);
   const float inv = rsqrtf(sumsq / static_cast<float>(n) + eps);
   char* orow = static_cast<char*>(normed) + static_cast<int64_t>(row) * n * 2;
-  const char* wr = static_cast<const char*>(norm_weight);
 #pragma unroll
   for (int c = 0; c < kCh; ++c) {
     const int chunk = r + c * kWave;
     if (chunk < chunks) {
       float f[8], wf[8];
       Chunk<T>::unpack(held[c], f);
-      Chunk<T>::unpack(load16(wr + chunk * 16), wf);
+      Chunk<T>::unpack(w_v[c], wf);
       u32x4 res_v;
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
@@ -435,7 +445,7 @@ hipError_t launch_m(const Out& out, const void* x, const void* w, int m, int n, 
     return hipGetLastError();
   }
   float* partials = static_cast<float*>(workspace);
-  skinny_partial_kernel<T, MB><<<dim3(tiles, t_waves / kGroup), kGroup * kWave, 0, stream>>>(
+  skinny_partial_kernel<T, MB><<<dim3(tiles, t_waves), kWave, 0, stream>>>(
       partials, x, w, m, k, t_waves);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -466,36 +476,35 @@ hipError_t launch_norm_m(void* h_out, void* normed, const void* x, const void* w
   const unsigned tiles = static_cast<unsigned>((n + kColTile - 1) / kColTile);
   const int t_waves = waves_of(k);
   float* partials = static_cast<float*>(workspace);
-  skinny_partial_kernel<T, MB><<<dim3(tiles, t_waves / kGroup), kGroup * kWave, 0, stream>>>(
+  skinny_partial_kernel<T, MB><<<dim3(tiles, t_waves), kWave, 0, stream>>>(
       partials, x, w, m, k, t_waves);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const unsigned rows = static_cast<unsigned>(m);
   const int per_lane = n / 8 / kWave;
+  // kB: the most waves' partials a lane loads at once that divides T (a multiple of
+  // 4), at most 32 / kCh of them (kCh x 2 x kB float4s in registers).
+  auto run = [&](auto ch, auto b) {
+    skinny_reduce_norm_kernel<T, MB, decltype(ch)::value, decltype(b)::value><<<rows, kWave, 0, stream>>>(
+        h_out, normed, partials, residual, norm_weight, m, n, t_waves, eps);
+  };
+  using C2 = std::integral_constant<int, 2>;
+  using C4 = std::integral_constant<int, 4>;
+  using C8 = std::integral_constant<int, 8>;
+  using B4 = std::integral_constant<int, 4>;
+  using B8 = std::integral_constant<int, 8>;
+  using B12 = std::integral_constant<int, 12>;
+  using B16 = std::integral_constant<int, 16>;
   if (per_lane <= 2) {
-    skinny_reduce_norm_kernel<T, MB, 2><<<rows, kWave, 0, stream>>>(
-        h_out, normed, partials, residual, norm_weight, m, n, t_waves, eps);
+    if (t_waves % 16 == 0) run(C2{}, B16{});
+    else if (t_waves % 12 == 0) run(C2{}, B12{});
+    else if (t_waves % 8 == 0) run(C2{}, B8{});
+    else run(C2{}, B4{});
   } else if (per_lane <= 4) {
-    skinny_reduce_norm_kernel<T, MB, 4><<<rows, kWave, 0, stream>>>(
-        h_out, normed, partials, residual, norm_weight, m, n, t_waves, eps);
+    if (t_waves % 8 == 0) run(C4{}, B8{});
+    else run(C4{}, B4{});
   } else {
-    skinny_reduce_norm_kernel<T, MB, 8><<<rows, kWave, 0, stream>>>(
-        h_out, normed, partials, residual, norm_weight, m, n, t_waves, eps);
-  }
-  return hipGetLastError();
-}
-
-template <typename T, int kCh>
-hipError_t launch_reduce_norm(void* h_out, void* normed, const float* partials, const void* residual,
-                              const void* norm_weight, int m, int n, int total_waves, float eps,
-                              int mb, hipStream_t stream) {
-  const unsigned rows = static_cast<unsigned>(m);
-  if (mb == 1) {
-    skinny_reduce_norm_kernel<T, 1, kCh><<<rows, kWave, 0, stream>>>(
-        h_out, normed, partials, residual, norm_weight, m, n, total_waves, eps);
-  } else {
-    skinny_reduce_norm_kernel<T, 2, kCh><<<rows, kWave, 0, stream>>>(
-        h_out, normed, partials, residual, norm_weight, m, n, total_waves, eps);
+    run(C8{}, B4{});
   }
   return hipGetLastError();
 }

@@ -218,10 +218,13 @@ def test_swiglu_equals_gate_up_then_swiglu(extension, device, m, i, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("m,n,k", [(1, 1024, 2048), (32, 1024, 3072), (33, 1024, 2048),
-                                   (64, 2048, 1088), (7, 4096, 4096)])
+                                   (64, 2048, 1088), (7, 4096, 4096), (3, 1024, 5120),
+                                   (9, 2048, 3072), (2, 1024, 4096)])
 def test_residual_rmsnorm_equals_the_unfused_pair(extension, device, m, n, k, dtype):
     """(h, normed) of the fused launch pair, bitwise linear_residual then the RMSNorm
-    kernel (random norm weight, eps 1e-6)."""
+    kernel (random norm weight, eps 1e-6). The K values give 8, 12, 16 and 20 split
+    waves, so every batch of partial loads (4, 8, 12 or 16 waves at a time, one round
+    or several) is run."""
     x, w, gen = _operands(m, n, k, dtype, 41 + m + k)
     r = torch.randn(m, n, generator=gen).to(dtype).cuda()
     nw = (torch.rand(n, generator=gen) + 0.5).to(dtype).cuda()
@@ -248,3 +251,4 @@ def test_residual_rmsnorm_refuses_what_it_does_not_serve(extension, device):
     pw = ops.pack_weight(w, use_cuda=True)
     r = torch.randn(4, 1000, generator=gen).to(torch.bfloat16).cuda()
     assert ops.linear_residual_rmsnorm(x, pw, r, nw[:1000], use_cuda=True) is None
+
