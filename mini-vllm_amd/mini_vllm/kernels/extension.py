@@ -1020,15 +1020,21 @@ class HipExtension:
         )
         return out
 
-    def argmax(self, logits: torch.Tensor) -> torch.Tensor:
+    def argmax(self, logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         """``logits.argmax(dim=-1)`` (int64) for a 2-D f32/f16/bf16 device tensor whose
-        rows are contiguous: torch's order (NaN highest, -0 == +0, first index wins)."""
+        rows are contiguous: torch's order (NaN highest, -0 == +0, first index wins).
+        ``out``: a contiguous int64 [rows] device tensor to write (default: a new one)."""
         if not logits.is_cuda or logits.dim() != 2 or logits.stride(1) != 1:
             raise RuntimeError("argmax: expected a 2-D CUDA tensor with contiguous rows, got "
                                f"{tuple(logits.shape)} strides {logits.stride()}")
         if logits.dtype not in (torch.float32, torch.float16, torch.bfloat16):
             raise RuntimeError(f"argmax: dtype {logits.dtype} is not served (f32, f16, bf16)")
-        out = torch.empty(logits.shape[0], dtype=torch.int64, device=logits.device)
+        if out is None:
+            out = torch.empty(logits.shape[0], dtype=torch.int64, device=logits.device)
+        elif (out.dtype != torch.int64 or out.shape != (logits.shape[0],) or not out.is_contiguous()
+              or out.device != logits.device):
+            raise RuntimeError(f"argmax: out must be a contiguous int64 [{logits.shape[0]}] tensor "
+                               "on the logits' device")
         if logits.shape[0] == 0:
             return out
         rows, vocab = logits.shape

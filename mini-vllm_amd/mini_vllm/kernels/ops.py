@@ -288,14 +288,19 @@ def swiglu(gate: torch.Tensor, up: torch.Tensor, use_cuda: bool = False) -> torc
     return torch_path.silu(gate) * up
 
 
-def argmax(logits: torch.Tensor, use_cuda: bool = False) -> torch.Tensor:
+def argmax(logits: torch.Tensor, use_cuda: bool = False,
+           out: torch.Tensor | None = None) -> torch.Tensor:
     """Greedy sampling, ``logits.argmax(dim=-1)`` over ``B x V`` logits (reference
     sampler.py:135-141). Kernel: ``csrc/sampler.hip`` (one pass over each row, torch's
-    tie and NaN order); other shapes and dtypes take torch's reduction."""
+    tie and NaN order); other shapes and dtypes take torch's reduction. ``out`` (int64
+    [B]): written in place and returned."""
     if (_use_kernel("argmax", use_cuda, logits) and logits.dim() == 2 and logits.shape[1] > 0
-            and logits.stride(1) == 1 and logits.dtype in (torch.float32, torch.float16, torch.bfloat16)):
-        return load_extension().argmax(logits)
-    return logits.argmax(dim=-1)
+            and logits.stride(1) == 1 and logits.dtype in (torch.float32, torch.float16, torch.bfloat16)
+            and (out is None or (out.is_contiguous() and out.dtype == torch.int64))):
+        return load_extension().argmax(logits, out)
+    if out is None:
+        return logits.argmax(dim=-1)
+    return torch.argmax(logits, dim=-1, out=out)
 
 
 @dataclass(frozen=True)

@@ -13,12 +13,16 @@ fixed, so one captured graph serves every decode step of a given shape:
   the block-table width is rounded up to a multiple of 64 pages;
 * before a replay, the iteration's metadata is packed into one pinned host buffer and
   copied into the graph's static input tensors with one host-to-device copy;
-* sampling (argmax) runs after the replay, outside the graph; :meth:`DecodeGraphs.keep`
-  stores the sampled tokens in a device buffer every graph reads, and a sequence whose
-  token from the previous iteration was committed takes its next input token from there
-  (the graph gathers it by the row the sequence had), so the host need not have read
-  that token yet: the engine schedules and packs the next decode step while the GPU
-  runs this one.
+* sampling (argmax) runs after the replay, outside the graph, and writes the sampled
+  tokens straight into a device buffer every graph reads (:attr:`DecodeGraphs.prev_tokens`;
+  :meth:`DecodeGraphs.keep` records which rows were committed); a sequence whose token
+  from the previous iteration was committed takes its next input token from there, so
+  the host need not have read that token yet: the engine schedules and packs the next
+  decode step while the GPU runs this one. That buffer is the head of one int64 device
+  buffer that also holds the host's ids, the gather indices and the positions of the
+  replay (``[prev tokens | ids | gather | positions]``, the last three sized by the
+  batch), so a replay's input ids are one ``index_select`` over it: row i takes element
+  ``gather[i]``, its row of the previous replay or its own host id.
 
 The paged-attention plan in stream mode depends only on the batch size and the bound on
 max_context_len, so the kernels launched inside a graph stay valid for every replay;
@@ -39,25 +43,27 @@ TABLE_QUANTUM = 64  # pages
 
 class _Captured:
     def __init__(self, model, batch_size: int, width: int, dummy_block: int, device,
-                 prev_tokens: torch.Tensor) -> None:
+                 tokens: torch.Tensor, head: int) -> None:
         p = model.manager.block_size
         self.batch_size, self.width = batch_size, width
         b = batch_size
         i32 = dict(dtype=torch.int32, device=device)
         i64 = dict(dtype=torch.int64, device=device)
-        # Dynamic inputs: [ids | positions | gather rows] int64 and [context | slots |
-        # tables] int32. Row i's input token is prev_tokens[gather[i]] when gather[i] >= 0
-        # (the token sampled for it by the previous replay, still on the device), else
-        # ids[i] from the host.
-        self.dyn64 = torch.zeros(3 * b, **i64)
+        # Dynamic inputs: [ids | gather | positions] int64 (in `tokens`, after its `head`
+        # elements of previous tokens) and [context | slots | tables] int32. Row i's input
+        # token is tokens[gather[i]]: the token sampled for it by the previous replay (an
+        # index below `head`, still on the device) or its id from the host (head + i).
+        self.dyn64 = tokens[head:head + 3 * b]
+        self.gather = self.dyn64[b:2 * b]
+        self.tokens = tokens
+        self.head = head
         self.dyn32 = torch.zeros(2 * b + b * width, **i32)
         self.host64 = torch.zeros(3 * b, dtype=torch.int64, pin_memory=True)
         self.host32 = torch.zeros(2 * b + b * width, dtype=torch.int32, pin_memory=True)
-        self.prev_tokens = prev_tokens
         self.input_ids = torch.zeros(b, **i64)
         self.batch = ForwardBatch(
             input_ids=self.input_ids,
-            positions=self.dyn64[b:2 * b],
+            positions=self.dyn64[2 * b:3 * b],
             cu_seqlens_q=torch.arange(b + 1, **i32),
             seq_lens=torch.ones(b, **i32),
             context_lens=self.dyn32[:b],
@@ -83,14 +89,15 @@ class _Captured:
     def fill(self, scheduled, gather: list[int] | None = None) -> None:
         b, w, p = self.batch_size, self.width, self.model.manager.block_size
         manager = self.model.manager
-        ids, pos, rows = self.np64[:b], self.np64[b:2 * b], self.np64[2 * b:]
+        ids, rows, pos = self.np64[:b], self.np64[b:2 * b], self.np64[2 * b:]
         ctx, slots = self.np32[:b], self.np32[b:2 * b]
         tables = self.np32[2 * b:].reshape(b, w)
         for i, (seq, _) in enumerate(scheduled):
             start = seq.num_computed_tokens
-            rows[i] = gather[i] if gather is not None else -1
+            g = gather[i] if gather is not None else -1
             # a gathered row's token may not have reached the host yet
-            ids[i] = seq.tokens(start, 1)[0] if rows[i] < 0 else 0
+            rows[i] = g if g >= 0 else self.head + i
+            ids[i] = seq.tokens(start, 1)[0] if g < 0 else 0
             pos[i] = start
             ctx[i] = start + 1
             table = manager.table(seq.seq_id)
@@ -101,7 +108,7 @@ class _Captured:
                 tables[i, len(table):] = PADDING_BLOCK
                 self.row_keys[i] = key
         for i in range(len(scheduled), b):
-            rows[i] = -1
+            rows[i] = self.head + i
             if self.row_keys[i] is not None:
                 ids[i], pos[i], ctx[i], slots[i] = 0, 0, 1, self.dummy_block * p
                 tables[i, 0] = self.dummy_block
@@ -111,10 +118,7 @@ class _Captured:
         self.dyn32.copy_(self.host32, non_blocking=True)
 
     def _gather_inputs(self) -> None:
-        b = self.batch_size
-        host_ids, rows = self.dyn64[:b], self.dyn64[2 * b:]
-        prev = self.prev_tokens.index_select(0, rows.clamp(min=0))
-        self.input_ids.copy_(torch.where(rows >= 0, prev, host_ids))
+        torch.index_select(self.tokens, 0, self.gather, out=self.input_ids)
 
     def _forward(self) -> torch.Tensor:
         self._gather_inputs()
@@ -168,9 +172,13 @@ class DecodeGraphs:
         self.dummy_block = manager.table(self._dummy_id)[0]
         self.graphs: dict[tuple[int, int], _Captured] = {}
         self.replays = 0
-        # Tokens sampled by the last replay (row i: sequence prev_rows' key with value i),
-        # read by the next replay's gather.
-        self.prev_tokens = torch.zeros(max(BUCKETS), dtype=torch.int64, device=self.device)
+        # [tokens sampled by the last replay | the replay's ids, gather rows, positions]:
+        # row i of the head is the token of sequence prev_rows' key with value i, read by
+        # the next replay's gather.
+        head = max(BUCKETS)
+        self._tokens = torch.zeros(4 * head, dtype=torch.int64, device=self.device)
+        self._head = head
+        self.prev_tokens = self._tokens[:head]
         self.prev_rows: dict[int, int] = {}
 
     def supports(self, scheduled) -> bool:
@@ -189,7 +197,7 @@ class DecodeGraphs:
         entry = self.graphs.get(key)
         if entry is None:
             entry = _Captured(self.model, bucket, width, self.dummy_block, self.device,
-                              self.prev_tokens)
+                              self._tokens, self._head)
             entry.fill(scheduled, gather)
             entry.capture()
             self.graphs[key] = entry
@@ -204,8 +212,11 @@ class DecodeGraphs:
         gathers its inputs from those rows only. A row whose token was discarded (a
         prompt chunk that did not reach the prompt's end, or a recompute chunk short of
         the sequence's end) is not kept: that sequence's next input is a token the host
-        already has."""
-        self.prev_tokens[: len(scheduled)].copy_(tokens)
+        already has. ``tokens`` may already be the head of :attr:`prev_tokens` (the
+        argmax wrote there): then nothing is copied."""
+        n = len(scheduled)
+        if tokens.data_ptr() != self.prev_tokens.data_ptr() or tokens.numel() != n:
+            self.prev_tokens[:n].copy_(tokens)
         self.prev_rows = {scheduled[i][0].seq_id: i for i in committed}
 
     def invalidate(self) -> None:

@@ -125,3 +125,19 @@ def test_device_draw_frequencies_follow_the_distribution(device):
     for t in range(6):
         se = math.sqrt(float(p[t]) * (1 - float(p[t])) / draws)
         assert abs(float(freq[t]) - float(p[t])) < 4 * se, f"token {t}"
+
+
+def test_writes_a_given_output(extension, device):
+    """``out``: the indices land in the caller's int64 tensor (a view into a larger
+    buffer, as the decode graphs pass), the rest of the buffer untouched; a wrong dtype
+    or length is refused."""
+    gen = torch.Generator().manual_seed(11)
+    logits = torch.randn(5, 151936, generator=gen).to(torch.bfloat16).cuda()
+    buf = torch.full((12,), -7, dtype=torch.int64, device="cuda")
+    got = ops.argmax(logits, use_cuda=True, out=buf[:5])
+    assert got.data_ptr() == buf.data_ptr()
+    assert torch.equal(buf[:5], logits.argmax(dim=-1)) and (buf[5:] == -7).all()
+    with pytest.raises(RuntimeError, match="int64"):
+        extension.argmax(logits, out=torch.empty(5, dtype=torch.int32, device="cuda"))
+    with pytest.raises(RuntimeError, match="int64"):
+        extension.argmax(logits, out=buf[:4])
