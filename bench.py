@@ -159,6 +159,58 @@ def run_engine(requests: int = 256, max_tokens: int = 256, max_sequences: int = 
     }
 
 
+def run_decode_step(steps: int = 40, warmup: int = 8, batch: int = 32, context: int = 1024) -> dict:
+    """One decode iteration of config 5's engine at a fixed shape: `batch` sequences whose
+    prompts (`context` random ids, seed 0) were prefilled by the engine, then `steps`
+    pure-decode iterations (the decode graphs, greedy, EOS ignored) timed back to back
+    with the host scheduling each next one while the GPU runs the current (what config 5
+    runs 92% of the time). Algorithmic bytes per step: every weight the forward reads
+    once (28 layers of q/k/v, o, gate/up, down; the LM head; norm weights) plus each
+    sequence's K and V over its context at that step, 2 bytes an element."""
+    from mini_vllm.block import BlockManager
+    from mini_vllm.model import ModelConfig, Qwen3Paged, random_weights
+    from mini_vllm.serve import LLMEngine, SchedulerConfig
+    from mini_vllm.workloads import CONFIG5_BUDGET, CONFIG5_CHUNK
+
+    config = ModelConfig()
+    weights = random_weights(config, seed=0, device="cuda")
+    gen = torch.Generator().manual_seed(0)
+    prompts = [torch.randint(0, config.vocab_size, (context,), generator=gen).tolist()
+               for _ in range(batch)]
+    total_tokens = context + warmup + steps + 4
+    blocks = batch * (-(-total_tokens // 16)) + 64
+    sched = SchedulerConfig(max_batched_tokens=CONFIG5_BUDGET, max_sequences=batch,
+                            chunk_size=CONFIG5_CHUNK)
+    manager = BlockManager(blocks, 16, config.num_hidden_layers, config.num_key_value_heads,
+                           config.head_dim, config.dtype, "cuda")
+    eng = LLMEngine(Qwen3Paged(config, weights, manager, use_cuda=True), sched, device="cuda",
+                    use_graphs=True)
+    seqs = [eng.add_request(p, warmup + steps + 4) for p in prompts]
+    while any(len(s.output) == 0 for s in seqs):  # prefill (and the first token)
+        eng.step()
+    for _ in range(warmup):
+        eng.step()
+    torch.cuda.synchronize()
+    ctx0 = min(len(s) for s in seqs)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        eng.step(resolve_finished=False)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    eng.flush()
+    c, layers = config, config.num_hidden_layers
+    per_layer = (c.q_size + 2 * c.kv_size) * c.hidden_size + c.hidden_size * c.q_size + \
+        2 * c.intermediate_size * c.hidden_size + c.hidden_size * c.intermediate_size
+    weight_bytes = 2 * (layers * per_layer + c.vocab_size * c.hidden_size)
+    mean_ctx = ctx0 + (steps - 1) / 2.0
+    kv_bytes = 2 * 2 * batch * mean_ctx * layers * c.num_key_value_heads * c.head_dim
+    gbs = (weight_bytes + kv_bytes) / (ms * 1e-3) / 1e9
+    return {"batch": batch, "context_at_start": ctx0, "steps": steps, "ms_per_step": round(ms, 4),
+            "output_tok_s": round(batch / (ms * 1e-3), 1),
+            "weight_bytes": int(weight_bytes), "kv_bytes_mean": int(kv_bytes),
+            "gbs": round(gbs, 1), "frac_of_hbm_peak": round(gbs / 8000.0, 4)}
+
+
 def run_prefill_occupancy(steps: int = 20, tiles: int = 16) -> dict:
     """Items of `tiles` 64-key tiles (128 queries after a prefix, bf16, GQA 16/8, D 128) on
     the item grid, as many as half the CUs and as all of them: the per-tile cost of one
@@ -758,11 +810,12 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--copies", type=int, default=3, help="rotated pool copies (defeat the MALL)")
     parser.add_argument("--skip-extras", action="store_true", help="headline config 2 only")
-    parser.add_argument("--extras", default="3,3fp8,4,5,ew,kv,dense,linear,gemm,ceiling,cases",
+    parser.add_argument("--extras", default="3,3fp8,4,5,step,ew,kv,dense,linear,gemm,ceiling,cases",
                         help="comma list of extras to run: 3 (prefill), 3fp8 (prefill over an "
                              "fp8 pool), 4 (fp8 decode), "
                              "5 (engine), 5small (engine, 64 x 128 tokens), 5fp8 (engine, fp8 "
-                             "KV cache), ew (elementwise "
+                             "KV cache), step (one config-5 decode iteration, 32 x 1024 "
+                             "tokens: ms, algorithmic bytes, fraction of HBM), ew (elementwise "
                              "kernels), kv (KV write), dense (dense-cache attention), linear "
                              "(decode projections and argmax), gemm (prefill projections on hipBLASLt), "
                              "ceiling (read-only HBM probe: sequential and shuffled 32 KB pages), "
@@ -861,6 +914,10 @@ def main() -> int:
         log("config 5: Qwen3-0.6B-shaped engine, 256 requests x 256 tokens")
         extras["config5_engine"] = run_engine()
         log(f"config 5 (decode graphs on): {extras['config5_engine']}")
+    if "step" in wanted:
+        extras["decode_step"] = run_decode_step()
+        log(f"decode step (32 sequences, 1024-token prompts): {extras['decode_step']}")
+        torch.cuda.empty_cache()
     if "pfocc" in wanted:
         extras["prefill_occupancy"] = run_prefill_occupancy()
         log(f"prefill occupancy: {extras['prefill_occupancy']}")
