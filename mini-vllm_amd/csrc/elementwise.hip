@@ -578,14 +578,18 @@ void launch_qk_norm_rope_r(const void* q, const void* k, const void* wq, const v
                            const KvSink& kv, TokenStrides ts, hipStream_t stream) {
   const int64_t rows = q_rows + k_rows + kv.v_rows;
   const int g = qk_rows_per_group(rows, KR, hq, hk);
-  const unsigned grid = static_cast<unsigned>((rows / g * KR + 255) / 256);
+  // A decode step's launch (a few thousand lanes) as one-wave workgroups, spread over
+  // four times the CUs (config 5 +0.3%); larger launches keep 256 threads.
+  const int64_t lanes = rows / g * KR;
+  const unsigned bs = lanes <= 65536 ? 64 : 256;
+  const unsigned grid = static_cast<unsigned>((lanes + bs - 1) / bs);
 #define MVLLM_QKNR(G)                                                                         \
   if (kv.k_pool != nullptr) {                                                                 \
-    qk_norm_rope_kernel<T, TPos, KR, G, true><<<grid, 256, 0, stream>>>(                      \
+    qk_norm_rope_kernel<T, TPos, KR, G, true><<<grid, bs, 0, stream>>>(                       \
         q, k, wq, wk, pos, cos_t, sin_t, q_out, k_out, q_rows, k_rows, hq, hk, num_positions, \
         max_positions, eps, kv, ts);                                                          \
   } else {                                                                                    \
-    qk_norm_rope_kernel<T, TPos, KR, G, false><<<grid, 256, 0, stream>>>(                     \
+    qk_norm_rope_kernel<T, TPos, KR, G, false><<<grid, bs, 0, stream>>>(                      \
         q, k, wq, wk, pos, cos_t, sin_t, q_out, k_out, q_rows, k_rows, hq, hk, num_positions, \
         max_positions, eps, kv, ts);                                                          \
   }
