@@ -269,6 +269,37 @@ int mvllm_qk_norm_rope_kv_write(void* q_out, void* key_pool, void* value_pool, c
  * views of the fused q/k/v projection's output pass its width, so the prefill path
  * needs no copies.) */
 
+/* A decode step's attention with its new token's QK-norm, RoPE and KV write in the same
+ * launch, for a decode-only batch (every sequence computes one token: seq_lens all 1,
+ * num_seqs rows) over a float16 or bfloat16 pool with head_dim 128. Sequence s's token
+ * sits at position context_lens[s] - 1 and goes to the slot its block table maps that
+ * position to. The result equals, bit for bit, mvllm_qk_norm_rope_kv_write (positions
+ * context_lens - 1, slot_mapping from the block tables) followed by
+ * mvllm_paged_attention over the rotated q: the decode kernel forms the rotated q and
+ * k rows itself (the same arithmetic), writes k and v to the pool, and takes the new
+ * token's rows from registers, one launch fewer per layer. Replaces, for decode steps,
+ * the reference Qwen3PagedAttention's norm/rope, PagedKvPool.write and
+ * ops.paged_attention calls (model/qwen3_paged.py:71-95); no counterpart in
+ * mini_vllm_C.
+ *   out [num_seqs, num_q_heads, 128]; q (raw, before QK-norm) [num_seqs, num_q_heads,
+ *   128] and k, v [num_seqs, num_kv_heads, 128] with token strides as for
+ *   mvllm_qk_norm_rope_kv_write; q_weight, k_weight [128]; cos_table, sin_table
+ *   [max_positions, 128] float32; the pools, tables and metadata as for
+ *   mvllm_paged_attention (a table entry outside [0, num_blocks) writes nothing).
+ * The workspace is the one mvllm_paged_attention_plan gives for num_tokens = num_seqs,
+ * max_query_len = 1 and these options. A plan on the grid schedule (options, or more
+ * than 4096 sequences) returns MVLLM_ERR_UNSUPPORTED: the caller then makes the two
+ * calls. */
+int mvllm_paged_decode_qk_norm_rope(
+    void* out, const void* q, const void* k, const void* v, int64_t q_token_stride,
+    int64_t kv_token_stride, const void* q_weight, const void* k_weight, const float* cos_table,
+    const float* sin_table, int64_t max_positions, float eps, void* key_pool, void* value_pool,
+    const int32_t* block_tables, const int32_t* cu_seqlens_q, const int32_t* context_lens,
+    const int32_t* seq_lens, int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t block_size, int64_t num_blocks, int32_t max_blocks_per_seq,
+    int32_t max_context_len, float scale, int32_t dtype, const mvllm_plan_options* options,
+    void* workspace, uint64_t workspace_bytes, void* stream);
+
 /* out = T(T(g * T(sigmoid(g))) * u) elementwise over n elements of `dtype`.
  * Replaces `mini_vllm_C.swiglu` (csrc/bindings.cpp:14,59-63 -> csrc/swiglu.cu:87-120),
  * called from mini_vllm/kernels/ops.py:161-162. */

@@ -572,7 +572,7 @@ extern "C" {
 
 const char* mvllm_last_error(void) { return g_error; }
 
-int mvllm_abi_version(void) { return 13; }
+int mvllm_abi_version(void) { return 14; }
 
 #ifndef MVLLM_SOURCE_HASH
 #define MVLLM_SOURCE_HASH "unstamped"
@@ -787,6 +787,125 @@ int mvllm_paged_attention_noalloc(void* out, const void* q, const void* key_pool
                                head_dim, block_size, num_blocks, max_blocks_per_seq,
                                max_query_len, max_context_len, scale, q_dtype, kv_dtype,
                                options, ws, kNoallocScratchBytes, stream, true);
+}
+
+int mvllm_paged_decode_qk_norm_rope(
+    void* out, const void* q, const void* k, const void* v, int64_t q_token_stride,
+    int64_t kv_token_stride, const void* q_weight, const void* k_weight, const float* cos_table,
+    const float* sin_table, int64_t max_positions, float eps, void* key_pool, void* value_pool,
+    const int32_t* block_tables, const int32_t* cu_seqlens_q, const int32_t* context_lens,
+    const int32_t* seq_lens, int32_t num_seqs, int32_t num_q_heads, int32_t num_kv_heads,
+    int32_t head_dim, int32_t block_size, int64_t num_blocks, int32_t max_blocks_per_seq,
+    int32_t max_context_len, float scale, int32_t dtype, const mvllm_plan_options* options,
+    void* workspace, uint64_t workspace_bytes, void* stream) {
+  g_error[0] = '\0';
+  const char* name = "paged_decode_qk_norm_rope";
+  int rc = check_paged_shape(num_seqs, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size,
+                             1, max_context_len, dtype, dtype);
+  if (rc != MVLLM_OK) return rc;
+  Options o;
+  rc = read_options(options, o);
+  if (rc != MVLLM_OK) return rc;
+  if (dtype != mvllm::kF16 && dtype != mvllm::kBF16) {
+    return fail(MVLLM_ERR_UNSUPPORTED,
+                "%s: dtype code %d is not served (float16 and bfloat16 pools are; call "
+                "mvllm_qk_norm_rope_kv_write then mvllm_paged_attention)",
+                name, dtype);
+  }
+  if (head_dim != 128) {
+    return fail(MVLLM_ERR_UNSUPPORTED, "%s: head dim %d is not served (128 is)", name, head_dim);
+  }
+  if (num_seqs == 0) return MVLLM_OK;
+  if (out == nullptr || q == nullptr || k == nullptr || v == nullptr || q_weight == nullptr ||
+      k_weight == nullptr || cos_table == nullptr || sin_table == nullptr ||
+      key_pool == nullptr || value_pool == nullptr || block_tables == nullptr ||
+      cu_seqlens_q == nullptr || context_lens == nullptr || seq_lens == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "%s: a required pointer is NULL", name);
+  }
+  if (num_blocks <= 0 || max_blocks_per_seq <= 0 || max_positions <= 0) {
+    return fail(MVLLM_ERR_INVALID, "%s: empty pool, block table or cos/sin tables", name);
+  }
+  const uintptr_t bits = reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(q) |
+                         reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
+                         reinterpret_cast<uintptr_t>(q_weight) |
+                         reinterpret_cast<uintptr_t>(k_weight) |
+                         reinterpret_cast<uintptr_t>(cos_table) |
+                         reinterpret_cast<uintptr_t>(sin_table) |
+                         reinterpret_cast<uintptr_t>(key_pool) |
+                         reinterpret_cast<uintptr_t>(value_pool);
+  if (bits % 16 != 0) return fail(MVLLM_ERR_INVALID, "%s: every tensor must be 16-byte aligned", name);
+  const int64_t q_row = static_cast<int64_t>(num_q_heads) * head_dim;
+  const int64_t kv_row = static_cast<int64_t>(num_kv_heads) * head_dim;
+  const int64_t qs = q_token_stride > 0 ? q_token_stride : q_row;
+  const int64_t kvs = kv_token_stride > 0 ? kv_token_stride : kv_row;
+  if (qs < q_row || kvs < kv_row || qs % 8 != 0 || kvs % 8 != 0) {
+    return fail(MVLLM_ERR_INVALID,
+                "%s: token strides %lld (q) and %lld (k, v) must cover the token's heads (%lld, "
+                "%lld elements) and keep every token 16-byte aligned",
+                name, static_cast<long long>(qs), static_cast<long long>(kvs),
+                static_cast<long long>(q_row), static_cast<long long>(kv_row));
+  }
+  const Plan plan = make_plan(num_seqs, num_seqs, num_q_heads, num_kv_heads, head_dim,
+                              block_size, 1, max_context_len, dtype, dtype, o);
+  if (plan.pub.decode_mode != MVLLM_DECODE_STREAM) {
+    return fail(MVLLM_ERR_UNSUPPORTED,
+                "%s: the plan puts this batch on the grid schedule, which the fused entry does "
+                "not serve (call mvllm_qk_norm_rope_kv_write then mvllm_paged_attention)",
+                name);
+  }
+  const uint64_t need = plan.pub.workspace_bytes;
+  if (workspace == nullptr || workspace_bytes < need) {
+    return fail(MVLLM_ERR_WORKSPACE,
+                "%s: workspace of %llu bytes is smaller than the %llu the plan needs (call "
+                "mvllm_paged_attention_plan with num_tokens = num_seqs, max_query_len = 1)",
+                name, static_cast<unsigned long long>(workspace_bytes),
+                static_cast<unsigned long long>(need));
+  }
+  if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) {
+    return fail(MVLLM_ERR_INVALID, "%s: the workspace must be 256-byte aligned", name);
+  }
+  int shift = 0;
+  while ((1 << shift) < block_size) ++shift;
+  mvllm::PagedParams p{};
+  p.out = out;
+  p.k_pool = key_pool;
+  p.v_pool = value_pool;
+  p.block_tables = block_tables;
+  p.cu_seqlens_q = cu_seqlens_q;
+  p.context_lens = context_lens;
+  p.seq_lens = seq_lens;
+  p.num_seqs = num_seqs;
+  p.num_tokens = num_seqs;
+  p.hq = num_q_heads;
+  p.hk = num_kv_heads;
+  p.max_blocks = max_blocks_per_seq;
+  p.block_shift = shift;
+  p.block_mask = block_size - 1;
+  p.table_shift = shift;
+  p.kv_head_bytes = static_cast<int64_t>(head_dim) * 2;
+  p.kv_row_bytes = p.kv_head_bytes * num_kv_heads;
+  p.scale = scale;
+  p.stream_wgs = plan.pub.decode_workgroups;
+  char* ws = static_cast<char*>(workspace);
+  p.seq_prefix = reinterpret_cast<int*>(ws);
+  p.part_o = reinterpret_cast<float*>(ws + plan.off_o);
+  p.part_ml = reinterpret_cast<float*>(ws + plan.off_ml);
+  mvllm::FreshParams f{};
+  f.q = q;
+  f.k = k;
+  f.v = v;
+  f.q_stride = qs;
+  f.kv_stride = kvs;
+  f.q_weight = q_weight;
+  f.k_weight = k_weight;
+  f.cos_t = cos_table;
+  f.sin_t = sin_table;
+  f.max_positions = max_positions;
+  f.num_blocks = num_blocks;
+  f.eps = eps;
+  return hip_status(mvllm::launch_paged_decode_fresh(p, f, dtype, head_dim,
+                                                     static_cast<hipStream_t>(stream)),
+                    name);
 }
 
 int mvllm_dense_attention_plan(const mvllm_dense_args* args, uint64_t* workspace_bytes) {

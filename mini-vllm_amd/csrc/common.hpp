@@ -301,6 +301,76 @@ __device__ __forceinline__ float group_max(float v) {
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
 __device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
 
+// Pack N floats (N = 16 / sizeof(T)) back into one 16-byte chunk of T.
+template <typename T>
+__device__ __forceinline__ u32x4 pack_chunk(const float* v) {
+  u32x4 r;
+  if constexpr (__is_same(T, float)) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = __float_as_uint(v[e]);
+  } else if constexpr (__is_same(T, bf16_t)) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = f32_to_f16_bits(v[2 * e]) | (f32_to_f16_bits(v[2 * e + 1]) << 16);
+  }
+  return r;
+}
+
+// Qwen3's per-head QK-norm followed by RoPE on one head row of D = kR N elements held
+// as one 16-byte chunk per lane of a kR-lane group (lane r: elements r N .. r N + N - 1):
+// rmsnorm -> rope with the unfused kernels' rounding points (the sum of squares in
+// rmsnorm_vec_kernel's order, the norm output rounded to T, then the rotation of those
+// rounded values). `wf` are the lane's norm weights, `c` and `sn` its cosines and sines
+// at the row's position, the sign of the low half already folded into `sn`
+// (x_lo cos - x_hi sin = x_lo cos + x_hi (-sin), exactly). The rotation partner holds
+// dims +-D/2, i.e. lane r ^ (kR / 2): for kR = 16 a rotation by 8 inside a 16-lane DPP
+// row. Every lane of the group must call it (cross-lane operations). Returns the
+// rotated chunk rounded to T. Shared by the QK-norm + RoPE kernel and the decode
+// attention that normalises the step's new token itself, so both give the same bits;
+// every file that calls it is compiled with -ffp-contract=off (each product and sum
+// rounded on its own, as the unfused kernels and torch round them).
+template <typename T, int kR>
+__device__ __forceinline__ u32x4 norm_rope_chunk(const u32x4& held, const float* wf,
+                                                 const float* c, const float* sn, float eps) {
+  constexpr int N = Chunk<T>::kN;
+  constexpr int D = kR * N;
+  float f[N];
+  Chunk<T>::unpack(held, f);
+  float sumsq = 0.0f;
+#pragma unroll
+  for (int e = 0; e < N; ++e) sumsq = fmaf(f[e], f[e], sumsq);
+  sumsq = group_sum<kR>(sumsq);
+  const float inv = rsqrtf(sumsq / static_cast<float>(D) + eps);
+  float y[N];
+#pragma unroll
+  for (int e = 0; e < N; e += 2) {
+    if constexpr (N == 4) {
+      y[e] = __fmul_rn(__fmul_rn(f[e], inv), wf[e]);
+      y[e + 1] = __fmul_rn(__fmul_rn(f[e + 1], inv), wf[e + 1]);
+    } else {
+      float n0 = __fmul_rn(f[e], inv), n1 = __fmul_rn(f[e + 1], inv);
+      round_pair<T>(n0, n1);
+      y[e] = __fmul_rn(n0, wf[e]);
+      y[e + 1] = __fmul_rn(n1, wf[e + 1]);
+      round_pair<T>(y[e], y[e + 1]);
+    }
+  }
+  float out[N];
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    float py;
+    if constexpr (kR == 16) {
+      py = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(y[e]), 0x128, 0xF, 0xF, false));
+    } else {
+      py = __shfl_xor(y[e], kR / 2, kWave);
+    }
+    out[e] = __fadd_rn(__fmul_rn(y[e], c[e]), __fmul_rn(py, sn[e]));
+  }
+  return pack_chunk<T>(out);
+}
+
 // Sum over a workgroup of `kWaves` waves, through `kWaves` floats of LDS. Every
 // thread of the workgroup must call it.
 template <int kWaves>

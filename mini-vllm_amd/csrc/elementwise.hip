@@ -260,23 +260,6 @@ __global__ __launch_bounds__(256) void rope_kernel(const void* __restrict__ x,
   Elem<T>::store(out, hi, __fadd_rn(__fmul_rn(xh, cos_t[th]), __fmul_rn(xl, sin_t[th])));
 }
 
-// Pack N floats (N = 16 / sizeof(T)) back into one 16-byte chunk of T.
-template <typename T>
-__device__ __forceinline__ u32x4 pack_chunk(const float* v) {
-  u32x4 r;
-  if constexpr (__is_same(T, float)) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) r[e] = __float_as_uint(v[e]);
-  } else if constexpr (__is_same(T, bf16_t)) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) r[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) r[e] = f32_to_f16_bits(v[2 * e]) | (f32_to_f16_bits(v[2 * e + 1]) << 16);
-  }
-  return r;
-}
-
 // Vectorised RoPE: one thread per 16-byte chunk of the lower half of a head vector and
 // the matching chunk of the upper half, so every access to x and out is a 16-byte
 // vector access and the cos/sin rows are read as 16-byte pieces. x and out are streamed
@@ -507,46 +490,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
 
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    // rmsnorm, as rmsnorm_vec_kernel<T, kR, 1>
-    float f[N];
-    Chunk<T>::unpack(held[g], f);
-    float sumsq = 0.0f;
-#pragma unroll
-    for (int e = 0; e < N; ++e) sumsq = fmaf(f[e], f[e], sumsq);
-    sumsq = group_sum<kR>(sumsq);
-    const float inv = rsqrtf(sumsq / static_cast<float>(D) + eps);
-    float y[N];
-#pragma unroll
-    for (int e = 0; e < N; e += 2) {
-      if constexpr (N == 4) {
-        y[e] = __fmul_rn(__fmul_rn(f[e], inv), wf[e]);
-        y[e + 1] = __fmul_rn(__fmul_rn(f[e + 1], inv), wf[e + 1]);
-      } else {
-        float n0 = __fmul_rn(f[e], inv), n1 = __fmul_rn(f[e + 1], inv);
-        round_pair<T>(n0, n1);
-        y[e] = __fmul_rn(n0, wf[e]);
-        y[e + 1] = __fmul_rn(n1, wf[e + 1]);
-        round_pair<T>(y[e], y[e + 1]);
-      }
-    }
-
-    // the rotation partner's values (dims +-D/2), across lanes: lane r ^ (kR / 2). For
-    // kR = 16 that is a rotation by 8 inside a 16-lane DPP row (one v_mov_dpp per value).
-    float py[N];
-#pragma unroll
-    for (int e = 0; e < N; ++e) {
-      if constexpr (kR == 16) {
-        py[e] = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(y[e]), 0x128, 0xF, 0xF, false));
-      } else {
-        py[e] = __shfl_xor(y[e], kR / 2, kWave);
-      }
-    }
+    // every lane of the group takes part (cross-lane sums and rotation)
+    const u32x4 packed = norm_rope_chunk<T, kR>(held[g], wf, c, sn, eps);
     if (!live) continue;
-
-    float out[N];
-#pragma unroll
-    for (int e = 0; e < N; ++e) out[e] = __fadd_rn(__fmul_rn(y[e], c[e]), __fmul_rn(py[e], sn[e]));
-    const u32x4 packed = pack_chunk<T>(out);
     if (!KV || !is_k || k_out != nullptr) {
       char* orow = static_cast<char*>(is_k ? k_out : q_out) + (local + g) * kRowBytes;
       nt_store16(orow + r * 16, packed);

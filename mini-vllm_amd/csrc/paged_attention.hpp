@@ -177,6 +177,32 @@ __host__ __device__ inline int decode_split_len(int visible, int nsplit) {
 hipError_t launch_paged_decode(const PagedParams& p, int q_dtype, int kv_dtype, int head_dim,
                                hipStream_t stream);
 
+// The decode step's new token, taken by the stream decode from the projection's output
+// rather than from the pool: every sequence s of a decode-only batch has its token at
+// position context_lens[s] - 1; its q head vectors are QK-normed and rotated in the
+// launch (as the QK-norm + RoPE kernel does, the same bits), its k row likewise, and k
+// and v go to the pool slot the block table maps that position to (a page id outside
+// [0, num_blocks) writes nothing) and into the attention straight from registers.
+struct FreshParams {
+  const void* q;          // raw q of row i at q + i q_stride (H_q D contiguous elements)
+  const void* k;          // raw k and v of row i at k / v + i kv_stride (H_k D elements)
+  const void* v;
+  int64_t q_stride;       // elements between consecutive rows
+  int64_t kv_stride;
+  const void* q_weight;   // QK-norm weights, [D]
+  const void* k_weight;
+  const float* cos_t;     // [max_positions][D]
+  const float* sin_t;
+  int64_t max_positions;  // a position at or past it gives NaN rows, as the unfused kernel
+  int64_t num_blocks;
+  float eps;
+};
+
+// Stream decode with the new token formed in the launch (16-bit q and pool, head dim
+// 128, p.stream_wgs > 0), then the merge, as launch_paged_decode.
+hipError_t launch_paged_decode_fresh(const PagedParams& p, const FreshParams& f, int dtype,
+                                     int head_dim, hipStream_t stream);
+
 hipError_t launch_paged_prefill(const PagedParams& p, int q_dtype, int kv_dtype, int head_dim,
                                 int max_query_len, hipStream_t stream);
 

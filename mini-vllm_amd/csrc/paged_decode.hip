@@ -35,6 +35,15 @@
 //    prefill kernel fits the shape): one workgroup per (row, split) with splits of
 //    `split_tokens` keys, page ids staged in LDS, merged by a second kernel.
 //
+// Fresh-token stream (a decode-only batch over a 16-bit pool): every sequence's last
+// key is the step's new token, taken from the q/k/v projection's output rather than
+// the pool. Each wave QK-norms and rotates its queries itself (norm_rope_chunk, the
+// QK-norm + RoPE kernel's code: this file is compiled with -ffp-contract=off so it
+// rounds the same), the share holding a sequence's last key forms that key's row
+// likewise, writes it and v to the pool slot, and uses them from registers in its last
+// step; the result is the QK-norm + RoPE + KV-write launch followed by the plain
+// stream, bit for bit, with one launch fewer.
+//
 // K/V are read with nontemporal 16-byte loads (they are streamed once); page ids are
 // fetched one step ahead of the K/V loads that need them. Scores are kept in the
 // log2 domain: s = (q.k) * scale * log2(e), p = 2^(s - m), exactly
@@ -134,6 +143,28 @@ struct Decode {
   __device__ static void stream(const PagedParams& p, const int32_t* table, const int* lds_pages,
                                 int first_page, int kvh, int sb, int se, int g, int r,
                                 const float (&qf)[GC][E], float score_scale, State& st) {
+    const Fresh none{-1, {}, {}};
+    stream_with<false>(p, table, lds_pages, first_page, kvh, sb, se, g, r, qf, score_scale, st,
+                       [] {}, none);
+  }
+
+  // The new token of a fresh-token stream: token `tok` of the run (< 0: none) takes this
+  // lane's chunks `k` and `v` as its K and V rows instead of the pool's.
+  struct Fresh {
+    int tok;
+    u32x4 k, v;
+  };
+
+  // stream() with two additions: `prep()` runs once the first step's page ids have been
+  // requested (a fresh-token stream forms its queries and the new token's rows there, in
+  // qf and `fresh`, so that arithmetic overlaps those loads), and with kFresh the step
+  // holding fresh.tok takes that token's rows from `fresh`.
+  template <bool kFresh, typename Prep>
+  __device__ static void stream_with(const PagedParams& p, const int32_t* table,
+                                     const int* lds_pages, int first_page, int kvh, int sb, int se,
+                                     int g, int r, const float (&qf)[GC][E], float score_scale,
+                                     State& st, Prep&& prep, const Fresh& fresh) {
+    static_assert(!(kFresh && kFp8), "the fresh-token stream serves 16-bit pools");
     const char* kbase = static_cast<const char*>(p.k_pool);
     const char* vbase = static_cast<const char*>(p.v_pool);
     constexpr int kElemBytes = Elem<TKV>::kBytes;
@@ -147,6 +178,7 @@ struct Decode {
     int pg[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) pg[u] = page_of(min(sb + u * RG + g, se - 1));
+    prep();
 
     for (int t0 = sb; t0 < se; t0 += kStep) {
       u32x4 kw[kUnroll], vw[kUnroll];
@@ -169,6 +201,19 @@ struct Decode {
       if (t0 + kStep < se) {
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) pg[u] = page_of(min(t0 + kStep + u * RG + g, se - 1));
+      }
+      if constexpr (kFresh) {
+        // The step holding the new token (wave-uniform test): its pool slot, read above
+        // before this launch wrote it, is replaced by the rows formed in the launch.
+        if (fresh.tok >= 0 && t0 + kStep > fresh.tok) {
+#pragma unroll
+          for (int u = 0; u < kUnroll; ++u) {
+            if (t0 + u * RG + g == fresh.tok) {
+              kw[u] = fresh.k;
+              vw[u] = fresh.v;
+            }
+          }
+        }
       }
 
       float s[kUnroll][GC];
@@ -296,8 +341,11 @@ __device__ __forceinline__ bool wave_unit(const PagedParams& p, int unit, int& k
 
 // ------------------------------------------------------------ stream schedule
 
-template <typename TQ, typename TKV, int D, int GC>
-__global__ __launch_bounds__(512) void paged_decode_stream_kernel(const PagedParams p) {
+// kFresh: every sequence's last key is the step's new token, formed here from the
+// projection's output (FreshParams) instead of read from the pool.
+template <typename TQ, typename TKV, int D, int GC, bool kFresh>
+__global__ __launch_bounds__(512) void paged_decode_stream_kernel(const PagedParams p,
+                                                                  const FreshParams f) {
   using K = Decode<TKV, D, GC>;
   __shared__ int s_prefix[kMaxStreamSeqs + 1];  // decode keys before sequence s
 
@@ -363,10 +411,72 @@ __global__ __launch_bounds__(512) void paged_decode_stream_kernel(const PagedPar
     typename K::State st;
     if (active) {
       float qf[GC][K::E];
-      K::template load_queries<TQ>(p, row, h0, r, qf);
       K::init(st);
       const int32_t* table = p.block_tables + static_cast<int64_t>(seq) * p.max_blocks;
-      K::stream(p, table, nullptr, 0, kvh, sb, se, g, r, qf, score_scale, st);
+      if constexpr (kFresh) {
+        static_assert(K::E == 8 && K::R == 16, "the fresh-token stream takes 16-bit D = 128");
+        // Loads first (all rows of the token, whether or not this run holds it: no
+        // divergent loads), the arithmetic in prep() once the page ids are requested.
+        const int pos = ctx - 1;
+        const bool pos_ok = pos < f.max_positions;
+        const int64_t trow = pos_ok ? pos : 0;  // out of range: row 0, NaN rows below
+        u32x4 qraw[GC];
+#pragma unroll
+        for (int h = 0; h < GC; ++h) {
+          qraw[h] = load16(static_cast<const char*>(f.q) +
+                           (static_cast<int64_t>(row) * f.q_stride + (h0 + h) * D + r * 8) * 2);
+        }
+        const int64_t kvoff = (static_cast<int64_t>(row) * f.kv_stride + kvh * D + r * 8) * 2;
+        const u32x4 kraw = load16(static_cast<const char*>(f.k) + kvoff);
+        const u32x4 vraw = load16(static_cast<const char*>(f.v) + kvoff);
+        const u32x4 wq = load16(static_cast<const char*>(f.q_weight) + r * 16);
+        const u32x4 wk = load16(static_cast<const char*>(f.k_weight) + r * 16);
+        float c[8], sn[8];
+        Chunk<float>::unpack(load16(f.cos_t + trow * D + r * 8), c);
+        Chunk<float>::unpack(load16(f.cos_t + trow * D + r * 8 + 4), c + 4);
+        Chunk<float>::unpack(load16(f.sin_t + trow * D + r * 8), sn);
+        Chunk<float>::unpack(load16(f.sin_t + trow * D + r * 8 + 4), sn + 4);
+        const int new_page = table[pos >> p.block_shift];
+        const bool has_new = se == ctx;
+        typename K::Fresh fresh{-1, {}, {}};
+        auto prep = [&]() {
+          if (r < 8) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sn[e] = -sn[e];
+          }
+          if (!pos_ok) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) c[e] = sn[e] = __int_as_float(0x7fc00000);
+          }
+          float wf[8];
+          Chunk<TQ>::unpack(wq, wf);
+#pragma unroll
+          for (int h = 0; h < GC; ++h) {
+            // rounded to TQ as the unfused kernel stores q, widened as the attention loads it
+            Chunk<TQ>::unpack(norm_rope_chunk<TQ, 16>(qraw[h], wf, c, sn, f.eps), qf[h]);
+          }
+          Chunk<TQ>::unpack(wk, wf);
+          fresh.k = norm_rope_chunk<TQ, 16>(kraw, wf, c, sn, f.eps);
+          fresh.v = vraw;
+          if (has_new) {
+            fresh.tok = pos;
+            // One wave per kv head writes the pool (the first of its query-head chunks),
+            // row group 0's 16 lanes one row each of K and V.
+            if (g == 0 && h0 % (p.hq / p.hk) == 0 && new_page >= 0 && new_page < f.num_blocks) {
+              const int64_t slot =
+                  (static_cast<int64_t>(new_page) << p.table_shift) + (pos & p.block_mask);
+              const int64_t off = slot * p.kv_row_bytes + kvh * p.kv_head_bytes + r * 16;
+              store16(static_cast<char*>(const_cast<void*>(p.k_pool)) + off, fresh.k);
+              store16(static_cast<char*>(const_cast<void*>(p.v_pool)) + off, fresh.v);
+            }
+          }
+        };
+        K::template stream_with<true>(p, table, nullptr, 0, kvh, sb, se, g, r, qf, score_scale,
+                                      st, prep, fresh);
+      } else {
+        K::template load_queries<TQ>(p, row, h0, r, qf);
+        K::stream(p, table, nullptr, 0, kvh, sb, se, g, r, qf, score_scale, st);
+      }
       K::merge_row_groups(st);
       if (g == 0) {
         if (whole) {
@@ -590,6 +700,15 @@ int decode_waves(const PagedParams& p, int gc) {
   return units < 8 ? units : 8;
 }
 
+template <typename TQ, int D>
+hipError_t launch_stream_merge(const PagedParams& p, hipStream_t stream) {
+  const int n4 = p.hq * D / 4;
+  const dim3 mgrid(p.num_seqs, (n4 + kMergeCols - 1) / kMergeCols);
+  paged_decode_stream_merge_kernel<TQ, D>
+      <<<mgrid, kMergeCols * kMergeGroups, 0, stream>>>(p, p.stream_wgs);
+  return hipGetLastError();
+}
+
 template <typename TQ, typename TKV, int D, int GC>
 hipError_t launch_decode_g(const PagedParams& p, hipStream_t stream) {
   const int units = p.hk * (p.hq / p.hk / GC);
@@ -597,14 +716,11 @@ hipError_t launch_decode_g(const PagedParams& p, hipStream_t stream) {
   constexpr int kHeadsPerMergeBlock = 4;
   if (p.stream_wgs > 0) {
     if (units > 8) return hipErrorInvalidValue;  // planner keeps stream mode to <= 8 units
-    paged_decode_stream_kernel<TQ, TKV, D, GC><<<p.stream_wgs, waves * kWave, 0, stream>>>(p);
+    paged_decode_stream_kernel<TQ, TKV, D, GC, false>
+        <<<p.stream_wgs, waves * kWave, 0, stream>>>(p, FreshParams{});
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
-    const int n4 = p.hq * D / 4;
-    const dim3 mgrid(p.num_seqs, (n4 + kMergeCols - 1) / kMergeCols);
-    paged_decode_stream_merge_kernel<TQ, D>
-        <<<mgrid, kMergeCols * kMergeGroups, 0, stream>>>(p, p.stream_wgs);
-    return hipGetLastError();
+    return launch_stream_merge<TQ, D>(p, stream);
   }
   const dim3 grid(p.max_splits, p.by_row ? p.num_tokens : p.num_seqs, (units + waves - 1) / waves);
   paged_decode_grid_kernel<TQ, TKV, D, GC><<<grid, waves * kWave, 0, stream>>>(p);
@@ -637,6 +753,41 @@ hipError_t launch_decode_t(const PagedParams& p, int head_dim, hipStream_t strea
 }
 
 }  // namespace
+
+namespace {
+
+template <typename T, int GC>
+hipError_t launch_fresh_g(const PagedParams& p, const FreshParams& f, hipStream_t stream) {
+  constexpr int D = 128;
+  const int units = p.hk * (p.hq / p.hk / GC);
+  if (units > 8) return hipErrorInvalidValue;  // planner keeps stream mode to <= 8 units
+  paged_decode_stream_kernel<T, T, D, GC, true>
+      <<<p.stream_wgs, decode_waves(p, GC) * kWave, 0, stream>>>(p, f);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  return launch_stream_merge<T, D>(p, stream);
+}
+
+template <typename T>
+hipError_t launch_fresh_t(const PagedParams& p, const FreshParams& f, hipStream_t stream) {
+  switch (decode_group_chunk(p.hq / p.hk)) {
+    case 4: return launch_fresh_g<T, 4>(p, f, stream);
+    case 2: return launch_fresh_g<T, 2>(p, f, stream);
+    default: return launch_fresh_g<T, 1>(p, f, stream);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_paged_decode_fresh(const PagedParams& p, const FreshParams& f, int dtype,
+                                     int head_dim, hipStream_t stream) {
+  if (head_dim != 128 || p.stream_wgs <= 0) return hipErrorInvalidValue;
+  switch (dtype) {
+    case kF16: return launch_fresh_t<f16_t>(p, f, stream);
+    case kBF16: return launch_fresh_t<bf16_t>(p, f, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 hipError_t launch_paged_decode(const PagedParams& p, int q_dtype, int kv_dtype, int head_dim,
                                hipStream_t stream) {

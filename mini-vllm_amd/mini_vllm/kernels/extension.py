@@ -57,14 +57,18 @@ HIP_FLAGS = [
 ]
 
 # Per-source extra flags. The elementwise kernels must round exactly where the
-# reference's PyTorch expressions round, so FMA contraction is off there.
-EXTRA_FLAGS = {"elementwise.hip": ["-ffp-contract=off"], "linear.hip": ["-ffp-contract=off"]}
+# reference's PyTorch expressions round, so FMA contraction is off there; the decode
+# kernels form the step's new token with the same QK-norm + RoPE code, which then has
+# to compile to the same bits (measured: contraction left on there moved one in ten
+# float16 rows by an ulp, and the decode ran no faster).
+EXTRA_FLAGS = {"elementwise.hip": ["-ffp-contract=off"], "linear.hip": ["-ffp-contract=off"],
+               "paged_decode.hip": ["-ffp-contract=off"]}
 
 # hipBLASLt (csrc/blas.hip). Its soname is the one torch's bundled copy carries, so in a
 # process that has imported torch the library binds to that copy.
 LINK_LIBS = ["-L/opt/rocm/lib", "-lhipblaslt"]
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 DTYPE_CODES: dict[torch.dtype, int] = {
     torch.float32: 0,
@@ -284,6 +288,10 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_qk_norm_rope_kv_write.restype = ctypes.c_int
     lib.mvllm_qk_norm_rope_kv_write.argtypes = (
         [p] * 9 + [i32, p, p, p, i64, i64, i32, i32, i32, i64, i64, f32, i64, i64, i32, p])
+    lib.mvllm_paged_decode_qk_norm_rope.restype = ctypes.c_int
+    lib.mvllm_paged_decode_qk_norm_rope.argtypes = (
+        [p] * 4 + [i64, i64] + [p] * 4 + [i64, f32] + [p] * 6 + [i32] * 5
+        + [i64, i32, i32, f32, i32, opts, p, u64, p])
     lib.mvllm_kv_write.restype = ctypes.c_int
     lib.mvllm_kv_write.argtypes = [p] * 7 + [i32] * 4 + [i64, i32, i32, p]
     lib.mvllm_argmax.restype = ctypes.c_int
@@ -338,6 +346,7 @@ EXPORTED_SYMBOLS = (
     "mvllm_qk_norm_rope",
     "mvllm_argmax",
     "mvllm_qk_norm_rope_kv_write",
+    "mvllm_paged_decode_qk_norm_rope",
     "mvllm_argmax_workspace_bytes",
     "mvllm_dense_attention_plan",
     "mvllm_dense_attention",
@@ -1174,9 +1183,11 @@ class HipExtension:
         return out
 
     def _paged_checks(self, q, key_pool, value_pool, block_tables, cu_seqlens_q, context_lens,
-                      seq_lens, max_query_len, max_context_len, k_scale, v_scale):
+                      seq_lens, max_query_len, max_context_len, k_scale, v_scale,
+                      strided_q: bool = False):
         """The reference's refusals for a paged call (``paged_attention.cu:608-676``) and this
-        library's: raises RuntimeError; returns the contiguous metadata."""
+        library's: raises RuntimeError; returns the contiguous metadata. ``strided_q``: q
+        may have any token stride (its caller checks the rows)."""
         if not (q.is_cuda and key_pool.is_cuda and value_pool.is_cuda):
             raise RuntimeError("paged_attention: q and the pools must be CUDA tensors")
         if q.dim() != 3:
@@ -1189,7 +1200,8 @@ class HipExtension:
                 "paged_attention: expected matching pools shaped num_blocks x P x H_k x D, got "
                 f"{list(key_pool.shape)} and {list(value_pool.shape)}"
             )
-        if not (q.is_contiguous() and key_pool.is_contiguous() and value_pool.is_contiguous()):
+        if not ((strided_q or q.is_contiguous()) and key_pool.is_contiguous()
+                and value_pool.is_contiguous()):
             raise RuntimeError(
                 "paged_attention: q and the pools must be contiguous; the kernel walks them by "
                 "slot arithmetic rather than by stride"
@@ -1367,6 +1379,97 @@ class HipExtension:
                 _stream(q.device),
             )
         )
+        return out
+
+    @staticmethod
+    def paged_decode_qk_norm_rope_supported(q: torch.Tensor, key_pool: torch.Tensor,
+                                            num_seqs: int) -> bool:
+        """Whether ``paged_decode_qk_norm_rope`` serves a decode-only batch of this shape
+        without options: a float16 or bfloat16 pool of q's dtype, head dim 128, a stream
+        plan (at most 4096 sequences, at most 8 wave units of (kv head, query-head
+        chunk)). The caller otherwise makes the two calls it fuses."""
+        if q.dtype not in (torch.float16, torch.bfloat16) or key_pool.dtype != q.dtype:
+            return False
+        if key_pool.dim() != 4 or key_pool.shape[3] != 128 or q.shape[-1] != 128:
+            return False
+        hk = key_pool.shape[2]
+        hq = q.shape[-2]
+        if hk <= 0 or hq % hk:
+            return False
+        group = hq // hk
+        chunk = 4 if group % 4 == 0 else (2 if group % 2 == 0 else 1)
+        return 0 < num_seqs <= 4096 and hk * (group // chunk) <= 8
+
+    def paged_decode_qk_norm_rope(
+        self,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        q_weight: torch.Tensor,
+        k_weight: torch.Tensor,
+        cos: torch.Tensor,
+        sin: torch.Tensor,
+        eps: float,
+        key_pool: torch.Tensor,
+        value_pool: torch.Tensor,
+        block_tables: torch.Tensor,
+        cu_seqlens_q: torch.Tensor,
+        context_lens: torch.Tensor,
+        seq_lens: torch.Tensor,
+        max_context_len: int,
+        scale: float,
+        out: torch.Tensor | None = None,
+        plan_options: dict[str, Any] | None = None,
+    ) -> torch.Tensor:
+        """A decode step's attention with its new token's QK-norm, RoPE and KV write in
+        the same launch (``mvllm_paged_decode_qk_norm_rope``): bitwise
+        ``qk_norm_rope_kv_write`` (positions ``context_lens - 1``, slots from the block
+        tables) then ``paged_attention`` of the rotated q. q (raw, ``S x H_q x D``), k
+        and v (``S x H_k x D``) may be column views of the fused projection's output;
+        every sequence computes one token (``S`` rows)."""
+        name = "paged_decode_qk_norm_rope"
+        self._qk_norm_rope_checks(name, q, k, q_weight, k_weight, context_lens, cos, sin)
+        cu_seqlens_q, context_lens, seq_lens = self._paged_checks(
+            q, key_pool, value_pool, block_tables, cu_seqlens_q, context_lens, seq_lens,
+            1, max_context_len, None, None, strided_q=True)
+        num_blocks, block_size, num_kv_heads, head_dim = key_pool.shape
+        num_seqs = seq_lens.shape[0]
+        if q.shape[0] != num_seqs or v.shape != k.shape or v.dtype != q.dtype or not v.is_cuda:
+            raise RuntimeError(
+                f"{name}: one token per sequence: q must be {num_seqs} x H_q x D and v shaped "
+                f"like k, got {tuple(q.shape)}, {tuple(k.shape)} and {tuple(v.shape)}")
+        if not self.paged_decode_qk_norm_rope_supported(q, key_pool, num_seqs):
+            raise RuntimeError(f"{name}: this dtype / head dim / batch is not served")
+        d = head_dim
+
+        def rows_ok(t):  # heads contiguous within each token
+            return t.stride(2) == 1 and t.stride(1) == d
+        if not (rows_ok(q) and rows_ok(k) and rows_ok(v)) or k.stride(0) != v.stride(0):
+            q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        if out is None:
+            out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        elif out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous():
+            raise RuntimeError(f"{name}: out must be a contiguous tensor shaped like q")
+        if num_seqs == 0:
+            return out
+        code = DTYPE_CODES[q.dtype]
+        num_q_heads = q.shape[1]
+        opts = make_plan_options(plan_options)
+        opts_ref = None if opts is None else ctypes.byref(opts)
+        plan = _Plan()
+        self._check(self.lib.mvllm_paged_attention_plan(
+            num_seqs, num_seqs, num_q_heads, num_kv_heads, head_dim, block_size, 1,
+            int(max_context_len), code, code, opts_ref, ctypes.byref(plan)))
+        workspace = self.workspace(q.device, max(int(plan.workspace_bytes), 256))
+        self._check(self.lib.mvllm_paged_decode_qk_norm_rope(
+            out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), q.stride(0), k.stride(0),
+            q_weight.contiguous().data_ptr(), k_weight.contiguous().data_ptr(),
+            cos.contiguous().data_ptr(), sin.contiguous().data_ptr(), cos.shape[0], float(eps),
+            key_pool.data_ptr(), value_pool.data_ptr(), block_tables.data_ptr(),
+            cu_seqlens_q.data_ptr(), context_lens.data_ptr(), seq_lens.data_ptr(), num_seqs,
+            num_q_heads, num_kv_heads, head_dim, block_size, num_blocks, block_tables.shape[1],
+            int(max_context_len), float(scale), code, opts_ref, workspace.data_ptr(),
+            workspace.numel(), _stream(q.device)))
         return out
 
 

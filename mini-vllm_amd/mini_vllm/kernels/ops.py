@@ -10,12 +10,15 @@ engine and tests above it run unchanged:
                     context_lens, seq_lens, max_query_len, max_context_len,
                     scale=None, use_cuda=False)                        ops.py:200-254
 
-plus two ops that fuse what the reference's caller does in several calls:
+plus ops that fuse what the reference's caller does in several calls:
 
     kv_write(key_pool, value_pool, key, value, slot_mapping, use_cuda=False,
              *, k_scale=None, v_scale=None)    PagedKvPool.write: kv_pool.py:116-155
     qk_norm_rope(q, k, q_weight, k_weight, positions, cos, sin, eps=1e-6,
                  use_cuda=False)               qwen3_paged.py:73-78 (2 rmsnorm + 2 rope)
+    qk_norm_rope_kv_write(...)                 the two above in one launch
+    paged_decode_qk_norm_rope(...)             a decode step's qk_norm_rope_kv_write and
+                                               paged_attention in one launch (71-95)
 
 The callee behind ``use_cuda=True`` is ``libminivllm_hip.so`` (HIP for gfx950).
 
@@ -60,6 +63,7 @@ __all__ = [
     "linear_swiglu",
     "pack_weight",
     "paged_attention",
+    "paged_decode_qk_norm_rope",
     "qk_norm_rope",
     "qk_norm_rope_kv_write",
     "rmsnorm",
@@ -277,6 +281,34 @@ def qk_norm_rope_kv_write(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         return None
     return ext.qk_norm_rope_kv_write(q, k, v, q_weight, k_weight, positions, cos, sin, eps,
                                      key_pool, value_pool, slot_mapping)
+
+
+def paged_decode_qk_norm_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                              q_weight: torch.Tensor, k_weight: torch.Tensor,
+                              cos: torch.Tensor, sin: torch.Tensor, eps: float,
+                              key_pool: torch.Tensor, value_pool: torch.Tensor,
+                              block_tables: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                              context_lens: torch.Tensor, seq_lens: torch.Tensor,
+                              max_context_len: int, scale: float,
+                              use_cuda: bool = False) -> torch.Tensor | None:
+    """A decode-only step's ``qk_norm_rope_kv_write`` (positions ``context_lens - 1``,
+    slots from the block tables) and ``paged_attention`` in one launch, bitwise the two
+    (reference qwen3_paged.py:71-95). Kernel: ``csrc/paged_decode.hip``. q (raw, one
+    row per sequence), k and v may be column views of the fused projection's output.
+    None where it does not serve the call (the PyTorch path, an fp8 pool, another head
+    dim, a batch the planner puts on the grid): the caller then makes the two calls."""
+    if not _use_kernel("paged_attention", use_cuda, q):
+        return None
+    ext = load_extension()
+    if (q.dim() != 3 or k.dtype != q.dtype or v.dtype != q.dtype or q_weight.dtype != q.dtype
+            or k_weight.dtype != q.dtype or value_pool.dtype != q.dtype
+            or _rope_reason(q, cos, sin) is not None or not key_pool.is_contiguous()
+            or not value_pool.is_contiguous()
+            or not ext.paged_decode_qk_norm_rope_supported(q, key_pool, seq_lens.shape[0])):
+        return None
+    return ext.paged_decode_qk_norm_rope(q, k, v, q_weight, k_weight, cos, sin, eps, key_pool,
+                                         value_pool, block_tables, cu_seqlens_q, context_lens,
+                                         seq_lens, int(max_context_len), scale)
 
 
 def swiglu(gate: torch.Tensor, up: torch.Tensor, use_cuda: bool = False) -> torch.Tensor:

@@ -9,7 +9,9 @@ hot path has to serve unchanged:
 
 (QK-norm + RoPE of q and k run as one fused op, bitwise equal to the unfused
 rmsnorm/rope pair, which with a 16-bit pool also writes K and V to their slots; the
-K/V write is otherwise one op for K and V. Decode-sized steps, at most
+K/V write is otherwise one op for K and V; a decode step over a 16-bit pool runs the
+QK-norm, RoPE and K/V write inside the attention launch, bitwise the same. Decode-sized
+steps, at most
 64 rows, also fuse the projections: q/k/v as one launch, gate/up with SwiGLU as one,
 and the o and down projections with their residual add, each rounded as the unfused
 ops round; larger steps run the same ops as one BLAS call each over the concatenated
@@ -186,12 +188,24 @@ class Qwen3Paged:
     def _attention(self, layer: int, w: dict, p: dict, x: torch.Tensor, batch,
                    fused: bool) -> torch.Tensor:
         """The attention output (``T x H_q D``) of normed input x, before ``wo``."""
-        return self._paged(layer, self._queries(layer, w, p, x, batch, fused), batch)
+        c = self.config
+        q, k, v = self._projections(w, p, x, fused)
+        if fused and batch.max_query_len == 1:
+            # A decode step: QK-norm, RoPE and the KV write inside the attention launch.
+            kv = self.manager.kv
+            out = ops.paged_decode_qk_norm_rope(
+                q, k, v, w["q_norm"], w["k_norm"], self.cos, self.sin, c.rms_norm_eps,
+                kv.layer_keys(layer), kv.layer_values(layer), batch.block_tables,
+                batch.cu_seqlens_q, batch.context_lens, batch.seq_lens, batch.max_context_len,
+                1.0 / math.sqrt(c.head_dim), use_cuda=self.use_cuda)
+            if out is not None:
+                return out.view(q.shape[0], c.q_size)
+        return self._paged(layer, self._queries(layer, w, q, k, v, batch), batch)
 
-    def _queries(self, layer: int, w: dict, p: dict, x: torch.Tensor, batch,
-                 fused: bool) -> torch.Tensor:
-        """q (``T x H_q x D``, contiguous) of normed input x after QK-norm and RoPE, with
-        this step's K and V written to the layer's pages."""
+    def _projections(self, w: dict, p: dict, x: torch.Tensor,
+                     fused: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """q (``T x H_q x D``), k and v (``T x H_k x D``) of normed input x, before
+        QK-norm and RoPE (with the fused projection, column views of its output)."""
         c = self.config
         t = x.shape[0]
         u = self.use_cuda
@@ -200,9 +214,16 @@ class Qwen3Paged:
                                        views=True)
         else:
             q, k, v = (ops.linear(x, w[n], use_cuda=u) for n in ("wq", "wk", "wv"))
-        q = q.view(t, c.num_attention_heads, c.head_dim)
-        k = k.view(t, c.num_key_value_heads, c.head_dim)
-        v = v.view(t, c.num_key_value_heads, c.head_dim)
+        return (q.view(t, c.num_attention_heads, c.head_dim),
+                k.view(t, c.num_key_value_heads, c.head_dim),
+                v.view(t, c.num_key_value_heads, c.head_dim))
+
+    def _queries(self, layer: int, w: dict, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                 batch) -> torch.Tensor:
+        """q (``T x H_q x D``, contiguous) after QK-norm and RoPE, with this step's K and
+        V written to the layer's pages."""
+        c = self.config
+        u = self.use_cuda
         kv = self.manager.kv
         qr = ops.qk_norm_rope_kv_write(q, k, v, w["q_norm"], w["k_norm"], batch.positions,
                                        self.cos, self.sin, c.rms_norm_eps, kv.layer_keys(layer),
