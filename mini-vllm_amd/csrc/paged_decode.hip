@@ -158,7 +158,8 @@ struct Decode {
   // stream() with two additions: `prep()` runs once the first step's page ids have been
   // requested (a fresh-token stream forms its queries and the new token's rows there, in
   // qf and `fresh`, so that arithmetic overlaps those loads), and with kFresh the step
-  // holding fresh.tok takes that token's rows from `fresh`.
+  // holding fresh.tok takes that token's rows from `fresh`. (Forming them under the
+  // first step's K/V requests instead measured the same, with 60% more registers.)
   template <bool kFresh, typename Prep>
   __device__ static void stream_with(const PagedParams& p, const int32_t* table,
                                      const int* lds_pages, int first_page, int kvh, int sb, int se,
@@ -406,7 +407,9 @@ __global__ __launch_bounds__(512) void paged_decode_stream_kernel(const PagedPar
     const int ctx = s_prefix[seq + 1] - base;
     const int sb = static_cast<int>(pos - base);
     const int se = static_cast<int>(min(hi, static_cast<int64_t>(s_prefix[seq + 1])) - base);
-    const int row = p.cu_seqlens_q[seq];
+    // A decode-only batch (the fresh-token stream) has row s for sequence s: no load
+    // ahead of the raw q/k/v reads that address by row.
+    const int row = kFresh ? seq : p.cu_seqlens_q[seq];
     const bool whole = sb == 0 && se == ctx;
     typename K::State st;
     if (active) {
@@ -448,15 +451,38 @@ __global__ __launch_bounds__(512) void paged_decode_stream_kernel(const PagedPar
 #pragma unroll
             for (int e = 0; e < 8; ++e) c[e] = sn[e] = __int_as_float(0x7fc00000);
           }
-          float wf[8];
-          Chunk<TQ>::unpack(wq, wf);
+          // The GC query rows and the key row, one per row group and pass (row group g
+          // of pass i forms row 4 i + g: query heads first, then k; a row group past
+          // the last row forms k again, unused), then each row's chunk r read by every
+          // row group from lane 16 (row % 4) + r. One pass for up to three query heads:
+          // a quarter of the arithmetic of every row group forming every row.
+          constexpr int kRows = GC + 1;
+          constexpr int kPasses = (kRows + K::RG - 1) / K::RG;
+          u32x4 formed[kPasses];
+#pragma unroll
+          for (int i = 0; i < kPasses; ++i) {
+            const int rix = i * K::RG + g;
+            u32x4 held = kraw;
+#pragma unroll
+            for (int h = 0; h < GC; ++h) held = rix == h ? qraw[h] : held;
+            float wf[8];
+            Chunk<TQ>::unpack(rix < GC ? wq : wk, wf);
+            formed[i] = norm_rope_chunk<TQ, 16>(held, wf, c, sn, f.eps);
+          }
+          auto row_of = [&](int rix) {
+            const int src = (rix % K::RG) * 16 + r;
+            const u32x4& x = formed[rix / K::RG];
+            return u32x4{static_cast<uint32_t>(__shfl(static_cast<int>(x[0]), src, kWave)),
+                         static_cast<uint32_t>(__shfl(static_cast<int>(x[1]), src, kWave)),
+                         static_cast<uint32_t>(__shfl(static_cast<int>(x[2]), src, kWave)),
+                         static_cast<uint32_t>(__shfl(static_cast<int>(x[3]), src, kWave))};
+          };
 #pragma unroll
           for (int h = 0; h < GC; ++h) {
             // rounded to TQ as the unfused kernel stores q, widened as the attention loads it
-            Chunk<TQ>::unpack(norm_rope_chunk<TQ, 16>(qraw[h], wf, c, sn, f.eps), qf[h]);
+            Chunk<TQ>::unpack(row_of(h), qf[h]);
           }
-          Chunk<TQ>::unpack(wk, wf);
-          fresh.k = norm_rope_chunk<TQ, 16>(kraw, wf, c, sn, f.eps);
+          fresh.k = row_of(GC);
           fresh.v = vraw;
           if (has_new) {
             fresh.tok = pos;
