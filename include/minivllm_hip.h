@@ -300,6 +300,20 @@ int mvllm_paged_decode_qk_norm_rope(
     int32_t max_context_len, float scale, int32_t dtype, const mvllm_plan_options* options,
     void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* The token embedding lookup and the first block's input RMSNorm in one launch:
+ * h_out[i] = table[ids[index ? index[i] : i]] (the row copied), out[i] =
+ * rmsnorm(h_out[i], weight), bitwise the lookup then mvllm_rmsnorm. A token id outside
+ * [0, vocab) gives NaN rows and reads nothing. `index` (may be NULL) gathers the ids in
+ * the same launch: a decode graph's input tokens, each either the token its sequence
+ * sampled in the previous replay or the host's id. Replaces the reference forward's
+ * Embedding lookup and its first block's attn_norm (model/qwen3_paged.py:219 and 134);
+ * no counterpart in mini_vllm_C.
+ *   table [vocab, dim], weight [dim], h_out / out [rows, dim], all of `dtype` and
+ *   16-byte aligned; ids, index int64. Dims as mvllm_add_rmsnorm. */
+int mvllm_embed_rmsnorm(void* h_out, void* out, const void* table, int64_t vocab,
+                        const int64_t* ids, const int64_t* index, int64_t rows, int32_t dim,
+                        const void* weight, float eps, int32_t dtype, void* stream);
+
 /* out = T(T(g * T(sigmoid(g))) * u) elementwise over n elements of `dtype`.
  * Replaces `mini_vllm_C.swiglu` (csrc/bindings.cpp:14,59-63 -> csrc/swiglu.cu:87-120),
  * called from mini_vllm/kernels/ops.py:161-162. */

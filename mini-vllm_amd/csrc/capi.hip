@@ -572,7 +572,7 @@ extern "C" {
 
 const char* mvllm_last_error(void) { return g_error; }
 
-int mvllm_abi_version(void) { return 14; }
+int mvllm_abi_version(void) { return 15; }
 
 #ifndef MVLLM_SOURCE_HASH
 #define MVLLM_SOURCE_HASH "unstamped"
@@ -1160,6 +1160,32 @@ int mvllm_add_rmsnorm(void* h_out, void* out, const void* x, const void* residua
   return hip_status(mvllm::launch_add_rmsnorm(x, residual, weight, h_out, out, rows, dim, eps,
                                               dtype, static_cast<hipStream_t>(stream)),
                     "add_rmsnorm: launch");
+}
+
+int mvllm_embed_rmsnorm(void* h_out, void* out, const void* table, int64_t vocab,
+                        const int64_t* ids, const int64_t* index, int64_t rows, int32_t dim,
+                        const void* weight, float eps, int32_t dtype, void* stream) {
+  g_error[0] = '\0';
+  if (!mvllm::add_rmsnorm_supported(dtype, dim)) {
+    return fail(MVLLM_ERR_UNSUPPORTED,
+                "embed_rmsnorm: dtype code %d with dim %d is not served (f32/f16/bf16, dim a "
+                "multiple of one 16-byte chunk, at most 512 chunks); look the rows up, then "
+                "call rmsnorm",
+                dtype, dim);
+  }
+  if (rows < 0 || vocab <= 0) return fail(MVLLM_ERR_INVALID, "embed_rmsnorm: bad row or vocab count");
+  if (rows == 0) return MVLLM_OK;
+  if (h_out == nullptr || out == nullptr || table == nullptr || ids == nullptr ||
+      weight == nullptr) {
+    return fail(MVLLM_ERR_INVALID, "embed_rmsnorm: a required pointer is NULL");
+  }
+  if ((reinterpret_cast<uintptr_t>(h_out) | reinterpret_cast<uintptr_t>(out) |
+       reinterpret_cast<uintptr_t>(table) | reinterpret_cast<uintptr_t>(weight)) % 16 != 0) {
+    return fail(MVLLM_ERR_INVALID, "embed_rmsnorm: the table, weight and outputs must be 16-byte aligned");
+  }
+  return hip_status(mvllm::launch_embed_rmsnorm(table, vocab, ids, index, weight, h_out, out, rows,
+                                                dim, eps, dtype, static_cast<hipStream_t>(stream)),
+                    "embed_rmsnorm: launch");
 }
 
 int mvllm_swiglu_interleaved(void* out, const void* gate_up, int64_t rows, int64_t cols,

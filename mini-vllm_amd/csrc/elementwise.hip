@@ -22,19 +22,40 @@ namespace mvllm {
 
 // ------------------------------------------------------------------- rmsnorm
 
+// Rows taken from an embedding table (x = the table): row i is table row
+// ids[index ? index[i] : i]; a token id outside [0, vocab) reads nothing and gives NaN
+// rows.
+struct RowSource {
+  const int64_t* ids = nullptr;
+  const int64_t* index = nullptr;
+  int64_t vocab = 0;
+};
+
+// A 16-byte chunk of T NaNs.
+template <typename T>
+__device__ __forceinline__ u32x4 nan_chunk() {
+  const uint32_t w = __is_same(T, float) ? 0x7fc00000u
+                     : __is_same(T, bf16_t) ? 0x7fc07fc0u : 0x7e007e00u;
+  return u32x4{w, w, w, w};
+}
+
 // kR lanes per row (a power of two <= 64), each holding up to kMaxCh 16-byte chunks of
 // the row in registers between the reduction and the scale pass; 64 / kR rows per wave.
 // x and out are streamed nontemporally, the weight row (shared by every row) is cached.
 // With kAdd the row is first h = T(x + residual) (torch's add: an fp32 sum rounded to
 // T), stored to h_out, and the norm runs on h: the residual add of a transformer block
-// and the RMSNorm after it in one pass.
-template <typename T, int kR, int kMaxCh, bool kAdd = false>
+// and the RMSNorm after it in one pass. With kGather the row is an embedding table row
+// picked by `src` (a token's embedding), also stored to h_out: the lookup and the
+// first block's input norm in one pass.
+template <typename T, int kR, int kMaxCh, bool kAdd = false, bool kGather = false>
 __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const void* __restrict__ x,
                                                           const void* __restrict__ w,
                                                           void* __restrict__ out, int64_t rows,
                                                           int dim, float eps,
                                                           const void* __restrict__ residual = nullptr,
-                                                          void* __restrict__ h_out = nullptr) {
+                                                          void* __restrict__ h_out = nullptr,
+                                                          RowSource src = {}) {
+  static_assert(!(kAdd && kGather), "one row source");
   constexpr int E = Chunk<T>::kN;
   const int lane = threadIdx.x % kWave;
   const int64_t row = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kR;
@@ -42,7 +63,16 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const void* __restrict
   const bool live = row < rows;
   const int chunks = dim / E;
 
-  const char* xr = static_cast<const char*>(x) + (live ? row : 0) * static_cast<int64_t>(dim) * Elem<T>::kBytes;
+  int64_t xrow = live ? row : 0;
+  bool tok_ok = true;
+  if constexpr (kGather) {
+    if (live) {
+      const int64_t tok = src.ids[src.index != nullptr ? src.index[row] : row];
+      tok_ok = tok >= 0 && tok < src.vocab;
+      xrow = tok_ok ? tok : 0;
+    }
+  }
+  const char* xr = static_cast<const char*>(x) + xrow * static_cast<int64_t>(dim) * Elem<T>::kBytes;
   u32x4 held[kMaxCh];
   float sumsq = 0.0f;
 #pragma unroll
@@ -50,6 +80,14 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const void* __restrict
     const int chunk = r + c * kR;
     if (chunk < chunks) {
       held[c] = nt_load16(xr + chunk * 16);
+      if constexpr (kGather) {
+        if (!tok_ok) held[c] = nan_chunk<T>();
+        if (live) {
+          nt_store16(static_cast<char*>(h_out) + row * static_cast<int64_t>(dim) * Elem<T>::kBytes +
+                         chunk * 16,
+                     held[c]);
+        }
+      }
       if constexpr (kAdd) {
         const int64_t off = (live ? row : 0) * static_cast<int64_t>(dim) * Elem<T>::kBytes + chunk * 16;
         float a[E], b[E];
@@ -141,22 +179,23 @@ __global__ __launch_bounds__(256) void rmsnorm_scalar_kernel(const void* __restr
 
 namespace {
 
-template <typename T, int kR, bool kAdd>
+template <typename T, int kR, bool kAdd, bool kGather = false>
 hipError_t launch_rmsnorm_rk(const void* x, const void* w, void* out, int64_t rows, int dim,
-                             float eps, const void* residual, void* h_out, hipStream_t stream) {
+                             float eps, const void* residual, void* h_out, hipStream_t stream,
+                             const RowSource& src = {}) {
   constexpr int E = Chunk<T>::kN;
   const int chunks = dim / E;
   const int per_lane = (chunks + kR - 1) / kR;
   const int64_t threads = rows * kR;
   const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
   if (per_lane <= 1) {
-    rmsnorm_vec_kernel<T, kR, 1, kAdd><<<grid, 256, 0, stream>>>(x, w, out, rows, dim, eps, residual, h_out);
+    rmsnorm_vec_kernel<T, kR, 1, kAdd, kGather><<<grid, 256, 0, stream>>>(x, w, out, rows, dim, eps, residual, h_out, src);
   } else if (per_lane <= 2) {
-    rmsnorm_vec_kernel<T, kR, 2, kAdd><<<grid, 256, 0, stream>>>(x, w, out, rows, dim, eps, residual, h_out);
+    rmsnorm_vec_kernel<T, kR, 2, kAdd, kGather><<<grid, 256, 0, stream>>>(x, w, out, rows, dim, eps, residual, h_out, src);
   } else if (per_lane <= 4) {
-    rmsnorm_vec_kernel<T, kR, 4, kAdd><<<grid, 256, 0, stream>>>(x, w, out, rows, dim, eps, residual, h_out);
+    rmsnorm_vec_kernel<T, kR, 4, kAdd, kGather><<<grid, 256, 0, stream>>>(x, w, out, rows, dim, eps, residual, h_out, src);
   } else {
-    rmsnorm_vec_kernel<T, kR, 8, kAdd><<<grid, 256, 0, stream>>>(x, w, out, rows, dim, eps, residual, h_out);
+    rmsnorm_vec_kernel<T, kR, 8, kAdd, kGather><<<grid, 256, 0, stream>>>(x, w, out, rows, dim, eps, residual, h_out, src);
   }
   return hipGetLastError();
 }
@@ -164,7 +203,11 @@ hipError_t launch_rmsnorm_rk(const void* x, const void* w, void* out, int64_t ro
 template <typename T, int kR>
 hipError_t launch_rmsnorm_r(const void* x, const void* w, void* out, int64_t rows, int dim,
                             float eps, hipStream_t stream, const void* residual = nullptr,
-                            void* h_out = nullptr) {
+                            void* h_out = nullptr, const RowSource* src = nullptr) {
+  if (src != nullptr) {
+    return launch_rmsnorm_rk<T, kR, false, true>(x, w, out, rows, dim, eps, nullptr, h_out, stream,
+                                                 *src);
+  }
   if (residual != nullptr) {
     return launch_rmsnorm_rk<T, kR, true>(x, w, out, rows, dim, eps, residual, h_out, stream);
   }
@@ -174,25 +217,26 @@ hipError_t launch_rmsnorm_r(const void* x, const void* w, void* out, int64_t row
 template <typename T>
 hipError_t launch_rmsnorm_t(const void* x, const void* w, void* out, int64_t rows, int dim,
                             float eps, hipStream_t stream, const void* res = nullptr,
-                            void* h_out = nullptr) {
+                            void* h_out = nullptr, const RowSource* src = nullptr) {
   constexpr int E = Chunk<T>::kN;
   const bool aligned = (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
                         reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(res) |
                         reinterpret_cast<uintptr_t>(h_out)) % 16 == 0;
   const int chunks = dim / E;
   if (!aligned || dim % E != 0 || chunks > 64 * 8) {
-    if (res != nullptr) return hipErrorInvalidValue;  // the add has the vector kernel only
+    // the add and the embedding lookup have the vector kernel only
+    if (res != nullptr || src != nullptr) return hipErrorInvalidValue;
     const dim3 grid(static_cast<unsigned>((rows * kWave + 255) / 256));
     rmsnorm_scalar_kernel<T><<<grid, 256, 0, stream>>>(x, w, out, rows, dim, eps);
     return hipGetLastError();
   }
-  if (chunks <= 1) return launch_rmsnorm_r<T, 1>(x, w, out, rows, dim, eps, stream, res, h_out);
-  if (chunks <= 2) return launch_rmsnorm_r<T, 2>(x, w, out, rows, dim, eps, stream, res, h_out);
-  if (chunks <= 4) return launch_rmsnorm_r<T, 4>(x, w, out, rows, dim, eps, stream, res, h_out);
-  if (chunks <= 8) return launch_rmsnorm_r<T, 8>(x, w, out, rows, dim, eps, stream, res, h_out);
-  if (chunks <= 16) return launch_rmsnorm_r<T, 16>(x, w, out, rows, dim, eps, stream, res, h_out);
-  if (chunks <= 32) return launch_rmsnorm_r<T, 32>(x, w, out, rows, dim, eps, stream, res, h_out);
-  return launch_rmsnorm_r<T, 64>(x, w, out, rows, dim, eps, stream, res, h_out);
+  if (chunks <= 1) return launch_rmsnorm_r<T, 1>(x, w, out, rows, dim, eps, stream, res, h_out, src);
+  if (chunks <= 2) return launch_rmsnorm_r<T, 2>(x, w, out, rows, dim, eps, stream, res, h_out, src);
+  if (chunks <= 4) return launch_rmsnorm_r<T, 4>(x, w, out, rows, dim, eps, stream, res, h_out, src);
+  if (chunks <= 8) return launch_rmsnorm_r<T, 8>(x, w, out, rows, dim, eps, stream, res, h_out, src);
+  if (chunks <= 16) return launch_rmsnorm_r<T, 16>(x, w, out, rows, dim, eps, stream, res, h_out, src);
+  if (chunks <= 32) return launch_rmsnorm_r<T, 32>(x, w, out, rows, dim, eps, stream, res, h_out, src);
+  return launch_rmsnorm_r<T, 64>(x, w, out, rows, dim, eps, stream, res, h_out, src);
 }
 
 }  // namespace
@@ -210,6 +254,18 @@ hipError_t launch_add_rmsnorm(const void* x, const void* residual, const void* w
     case kF32: return launch_rmsnorm_t<float>(x, w, out, rows, dim, eps, stream, residual, h_out);
     case kF16: return launch_rmsnorm_t<f16_t>(x, w, out, rows, dim, eps, stream, residual, h_out);
     case kBF16: return launch_rmsnorm_t<bf16_t>(x, w, out, rows, dim, eps, stream, residual, h_out);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_embed_rmsnorm(const void* table, int64_t vocab, const int64_t* ids,
+                                const int64_t* index, const void* w, void* h_out, void* out,
+                                int64_t rows, int dim, float eps, int dtype, hipStream_t stream) {
+  const RowSource src{ids, index, vocab};
+  switch (dtype) {
+    case kF32: return launch_rmsnorm_t<float>(table, w, out, rows, dim, eps, stream, nullptr, h_out, &src);
+    case kF16: return launch_rmsnorm_t<f16_t>(table, w, out, rows, dim, eps, stream, nullptr, h_out, &src);
+    case kBF16: return launch_rmsnorm_t<bf16_t>(table, w, out, rows, dim, eps, stream, nullptr, h_out, &src);
     default: return hipErrorInvalidValue;
   }
 }

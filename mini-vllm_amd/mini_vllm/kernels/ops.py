@@ -17,6 +17,8 @@ plus ops that fuse what the reference's caller does in several calls:
     qk_norm_rope(q, k, q_weight, k_weight, positions, cos, sin, eps=1e-6,
                  use_cuda=False)               qwen3_paged.py:73-78 (2 rmsnorm + 2 rope)
     qk_norm_rope_kv_write(...)                 the two above in one launch
+    embed_rmsnorm(table, ids, weight, eps)     the token embedding and the first block's
+                                               input norm in one launch (219, 134)
     paged_decode_qk_norm_rope(...)             a decode step's qk_norm_rope_kv_write and
                                                paged_attention in one launch (71-95)
 
@@ -54,6 +56,7 @@ __all__ = [
     "attention",
     "cuda_kernel_names",
     "dispatch_report",
+    "embed_rmsnorm",
     "kv_write",
     "PackedWeight",
     "linear",
@@ -193,6 +196,22 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
             "rmsnorm", _same_dtype_reason(x, weight, "weight")):
         return load_extension().rmsnorm(x, weight, eps)
     return torch_path.rms_norm(x, weight, eps)
+
+
+def embed_rmsnorm(table: torch.Tensor, ids: torch.Tensor, weight: torch.Tensor,
+                  eps: float = 1e-6, use_cuda: bool = False,
+                  index: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(h, rmsnorm(h))`` for ``h = table[ids]`` (``table[ids[index]]`` with ``index``):
+    the token embedding and the first block's input norm (reference
+    model/qwen3_paged.py:219,134). Kernel: ``csrc/elementwise.hip``, one launch, bitwise
+    the lookup then :func:`rmsnorm`; otherwise the torch lookup and :func:`rmsnorm`."""
+    if _use_kernel("rmsnorm", use_cuda, table) and load_extension().embed_rmsnorm_supported(
+            table, ids, weight, index):
+        return load_extension().embed_rmsnorm(table, ids, weight, eps, index)
+    if index is not None:
+        ids = ids.index_select(0, index)
+    h = table.index_select(0, ids)
+    return h, rmsnorm(h, weight, eps, use_cuda=use_cuda)
 
 
 def _same_dtype_reason(x: torch.Tensor, other: torch.Tensor, what: str) -> str | None:

@@ -271,13 +271,16 @@ class Qwen3Paged:
     def __call__(self, batch) -> torch.Tensor:
         c = self.config
         u = self.use_cuda
-        h = self.weights["embedding"].index_select(0, batch.input_ids)
+        # The token embeddings and the first block's input norm (one launch with the
+        # kernels on); a decode graph's batch names its input tokens by (buffer, index).
+        ids, index = batch.input_source or (batch.input_ids, None)
+        h, normed = ops.embed_rmsnorm(self.weights["embedding"], ids, self.layers[0]["attn_norm"],
+                                      c.rms_norm_eps, use_cuda=u, index=index)
         # With the kernels on, every step takes the fused ops: decode-sized ones run the
         # skinny kernels, larger ones (prefill chunks) one BLAS call over the
         # concatenated weights instead of three (q/k/v) or two (gate/up).
         fused = u
         n_layers = len(self.layers)
-        normed = ops.rmsnorm(h, self.layers[0]["attn_norm"], c.rms_norm_eps, use_cuda=u)
         for layer, (w, p) in enumerate(zip(self.layers, self.packed)):
             # normed = attn_norm(h) of this layer, computed by the previous layer's
             # down projection (or above, for the first layer).

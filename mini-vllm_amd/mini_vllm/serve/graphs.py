@@ -21,8 +21,10 @@ fixed, so one captured graph serves every decode step of a given shape:
   decode step while the GPU runs this one. That buffer is the head of one int64 device
   buffer that also holds the host's ids, the gather indices and the positions of the
   replay (``[prev tokens | ids | gather | positions]``, the last three sized by the
-  batch), so a replay's input ids are one ``index_select`` over it: row i takes element
-  ``gather[i]``, its row of the previous replay or its own host id.
+  batch), from which the model's first launch (the embedding lookup with the first
+  block's input norm) takes each row's token: row i takes element ``gather[i]``, its
+  row of the previous replay or its own host id (the batch's ``input_source``; its
+  ``input_ids`` are not filled).
 
 The paged-attention plan in stream mode depends only on the batch size and the bound on
 max_context_len, so the kernels launched inside a graph stay valid for every replay;
@@ -73,6 +75,7 @@ class _Captured:
             max_query_len=1,
             max_context_len=width * p,
             seq_ids=tuple(range(b)),
+            input_source=(tokens, self.gather),
         )
         self.dummy_block = dummy_block
         self.model = model
@@ -117,11 +120,7 @@ class _Captured:
         self.dyn64.copy_(self.host64, non_blocking=True)
         self.dyn32.copy_(self.host32, non_blocking=True)
 
-    def _gather_inputs(self) -> None:
-        torch.index_select(self.tokens, 0, self.gather, out=self.input_ids)
-
     def _forward(self) -> torch.Tensor:
-        self._gather_inputs()
         return self.model(self.batch)
 
     def capture(self) -> None:

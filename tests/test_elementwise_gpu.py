@@ -225,6 +225,64 @@ def test_add_rmsnorm_is_the_add_then_rmsnorm(extension, device, dtype, rows, dim
     assert torch.equal(h2, h) and torch.equal(n2, normed)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("rows,dim,vocab", [(1, 128, 50), (32, 1024, 151936), (300, 1024, 4000),
+                                            (5, 2048, 77)])
+@pytest.mark.parametrize("indexed", [False, True])
+def test_embed_rmsnorm_is_the_lookup_then_rmsnorm(extension, device, dtype, rows, dim, vocab,
+                                                  indexed):
+    """The token embedding and the first block's input norm in one launch: h bitwise the
+    table rows (index_select), the normed rows bitwise the rmsnorm kernel on them; with
+    an index, the ids gathered first (a decode graph's [previous tokens | host ids]
+    buffer); ops routes to it."""
+    gen = torch.Generator().manual_seed(rows + dim + vocab)
+    table = (torch.randn(vocab, dim, generator=gen) * 0.5).to(dtype).to(device)
+    w = (torch.rand(dim, generator=gen) + 0.5).to(dtype).to(device)
+    if indexed:
+        buf = torch.randint(0, vocab, (rows + 40,), generator=gen).to(device)
+        index = torch.randint(0, rows + 40, (rows,), generator=gen).to(device)
+        ids = buf.index_select(0, index)
+        h, normed = extension.embed_rmsnorm(table, buf, w, 1e-6, index=index)
+    else:
+        buf, index = torch.randint(0, vocab, (rows,), generator=gen).to(device), None
+        ids = buf
+        h, normed = extension.embed_rmsnorm(table, buf, w, 1e-6)
+    want_h = table.index_select(0, ids)
+    assert torch.equal(h, want_h)
+    assert torch.equal(normed, extension.rmsnorm(want_h, w, 1e-6))
+    h2, n2 = ops.embed_rmsnorm(table, buf, w, 1e-6, use_cuda=True, index=index)
+    assert torch.equal(h2, h) and torch.equal(n2, normed)
+
+
+def test_embed_rmsnorm_out_of_range_ids_give_nan_rows(extension, device):
+    """A token id outside [0, vocab) reads nothing and yields NaN rows; its neighbours are
+    unaffected. The torch path (use_cuda=False) agrees on the valid rows."""
+    table = torch.randn(10, 256, dtype=torch.bfloat16, device=device)
+    w = torch.ones(256, dtype=torch.bfloat16, device=device)
+    ids = torch.tensor([3, -1, 10, 9], device=device)
+    h, normed = extension.embed_rmsnorm(table, ids, w, 1e-6)
+    torch.cuda.synchronize()
+    for i in (1, 2):
+        assert torch.isnan(h[i]).all() and torch.isnan(normed[i]).all()
+    ok = torch.tensor([0, 3], device=device)
+    valid = ids.index_select(0, ok)
+    h_t, n_t = ops.embed_rmsnorm(table, valid, w, 1e-6, use_cuda=False)
+    assert torch.equal(h.index_select(0, ok), h_t)
+    assert torch.equal(normed.index_select(0, ok), extension.rmsnorm(h_t, w, 1e-6))
+
+
+def test_embed_rmsnorm_refusals_and_fallback(extension, device):
+    table = torch.randn(10, 100, dtype=torch.bfloat16, device=device)  # rows not whole chunks
+    w = torch.ones(100, dtype=torch.bfloat16, device=device)
+    ids = torch.tensor([1, 2], device=device)
+    assert not extension.embed_rmsnorm_supported(table, ids, w)
+    with pytest.raises(RuntimeError, match="16-byte chunks"):
+        extension.embed_rmsnorm(table, ids, w)
+    assert not extension.embed_rmsnorm_supported(table[:, :96].contiguous(), ids.int(), w[:96])
+    h, n = ops.embed_rmsnorm(table, ids, w, use_cuda=True)  # the lookup and rmsnorm instead
+    assert torch.equal(h, table[ids]) and torch.equal(n, extension.rmsnorm(table[ids], w))
+
+
 def test_add_rmsnorm_refusals_and_fallback(extension, device):
     x = torch.randn(4, 100, dtype=torch.bfloat16, device=device)  # 100 not a whole chunk count
     w = torch.ones(100, dtype=torch.bfloat16, device=device)
