@@ -13,9 +13,10 @@ fixed, so one captured graph serves every decode step of a given shape:
   the block-table width is rounded up to a multiple of 64 pages;
 * before a replay, the iteration's metadata is packed into one pinned host buffer and
   copied into the graph's static input tensors with one host-to-device copy;
-* sampling (argmax) runs after the replay, outside the graph, and writes the sampled
-  tokens straight into a device buffer every graph reads (:attr:`DecodeGraphs.prev_tokens`;
-  :meth:`DecodeGraphs.keep` records which rows were committed); a sequence whose token
+* greedy sampling (argmax) is the graph's last launch and writes the sampled tokens
+  straight into a device buffer every graph reads (:attr:`DecodeGraphs.prev_tokens`;
+  other sampling runs after the replay on its logits and :meth:`DecodeGraphs.keep`
+  copies its tokens there; keep records which rows were committed); a sequence whose token
   from the previous iteration was committed takes its next input token from there, so
   the host need not have read that token yet: the engine schedules and packs the next
   decode step while the GPU runs this one. That buffer is the head of one int64 device
@@ -34,6 +35,8 @@ they read the real context lengths from the static buffers.
 from __future__ import annotations
 
 import torch
+
+from mini_vllm.kernels import ops
 
 from mini_vllm.serve.batch import PADDING_BLOCK, ForwardBatch
 
@@ -120,8 +123,10 @@ class _Captured:
         self.dyn64.copy_(self.host64, non_blocking=True)
         self.dyn32.copy_(self.host32, non_blocking=True)
 
-    def _forward(self) -> torch.Tensor:
-        return self.model(self.batch)
+    def _forward(self, sampled: torch.Tensor) -> torch.Tensor:
+        logits = self.model(self.batch)
+        ops.argmax(logits, use_cuda=self.model.use_cuda, out=sampled)
+        return logits
 
     def capture(self) -> None:
         # Warm up on a side stream (allocator pools, BLAS handles, the kernels' per-stream
@@ -129,13 +134,18 @@ class _Captured:
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
+            # (the warm-up's tokens go to a scratch buffer: the shared one still holds
+            # the previous replay's, which this iteration's replay gathers)
+            scratch = torch.empty(self.batch_size, dtype=torch.int64, device=self.tokens.device)
             for _ in range(2):
-                self._forward()
+                self._forward(scratch)
         torch.cuda.current_stream().wait_stream(side)
         self.graph = torch.cuda.CUDAGraph()
         recorder = _workspace_recorder(self.model)
         with recorder as workspaces, torch.cuda.graph(self.graph, stream=side):
-            self.logits = self._forward()
+            # The greedy tokens, into the head of the shared token buffer the next
+            # replay gathers from (dummy rows' too, beyond the real ones: never gathered).
+            self.logits = self._forward(self.tokens[:self.batch_size])
         self.workspaces = list(workspaces)
 
 
@@ -184,9 +194,10 @@ class DecodeGraphs:
         return 0 < len(scheduled) <= self.max_batch and all(n == 1 for _, n in scheduled)
 
     def run(self, scheduled) -> torch.Tensor:
-        """Logits ``len(scheduled) x V`` for a pure-decode iteration. A sequence that was
-        in the previous replay, and whose token from it was handed to :meth:`keep`, reads
-        that token on the device."""
+        """Logits ``len(scheduled) x V`` for a pure-decode iteration; their argmax is in
+        ``prev_tokens[:len(scheduled)]`` when the replay ends. A sequence that was in the
+        previous replay, and whose token from it was handed to :meth:`keep`, reads that
+        token on the device."""
         n = len(scheduled)
         bucket = next(b for b in BUCKETS if b >= n)
         widest = max(len(self.model.manager.table(s.seq_id)) for s, _ in scheduled)

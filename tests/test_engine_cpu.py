@@ -189,9 +189,10 @@ def test_sampled_requests_are_reproducible_and_greedy_ones_unchanged(model):
 class _EagerGraphs:
     """Stands in for DecodeGraphs.run on the CPU: the same input rule (a sequence in
     ``prev_rows`` takes ``prev_tokens[row]`` as its input token, every other row the
-    host's token) without capturing a graph, so the engine's bookkeeping of which
-    sampled tokens the next iteration may gather is checked here. Records every
-    (sequence, position, token fed)."""
+    host's token) and the same output (the logits, their argmax written to the head of
+    ``prev_tokens`` as a replay's last launch does) without capturing a graph, so the
+    engine's bookkeeping of which sampled tokens the next iteration may gather is
+    checked here. Records every (sequence, position, token fed)."""
 
     def __init__(self, graphs):
         self.graphs = graphs
@@ -211,7 +212,9 @@ class _EagerGraphs:
                 ids[i] = g.prev_tokens[row]
             self.fed.append((seq, seq.num_computed_tokens, int(ids[i])))
         g.replays += 1
-        return g.model(replace(batch, input_ids=ids))
+        logits = g.model(replace(batch, input_ids=ids))
+        g.prev_tokens[:len(scheduled)].copy_(logits.argmax(dim=-1))
+        return logits
 
 
 @pytest.mark.parametrize("lengths,sched", [
