@@ -301,18 +301,20 @@ int mvllm_paged_decode_qk_norm_rope(
     void* workspace, uint64_t workspace_bytes, void* stream);
 
 /* The token embedding lookup and the first block's input RMSNorm in one launch:
- * h_out[i] = table[ids[index ? index[i] : i]] (the row copied), out[i] =
- * rmsnorm(h_out[i], weight), bitwise the lookup then mvllm_rmsnorm. A token id outside
- * [0, vocab) gives NaN rows and reads nothing. `index` (may be NULL) gathers the ids in
- * the same launch: a decode graph's input tokens, each either the token its sequence
- * sampled in the previous replay or the host's id. Replaces the reference forward's
- * Embedding lookup and its first block's attn_norm (model/qwen3_paged.py:219 and 134);
- * no counterpart in mini_vllm_C.
+ * h_out[i] = the table row of row i's token (copied), out[i] = rmsnorm(h_out[i],
+ * weight), bitwise the lookup then mvllm_rmsnorm. Row i's token is prev[index[i]] when
+ * `index` is given and index[i] >= 0, else ids[i]: a decode step's input token is
+ * either the one its sequence sampled in the previous step, still on the device
+ * (`prev`), or the host's id. A token id outside [0, vocab) gives NaN rows and reads
+ * nothing. Replaces the reference forward's Embedding lookup and its first block's
+ * attn_norm (model/qwen3_paged.py:219 and 134); no counterpart in mini_vllm_C.
  *   table [vocab, dim], weight [dim], h_out / out [rows, dim], all of `dtype` and
- *   16-byte aligned; ids, index int64. Dims as mvllm_add_rmsnorm. */
+ *   16-byte aligned; ids, index [rows] and prev int64 (index may be NULL, and prev
+ *   then too). Dims as mvllm_add_rmsnorm. */
 int mvllm_embed_rmsnorm(void* h_out, void* out, const void* table, int64_t vocab,
-                        const int64_t* ids, const int64_t* index, int64_t rows, int32_t dim,
-                        const void* weight, float eps, int32_t dtype, void* stream);
+                        const int64_t* ids, const int64_t* index, const int64_t* prev,
+                        int64_t rows, int32_t dim, const void* weight, float eps, int32_t dtype,
+                        void* stream);
 
 /* out = T(T(g * T(sigmoid(g))) * u) elementwise over n elements of `dtype`.
  * Replaces `mini_vllm_C.swiglu` (csrc/bindings.cpp:14,59-63 -> csrc/swiglu.cu:87-120),

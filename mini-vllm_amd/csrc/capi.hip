@@ -1163,8 +1163,9 @@ int mvllm_add_rmsnorm(void* h_out, void* out, const void* x, const void* residua
 }
 
 int mvllm_embed_rmsnorm(void* h_out, void* out, const void* table, int64_t vocab,
-                        const int64_t* ids, const int64_t* index, int64_t rows, int32_t dim,
-                        const void* weight, float eps, int32_t dtype, void* stream) {
+                        const int64_t* ids, const int64_t* index, const int64_t* prev,
+                        int64_t rows, int32_t dim, const void* weight, float eps, int32_t dtype,
+                        void* stream) {
   g_error[0] = '\0';
   if (!mvllm::add_rmsnorm_supported(dtype, dim)) {
     return fail(MVLLM_ERR_UNSUPPORTED,
@@ -1176,15 +1177,16 @@ int mvllm_embed_rmsnorm(void* h_out, void* out, const void* table, int64_t vocab
   if (rows < 0 || vocab <= 0) return fail(MVLLM_ERR_INVALID, "embed_rmsnorm: bad row or vocab count");
   if (rows == 0) return MVLLM_OK;
   if (h_out == nullptr || out == nullptr || table == nullptr || ids == nullptr ||
-      weight == nullptr) {
+      weight == nullptr || (index != nullptr && prev == nullptr)) {
     return fail(MVLLM_ERR_INVALID, "embed_rmsnorm: a required pointer is NULL");
   }
   if ((reinterpret_cast<uintptr_t>(h_out) | reinterpret_cast<uintptr_t>(out) |
        reinterpret_cast<uintptr_t>(table) | reinterpret_cast<uintptr_t>(weight)) % 16 != 0) {
     return fail(MVLLM_ERR_INVALID, "embed_rmsnorm: the table, weight and outputs must be 16-byte aligned");
   }
-  return hip_status(mvllm::launch_embed_rmsnorm(table, vocab, ids, index, weight, h_out, out, rows,
-                                                dim, eps, dtype, static_cast<hipStream_t>(stream)),
+  return hip_status(mvllm::launch_embed_rmsnorm(table, vocab, ids, index, prev, weight, h_out, out,
+                                                rows, dim, eps, dtype,
+                                                static_cast<hipStream_t>(stream)),
                     "embed_rmsnorm: launch");
 }
 

@@ -22,12 +22,13 @@ namespace mvllm {
 
 // ------------------------------------------------------------------- rmsnorm
 
-// Rows taken from an embedding table (x = the table): row i is table row
-// ids[index ? index[i] : i]; a token id outside [0, vocab) reads nothing and gives NaN
-// rows.
+// Rows taken from an embedding table (x = the table): row i is the table row of token
+// prev[index[i]] when index is given and index[i] >= 0, else of token ids[i]; a token
+// id outside [0, vocab) reads nothing and gives NaN rows.
 struct RowSource {
   const int64_t* ids = nullptr;
   const int64_t* index = nullptr;
+  const int64_t* prev = nullptr;
   int64_t vocab = 0;
 };
 
@@ -67,7 +68,8 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const void* __restrict
   bool tok_ok = true;
   if constexpr (kGather) {
     if (live) {
-      const int64_t tok = src.ids[src.index != nullptr ? src.index[row] : row];
+      const int64_t at = src.index != nullptr ? src.index[row] : -1;
+      const int64_t tok = at >= 0 ? src.prev[at] : src.ids[row];
       tok_ok = tok >= 0 && tok < src.vocab;
       xrow = tok_ok ? tok : 0;
     }
@@ -259,9 +261,10 @@ hipError_t launch_add_rmsnorm(const void* x, const void* residual, const void* w
 }
 
 hipError_t launch_embed_rmsnorm(const void* table, int64_t vocab, const int64_t* ids,
-                                const int64_t* index, const void* w, void* h_out, void* out,
-                                int64_t rows, int dim, float eps, int dtype, hipStream_t stream) {
-  const RowSource src{ids, index, vocab};
+                                const int64_t* index, const int64_t* prev, const void* w,
+                                void* h_out, void* out, int64_t rows, int dim, float eps,
+                                int dtype, hipStream_t stream) {
+  const RowSource src{ids, index, prev, vocab};
   switch (dtype) {
     case kF32: return launch_rmsnorm_t<float>(table, w, out, rows, dim, eps, stream, nullptr, h_out, &src);
     case kF16: return launch_rmsnorm_t<f16_t>(table, w, out, rows, dim, eps, stream, nullptr, h_out, &src);

@@ -14,12 +14,14 @@ bool add_rmsnorm_supported(int dtype, int dim);
 hipError_t launch_add_rmsnorm(const void* x, const void* residual, const void* w, void* h_out,
                               void* out, int64_t rows, int dim, float eps, int dtype,
                               hipStream_t stream);
-// h_out[i] = table[ids[index ? index[i] : i]] and out = RMSNorm(h_out) in one pass (the
-// token embedding and the first block's input norm; same dims and alignment as the add;
-// a token id outside [0, vocab) gives NaN rows).
+// h_out[i] = the table row of token (index && index[i] >= 0 ? prev[index[i]] : ids[i])
+// and out = RMSNorm(h_out) in one pass (the token embedding and the first block's input
+// norm; same dims and alignment as the add; a token id outside [0, vocab) gives NaN
+// rows).
 hipError_t launch_embed_rmsnorm(const void* table, int64_t vocab, const int64_t* ids,
-                                const int64_t* index, const void* w, void* h_out, void* out,
-                                int64_t rows, int dim, float eps, int dtype, hipStream_t stream);
+                                const int64_t* index, const int64_t* prev, const void* w,
+                                void* h_out, void* out, int64_t rows, int dim, float eps,
+                                int dtype, hipStream_t stream);
 hipError_t launch_rope(const void* x, const void* positions, int pos_bytes, const float* cos_t,
                        const float* sin_t, void* out, int64_t rows, int64_t heads, int dim,
                        int64_t num_positions, int64_t max_positions, int dtype,

@@ -274,7 +274,7 @@ def _bind(lib: ctypes.CDLL) -> None:
     lib.mvllm_rmsnorm.restype = ctypes.c_int
     lib.mvllm_rmsnorm.argtypes = [p, p, p, i64, i64, f32, i32, p]
     lib.mvllm_embed_rmsnorm.restype = ctypes.c_int
-    lib.mvllm_embed_rmsnorm.argtypes = [p, p, p, i64, p, p, i64, i32, p, f32, i32, p]
+    lib.mvllm_embed_rmsnorm.argtypes = [p, p, p, i64, p, p, p, i64, i32, p, f32, i32, p]
     lib.mvllm_add_rmsnorm.restype = ctypes.c_int
     lib.mvllm_add_rmsnorm.argtypes = [p, p, p, p, p, i64, i32, f32, i32, p]
     lib.mvllm_rope.restype = ctypes.c_int
@@ -506,37 +506,44 @@ class HipExtension:
 
     @staticmethod
     def embed_rmsnorm_supported(table: torch.Tensor, ids: torch.Tensor, weight: torch.Tensor,
-                                index: torch.Tensor | None = None) -> bool:
+                                index: torch.Tensor | None = None,
+                                prev: torch.Tensor | None = None) -> bool:
         """Whether ``embed_rmsnorm`` serves these tensors: a contiguous 2-D table of f32,
         f16 or bf16 on the GPU with rows of whole 16-byte chunks (at most 512), the
-        weight alike, int64 ids (and index) on the same device."""
+        weight alike, 1-D int64 ids (and index of the same length, with prev) on the
+        same device."""
         e = 4 if table.dtype == torch.float32 else 8
         dim = table.shape[-1] if table.dim() == 2 else 0
+
+        def i64(t):
+            return t.dtype == torch.int64 and t.dim() == 1 and t.device == table.device
         return (table.dtype in (torch.float32, torch.float16, torch.bfloat16) and table.is_cuda
                 and table.is_contiguous() and weight.dtype == table.dtype
                 and weight.shape == (dim,) and dim > 0 and dim % e == 0 and dim // e <= 512
-                and ids.dtype == torch.int64 and ids.dim() == 1 and ids.device == table.device
-                and (index is None or (index.dtype == torch.int64 and index.dim() == 1
-                                       and index.device == table.device)))
+                and i64(ids) and (index is None or (prev is not None and i64(index) and i64(prev)
+                                                    and index.shape == ids.shape)))
 
     def embed_rmsnorm(self, table: torch.Tensor, ids: torch.Tensor, weight: torch.Tensor,
-                      eps: float = 1e-6, index: torch.Tensor | None = None
-                      ) -> tuple[torch.Tensor, torch.Tensor]:
-        """``h = table[ids]`` (with ``index``: ``table[ids[index]]``) and ``rmsnorm(h)`` in
-        one launch; returns (h, normed). A token id outside the table gives NaN rows."""
-        if not self.embed_rmsnorm_supported(table, ids, weight, index):
+                      eps: float = 1e-6, index: torch.Tensor | None = None,
+                      prev: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """``h`` = the table rows of the tokens (row i: ``prev[index[i]]`` where ``index``
+        is given and ``index[i] >= 0``, else ``ids[i]``) and ``rmsnorm(h)`` in one launch;
+        returns (h, normed). A token id outside the table gives NaN rows."""
+        if not self.embed_rmsnorm_supported(table, ids, weight, index, prev):
             raise RuntimeError("embed_rmsnorm: a contiguous f32/f16/bf16 CUDA table with rows "
-                               "of whole 16-byte chunks (at most 512), its weight, and int64 "
-                               "ids (and index) on its device")
+                               "of whole 16-byte chunks (at most 512), its weight, and 1-D "
+                               "int64 ids (and an index of their length, with prev) on its "
+                               "device")
         ids = ids.contiguous()
-        index = None if index is None else index.contiguous()
-        rows = ids.shape[0] if index is None else index.shape[0]
+        if index is not None:
+            index, prev = index.contiguous(), prev.contiguous()
+        rows = ids.shape[0]
         h = torch.empty(rows, table.shape[1], dtype=table.dtype, device=table.device)
         out = torch.empty_like(h)
         self._check(self.lib.mvllm_embed_rmsnorm(
             h.data_ptr(), out.data_ptr(), table.data_ptr(), table.shape[0], ids.data_ptr(),
-            _ptr(index), rows, table.shape[1], weight.contiguous().data_ptr(), float(eps),
-            DTYPE_CODES[table.dtype], _stream(table.device)))
+            _ptr(index), _ptr(prev), rows, table.shape[1], weight.contiguous().data_ptr(),
+            float(eps), DTYPE_CODES[table.dtype], _stream(table.device)))
         return h, out
 
     def rmsnorm(self, x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:

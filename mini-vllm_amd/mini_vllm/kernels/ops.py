@@ -199,17 +199,18 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
 
 
 def embed_rmsnorm(table: torch.Tensor, ids: torch.Tensor, weight: torch.Tensor,
-                  eps: float = 1e-6, use_cuda: bool = False,
-                  index: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
-    """``(h, rmsnorm(h))`` for ``h = table[ids]`` (``table[ids[index]]`` with ``index``):
+                  eps: float = 1e-6, use_cuda: bool = False, index: torch.Tensor | None = None,
+                  prev: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(h, rmsnorm(h))`` for ``h`` = the table rows of the tokens (row i's token:
+    ``prev[index[i]]`` where ``index`` is given and ``index[i] >= 0``, else ``ids[i]``):
     the token embedding and the first block's input norm (reference
     model/qwen3_paged.py:219,134). Kernel: ``csrc/elementwise.hip``, one launch, bitwise
     the lookup then :func:`rmsnorm`; otherwise the torch lookup and :func:`rmsnorm`."""
     if _use_kernel("rmsnorm", use_cuda, table) and load_extension().embed_rmsnorm_supported(
-            table, ids, weight, index):
-        return load_extension().embed_rmsnorm(table, ids, weight, eps, index)
+            table, ids, weight, index, prev):
+        return load_extension().embed_rmsnorm(table, ids, weight, eps, index, prev)
     if index is not None:
-        ids = ids.index_select(0, index)
+        ids = torch.where(index >= 0, prev.index_select(0, index.clamp(min=0)), ids)
     h = table.index_select(0, ids)
     return h, rmsnorm(h, weight, eps, use_cuda=use_cuda)
 

@@ -272,10 +272,10 @@ class Qwen3Paged:
         c = self.config
         u = self.use_cuda
         # The token embeddings and the first block's input norm (one launch with the
-        # kernels on); a decode graph's batch names its input tokens by (buffer, index).
-        ids, index = batch.input_source or (batch.input_ids, None)
+        # kernels on); a decode graph's batch names its input tokens by (ids, index, prev).
+        ids, index, prev = batch.input_source or (batch.input_ids, None, None)
         h, normed = ops.embed_rmsnorm(self.weights["embedding"], ids, self.layers[0]["attn_norm"],
-                                      c.rms_norm_eps, use_cuda=u, index=index)
+                                      c.rms_norm_eps, use_cuda=u, index=index, prev=prev)
         # With the kernels on, every step takes the fused ops: decode-sized ones run the
         # skinny kernels, larger ones (prefill chunks) one BLAS call over the
         # concatenated weights instead of three (q/k/v) or two (gate/up).

@@ -31,9 +31,10 @@ class ForwardBatch:
     max_query_len: int
     max_context_len: int
     seq_ids: tuple[int, ...]
-    # (buffer, index): the input tokens are buffer[index] instead of input_ids (a decode
-    # graph's, gathered on the device in the embedding launch); None: input_ids.
-    input_source: tuple[torch.Tensor, torch.Tensor] | None = None
+    # (ids, index, prev): row i's input token is prev[index[i]] where index[i] >= 0, else
+    # ids[i] (a decode graph's: the previous replay's tokens still on the device, picked
+    # in the embedding launch); None: input_ids.
+    input_source: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None
 
     @property
     def num_sequences(self) -> int:

@@ -19,13 +19,10 @@ fixed, so one captured graph serves every decode step of a given shape:
   copies its tokens there; keep records which rows were committed); a sequence whose token
   from the previous iteration was committed takes its next input token from there, so
   the host need not have read that token yet: the engine schedules and packs the next
-  decode step while the GPU runs this one. That buffer is the head of one int64 device
-  buffer that also holds the host's ids, the gather indices and the positions of the
-  replay (``[prev tokens | ids | gather | positions]``, the last three sized by the
-  batch), from which the model's first launch (the embedding lookup with the first
-  block's input norm) takes each row's token: row i takes element ``gather[i]``, its
-  row of the previous replay or its own host id (the batch's ``input_source``; its
-  ``input_ids`` are not filled).
+  decode step while the GPU runs this one. The model's first launch (the embedding
+  lookup with the first block's input norm) picks each row's token: row i takes
+  ``prev_tokens[gather[i]]``, its row of the previous replay, or with ``gather[i] = -1``
+  its host id (the batch's ``input_source``: host ids, gather, prev_tokens).
 
 The paged-attention plan in stream mode depends only on the batch size and the bound on
 max_context_len, so the kernels launched inside a graph stay valid for every replay;
@@ -48,48 +45,46 @@ TABLE_QUANTUM = 64  # pages
 
 class _Captured:
     def __init__(self, model, batch_size: int, width: int, dummy_block: int, device,
-                 tokens: torch.Tensor, head: int) -> None:
+                 prev: torch.Tensor) -> None:
         p = model.manager.block_size
         self.batch_size, self.width = batch_size, width
         b = batch_size
         i32 = dict(dtype=torch.int32, device=device)
         i64 = dict(dtype=torch.int64, device=device)
-        # Dynamic inputs: [ids | gather | positions] int64 (in `tokens`, after its `head`
-        # elements of previous tokens) and [context | slots | tables] int32. Row i's input
-        # token is tokens[gather[i]]: the token sampled for it by the previous replay (an
-        # index below `head`, still on the device) or its id from the host (head + i).
-        self.dyn64 = tokens[head:head + 3 * b]
-        self.gather = self.dyn64[b:2 * b]
-        self.tokens = tokens
-        self.head = head
-        self.dyn32 = torch.zeros(2 * b + b * width, **i32)
-        self.host64 = torch.zeros(3 * b, dtype=torch.int64, pin_memory=True)
-        self.host32 = torch.zeros(2 * b + b * width, dtype=torch.int32, pin_memory=True)
-        self.input_ids = torch.zeros(b, **i64)
+        # Dynamic inputs, one device buffer written by one copy from one pinned host
+        # buffer: int64 [ids | gather | positions], then int32 [context | slots | tables].
+        # Row i's input token is prev[gather[i]], the token sampled for it by the previous
+        # replay (still on the device), or with gather[i] = -1 its id from the host.
+        n64, n32 = 3 * b, 2 * b + b * width
+        self.dyn = torch.zeros(8 * n64 + 4 * n32, dtype=torch.uint8, device=device)
+        self.host = torch.zeros(8 * n64 + 4 * n32, dtype=torch.uint8, pin_memory=True)
+        dyn64 = self.dyn[:8 * n64].view(torch.int64)
+        dyn32 = self.dyn[8 * n64:].view(torch.int32)
+        self.prev = prev
         self.batch = ForwardBatch(
-            input_ids=self.input_ids,
-            positions=self.dyn64[2 * b:3 * b],
+            input_ids=dyn64[:b],  # the host's ids (0 in gathered rows): see input_source
+            positions=dyn64[2 * b:3 * b],
             cu_seqlens_q=torch.arange(b + 1, **i32),
             seq_lens=torch.ones(b, **i32),
-            context_lens=self.dyn32[:b],
-            slot_mapping=self.dyn32[b:2 * b],
-            block_tables=self.dyn32[2 * b:].view(b, width),
+            context_lens=dyn32[:b],
+            slot_mapping=dyn32[b:2 * b],
+            block_tables=dyn32[2 * b:].view(b, width),
             last_row_indices=torch.arange(b, **i64),
             max_query_len=1,
             max_context_len=width * p,
             seq_ids=tuple(range(b)),
-            input_source=(tokens, self.gather),
+            input_source=(dyn64[:b], dyn64[b:2 * b], prev),
         )
         self.dummy_block = dummy_block
         self.model = model
         self.graph = None
         self.logits = None
         self.workspaces: list[torch.Tensor] = []  # kernel workspaces the graph names
-        # numpy views of the pinned buffers, written in place; each table row is
+        # numpy views of the pinned buffer, written in place; each table row is
         # rewritten only when the block manager reports a change of that sequence's
         # table (row_keys: (seq_id, version), or None for a dummy row).
-        self.np64 = self.host64.numpy()
-        self.np32 = self.host32.numpy()
+        self.np64 = self.host[:8 * n64].view(torch.int64).numpy()
+        self.np32 = self.host[8 * n64:].view(torch.int32).numpy()
         self.row_keys: list = [()] * b
 
     def fill(self, scheduled, gather: list[int] | None = None) -> None:
@@ -102,7 +97,7 @@ class _Captured:
             start = seq.num_computed_tokens
             g = gather[i] if gather is not None else -1
             # a gathered row's token may not have reached the host yet
-            rows[i] = g if g >= 0 else self.head + i
+            rows[i] = g if g >= 0 else -1
             ids[i] = seq.tokens(start, 1)[0] if g < 0 else 0
             pos[i] = start
             ctx[i] = start + 1
@@ -114,14 +109,13 @@ class _Captured:
                 tables[i, len(table):] = PADDING_BLOCK
                 self.row_keys[i] = key
         for i in range(len(scheduled), b):
-            rows[i] = self.head + i
+            rows[i] = -1
             if self.row_keys[i] is not None:
                 ids[i], pos[i], ctx[i], slots[i] = 0, 0, 1, self.dummy_block * p
                 tables[i, 0] = self.dummy_block
                 tables[i, 1:] = PADDING_BLOCK
                 self.row_keys[i] = None
-        self.dyn64.copy_(self.host64, non_blocking=True)
-        self.dyn32.copy_(self.host32, non_blocking=True)
+        self.dyn.copy_(self.host, non_blocking=True)
 
     def _forward(self, sampled: torch.Tensor) -> torch.Tensor:
         logits = self.model(self.batch)
@@ -136,7 +130,7 @@ class _Captured:
         with torch.cuda.stream(side):
             # (the warm-up's tokens go to a scratch buffer: the shared one still holds
             # the previous replay's, which this iteration's replay gathers)
-            scratch = torch.empty(self.batch_size, dtype=torch.int64, device=self.tokens.device)
+            scratch = torch.empty(self.batch_size, dtype=torch.int64, device=self.prev.device)
             for _ in range(2):
                 self._forward(scratch)
         torch.cuda.current_stream().wait_stream(side)
@@ -145,7 +139,7 @@ class _Captured:
         with recorder as workspaces, torch.cuda.graph(self.graph, stream=side):
             # The greedy tokens, into the head of the shared token buffer the next
             # replay gathers from (dummy rows' too, beyond the real ones: never gathered).
-            self.logits = self._forward(self.tokens[:self.batch_size])
+            self.logits = self._forward(self.prev[:self.batch_size])
         self.workspaces = list(workspaces)
 
 
@@ -181,13 +175,9 @@ class DecodeGraphs:
         self.dummy_block = manager.table(self._dummy_id)[0]
         self.graphs: dict[tuple[int, int], _Captured] = {}
         self.replays = 0
-        # [tokens sampled by the last replay | the replay's ids, gather rows, positions]:
-        # row i of the head is the token of sequence prev_rows' key with value i, read by
-        # the next replay's gather.
-        head = max(BUCKETS)
-        self._tokens = torch.zeros(4 * head, dtype=torch.int64, device=self.device)
-        self._head = head
-        self.prev_tokens = self._tokens[:head]
+        # The tokens sampled by the last replay: row i is the token of the sequence
+        # prev_rows maps to i, read by the next replay's gather.
+        self.prev_tokens = torch.zeros(max(BUCKETS), dtype=torch.int64, device=self.device)
         self.prev_rows: dict[int, int] = {}
 
     def supports(self, scheduled) -> bool:
@@ -207,7 +197,7 @@ class DecodeGraphs:
         entry = self.graphs.get(key)
         if entry is None:
             entry = _Captured(self.model, bucket, width, self.dummy_block, self.device,
-                              self._tokens, self._head)
+                              self.prev_tokens)
             entry.fill(scheduled, gather)
             entry.capture()
             self.graphs[key] = entry

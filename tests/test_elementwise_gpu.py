@@ -233,25 +233,28 @@ def test_embed_rmsnorm_is_the_lookup_then_rmsnorm(extension, device, dtype, rows
                                                   indexed):
     """The token embedding and the first block's input norm in one launch: h bitwise the
     table rows (index_select), the normed rows bitwise the rmsnorm kernel on them; with
-    an index, the ids gathered first (a decode graph's [previous tokens | host ids]
-    buffer); ops routes to it."""
+    an index, row i's token is prev[index[i]] where index[i] >= 0 and the row's own id
+    where it is -1 (a decode graph's previous tokens and host ids); ops routes to it, and
+    its torch path (use_cuda=False) picks the same tokens."""
     gen = torch.Generator().manual_seed(rows + dim + vocab)
     table = (torch.randn(vocab, dim, generator=gen) * 0.5).to(dtype).to(device)
     w = (torch.rand(dim, generator=gen) + 0.5).to(dtype).to(device)
+    own = torch.randint(0, vocab, (rows,), generator=gen).to(device)
+    index = prev = None
+    ids = own
     if indexed:
-        buf = torch.randint(0, vocab, (rows + 40,), generator=gen).to(device)
-        index = torch.randint(0, rows + 40, (rows,), generator=gen).to(device)
-        ids = buf.index_select(0, index)
-        h, normed = extension.embed_rmsnorm(table, buf, w, 1e-6, index=index)
-    else:
-        buf, index = torch.randint(0, vocab, (rows,), generator=gen).to(device), None
-        ids = buf
-        h, normed = extension.embed_rmsnorm(table, buf, w, 1e-6)
+        prev = torch.randint(0, vocab, (rows + 40,), generator=gen).to(device)
+        index = torch.randint(-1, rows + 40, (rows,), generator=gen).to(device)
+        index[0] = -1
+        ids = torch.where(index >= 0, prev.index_select(0, index.clamp(min=0)), own)
+    h, normed = extension.embed_rmsnorm(table, own, w, 1e-6, index=index, prev=prev)
     want_h = table.index_select(0, ids)
     assert torch.equal(h, want_h)
     assert torch.equal(normed, extension.rmsnorm(want_h, w, 1e-6))
-    h2, n2 = ops.embed_rmsnorm(table, buf, w, 1e-6, use_cuda=True, index=index)
+    h2, n2 = ops.embed_rmsnorm(table, own, w, 1e-6, use_cuda=True, index=index, prev=prev)
     assert torch.equal(h2, h) and torch.equal(n2, normed)
+    h3, _ = ops.embed_rmsnorm(table, own, w, 1e-6, use_cuda=False, index=index, prev=prev)
+    assert torch.equal(h3, want_h)
 
 
 def test_embed_rmsnorm_out_of_range_ids_give_nan_rows(extension, device):
