@@ -86,10 +86,15 @@ class _Captured:
         self.np64 = self.host[:8 * n64].view(torch.int64).numpy()
         self.np32 = self.host[8 * n64:].view(torch.int32).numpy()
         self.row_keys: list = [()] * b
+        self._copied = None  # event after the last copy out of the pinned buffer
 
     def fill(self, scheduled, gather: list[int] | None = None) -> None:
         b, w, p = self.batch_size, self.width, self.model.manager.block_size
         manager = self.model.manager
+        if self._copied is not None:
+            # the previous replay's copy must have read the pinned buffer before it is
+            # rewritten (it normally has: it runs as that replay starts)
+            self._copied.synchronize()
         ids, rows, pos = self.np64[:b], self.np64[b:2 * b], self.np64[2 * b:]
         ctx, slots = self.np32[:b], self.np32[b:2 * b]
         tables = self.np32[2 * b:].reshape(b, w)
@@ -116,6 +121,9 @@ class _Captured:
                 tables[i, 1:] = PADDING_BLOCK
                 self.row_keys[i] = None
         self.dyn.copy_(self.host, non_blocking=True)
+        if self.dyn.is_cuda:
+            self._copied = torch.cuda.Event()
+            self._copied.record()
 
     def _forward(self, sampled: torch.Tensor) -> torch.Tensor:
         logits = self.model(self.batch)
