@@ -271,7 +271,8 @@ int mvllm_qk_norm_rope_kv_write(void* q_out, void* key_pool, void* value_pool, c
 
 /* A decode step's attention with its new token's QK-norm, RoPE and KV write in the same
  * launch, for a decode-only batch (every sequence computes one token: seq_lens all 1,
- * num_seqs rows) over a float16 or bfloat16 pool with head_dim 128. Sequence s's token
+ * cu_seqlens_q = 0, 1, ..., num_seqs, so row s is sequence s's) over a float16 or
+ * bfloat16 pool with head_dim 128. Sequence s's token
  * sits at position context_lens[s] - 1 and goes to the slot its block table maps that
  * position to. The result equals, bit for bit, mvllm_qk_norm_rope_kv_write (positions
  * context_lens - 1, slot_mapping from the block tables) followed by
