@@ -206,7 +206,10 @@ struct Decode {
       if constexpr (kFresh) {
         // The step holding the new token (wave-uniform test): its pool slot, read above
         // before this launch wrote it, is replaced by the rows formed in the launch.
-        if (fresh.tok >= 0 && t0 + kStep > fresh.tok) {
+        if (fresh.tok >= 0 && t0 + kStep > fresh.tok) [[unlikely]] {
+          // a real branch, taken once per share: without the barrier the compiler turns
+          // the substitution into selects executed in every step
+          asm volatile("" ::: "memory");
 #pragma unroll
           for (int u = 0; u < kUnroll; ++u) {
             if (t0 + u * RG + g == fresh.tok) {
