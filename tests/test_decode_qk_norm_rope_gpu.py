@@ -207,3 +207,25 @@ def test_op_seam_routes_and_declines(extension, device):
     assert ops.paged_decode_qk_norm_rope(q, k, v, wq, wk, cos, sin, EPS, pk, pv, b.block_tables,
                                          b.cu_seqlens_q, b.context_lens, b.seq_lens,
                                          b.max_context_len, b.scale, use_cuda=False) is None
+
+
+@pytest.mark.parametrize("contexts", [[700], [64, 1000, 2500]], ids=["one", "three"])
+def test_a_spike_on_the_new_token(extension, device, contexts):
+    """The reference's late-spike known answer (tests/test_decode_attention_cuda.py:85-109)
+    placed on the key formed inside the launch: each sequence's new k is its q's first
+    head, norm weights of 8 make that score ~64 / sqrt(128) x 8 above the rest, so every
+    accumulator is rescaled on the last key and the output is ~ that token's v. Bitwise
+    the unfused pair, and within the bf16 tolerance of the oracle chain."""
+    b, q, k, v, wq, wk = _case(contexts, 16, 8, torch.bfloat16, device, seed=5)
+    k[:, :, :] = q[:, 0:1, :]  # the new key points along query head 0 (every kv head)
+    wq = torch.full_like(wq, 8.0)
+    wk = torch.full_like(wk, 8.0)
+    cos, sin = torch_path.rope_tables(128, MAX_POS, device=device)
+    want, wk_pool, wv_pool = _pair(extension, b, q, k, v, wq, wk, cos, sin)
+    got, gk_pool, gv_pool = _fused(extension, b, q, k, v, wq, wk, cos, sin)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert torch.equal(gk_pool, wk_pool) and torch.equal(gv_pool, wv_pool)
+    # query head 0 of each sequence attends (almost) only to the new token: its output
+    # is that token's v row of kv head 0
+    assert_max_abs(got[:, 0, :], v[:, 0, :].float(), 2e-2, "spike")
